@@ -1,0 +1,51 @@
+// common.h -- shared plumbing for the gfx950 kernels behind the doe_mi355x C ABI.
+//
+// Every entry point returns DOE_OK (0) or a negative DOE_E* status and records
+// a thread-local message readable through doe_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/doe_mi355x.h"
+
+namespace doe {
+
+// Sets the thread-local error message; returns `status` for tail calls.
+int set_error(int status, const char *fmt, ...);
+// Clears the thread-local error message.
+void clear_error();
+// Maps a HIP error to DOE_E_HIP with the HIP error string and a context.
+int hip_fail(hipError_t e, const char *what);
+// Checks that the library was initialised on the calling thread's device.
+int require_init();
+
+}  // namespace doe
+
+#define DOE_HIP_CHECK(expr)                                        \
+    do {                                                           \
+        hipError_t doe_e_ = (expr);                                \
+        if (doe_e_ != hipSuccess) return doe::hip_fail(doe_e_, #expr); \
+    } while (0)
+
+// Launch-error check after a kernel launch (asynchronous faults surface at sync).
+#define DOE_LAUNCH_CHECK(name)                                        \
+    do {                                                              \
+        hipError_t doe_e_ = hipGetLastError();                        \
+        if (doe_e_ != hipSuccess) return doe::hip_fail(doe_e_, name); \
+    } while (0)
+
+#define DOE_REQUIRE(cond, status, ...)                            \
+    do {                                                          \
+        if (!(cond)) return doe::set_error((status), __VA_ARGS__); \
+    } while (0)
+
+// Q4_K_M block constants (256 weights in 144 bytes).
+#define DOE_Q4K_BLOCK_BYTES 144
+#define DOE_Q4K_BLOCK_ELEMS 256
+
+__device__ __forceinline__ float doe_half_bits_to_float(uint32_t bits16) {
+    return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
+}

@@ -1,0 +1,352 @@
+// q4k_gemv.hip -- Q4_K_M dequant and decode GEMV (M = 1) for gfx950.
+//
+// Weight layout (bench/tools/doppler_rdrr_q4k.py:11-15, 56-101, 128-156): row r
+// of W[n][k] is ceil(k/256) blocks of 144 bytes; block bytes [0:2] f16 d,
+// [2:4] f16 dmin, [4:16] packed 6-bit scales/mins, [16:144] nibbles.  Nibble
+// byte 16 + 32c + i holds element 64c + i (sub-block 2c) in its low nibble
+// and element 64c + 32 + i (sub-block 2c + 1) in its high nibble.
+//
+// GEMV work decomposition (one workgroup = `rowslots * R` rows):
+//   * a "chunk" is the 32 nibble bytes c of one block: 64 weights from two
+//     sub-blocks.  A row has nchunk = ceil(k/64) chunks.
+//   * thread t owns chunk t % nchunk of rows slot + r*rowslots (slot =
+//     t / nchunk, r < R).  Its 64 activation values never change, so they are
+//     staged once per workgroup into LDS as f16 and then held in VGPRs.
+//     Consecutive lanes read consecutive 16-byte pieces of one row: the
+//     weight stream is fully coalesced with dwordx4 loads.
+//   * nibbles become f16 operands with one AND each: a nibble q in the low
+//     bits of a half is the subnormal q * 2^-24, a nibble in bits 4..7 is
+//     q * 2^-20.  v_dot2_f32_f16 multiplies two such pairs with two activation
+//     halves and accumulates in f32; every product is exact.
+//   * activations are scaled by a power of two so max|x| sits near 2^14 and
+//     split into x_hi = f16(x) and x_lo = f16(x - x_hi): the dot products
+//     then carry ~22 bits of the f32 activation.
+//   * per sub-block: y += d*sc * sum(q*x) - dmin*m * sum(x).  sum(x) over each
+//     sub-block is computed once per workgroup from the f32 activations.
+//   * per-chunk partials are reduced through LDS, eight lanes per row.
+#include "common.h"
+
+#include <math.h>
+#include <stdlib.h>
+
+namespace {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+constexpr int kLdsChunkDwords = 36;  // 64 halves + 16 bytes pad: conflict-free b128 reads
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, a), __builtin_bit_cast(half2v, b), c,
+                                  false);
+}
+
+__device__ __forceinline__ uint32_t pack_half2(_Float16 lo, _Float16 hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Scale/min pair of sub-blocks 2*c4 and 2*c4+1 (doppler_rdrr_q4k.py:56-76),
+// returned as two bytes each: low byte sub-block 2*c4, high byte 2*c4+1.
+__device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int c4,
+                                                   uint32_t &scp, uint32_t &mnp) {
+    const int sh = (c4 & 1) * 16;
+    if (c4 < 2) {
+        scp = (s0 >> sh) & 0x3f3fu;
+        mnp = (s1 >> sh) & 0x3f3fu;
+    } else {
+        scp = ((s2 >> sh) & 0x0f0fu) | ((s0 >> (sh + 2)) & 0x3030u);
+        mnp = ((s2 >> (sh + 4)) & 0x0f0fu) | ((s1 >> (sh + 2)) & 0x3030u);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dequant: out[r][k] = RN_f32(d*sc*q - dmin*m).  d*sc and dmin*m are exact in
+// f32 (11 x 6 significant bits), so one fma rounds the exact value once.
+// ---------------------------------------------------------------------------
+__global__ void q4k_dequant_kernel(const uint8_t *__restrict__ w, float *__restrict__ out,
+                                   int64_t n, int64_t k, int64_t nb) {
+    const int64_t total = n * nb * 128;
+    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+         g += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = g / (nb * 128);
+        const int64_t rem = g - row * nb * 128;
+        const int64_t blk = rem >> 7;
+        const int byte = (int)(rem & 127);
+        const int c4 = byte >> 5, i = byte & 31;
+        const uint8_t *b = w + (row * nb + blk) * DOE_Q4K_BLOCK_BYTES;
+        const uint32_t *bw = reinterpret_cast<const uint32_t *>(b);
+        const uint32_t h = bw[0];
+        uint32_t scp, mnp;
+        q4k_scale_min_pair(bw[1], bw[2], bw[3], c4, scp, mnp);
+        const float d = doe_half_bits_to_float(h), dmin = doe_half_bits_to_float(h >> 16);
+        const uint32_t packed = b[16 + byte];
+        const float dsc_lo = d * (float)(scp & 0xffu), dm_lo = dmin * (float)(mnp & 0xffu);
+        const float dsc_hi = d * (float)(scp >> 8), dm_hi = dmin * (float)(mnp >> 8);
+        const int64_t lo = blk * 256 + c4 * 64 + i, hi = lo + 32;
+        if (lo < k) out[row * k + lo] = fmaf(dsc_lo, (float)(packed & 15u), -dm_lo);
+        if (hi < k) out[row * k + hi] = fmaf(dsc_hi, (float)(packed >> 4), -dm_hi);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV.
+// LDS layout (dynamic): xh[nchunk*36] dwords, xl[nchunk*36] dwords (f16 pairs
+// of x_hi / x_lo), sx[2*nchunk] f32 sub-block sums, red[rows_wg*nchunk] f32
+// partials, wmax[16] f32.
+// Within a chunk, dwords 0..15 hold the low sub-block and 16..31 the high one;
+// each 4-element group (e0,e1,e2,e3) is stored as pairs (e0,e2), (e1,e3) so
+// that `D & 0x000F000F` (bytes 0 and 2 of a nibble dword) meets (e0,e2) and
+// `(D >> 8) & 0x000F000F` meets (e1,e3).
+// ---------------------------------------------------------------------------
+template <int R>
+__global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restrict__ w,
+                                                        const float *__restrict__ x,
+                                                        float *__restrict__ y, int n, int k, int nb,
+                                                        int nchunk, int rowslots) {
+    extern __shared__ uint32_t smem[];
+    uint32_t *xh = smem;
+    uint32_t *xl = xh + nchunk * kLdsChunkDwords;
+    float *sx = reinterpret_cast<float *>(xl + nchunk * kLdsChunkDwords);
+    float *red = sx + 2 * nchunk;
+    const int rows_wg = rowslots * R;
+    float *wmax = red + rows_wg * nchunk;
+
+    const int tid = threadIdx.x;
+    const int nthreads = blockDim.x;
+    const int nquads = nchunk * 16;
+
+    // Phase 1: max |x| over the (zero padded) activation.
+    float amax = 0.0f;
+    for (int qd = tid; qd < nquads; qd += nthreads) {
+        const int e = qd * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(e + j < k ? x[e + j] : 0.0f));
+    }
+    amax = wave_max(amax);
+    if ((tid & 63) == 0) wmax[tid >> 6] = amax;
+    __syncthreads();
+    float gmax = 0.0f;
+    for (int i = 0; i < (nthreads >> 6); ++i) gmax = fmaxf(gmax, wmax[i]);
+    int sigma = 0;
+    if (gmax > 0.0f && gmax <= 3.0e38f) {
+        int e2;
+        frexpf(gmax, &e2);
+        sigma = 14 - e2;
+        sigma = sigma < -100 ? -100 : (sigma > 100 ? 100 : sigma);
+    }
+    const float xs = ldexpf(1.0f, sigma);
+
+    // Phase 2: stage x_hi / x_lo as f16 pairs and the sub-block sums.
+    for (int qd = tid; qd < nquads; qd += nthreads) {
+        const int e = qd * 4;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = e + j < k ? x[e + j] : 0.0f;
+        // The 8 quads of one sub-block are 8 consecutive lanes (nthreads % 64 == 0).
+        float s = (v[0] + v[1]) + (v[2] + v[3]);
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        if ((qd & 7) == 0) sx[qd >> 3] = s;
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float t = v[j] * xs;
+            hi[j] = (_Float16)t;
+            lo[j] = (_Float16)(t - (float)hi[j]);
+        }
+        const int chunk = qd >> 4;
+        const int off = chunk * kLdsChunkDwords + 2 * (qd & 15);
+        *reinterpret_cast<uint2 *>(xh + off) = make_uint2(pack_half2(hi[0], hi[2]), pack_half2(hi[1], hi[3]));
+        *reinterpret_cast<uint2 *>(xl + off) = make_uint2(pack_half2(lo[0], lo[2]), pack_half2(lo[1], lo[3]));
+    }
+    __syncthreads();
+
+    // Phase 3: stream the weights.
+    const int active = rowslots * nchunk;
+    if (tid < active) {
+        const int chunk = tid % nchunk;
+        const int slot = tid / nchunk;
+        const int blk = chunk >> 2, c4 = chunk & 3;
+        const int row0 = blockIdx.x * rows_wg + slot;
+
+        uint4 hdr[R], qa[R], qb[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = row0 + r * rowslots;
+            if (row < n) {
+                const uint8_t *p = w + ((size_t)row * nb + blk) * DOE_Q4K_BLOCK_BYTES;
+                hdr[r] = *reinterpret_cast<const uint4 *>(p);
+                qa[r] = *reinterpret_cast<const uint4 *>(p + 16 + 32 * c4);
+                qb[r] = *reinterpret_cast<const uint4 *>(p + 32 + 32 * c4);
+            } else {
+                hdr[r] = make_uint4(0, 0, 0, 0);
+                qa[r] = make_uint4(0, 0, 0, 0);
+                qb[r] = make_uint4(0, 0, 0, 0);
+            }
+        }
+
+        uint32_t xhv[32], xlv[32];
+        const uint4 *xh4 = reinterpret_cast<const uint4 *>(xh + chunk * kLdsChunkDwords);
+        const uint4 *xl4 = reinterpret_cast<const uint4 *>(xl + chunk * kLdsChunkDwords);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint4 a = xh4[i], b = xl4[i];
+            xhv[4 * i] = a.x; xhv[4 * i + 1] = a.y; xhv[4 * i + 2] = a.z; xhv[4 * i + 3] = a.w;
+            xlv[4 * i] = b.x; xlv[4 * i + 1] = b.y; xlv[4 * i + 2] = b.z; xlv[4 * i + 3] = b.w;
+        }
+        const float sxl = sx[2 * chunk], sxh = sx[2 * chunk + 1];
+        const float f_lo = ldexpf(1.0f, 24 - sigma), f_hi = ldexpf(1.0f, 20 - sigma);
+
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            uint32_t scp, mnp;
+            q4k_scale_min_pair(hdr[r].y, hdr[r].z, hdr[r].w, c4, scp, mnp);
+            const float d = doe_half_bits_to_float(hdr[r].x);
+            const float dmin = doe_half_bits_to_float(hdr[r].x >> 16);
+            const uint32_t q[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w,
+                                   qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+            float lo_a = 0.0f, lo_b = 0.0f, hi_a = 0.0f, hi_b = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t dw = q[i], ew = dw >> 8;
+                const uint32_t p0 = dw & 0x000f000fu, p1 = ew & 0x000f000fu;
+                const uint32_t p2 = dw & 0x00f000f0u, p3 = ew & 0x00f000f0u;
+                lo_a = dot2(p0, xhv[2 * i], lo_a);
+                lo_a = dot2(p1, xhv[2 * i + 1], lo_a);
+                hi_a = dot2(p2, xhv[16 + 2 * i], hi_a);
+                hi_a = dot2(p3, xhv[16 + 2 * i + 1], hi_a);
+                lo_b = dot2(p0, xlv[2 * i], lo_b);
+                lo_b = dot2(p1, xlv[2 * i + 1], lo_b);
+                hi_b = dot2(p2, xlv[16 + 2 * i], hi_b);
+                hi_b = dot2(p3, xlv[16 + 2 * i + 1], hi_b);
+            }
+            const float qx_lo = (lo_a + lo_b) * f_lo;
+            const float qx_hi = (hi_a + hi_b) * f_hi;
+            const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
+            const float m_lo = (float)(mnp & 0xffu), m_hi = (float)(mnp >> 8);
+            const float part = d * (sc_lo * qx_lo + sc_hi * qx_hi) - dmin * (m_lo * sxl + m_hi * sxh);
+            red[(slot + r * rowslots) * nchunk + chunk] = part;
+        }
+    }
+    __syncthreads();
+
+    // Phase 4: reduce each row's nchunk partials, eight lanes per row.
+    for (int idx = tid; idx < rows_wg * 8; idx += nthreads) {
+        const int lr = idx >> 3, l8 = idx & 7;
+        float s = 0.0f;
+        for (int j = l8; j < nchunk; j += 8) s += red[lr * nchunk + j];
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        const int row = blockIdx.x * rows_wg + lr;
+        if (l8 == 0 && row < n) y[row] = s;
+    }
+}
+
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+// Launch shape for the GEMV: rowslots * nchunk threads (rounded up to whole
+// waves), rows per thread R.
+struct GemvShape {
+    int rowslots, rows_per_thread, threads;
+    size_t lds;
+};
+
+GemvShape gemv_shape(int nchunk) {
+    static const int env_slots = env_int("DOE_Q4K_ROWSLOTS", 0);
+    static const int env_r = env_int("DOE_Q4K_ROWS", 0);
+    GemvShape s;
+    int max_slots = 1024 / nchunk;
+    int slots = env_slots > 0 ? env_slots : (576 + nchunk / 2) / nchunk;
+    if (slots < 1) slots = 1;
+    if (slots > max_slots) slots = max_slots;
+    s.rowslots = slots;
+    s.rows_per_thread = (env_r == 1 || env_r == 2 || env_r == 4) ? env_r : 2;
+    s.threads = ((slots * nchunk + 63) / 64) * 64;
+    const int rows_wg = slots * s.rows_per_thread;
+    s.lds = (size_t)nchunk * kLdsChunkDwords * 4 * 2 + (size_t)2 * nchunk * 4 +
+            (size_t)rows_wg * nchunk * 4 + 16 * 4;
+    return s;
+}
+
+}  // namespace
+
+extern "C" {
+
+int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
+                    doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n >= 0 && k >= 0, DOE_E_INVALID, "negative shape n=%lld k=%lld", (long long)n,
+                (long long)k);
+    if (n == 0 || k == 0) return DOE_OK;
+    DOE_REQUIRE(weight_q4k && out, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(((uintptr_t)weight_q4k & 15) == 0, DOE_E_INVALID, "weight must be 16-byte aligned");
+    const int64_t nb = (k + 255) / 256;
+    const int64_t total = n * nb * 128;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(q4k_dequant_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, (const uint8_t *)weight_q4k, out, n, k, nb);
+    DOE_LAUNCH_CHECK("q4k_dequant_kernel");
+    return DOE_OK;
+}
+
+int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output, int64_t n,
+                 int64_t k, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n >= 0 && k >= 0, DOE_E_INVALID, "negative shape n=%lld k=%lld", (long long)n,
+                (long long)k);
+    if (n == 0) return DOE_OK;
+    DOE_REQUIRE(output, DOE_E_INVALID, "null output");
+    if (k == 0) {
+        // Empty reduction: the sum identity (reference_interpreter.zig:323-327).
+        DOE_HIP_CHECK(hipMemsetAsync(output, 0, (size_t)n * sizeof(float), (hipStream_t)stream));
+        return DOE_OK;
+    }
+    DOE_REQUIRE(weight_q4k && activation, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(((uintptr_t)weight_q4k & 15) == 0, DOE_E_INVALID, "weight must be 16-byte aligned");
+    DOE_REQUIRE(n <= 0x7fffffff && k <= 65536, DOE_E_UNSUPPORTED,
+                "q4k_gemv supports n < 2^31 and k <= 65536 (got n=%lld k=%lld)", (long long)n,
+                (long long)k);
+    const int nb = (int)((k + 255) / 256);
+    const int nchunk = (int)((k + 63) / 64);
+    const GemvShape s = gemv_shape(nchunk);
+    DOE_REQUIRE(s.lds <= 64 * 1024, DOE_E_UNSUPPORTED, "k=%lld needs %zu bytes of LDS",
+                (long long)k, s.lds);
+    const int rows_wg = s.rowslots * s.rows_per_thread;
+    const unsigned grid = (unsigned)((n + rows_wg - 1) / rows_wg);
+    const hipStream_t st = (hipStream_t)stream;
+    switch (s.rows_per_thread) {
+        case 1:
+            hipLaunchKernelGGL(q4k_gemv_kernel<1>, dim3(grid), dim3(s.threads), s.lds, st,
+                               (const uint8_t *)weight_q4k, activation, output, (int)n, (int)k, nb,
+                               nchunk, s.rowslots);
+            break;
+        case 4:
+            hipLaunchKernelGGL(q4k_gemv_kernel<4>, dim3(grid), dim3(s.threads), s.lds, st,
+                               (const uint8_t *)weight_q4k, activation, output, (int)n, (int)k, nb,
+                               nchunk, s.rowslots);
+            break;
+        default:
+            hipLaunchKernelGGL(q4k_gemv_kernel<2>, dim3(grid), dim3(s.threads), s.lds, st,
+                               (const uint8_t *)weight_q4k, activation, output, (int)n, (int)k, nb,
+                               nchunk, s.rowslots);
+            break;
+    }
+    DOE_LAUNCH_CHECK("q4k_gemv_kernel");
+    return DOE_OK;
+}
+
+}  // extern "C"

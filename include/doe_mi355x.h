@@ -1,0 +1,111 @@
+/*
+ * doe_mi355x.h -- C ABI of the MI355X (gfx950) quantized-decode hot path.
+ *
+ * Each compute entry point replaces ONE dispatch of one reference kernel: the
+ * reference binds buffers to a WGSL bind group, writes a Uniforms struct and
+ * calls wgpuComputePassEncoderDispatchWorkgroups through its webgpu.h drop-in
+ * (runtime/zig/src/dropin/dropin_abi_procs.zig:232 SetBindGroup, :237
+ * DispatchWorkgroups, :309 QueueSubmit), or memcpy_h2d -> launch("compute") ->
+ * memcpy_d2h on the CSL lane (bench/runners/csl-runners/
+ * fused_gemv_dequant_sim_runner.py:96-118).  Here each binding becomes a
+ * plain device pointer and each Uniforms field a scalar argument, keeping the
+ * reference's binding roles, block layouts and shape parameters.
+ *
+ * Conventions
+ *   - Every function returns DOE_OK (0) or a negative DOE_E_* status; the
+ *     message of the last failure on the calling thread is doe_last_error().
+ *   - Pointers passed to compute entry points are device pointers owned by
+ *     the caller (doe_malloc or any hipMalloc'd memory).  The library owns no
+ *     per-call state; kernels are re-entrant per stream.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Compute
+ *     entry points are asynchronous; errors in arguments are reported
+ *     synchronously, device faults at the next synchronising call.
+ *   - Sizes are int64_t element counts unless named *_bytes.
+ */
+#ifndef DOE_MI355X_H
+#define DOE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DOE_OK 0
+#define DOE_E_INVALID (-1)     /* bad argument (shape, alignment, null) */
+#define DOE_E_NOT_INIT (-2)    /* doe_init was not called */
+#define DOE_E_HIP (-3)         /* HIP runtime error */
+#define DOE_E_UNSUPPORTED (-4) /* valid but unsupported configuration */
+#define DOE_E_OOM (-5)         /* device allocation failed */
+
+typedef void *doe_stream_t; /* hipStream_t */
+typedef void *doe_event_t;  /* hipEvent_t */
+typedef void *doe_graph_t;  /* hipGraphExec_t */
+
+/* ---- lifecycle ------------------------------------------------------------
+ * Replaces the drop-in's instance/adapter/device acquisition
+ * (runtime/zig/src/dropin/dropin_abi_procs.zig:156-170 region) for one GPU. */
+int doe_init(int device);
+int doe_shutdown(void);
+const char *doe_last_error(void);
+/* Writes a JSON object describing the device (name, arch, CUs, clocks). */
+int doe_device_info(char *buf, size_t buf_bytes);
+int doe_device_synchronize(void);
+
+/* ---- memory ----------------------------------------------------------------
+ * Replaces wgpuDeviceCreateBuffer (dropin_abi_procs.zig:156) and
+ * wgpuQueueWriteBuffer (:326) / buffer map-read for readback. */
+int doe_malloc(void **ptr, size_t bytes);
+int doe_free(void *ptr);
+int doe_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int doe_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int doe_memcpy_d2d(void *dst, const void *src, size_t bytes, doe_stream_t stream);
+int doe_memset(void *dst, int value, size_t bytes, doe_stream_t stream);
+
+/* ---- streams, events, graphs -----------------------------------------------
+ * Replace queue submission (dropin_abi_procs.zig:309) and the timestamp
+ * queries of runtime/zig/src/doe_query_native.zig.  Streams are created at
+ * the default priority. */
+int doe_stream_create(doe_stream_t *stream);
+int doe_stream_destroy(doe_stream_t stream);
+int doe_stream_synchronize(doe_stream_t stream);
+int doe_event_create(doe_event_t *event);
+int doe_event_destroy(doe_event_t event);
+int doe_event_record(doe_event_t event, doe_stream_t stream);
+int doe_event_synchronize(doe_event_t event);
+int doe_event_elapsed_ms(float *ms, doe_event_t start, doe_event_t end);
+int doe_graph_capture_begin(doe_stream_t stream);
+int doe_graph_capture_end(doe_stream_t stream, doe_graph_t *graph);
+int doe_graph_launch(doe_graph_t graph, doe_stream_t stream);
+int doe_graph_destroy(doe_graph_t graph);
+
+/* ---- Q4_K_M quantized weights ----------------------------------------------
+ * Block: 256 weights in 144 bytes -- f16 d, f16 dmin, 12 bytes of packed
+ * 6-bit scales/mins, 128 bytes of nibbles (bench/tools/doppler_rdrr_q4k.py:
+ * 11-15, 56-101).  A weight matrix [n][k] is row-wise: ceil(k/256) blocks
+ * per row, row stride ceil(k/256)*144 bytes, values past k in the last block
+ * ignored (doppler_rdrr_q4k.py:128-156).  The pointer must be 16-byte aligned.
+ */
+
+/* Dequantize to f32 out[n][k]; bit-exact RN_f32(d*sc*q - dmin*m).
+ * Replaces the `dequant` op (runtime/zig/src/doe_wgsl/emit_csl_exec_v1.zig:
+ * 164, pattern emitted by emit_csl_dequant.zig) with the canonical block
+ * decode of doppler_rdrr_q4k.py:79-101. */
+int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
+                    doe_stream_t stream);
+
+/* Decode GEMV output[i] = sum_k dequant(weight)[i,k] * activation[k], f32.
+ * Replaces the `matmul_q4k` op (emit_csl_exec_v1.zig:162 -> pattern
+ * fused_gemv_dequant, runtime/zig/src/doe_wgsl/emit_csl_fused.zig:47-200,
+ * exported symbols activation/weight/output) and the reference interpreter's
+ * fused_gemv (runtime/zig/src/tsir/reference_interpreter.zig:169-394).
+ * activation: f32[k] (16-byte aligned), output: f32[n]. */
+int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
+                 int64_t n, int64_t k, doe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DOE_MI355X_H */

@@ -1,0 +1,87 @@
+/*
+ * doe_oracle.h -- CPU oracle for the quantized-decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference's
+ * CPU evaluation of each hot-path kernel (the TSIR reference interpreter, the
+ * CSL/WebGPU emulator's CPU backend and the Doppler RDRR Q4_K decoder).  Only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it,
+ * and only as the checker.  The product library (doe_amd) never calls it.
+ *
+ * Numerics: every function runs single-threaded, in the reference's strict
+ * order (f32 left-fold accumulation unless noted), built with
+ * -O2 -ffp-contract=off and no fast-math.
+ *
+ * All functions return 0 on success and a negative value on invalid sizes.
+ */
+#ifndef DOE_ORACLE_H
+#define DOE_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar conversions ------------------------------------------------ */
+float ora_f16_to_f32(uint16_t h);
+uint16_t ora_f32_to_f16(float f);          /* round to nearest even */
+float ora_bf16_to_f32(uint16_t h);
+uint16_t ora_f32_to_bf16(float f);         /* RNE, NaN kept quiet */
+
+/* ---- Q4_K (144-byte block, 256 weights) ---------------------------------- */
+void ora_q4k_unpack_scale_min(const uint8_t *block, uint8_t sc[8], uint8_t mn[8],
+                              float *d, float *dmin);
+void ora_q4k_dequant_block(const uint8_t *block, float out[256]);
+int ora_q4k_dequant_rowwise(const uint8_t *w, int64_t rows, int64_t cols, float *out);
+int ora_q4k_gemv(const uint8_t *w, const float *x, float *y, int64_t n, int64_t k);
+int ora_q4k_gemv_rows(const uint8_t *w, const float *x, float *y, int64_t n, int64_t k,
+                      int64_t row_begin, int64_t row_end);
+int ora_q4k_gemm_sampled(const uint16_t *a_bf16, const uint8_t *b, int64_t m, int64_t n,
+                         int64_t k, const int64_t *mi, const int64_t *ni, int64_t count,
+                         float *out);
+int ora_q4k_gemm(const uint16_t *a_bf16, const uint8_t *b, float *c, int64_t m, int64_t n,
+                 int64_t k);
+
+/* ---- dense GEMVs --------------------------------------------------------- */
+int ora_f32_gemv(const float *w, const float *x, float *y, int64_t m, int64_t k);
+int ora_f16_gemv(const uint16_t *b, const float *a, float *c, int64_t n, int64_t k,
+                 float alpha);
+int ora_int4g32_gemv(const uint32_t *q, const uint16_t *scales, const float *x, float *y,
+                     int64_t m, int64_t n, int64_t k);
+
+/* ---- elementwise / normalisation ---------------------------------------- */
+int ora_rmsnorm(const float *x, const float *w, float *out, int64_t rows, int64_t h,
+                float eps, int weight_offset);
+int ora_rope_table(float *freq_cis, int64_t max_pos, int64_t head_dim, double base);
+int ora_rope(float *qk, const float *freq_cis, int64_t seq_len, int64_t num_heads,
+             int64_t head_dim, int64_t position_offset);
+int ora_rope_pairs(float *x, const float *cos_t, const float *sin_t, int64_t head_dim,
+                   int64_t num_pairs, int interleaved);
+int ora_gelu(const float *x, float *out, int64_t n);
+int ora_geglu(const float *gate, const float *up, float *out, int64_t n);
+int ora_residual(const float *a, const float *b, float *out, int64_t n);
+int64_t ora_argmax(const float *logits, int64_t n);
+int ora_embed_gather(const uint16_t *table_f16, const int32_t *ids, float *out,
+                     int64_t n_ids, int64_t vocab, int64_t hidden, float scale);
+int ora_kv_write(const float *k_proj, const float *v_proj, uint16_t *k_cache,
+                 uint16_t *v_cache, int64_t num_kv_heads, int64_t max_seq, int64_t head_dim,
+                 int64_t pos, int kv_layout);
+
+/* ---- attention ------------------------------------------------------------
+ * kv_layout 0: [kv_head][pos][dim]   kv_layout 1: [pos][kv_head][dim]
+ * q is [num_heads][head_dim] (decode) or [q_len][num_heads][head_dim] (prefill).
+ */
+int ora_attn_decode(const float *q, const uint16_t *k, const uint16_t *v, float *o,
+                    int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                    int64_t kv_len, int64_t kv_stride, float scale, float softcap,
+                    int64_t sliding_window, int kv_layout);
+int ora_attn_prefill(const float *q, const float *k, const float *v, float *o,
+                     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                     int64_t q_len, int64_t kv_len, int64_t start_pos, float scale,
+                     int causal, int64_t row_begin, int64_t row_end);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,39 @@
+import json
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")
+
+
+@pytest.fixture(scope="session")
+def known_answers():
+    return json.loads((GOLDEN / "reference_known_answers.json").read_text())
+
+
+@pytest.fixture(scope="session")
+def ora():
+    from oracle import oracle as o
+    o.build()
+    return o
+
+
+@pytest.fixture(scope="session")
+def dev():
+    """Initialises the HIP library on device 0; fails loudly if it is not built."""
+    import doe_amd
+    if not doe_amd.LIB_PATH.exists():
+        pytest.fail(f"{doe_amd.LIB_PATH} is missing: build it before running GPU tests")
+    doe_amd.init(0)
+    info = doe_amd.device_info()
+    print(f"[dev] {info}", flush=True)
+    return doe_amd

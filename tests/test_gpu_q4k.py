@@ -1,0 +1,152 @@
+"""GPU parity of the Q4_K dequant (bit-exact) and decode GEMV (rel-L2 <= 1e-3)
+kernels against the CPU oracle, through the C ABI."""
+import numpy as np
+import pytest
+
+from doe_amd import DeviceBuffer, DoeError, Graph, Stream, ops, q4k
+
+pytestmark = pytest.mark.gpu
+
+GEMV_REL_L2 = 1e-3  # north-star tolerance for GEMV outputs (fp32 accumulate)
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def _extreme_q4k(rng, n, k):
+    """Random blocks whose d/dmin run over the whole f16 range incl. subnormals."""
+    w = q4k.random_q4k(rng, n, k).reshape(-1, 144).copy()
+    vals = np.array([2.0 ** -24, 1023 * 2.0 ** -24, 2.0 ** -14, 0.0123, 0.5, 3.0, 1000.0, 65504.0],
+                    np.float16)
+    d = vals[rng.integers(0, len(vals), w.shape[0])]
+    dmin = vals[rng.integers(0, len(vals), w.shape[0])]
+    w[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    w[:, 2:4] = dmin.view(np.uint8).reshape(-1, 2)
+    return w.reshape(n, -1)
+
+
+@pytest.mark.parametrize("n,k", [(1, 256), (7, 300), (33, 2304), (64, 9216), (5, 5376)])
+def test_dequant_bit_exact(dev, ora, n, k):
+    rng = np.random.default_rng(100 + n)
+    w = _extreme_q4k(rng, n, k)
+    dw = DeviceBuffer.from_array(w)
+    out = DeviceBuffer.empty((n, k), np.float32)
+    ops.dequant_q4k(dw, out, n, k)
+    got = out.download()
+    want = ora.q4k_dequant_rowwise(w, n, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_reference_tail_fixture(dev, known_answers):
+    e = known_answers["q4k_rowwise_tail"]
+    blocks = [q4k.pack_blocks(np.array([1.0]), np.array([0.0]), np.ones((1, 8)), np.zeros((1, 8)),
+                              np.full((1, 256), f))[0] for f in e["block_quant_fill"]]
+    raw = np.concatenate(blocks)
+    rows, cols = e["shape"]
+    out = DeviceBuffer.empty((rows, cols), np.float32)
+    ops.dequant_q4k(DeviceBuffer.from_array(raw), out, rows, cols)
+    want = np.concatenate([np.full(c, v, np.float32) for v, c in e["expected_runs"]])
+    assert np.array_equal(out.download().reshape(-1), want)
+
+
+def _gemv(w, x, n, k, stream=None):
+    dw = DeviceBuffer.from_array(w)
+    dx = DeviceBuffer.from_array(x.astype(np.float32))
+    dy = DeviceBuffer.empty((n,), np.float32)
+    ops.matmul_q4k(dw, dx, dy, n, k, stream)
+    if stream is not None:
+        stream.synchronize()
+    return dy.download()
+
+
+# config-0 shape, every 2B-class projection shape, 31B prefill K, tails
+GEMV_SHAPES = [(9216, 2304), (2048, 2304), (1024, 2304), (2304, 2048), (2304, 9216),
+               (21504 // 16, 5376), (1, 256), (3, 300), (37, 64 * 3 + 5), (1000, 1024)]
+
+
+@pytest.mark.parametrize("n,k", GEMV_SHAPES)
+def test_gemv_matches_oracle(dev, ora, n, k):
+    rng = np.random.default_rng(n * 7 + k)
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    got = _gemv(w, x, n, k)
+    want = ora.q4k_gemv(w, x, n, k)
+    err = rel_l2(got, want)
+    print(f"[gemv {n}x{k}] rel_l2={err:.3e}", flush=True)
+    assert err <= GEMV_REL_L2
+    # The hi/lo activation split keeps the GEMV near f32 quality.
+    assert err < 1e-5
+
+
+def test_gemv_reference_block_one_hot(dev, known_answers):
+    # The reference's known-answer block (test_doppler_rdrr_q4k.py:63-85)
+    # through the GEMV: a one-hot activation picks out one dequantized value.
+    e = known_answers["q4k_scale_min_block"]
+    blk = q4k.pack_blocks(np.array([e["d"]]), np.array([e["dmin"]]), np.array([e["scale_bits"]]),
+                          np.array([e["min_bits"]]), np.array([[i % 16 for i in range(256)]]))
+    for idx, want in e["expected_values"].items():
+        x = np.zeros(256, np.float32)
+        x[int(idx)] = 1.0
+        assert _gemv(blk, x, 1, 256)[0] == np.float32(want)
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-8, 1e6, 1e30])
+def test_gemv_activation_range(dev, ora, scale):
+    rng = np.random.default_rng(7)
+    n, k = 256, 2304
+    w = q4k.random_q4k(rng, n, k)
+    x = (rng.standard_normal(k) * scale).astype(np.float32)
+    assert rel_l2(_gemv(w, x, n, k), ora.q4k_gemv(w, x, n, k)) < 1e-5
+
+
+def test_gemv_extreme_scales(dev, ora):
+    rng = np.random.default_rng(8)
+    n, k = 128, 1024
+    w = _extreme_q4k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    assert rel_l2(_gemv(w, x, n, k), ora.q4k_gemv(w, x, n, k)) < 1e-5
+
+
+def test_gemv_zero_k_and_zero_n(dev):
+    dy = DeviceBuffer.from_array(np.full(4, 7.0, np.float32))
+    ops.matmul_q4k(DeviceBuffer(0), DeviceBuffer(0), dy, 4, 0)
+    assert dy.download().tolist() == [0.0] * 4
+    ops.matmul_q4k(DeviceBuffer(0), DeviceBuffer(16), DeviceBuffer(0), 0, 4)
+
+
+def test_gemv_stream_and_graph_replays(dev, ora):
+    rng = np.random.default_rng(9)
+    n, k = 2048, 2304
+    w = q4k.random_q4k(rng, n, k)
+    dw = DeviceBuffer.from_array(w)
+    dx = DeviceBuffer.empty((k,), np.float32)
+    dy = DeviceBuffer.empty((n,), np.float32)
+    s = Stream()
+    g = Graph.capture(s, lambda: ops.matmul_q4k(dw, dx, dy, n, k, s))
+    for rep in range(4):
+        x = rng.standard_normal(k).astype(np.float32)
+        dx.upload(x)
+        g.launch(s)
+        s.synchronize()
+        assert rel_l2(dy.download(), ora.q4k_gemv(w, x, n, k)) < 1e-5, rep
+    g.destroy()
+    s.destroy()
+
+
+def test_gemv_rejects_misaligned_weight(dev):
+    dw = DeviceBuffer(144 * 2 + 16)
+    dx = DeviceBuffer.empty((256,), np.float32)
+    dy = DeviceBuffer.empty((2,), np.float32)
+    import ctypes as C
+    from doe_amd import _lib
+    with pytest.raises(DoeError) as ei:
+        _lib.call("doe_q4k_gemv", C.c_void_p(dw.ptr + 8), C.c_void_p(dx.ptr), C.c_void_p(dy.ptr), 2, 256,
+                  C.c_void_p(None))
+    assert ei.value.status == -1
+    with pytest.raises(DoeError) as ei:
+        _lib.call("doe_q4k_gemv", C.c_void_p(dw.ptr), C.c_void_p(dx.ptr), C.c_void_p(dy.ptr), 2, 70000,
+                  C.c_void_p(None))
+    assert ei.value.status == -4
