@@ -28,6 +28,7 @@
 
 #include <math.h>
 #include <stdlib.h>
+#include <string.h>
 
 namespace {
 
@@ -38,6 +39,14 @@ constexpr int kLdsChunkDwords = 36;  // 64 halves + 16 bytes pad: conflict-free 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, a), __builtin_bit_cast(half2v, b), c,
                                   false);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (weights are read exactly once).
+__device__ __forceinline__ uint4 load_stream16(const uint8_t *p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 __device__ __forceinline__ uint32_t pack_half2(_Float16 lo, _Float16 hi) {
@@ -97,14 +106,50 @@ __global__ void q4k_dequant_kernel(const uint8_t *__restrict__ w, float *__restr
 // ---------------------------------------------------------------------------
 // GEMV.
 // LDS layout (dynamic): xh[nchunk*36] dwords, xl[nchunk*36] dwords (f16 pairs
-// of x_hi / x_lo), sx[2*nchunk] f32 sub-block sums, red[rows_wg*nchunk] f32
-// partials, wmax[16] f32.
+// of x_hi / x_lo), sx[2*nchunk] f32 sub-block sums, sig[nchunk] i32 chunk
+// scale exponents, red[rows_wg*nchunk] f32 partials.
 // Within a chunk, dwords 0..15 hold the low sub-block and 16..31 the high one;
 // each 4-element group (e0,e1,e2,e3) is stored as pairs (e0,e2), (e1,e3) so
 // that `D & 0x000F000F` (bytes 0 and 2 of a nibble dword) meets (e0,e2) and
 // `(D >> 8) & 0x000F000F` meets (e1,e3).
+// Each chunk's 64 activations are scaled by their own power of two (max|x|
+// of the chunk near 2^14); the chunk's partial is scaled back exactly.
 // ---------------------------------------------------------------------------
-template <int R>
+// Stages activation quad `qd` (elements 4qd..4qd+3): sub-block sum, chunk
+// scale exponent, and the scaled x_hi / x_lo halves in dot2 pair order.
+__device__ __forceinline__ void stage_quad(int qd, bool valid, const float *v, uint32_t *xh,
+                                           uint32_t *xl, float *sx, int *sig) {
+    float s = (v[0] + v[1]) + (v[2] + v[3]);
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 8, 64));
+    int sigma = 0;
+    if (amax > 0.0f && amax <= 3.0e38f) {
+        sigma = 14 - __builtin_amdgcn_frexp_expf(amax);
+        sigma = sigma < -100 ? -100 : (sigma > 100 ? 100 : sigma);
+    }
+    const float xs = __builtin_amdgcn_ldexpf(1.0f, sigma);
+    if (!valid) return;
+    if ((qd & 7) == 0) sx[qd >> 3] = s;
+    if ((qd & 15) == 0) sig[qd >> 4] = sigma;
+    _Float16 hi[4], lo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float t = v[j] * xs;
+        hi[j] = (_Float16)t;
+        lo[j] = (_Float16)(t - (float)hi[j]);
+    }
+    const int off = (qd >> 4) * kLdsChunkDwords + 2 * (qd & 15);
+    *reinterpret_cast<uint2 *>(xh + off) = make_uint2(pack_half2(hi[0], hi[2]), pack_half2(hi[1], hi[3]));
+    *reinterpret_cast<uint2 *>(xl + off) = make_uint2(pack_half2(lo[0], lo[2]), pack_half2(lo[1], lo[3]));
+}
+
+template <int R, int Q>
 __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restrict__ w,
                                                         const float *__restrict__ x,
                                                         float *__restrict__ y, int n, int k, int nb,
@@ -113,85 +158,69 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
     uint32_t *xh = smem;
     uint32_t *xl = xh + nchunk * kLdsChunkDwords;
     float *sx = reinterpret_cast<float *>(xl + nchunk * kLdsChunkDwords);
-    float *red = sx + 2 * nchunk;
+    int *sig = reinterpret_cast<int *>(sx + 2 * nchunk);
+    float *red = reinterpret_cast<float *>(sig + nchunk);
     const int rows_wg = rowslots * R;
-    float *wmax = red + rows_wg * nchunk;
 
     const int tid = threadIdx.x;
     const int nthreads = blockDim.x;
     const int nquads = nchunk * 16;
+    const int active = rowslots * nchunk;
+    const bool worker = tid < active;
+    const int chunk = worker ? tid % nchunk : 0;
+    const int slot = worker ? tid / nchunk : 0;
+    const int blk = chunk >> 2, c4 = chunk & 3;
+    const int row0 = blockIdx.x * rows_wg + slot;
 
-    // Phase 1: max |x| over the (zero padded) activation.
-    float amax = 0.0f;
-    for (int qd = tid; qd < nquads; qd += nthreads) {
-        const int e = qd * 4;
+    // Phase 1: this thread's activation quads go out first (vector-memory
+    // returns are in order, so staging never waits on the weight stream),
+    // then its weight bytes.  Each thread stages Q quads in registers; the
+    // host picks Q >= nquads / nthreads when it can.
+    // Loads are unconditional (indices clamped into range, results masked
+    // later) so they stay in straight-line code and the compiler can wait on
+    // the activation without waiting on the weights.
+    float xv[Q][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(e + j < k ? x[e + j] : 0.0f));
+    for (int it = 0; it < Q; ++it) {
+        const int e = (tid + it * nthreads) * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[it][j] = x[min(e + j, k - 1)];  // masked when staged
     }
-    amax = wave_max(amax);
-    if ((tid & 63) == 0) wmax[tid >> 6] = amax;
-    __syncthreads();
-    float gmax = 0.0f;
-    for (int i = 0; i < (nthreads >> 6); ++i) gmax = fmaxf(gmax, wmax[i]);
-    int sigma = 0;
-    if (gmax > 0.0f && gmax <= 3.0e38f) {
-        int e2;
-        frexpf(gmax, &e2);
-        sigma = 14 - e2;
-        sigma = sigma < -100 ? -100 : (sigma > 100 ? 100 : sigma);
+    // keep the activation loads ahead of the weight loads in issue order
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 hdr[R], qa[R], qb[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r * rowslots, n - 1);
+        const uint8_t *p = w + ((size_t)row * nb + blk) * DOE_Q4K_BLOCK_BYTES;
+        hdr[r] = load_stream16(p);
+        qa[r] = load_stream16(p + 16 + 32 * c4);
+        qb[r] = load_stream16(p + 32 + 32 * c4);
     }
-    const float xs = ldexpf(1.0f, sigma);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // Phase 2: stage x_hi / x_lo as f16 pairs and the sub-block sums.
-    for (int qd = tid; qd < nquads; qd += nthreads) {
-        const int e = qd * 4;
+    // Phase 2: stage the activation once per workgroup.  The 16 quads of a
+    // chunk are 16 consecutive lanes and the 8 quads of a sub-block 8 lanes
+    // (nthreads % 64 == 0, nquads % 16 == 0), so every shuffle group below
+    // is either fully active or fully idle.
+#pragma unroll
+    for (int it = 0; it < Q; ++it) {
+        const int qd = tid + it * nthreads;
         float v[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = e + j < k ? x[e + j] : 0.0f;
-        // The 8 quads of one sub-block are 8 consecutive lanes (nthreads % 64 == 0).
-        float s = (v[0] + v[1]) + (v[2] + v[3]);
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
-        if ((qd & 7) == 0) sx[qd >> 3] = s;
-        _Float16 hi[4], lo[4];
+        for (int j = 0; j < 4; ++j) v[j] = (qd * 4 + j < k) ? xv[it][j] : 0.0f;
+        stage_quad(qd, qd < nquads, v, xh, xl, sx, sig);
+    }
+    for (int qd = tid + Q * nthreads; qd < nquads; qd += nthreads) {
+        float v[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float t = v[j] * xs;
-            hi[j] = (_Float16)t;
-            lo[j] = (_Float16)(t - (float)hi[j]);
-        }
-        const int chunk = qd >> 4;
-        const int off = chunk * kLdsChunkDwords + 2 * (qd & 15);
-        *reinterpret_cast<uint2 *>(xh + off) = make_uint2(pack_half2(hi[0], hi[2]), pack_half2(hi[1], hi[3]));
-        *reinterpret_cast<uint2 *>(xl + off) = make_uint2(pack_half2(lo[0], lo[2]), pack_half2(lo[1], lo[3]));
+        for (int j = 0; j < 4; ++j) v[j] = (qd * 4 + j < k) ? x[qd * 4 + j] : 0.0f;
+        stage_quad(qd, true, v, xh, xl, sx, sig);
     }
     __syncthreads();
 
-    // Phase 3: stream the weights.
-    const int active = rowslots * nchunk;
-    if (tid < active) {
-        const int chunk = tid % nchunk;
-        const int slot = tid / nchunk;
-        const int blk = chunk >> 2, c4 = chunk & 3;
-        const int row0 = blockIdx.x * rows_wg + slot;
-
-        uint4 hdr[R], qa[R], qb[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int row = row0 + r * rowslots;
-            if (row < n) {
-                const uint8_t *p = w + ((size_t)row * nb + blk) * DOE_Q4K_BLOCK_BYTES;
-                hdr[r] = *reinterpret_cast<const uint4 *>(p);
-                qa[r] = *reinterpret_cast<const uint4 *>(p + 16 + 32 * c4);
-                qb[r] = *reinterpret_cast<const uint4 *>(p + 32 + 32 * c4);
-            } else {
-                hdr[r] = make_uint4(0, 0, 0, 0);
-                qa[r] = make_uint4(0, 0, 0, 0);
-                qb[r] = make_uint4(0, 0, 0, 0);
-            }
-        }
-
+    // Phase 3: dot products of this thread's chunk for its R rows.
+    if (worker) {
         uint32_t xhv[32], xlv[32];
         const uint4 *xh4 = reinterpret_cast<const uint4 *>(xh + chunk * kLdsChunkDwords);
         const uint4 *xl4 = reinterpret_cast<const uint4 *>(xl + chunk * kLdsChunkDwords);
@@ -202,7 +231,9 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
             xlv[4 * i] = b.x; xlv[4 * i + 1] = b.y; xlv[4 * i + 2] = b.z; xlv[4 * i + 3] = b.w;
         }
         const float sxl = sx[2 * chunk], sxh = sx[2 * chunk + 1];
-        const float f_lo = ldexpf(1.0f, 24 - sigma), f_hi = ldexpf(1.0f, 20 - sigma);
+        const int sigma = sig[chunk];
+        const float f_lo = __builtin_amdgcn_ldexpf(1.0f, 24 - sigma);
+        const float f_hi = __builtin_amdgcn_ldexpf(1.0f, 20 - sigma);
 
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -250,34 +281,52 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
     }
 }
 
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
+// Tunable launch-shape overrides (0 = automatic), set via doe_tune_set.
+int g_tune_rowslots = 0;
+int g_tune_rows = 0;
 
 // Launch shape for the GEMV: rowslots * nchunk threads (rounded up to whole
-// waves), rows per thread R.
+// waves) and R rows per thread.  The automatic choice spreads the rows over
+// the CUs in whole workgroups: rows_wg ~ rows per CU / workgroups per CU.
 struct GemvShape {
     int rowslots, rows_per_thread, threads;
     size_t lds;
 };
 
-GemvShape gemv_shape(int nchunk) {
-    static const int env_slots = env_int("DOE_Q4K_ROWSLOTS", 0);
-    static const int env_r = env_int("DOE_Q4K_ROWS", 0);
+size_t gemv_lds_bytes(int nchunk, int rows_wg) {
+    return (size_t)nchunk * kLdsChunkDwords * 4 * 2 + (size_t)2 * nchunk * 4 + (size_t)nchunk * 4 +
+           (size_t)rows_wg * nchunk * 4;
+}
+
+GemvShape gemv_shape(int64_t n, int nchunk, int num_cus) {
+    // Measured on MI355X (graph replays over 64 rotating weight copies): one
+    // row per thread and all of a CU's rows in one workgroup while that stays
+    // near 10 waves, otherwise two workgroups per CU; long rows (k >= 6144)
+    // take two rows per thread to amortise the activation staging.
     GemvShape s;
     int max_slots = 1024 / nchunk;
-    int slots = env_slots > 0 ? env_slots : (576 + nchunk / 2) / nchunk;
-    if (slots < 1) slots = 1;
+    if (max_slots < 1) max_slots = 1;
+    int r = nchunk >= 96 ? 2 : 1;
+    if (g_tune_rows == 1 || g_tune_rows == 2 || g_tune_rows == 4) r = g_tune_rows;
+    int slots;
+    if (g_tune_rowslots > 0) {
+        slots = g_tune_rowslots;
+    } else {
+        const int64_t rows_per_cu = (n + num_cus - 1) / num_cus;
+        int64_t want = (rows_per_cu + r - 1) / r;
+        if (want * nchunk > 640 && nchunk < 96) want = (want + 1) / 2;
+        slots = (int)(want < 4 ? 4 : want);
+    }
     if (slots > max_slots) slots = max_slots;
+    if (slots < 1) slots = 1;
     s.rowslots = slots;
-    s.rows_per_thread = (env_r == 1 || env_r == 2 || env_r == 4) ? env_r : 2;
+    s.rows_per_thread = r;
     s.threads = ((slots * nchunk + 63) / 64) * 64;
-    const int rows_wg = slots * s.rows_per_thread;
-    s.lds = (size_t)nchunk * kLdsChunkDwords * 4 * 2 + (size_t)2 * nchunk * 4 +
-            (size_t)rows_wg * nchunk * 4 + 16 * 4;
+    s.lds = gemv_lds_bytes(nchunk, slots * r);
     return s;
 }
+
+int g_num_cus = 0;
 
 }  // namespace
 
@@ -322,30 +371,50 @@ int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
                 (long long)k);
     const int nb = (int)((k + 255) / 256);
     const int nchunk = (int)((k + 63) / 64);
-    const GemvShape s = gemv_shape(nchunk);
+    if (g_num_cus == 0) {
+        int dev = 0, cus = 0;
+        DOE_HIP_CHECK(hipGetDevice(&dev));
+        DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        g_num_cus = cus > 0 ? cus : 256;
+    }
+    const GemvShape s = gemv_shape(n, nchunk, g_num_cus);
     DOE_REQUIRE(s.lds <= 64 * 1024, DOE_E_UNSUPPORTED, "k=%lld needs %zu bytes of LDS",
                 (long long)k, s.lds);
     const int rows_wg = s.rowslots * s.rows_per_thread;
     const unsigned grid = (unsigned)((n + rows_wg - 1) / rows_wg);
     const hipStream_t st = (hipStream_t)stream;
-    switch (s.rows_per_thread) {
-        case 1:
-            hipLaunchKernelGGL(q4k_gemv_kernel<1>, dim3(grid), dim3(s.threads), s.lds, st,
-                               (const uint8_t *)weight_q4k, activation, output, (int)n, (int)k, nb,
-                               nchunk, s.rowslots);
-            break;
-        case 4:
-            hipLaunchKernelGGL(q4k_gemv_kernel<4>, dim3(grid), dim3(s.threads), s.lds, st,
-                               (const uint8_t *)weight_q4k, activation, output, (int)n, (int)k, nb,
-                               nchunk, s.rowslots);
-            break;
-        default:
-            hipLaunchKernelGGL(q4k_gemv_kernel<2>, dim3(grid), dim3(s.threads), s.lds, st,
-                               (const uint8_t *)weight_q4k, activation, output, (int)n, (int)k, nb,
-                               nchunk, s.rowslots);
-            break;
+    const int nquads = nchunk * 16;
+    const int q = (nquads + s.threads - 1) / s.threads;
+    const int qsel = q <= 1 ? 1 : (q <= 2 ? 2 : 4);
+    const uint8_t *wp = (const uint8_t *)weight_q4k;
+#define DOE_GEMV_LAUNCH(RR, QQ)                                                                 \
+    hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ>), dim3(grid), dim3(s.threads), s.lds, st, wp, \
+                       activation, output, (int)n, (int)k, nb, nchunk, s.rowslots)
+    switch (s.rows_per_thread * 8 + qsel) {
+        case 1 * 8 + 1: DOE_GEMV_LAUNCH(1, 1); break;
+        case 1 * 8 + 2: DOE_GEMV_LAUNCH(1, 2); break;
+        case 1 * 8 + 4: DOE_GEMV_LAUNCH(1, 4); break;
+        case 2 * 8 + 1: DOE_GEMV_LAUNCH(2, 1); break;
+        case 2 * 8 + 2: DOE_GEMV_LAUNCH(2, 2); break;
+        case 2 * 8 + 4: DOE_GEMV_LAUNCH(2, 4); break;
+        case 4 * 8 + 1: DOE_GEMV_LAUNCH(4, 1); break;
+        case 4 * 8 + 2: DOE_GEMV_LAUNCH(4, 2); break;
+        default: DOE_GEMV_LAUNCH(4, 4); break;
     }
+#undef DOE_GEMV_LAUNCH
     DOE_LAUNCH_CHECK("q4k_gemv_kernel");
+    return DOE_OK;
+}
+
+int doe_tune_set(const char *key, int value) {
+    DOE_REQUIRE(key, DOE_E_INVALID, "null key");
+    if (!strcmp(key, "q4k_gemv.rowslots")) {
+        g_tune_rowslots = value;
+    } else if (!strcmp(key, "q4k_gemv.rows")) {
+        g_tune_rows = value;
+    } else {
+        return doe::set_error(DOE_E_INVALID, "unknown tuning key '%s'", key);
+    }
     return DOE_OK;
 }
 

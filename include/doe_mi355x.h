@@ -104,6 +104,13 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
 int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
                  int64_t n, int64_t k, doe_stream_t stream);
 
+/* ---- tuning ----------------------------------------------------------------
+ * Overrides a kernel launch-shape choice (0 restores the automatic choice).
+ * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows".  No reference counterpart:
+ * the reference fixes workgroup shapes per WGSL override constant
+ * (lm_head_gemv.wgsl:168-169 MULTICOL_* overrides). */
+int doe_tune_set(const char *key, int value);
+
 #ifdef __cplusplus
 }
 #endif
