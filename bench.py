@@ -117,6 +117,73 @@ def bench_gemv(args, doe):
     }
 
 
+ATT_HQ, ATT_HKV, ATT_D, ATT_T = 8, 4, 256, 4096
+ATT_BYTES = 2 * ATT_HKV * ATT_T * ATT_D * 2 + 2 * ATT_HQ * ATT_D * 2  # K + V + q + o = 16,785,408
+
+
+def bench_attention(args, doe):
+    """GQA decode attention (8 q / 4 kv heads, head_dim 256, context 4096, f16
+    q/K/V, f16 out) over rotating KV-cache copies; HIP events around graph
+    replays of back-to-back calls."""
+    from doe_amd import DeviceBuffer, Event, Graph, Stream, ops
+
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((1, ATT_HQ, ATT_D)).astype(np.float16)
+    k = rng.standard_normal((1, ATT_HKV, ATT_T, ATT_D)).astype(np.float16)
+    v = rng.standard_normal((1, ATT_HKV, ATT_T, ATT_D)).astype(np.float16)
+    ncopy = args.attn_copies
+    dq = DeviceBuffer.from_array(q)
+    ks, vs = [DeviceBuffer.from_array(k)], [DeviceBuffer.from_array(v)]
+    for _ in range(ncopy - 1):
+        kb, vb = DeviceBuffer(k.nbytes), DeviceBuffer(v.nbytes)
+        kb.copy_from(ks[0])
+        vb.copy_from(vs[0])
+        ks.append(kb)
+        vs.append(vb)
+    out = DeviceBuffer.empty((1, ATT_HQ, ATT_D), np.float16)
+    doe.synchronize()
+    s = Stream()
+
+    def body():
+        for kb, vb in zip(ks, vs):
+            ops.attention(dq, kb, vb, out, batch=1, num_heads=ATT_HQ, num_kv_heads=ATT_HKV, head_dim=ATT_D,
+                          kv_len=ATT_T, kv_stride=ATT_T, scale=1.0 / 16, q_f16=True, out_f16=True, stream=s)
+
+    body()  # first call outside capture allocates the split workspace
+    s.synchronize()
+    graph = Graph.capture(s, body)
+    graph.launch(s)
+    s.synchronize()
+    reps = max(1, -(-args.attn_steps // ncopy))
+    e0, e1 = Event(), Event()
+    e0.record(s)
+    for _ in range(reps):
+        graph.launch(s)
+    e1.record(s)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / (reps * ncopy)
+    from oracle import oracle as ora
+
+    want = ora.attn_decode(q[0].astype(np.float32), k[0], v[0], ATT_HQ, ATT_HKV, ATT_D, ATT_T, ATT_T, 1.0 / 16)
+    got = out.download()[0].astype(np.float64)
+    rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    graph.destroy()
+    s.destroy()
+    for b in ks + vs:
+        b.free()
+    gbs = ATT_BYTES / (ms * 1e-3) / 1e9
+    log(f"attention: {ms * 1e3:.2f} us/call, {gbs:.0f} GB/s, rel_l2 {rel:.2e}")
+    return {
+        "workload": f"GQA decode attention Hq={ATT_HQ} Hkv={ATT_HKV} D={ATT_D} T={ATT_T}, f16 q/K/V/out, "
+                    f"{ncopy} rotating KV copies",
+        "us_per_call": round(ms * 1e3, 3),
+        "bytes_per_call": ATT_BYTES,
+        "achieved_gbs": round(gbs, 1),
+        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "rel_l2_vs_oracle": rel,
+    }
+
+
 def traffic_bytes(summary: str):
     """HBM bytes per launch recorded in a committed rocprofv3 summary
     (line `traffic_bytes_per_launch: <int>`), or None."""
@@ -159,6 +226,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1280)
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--copies", type=int, default=64)
+    ap.add_argument("--attn-copies", type=int, default=48)
+    ap.add_argument("--attn-steps", type=int, default=480)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -180,6 +249,7 @@ def main() -> int:
     log(f"device {info}")
 
     g = bench_gemv(args, doe_amd)
+    att = bench_attention(args, doe_amd)
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of the single-threaded oracle")
@@ -216,6 +286,7 @@ def main() -> int:
             "kernel_us": round(g["kernel_ms"] * 1e3, 3),
         },
         "cpu_baseline": cpu,
+        "attention_decode": att,
     }
     print(json.dumps(out), flush=True)
     return 0

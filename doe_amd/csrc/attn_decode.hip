@@ -1,0 +1,494 @@
+// attn_decode.hip -- GQA decode attention over an f16 KV cache for gfx950.
+//
+// Semantics (runtime/zig/tests/tsir/real/attention_head256_f16kv/
+// attention_head256_f16kv.wgsl:46-49, 72-267 and the two-pass softmax of
+// runtime/zig/src/tsir/reference_interpreter.zig:1175-1265): for every query
+// head h, kv head = h / (Hq / Hkv); the query sits at position kv_len - 1;
+// keys [min_key, kv_len) are visible, min_key = kv_len - window when a sliding
+// window is set and kv_len - 1 >= window; s = (q . k) * scale, optionally
+// softcapped tanh(s / cap) * cap; o = softmax(s) V.
+//
+// Work decomposition: grid (splits, kv heads, batch), 256 threads.  A
+// workgroup owns one kv head of one sequence and a contiguous range of
+// 16-position blocks; wave w takes blocks w, w+4, ...  All G = Hq/Hkv query
+// heads of the group share every K/V byte the workgroup reads.
+//   * q.K^T: v_mfma_f32_16x16x32_f16 with A = the G query rows (rows >= G are
+//     zero; an f32 query is split into f16 hi + lo rows accumulated by a second
+//     MFMA) and B = 16 key rows (lane l reads 16 contiguous bytes of key
+//     l % 16).  Lane l then holds the scores of heads 4*(l/16)+i, i < 4, for
+//     position l % 16.
+//   * online softmax per head inside the wave (16-lane max / sum reductions).
+//   * P.V on the VALU: lane l owns dims l*D/64 .. of every head; the block's
+//     probabilities are broadcast through LDS into f32 FMAs against the f16
+//     V row.  Each wave prefetches its next block while computing this one.
+//   * the four waves combine through LDS; with more than one split, each
+//     workgroup writes (m, l, o) partials to the workspace and a second,
+//     small kernel combines them (a kernel boundary orders the partials
+//     across XCDs far cheaper than per-workgroup release fences, which write
+//     back the L2).
+#include "common.h"
+
+#include <math.h>
+#include <mutex>
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+struct AttnArgs {
+    const void *q;
+    const uint16_t *k;
+    const uint16_t *v;
+    void *out;
+    const int32_t *kv_len_dev;
+    float *ws_o;       // [B*Hq][S][D] partial outputs
+    float *ws_ml;      // [B*Hq][S][2] partial (max, sum)
+    int q_f16, out_f16;
+    int num_heads, num_kv_heads, kv_len, kv_stride, kv_layout, splits;
+    float scale_log2e;  // scale * log2(e)
+    float softcap;
+    int sliding_window;
+};
+
+constexpr int kMaxSplits = 512;
+constexpr int kWaves = 4;
+
+// K fragment and V rows of one 16-position block, as loaded by one lane.
+template <int D>
+struct KVBlock {
+    h8 kf[D / 32];
+    _Float16 vv[16][D / 64];
+};
+
+template <int D>
+__device__ __forceinline__ void load_block(KVBlock<D> &blk, const uint16_t *kb, const uint16_t *vb,
+                                           int p0, int kv_len, size_t pos_stride, int lane) {
+    constexpr int KSTEPS = D / 32, DPL = D / 64;
+    // key p0 + lane % 16, dims 8 (lane / 16) + 32 s (clamped into range, masked later)
+    const uint16_t *krow = kb + (size_t)min(p0 + (lane & 15), kv_len - 1) * pos_stride + 8 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) blk.kf[s] = *reinterpret_cast<const h8 *>(krow + 32 * s);
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+        const _Float16 *vrow = reinterpret_cast<const _Float16 *>(
+            vb + (size_t)min(p0 + n, kv_len - 1) * pos_stride + lane * DPL);
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
+    }
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+    constexpr int KSTEPS = D / 32;  // MFMA k-steps over the head dimension
+    constexpr int DPL = D / 64;     // P.V dims per lane
+    constexpr int G4 = (G + 3) / 4; // 4-head groups of the probability broadcast
+    constexpr float kLog2e = 1.4426950408889634f;
+    // The query fragments are dead once the block loop ends; the wave
+    // combine and the cross-split combine reuse their LDS.
+    __shared__ union {
+        h8 qfrag[2][KSTEPS][64];
+        float wo[kWaves][G][D];
+    } sm;
+    __shared__ float4 pb[kWaves][17][G4];  // per wave: probabilities [position][head], row 16: max/sum
+    __shared__ float wm[kWaves][G], wl[kWaves][G];
+
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hq0 = kvh * G;  // first query head of this group
+
+    int kv_len = a.kv_len_dev ? a.kv_len_dev[0] : a.kv_len;
+    kv_len = kv_len < 0 ? 0 : (kv_len > a.kv_stride ? a.kv_stride : kv_len);
+    const int min_key = (a.sliding_window > 0 && kv_len - 1 >= a.sliding_window)
+                            ? kv_len - a.sliding_window : 0;
+    const int nblk = (kv_len + 15) >> 4;
+    const int bps = (nblk + a.splits - 1) / a.splits;
+    const int blk_begin = split * bps;
+    const int blk_end = min(nblk, blk_begin + bps);
+
+    const size_t pos_stride = a.kv_layout == 0 ? (size_t)D : (size_t)a.num_kv_heads * D;
+    const size_t kv_base = a.kv_layout == 0
+                               ? ((size_t)b * a.num_kv_heads + kvh) * a.kv_stride * D
+                               : (size_t)b * a.kv_stride * a.num_kv_heads * D + (size_t)kvh * D;
+    const uint16_t *kb = a.k + kv_base;
+    const uint16_t *vb = a.v + kv_base;
+
+    // First block's loads go out before the query staging.
+    KVBlock<D> cur;
+    int blk = blk_begin + wave;
+    if (blk < blk_end) load_block<D>(cur, kb, vb, blk * 16, kv_len, pos_stride, lane);
+
+    // Query fragments (A operand) into LDS: lane l holds row l % 16 (query
+    // head hq0 + l % 16 when < G), dims 32 s + 8 (l / 16) .. + 7.
+    for (int idx = tid; idx < KSTEPS * 64; idx += 256) {
+        const int s = idx >> 6, l = idx & 63;
+        const int m = l & 15;
+        h8 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float v = 0.0f;
+            if (m < G) {
+                const size_t qi = ((size_t)b * a.num_heads + hq0 + m) * D + 32 * s + 8 * (l >> 4) + j;
+                v = a.q_f16 ? (float)reinterpret_cast<const _Float16 *>(a.q)[qi]
+                            : reinterpret_cast<const float *>(a.q)[qi];
+            }
+            hi[j] = (_Float16)v;
+            lo[j] = (_Float16)(v - (float)hi[j]);
+        }
+        sm.qfrag[0][s][l] = hi;
+        sm.qfrag[1][s][l] = lo;
+    }
+    __syncthreads();
+
+    float o[G][DPL];
+    float mrow[G], lrow[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        mrow[h] = -INFINITY;
+        lrow[h] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) o[h][d] = 0.0f;
+    }
+    // running max of the heads whose scores this lane holds (4*(lane/16)+i)
+    float mlane[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    const int grp = lane >> 4;
+    float *pbw = reinterpret_cast<float *>(&pb[wave][0][0]);  // [17][G4*4]
+
+    for (; blk < blk_end; blk += kWaves) {
+        // Prefetch the next block of this wave (clamped to the current one at
+        // the end, which then hits in cache) while this one is computed.
+        KVBlock<D> nxt;
+        const int nb = blk + kWaves < blk_end ? blk + kWaves : blk;
+        load_block<D>(nxt, kb, vb, nb * 16, kv_len, pos_stride, lane);
+
+        const int p0 = blk * 16;
+        const int pk = p0 + (lane & 15);
+        f4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(sm.qfrag[0][s][lane], cur.kf[s], c, 0, 0, 0);
+        if (!a.q_f16) {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s)
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(sm.qfrag[1][s][lane], cur.kf[s], c, 0, 0, 0);
+        }
+        const bool valid = pk < kv_len && pk >= min_key;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float s = c[i];
+            if (a.softcap > 0.0f) {
+                s = tanhf(s * (a.scale_log2e / kLog2e) / a.softcap) * a.softcap * kLog2e;
+            } else {
+                s *= a.scale_log2e;
+            }
+            const float sc = valid ? s : -INFINITY;  // score in log2 units
+            float m = sc;
+            m = fmaxf(m, __shfl_xor(m, 1, 16));
+            m = fmaxf(m, __shfl_xor(m, 2, 16));
+            m = fmaxf(m, __shfl_xor(m, 4, 16));
+            m = fmaxf(m, __shfl_xor(m, 8, 16));
+            const float bm = fmaxf(mlane[i], m);
+            mlane[i] = bm;
+            const float p = valid ? exp2f(sc - bm) : 0.0f;
+            float t = p;
+            t += __shfl_xor(t, 1, 16);
+            t += __shfl_xor(t, 2, 16);
+            t += __shfl_xor(t, 4, 16);
+            t += __shfl_xor(t, 8, 16);
+            const int h = 4 * grp + i;
+            if (h < G) {
+                pbw[(lane & 15) * (G4 * 4) + h] = p;
+                if ((lane & 15) == 0) {
+                    pbw[16 * (G4 * 4) + h] = bm;  // new running max of head h
+                }
+                if ((lane & 15) == 1) {
+                    wl[wave][h] = t;  // block probability sum of head h (scratch)
+                }
+            }
+        }
+        // The wave reads back what its own lanes wrote (LDS ops are ordered
+        // within a wave); every lane gets each head's max and sum.
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float mnew = pbw[16 * (G4 * 4) + h];
+            const float alpha = (mnew == -INFINITY) ? 1.0f : exp2f(mrow[h] - mnew);
+            mrow[h] = mnew;
+            lrow[h] = lrow[h] * alpha + wl[wave][h];
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) o[h][d] *= alpha;
+        }
+#pragma unroll
+        for (int n = 0; n < 16; ++n) {
+            float pv[G4 * 4];
+#pragma unroll
+            for (int g4 = 0; g4 < G4; ++g4) {
+                const float4 t = pb[wave][n][g4];
+                pv[4 * g4] = t.x; pv[4 * g4 + 1] = t.y; pv[4 * g4 + 2] = t.z; pv[4 * g4 + 3] = t.w;
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) o[h][d] = fmaf(pv[h], (float)cur.vv[n][d], o[h][d]);
+        }
+        __builtin_amdgcn_wave_barrier();  // pb is rewritten by the next block
+        cur = nxt;
+    }
+
+    // Combine the waves.
+    __syncthreads();  // every wave is done with the query fragments
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            wm[wave][h] = mrow[h];
+            wl[wave][h] = lrow[h];
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) sm.wo[wave][h][lane * DPL + d] = o[h][d];
+    __syncthreads();
+
+    const size_t bh0 = (size_t)b * a.num_heads + hq0;
+    for (int idx = tid; idx < G * D; idx += 256) {
+        const int h = idx / D, d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm[w][h]);
+        float L = 0.0f, O = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float f = exp2f(wm[w][h] - M);
+                L += wl[w][h] * f;
+                O += sm.wo[w][h][d] * f;
+            }
+        }
+        if (a.splits == 1) {
+            const float r = L > 0.0f ? O / L : 0.0f;
+            const size_t oi = (bh0 + h) * D + d;
+            if (a.out_f16) reinterpret_cast<_Float16 *>(a.out)[oi] = (_Float16)r;
+            else reinterpret_cast<float *>(a.out)[oi] = r;
+        } else {
+            const size_t pi = (bh0 + h) * a.splits + split;
+            a.ws_o[pi * D + d] = O;
+            if (d == 0) {
+                a.ws_ml[pi * 2] = M;
+                a.ws_ml[pi * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// Combine of the split partials, one workgroup per query head:
+// out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s.
+// Thread (column c4, phase ph) sums splits ph, ph + PH, ...; every load of a
+// 16-split batch is issued before the first is used, the phases fold in LDS.
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+    constexpr int C4 = D / 4;
+    constexpr int PH = 256 / C4;
+    __shared__ float wts[kMaxSplits];
+    __shared__ float red_l[kMaxSplits];
+    __shared__ float4 fold[256];
+    __shared__ float sM, sL;
+    const int bh = blockIdx.x, tid = threadIdx.x;
+    const int S = a.splits;
+    const float *ml = a.ws_ml + (size_t)bh * S * 2;
+    const int c4 = tid % C4, ph = tid / C4;
+    const float4 *po = reinterpret_cast<const float4 *>(a.ws_o + (size_t)bh * S * D) + c4;
+
+    // first batch of partial outputs in flight before the (m, l) pass
+    float4 v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = po[(size_t)min(ph + u * PH, S - 1) * C4];
+    for (int sp = tid; sp < S; sp += 256) {
+        wts[sp] = ml[2 * sp];
+        red_l[sp] = ml[2 * sp + 1];
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float M = -INFINITY;
+        for (int sp = 0; sp < S; ++sp) M = fmaxf(M, wts[sp]);
+        sM = M;
+    }
+    __syncthreads();
+    const float M = sM;
+    for (int sp = tid; sp < S; sp += 256) {
+        const float m = wts[sp];
+        const float f = (m == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(m - M);
+        wts[sp] = f;
+        red_l[sp] *= f;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float L = 0.0f;
+        for (int sp = 0; sp < S; ++sp) L += red_l[sp];
+        sL = L;
+    }
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int base = 0; base < S; base += 16 * PH) {
+        if (base > 0) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = po[(size_t)min(base + ph + u * PH, S - 1) * C4];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int sp = base + ph + u * PH;
+            const float f = sp < S ? wts[sp] : 0.0f;
+            t.x = fmaf(v[u].x, f, t.x); t.y = fmaf(v[u].y, f, t.y);
+            t.z = fmaf(v[u].z, f, t.z); t.w = fmaf(v[u].w, f, t.w);
+        }
+    }
+    fold[tid] = t;
+    __syncthreads();
+    if (tid < C4) {
+        float4 r = fold[tid];
+        for (int p2 = 1; p2 < PH; ++p2) {
+            const float4 u = fold[p2 * C4 + tid];
+            r.x += u.x; r.y += u.y; r.z += u.z; r.w += u.w;
+        }
+        const float L = sL;
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const float rv[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+        const size_t oi = (size_t)bh * D + 4 * tid;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (a.out_f16) reinterpret_cast<_Float16 *>(a.out)[oi + j] = (_Float16)rv[j];
+            else reinterpret_cast<float *>(a.out)[oi + j] = rv[j];
+        }
+    }
+}
+
+// Library-owned workspace (grow-only) for split partials.
+std::mutex g_ws_mu;
+void *g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+int g_num_cus = 0;
+int g_tune_splits = 0;
+
+template <int D>
+int launch_main(int g, dim3 grid, hipStream_t st, const AttnArgs &a) {
+    switch (g) {
+        case 1: hipLaunchKernelGGL((attn_decode_kernel<D, 1>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((attn_decode_kernel<D, 2>), grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((attn_decode_kernel<D, 4>), grid, dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((attn_decode_kernel<D, 8>), grid, dim3(256), 0, st, a); break;
+        default: return doe::set_error(DOE_E_UNSUPPORTED, "query heads per kv head must be 1, 2, 4 or 8 (got %d)", g);
+    }
+    DOE_LAUNCH_CHECK("attn_decode_kernel");
+    return DOE_OK;
+}
+
+template <int D>
+int launch_d(int g, dim3 grid, hipStream_t st, const AttnArgs &a) {
+    int rc = launch_main<D>(g, grid, st, a);
+    if (rc || a.splits == 1) return rc;
+    const unsigned total_heads = grid.z * (unsigned)a.num_heads;
+    hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(total_heads), dim3(256), 0, st, a);
+    DOE_LAUNCH_CHECK("attn_combine_kernel");
+    return DOE_OK;
+}
+
+
+}  // namespace
+
+namespace doe {
+int attn_set_splits(int v) {
+    g_tune_splits = v;
+    return DOE_OK;
+}
+}  // namespace doe
+
+extern "C" {
+
+int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uint16_t *v_cache,
+                    void *out, int out_f16, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                    int64_t head_dim, int64_t kv_len, const int32_t *kv_len_dev, int64_t kv_stride,
+                    int kv_layout, float scale, float softcap, int64_t sliding_window,
+                    doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(batch >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && kv_stride >= 0,
+                DOE_E_INVALID, "bad attention shape");
+    DOE_REQUIRE(num_heads % num_kv_heads == 0, DOE_E_INVALID,
+                "num_heads %lld is not a multiple of num_kv_heads %lld", (long long)num_heads,
+                (long long)num_kv_heads);
+    DOE_REQUIRE(kv_layout == 0 || kv_layout == 1, DOE_E_UNSUPPORTED,
+                "kv_layout %d unsupported (0: [kv_head][pos][dim], 1: [pos][kv_head][dim])", kv_layout);
+    DOE_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512,
+                DOE_E_UNSUPPORTED, "head_dim %lld unsupported (64, 128, 256, 512)", (long long)head_dim);
+    DOE_REQUIRE(kv_len_dev != nullptr || (kv_len >= 0 && kv_len <= kv_stride), DOE_E_INVALID,
+                "kv_len %lld out of range [0, kv_stride=%lld]", (long long)kv_len, (long long)kv_stride);
+    DOE_REQUIRE(sliding_window >= 0 && softcap >= 0.0f, DOE_E_INVALID, "negative window or softcap");
+    if (batch == 0) return DOE_OK;
+    DOE_REQUIRE(q && k_cache && v_cache && out, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0, DOE_E_INVALID,
+                "k/v caches must be 16-byte aligned");
+    DOE_REQUIRE(batch * num_kv_heads <= 65535 && kv_stride <= 0x7fffffff, DOE_E_UNSUPPORTED,
+                "too many sequences x kv heads");
+    const int g = (int)(num_heads / num_kv_heads);
+    if (g_num_cus == 0) {
+        int dev = 0, cus = 0;
+        DOE_HIP_CHECK(hipGetDevice(&dev));
+        DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        g_num_cus = cus > 0 ? cus : 256;
+    }
+    // Splits: about two workgroups per CU, at least four 16-position blocks each.
+    const int64_t len_for_split = kv_len_dev ? kv_stride : kv_len;
+    const int64_t nblk = (len_for_split + 15) / 16;
+    int64_t splits = (2 * g_num_cus + batch * num_kv_heads - 1) / (batch * num_kv_heads);
+    const int64_t max_splits = (nblk + 3) / 4;
+    if (g_tune_splits > 0) splits = g_tune_splits;
+    if (splits > max_splits) splits = max_splits;
+    if (splits > kMaxSplits) splits = kMaxSplits;
+    if (splits < 1) splits = 1;
+
+    AttnArgs a{};
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.out = out;
+    a.kv_len_dev = kv_len_dev;
+    a.q_f16 = q_f16 != 0;
+    a.out_f16 = out_f16 != 0;
+    a.num_heads = (int)num_heads;
+    a.num_kv_heads = (int)num_kv_heads;
+    a.kv_len = (int)kv_len;
+    a.kv_stride = (int)kv_stride;
+    a.kv_layout = kv_layout;
+    a.splits = (int)splits;
+    a.scale_log2e = scale * 1.4426950408889634f;
+    a.softcap = softcap;
+    a.sliding_window = (int)sliding_window;
+    if (splits > 1) {
+        const size_t o_bytes = (size_t)batch * num_heads * splits * head_dim * 4;
+        const size_t ml_bytes = (size_t)batch * num_heads * splits * 2 * 4;
+        const size_t ml_off = (o_bytes + 255) & ~(size_t)255;
+        const size_t need = ml_off + ml_bytes;
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        if (need > g_ws_bytes) {
+            if (g_ws) DOE_HIP_CHECK(hipFree(g_ws));
+            g_ws = nullptr;
+            g_ws_bytes = 0;
+            DOE_HIP_CHECK(hipMalloc(&g_ws, need));
+            g_ws_bytes = need;
+        }
+        a.ws_o = (float *)g_ws;
+        a.ws_ml = (float *)((char *)g_ws + ml_off);
+    }
+    const dim3 grid((unsigned)splits, (unsigned)num_kv_heads, (unsigned)batch);
+    const hipStream_t st = (hipStream_t)stream;
+    switch (head_dim) {
+        case 64: return launch_d<64>(g, grid, st, a);
+        case 128: return launch_d<128>(g, grid, st, a);
+        case 256: return launch_d<256>(g, grid, st, a);
+        default:
+            DOE_REQUIRE(g <= 2, DOE_E_UNSUPPORTED, "head_dim 512 supports at most 2 query heads per kv head");
+            return launch_d<512>(g, grid, st, a);
+    }
+}
+
+}  // extern "C"

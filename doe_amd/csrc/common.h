@@ -21,6 +21,8 @@ void clear_error();
 int hip_fail(hipError_t e, const char *what);
 // Checks that the library was initialised on the calling thread's device.
 int require_init();
+// Tuning hooks of individual kernels (0 = automatic).
+int attn_set_splits(int value);
 
 }  // namespace doe
 

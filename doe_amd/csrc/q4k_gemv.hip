@@ -412,6 +412,8 @@ int doe_tune_set(const char *key, int value) {
         g_tune_rowslots = value;
     } else if (!strcmp(key, "q4k_gemv.rows")) {
         g_tune_rows = value;
+    } else if (!strcmp(key, "attn_decode.splits")) {
+        return doe::attn_set_splits(value);
     } else {
         return doe::set_error(DOE_E_INVALID, "unknown tuning key '%s'", key);
     }

@@ -53,7 +53,38 @@ def matmul_q4k(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuf
     _lib.call("doe_q4k_gemv", _p(weight), _p(activation), _p(output), n, k, _stream_ptr(stream))
 
 
+def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, output: DeviceBuffer, *,
+              batch: int, num_heads: int, num_kv_heads: int, head_dim: int, kv_len: int,
+              kv_stride: int, scale: float, q_f16: bool = False, out_f16: bool = False,
+              softcap: float = 0.0, sliding_window: int = 0, kv_layout: int = 0,
+              kv_len_buffer: DeviceBuffer | None = None, stream=None) -> None:
+    """``attention`` op (pattern ``attention_decode``): one query token per
+    sequence against an f16 KV cache (GQA, kv head = h / (Hq / Hkv)).
+
+    ``kv_len_buffer`` (a device int32) replaces ``kv_len`` when given, as the
+    reference's ``kv_len_source = 1`` does."""
+    if num_kv_heads <= 0 or num_heads % num_kv_heads:
+        raise ValueError(f"num_heads {num_heads} is not a multiple of num_kv_heads {num_kv_heads}")
+    if kv_len_buffer is None and not 0 <= kv_len <= kv_stride:
+        raise ValueError(f"kv_len {kv_len} outside [0, kv_stride={kv_stride}]")
+    _need(q, batch * num_heads * head_dim * (2 if q_f16 else 4), "q")
+    cache_bytes = batch * num_kv_heads * kv_stride * head_dim * 2
+    _need(k_cache, cache_bytes, "k_cache")
+    _need(v_cache, cache_bytes, "v_cache")
+    _need(output, batch * num_heads * head_dim * (2 if out_f16 else 4), "output")
+    kvp = C.c_void_p(kv_len_buffer.ptr) if kv_len_buffer is not None else C.c_void_p(None)
+    _lib.call("doe_attn_decode", _p(q), int(q_f16), _p(k_cache), _p(v_cache), _p(output), int(out_f16),
+              batch, num_heads, num_kv_heads, head_dim, kv_len, kvp, kv_stride, kv_layout, scale, softcap,
+              sliding_window, _stream_ptr(stream))
+
+
+def tune(key: str, value: int) -> None:
+    """Overrides a launch-shape choice (``doe_tune_set``); 0 restores automatic."""
+    _lib.call("doe_tune_set", key.encode(), int(value))
+
+
 OPS = {
+    "attention": attention,
     "dequant": dequant_q4k,
     "matmul_q4k": matmul_q4k,
 }

@@ -104,9 +104,36 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
 int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
                  int64_t n, int64_t k, doe_stream_t stream);
 
+/* ---- attention ---------------------------------------------------------------
+ * GQA decode attention over an f16 KV cache: one query token per sequence.
+ * Replaces the `attention` op (emit_csl_exec_v1.zig:117 -> attention_decode;
+ * Doppler kernel runtime/zig/tests/tsir/real/attention_head256_f16kv/
+ * attention_head256_f16kv.wgsl: bindings Q (1), K (2), V (3), output (4),
+ * kv_len_buffer (5); Uniforms num_heads, num_kv_heads, head_dim, seq_len,
+ * scale, attn_softcap, sliding_window, kv_len_source, kv_layout, :14-38).
+ *   q        [batch][num_heads][head_dim], f16 (q_f16 = 1) or f32
+ *   k/v      f16; kv_layout 0: [batch][num_kv_heads][kv_stride][head_dim]
+ *                  kv_layout 1: [batch][kv_stride][num_kv_heads][head_dim]
+ *   out      [batch][num_heads][head_dim], f16 (out_f16 = 1) or f32
+ *   kv_len   valid positions (0 <= kv_len <= kv_stride); when kv_len_dev is
+ *            non-NULL the length is read from that device int32 instead
+ *            (the reference's kv_len_buffer), so a captured graph can replay
+ *            with a growing cache.
+ *   the query sits at position kv_len - 1; sliding_window > 0 keeps keys
+ *   [kv_len - sliding_window, kv_len); softcap > 0 applies tanh(s/cap)*cap.
+ * head_dim 64/128/256/512, num_heads / num_kv_heads in {1, 2, 4, 8} (512: <= 2).
+ * Uses a library-owned workspace for split-K partials: calls on one device
+ * must not run concurrently on different streams. */
+int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uint16_t *v_cache,
+                    void *out, int out_f16, int64_t batch, int64_t num_heads,
+                    int64_t num_kv_heads, int64_t head_dim, int64_t kv_len,
+                    const int32_t *kv_len_dev, int64_t kv_stride, int kv_layout, float scale,
+                    float softcap, int64_t sliding_window, doe_stream_t stream);
+
 /* ---- tuning ----------------------------------------------------------------
  * Overrides a kernel launch-shape choice (0 restores the automatic choice).
- * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows".  No reference counterpart:
+ * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows", "attn_decode.splits".  No
+ * reference counterpart:
  * the reference fixes workgroup shapes per WGSL override constant
  * (lm_head_gemv.wgsl:168-169 MULTICOL_* overrides). */
 int doe_tune_set(const char *key, int value);

@@ -1,0 +1,186 @@
+"""GPU parity of GQA decode attention (f16 KV cache) against the CPU oracle,
+through the C ABI.  Tolerance: rel-L2 <= 1e-3 (fp32 accumulate)."""
+import math
+
+import numpy as np
+import pytest
+
+from doe_amd import DeviceBuffer, Graph, Stream, ops
+
+pytestmark = pytest.mark.gpu
+
+ATTN_REL_L2 = 1e-3
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def run_attn(q, k, v, *, hq, hkv, d, kv_len, kv_stride, scale, q_f16, out_f16, softcap=0.0, window=0,
+             layout=0, batch=1, kv_len_buffer=None, stream=None):
+    dq = DeviceBuffer.from_array(q)
+    dk = DeviceBuffer.from_array(k)
+    dv = DeviceBuffer.from_array(v)
+    out = DeviceBuffer.empty((batch, hq, d), np.float16 if out_f16 else np.float32)
+    ops.attention(dq, dk, dv, out, batch=batch, num_heads=hq, num_kv_heads=hkv, head_dim=d, kv_len=kv_len,
+                  kv_stride=kv_stride, scale=scale, q_f16=q_f16, out_f16=out_f16, softcap=softcap,
+                  sliding_window=window, kv_layout=layout, kv_len_buffer=kv_len_buffer, stream=stream)
+    return out.download().astype(np.float32)
+
+
+def oracle_attn(ora, q, k, v, *, batch, hq, hkv, d, kv_len, kv_stride, scale, softcap=0.0, window=0,
+                layout=0):
+    outs = []
+    for b in range(batch):
+        outs.append(ora.attn_decode(q[b].astype(np.float32), k[b], v[b], hq, hkv, d, kv_len, kv_stride, scale,
+                                    softcap, window, layout))
+    return np.stack(outs)
+
+
+def test_config1_gqa_decode(dev, ora):
+    # 8 query / 4 KV heads, head_dim 256, context 4096, f16 Q/K/V N(0,1),
+    # scale 1/16, f16 output; KV cache [kv_head][pos][dim].
+    rng = np.random.default_rng(1)
+    hq, hkv, d, t = 8, 4, 256, 4096
+    q = rng.standard_normal((1, hq, d)).astype(np.float16)
+    k = rng.standard_normal((1, hkv, t, d)).astype(np.float16)
+    v = rng.standard_normal((1, hkv, t, d)).astype(np.float16)
+    got = run_attn(q, k, v, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=1 / 16, q_f16=True, out_f16=True)
+    want = oracle_attn(ora, q, k, v, batch=1, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=1 / 16)
+    err = rel_l2(got, want)
+    print(f"[attn cfg1] rel_l2={err:.3e}", flush=True)
+    assert err <= ATTN_REL_L2
+
+
+@pytest.mark.parametrize("d", [64, 128, 256, 512])
+@pytest.mark.parametrize("g", [1, 2, 4, 8])
+def test_head_dims_and_groups(dev, ora, d, g):
+    if d == 512 and g > 2:
+        pytest.skip("head_dim 512 supports at most 2 query heads per kv head")
+    rng = np.random.default_rng(d + g)
+    hkv = 2
+    hq = hkv * g
+    t, stride, batch = 300, 320, 2
+    q = rng.standard_normal((batch, hq, d)).astype(np.float32)
+    k = rng.standard_normal((batch, hkv, stride, d)).astype(np.float16)
+    v = rng.standard_normal((batch, hkv, stride, d)).astype(np.float16)
+    scale = 1 / math.sqrt(d)
+    got = run_attn(q, k, v, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=scale, q_f16=False,
+                   out_f16=False, batch=batch)
+    want = oracle_attn(ora, q, k, v, batch=batch, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=scale)
+    assert rel_l2(got, want) <= 1e-5  # f32 query (hi/lo split), f32 output
+
+
+@pytest.mark.parametrize("t", [1, 15, 16, 17, 63, 64, 65, 1000])
+def test_ragged_lengths(dev, ora, t):
+    rng = np.random.default_rng(t)
+    hq, hkv, d, stride = 4, 2, 128, 1024
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    k = rng.standard_normal((1, hkv, stride, d)).astype(np.float16)
+    v = rng.standard_normal((1, hkv, stride, d)).astype(np.float16)
+    got = run_attn(q, k, v, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=0.1, q_f16=False, out_f16=False)
+    want = oracle_attn(ora, q, k, v, batch=1, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=0.1)
+    assert rel_l2(got, want) <= 1e-5
+    if t == 1:  # a single key returns its value row
+        assert np.allclose(got[0, 0], v[0, 0, 0].astype(np.float32), atol=1e-6)
+
+
+def test_layout1_window_softcap(dev, ora):
+    rng = np.random.default_rng(5)
+    hq, hkv, d, t = 8, 4, 256, 777
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    k0 = rng.standard_normal((1, hkv, t, d)).astype(np.float16)
+    v0 = rng.standard_normal((1, hkv, t, d)).astype(np.float16)
+    k1 = np.ascontiguousarray(k0.transpose(0, 2, 1, 3))
+    v1 = np.ascontiguousarray(v0.transpose(0, 2, 1, 3))
+    for window, cap in [(0, 0.0), (100, 0.0), (0, 2.0), (50, 1.5)]:
+        want = oracle_attn(ora, q, k0, v0, batch=1, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=0.0625,
+                           softcap=cap, window=window)
+        g0 = run_attn(q, k0, v0, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=0.0625, q_f16=False,
+                      out_f16=False, softcap=cap, window=window, layout=0)
+        g1 = run_attn(q, k1, v1, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=0.0625, q_f16=False,
+                      out_f16=False, softcap=cap, window=window, layout=1)
+        assert rel_l2(g0, want) <= 1e-5, (window, cap)
+        assert rel_l2(g1, want) <= 1e-5, (window, cap)
+
+
+def test_split_count_does_not_change_the_result(dev, ora):
+    rng = np.random.default_rng(6)
+    hq, hkv, d, t = 8, 4, 256, 4096
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    k = rng.standard_normal((1, hkv, t, d)).astype(np.float16)
+    v = rng.standard_normal((1, hkv, t, d)).astype(np.float16)
+    want = oracle_attn(ora, q, k, v, batch=1, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=1 / 16)
+    try:
+        for splits in (1, 2, 7, 64, 256):
+            ops.tune("attn_decode.splits", splits)
+            for rep in range(2):  # the split counters must be back at zero
+                got = run_attn(q, k, v, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=1 / 16, q_f16=False,
+                               out_f16=False)
+                assert rel_l2(got, want) <= 1e-5, (splits, rep)
+    finally:
+        ops.tune("attn_decode.splits", 0)
+
+
+def test_device_kv_len_graph_replays(dev, ora):
+    # The decode loop captures attention once and replays it as the cache
+    # grows: the length comes from a device int32 (kv_len_source = 1).
+    rng = np.random.default_rng(7)
+    hq, hkv, d, stride = 8, 4, 256, 2048
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    k = rng.standard_normal((1, hkv, stride, d)).astype(np.float16)
+    v = rng.standard_normal((1, hkv, stride, d)).astype(np.float16)
+    dq, dk, dv = DeviceBuffer.from_array(q), DeviceBuffer.from_array(k), DeviceBuffer.from_array(v)
+    out = DeviceBuffer.empty((1, hq, d), np.float32)
+    klen = DeviceBuffer.from_array(np.array([1], np.int32))
+    s = Stream()
+    g = Graph.capture(s, lambda: ops.attention(dq, dk, dv, out, batch=1, num_heads=hq, num_kv_heads=hkv,
+                                               head_dim=d, kv_len=0, kv_stride=stride, scale=1 / 16,
+                                               kv_len_buffer=klen, stream=s))
+    for t in (1, 17, 500, 2048, 129):
+        klen.upload(np.array([t], np.int32))
+        g.launch(s)
+        s.synchronize()
+        want = oracle_attn(ora, q, k, v, batch=1, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=1 / 16)
+        assert rel_l2(out.download(), want) <= 1e-5, t
+    g.destroy()
+    s.destroy()
+
+
+def test_empty_cache_gives_zeros(dev):
+    hq, hkv, d = 2, 1, 64
+    q = np.ones((1, hq, d), np.float32)
+    k = np.ones((1, hkv, 16, d), np.float16)
+    got = run_attn(q, k, k, hq=hq, hkv=hkv, d=d, kv_len=0, kv_stride=16, scale=1.0, q_f16=False, out_f16=False)
+    assert not got.any()
+
+
+def test_rejects_bad_shapes(dev):
+    from doe_amd import DoeError
+    q = DeviceBuffer.empty((1, 3, 64), np.float32)
+    kv = DeviceBuffer.empty((1, 1, 16, 64), np.float16)
+    with pytest.raises(DoeError):  # 3 query heads per kv head is not supported
+        ops.attention(q, kv, kv, q, batch=1, num_heads=3, num_kv_heads=1, head_dim=64, kv_len=16, kv_stride=16,
+                      scale=1.0)
+    with pytest.raises(ValueError):
+        ops.attention(q, kv, kv, q, batch=1, num_heads=3, num_kv_heads=2, head_dim=64, kv_len=16, kv_stride=16,
+                      scale=1.0)
+    with pytest.raises(ValueError):
+        ops.attention(q, kv, kv, q, batch=1, num_heads=1, num_kv_heads=1, head_dim=64, kv_len=17, kv_stride=16,
+                      scale=1.0)
+
+
+def test_workspace_reuse_after_larger_call(dev, ora):
+    # Regression: a large multi-split call followed by a smaller one must still
+    # find the split counters at zero.
+    rng = np.random.default_rng(8)
+    for hq, hkv, d, t, batch in [(8, 4, 256, 4096, 2), (2, 2, 64, 300, 1), (8, 4, 256, 2000, 1)]:
+        q = rng.standard_normal((batch, hq, d)).astype(np.float32)
+        k = rng.standard_normal((batch, hkv, t, d)).astype(np.float16)
+        v = rng.standard_normal((batch, hkv, t, d)).astype(np.float16)
+        got = run_attn(q, k, v, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=0.05, q_f16=False,
+                       out_f16=False, batch=batch)
+        want = oracle_attn(ora, q, k, v, batch=batch, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=0.05)
+        assert rel_l2(got, want) <= 1e-5, (hq, hkv, d, t, batch)
