@@ -70,6 +70,15 @@ SIGNATURES: dict[str, list] = {
     "doe_q4k_gemv": [_vp, _vp, _vp, _i64, _i64, _vp],
     "doe_attn_decode": [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i32,
                         _f32, _f32, _i64, _vp],
+    "doe_q4k_gemv_fused": [_vp, _vp, _vp, _i64, _i64, _vp, _f32, _i32, _vp, _i32, _vp],
+    "doe_rmsnorm": [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp],
+    "doe_rope": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp],
+    "doe_geglu": [_vp, _vp, _vp, _i64, _vp],
+    "doe_residual_add": [_vp, _vp, _vp, _i64, _vp],
+    "doe_argmax": [_vp, _i64, _vp, _vp, _vp],
+    "doe_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _vp],
+    "doe_embed_gather": [_vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp],
+    "doe_f16_gemv": [_vp, _vp, _vp, _i64, _i64, _f32, _vp],
     "doe_tune_set": [C.c_char_p, _i32],
 }
 

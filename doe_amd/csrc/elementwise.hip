@@ -1,0 +1,291 @@
+// elementwise.hip -- RMSNorm, RoPE, GeGLU, residual add, argmax, KV write and
+// embedding gather for gfx950.  These are the small ops around the decode
+// GEMVs; each is HBM- or latency-bound and written for one pass over its data.
+#include "common.h"
+
+#include <math.h>
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Sum over a workgroup of `nwaves` waves through LDS (result in every thread).
+__device__ __forceinline__ float block_sum(float v, float *sh, int nwaves) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int w = 0; w < nwaves; ++w) t += sh[w];
+    __syncthreads();
+    return t;
+}
+
+// RMSNorm, one workgroup per row (rmsnorm.wgsl:15-53 / :55-93; the
+// interpreter's numerics, reference_interpreter.zig:510-526, are an f32 sum of
+// squares, mean = sum / H, inv = 1 / sqrt(mean + eps), out = x * inv * w).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x,
+                                                      const float *__restrict__ w,
+                                                      float *__restrict__ out, int h, float eps,
+                                                      int weight_offset) {
+    __shared__ float sh[4];
+    const float *xr = x + (size_t)blockIdx.x * h;
+    float *orow = out + (size_t)blockIdx.x * h;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < h; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum(ss, sh, 4);
+    const float inv = 1.0f / sqrtf(ss / (float)h + eps);
+    for (int i = threadIdx.x; i < h; i += 256) {
+        const float scale = weight_offset ? 1.0f + w[i] : w[i];
+        orow[i] = xr[i] * inv * scale;
+    }
+}
+
+// RoPE, rotate-half pairs (i, i + D/2) (rope.wgsl:12-35).  Products and
+// differences are rounded separately, as the reference's scalar code does.
+__global__ __launch_bounds__(256) void rope_kernel(float *__restrict__ qk,
+                                                   const float *__restrict__ freq_cis, int seq_len,
+                                                   int num_heads, int head_dim, int pos_off,
+                                                   const int32_t *__restrict__ pos_dev) {
+#pragma clang fp contract(off)
+    const int half = head_dim >> 1;
+    const long total = (long)seq_len * num_heads * half;
+    const int base_pos = pos_dev ? pos_dev[0] : pos_off;
+    for (long g = (long)blockIdx.x * 256 + threadIdx.x; g < total; g += (long)gridDim.x * 256) {
+        const int i = (int)(g % half);
+        const long sh = g / half;  // seq * num_heads + head
+        const int s = (int)(sh / num_heads);
+        const long pos = (long)s + base_pos;
+        float *base = qk + sh * head_dim;
+        const float x0 = base[i], x1 = base[i + half];
+        const float c = freq_cis[(pos * half + i) * 2], sn = freq_cis[(pos * half + i) * 2 + 1];
+        base[i] = x0 * c - x1 * sn;
+        base[i + half] = x0 * sn + x1 * c;
+    }
+}
+
+__device__ __forceinline__ float gelu_tanh_clamped(float x) {
+    // gelu_gated.wgsl:5-8, reference_interpreter.zig:1027-1045
+    float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    inner = fminf(fmaxf(inner, -15.0f), 15.0f);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+__global__ __launch_bounds__(256) void geglu_kernel(const float *__restrict__ gate,
+                                                    const float *__restrict__ up,
+                                                    float *__restrict__ out, long n) {
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+        out[i] = gelu_tanh_clamped(gate[i]) * up[i];
+}
+
+__global__ __launch_bounds__(256) void residual_kernel(const float *__restrict__ a,
+                                                       const float *__restrict__ b,
+                                                       float *__restrict__ out, long n) {
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+        out[i] = a[i] + b[i];
+}
+
+// Argmax keys: ordered float bits in the high word, inverted index in the low
+// word, so an unsigned max picks the largest value and, on a tie, the lowest
+// index (run_csl_webgpu_emulator.mjs:841-878: strict '>' from -FLT_MAX, index
+// 0).  NaN never wins (it fails every '>' in the reference).
+__device__ __forceinline__ unsigned long long argmax_key(float v, unsigned idx) {
+    if (v != v) return 0ull;
+    unsigned u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (0xffffffffu - idx);
+}
+
+__device__ __forceinline__ unsigned long long max_u64(unsigned long long a, unsigned long long b) {
+    return a > b ? a : b;
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float *__restrict__ logits, long n,
+                                                             unsigned long long *__restrict__ part) {
+    __shared__ unsigned long long sh[4];
+    unsigned long long best = 0;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+        best = max_u64(best, argmax_key(logits[i], (unsigned)i));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) best = max_u64(best, __shfl_xor(best, o, 64));
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = max_u64(max_u64(sh[0], sh[1]), max_u64(sh[2], sh[3]));
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const unsigned long long *__restrict__ part,
+                                                           int nparts, int32_t *__restrict__ out) {
+    __shared__ unsigned long long sh[4];
+    // the reference's starting point: value -FLT_MAX at index 0
+    unsigned long long best = argmax_key(-3.402823466e38f, 0u);
+    for (int i = threadIdx.x; i < nparts; i += 256) best = max_u64(best, part[i]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) best = max_u64(best, __shfl_xor(best, o, 64));
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        best = max_u64(max_u64(sh[0], sh[1]), max_u64(sh[2], sh[3]));
+        out[0] = (int32_t)(0xffffffffu - (unsigned)(best & 0xffffffffull));
+    }
+}
+
+// KV write (run_csl_webgpu_emulator.mjs:615-644): cache[h][pos][:] =
+// f16(proj[h][:]) (RNE).  A position outside the cache writes nothing.
+__global__ __launch_bounds__(256) void kv_write_kernel(const float *__restrict__ kp,
+                                                       const float *__restrict__ vp,
+                                                       _Float16 *__restrict__ kc,
+                                                       _Float16 *__restrict__ vc, int kvh,
+                                                       int max_seq, int head_dim, int pos_host,
+                                                       const int32_t *__restrict__ pos_dev,
+                                                       int layout) {
+    const int pos = pos_dev ? pos_dev[0] : pos_host;
+    if (pos < 0 || pos >= max_seq) return;
+    const int total = kvh * head_dim;
+    for (int g = blockIdx.x * 256 + threadIdx.x; g < total; g += gridDim.x * 256) {
+        const int h = g / head_dim, d = g % head_dim;
+        const size_t dst = layout == 0 ? ((size_t)h * max_seq + pos) * head_dim + d
+                                       : ((size_t)pos * kvh + h) * head_dim + d;
+        kc[dst] = (_Float16)kp[g];
+        vc[dst] = (_Float16)vp[g];
+    }
+}
+
+// Embedding gather (run_csl_webgpu_emulator.mjs:528-551): out[t] =
+// scale * f32(table[id[t]]), zeros for ids outside the table.
+__global__ __launch_bounds__(256) void embed_kernel(const _Float16 *__restrict__ table,
+                                                    const int32_t *__restrict__ ids,
+                                                    float *__restrict__ out, int n_ids, int vocab,
+                                                    int hidden, float scale) {
+    const long total = (long)n_ids * hidden;
+    for (long g = (long)blockIdx.x * 256 + threadIdx.x; g < total; g += (long)gridDim.x * 256) {
+        const int t = (int)(g / hidden), d = (int)(g % hidden);
+        const int id = ids[t];
+        out[g] = (id >= 0 && id < vocab) ? (float)table[(size_t)id * hidden + d] * scale : 0.0f;
+    }
+}
+
+unsigned grid_for(long n, unsigned cap = 4096) {
+    long b = (n + 255) / 256;
+    if (b < 1) b = 1;
+    return (unsigned)(b > cap ? cap : b);
+}
+
+}  // namespace
+
+extern "C" {
+
+int doe_rmsnorm(const float *input, const float *weight, float *output, int64_t rows, int64_t size,
+                float eps, int weight_offset, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(rows >= 0 && size >= 0 && rows <= 0x7fffffff && size <= 0x7fffffff, DOE_E_INVALID,
+                "bad rmsnorm shape");
+    if (rows == 0 || size == 0) return DOE_OK;
+    DOE_REQUIRE(input && weight && output, DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, input,
+                       weight, output, (int)size, eps, weight_offset);
+    DOE_LAUNCH_CHECK("rmsnorm_kernel");
+    return DOE_OK;
+}
+
+int doe_rope(float *qk, const float *freq_cis, int64_t seq_len, int64_t num_heads, int64_t head_dim,
+             int64_t position_offset, const int32_t *position_dev, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(seq_len >= 0 && num_heads >= 0 && head_dim > 0 && (head_dim % 2) == 0 &&
+                    position_offset >= 0,
+                DOE_E_INVALID, "bad rope shape");
+    const long total = (long)seq_len * num_heads * (head_dim / 2);
+    if (total == 0) return DOE_OK;
+    DOE_REQUIRE(qk && freq_cis, DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, qk,
+                       freq_cis, (int)seq_len, (int)num_heads, (int)head_dim, (int)position_offset,
+                       position_dev);
+    DOE_LAUNCH_CHECK("rope_kernel");
+    return DOE_OK;
+}
+
+int doe_geglu(const float *gate, const float *up, float *output, int64_t n, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n >= 0, DOE_E_INVALID, "negative size");
+    if (n == 0) return DOE_OK;
+    DOE_REQUIRE(gate && up && output, DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(geglu_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, gate, up,
+                       output, (long)n);
+    DOE_LAUNCH_CHECK("geglu_kernel");
+    return DOE_OK;
+}
+
+int doe_residual_add(const float *input, const float *residual, float *output, int64_t n,
+                     doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n >= 0, DOE_E_INVALID, "negative size");
+    if (n == 0) return DOE_OK;
+    DOE_REQUIRE(input && residual && output, DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(residual_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, input,
+                       residual, output, (long)n);
+    DOE_LAUNCH_CHECK("residual_kernel");
+    return DOE_OK;
+}
+
+int doe_argmax(const float *logits, int64_t n, int32_t *token, void *workspace,
+               doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n > 0 && n <= 0x7fffffff, DOE_E_INVALID, "argmax needs 0 < n < 2^31");
+    DOE_REQUIRE(logits && token && workspace, DOE_E_INVALID, "null pointer");
+    const unsigned parts = grid_for(n, 1024);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(parts), dim3(256), 0, (hipStream_t)stream, logits,
+                       (long)n, (unsigned long long *)workspace);
+    DOE_LAUNCH_CHECK("argmax_partial_kernel");
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream,
+                       (const unsigned long long *)workspace, (int)parts, token);
+    DOE_LAUNCH_CHECK("argmax_final_kernel");
+    return DOE_OK;
+}
+
+int doe_kv_write(const float *key_proj, const float *val_proj, uint16_t *key_cache,
+                 uint16_t *val_cache, int64_t num_kv_heads, int64_t max_seq_len, int64_t head_dim,
+                 int64_t position, const int32_t *position_dev, int kv_layout,
+                 doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(num_kv_heads >= 0 && head_dim >= 0 && max_seq_len > 0, DOE_E_INVALID,
+                "bad kv_write shape");
+    DOE_REQUIRE(kv_layout == 0 || kv_layout == 1, DOE_E_UNSUPPORTED, "kv_layout must be 0 or 1");
+    DOE_REQUIRE(position_dev || (position >= 0 && position < max_seq_len), DOE_E_INVALID,
+                "position %lld exceeds max_seq_len %lld", (long long)position, (long long)max_seq_len);
+    const long total = (long)num_kv_heads * head_dim;
+    if (total == 0) return DOE_OK;
+    DOE_REQUIRE(key_proj && val_proj && key_cache && val_cache, DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(kv_write_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream,
+                       key_proj, val_proj, (_Float16 *)key_cache, (_Float16 *)val_cache,
+                       (int)num_kv_heads, (int)max_seq_len, (int)head_dim, (int)position,
+                       position_dev, kv_layout);
+    DOE_LAUNCH_CHECK("kv_write_kernel");
+    return DOE_OK;
+}
+
+int doe_embed_gather(const uint16_t *table_f16, const int32_t *ids, float *output, int64_t n_ids,
+                     int64_t vocab, int64_t hidden, float scale, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n_ids >= 0 && vocab >= 0 && hidden >= 0 && vocab <= 0x7fffffff, DOE_E_INVALID,
+                "bad gather shape");
+    const long total = (long)n_ids * hidden;
+    if (total == 0) return DOE_OK;
+    DOE_REQUIRE(table_f16 && ids && output, DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(embed_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream,
+                       (const _Float16 *)table_f16, ids, output, (int)n_ids, (int)vocab, (int)hidden,
+                       scale);
+    DOE_LAUNCH_CHECK("embed_kernel");
+    return DOE_OK;
+}
+
+}  // extern "C"

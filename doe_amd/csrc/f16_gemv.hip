@@ -1,0 +1,173 @@
+// f16_gemv.hip -- f16-weight GEMV (the lm_head) for gfx950.
+//
+// C[n] = alpha * sum_k A[k] * f32(B[n*K + k]) with B f16 [N][K] row-major
+// (runtime/zig/tests/tsir/real/lm_head_gemv/lm_head_gemv.wgsl:78-180,
+// transpose_b = 1), A and C f32.
+//
+// Decomposition: persistent waves; a wave owns whole rows (row = wave id +
+// i * total waves) and each lane a fixed set of 16-byte pieces of the row
+// (pieces lane, lane + 64, ...), so its 8-element activation slices stay in
+// VGPRs for the whole kernel, split into f16 hi/lo pairs (~22 significant
+// bits).  A row is U 16-byte loads per lane, v_dot2c_f32_f16 against the hi
+// and lo pairs, and one wave reduction.  Two rows are processed per step and
+// the next step's rows are loaded before the current ones are reduced.
+#include "common.h"
+
+#include <math.h>
+
+namespace {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, a), __builtin_bit_cast(half2v, b), c,
+                                  false);
+}
+
+__device__ __forceinline__ uint32_t pack2(_Float16 lo, _Float16 hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+__device__ __forceinline__ u32x4 load16(const uint16_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+
+template <int P>
+__device__ __forceinline__ float row_dot(const u32x4 (&w)[P], const uint32_t (&xh)[P][4],
+                                         const uint32_t (&xl)[P][4]) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            a0 = dot2(w[i][j], xh[i][j], a0);
+            a1 = dot2(w[i][j], xl[i][j], a1);
+        }
+    }
+    return a0 + a1;
+}
+
+template <int P>
+__global__ __launch_bounds__(256) void f16_gemv_kernel(const uint16_t *__restrict__ b,
+                                                       const float *__restrict__ a,
+                                                       float *__restrict__ c, int n, int k,
+                                                       float alpha) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * 4;
+    const int npieces = k >> 3;
+
+    // activation slices of this lane, f16 hi/lo pairs; pieces past k are zero
+    uint32_t xh[P][4], xl[P][4];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const int p = lane + 64 * i;
+        const bool ok = p < npieces;
+        const float4 *src = reinterpret_cast<const float4 *>(a + 8 * (ok ? p : 0));
+        const float4 lo4 = src[0], hi4 = src[1];
+        const float v[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float x0 = ok ? v[2 * j] : 0.0f, x1 = ok ? v[2 * j + 1] : 0.0f;
+            const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+            xh[i][j] = pack2(h0, h1);
+            xl[i][j] = pack2((_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1));
+        }
+    }
+
+    // rows of this wave: wave, wave + nwaves, ...; two per step, prefetched
+    u32x4 w0[P], w1[P];
+    int row = wave;
+    auto load_rows = [&](int r, u32x4 (&d0)[P], u32x4 (&d1)[P]) {
+        const int r0 = min(r, n - 1), r1 = min(r + nwaves, n - 1);
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int p = min(lane + 64 * i, npieces - 1);
+            d0[i] = load16(b + (size_t)r0 * k + 8 * p);
+            d1[i] = load16(b + (size_t)r1 * k + 8 * p);
+        }
+    };
+    if (row < n) load_rows(row, w0, w1);
+    for (; row < n; row += 2 * nwaves) {
+        u32x4 n0[P], n1[P];
+        load_rows(row + 2 * nwaves, n0, n1);
+        // pieces past k were clamped onto a valid piece: mask them out
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            if (lane + 64 * i >= npieces) {
+                w0[i] = u32x4{0, 0, 0, 0};
+                w1[i] = u32x4{0, 0, 0, 0};
+            }
+        }
+        float s0 = row_dot<P>(w0, xh, xl);
+        float s1 = row_dot<P>(w1, xh, xl);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            s0 += __shfl_xor(s0, o, 64);
+            s1 += __shfl_xor(s1, o, 64);
+        }
+        if (lane == 0) {
+            c[row] = s0 * alpha;
+            if (row + nwaves < n) c[row + nwaves] = s1 * alpha;
+        }
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            w0[i] = n0[i];
+            w1[i] = n1[i];
+        }
+    }
+}
+
+int g_num_cus = 0;
+
+}  // namespace
+
+extern "C" {
+
+int doe_f16_gemv(const uint16_t *b_f16, const float *a, float *c, int64_t n, int64_t k, float alpha,
+                 doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n >= 0 && k >= 0 && n <= 0x7fffffff, DOE_E_INVALID, "bad f16_gemv shape");
+    if (n == 0) return DOE_OK;
+    DOE_REQUIRE(c, DOE_E_INVALID, "null output");
+    if (k == 0) {
+        DOE_HIP_CHECK(hipMemsetAsync(c, 0, (size_t)n * 4, (hipStream_t)stream));
+        return DOE_OK;
+    }
+    DOE_REQUIRE(b_f16 && a, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE((k % 8) == 0 && k <= 64 * 8 * 16, DOE_E_UNSUPPORTED,
+                "f16_gemv needs k %% 8 == 0 and k <= 8192 (got %lld)", (long long)k);
+    DOE_REQUIRE(((uintptr_t)b_f16 & 15) == 0 && ((uintptr_t)a & 15) == 0, DOE_E_INVALID,
+                "weights and activation must be 16-byte aligned");
+    if (g_num_cus == 0) {
+        int dev = 0, cus = 0;
+        DOE_HIP_CHECK(hipGetDevice(&dev));
+        DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        g_num_cus = cus > 0 ? cus : 256;
+    }
+    const int pieces = (int)(k / 8);
+    const int p = (pieces + 63) / 64;
+    long waves = (n + 1) / 2;
+    long blocks = (waves + 3) / 4;
+    const long cap = (long)g_num_cus * 4;  // persistent: 16 waves per CU
+    if (blocks > cap) blocks = cap;
+    const hipStream_t st = (hipStream_t)stream;
+    const dim3 grid((unsigned)blocks), blk(256);
+    const uint16_t *bp = b_f16;
+    switch (p) {
+#define DOE_F16_CASE(PP) \
+    case PP: hipLaunchKernelGGL(f16_gemv_kernel<PP>, grid, blk, 0, st, bp, a, c, (int)n, (int)k, alpha); break;
+        DOE_F16_CASE(1) DOE_F16_CASE(2) DOE_F16_CASE(3) DOE_F16_CASE(4) DOE_F16_CASE(5)
+        DOE_F16_CASE(6) DOE_F16_CASE(7) DOE_F16_CASE(8) DOE_F16_CASE(9) DOE_F16_CASE(10)
+        DOE_F16_CASE(11) DOE_F16_CASE(12) DOE_F16_CASE(13) DOE_F16_CASE(14) DOE_F16_CASE(15)
+        DOE_F16_CASE(16)
+#undef DOE_F16_CASE
+        default: return doe::set_error(DOE_E_UNSUPPORTED, "k too large");
+    }
+    DOE_LAUNCH_CHECK("f16_gemv_kernel");
+    return DOE_OK;
+}
+
+}  // extern "C"

@@ -149,11 +149,26 @@ __device__ __forceinline__ void stage_quad(int qd, bool valid, const float *v, u
     *reinterpret_cast<uint2 *>(xl + off) = make_uint2(pack_half2(lo[0], lo[2]), pack_half2(lo[1], lo[3]));
 }
 
-template <int R, int Q>
+// Optional fusions around the GEMV (all off for the plain matmul_q4k op).
+struct GemvFusion {
+    const float *norm_w;    // RMSNorm weight: x <- x * inv_rms * (w or 1 + w)
+    float norm_eps;
+    int norm_offset;        // 1: (1 + w) form
+    const float *residual;  // y[i] += residual[i]
+    int gated;              // rows (2i, 2i+1) -> y[i] = gelu(y_2i) * y_2i+1
+};
+
+__device__ __forceinline__ float gelu_tanh_clamped(float v) {
+    float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    inner = fminf(fmaxf(inner, -15.0f), 15.0f);
+    return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+template <int R, int Q, bool NORM>
 __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restrict__ w,
                                                         const float *__restrict__ x,
                                                         float *__restrict__ y, int n, int k, int nb,
-                                                        int nchunk, int rowslots) {
+                                                        int nchunk, int rowslots, GemvFusion fz) {
     extern __shared__ uint32_t smem[];
     uint32_t *xh = smem;
     uint32_t *xl = xh + nchunk * kLdsChunkDwords;
@@ -161,6 +176,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
     int *sig = reinterpret_cast<int *>(sx + 2 * nchunk);
     float *red = reinterpret_cast<float *>(sig + nchunk);
     const int rows_wg = rowslots * R;
+    float *wsum = red + rows_wg * nchunk;  // [16] per-wave partial sums (RMSNorm)
 
     const int tid = threadIdx.x;
     const int nthreads = blockDim.x;
@@ -198,6 +214,37 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
         qb[r] = load_stream16(p + 32 + 32 * c4);
     }
     __builtin_amdgcn_sched_barrier(0);
+
+    // Fused RMSNorm (the host guarantees Q * nthreads >= nquads): scale the
+    // activation by 1 / sqrt(mean(x^2) + eps) and the norm weight.
+    if (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int it = 0; it < Q; ++it) {
+            const int e = (tid + it * nthreads) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float v = (e + j < k) ? xv[it][j] : 0.0f;
+                ss = fmaf(v, v, ss);
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int i = 0; i < (nthreads >> 6); ++i) tot += wsum[i];
+        const float inv = 1.0f / sqrtf(tot / (float)k + fz.norm_eps);
+#pragma unroll
+        for (int it = 0; it < Q; ++it) {
+            const int e = (tid + it * nthreads) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float nw = fz.norm_w[min(e + j, k - 1)];
+                xv[it][j] = xv[it][j] * inv * (fz.norm_offset ? 1.0f + nw : nw);
+            }
+        }
+    }
 
     // Phase 2: stage the activation once per workgroup.  The 16 quads of a
     // chunk are 16 consecutive lanes and the 8 quads of a sub-block 8 lanes
@@ -277,7 +324,13 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
         s += __shfl_xor(s, 2, 64);
         s += __shfl_xor(s, 4, 64);
         const int row = blockIdx.x * rows_wg + lr;
-        if (l8 == 0 && row < n) y[row] = s;
+        if (fz.gated) {
+            // the partner row (lr ^ 1) is the adjacent 8-lane group of this wave
+            const float other = __shfl_xor(s, 8, 64);
+            if (l8 == 0 && (lr & 1) == 0 && row < n) y[row >> 1] = gelu_tanh_clamped(s) * other;
+        } else if (l8 == 0 && row < n) {
+            y[row] = fz.residual ? s + fz.residual[row] : s;
+        }
     }
 }
 
@@ -295,7 +348,7 @@ struct GemvShape {
 
 size_t gemv_lds_bytes(int nchunk, int rows_wg) {
     return (size_t)nchunk * kLdsChunkDwords * 4 * 2 + (size_t)2 * nchunk * 4 + (size_t)nchunk * 4 +
-           (size_t)rows_wg * nchunk * 4;
+           (size_t)rows_wg * nchunk * 4 + 16 * 4;
 }
 
 GemvShape gemv_shape(int64_t n, int nchunk, int num_cus) {
@@ -351,17 +404,24 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
     return DOE_OK;
 }
 
-int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output, int64_t n,
-                 int64_t k, doe_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+int gemv_launch(const void *weight_q4k, const float *activation, float *output, int64_t n,
+                int64_t k, const GemvFusion &fz, hipStream_t st) {
     int rc = doe::require_init();
     if (rc) return rc;
     DOE_REQUIRE(n >= 0 && k >= 0, DOE_E_INVALID, "negative shape n=%lld k=%lld", (long long)n,
                 (long long)k);
+    DOE_REQUIRE(!fz.gated || (n % 2) == 0, DOE_E_INVALID, "gated GEMV needs an even row count");
+    DOE_REQUIRE(!(fz.gated && fz.residual), DOE_E_UNSUPPORTED, "gated and residual are exclusive");
     if (n == 0) return DOE_OK;
     DOE_REQUIRE(output, DOE_E_INVALID, "null output");
     if (k == 0) {
         // Empty reduction: the sum identity (reference_interpreter.zig:323-327).
-        DOE_HIP_CHECK(hipMemsetAsync(output, 0, (size_t)n * sizeof(float), (hipStream_t)stream));
+        DOE_REQUIRE(!fz.residual && !fz.gated, DOE_E_UNSUPPORTED, "fused epilogues need k > 0");
+        DOE_HIP_CHECK(hipMemsetAsync(output, 0, (size_t)n * sizeof(float), st));
         return DOE_OK;
     }
     DOE_REQUIRE(weight_q4k && activation, DOE_E_INVALID, "null pointer");
@@ -377,19 +437,32 @@ int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
         DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         g_num_cus = cus > 0 ? cus : 256;
     }
-    const GemvShape s = gemv_shape(n, nchunk, g_num_cus);
+    GemvShape s = gemv_shape(n, nchunk, g_num_cus);
+    if (fz.gated && ((s.rowslots * s.rows_per_thread) & 1)) {
+        // a gate/up row pair must not straddle two workgroups
+        if (s.rowslots + 1 <= 1024 / nchunk) s.rowslots += 1;
+        else if (s.rowslots > 1) s.rowslots -= 1;
+        else s.rows_per_thread = 2;
+        s.threads = ((s.rowslots * nchunk + 63) / 64) * 64;
+        s.lds = gemv_lds_bytes(nchunk, s.rowslots * s.rows_per_thread);
+    }
     DOE_REQUIRE(s.lds <= 64 * 1024, DOE_E_UNSUPPORTED, "k=%lld needs %zu bytes of LDS",
                 (long long)k, s.lds);
     const int rows_wg = s.rowslots * s.rows_per_thread;
     const unsigned grid = (unsigned)((n + rows_wg - 1) / rows_wg);
-    const hipStream_t st = (hipStream_t)stream;
     const int nquads = nchunk * 16;
     const int q = (nquads + s.threads - 1) / s.threads;
+    DOE_REQUIRE(!fz.norm_w || q <= 4, DOE_E_UNSUPPORTED, "fused RMSNorm needs k <= %d here",
+                4 * s.threads * 4);
     const int qsel = q <= 1 ? 1 : (q <= 2 ? 2 : 4);
     const uint8_t *wp = (const uint8_t *)weight_q4k;
-#define DOE_GEMV_LAUNCH(RR, QQ)                                                                 \
-    hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ>), dim3(grid), dim3(s.threads), s.lds, st, wp, \
-                       activation, output, (int)n, (int)k, nb, nchunk, s.rowslots)
+#define DOE_GEMV_LAUNCH(RR, QQ)                                                                  \
+    if (fz.norm_w)                                                                                \
+        hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ, true>), dim3(grid), dim3(s.threads), s.lds,  \
+                           st, wp, activation, output, (int)n, (int)k, nb, nchunk, s.rowslots, fz); \
+    else                                                                                          \
+        hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ, false>), dim3(grid), dim3(s.threads), s.lds, \
+                           st, wp, activation, output, (int)n, (int)k, nb, nchunk, s.rowslots, fz)
     switch (s.rows_per_thread * 8 + qsel) {
         case 1 * 8 + 1: DOE_GEMV_LAUNCH(1, 1); break;
         case 1 * 8 + 2: DOE_GEMV_LAUNCH(1, 2); break;
@@ -404,6 +477,23 @@ int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
 #undef DOE_GEMV_LAUNCH
     DOE_LAUNCH_CHECK("q4k_gemv_kernel");
     return DOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output, int64_t n,
+                 int64_t k, doe_stream_t stream) {
+    const GemvFusion fz{nullptr, 0.0f, 0, nullptr, 0};
+    return gemv_launch(weight_q4k, activation, output, n, k, fz, (hipStream_t)stream);
+}
+
+int doe_q4k_gemv_fused(const void *weight_q4k, const float *activation, float *output, int64_t n,
+                       int64_t k, const float *norm_weight, float norm_eps, int norm_weight_offset,
+                       const float *residual, int gated, doe_stream_t stream) {
+    const GemvFusion fz{norm_weight, norm_eps, norm_weight_offset, residual, gated};
+    return gemv_launch(weight_q4k, activation, output, n, k, fz, (hipStream_t)stream);
 }
 
 int doe_tune_set(const char *key, int value) {

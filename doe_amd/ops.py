@@ -78,6 +78,102 @@ def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, out
               sliding_window, _stream_ptr(stream))
 
 
+def matmul_q4k_fused(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int, *,
+                     norm_weight: DeviceBuffer | None = None, norm_eps: float = 1e-6,
+                     norm_weight_offset: bool = True, residual: DeviceBuffer | None = None,
+                     gated: bool = False, stream=None) -> None:
+    """``matmul_q4k`` with its step-list neighbours folded in: an ``rmsnorm``
+    prologue (``norm_weight``), an ``attn_residual``/``ffn_residual``
+    epilogue (``residual``) or a ``gelu_gated`` epilogue over interleaved
+    (gate, up) rows (``gated``: output has n/2 values)."""
+    _q4k_weight_check(weight, n, k)
+    _need(activation, k * 4, "activation")
+    _need(output, (n // 2 if gated else n) * 4, "output")
+    if norm_weight is not None:
+        _need(norm_weight, k * 4, "norm_weight")
+    if residual is not None:
+        _need(residual, n * 4, "residual")
+    nw = C.c_void_p(norm_weight.ptr) if norm_weight is not None else C.c_void_p(None)
+    rs = C.c_void_p(residual.ptr) if residual is not None else C.c_void_p(None)
+    _lib.call("doe_q4k_gemv_fused", _p(weight), _p(activation), _p(output), n, k, nw, norm_eps,
+              int(norm_weight_offset), rs, int(gated), _stream_ptr(stream))
+
+
+def rmsnorm(input: DeviceBuffer, weight: DeviceBuffer, output: DeviceBuffer, rows: int, size: int,
+            eps: float = 1e-6, weight_offset: bool = False, stream=None) -> None:
+    """``rmsnorm`` op: per row x * 1/sqrt(mean(x^2) + eps) * (w or 1 + w)."""
+    _need(input, rows * size * 4, "input")
+    _need(weight, size * 4, "weight")
+    _need(output, rows * size * 4, "output")
+    _lib.call("doe_rmsnorm", _p(input), _p(weight), _p(output), rows, size, eps, int(weight_offset),
+              _stream_ptr(stream))
+
+
+def rope(qk: DeviceBuffer, freq_cis: DeviceBuffer, seq_len: int, num_heads: int, head_dim: int,
+         position_offset: int = 0, position_buffer: DeviceBuffer | None = None, stream=None) -> None:
+    """``rope`` op: rotate-half RoPE in place on qk[seq][heads][head_dim]."""
+    _need(qk, seq_len * num_heads * head_dim * 4, "qk")
+    pb = C.c_void_p(position_buffer.ptr) if position_buffer is not None else C.c_void_p(None)
+    _lib.call("doe_rope", _p(qk), _p(freq_cis), seq_len, num_heads, head_dim, position_offset, pb,
+              _stream_ptr(stream))
+
+
+def gelu_gated(gate: DeviceBuffer, up: DeviceBuffer, output: DeviceBuffer, n: int, stream=None) -> None:
+    """``gelu_gated`` op: gelu_tanh(gate) * up."""
+    for buf, role in ((gate, "gate"), (up, "up"), (output, "output")):
+        _need(buf, n * 4, role)
+    _lib.call("doe_geglu", _p(gate), _p(up), _p(output), n, _stream_ptr(stream))
+
+
+def residual(input: DeviceBuffer, residual_in: DeviceBuffer, output: DeviceBuffer, n: int, stream=None) -> None:
+    """``residual`` op: input + residual."""
+    for buf, role in ((input, "input"), (residual_in, "residual"), (output, "output")):
+        _need(buf, n * 4, role)
+    _lib.call("doe_residual_add", _p(input), _p(residual_in), _p(output), n, _stream_ptr(stream))
+
+
+def sample(logits: DeviceBuffer, n: int, token: DeviceBuffer, workspace: DeviceBuffer, stream=None) -> None:
+    """``sample`` op (greedy): token = argmax(logits), lowest index on ties."""
+    _need(logits, n * 4, "logits")
+    _need(token, 4, "token")
+    _need(workspace, 8192, "workspace")
+    _lib.call("doe_argmax", _p(logits), n, _p(token), _p(workspace), _stream_ptr(stream))
+
+
+def kv_write(key_proj: DeviceBuffer, val_proj: DeviceBuffer, key_cache: DeviceBuffer, val_cache: DeviceBuffer,
+             num_kv_heads: int, max_seq_len: int, head_dim: int, position: int = 0,
+             position_buffer: DeviceBuffer | None = None, kv_layout: int = 0, stream=None) -> None:
+    """``kv_write`` op: cache[h][pos][:] = f16(proj[h][:]) for K and V."""
+    if position_buffer is None and not 0 <= position < max_seq_len:
+        raise ValueError(f"position {position} exceeds max_seq_len {max_seq_len}")
+    _need(key_proj, num_kv_heads * head_dim * 4, "key_proj")
+    _need(val_proj, num_kv_heads * head_dim * 4, "val_proj")
+    _need(key_cache, num_kv_heads * max_seq_len * head_dim * 2, "key_cache")
+    _need(val_cache, num_kv_heads * max_seq_len * head_dim * 2, "val_cache")
+    pb = C.c_void_p(position_buffer.ptr) if position_buffer is not None else C.c_void_p(None)
+    _lib.call("doe_kv_write", _p(key_proj), _p(val_proj), _p(key_cache), _p(val_cache), num_kv_heads,
+              max_seq_len, head_dim, position, pb, kv_layout, _stream_ptr(stream))
+
+
+def embed(table: DeviceBuffer, ids: DeviceBuffer, output: DeviceBuffer, n_ids: int, vocab: int, hidden: int,
+          scale: float = 1.0, stream=None) -> None:
+    """``embed`` op (pattern ``gather``): output[t] = scale * table[ids[t]]."""
+    _need(table, vocab * hidden * 2, "table")
+    _need(ids, n_ids * 4, "ids")
+    _need(output, n_ids * hidden * 4, "output")
+    _lib.call("doe_embed_gather", _p(table), _p(ids), _p(output), n_ids, vocab, hidden, scale,
+              _stream_ptr(stream))
+
+
+def lm_head(weight_f16: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int,
+            alpha: float = 1.0, stream=None) -> None:
+    """f16-weight GEMV (lm_head_gemv): output[n] = alpha * weight[n][k] @ activation[k]."""
+    _need(weight_f16, n * k * 2, "weight")
+    _need(activation, k * 4, "activation")
+    _need(output, n * 4, "output")
+    _lib.call("doe_f16_gemv", _p(weight_f16), _p(activation), _p(output), n, k, alpha, _stream_ptr(stream))
+
+
 def tune(key: str, value: int) -> None:
     """Overrides a launch-shape choice (``doe_tune_set``); 0 restores automatic."""
     _lib.call("doe_tune_set", key.encode(), int(value))
@@ -86,5 +182,13 @@ def tune(key: str, value: int) -> None:
 OPS = {
     "attention": attention,
     "dequant": dequant_q4k,
+    "embed": embed,
+    "gelu_gated": gelu_gated,
+    "kv_write": kv_write,
+    "lm_head": lm_head,
     "matmul_q4k": matmul_q4k,
+    "residual": residual,
+    "rmsnorm": rmsnorm,
+    "rope": rope,
+    "sample": sample,
 }

@@ -104,6 +104,24 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
 int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
                  int64_t n, int64_t k, doe_stream_t stream);
 
+/* Fused decode GEMV: the plain Q4_K GEMV with the neighbouring steps of the
+ * Doppler decode step list folded in (runtime/zig/examples/execution-v1/
+ * gemma-3-270m-smoke.json: input_norm -> q/k/v_proj, o_proj ->
+ * attn_residual, post_attn_norm -> gate/up_proj -> activation, down_proj ->
+ * ffn_residual; the reference's own fused_ffn pattern,
+ * runtime/zig/src/doe_wgsl/emit_csl_fused_ffn.zig, fuses gate/up + activation).
+ *   norm_weight != NULL: activation <- rmsnorm(activation) with eps
+ *     norm_eps, weight w (norm_weight_offset 0) or 1 + w (1), as
+ *     bench/inference-pipeline/kernels/rmsnorm.wgsl:15-93.
+ *   residual != NULL: output[i] = dot_i + residual[i] (residual.wgsl).
+ *   gated != 0: rows come as interleaved (gate, up) pairs; output has n/2
+ *     values gelu_tanh(dot_2i) * dot_2i+1 (gelu_gated.wgsl:1-14).
+ * gated and residual are exclusive; gated needs n even. */
+int doe_q4k_gemv_fused(const void *weight_q4k, const float *activation, float *output,
+                       int64_t n, int64_t k, const float *norm_weight, float norm_eps,
+                       int norm_weight_offset, const float *residual, int gated,
+                       doe_stream_t stream);
+
 /* ---- attention ---------------------------------------------------------------
  * GQA decode attention over an f16 KV cache: one query token per sequence.
  * Replaces the `attention` op (emit_csl_exec_v1.zig:117 -> attention_decode;
@@ -129,6 +147,51 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
                     int64_t num_kv_heads, int64_t head_dim, int64_t kv_len,
                     const int32_t *kv_len_dev, int64_t kv_stride, int kv_layout, float scale,
                     float softcap, int64_t sliding_window, doe_stream_t stream);
+
+/* ---- normalisation, position and elementwise ops ---------------------------
+ * RMSNorm per row: out = x * 1/sqrt(mean(x^2) + eps) * (w or 1 + w).
+ * Replaces the `rmsnorm` op (emit_csl_exec_v1.zig:128; rmsnorm.wgsl:1-93,
+ * bindings input (1) weight (2) output (3), Uniforms size, eps). */
+int doe_rmsnorm(const float *input, const float *weight, float *output, int64_t rows,
+                int64_t size, float eps, int weight_offset, doe_stream_t stream);
+/* RoPE, rotate-half pairs (i, i + D/2) in place on qk[seq][heads][head_dim]
+ * with freq_cis[pos][D/2][2] = (cos, sin); pos = seq index + position_offset
+ * (or + *position_dev when non-NULL).  Replaces the `rope` op (rope.wgsl:1-35:
+ * bindings qk (1) freq_cis (2); Uniforms seq_len, head_dim, num_heads,
+ * position_offset). */
+int doe_rope(float *qk, const float *freq_cis, int64_t seq_len, int64_t num_heads,
+             int64_t head_dim, int64_t position_offset, const int32_t *position_dev,
+             doe_stream_t stream);
+/* out = gelu_tanh(gate) * up (clamped inner, gelu_gated.wgsl:1-14). */
+int doe_geglu(const float *gate, const float *up, float *output, int64_t n, doe_stream_t stream);
+/* out = input + residual (residual.wgsl; run_csl_webgpu_emulator.mjs:482-489). */
+int doe_residual_add(const float *input, const float *residual, float *output, int64_t n,
+                     doe_stream_t stream);
+/* Greedy sample: token = argmax(logits), lowest index on ties (sample.wgsl:
+ * 17-55, run_csl_webgpu_emulator.mjs:841-878).  workspace: >= 8192 device
+ * bytes. */
+int doe_argmax(const float *logits, int64_t n, int32_t *token, void *workspace,
+               doe_stream_t stream);
+/* cache[h][pos][:] = f16(proj[h][:]) for K and V (run_csl_webgpu_emulator.mjs:
+ * 615-644); position from `position` or *position_dev; positions outside
+ * the cache are rejected (host) or skipped (device value). */
+int doe_kv_write(const float *key_proj, const float *val_proj, uint16_t *key_cache,
+                 uint16_t *val_cache, int64_t num_kv_heads, int64_t max_seq_len,
+                 int64_t head_dim, int64_t position, const int32_t *position_dev, int kv_layout,
+                 doe_stream_t stream);
+/* out[t][:] = scale * f32(table[ids[t]][:]), zeros for ids outside the table
+ * (the `embed` op, run_csl_webgpu_emulator.mjs:528-551; gather.wgsl). */
+int doe_embed_gather(const uint16_t *table_f16, const int32_t *ids, float *output,
+                     int64_t n_ids, int64_t vocab, int64_t hidden, float scale,
+                     doe_stream_t stream);
+
+/* ---- f16-weight GEMV (lm_head) -----------------------------------------------
+ * c[n] = alpha * sum_k a[k] * f32(b[n][k]); b f16 row-major (transpose_b = 1).
+ * Replaces lm_head_gemv.wgsl main / main_multicol (runtime/zig/tests/tsir/
+ * real/lm_head_gemv/lm_head_gemv.wgsl:58-180: bindings A (1) B (2) C (3),
+ * Uniforms M, N, K, alpha, transpose_b).  k % 8 == 0, k <= 8192. */
+int doe_f16_gemv(const uint16_t *b_f16, const float *a, float *c, int64_t n, int64_t k,
+                 float alpha, doe_stream_t stream);
 
 /* ---- tuning ----------------------------------------------------------------
  * Overrides a kernel launch-shape choice (0 restores the automatic choice).

@@ -1,0 +1,178 @@
+"""GPU parity of the decode-loop ops (RMSNorm, RoPE, GeGLU, residual, argmax,
+KV write, embed gather, f16 lm_head GEMV, fused Q4_K GEMVs) against the CPU
+oracle, through the C ABI.  Byte/index work and exactly-rounded elementwise
+ops are compared bit-exactly; reductions and transcendentals by rel-L2."""
+import math
+
+import numpy as np
+import pytest
+
+from doe_amd import DeviceBuffer, ops, q4k
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def up(a):
+    return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+@pytest.mark.parametrize("rows,h,offset", [(1, 2304, True), (3, 2304, False), (2, 5, True), (4, 9216, True)])
+def test_rmsnorm(dev, ora, rows, h, offset):
+    rng = np.random.default_rng(h + rows)
+    x = rng.standard_normal((rows, h)).astype(np.float32) * 3
+    w = (0.1 * rng.standard_normal(h)).astype(np.float32)
+    out = DeviceBuffer.empty((rows, h), np.float32)
+    ops.rmsnorm(up(x), up(w), out, rows, h, 1e-6, offset)
+    assert rel_l2(out.download(), ora.rmsnorm(x, w, 1e-6, offset)) < 1e-6
+
+
+def test_rmsnorm_reference_fixture(dev, known_answers):
+    e = known_answers["fixture_rmsnorm"]
+    out = DeviceBuffer.empty((4,), np.float32)
+    ops.rmsnorm(up(np.array(e["input"], np.float32)), up(np.array(e["weight"], np.float32)), out, 1, 4, e["eps"])
+    got = out.download()
+    want = np.array(e["output"], np.float32)
+    assert np.abs(got.view(np.int32) - want.view(np.int32)).max() <= 2
+
+
+def test_rope_bit_exact(dev, ora):
+    rng = np.random.default_rng(2)
+    seq, heads, d, maxpos = 3, 12, 256, 600
+    table = ora.rope_table(maxpos, d, 10000.0)
+    x = rng.standard_normal(seq * heads * d).astype(np.float32)
+    for off in (0, 7, 512):
+        buf = up(x)
+        ops.rope(buf, up(table), seq, heads, d, off)
+        assert np.array_equal(buf.download(), ora.rope(x, table, seq, heads, d, off)), off
+    # device-side position
+    buf = up(x)
+    ops.rope(buf, up(table), seq, heads, d, 0, position_buffer=up(np.array([41], np.int32)))
+    assert np.array_equal(buf.download(), ora.rope(x, table, seq, heads, d, 41))
+
+
+def test_geglu_and_residual(dev, ora):
+    rng = np.random.default_rng(3)
+    n = 9216 * 3 + 5
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    out = DeviceBuffer.empty((n,), np.float32)
+    ops.gelu_gated(up(g), up(u), out, n)
+    assert rel_l2(out.download(), ora.geglu(g, u)) < 1e-6
+    ops.residual(up(g), up(u), out, n)
+    assert np.array_equal(out.download(), ora.residual(g, u))
+
+
+def test_argmax(dev, ora, known_answers):
+    ws = DeviceBuffer(8192)
+    tok = DeviceBuffer.empty((1,), np.int32)
+    e = known_answers["emulator_sample"]
+    for logits in (e["logits"], e["tie_logits"]):
+        x = np.array(logits, np.float32)
+        ops.sample(up(x), x.size, tok, ws)
+        assert tok.download()[0] == ora.argmax(x)
+    rng = np.random.default_rng(4)
+    for n in (1, 255, 256000):
+        x = rng.standard_normal(n).astype(np.float32)
+        ops.sample(up(x), n, tok, ws)
+        assert tok.download()[0] == ora.argmax(x)
+    # ties at the maximum: lowest index wins; NaN never wins; all -inf -> 0
+    x = np.zeros(100000, np.float32)
+    x[[99999, 31337, 777]] = 5.0
+    x[5] = np.nan
+    ops.sample(up(x), x.size, tok, ws)
+    assert tok.download()[0] == 777
+    x = np.full(1000, -np.inf, np.float32)
+    ops.sample(up(x), x.size, tok, ws)
+    assert tok.download()[0] == 0
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_kv_write_bit_exact(dev, ora, layout):
+    rng = np.random.default_rng(5)
+    kvh, maxs, d = 4, 64, 256
+    kp = (rng.standard_normal((kvh, d)) * 100).astype(np.float32)
+    vp = rng.standard_normal((kvh, d)).astype(np.float32)
+    shape = (kvh, maxs, d) if layout == 0 else (maxs, kvh, d)
+    kc_h = np.zeros(shape, np.float16)
+    vc_h = np.zeros(shape, np.float16)
+    kc, vc = up(kc_h), up(vc_h)
+    ops.kv_write(up(kp), up(vp), kc, vc, kvh, maxs, d, 13, kv_layout=layout)
+    ops.kv_write(up(kp * 2), up(vp * 2), kc, vc, kvh, maxs, d, 0, position_buffer=up(np.array([20], np.int32)),
+                 kv_layout=layout)
+    ora.kv_write(kp, vp, kc_h, vc_h, kvh, maxs, d, 13, layout)
+    ora.kv_write(kp * 2, vp * 2, kc_h, vc_h, kvh, maxs, d, 20, layout)
+    assert np.array_equal(kc.download().view(np.uint16), kc_h.view(np.uint16))
+    assert np.array_equal(vc.download().view(np.uint16), vc_h.view(np.uint16))
+
+
+def test_embed_gather_bit_exact(dev, ora):
+    rng = np.random.default_rng(6)
+    vocab, hidden = 1000, 2304
+    table = (rng.standard_normal((vocab, hidden)) * 0.02).astype(np.float16)
+    ids = np.array([5, 999, 0, 1000, -3, 512], np.int32)
+    out = DeviceBuffer.empty((ids.size, hidden), np.float32)
+    ops.embed(up(table), up(ids), out, ids.size, vocab, hidden)
+    assert np.array_equal(out.download(), ora.embed_gather(table, ids))
+    ops.embed(up(table), up(ids), out, ids.size, vocab, hidden, scale=48.0)
+    assert np.array_equal(out.download(), ora.embed_gather(table, ids, 48.0))
+
+
+@pytest.mark.parametrize("n,k", [(256000 // 8, 2304), (1000, 2304), (7, 8), (100, 5120), (33, 512)])
+def test_f16_gemv(dev, ora, n, k):
+    rng = np.random.default_rng(n + k)
+    b = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    a = rng.standard_normal(k).astype(np.float32)
+    out = DeviceBuffer.empty((n,), np.float32)
+    ops.lm_head(up(b), up(a), out, n, k, alpha=0.5)
+    assert rel_l2(out.download(), ora.f16_gemv(b, a, 0.5)) < 1e-5
+
+
+def test_f16_gemv_full_vocab_shape(dev):
+    # 256000 x 2304 (the 2B-class lm_head): float64 check on sampled rows
+    rng = np.random.default_rng(7)
+    n, k = 256000, 2304
+    b = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float16)
+    a = rng.standard_normal(k).astype(np.float32)
+    out = DeviceBuffer.empty((n,), np.float32)
+    ops.lm_head(up(b), up(a), out, n, k)
+    got = out.download()
+    rows = rng.integers(0, n, 2000)
+    want = b[rows].astype(np.float64) @ a.astype(np.float64)
+    assert rel_l2(got[rows], want) < 1e-5
+
+
+def test_fused_gemv_norm_residual_gated(dev, ora):
+    rng = np.random.default_rng(8)
+    k = 2304
+    x = (rng.standard_normal(k) * 5).astype(np.float32)
+    nw = (0.1 * rng.standard_normal(k)).astype(np.float32)
+    xn = ora.rmsnorm(x, nw, 1e-6, True)
+    # norm prologue: QKV-shaped GEMV (4096 rows)
+    n = 4096
+    w = q4k.random_q4k(rng, n, k)
+    out = DeviceBuffer.empty((n,), np.float32)
+    ops.matmul_q4k_fused(up(w), up(x), out, n, k, norm_weight=up(nw), norm_eps=1e-6, norm_weight_offset=True)
+    assert rel_l2(out.download(), ora.q4k_gemv(w, xn, n, k)) < 1e-5
+    # residual epilogue: O-projection shape
+    n2, k2 = 2304, 2048
+    w2 = q4k.random_q4k(rng, n2, k2)
+    x2 = rng.standard_normal(k2).astype(np.float32)
+    res = rng.standard_normal(n2).astype(np.float32)
+    out2 = DeviceBuffer.empty((n2,), np.float32)
+    ops.matmul_q4k_fused(up(w2), up(x2), out2, n2, k2, residual=up(res))
+    want2 = ora.residual(ora.q4k_gemv(w2, x2, n2, k2), res)
+    assert rel_l2(out2.download(), want2) < 1e-5
+    # gated epilogue with the norm prologue: interleaved gate/up rows
+    ff = 9216
+    wg = q4k.random_q4k(rng, 2 * ff, k)
+    out3 = DeviceBuffer.empty((ff,), np.float32)
+    ops.matmul_q4k_fused(up(wg), up(x), out3, 2 * ff, k, norm_weight=up(nw), norm_eps=1e-6, gated=True)
+    y = ora.q4k_gemv(wg, xn, 2 * ff, k)
+    want3 = ora.geglu(y[0::2], y[1::2])
+    assert rel_l2(out3.download(), want3) < 1e-5
