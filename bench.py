@@ -184,6 +184,52 @@ def bench_attention(args, doe):
     }
 
 
+def bench_decode(args, doe):
+    """2B-class decode loop at batch 1 (26 layers, hidden 2304, 8/4 heads of
+    256, FFN 9216 GeGLU, Q4_K projections, f16 lm_head over 256000): a
+    128-token prompt then `--decode-steps` greedy steps, each step a replay of
+    a captured HIP graph; tokens/s over the decode steps (HIP events)."""
+    from doe_amd import Stream
+    from doe_amd.model import Decoder, DecoderConfig
+
+    cfg = DecoderConfig()
+    dec = Decoder(cfg)
+    dec.init_random(seed=2)
+    rng = np.random.default_rng(2)
+    prompt = rng.integers(0, cfg.vocab, args.prompt_len, dtype=np.int64).astype(np.int32)
+    s = Stream()
+    dec.reset(prompt)
+    dec.step(s)  # allocates the attention workspace outside capture
+    s.synchronize()
+    spg = args.steps_per_graph  # 0: eager launches (no graph), e.g. under a profiler
+    graph = dec.capture(s, spg) if spg > 0 else None
+    dec.generate(prompt, min(16, args.decode_steps), s, graph=graph, steps_per_graph=max(spg, 1))  # warm
+    timing = {}
+    ids = dec.generate(prompt, args.decode_steps, s, graph=graph, steps_per_graph=max(spg, 1), timing=timing)
+    if graph is not None:
+        graph.destroy()
+    tok_s = args.decode_steps / timing["decode_s"]
+    mean_len = args.prompt_len + (args.decode_steps + 1) / 2.0
+    bpt = cfg.decode_bytes_per_token(mean_len)
+    gbs = bpt * tok_s / 1e9
+    log(f"decode: {tok_s:.1f} tok/s ({timing['decode_s'] * 1e3 / args.decode_steps:.3f} ms/token), "
+        f"prompt {timing['prompt_s']:.3f} s, {gbs:.0f} GB/s of algorithmic bytes")
+    return {
+        "workload": f"2B-class decoder bs=1: {cfg.layers} layers, hidden {cfg.hidden}, {cfg.heads}/{cfg.kv_heads} "
+                    f"heads x {cfg.head_dim}, FFN {cfg.ffn} GeGLU, vocab {cfg.vocab}; Q4_K projections, f16 "
+                    f"lm_head, f16 KV; prompt {args.prompt_len} then {args.decode_steps} greedy steps; "
+                    f"random-init weights; " + (f"{spg} steps per HIP graph" if spg > 0 else "eager launches"),
+        "tok_s": round(tok_s, 2),
+        "ms_per_token": round(timing["decode_s"] * 1e3 / args.decode_steps, 4),
+        "bytes_per_token": int(bpt),
+        "achieved_gbs": round(gbs, 1),
+        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "ceiling_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
+        "prompt_s": round(timing["prompt_s"], 4),
+        "last_tokens": [int(t) for t in ids[-4:]],
+    }
+
+
 def traffic_bytes(summary: str):
     """HBM bytes per launch recorded in a committed rocprofv3 summary
     (line `traffic_bytes_per_launch: <int>`), or None."""
@@ -228,6 +274,10 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=64)
     ap.add_argument("--attn-copies", type=int, default=48)
     ap.add_argument("--attn-steps", type=int, default=480)
+    ap.add_argument("--prompt-len", type=int, default=128)
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--steps-per-graph", type=int, default=8)
+    ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -250,6 +300,7 @@ def main() -> int:
 
     g = bench_gemv(args, doe_amd)
     att = bench_attention(args, doe_amd)
+    dec = None if args.no_decode else bench_decode(args, doe_amd)
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of the single-threaded oracle")
@@ -287,6 +338,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "attention_decode": att,
+        "decode": dec,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -71,6 +71,8 @@ SIGNATURES: dict[str, list] = {
     "doe_attn_decode": [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i32,
                         _f32, _f32, _i64, _vp],
     "doe_q4k_gemv_fused": [_vp, _vp, _vp, _i64, _i64, _vp, _f32, _i32, _vp, _i32, _vp],
+    "doe_q4k_gemv_qkv_rope_kv": [_vp, _vp, _vp, _i64, _vp, _f32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64,
+                                 _vp],
     "doe_rmsnorm": [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp],
     "doe_rope": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp],
     "doe_geglu": [_vp, _vp, _vp, _i64, _vp],
@@ -79,6 +81,12 @@ SIGNATURES: dict[str, list] = {
     "doe_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _vp],
     "doe_embed_gather": [_vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp],
     "doe_f16_gemv": [_vp, _vp, _vp, _i64, _i64, _f32, _vp],
+    "doe_f16_gemv_argmax": [_vp, _vp, _vp, _i64, _i64, _f32, _vp, _f32, _i32, _vp, _i64, C.POINTER(_i32), _vp],
+    "doe_fill_normal_f16": [_vp, _i64, C.c_uint64, _f32, _f32, _vp],
+    "doe_fill_normal_f32": [_vp, _i64, C.c_uint64, _f32, _f32, _vp],
+    "doe_fill_uniform_i32": [_vp, _i64, C.c_uint64, _i32, _i32, _vp],
+    "doe_fill_random_q4k": [_vp, _i64, C.c_uint64, _f32, _f32, _vp],
+    "doe_decode_advance": [_vp, _vp, _vp, _i64, _vp, _i32, _vp],
     "doe_tune_set": [C.c_char_p, _i32],
 }
 

@@ -48,18 +48,37 @@ __device__ __forceinline__ float row_dot(const u32x4 (&w)[P], const uint32_t (&x
     return a0 + a1;
 }
 
+// Argmax keys (see elementwise.hip): ordered float bits high, inverted index
+// low; the unsigned max is the largest logit at the lowest index; NaN never wins.
+__device__ __forceinline__ unsigned long long argmax_key(float v, unsigned idx) {
+    if (v != v) return 0ull;
+    unsigned u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (0xffffffffu - idx);
+}
+
+// Optional fusions: RMSNorm of the activation (every wave holds the whole
+// activation, so it normalises on its own) and a per-workgroup argmax
+// partial (the greedy sample over the output).
+struct F16Fusion {
+    const float *norm_w;
+    float norm_eps;
+    int norm_offset;
+    unsigned long long *argmax_part;  // [gridDim.x] best key per workgroup
+};
+
 template <int P>
 __global__ __launch_bounds__(256) void f16_gemv_kernel(const uint16_t *__restrict__ b,
                                                        const float *__restrict__ a,
                                                        float *__restrict__ c, int n, int k,
-                                                       float alpha) {
+                                                       float alpha, F16Fusion fz) {
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int nwaves = gridDim.x * 4;
     const int npieces = k >> 3;
 
-    // activation slices of this lane, f16 hi/lo pairs; pieces past k are zero
-    uint32_t xh[P][4], xl[P][4];
+    // activation slices of this lane; pieces past k are zero
+    float xs[P][8];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
         const int p = lane + 64 * i;
@@ -68,8 +87,35 @@ __global__ __launch_bounds__(256) void f16_gemv_kernel(const uint16_t *__restric
         const float4 lo4 = src[0], hi4 = src[1];
         const float v[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
 #pragma unroll
+        for (int j = 0; j < 8; ++j) xs[i][j] = ok ? v[j] : 0.0f;
+    }
+    if (fz.norm_w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss = fmaf(xs[i][j], xs[i][j], ss);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float inv = 1.0f / sqrtf(ss / (float)k + fz.norm_eps);
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int p = min(lane + 64 * i, npieces - 1);
+            const float4 *ws = reinterpret_cast<const float4 *>(fz.norm_w + 8 * p);
+            const float4 w0 = ws[0], w1 = ws[1];
+            const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xs[i][j] = xs[i][j] * inv * (fz.norm_offset ? 1.0f + wv[j] : wv[j]);
+        }
+    }
+
+    // f16 hi/lo pairs
+    uint32_t xh[P][4], xl[P][4];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+#pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float x0 = ok ? v[2 * j] : 0.0f, x1 = ok ? v[2 * j + 1] : 0.0f;
+            const float x0 = xs[i][2 * j], x1 = xs[i][2 * j + 1];
             const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
             xh[i][j] = pack2(h0, h1);
             xl[i][j] = pack2((_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1));
@@ -88,6 +134,7 @@ __global__ __launch_bounds__(256) void f16_gemv_kernel(const uint16_t *__restric
             d1[i] = load16(b + (size_t)r1 * k + 8 * p);
         }
     };
+    unsigned long long best = 0;
     if (row < n) load_rows(row, w0, w1);
     for (; row < n; row += 2 * nwaves) {
         u32x4 n0[P], n1[P];
@@ -107,9 +154,16 @@ __global__ __launch_bounds__(256) void f16_gemv_kernel(const uint16_t *__restric
             s0 += __shfl_xor(s0, o, 64);
             s1 += __shfl_xor(s1, o, 64);
         }
-        if (lane == 0) {
-            c[row] = s0 * alpha;
-            if (row + nwaves < n) c[row + nwaves] = s1 * alpha;
+        s0 *= alpha;
+        s1 *= alpha;
+        if (lane == 0 && c) {
+            c[row] = s0;
+            if (row + nwaves < n) c[row + nwaves] = s1;
+        }
+        best = argmax_key(s0, (unsigned)row) > best ? argmax_key(s0, (unsigned)row) : best;
+        if (row + nwaves < n) {
+            const unsigned long long k1 = argmax_key(s1, (unsigned)(row + nwaves));
+            best = k1 > best ? k1 : best;
         }
 #pragma unroll
         for (int i = 0; i < P; ++i) {
@@ -117,30 +171,38 @@ __global__ __launch_bounds__(256) void f16_gemv_kernel(const uint16_t *__restric
             w1[i] = n1[i];
         }
     }
+    if (fz.argmax_part) {
+        __shared__ unsigned long long wb[4];
+        if (lane == 0) wb[threadIdx.x >> 6] = best;  // identical in every lane of the wave
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long m = wb[0];
+            for (int i = 1; i < 4; ++i) m = wb[i] > m ? wb[i] : m;
+            fz.argmax_part[blockIdx.x] = m;
+        }
+    }
 }
 
 int g_num_cus = 0;
 
-}  // namespace
-
-extern "C" {
-
-int doe_f16_gemv(const uint16_t *b_f16, const float *a, float *c, int64_t n, int64_t k, float alpha,
-                 doe_stream_t stream) {
+int f16_launch(const uint16_t *b_f16, const float *a, float *c, int64_t n, int64_t k, float alpha,
+               const F16Fusion &fz, hipStream_t st, long max_blocks, unsigned *blocks_out) {
     int rc = doe::require_init();
     if (rc) return rc;
     DOE_REQUIRE(n >= 0 && k >= 0 && n <= 0x7fffffff, DOE_E_INVALID, "bad f16_gemv shape");
     if (n == 0) return DOE_OK;
-    DOE_REQUIRE(c, DOE_E_INVALID, "null output");
+    DOE_REQUIRE(c || fz.argmax_part, DOE_E_INVALID, "null output");
     if (k == 0) {
-        DOE_HIP_CHECK(hipMemsetAsync(c, 0, (size_t)n * 4, (hipStream_t)stream));
+        DOE_REQUIRE(c && !fz.argmax_part, DOE_E_UNSUPPORTED, "k == 0 with argmax");
+        DOE_HIP_CHECK(hipMemsetAsync(c, 0, (size_t)n * 4, st));
         return DOE_OK;
     }
     DOE_REQUIRE(b_f16 && a, DOE_E_INVALID, "null pointer");
     DOE_REQUIRE((k % 8) == 0 && k <= 64 * 8 * 16, DOE_E_UNSUPPORTED,
                 "f16_gemv needs k %% 8 == 0 and k <= 8192 (got %lld)", (long long)k);
-    DOE_REQUIRE(((uintptr_t)b_f16 & 15) == 0 && ((uintptr_t)a & 15) == 0, DOE_E_INVALID,
-                "weights and activation must be 16-byte aligned");
+    DOE_REQUIRE(((uintptr_t)b_f16 & 15) == 0 && ((uintptr_t)a & 15) == 0 &&
+                    ((uintptr_t)fz.norm_w & 15) == 0,
+                DOE_E_INVALID, "weights, activation and norm weight must be 16-byte aligned");
     if (g_num_cus == 0) {
         int dev = 0, cus = 0;
         DOE_HIP_CHECK(hipGetDevice(&dev));
@@ -153,12 +215,12 @@ int doe_f16_gemv(const uint16_t *b_f16, const float *a, float *c, int64_t n, int
     long blocks = (waves + 3) / 4;
     const long cap = (long)g_num_cus * 4;  // persistent: 16 waves per CU
     if (blocks > cap) blocks = cap;
-    const hipStream_t st = (hipStream_t)stream;
+    if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
+    if (blocks_out) *blocks_out = (unsigned)blocks;
     const dim3 grid((unsigned)blocks), blk(256);
-    const uint16_t *bp = b_f16;
     switch (p) {
 #define DOE_F16_CASE(PP) \
-    case PP: hipLaunchKernelGGL(f16_gemv_kernel<PP>, grid, blk, 0, st, bp, a, c, (int)n, (int)k, alpha); break;
+    case PP: hipLaunchKernelGGL(f16_gemv_kernel<PP>, grid, blk, 0, st, b_f16, a, c, (int)n, (int)k, alpha, fz); break;
         DOE_F16_CASE(1) DOE_F16_CASE(2) DOE_F16_CASE(3) DOE_F16_CASE(4) DOE_F16_CASE(5)
         DOE_F16_CASE(6) DOE_F16_CASE(7) DOE_F16_CASE(8) DOE_F16_CASE(9) DOE_F16_CASE(10)
         DOE_F16_CASE(11) DOE_F16_CASE(12) DOE_F16_CASE(13) DOE_F16_CASE(14) DOE_F16_CASE(15)
@@ -168,6 +230,30 @@ int doe_f16_gemv(const uint16_t *b_f16, const float *a, float *c, int64_t n, int
     }
     DOE_LAUNCH_CHECK("f16_gemv_kernel");
     return DOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int doe_f16_gemv(const uint16_t *b_f16, const float *a, float *c, int64_t n, int64_t k, float alpha,
+                 doe_stream_t stream) {
+    const F16Fusion fz{nullptr, 0.0f, 0, nullptr};
+    return f16_launch(b_f16, a, c, n, k, alpha, fz, (hipStream_t)stream, 0, nullptr);
+}
+
+int doe_f16_gemv_argmax(const uint16_t *b_f16, const float *a, float *logits, int64_t n, int64_t k,
+                        float alpha, const float *norm_weight, float norm_eps, int norm_weight_offset,
+                        uint64_t *argmax_partials, int64_t partials_capacity, int32_t *num_partials,
+                        doe_stream_t stream) {
+    DOE_REQUIRE(argmax_partials && partials_capacity >= 1024, DOE_E_INVALID,
+                "argmax partials need room for 1024 keys");
+    const F16Fusion fz{norm_weight, norm_eps, norm_weight_offset, (unsigned long long *)argmax_partials};
+    unsigned blocks = 0;
+    const long cap = partials_capacity > 0x7fffffff ? 0x7fffffffL : (long)partials_capacity;
+    int rc = f16_launch(b_f16, a, logits, n, k, alpha, fz, (hipStream_t)stream, cap, &blocks);
+    if (num_partials) *num_partials = (int32_t)blocks;
+    return rc;
 }
 
 }  // extern "C"

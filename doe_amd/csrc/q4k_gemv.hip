@@ -156,12 +156,51 @@ struct GemvFusion {
     int norm_offset;        // 1: (1 + w) form
     const float *residual;  // y[i] += residual[i]
     int gated;              // rows (2i, 2i+1) -> y[i] = gelu(y_2i) * y_2i+1
+    // RoPE + KV-cache write over a fused [q; k; v] projection whose q and k
+    // rows come as interleaved rotation pairs (row 2i = dim i, row 2i+1 =
+    // dim i + head_dim/2 of the rotate-half form): pairs of q/k rows are
+    // rotated by freq_cis[pos][i]; k and v rows are also stored as f16 into
+    // the caches [kv_heads][max_seq][head_dim] at pos.
+    int rope_kv;
+    const float *freq_cis;
+    const int32_t *pos_dev;
+    _Float16 *k_cache, *v_cache;
+    int q_rows, kv_rows, head_dim, max_seq;
 };
 
 __device__ __forceinline__ float gelu_tanh_clamped(float v) {
     float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
     inner = fminf(fmaxf(inner, -15.0f), 15.0f);
     return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+// Epilogue of one (even row, odd row) pair of a fused q/k/v projection.
+__device__ __forceinline__ void rope_kv_pair(const GemvFusion &fz, int row, float s0, float s1,
+                                             float *__restrict__ y) {
+#pragma clang fp contract(off)
+    const int pos = fz.pos_dev[0];
+    const bool in_cache = pos >= 0 && pos < fz.max_seq;  // freq_cis holds max_seq positions
+    float r0 = s0, r1 = s1;
+    const int dim = row % fz.head_dim;
+    if (in_cache && row < fz.q_rows + fz.kv_rows) {
+        const int i = dim >> 1, half = fz.head_dim >> 1;
+        const float c = fz.freq_cis[((size_t)pos * half + i) * 2];
+        const float sn = fz.freq_cis[((size_t)pos * half + i) * 2 + 1];
+        r0 = s0 * c - s1 * sn;
+        r1 = s0 * sn + s1 * c;
+    }
+    y[row] = r0;
+    y[row + 1] = r1;
+    if (row >= fz.q_rows && in_cache) {
+        const int kvr = row - fz.q_rows;
+        const bool is_v = kvr >= fz.kv_rows;
+        const int rr = is_v ? kvr - fz.kv_rows : kvr;
+        const int h = rr / fz.head_dim;
+        _Float16 *cache = is_v ? fz.v_cache : fz.k_cache;
+        const size_t ci = ((size_t)h * fz.max_seq + pos) * fz.head_dim + dim;
+        cache[ci] = (_Float16)r0;
+        cache[ci + 1] = (_Float16)r1;
+    }
 }
 
 template <int R, int Q, bool NORM>
@@ -202,6 +241,15 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
 #pragma unroll
         for (int j = 0; j < 4; ++j) xv[it][j] = x[min(e + j, k - 1)];  // masked when staged
     }
+    float nwv[NORM ? Q : 1][4];
+    if (NORM) {
+#pragma unroll
+        for (int it = 0; it < Q; ++it) {
+            const int e = (tid + it * nthreads) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) nwv[it][j] = fz.norm_w[min(e + j, k - 1)];
+        }
+    }
     // keep the activation loads ahead of the weight loads in issue order
     __builtin_amdgcn_sched_barrier(0);
     uint4 hdr[R], qa[R], qb[R];
@@ -237,10 +285,9 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
         const float inv = 1.0f / sqrtf(tot / (float)k + fz.norm_eps);
 #pragma unroll
         for (int it = 0; it < Q; ++it) {
-            const int e = (tid + it * nthreads) * 4;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float nw = fz.norm_w[min(e + j, k - 1)];
+                const float nw = nwv[it][j];
                 xv[it][j] = xv[it][j] * inv * (fz.norm_offset ? 1.0f + nw : nw);
             }
         }
@@ -328,6 +375,9 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
             // the partner row (lr ^ 1) is the adjacent 8-lane group of this wave
             const float other = __shfl_xor(s, 8, 64);
             if (l8 == 0 && (lr & 1) == 0 && row < n) y[row >> 1] = gelu_tanh_clamped(s) * other;
+        } else if (fz.rope_kv) {
+            const float other = __shfl_xor(s, 8, 64);
+            if (l8 == 0 && (lr & 1) == 0 && row < n) rope_kv_pair(fz, row, s, other, y);
         } else if (l8 == 0 && row < n) {
             y[row] = fz.residual ? s + fz.residual[row] : s;
         }
@@ -367,7 +417,7 @@ GemvShape gemv_shape(int64_t n, int nchunk, int num_cus) {
     } else {
         const int64_t rows_per_cu = (n + num_cus - 1) / num_cus;
         int64_t want = (rows_per_cu + r - 1) / r;
-        if (want * nchunk > 640 && nchunk < 96) want = (want + 1) / 2;
+        while (want * nchunk > 640 && nchunk < 96 && want > 4) want = (want + 1) / 2;
         slots = (int)(want < 4 ? 4 : want);
     }
     if (slots > max_slots) slots = max_slots;
@@ -415,6 +465,8 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     DOE_REQUIRE(n >= 0 && k >= 0, DOE_E_INVALID, "negative shape n=%lld k=%lld", (long long)n,
                 (long long)k);
     DOE_REQUIRE(!fz.gated || (n % 2) == 0, DOE_E_INVALID, "gated GEMV needs an even row count");
+    DOE_REQUIRE(!(fz.gated && fz.rope_kv) && !(fz.rope_kv && fz.residual), DOE_E_UNSUPPORTED,
+                "rope/kv epilogue excludes gated and residual");
     DOE_REQUIRE(!(fz.gated && fz.residual), DOE_E_UNSUPPORTED, "gated and residual are exclusive");
     if (n == 0) return DOE_OK;
     DOE_REQUIRE(output, DOE_E_INVALID, "null output");
@@ -438,7 +490,7 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         g_num_cus = cus > 0 ? cus : 256;
     }
     GemvShape s = gemv_shape(n, nchunk, g_num_cus);
-    if (fz.gated && ((s.rowslots * s.rows_per_thread) & 1)) {
+    if ((fz.gated || fz.rope_kv) && ((s.rowslots * s.rows_per_thread) & 1)) {
         // a gate/up row pair must not straddle two workgroups
         if (s.rowslots + 1 <= 1024 / nchunk) s.rowslots += 1;
         else if (s.rowslots > 1) s.rowslots -= 1;
@@ -485,15 +537,47 @@ extern "C" {
 
 int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output, int64_t n,
                  int64_t k, doe_stream_t stream) {
-    const GemvFusion fz{nullptr, 0.0f, 0, nullptr, 0};
+    GemvFusion fz{};
     return gemv_launch(weight_q4k, activation, output, n, k, fz, (hipStream_t)stream);
 }
 
 int doe_q4k_gemv_fused(const void *weight_q4k, const float *activation, float *output, int64_t n,
                        int64_t k, const float *norm_weight, float norm_eps, int norm_weight_offset,
                        const float *residual, int gated, doe_stream_t stream) {
-    const GemvFusion fz{norm_weight, norm_eps, norm_weight_offset, residual, gated};
+    GemvFusion fz{};
+    fz.norm_w = norm_weight;
+    fz.norm_eps = norm_eps;
+    fz.norm_offset = norm_weight_offset;
+    fz.residual = residual;
+    fz.gated = gated;
     return gemv_launch(weight_q4k, activation, output, n, k, fz, (hipStream_t)stream);
+}
+
+int doe_q4k_gemv_qkv_rope_kv(const void *weight_q4k, const float *activation, float *output,
+                             int64_t hidden, const float *norm_weight, float norm_eps,
+                             int norm_weight_offset, int64_t num_heads, int64_t num_kv_heads,
+                             int64_t head_dim, const float *freq_cis, const int32_t *position_dev,
+                             uint16_t *key_cache, uint16_t *val_cache, int64_t max_seq_len,
+                             doe_stream_t stream) {
+    DOE_REQUIRE(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && (head_dim % 2) == 0 &&
+                    max_seq_len > 0,
+                DOE_E_INVALID, "bad qkv shape");
+    DOE_REQUIRE(freq_cis && position_dev && key_cache && val_cache, DOE_E_INVALID, "null pointer");
+    GemvFusion fz{};
+    fz.norm_w = norm_weight;
+    fz.norm_eps = norm_eps;
+    fz.norm_offset = norm_weight_offset;
+    fz.rope_kv = 1;
+    fz.freq_cis = freq_cis;
+    fz.pos_dev = position_dev;
+    fz.k_cache = (_Float16 *)key_cache;
+    fz.v_cache = (_Float16 *)val_cache;
+    fz.q_rows = (int)(num_heads * head_dim);
+    fz.kv_rows = (int)(num_kv_heads * head_dim);
+    fz.head_dim = (int)head_dim;
+    fz.max_seq = (int)max_seq_len;
+    const int64_t n = (num_heads + 2 * num_kv_heads) * head_dim;
+    return gemv_launch(weight_q4k, activation, output, n, hidden, fz, (hipStream_t)stream);
 }
 
 int doe_tune_set(const char *key, int value) {

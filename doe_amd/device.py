@@ -82,6 +82,9 @@ class DeviceBuffer:
         _lib.call("doe_memcpy_d2d", C.c_void_p(self.ptr), C.c_void_p(other.ptr), self.nbytes,
                   _stream_ptr(stream))
 
+    def view(self, offset: int, nbytes: int, dtype=np.uint8, shape=None) -> DeviceView:
+        return DeviceView(self, offset, nbytes, dtype, shape)
+
     def fill_zero(self, stream: "Stream | None" = None) -> None:
         _lib.call("doe_memset", C.c_void_p(self.ptr), 0, self.nbytes, _stream_ptr(stream))
 
@@ -97,6 +100,35 @@ class DeviceBuffer:
                 self._ptr = None
         except Exception:
             pass
+
+
+class DeviceView:
+    """A non-owning window [offset, offset + nbytes) into a DeviceBuffer,
+    usable wherever an op takes a buffer (binding at a byte offset)."""
+
+    def __init__(self, base: "DeviceBuffer", offset: int, nbytes: int, dtype=np.uint8, shape=None):
+        if offset < 0 or nbytes < 0 or offset + nbytes > base.nbytes:
+            raise ValueError(f"view [{offset}, {offset + nbytes}) outside a {base.nbytes}-byte buffer")
+        self.base = base
+        self.offset = int(offset)
+        self.nbytes = int(nbytes)
+        self.dtype = np.dtype(dtype)
+        self.shape = shape if shape is not None else (self.nbytes // self.dtype.itemsize,)
+
+    @property
+    def ptr(self) -> int:
+        return self.base.ptr + self.offset
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        _lib.call("doe_memcpy_d2h", out.ctypes.data_as(C.c_void_p), C.c_void_p(self.ptr), self.nbytes)
+        return out
+
+    def upload(self, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        if arr.nbytes != self.nbytes:
+            raise ValueError(f"upload of {arr.nbytes} bytes into a {self.nbytes}-byte view")
+        _lib.call("doe_memcpy_h2d", C.c_void_p(self.ptr), arr.ctypes.data_as(C.c_void_p), self.nbytes)
 
 
 class Stream:

@@ -1,0 +1,242 @@
+"""A Gemma-style decoder driven through the C ABI: the 2B-class decode loop.
+
+Step order follows the reference's execution-v1 decode step list
+(runtime/zig/examples/execution-v1/gemma-3-270m-smoke.json: embed;
+per layer input_norm, q/k/v_proj, rope_q/rope_k, attention, o_proj,
+attn_residual, post_attn_norm, gate/up_proj, activation (GeGLU), down_proj,
+ffn_residual; final norm, lm_head, sample).  On the MI355X the neighbouring
+steps are fused into the Q4_K GEMVs (a kernel boundary costs ~1.8 us here,
+an in-kernel grid barrier more), five dispatches per layer:
+
+  1. qkv   = Wqkv . rmsnorm(x), RoPE on q/k, k and v stored into the f16
+             caches at pos              (q/k rows interleaved rotation pairs)
+  2. attn  = attention(q, K cache, V cache, kv_len = pos + 1)
+  3. x     = Wo . attn + x                (residual epilogue)
+  4. h     = gelu(Wg . n) * (Wu . n), n = rmsnorm(x)   (gate/up rows
+             interleaved, GeGLU epilogue)
+  5. x     = Wd . h + x                   (residual epilogue)
+
+then the lm_head over rmsnorm(x) with per-workgroup argmax partials, and an
+on-device advance that reduces them to the token and moves (pos, kv_len,
+next token).  The whole step is captured once into a HIP graph and replayed;
+nothing returns to the host until generation ends.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib, ops
+from . import q4k as _q4k
+from .device import DeviceBuffer, Event, Graph, Stream, _stream_ptr
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    layers: int = 26
+    hidden: int = 2304
+    heads: int = 8
+    kv_heads: int = 4
+    head_dim: int = 256
+    ffn: int = 9216
+    vocab: int = 256000
+    eps: float = 1e-6
+    rope_base: float = 10000.0
+    max_seq: int = 384
+    embed_scale: float = 1.0
+
+    @property
+    def q_dim(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.kv_heads * self.head_dim
+
+    @property
+    def qkv_rows(self) -> int:
+        return self.q_dim + 2 * self.kv_dim
+
+    def q4k_bytes_per_layer(self) -> int:
+        rb = _q4k.row_bytes
+        return (self.qkv_rows * rb(self.hidden) + self.hidden * rb(self.q_dim)
+                + 2 * self.ffn * rb(self.hidden) + self.hidden * rb(self.ffn))
+
+    def decode_bytes_per_token(self, kv_len: float) -> float:
+        """Algorithmic HBM bytes of one decode step: every weight once, the
+        KV cache up to kv_len, plus the embedding row."""
+        w = self.layers * self.q4k_bytes_per_layer() + self.vocab * self.hidden * 2
+        kv = self.layers * 2 * self.kv_heads * kv_len * self.head_dim * 2
+        return float(w + kv + self.hidden * 2)
+
+
+def rope_table(max_pos: int, head_dim: int, base: float) -> np.ndarray:
+    """freq_cis[pos][i] = (cos, sin)(pos * base^(-2i/D)), angle in float64,
+    rounded once to f32 (the table layout rope.wgsl:27-29 reads)."""
+    half = head_dim // 2
+    inv = base ** (-2.0 * np.arange(half, dtype=np.float64) / head_dim)
+    ang = np.arange(max_pos, dtype=np.float64)[:, None] * inv[None, :]
+    t = np.empty((max_pos, half, 2), np.float32)
+    t[:, :, 0] = np.cos(ang)
+    t[:, :, 1] = np.sin(ang)
+    return t.reshape(-1)
+
+
+class LayerWeights:
+    def __init__(self, cfg: DecoderConfig):
+        rb = _q4k.row_bytes
+        self.wqkv = DeviceBuffer(cfg.qkv_rows * rb(cfg.hidden))
+        self.wo = DeviceBuffer(cfg.hidden * rb(cfg.q_dim))
+        self.wgu = DeviceBuffer(2 * cfg.ffn * rb(cfg.hidden))  # rows: gate_0, up_0, gate_1, up_1, ...
+        self.wd = DeviceBuffer(cfg.hidden * rb(cfg.ffn))
+        self.norm_attn = DeviceBuffer.empty((cfg.hidden,), np.float32)
+        self.norm_ffn = DeviceBuffer.empty((cfg.hidden,), np.float32)
+        self.k_cache = DeviceBuffer.empty((cfg.kv_heads, cfg.max_seq, cfg.head_dim), np.float16)
+        self.v_cache = DeviceBuffer.empty((cfg.kv_heads, cfg.max_seq, cfg.head_dim), np.float16)
+
+
+class Decoder:
+    """Device-resident weights, KV cache and activations of one decoder."""
+
+    def __init__(self, cfg: DecoderConfig, keep_logits: bool = False):
+        self.cfg = cfg
+        self.keep_logits = keep_logits  # also write the logits (tests); the sample does not need them
+        c = cfg
+        self.layers = [LayerWeights(c) for _ in range(c.layers)]
+        self.embed = DeviceBuffer.empty((c.vocab, c.hidden), np.float16)
+        self.lm_head = DeviceBuffer.empty((c.vocab, c.hidden), np.float16)
+        self.norm_final = DeviceBuffer.empty((c.hidden,), np.float32)
+        self.freq_cis = DeviceBuffer.from_array(rope_table(c.max_seq, c.head_dim, c.rope_base))
+        self.x = DeviceBuffer.empty((c.hidden,), np.float32)
+        self.xn = DeviceBuffer.empty((c.hidden,), np.float32)
+        self.qkv = DeviceBuffer.empty((c.qkv_rows,), np.float32)
+        self.attn = DeviceBuffer.empty((c.q_dim,), np.float32)
+        self.h = DeviceBuffer.empty((c.ffn,), np.float32)
+        self.logits = DeviceBuffer.empty((c.vocab,), np.float32)
+        self.token = DeviceBuffer.empty((1,), np.int32)
+        self.state = DeviceBuffer.empty((4,), np.int32)  # pos, kv_len, prompt_len, token
+        self.ids = DeviceBuffer.empty((c.max_seq,), np.int32)
+        self.argmax_parts = DeviceBuffer(1024 * 8)
+        # views of the fused QKV output
+        f4 = 4
+        self.q_view = self.qkv.view(0, c.q_dim * f4, np.float32)
+        self.qk_view = self.qkv.view(0, (c.q_dim + c.kv_dim) * f4, np.float32)
+        self.k_view = self.qkv.view(c.q_dim * f4, c.kv_dim * f4, np.float32)
+        self.v_view = self.qkv.view((c.q_dim + c.kv_dim) * f4, c.kv_dim * f4, np.float32)
+        self.pos_view = self.state.view(0, 4, np.int32)
+        self.kvlen_view = self.state.view(4, 4, np.int32)
+        self.tok_view = self.state.view(12, 4, np.int32)
+
+    # ---- weights -------------------------------------------------------------
+    def init_random(self, seed: int = 2, stream=None) -> None:
+        """Seeded random-init weights of this architecture: Q4_K projections
+        (d ~ |N(0,0.02)|, dmin ~ |N(0,0.01)|), f16 embedding and lm_head
+        N(0,0.02), norm weights N(0,0.1) used as (1 + w)."""
+        c = self.cfg
+        sp = _stream_ptr(stream)
+        s = seed * 1000
+
+        def q4k(buf, tag):
+            _lib.call("doe_fill_random_q4k", C.c_void_p(buf.ptr), buf.nbytes // _q4k.BLOCK_BYTES, s + tag, 0.02,
+                      0.01, sp)
+
+        def nrm(buf, tag, sigma, dtype_f16=False):
+            fn = "doe_fill_normal_f16" if dtype_f16 else "doe_fill_normal_f32"
+            n = buf.nbytes // (2 if dtype_f16 else 4)
+            _lib.call(fn, C.c_void_p(buf.ptr), n, s + tag, 0.0, sigma, sp)
+
+        for i, L in enumerate(self.layers):
+            base = 100 * (i + 1)
+            q4k(L.wqkv, base + 1)
+            q4k(L.wo, base + 2)
+            q4k(L.wgu, base + 3)
+            q4k(L.wd, base + 4)
+            nrm(L.norm_attn, base + 5, 0.1)
+            nrm(L.norm_ffn, base + 6, 0.1)
+        nrm(self.embed, 7, 0.02, True)
+        nrm(self.lm_head, 8, 0.02, True)
+        nrm(self.norm_final, 9, 0.1)
+
+    # ---- one decode step -------------------------------------------------------
+    def step(self, stream=None) -> None:
+        """Enqueues one decode step at position state.pos on `stream`."""
+        c = self.cfg
+        ops.embed(self.embed, self.tok_view, self.x, 1, c.vocab, c.hidden, c.embed_scale, stream=stream)
+        scale = 1.0 / math.sqrt(c.head_dim)
+        for L in self.layers:
+            ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads, num_kv_heads=c.kv_heads,
+                            head_dim=c.head_dim, freq_cis=self.freq_cis, position_buffer=self.pos_view,
+                            key_cache=L.k_cache, val_cache=L.v_cache, max_seq_len=c.max_seq,
+                            norm_weight=L.norm_attn, norm_eps=c.eps, norm_weight_offset=True, stream=stream)
+            ops.attention(self.q_view, L.k_cache, L.v_cache, self.attn, batch=1, num_heads=c.heads,
+                          num_kv_heads=c.kv_heads, head_dim=c.head_dim, kv_len=0, kv_stride=c.max_seq,
+                          scale=scale, kv_len_buffer=self.kvlen_view, stream=stream)
+            ops.matmul_q4k_fused(L.wo, self.attn, self.x, c.hidden, c.q_dim, residual=self.x, stream=stream)
+            ops.matmul_q4k_fused(L.wgu, self.x, self.h, 2 * c.ffn, c.hidden, norm_weight=L.norm_ffn,
+                                 norm_eps=c.eps, norm_weight_offset=True, gated=True, stream=stream)
+            ops.matmul_q4k_fused(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)
+        nparts = ops.lm_head_sample(self.lm_head, self.x, c.vocab, c.hidden, self.argmax_parts,
+                                    logits=self.logits if self.keep_logits else None, norm_weight=self.norm_final,
+                                    norm_eps=c.eps, norm_weight_offset=True, stream=stream)
+        _lib.call("doe_decode_advance", C.c_void_p(self.state.ptr), C.c_void_p(self.token.ptr),
+                  C.c_void_p(self.ids.ptr), c.max_seq, C.c_void_p(self.argmax_parts.ptr), nparts,
+                  _stream_ptr(stream))
+
+    # ---- generation ----------------------------------------------------------
+    def reset(self, prompt: np.ndarray) -> None:
+        """Loads a prompt: ids[0:len] = prompt, state = (0, 1, len, prompt[0])."""
+        c = self.cfg
+        prompt = np.asarray(prompt, np.int32)
+        if not 1 <= prompt.size <= c.max_seq:
+            raise ValueError(f"prompt of {prompt.size} tokens for max_seq {c.max_seq}")
+        ids = np.zeros(c.max_seq, np.int32)
+        ids[: prompt.size] = prompt
+        self.ids.upload(ids)
+        self.state.upload(np.array([0, 1, prompt.size, prompt[0]], np.int32))
+
+    def capture(self, stream: Stream, steps: int = 1) -> Graph:
+        """Graph of `steps` consecutive decode steps.  The first step at a new
+        shape allocates the attention workspace, so one eager step must run
+        before capturing (reset() afterwards)."""
+        def body():
+            for _ in range(steps):
+                self.step(stream)
+        return Graph.capture(stream, body)
+
+    def generate(self, prompt: np.ndarray, n_new: int, stream: Stream, graph: Graph | None = None,
+                 steps_per_graph: int = 1, timing: dict | None = None) -> np.ndarray:
+        """Prompt (teacher-forced decode steps), then `n_new` greedy tokens.
+        Returns ids[0 : len(prompt) + n_new].  With `timing`, records the
+        seconds spent in the prompt and in the decode steps (HIP events)."""
+        prompt = np.asarray(prompt, np.int32)
+        total = prompt.size + n_new
+        if total > self.cfg.max_seq:
+            raise ValueError("prompt + n_new exceeds max_seq")
+        self.reset(prompt)
+        n_prompt_steps = prompt.size - 1
+        e0, e1, e2 = Event(), Event(), Event()
+
+        def run(n):
+            if graph is None:
+                for _ in range(n):
+                    self.step(stream)
+            else:
+                full, rest = divmod(n, steps_per_graph)
+                for _ in range(full):
+                    graph.launch(stream)
+                for _ in range(rest):
+                    self.step(stream)
+
+        e0.record(stream)
+        run(n_prompt_steps)
+        e1.record(stream)
+        run(n_new)
+        e2.record(stream)
+        e2.synchronize()
+        if timing is not None:
+            timing["prompt_s"] = e0.elapsed_ms(e1) / 1e3
+            timing["decode_s"] = e1.elapsed_ms(e2) / 1e3
+        return self.ids.download()[:total]

@@ -99,6 +99,50 @@ def matmul_q4k_fused(weight: DeviceBuffer, activation: DeviceBuffer, output: Dev
               int(norm_weight_offset), rs, int(gated), _stream_ptr(stream))
 
 
+def qkv_rope_kv(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, *, hidden: int,
+                num_heads: int, num_kv_heads: int, head_dim: int, freq_cis: DeviceBuffer,
+                position_buffer: DeviceBuffer, key_cache: DeviceBuffer, val_cache: DeviceBuffer,
+                max_seq_len: int, norm_weight: DeviceBuffer | None = None, norm_eps: float = 1e-6,
+                norm_weight_offset: bool = True, stream=None) -> None:
+    """input_norm + q/k/v_proj + rope_q/rope_k + cache write in one dispatch.
+
+    Q and K weight rows must be interleaved rotation pairs per head (see
+    ``interleave_rope_rows``); output holds [q; k; v] in that order."""
+    n = (num_heads + 2 * num_kv_heads) * head_dim
+    _q4k_weight_check(weight, n, hidden)
+    _need(activation, hidden * 4, "activation")
+    _need(output, n * 4, "output")
+    cache = num_kv_heads * max_seq_len * head_dim * 2
+    _need(key_cache, cache, "key_cache")
+    _need(val_cache, cache, "val_cache")
+    _need(freq_cis, max_seq_len * head_dim * 4, "freq_cis")
+    _need(position_buffer, 4, "position_buffer")
+    nw = C.c_void_p(norm_weight.ptr) if norm_weight is not None else C.c_void_p(None)
+    _lib.call("doe_q4k_gemv_qkv_rope_kv", _p(weight), _p(activation), _p(output), hidden, nw, norm_eps,
+              int(norm_weight_offset), num_heads, num_kv_heads, head_dim, _p(freq_cis), _p(position_buffer),
+              _p(key_cache), _p(val_cache), max_seq_len, _stream_ptr(stream))
+
+
+def interleave_rope_rows(rows: np.ndarray, head_dim: int) -> np.ndarray:
+    """Reorders the rows of each head so that rows (2i, 2i+1) are the
+    rotate-half pair (i, i + head_dim/2).  Works on any per-row array
+    (Q4_K row bytes included)."""
+    r = np.asarray(rows)
+    heads = r.shape[0] // head_dim
+    half = head_dim // 2
+    v = r.reshape(heads, 2, half, *r.shape[1:])
+    return np.ascontiguousarray(np.swapaxes(v, 1, 2).reshape(r.shape))
+
+
+def deinterleave_rope_rows(rows: np.ndarray, head_dim: int) -> np.ndarray:
+    """Inverse of ``interleave_rope_rows``."""
+    r = np.asarray(rows)
+    heads = r.shape[0] // head_dim
+    half = head_dim // 2
+    v = r.reshape(heads, half, 2, *r.shape[1:])
+    return np.ascontiguousarray(np.swapaxes(v, 1, 2).reshape(r.shape))
+
+
 def rmsnorm(input: DeviceBuffer, weight: DeviceBuffer, output: DeviceBuffer, rows: int, size: int,
             eps: float = 1e-6, weight_offset: bool = False, stream=None) -> None:
     """``rmsnorm`` op: per row x * 1/sqrt(mean(x^2) + eps) * (w or 1 + w)."""
@@ -172,6 +216,25 @@ def lm_head(weight_f16: DeviceBuffer, activation: DeviceBuffer, output: DeviceBu
     _need(activation, k * 4, "activation")
     _need(output, n * 4, "output")
     _lib.call("doe_f16_gemv", _p(weight_f16), _p(activation), _p(output), n, k, alpha, _stream_ptr(stream))
+
+
+def lm_head_sample(weight_f16: DeviceBuffer, activation: DeviceBuffer, n: int, k: int, partials: DeviceBuffer, *,
+                   logits: DeviceBuffer | None = None, norm_weight: DeviceBuffer | None = None,
+                   norm_eps: float = 1e-6, norm_weight_offset: bool = True, alpha: float = 1.0,
+                   stream=None) -> int:
+    """Final norm + lm_head + greedy-sample partials in one dispatch; returns
+    the number of argmax partial keys written to ``partials`` (u64, >= 1024)."""
+    _need(weight_f16, n * k * 2, "weight")
+    _need(activation, k * 4, "activation")
+    _need(partials, 1024 * 8, "partials")
+    if logits is not None:
+        _need(logits, n * 4, "logits")
+    cnt = C.c_int32()
+    _lib.call("doe_f16_gemv_argmax", _p(weight_f16), _p(activation),
+              C.c_void_p(logits.ptr) if logits is not None else C.c_void_p(None), n, k, alpha,
+              C.c_void_p(norm_weight.ptr) if norm_weight is not None else C.c_void_p(None), norm_eps,
+              int(norm_weight_offset), _p(partials), partials.nbytes // 8, C.byref(cnt), _stream_ptr(stream))
+    return int(cnt.value)
 
 
 def tune(key: str, value: int) -> None:

@@ -122,6 +122,26 @@ int doe_q4k_gemv_fused(const void *weight_q4k, const float *activation, float *o
                        int norm_weight_offset, const float *residual, int gated,
                        doe_stream_t stream);
 
+/* Fused q/k/v projection of one decode step: output = Wqkv . rmsnorm(x)
+ * (rows [num_heads + 2 num_kv_heads][head_dim]), then RoPE on the q and k
+ * rows and the f16 write of k, v into the caches [kv_heads][max_seq][head_dim]
+ * at *position_dev -- the reference steps input_norm, q/k/v_proj, rope_q,
+ * rope_k and the cache write of attention (execution-v1
+ * gemma-3-270m-smoke.json decode steps; rope.wgsl; run_csl_webgpu_emulator.mjs:
+ * 615-644) in one dispatch.  Within each q/k head the weight rows are
+ * interleaved rotation pairs: row 2i holds dim i and row 2i+1 dim
+ * i + head_dim/2 of the rotate-half form (a row permutation applied at load
+ * time; q . k is unchanged because q and k share it, and k is cached in the
+ * same order).  norm_weight may be NULL (no norm).  freq_cis holds
+ * max_seq_len positions; a position outside [0, max_seq_len) leaves q/k
+ * unrotated and writes no cache row. */
+int doe_q4k_gemv_qkv_rope_kv(const void *weight_q4k, const float *activation, float *output,
+                             int64_t hidden, const float *norm_weight, float norm_eps,
+                             int norm_weight_offset, int64_t num_heads, int64_t num_kv_heads,
+                             int64_t head_dim, const float *freq_cis,
+                             const int32_t *position_dev, uint16_t *key_cache,
+                             uint16_t *val_cache, int64_t max_seq_len, doe_stream_t stream);
+
 /* ---- attention ---------------------------------------------------------------
  * GQA decode attention over an f16 KV cache: one query token per sequence.
  * Replaces the `attention` op (emit_csl_exec_v1.zig:117 -> attention_decode;
@@ -192,6 +212,42 @@ int doe_embed_gather(const uint16_t *table_f16, const int32_t *ids, float *outpu
  * Uniforms M, N, K, alpha, transpose_b).  k % 8 == 0, k <= 8192. */
 int doe_f16_gemv(const uint16_t *b_f16, const float *a, float *c, int64_t n, int64_t k,
                  float alpha, doe_stream_t stream);
+/* The lm_head with the final norm and the greedy sample folded in: a =
+ * rmsnorm(a) when norm_weight != NULL; logits written when non-NULL; every
+ * workgroup writes its best argmax key (see doe_decode_advance) to
+ * argmax_partials (>= 1024 entries), *num_partials = workgroups used.
+ * Replaces the final rmsnorm + lm_head + `sample` steps of a decode step. */
+int doe_f16_gemv_argmax(const uint16_t *b_f16, const float *a, float *logits, int64_t n,
+                        int64_t k, float alpha, const float *norm_weight, float norm_eps,
+                        int norm_weight_offset, uint64_t *argmax_partials,
+                        int64_t partials_capacity, int32_t *num_partials, doe_stream_t stream);
+
+/* ---- synthetic inputs and decode-loop bookkeeping -----------------------------
+ * No reference counterpart: the reference's decode numbers come from real
+ * model weights (Doppler RDRR shards); benchmarks here run on seeded random
+ * weights of the same shapes, drawn on the device.  Element i of a tensor
+ * with seed s is a pure function of (s, i), so tensors are reproducible.
+ * Q4_K blocks get d = f16(|N(0, d_sigma)|), dmin = f16(|N(0, dmin_sigma)|),
+ * uniform 6-bit scales/mins and uniform nibbles. */
+int doe_fill_normal_f16(uint16_t *out, int64_t n, uint64_t seed, float mean, float sigma,
+                        doe_stream_t stream);
+int doe_fill_normal_f32(float *out, int64_t n, uint64_t seed, float mean, float sigma,
+                        doe_stream_t stream);
+int doe_fill_uniform_i32(int32_t *out, int64_t n, uint64_t seed, int32_t lo, int32_t hi,
+                         doe_stream_t stream);
+int doe_fill_random_q4k(void *weight_q4k, int64_t nblocks, uint64_t seed, float d_sigma,
+                        float dmin_sigma, doe_stream_t stream);
+/* After a decode step, on the device: state = {pos, kv_len, prompt_len,
+ * token}; pos += 1, kv_len = pos + 1, and the next token is ids[pos] inside
+ * the prompt or the sampled *token (also stored to ids[pos]) after it.  With
+ * argmax_partials (from doe_f16_gemv_argmax) the sampled token is first
+ * reduced from them and stored to *token.  Keeps
+ * a captured step graph replayable with no host round trip (the reference
+ * reads back per token, bench/fixtures/r3-2-27b-doppler-frozen-af16/
+ * reference-report.json:75 readbackInterval). */
+int doe_decode_advance(int32_t *state, int32_t *token, int32_t *ids, int64_t max_seq,
+                       const uint64_t *argmax_partials, int32_t num_partials,
+                       doe_stream_t stream);
 
 /* ---- tuning ----------------------------------------------------------------
  * Overrides a kernel launch-shape choice (0 restores the automatic choice).

@@ -176,3 +176,109 @@ def test_fused_gemv_norm_residual_gated(dev, ora):
     y = ora.q4k_gemv(wg, xn, 2 * ff, k)
     want3 = ora.geglu(y[0::2], y[1::2])
     assert rel_l2(out3.download(), want3) < 1e-5
+
+
+@pytest.mark.parametrize("pos", [0, 17, 63, 64])
+def test_qkv_rope_kv(dev, ora, pos):
+    # the fused input_norm + q/k/v_proj + rope + cache write, 2B-class head
+    # shape (8 q / 4 kv heads of 256 over hidden 2304); pos 64 is outside the
+    # 64-position cache: unrotated q/k and no cache write
+    rng = np.random.default_rng(9 + pos)
+    hidden, hq, hkv, d, maxs = 2304, 8, 4, 256, 64
+    qd, kd = hq * d, hkv * d
+    n = qd + 2 * kd
+    w_plain = q4k.random_q4k(rng, n, hidden).reshape(n, -1)
+    w_dev = w_plain.copy()
+    w_dev[: qd + kd] = ops.interleave_rope_rows(w_plain[: qd + kd], d)
+    x = (rng.standard_normal(hidden) * 3).astype(np.float32)
+    nw = (0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    table = ora.rope_table(maxs, d, 10000.0)
+    kc0 = (rng.standard_normal((hkv, maxs, d))).astype(np.float16)
+    vc0 = (rng.standard_normal((hkv, maxs, d))).astype(np.float16)
+    kc, vc = up(kc0), up(vc0)
+    out = DeviceBuffer.empty((n,), np.float32)
+    ops.qkv_rope_kv(up(w_dev), up(x), out, hidden=hidden, num_heads=hq, num_kv_heads=hkv, head_dim=d,
+                    freq_cis=up(table), position_buffer=up(np.array([pos], np.int32)), key_cache=kc,
+                    val_cache=vc, max_seq_len=maxs, norm_weight=up(nw), norm_eps=1e-6, norm_weight_offset=True)
+    qkv = ora.q4k_gemv(w_plain, ora.rmsnorm(x, nw, 1e-6, True), n, hidden)
+    inside = pos < maxs
+    qk = ora.rope(qkv[: qd + kd], table, 1, hq + hkv, d, pos) if inside else qkv[: qd + kd]
+    want = np.concatenate([ops.interleave_rope_rows(qk, d), qkv[qd + kd:]])
+    got = out.download()
+    assert rel_l2(got, want) < 1e-5
+    kc_want, vc_want = kc0.copy(), vc0.copy()
+    if inside:
+        kc_want[:, pos] = ops.interleave_rope_rows(qk[qd:], d).reshape(hkv, d)
+        vc_want[:, pos] = qkv[qd + kd:].reshape(hkv, d)
+    # untouched rows bit-exact; the written row within f16 rounding of the oracle
+    kg, vg = kc.download(), vc.download()
+    other = [p for p in range(maxs) if p != pos]
+    assert np.array_equal(kg[:, other].view(np.uint16), kc0[:, other].view(np.uint16))
+    assert np.array_equal(vg[:, other].view(np.uint16), vc0[:, other].view(np.uint16))
+    if inside:
+        assert rel_l2(kg[:, pos].astype(np.float32), kc_want[:, pos].astype(np.float32)) < 1e-3
+        assert rel_l2(vg[:, pos].astype(np.float32), vc_want[:, pos].astype(np.float32)) < 1e-3
+        # the cache row is exactly the f16 rounding of the device's own output
+        assert np.array_equal(kg[:, pos].reshape(-1).view(np.uint16),
+                              got[qd: qd + kd].astype(np.float16).view(np.uint16))
+
+
+def _advance_token(parts, nparts):
+    """Reduces lm_head argmax partials through doe_decode_advance and returns
+    (token, recorded id, state) for a step past the prompt."""
+    import ctypes as C
+
+    from doe_amd import _lib
+    state = up(np.array([5, 6, 0, -1], np.int32))
+    tok = DeviceBuffer.empty((1,), np.int32)
+    ids = up(np.full(16, -7, np.int32))
+    _lib.call("doe_decode_advance", C.c_void_p(state.ptr), C.c_void_p(tok.ptr), C.c_void_p(ids.ptr), 16,
+              C.c_void_p(parts.ptr), nparts, C.c_void_p(None))
+    return int(tok.download()[0]), int(ids.download()[6]), state.download().tolist()
+
+
+@pytest.mark.parametrize("n,seed", [(256000, 11), (256000, 12), (4096, 13), (77, 14)])
+def test_lm_head_sample(dev, ora, n, seed):
+    # final norm + lm_head + greedy sample: logits to rel-L2 1e-5 and the
+    # token equal to the oracle's argmax (when the top two logits are apart
+    # by more than the GEMV tolerance)
+    rng = np.random.default_rng(seed)
+    k = 2304
+    b = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float16)
+    a = (rng.standard_normal(k) * 4).astype(np.float32)
+    nw = (0.1 * rng.standard_normal(k)).astype(np.float32)
+    logits = DeviceBuffer.empty((n,), np.float32)
+    parts = DeviceBuffer(1024 * 8)
+    cnt = ops.lm_head_sample(up(b), up(a), n, k, parts, logits=logits, norm_weight=up(nw), norm_eps=1e-6)
+    assert 1 <= cnt <= 1024
+    want = ora.f16_gemv(b, ora.rmsnorm(a, nw, 1e-6, True))
+    got = logits.download()
+    assert rel_l2(got, want) < 1e-5
+    tok, rec, state = _advance_token(parts, cnt)
+    assert tok == int(np.argmax(got))  # exact reduction of the device's own logits
+    top = np.sort(want)[-2:]
+    if top[1] - top[0] > 1e-4 * abs(top[1]):
+        assert tok == ora.argmax(want)
+    assert rec == tok and state == [6, 7, 0, tok]
+    # without the logits output the partials are the same
+    parts2 = DeviceBuffer(1024 * 8)
+    cnt2 = ops.lm_head_sample(up(b), up(a), n, k, parts2, norm_weight=up(nw), norm_eps=1e-6)
+    assert cnt2 == cnt and np.array_equal(parts2.download()[: cnt * 8], parts.download()[: cnt * 8])
+
+
+def test_lm_head_sample_ties_and_nan(dev, ora):
+    # equal logits across workgroups: the lowest index wins; NaN never wins;
+    # all NaN gives index 0 (the reference's starting index)
+    rng = np.random.default_rng(15)
+    n, k = 50000, 256
+    row = (rng.standard_normal(k) * 0.02).astype(np.float16)
+    b = np.tile(row, (n, 1))
+    a = rng.standard_normal(k).astype(np.float32)
+    b[:10] = np.float16(np.nan)
+    parts = DeviceBuffer(1024 * 8)
+    cnt = ops.lm_head_sample(up(b), up(a), n, k, parts)
+    logits = np.where(np.arange(n) < 10, np.nan, 1.0).astype(np.float32)
+    assert _advance_token(parts, cnt)[0] == 10 == ora.argmax(logits)
+    b[:] = np.float16(np.nan)
+    cnt = ops.lm_head_sample(up(b), up(a), n, k, parts)
+    assert _advance_token(parts, cnt)[0] == 0 == ora.argmax(np.full(n, np.nan, np.float32))
