@@ -230,6 +230,71 @@ def bench_decode(args, doe):
     }
 
 
+GEMM_M, GEMM_N, GEMM_K = 2048, 21504, 5376
+GEMM_FLOP = 2 * GEMM_M * GEMM_N * GEMM_K  # 473,520,144,384
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16/bf16
+
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bench_gemm(args, doe):
+    """Q4_K dequant-fused prefill GEMM at the 31B-class shape (M=2048 tokens,
+    K=5376, N=21504; bf16 activations N(0,1), Q4_K weights, f32 output); HIP
+    events around back-to-back calls (each call = the bf16->f16 row pre-pass
+    plus the GEMM kernel); sampled parity against the oracle."""
+    import ctypes as C
+
+    from doe_amd import DeviceBuffer, Event, Stream, _lib, ops
+    from doe_amd import q4k as q4kmod
+
+    rng = np.random.default_rng(3)
+    a = to_bf16(rng.standard_normal((GEMM_M, GEMM_K), dtype=np.float32))
+    da = DeviceBuffer.from_array(a)
+    db = DeviceBuffer(GEMM_N * q4kmod.row_bytes(GEMM_K))
+    _lib.call("doe_fill_random_q4k", C.c_void_p(db.ptr), db.nbytes // q4kmod.BLOCK_BYTES, 33, 0.02, 0.01,
+              C.c_void_p(None))
+    dc = DeviceBuffer.empty((GEMM_M, GEMM_N), np.float32)
+    s = Stream()
+    for _ in range(2):
+        ops.matmul_q4k_gemm(da, db, dc, GEMM_M, GEMM_N, GEMM_K, stream=s)
+    s.synchronize()
+    reps = args.gemm_steps
+    e0, e1 = Event(), Event()
+    e0.record(s)
+    for _ in range(reps):
+        ops.matmul_q4k_gemm(da, db, dc, GEMM_M, GEMM_N, GEMM_K, stream=s)
+    e1.record(s)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    from oracle import oracle as ora
+
+    b = db.download().reshape(GEMM_N, -1)
+    mi = np.arange(0, GEMM_M, 8, dtype=np.int64)
+    ni = np.sort(rng.integers(0, GEMM_N, mi.size)).astype(np.int64)
+    want = ora.q4k_gemm_sampled(a, b, GEMM_M, GEMM_N, GEMM_K, mi, ni)
+    got = dc.download()[mi, ni].astype(np.float64)
+    rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    s.destroy()
+    for buf in (da, db, dc):
+        buf.free()
+    tflops = GEMM_FLOP / (ms * 1e-3) / 1e12
+    log(f"gemm: {ms * 1e3:.1f} us/call, {tflops:.0f} TFLOP/s ({100 * tflops / MFMA_F16_PEAK_TFLOPS:.1f}% of "
+        f"the f16 MFMA peak), sampled rel_l2 {rel:.2e}")
+    return {
+        "workload": f"q4k_gemm M={GEMM_M} N={GEMM_N} K={GEMM_K}: bf16 activations, Q4_K_M weights, f32 out "
+                    f"(f16 matrix cores, f32 accumulate)",
+        "us_per_call": round(ms * 1e3, 2),
+        "flop_per_call": GEMM_FLOP,
+        "achieved_tflops": round(tflops, 1),
+        "mfma_peak_tflops": MFMA_F16_PEAK_TFLOPS,
+        "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+        "rel_l2_vs_oracle_sampled": rel,
+    }
+
+
 def traffic_bytes(summary: str):
     """HBM bytes per launch recorded in a committed rocprofv3 summary
     (line `traffic_bytes_per_launch: <int>`), or None."""
@@ -278,6 +343,8 @@ def main() -> int:
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--steps-per-graph", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--gemm-steps", type=int, default=20)
+    ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -301,6 +368,7 @@ def main() -> int:
     g = bench_gemv(args, doe_amd)
     att = bench_attention(args, doe_amd)
     dec = None if args.no_decode else bench_decode(args, doe_amd)
+    gemm = None if args.no_gemm else bench_gemm(args, doe_amd)
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of the single-threaded oracle")
@@ -339,6 +407,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "attention_decode": att,
         "decode": dec,
+        "prefill_gemm": gemm,
     }
     print(json.dumps(out), flush=True)
     return 0

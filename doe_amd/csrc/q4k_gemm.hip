@@ -1,0 +1,304 @@
+// q4k_gemm.hip -- Q4_K_M dequant-fused GEMM (prefill) on the gfx950 matrix cores.
+//
+// C[m][n] = sum_k A[m][k] * dequant(B)[n][k]: A bf16 [M][K] row-major, B the
+// row-wise Q4_K_M matrix [N][ceil(K/256) blocks] (bench/tools/doppler_rdrr_q4k.py:
+// 128-156), C f32 [M][N] -- the `matmul_q4k` prefill pattern
+// (runtime/zig/src/doe_wgsl/emit_csl_classify.zig:287-297; SUMMA with a
+// dequantised B tile in emit_csl_matmul_q4k.zig:66-345).
+//
+// Numerics.  Products run on v_mfma_f32_32x32x16_f16 with f32 accumulation:
+//   * A is copied once to f16 by a pre-pass, each row scaled by a power of two
+//     2^s_m that puts max|A[m]| just under 2^14; bf16 has 8 significant bits
+//     and f16 11, so every element whose scaled magnitude is >= 2^-14 converts
+//     exactly (smaller ones carry at least the absolute precision 2^-24 of the
+//     row maximum).  The epilogue multiplies row m by 2^-s_m, exactly.
+//   * B is dequantised per 64-element chunk into LDS as f16: q is produced
+//     exactly with packed-f16 arithmetic ((1024 + q) - 1024 for low nibbles,
+//     (64 + q) - 64 for high nibbles, from an OR of the nibble into the
+//     mantissa) and w = RN_f16(q * RN_f16(d*sc) - RN_f16(dmin*m)) by one
+//     packed fma.  The relative error of w is ~2^-11, far inside the rel-L2
+//     1e-3 contract; a bf16 B (8 bits) would sit at ~1.1e-3.
+//
+// Tiling: 128 x 128 output tile per 256-thread workgroup (2 x 2 waves, each a
+// 64 x 64 block of four 32x32 accumulators), K in steps of one Q4_K chunk
+// (64), A and B tiles double-buffered in LDS with the next chunk's global loads
+// in flight during the current chunk's MFMAs.  Tiles are ordered in groups of
+// 8 M-tiles and each XCD (workgroup id mod 8) gets a contiguous range of that
+// order, so the workgroups resident on one XCD share A and B chunks in its L2.
+#include "common.h"
+
+#include <math.h>
+#include <mutex>
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kLdsRow = kBK + 8;  // halves per LDS row: 144 bytes, b128 reads conflict-free
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+__device__ __forceinline__ uint32_t as_u32(half2v v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Scale/min pair of sub-blocks 2*c4 and 2*c4+1 (doppler_rdrr_q4k.py:56-76):
+// low byte sub-block 2*c4, high byte 2*c4+1.
+__device__ __forceinline__ void scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int c4,
+                                               uint32_t &scp, uint32_t &mnp) {
+    const int sh = (c4 & 1) * 16;
+    if (c4 < 2) {
+        scp = (s0 >> sh) & 0x3f3fu;
+        mnp = (s1 >> sh) & 0x3f3fu;
+    } else {
+        scp = ((s2 >> sh) & 0x0f0fu) | ((s0 >> (sh + 2)) & 0x3030u);
+        mnp = ((s2 >> (sh + 4)) & 0x0f0fu) | ((s1 >> (sh + 2)) & 0x3030u);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pre-pass: A bf16 [M][K] -> f16 [M][Kp] (zero padded to Kp, a multiple of
+// 64) scaled by 2^sig[m]; one workgroup per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void a_rows_to_f16_kernel(const uint16_t *__restrict__ a,
+                                                            _Float16 *__restrict__ a16,
+                                                            int *__restrict__ sig, int K, int Kp) {
+    const int m = blockIdx.x;
+    const uint16_t *row = a + (size_t)m * K;
+    float amax = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(__uint_as_float((uint32_t)row[k] << 16)));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    __shared__ float wmax[4];
+    __shared__ int ssig;
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        int s = 0;
+        if (mx > 0.0f && mx <= 3.0e38f) {
+            s = 14 - __builtin_amdgcn_frexp_expf(mx);
+            s = s < -120 ? -120 : (s > 120 ? 120 : s);
+        }
+        ssig = s;
+        sig[m] = s;
+    }
+    __syncthreads();
+    const float scale = __builtin_amdgcn_ldexpf(1.0f, ssig);
+    _Float16 *out = a16 + (size_t)m * Kp;
+    for (int k = threadIdx.x; k < Kp; k += 256)
+        out[k] = k < K ? (_Float16)(__uint_as_float((uint32_t)row[k] << 16) * scale) : (_Float16)0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// GEMM.
+// ---------------------------------------------------------------------------
+struct GemmArgs {
+    const _Float16 *a16;
+    const int *sig;
+    const uint8_t *b;
+    float *c;
+    int M, N, Kp, nb, nchunk, tiles_m, tiles_n;
+};
+
+// Four halves from the low nibbles and four from the high nibbles of one
+// nibble dword (bytes b0..b3 = consecutive k), each as exact f16 values
+// q * dsc - dmm rounded once.
+__device__ __forceinline__ void dequant_dword(uint32_t w, half2v dsc_lo, half2v ndmm_lo, half2v dsc_hi,
+                                              half2v ndmm_hi, uint32_t *lo, uint32_t *hi) {
+    // t0 = [b0, 0, b1, 0], t1 = [b2, 0, b3, 0]
+    const uint32_t t0 = __builtin_amdgcn_perm(0u, w, 0x0c010c00u);
+    const uint32_t t1 = __builtin_amdgcn_perm(0u, w, 0x0c030c02u);
+    const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const half2v k64 = {(_Float16)64.0f, (_Float16)64.0f};
+    const half2v ql0 = as_h2((t0 & 0x000f000fu) | 0x64006400u) - k1024;
+    const half2v ql1 = as_h2((t1 & 0x000f000fu) | 0x64006400u) - k1024;
+    const half2v qh0 = as_h2((t0 & 0x00f000f0u) | 0x54005400u) - k64;
+    const half2v qh1 = as_h2((t1 & 0x00f000f0u) | 0x54005400u) - k64;
+    lo[0] = as_u32(__builtin_elementwise_fma(ql0, dsc_lo, ndmm_lo));
+    lo[1] = as_u32(__builtin_elementwise_fma(ql1, dsc_lo, ndmm_lo));
+    hi[0] = as_u32(__builtin_elementwise_fma(qh0, dsc_hi, ndmm_hi));
+    hi[1] = as_u32(__builtin_elementwise_fma(qh1, dsc_hi, ndmm_hi));
+}
+
+__global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][kBM * kLdsRow];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][kBN * kLdsRow];
+
+    // tile order: XCD-contiguous ranges of an M-grouped raster
+    const int T = g.tiles_m * g.tiles_n;
+    int t = blockIdx.x;
+    if ((T & 7) == 0) t = (blockIdx.x & 7) * (T >> 3) + (blockIdx.x >> 3);
+    const int per_group = kGroupM * g.tiles_n;
+    const int grp = t / per_group;
+    const int first_m = grp * kGroupM;
+    const int gsize = min(kGroupM, g.tiles_m - first_m);
+    const int within = t - grp * per_group;
+    const int tm = first_m + within % gsize;
+    const int tn = within / gsize;
+    const int m0 = tm * kBM, n0 = tn * kBN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // global -> register staging assignments
+    // A: 1024 granules of 8 halves; granule gi = tid + 256 i: row gi >> 3, col (gi & 7) * 8
+    // B: row tid >> 1, nibble half h = tid & 1 (16 bytes: k = 16h..16h+15 and 32+16h..)
+    const int brow = tid >> 1, bh = tid & 1;
+    const uint8_t *brow_ptr = g.b + (size_t)min(n0 + brow, g.N - 1) * g.nb * DOE_Q4K_BLOCK_BYTES;
+    const _Float16 *arow_ptr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int gi = tid + 256 * i;
+        arow_ptr[i] = g.a16 + (size_t)min(m0 + (gi >> 3), g.M - 1) * g.Kp + (gi & 7) * 8;
+    }
+
+    uint4 ra[4], rh, rq;
+    auto load_chunk = [&](int kc) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const uint4 *>(arow_ptr[i] + kc * kBK);
+        const uint8_t *blk = brow_ptr + (size_t)(kc >> 2) * DOE_Q4K_BLOCK_BYTES;
+        rh = *reinterpret_cast<const uint4 *>(blk);
+        rq = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * (kc & 3) + 16 * bh);
+    };
+    auto store_chunk = [&](int buf, int kc) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int gi = tid + 256 * i;
+            *reinterpret_cast<uint4 *>(&As[buf][(gi >> 3) * kLdsRow + (gi & 7) * 8]) = ra[i];
+        }
+        uint32_t scp, mnp;
+        scale_min_pair(rh.y, rh.z, rh.w, kc & 3, scp, mnp);
+        const float d = doe_half_bits_to_float(rh.x), dmin = doe_half_bits_to_float(rh.x >> 16);
+        const _Float16 dsl = (_Float16)(d * (float)(scp & 0xffu)), dsh = (_Float16)(d * (float)(scp >> 8));
+        const _Float16 dml = (_Float16)(-(dmin * (float)(mnp & 0xffu))), dmh = (_Float16)(-(dmin * (float)(mnp >> 8)));
+        const half2v dsc_lo = {dsl, dsl}, dsc_hi = {dsh, dsh}, ndmm_lo = {dml, dml}, ndmm_hi = {dmh, dmh};
+        const uint32_t q[4] = {rq.x, rq.y, rq.z, rq.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dequant_dword(q[j], dsc_lo, ndmm_lo, dsc_hi, ndmm_hi, lo + 2 * j, hi + 2 * j);
+        _Float16 *bl = &Bs[buf][brow * kLdsRow + 16 * bh];
+        *reinterpret_cast<uint4 *>(bl) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        *reinterpret_cast<uint4 *>(bl + 8) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+        *reinterpret_cast<uint4 *>(bl + 32) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        *reinterpret_cast<uint4 *>(bl + 40) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+    };
+
+    float16v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    load_chunk(0);
+    store_chunk(0, 0);
+    __syncthreads();
+    const int lr = lane & 31, lk = 8 * (lane >> 5);
+    for (int kc = 0; kc < g.nchunk; ++kc) {
+        const int buf = kc & 1;
+        if (kc + 1 < g.nchunk) load_chunk(kc + 1);
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            half8 af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                af[i] = *reinterpret_cast<const half8 *>(&As[buf][(wm * 64 + i * 32 + lr) * kLdsRow + ks * 16 + lk]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                bf[j] = *reinterpret_cast<const half8 *>(&Bs[buf][(wn * 64 + j * 32 + lr) * kLdsRow + ks * 16 + lk]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kc + 1 < g.nchunk) store_chunk(buf ^ 1, kc + 1);
+        __syncthreads();
+    }
+
+    // epilogue: D lane l, r: row (r%4) + 8(r/4) + 4(l/32), column l%32
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + wm * 64 + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+            if (m >= g.M) continue;
+            const float us = __builtin_amdgcn_ldexpf(1.0f, -g.sig[m]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn * 64 + j * 32 + lr;
+                if (n < g.N) g.c[(size_t)m * g.N + n] = acc[i][j][r] * us;
+            }
+        }
+    }
+}
+
+// Library-owned workspace (grow-only) for the f16 copy of A and its row scales.
+std::mutex g_ws_mu;
+void *g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+}  // namespace
+
+extern "C" {
+
+int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m, int64_t n,
+                 int64_t k, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(m >= 0 && n >= 0 && k >= 0, DOE_E_INVALID, "negative shape");
+    if (m == 0 || n == 0) return DOE_OK;
+    DOE_REQUIRE(c, DOE_E_INVALID, "null output");
+    hipStream_t st = (hipStream_t)stream;
+    if (k == 0) {
+        // empty reduction: the sum identity
+        DOE_HIP_CHECK(hipMemsetAsync(c, 0, (size_t)m * (size_t)n * sizeof(float), st));
+        return DOE_OK;
+    }
+    DOE_REQUIRE(a_bf16 && b_q4k, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(((uintptr_t)b_q4k & 15) == 0, DOE_E_INVALID, "weight must be 16-byte aligned");
+    DOE_REQUIRE(m <= (1 << 24) && n <= (1 << 24) && k <= (1 << 20) && m * n <= ((int64_t)1 << 40),
+                DOE_E_UNSUPPORTED, "q4k_gemm shape too large (m=%lld n=%lld k=%lld)", (long long)m,
+                (long long)n, (long long)k);
+    const int64_t kp = (k + kBK - 1) / kBK * kBK;
+    const size_t a16_bytes = (size_t)m * (size_t)kp * 2;
+    const size_t need = a16_bytes + (size_t)m * 4;
+    void *ws;
+    {
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        if (g_ws_bytes < need) {
+            if (g_ws) DOE_HIP_CHECK(hipFree(g_ws));
+            g_ws = nullptr;
+            g_ws_bytes = 0;
+            DOE_HIP_CHECK(hipMalloc(&g_ws, need));
+            g_ws_bytes = need;
+        }
+        ws = g_ws;
+    }
+    _Float16 *a16 = (_Float16 *)ws;
+    int *sig = (int *)((char *)ws + a16_bytes);
+    hipLaunchKernelGGL(a_rows_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, a_bf16, a16, sig, (int)k, (int)kp);
+    DOE_LAUNCH_CHECK("a_rows_to_f16_kernel");
+    GemmArgs g;
+    g.a16 = a16;
+    g.sig = sig;
+    g.b = (const uint8_t *)b_q4k;
+    g.c = c;
+    g.M = (int)m;
+    g.N = (int)n;
+    g.Kp = (int)kp;
+    g.nb = (int)((k + 255) / 256);
+    g.nchunk = (int)(kp / kBK);
+    g.tiles_m = (int)((m + kBM - 1) / kBM);
+    g.tiles_n = (int)((n + kBN - 1) / kBN);
+    const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
+    DOE_REQUIRE(tiles <= 0x7fffffff, DOE_E_UNSUPPORTED, "too many tiles");
+    hipLaunchKernelGGL(q4k_gemm_kernel, dim3((unsigned)tiles), dim3(256), 0, st, g);
+    DOE_LAUNCH_CHECK("q4k_gemm_kernel");
+    return DOE_OK;
+}
+
+}  // extern "C"

@@ -53,6 +53,16 @@ def matmul_q4k(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuf
     _lib.call("doe_q4k_gemv", _p(weight), _p(activation), _p(output), n, k, _stream_ptr(stream))
 
 
+def matmul_q4k_gemm(a_bf16: DeviceBuffer, weight: DeviceBuffer, output: DeviceBuffer, m: int, n: int, k: int,
+                    stream=None) -> None:
+    """``matmul_q4k`` at M > 1 (prefill): output f32[m][n] = a bf16[m][k] @
+    dequant(weight)[n][k]^T on the matrix cores."""
+    _q4k_weight_check(weight, n, k)
+    _need(a_bf16, m * k * 2, "a")
+    _need(output, m * n * 4, "output")
+    _lib.call("doe_q4k_gemm", _p(a_bf16), _p(weight), _p(output), m, n, k, _stream_ptr(stream))
+
+
 def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, output: DeviceBuffer, *,
               batch: int, num_heads: int, num_kv_heads: int, head_dim: int, kv_len: int,
               kv_stride: int, scale: float, q_f16: bool = False, out_f16: bool = False,
@@ -250,6 +260,7 @@ OPS = {
     "kv_write": kv_write,
     "lm_head": lm_head,
     "matmul_q4k": matmul_q4k,
+    "matmul_q4k_gemm": matmul_q4k_gemm,
     "residual": residual,
     "rmsnorm": rmsnorm,
     "rope": rope,

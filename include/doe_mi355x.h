@@ -104,6 +104,18 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
 int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
                  int64_t n, int64_t k, doe_stream_t stream);
 
+/* Prefill GEMM c[m][n] = sum_k a[m][k] * dequant(b)[n][k]: a bf16 [m][k]
+ * row-major, b row-wise Q4_K_M [n][k] (16-byte aligned), c f32 [m][n]
+ * row-major.  Replaces the `matmul_q4k` op at M > 1 (pattern classified in
+ * runtime/zig/src/doe_wgsl/emit_csl_classify.zig:287-297, lowered to SUMMA
+ * with a dequantised B tile in emit_csl_matmul_q4k.zig:66-345).  Products
+ * run on f16 matrix cores with f32 accumulation (a converted exactly to f16
+ * with a per-row power-of-two scale, b dequantised to f16); rel-L2 against
+ * the f32 reference ~2e-4.  Uses a library-owned workspace of m*ceil(k/64)*64*2
+ * + 4m bytes, grown on demand (not during stream capture). */
+int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m, int64_t n,
+                 int64_t k, doe_stream_t stream);
+
 /* Fused decode GEMV: the plain Q4_K GEMV with the neighbouring steps of the
  * Doppler decode step list folded in (runtime/zig/examples/execution-v1/
  * gemma-3-270m-smoke.json: input_norm -> q/k/v_proj, o_proj ->

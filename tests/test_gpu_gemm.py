@@ -1,0 +1,115 @@
+"""GPU parity of the Q4_K dequant-fused prefill GEMM against the CPU oracle
+(f32 left-fold over dequantised rows, bf16 activations upcast exactly),
+through the C ABI.  Contract: rel-L2 <= 1e-3 (f32 accumulate)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from doe_amd import DeviceBuffer, _lib, ops, q4k
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 bits, round to nearest even (NaN kept quiet)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    r[nan] = 0x7FC0
+    return r
+
+
+def up(a):
+    return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 256), (37, 200, 300), (128, 128, 512), (130, 257, 2304),
+                                   (256, 384, 5376), (5, 1000, 64)])
+def test_gemm_matches_oracle(dev, ora, m, n, k):
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = to_bf16(rng.standard_normal((m, k), dtype=np.float32))
+    b = q4k.random_q4k(rng, n, k)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_q4k_gemm(up(a), up(b), out, m, n, k)
+    got = out.download()
+    want = ora.q4k_gemm(a, b, m, n, k)
+    err = rel_l2(got, want)
+    print(f"[gemm {m}x{n}x{k}] rel_l2 {err:.2e}", flush=True)
+    assert err <= TOL
+
+
+def test_gemm_prefill_config_sampled(dev, ora):
+    # the 31B-class prefill shape: M=2048 tokens, K=5376, N=21504; the oracle
+    # evaluates 2048 sampled entries (every row once, at a random column)
+    m, n, k = 2048, 21504, 5376
+    rng = np.random.default_rng(3)
+    a = to_bf16(rng.standard_normal((m, k), dtype=np.float32))
+    b = q4k.random_q4k(rng, n, k)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_q4k_gemm(up(a), up(b), out, m, n, k)
+    got = out.download()
+    mi = np.arange(m, dtype=np.int64)
+    ni = rng.integers(0, n, m).astype(np.int64)
+    order = np.argsort(ni, kind="stable")  # the oracle caches one dequantised row
+    mi, ni = mi[order], ni[order]
+    want = ora.q4k_gemm_sampled(a, b, m, n, k, mi, ni)
+    err = rel_l2(got[mi, ni], want)
+    print(f"[gemm config] sampled rel_l2 {err:.2e}", flush=True)
+    assert err <= TOL
+    assert np.isfinite(got).all()
+
+
+def test_gemm_row_scaling_extremes(dev, ora):
+    # rows of very different magnitude (2^-60 .. 2^60, a zero row, a row with
+    # one non-zero): each row keeps the contract on its own
+    rng = np.random.default_rng(4)
+    m, n, k = 8, 96, 768
+    base = rng.standard_normal((m, k), dtype=np.float32)
+    scales = np.array([1.0, 2.0 ** 60, 2.0 ** -60, 1e-20, 3e4, 0.0, 1.0, 1.0], np.float32)
+    x = base * scales[:, None]
+    x[6] = 0.0
+    x[6, 17] = 5.0
+    x[7, ::2] *= 1e-6  # mixed magnitudes inside one row
+    a = to_bf16(x)
+    b = q4k.random_q4k(rng, n, k)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_q4k_gemm(up(a), up(b), out, m, n, k)
+    got = out.download()
+    want = ora.q4k_gemm(a, b, m, n, k)
+    for r in range(m):
+        if r == 5:
+            assert np.array_equal(got[r], np.zeros(n, np.float32))
+        else:
+            assert rel_l2(got[r], want[r]) <= TOL, r
+
+
+def test_gemm_zero_k_and_empty(dev):
+    out = up(np.full((3, 4), 7.0, np.float32))
+    dummy = DeviceBuffer(256)
+    _lib.call("doe_q4k_gemm", C.c_void_p(dummy.ptr), C.c_void_p(dummy.ptr), C.c_void_p(out.ptr), 3, 4, 0,
+              C.c_void_p(None))
+    assert np.array_equal(out.download(), np.zeros((3, 4), np.float32))
+    # m == 0 / n == 0: nothing launched, nothing written
+    _lib.call("doe_q4k_gemm", C.c_void_p(dummy.ptr), C.c_void_p(dummy.ptr), C.c_void_p(out.ptr), 0, 4, 256,
+              C.c_void_p(None))
+    _lib.call("doe_q4k_gemm", C.c_void_p(dummy.ptr), C.c_void_p(dummy.ptr), C.c_void_p(out.ptr), 3, 0, 256,
+              C.c_void_p(None))
+    assert np.array_equal(out.download(), np.zeros((3, 4), np.float32))
+
+
+def test_gemm_rejects_misaligned_weight(dev):
+    buf = DeviceBuffer(144 * 4 + 16)
+    out = DeviceBuffer.empty((1, 1), np.float32)
+    a = DeviceBuffer(256 * 2)
+    with pytest.raises(_lib.DoeError):
+        _lib.call("doe_q4k_gemm", C.c_void_p(a.ptr), C.c_void_p(buf.ptr + 8), C.c_void_p(out.ptr), 1, 1, 256,
+                  C.c_void_p(None))
