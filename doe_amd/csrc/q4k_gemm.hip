@@ -19,8 +19,9 @@
 //     packed fma.  The relative error of w is ~2^-11, far inside the rel-L2
 //     1e-3 contract; a bf16 B (8 bits) would sit at ~1.1e-3.
 //
-// Tiling: 128 x 128 output tile per 256-thread workgroup (2 x 2 waves, each a
-// 64 x 64 block of four 32x32 accumulators), K in steps of one Q4_K chunk
+// Tiling: 256 x 256 output tile per 256-thread workgroup (2 x 2 waves, each a
+// 128 x 128 block of sixteen 32x32 accumulators; 128 x 128 tiles for small
+// problems), K in steps of one Q4_K chunk
 // (64), A and B tiles double-buffered in LDS with the next chunk's global loads
 // in flight during the current chunk's MFMAs.  Tiles are ordered in groups of
 // 8 M-tiles and each XCD (workgroup id mod 8) gets a contiguous range of that
@@ -35,8 +36,10 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kBK = 64;
 constexpr int kLdsRow = kBK + 8;  // halves per LDS row: 144 bytes, b128 reads conflict-free
 constexpr int kGroupM = 8;
 
@@ -122,9 +125,16 @@ __device__ __forceinline__ void dequant_dword(uint32_t w, half2v dsc_lo, half2v 
     hi[1] = as_u32(__builtin_elementwise_fma(qh1, dsc_hi, ndmm_hi));
 }
 
+// TM x TN 32x32 accumulators per wave, 2 x 2 waves: a (64 TM) x (64 TN) tile.
+template <int TM, int TN>
 __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][kBM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][kBN * kLdsRow];
+    constexpr int BM = 64 * TM, BN = 64 * TN;
+    constexpr int GA = BM / 32;      // 16-byte A granules per thread per chunk
+    constexpr int TPR = 256 / BN;    // threads per B row (1 or 2)
+    constexpr int NBY = 32 / TPR;    // nibble bytes per thread per chunk (32 or 16)
+    constexpr int NQ = NBY / 16;     // 16-byte nibble loads per thread
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLdsRow];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * kLdsRow];
 
     // tile order: XCD-contiguous ranges of an M-grouped raster
     const int T = g.tiles_m * g.tiles_n;
@@ -137,99 +147,289 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
     const int within = t - grp * per_group;
     const int tm = first_m + within % gsize;
     const int tn = within / gsize;
-    const int m0 = tm * kBM, n0 = tn * kBN;
+    const int m0 = tm * BM, n0 = tn * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
     // global -> register staging assignments
-    // A: 1024 granules of 8 halves; granule gi = tid + 256 i: row gi >> 3, col (gi & 7) * 8
-    // B: row tid >> 1, nibble half h = tid & 1 (16 bytes: k = 16h..16h+15 and 32+16h..)
-    const int brow = tid >> 1, bh = tid & 1;
+    // A: granule gi = tid + 256 i: row gi >> 3, col (gi & 7) * 8
+    // B: row tid / TPR, nibble bytes [boff, boff + NBY) of the chunk
+    const int brow = tid / TPR, boff = (tid % TPR) * NBY;
     const uint8_t *brow_ptr = g.b + (size_t)min(n0 + brow, g.N - 1) * g.nb * DOE_Q4K_BLOCK_BYTES;
-    const _Float16 *arow_ptr[4];
+    const _Float16 *arow_ptr[GA];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < GA; ++i) {
         const int gi = tid + 256 * i;
         arow_ptr[i] = g.a16 + (size_t)min(m0 + (gi >> 3), g.M - 1) * g.Kp + (gi & 7) * 8;
     }
 
-    uint4 ra[4], rh, rq;
-    auto load_chunk = [&](int kc) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const uint4 *>(arow_ptr[i] + kc * kBK);
-        const uint8_t *blk = brow_ptr + (size_t)(kc >> 2) * DOE_Q4K_BLOCK_BYTES;
-        rh = *reinterpret_cast<const uint4 *>(blk);
-        rq = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * (kc & 3) + 16 * bh);
-    };
-    auto store_chunk = [&](int buf, int kc) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int gi = tid + 256 * i;
-            *reinterpret_cast<uint4 *>(&As[buf][(gi >> 3) * kLdsRow + (gi & 7) * 8]) = ra[i];
-        }
-        uint32_t scp, mnp;
-        scale_min_pair(rh.y, rh.z, rh.w, kc & 3, scp, mnp);
-        const float d = doe_half_bits_to_float(rh.x), dmin = doe_half_bits_to_float(rh.x >> 16);
-        const _Float16 dsl = (_Float16)(d * (float)(scp & 0xffu)), dsh = (_Float16)(d * (float)(scp >> 8));
-        const _Float16 dml = (_Float16)(-(dmin * (float)(mnp & 0xffu))), dmh = (_Float16)(-(dmin * (float)(mnp >> 8)));
-        const half2v dsc_lo = {dsl, dsl}, dsc_hi = {dsh, dsh}, ndmm_lo = {dml, dml}, ndmm_hi = {dmh, dmh};
-        const uint32_t q[4] = {rq.x, rq.y, rq.z, rq.w};
-        uint32_t lo[8], hi[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dequant_dword(q[j], dsc_lo, ndmm_lo, dsc_hi, ndmm_hi, lo + 2 * j, hi + 2 * j);
-        _Float16 *bl = &Bs[buf][brow * kLdsRow + 16 * bh];
-        *reinterpret_cast<uint4 *>(bl) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        *reinterpret_cast<uint4 *>(bl + 8) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-        *reinterpret_cast<uint4 *>(bl + 32) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        *reinterpret_cast<uint4 *>(bl + 40) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-    };
+    u32x4 ra[GA], rh, rq[NQ];
+    // (macros, not lambdas: the staging arrays must stay in registers)
+#define DOE_GEMM_LOAD_CHUNK(KC)                                                                        \
+    do {                                                                                               \
+        _Pragma("unroll") for (int i = 0; i < GA; ++i)                                                 \
+            ra[i] = *reinterpret_cast<const u32x4 *>(arow_ptr[i] + (KC) * kBK);                        \
+        const uint8_t *blk_ = brow_ptr + (size_t)((KC) >> 2) * DOE_Q4K_BLOCK_BYTES;                    \
+        rh = *reinterpret_cast<const u32x4 *>(blk_);                                                   \
+        _Pragma("unroll") for (int j = 0; j < NQ; ++j)                                                 \
+            rq[j] = *reinterpret_cast<const u32x4 *>(blk_ + 16 + 32 * ((KC) & 3) + boff + 16 * j);     \
+    } while (0)
+#define DOE_GEMM_STORE_CHUNK(BUF, KC)                                                                  \
+    do {                                                                                               \
+        _Pragma("unroll") for (int i = 0; i < GA; ++i) {                                               \
+            const int gi = tid + 256 * i;                                                              \
+            *reinterpret_cast<u32x4 *>(&As[BUF][(gi >> 3) * kLdsRow + (gi & 7) * 8]) = ra[i];          \
+        }                                                                                              \
+        uint32_t scp_, mnp_;                                                                           \
+        scale_min_pair(rh.y, rh.z, rh.w, (KC) & 3, scp_, mnp_);                                        \
+        const float d_ = doe_half_bits_to_float(rh.x), dmin_ = doe_half_bits_to_float(rh.x >> 16);     \
+        const _Float16 dsl_ = (_Float16)(d_ * (float)(scp_ & 0xffu));                                  \
+        const _Float16 dsh_ = (_Float16)(d_ * (float)(scp_ >> 8));                                     \
+        const _Float16 dml_ = (_Float16)(-(dmin_ * (float)(mnp_ & 0xffu)));                            \
+        const _Float16 dmh_ = (_Float16)(-(dmin_ * (float)(mnp_ >> 8)));                               \
+        const half2v dsc_lo = {dsl_, dsl_}, dsc_hi = {dsh_, dsh_}, ndmm_lo = {dml_, dml_},             \
+                     ndmm_hi = {dmh_, dmh_};                                                           \
+        _Pragma("unroll") for (int j = 0; j < NQ; ++j) {                                               \
+            uint32_t lo[8], hi[8];                                                                     \
+            dequant_dword(rq[j].x, dsc_lo, ndmm_lo, dsc_hi, ndmm_hi, lo + 0, hi + 0);                  \
+            dequant_dword(rq[j].y, dsc_lo, ndmm_lo, dsc_hi, ndmm_hi, lo + 2, hi + 2);                  \
+            dequant_dword(rq[j].z, dsc_lo, ndmm_lo, dsc_hi, ndmm_hi, lo + 4, hi + 4);                  \
+            dequant_dword(rq[j].w, dsc_lo, ndmm_lo, dsc_hi, ndmm_hi, lo + 6, hi + 6);                  \
+            _Float16 *bl = &Bs[BUF][brow * kLdsRow + boff + 16 * j];                                   \
+            *reinterpret_cast<u32x4 *>(bl) = u32x4{lo[0], lo[1], lo[2], lo[3]};                        \
+            *reinterpret_cast<u32x4 *>(bl + 8) = u32x4{lo[4], lo[5], lo[6], lo[7]};                    \
+            *reinterpret_cast<u32x4 *>(bl + 32) = u32x4{hi[0], hi[1], hi[2], hi[3]};                   \
+            *reinterpret_cast<u32x4 *>(bl + 40) = u32x4{hi[4], hi[5], hi[6], hi[7]};                   \
+        }                                                                                              \
+    } while (0)
 
-    float16v acc[2][2];
+    float16v acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    DOE_GEMM_LOAD_CHUNK(0);
+    DOE_GEMM_STORE_CHUNK(0, 0);
+    __syncthreads();
+    const int lr = lane & 31, lk = 8 * (lane >> 5);
+    for (int kc = 0; kc < g.nchunk; ++kc) {
+        const int buf = kc & 1;
+        if (kc + 1 < g.nchunk) DOE_GEMM_LOAD_CHUNK(kc + 1);
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            half8 af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                af[i] = *reinterpret_cast<const half8 *>(&As[buf][(wm * 32 * TM + i * 32 + lr) * kLdsRow + ks * 16 + lk]);
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                bf[j] = *reinterpret_cast<const half8 *>(&Bs[buf][(wn * 32 * TN + j * 32 + lr) * kLdsRow + ks * 16 + lk]);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kc + 1 < g.nchunk) DOE_GEMM_STORE_CHUNK(buf ^ 1, kc + 1);
+        __syncthreads();
+    }
+#undef DOE_GEMM_LOAD_CHUNK
+#undef DOE_GEMM_STORE_CHUNK
+
+    // epilogue: D lane l, r: row (r%4) + 8(r/4) + 4(l/32), column l%32
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + wm * 32 * TM + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+            if (m >= g.M) continue;
+            const float us = __builtin_amdgcn_ldexpf(1.0f, -g.sig[m]);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = n0 + wn * 32 * TN + j * 32 + lr;
+                if (n < g.N) g.c[(size_t)m * g.N + n] = acc[i][j][r] * us;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Large-problem GEMM: 256 (M) x 256 (N) tile, the four waves side by side in
+// N (wave w owns columns 64w..64w+63 for all 256 rows: 8 x 2 accumulators).
+// B is staged raw: each Q4_K block (144 bytes) of the tile's 256 rows is
+// loaded once per 256-element K step with line-contiguous 16-byte granules
+// and kept in LDS, and each wave dequantises its MFMA B operands straight
+// from those bytes (8 nibbles -> 8 f16 per lane per 16-k step).  A is staged
+// as f16 per 64-element chunk.  Both are double-buffered; the raw B block
+// for step b + 2 is in flight during the four chunks of step b.
+// ---------------------------------------------------------------------------
+constexpr int kRawRow = 152;  // bytes per raw B row: 144 + 8 pad, conflict-free b64 reads
+
+// Eight f16 operands from 8 nibble bytes (two dwords): low (HI = false) or
+// high nibbles, w = RN_f16(q * dsc - dmm).
+template <bool HI>
+__device__ __forceinline__ half8 dequant8(uint32_t w0, uint32_t w1, half2v dsc, half2v ndmm) {
+    const half2v bias = HI ? half2v{(_Float16)64.0f, (_Float16)64.0f} : half2v{(_Float16)1024.0f, (_Float16)1024.0f};
+    const uint32_t mask = HI ? 0x00f000f0u : 0x000f000fu;
+    const uint32_t magic = HI ? 0x54005400u : 0x64006400u;
+    const uint32_t t[4] = {__builtin_amdgcn_perm(0u, w0, 0x0c010c00u), __builtin_amdgcn_perm(0u, w0, 0x0c030c02u),
+                           __builtin_amdgcn_perm(0u, w1, 0x0c010c00u), __builtin_amdgcn_perm(0u, w1, 0x0c030c02u)};
+    half8 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const half2v q = as_h2((t[e] & mask) | magic) - bias;
+        const half2v v = __builtin_elementwise_fma(q, dsc, ndmm);
+        r[2 * e] = v[0];
+        r[2 * e + 1] = v[1];
+    }
+    return r;
+}
+
+__global__ __launch_bounds__(256) void q4k_gemm_big_kernel(GemmArgs g) {
+    constexpr int BM = 256, BN = 256;
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLdsRow];
+    __shared__ __attribute__((aligned(16))) uint8_t Braw[2][BN * kRawRow];
+
+    const int T = g.tiles_m * g.tiles_n;
+    int t = blockIdx.x;
+    if ((T & 7) == 0) t = (blockIdx.x & 7) * (T >> 3) + (blockIdx.x >> 3);
+    const int per_group = kGroupM * g.tiles_n;
+    const int grp = t / per_group;
+    const int first_m = grp * kGroupM;
+    const int gsize = min(kGroupM, g.tiles_m - first_m);
+    const int within = t - grp * per_group;
+    const int m0 = (first_m + within % gsize) * BM;
+    const int n0 = (within / gsize) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 31, lk = 8 * (lane >> 5);
+
+    // A granules: gi = tid + 256 i -> row gi >> 3, column (gi & 7) * 8
+    const _Float16 *aptr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int gi = tid + 256 * i;
+        aptr[i] = g.a16 + (size_t)min(m0 + (gi >> 3), g.M - 1) * g.Kp + (gi & 7) * 8;
+    }
+    // raw B granules: gi = tid + 256 i -> row gi / 9, 16-byte piece gi % 9
+    const size_t brow_bytes = (size_t)g.nb * DOE_Q4K_BLOCK_BYTES;
+    const uint8_t *bptr[9];
+    int bdst[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+        const int gi = tid + 256 * i;
+        const int row = gi / 9, piece = gi - 9 * (gi / 9);
+        bptr[i] = g.b + (size_t)min(n0 + row, g.N - 1) * brow_bytes + piece * 16;
+        bdst[i] = row * kRawRow + piece * 16;
+    }
+
+    u32x4 ra[8], rb[9];
+    // (macros, not lambdas: the staging arrays must stay in registers)
+#define DOE_BIG_LOAD_A(KC)                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(aptr[i] + (KC) * kBK)
+#define DOE_BIG_STORE_A(BUF)                                                                        \
+    _Pragma("unroll") for (int i = 0; i < 8; ++i)                                                   \
+        *reinterpret_cast<u32x4 *>(&As[BUF][((tid + 256 * i) >> 3) * kLdsRow + ((tid + 256 * i) & 7) * 8]) = ra[i]
+#define DOE_BIG_LOAD_B(BLK)                                                                         \
+    _Pragma("unroll") for (int i = 0; i < 9; ++i)                                                   \
+        rb[i] = *reinterpret_cast<const u32x4 *>(bptr[i] + (size_t)(BLK) * DOE_Q4K_BLOCK_BYTES)
+#define DOE_BIG_STORE_B(BUF)                                                                        \
+    _Pragma("unroll") for (int i = 0; i < 9; ++i) {                                                 \
+        u32x2 *d_ = reinterpret_cast<u32x2 *>(&Braw[BUF][bdst[i]]);                                 \
+        d_[0] = u32x2{rb[i].x, rb[i].y};                                                            \
+        d_[1] = u32x2{rb[i].z, rb[i].w};                                                            \
+    }
+
+    float16v acc[8][2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    load_chunk(0);
-    store_chunk(0, 0);
+    DOE_BIG_LOAD_A(0);
+    DOE_BIG_LOAD_B(0);
+    DOE_BIG_STORE_A(0);
+    DOE_BIG_STORE_B(0);
+    if (g.nb > 1) {
+        DOE_BIG_LOAD_B(1);
+    }
     __syncthreads();
-    const int lr = lane & 31, lk = 8 * (lane >> 5);
+
     for (int kc = 0; kc < g.nchunk; ++kc) {
-        const int buf = kc & 1;
-        if (kc + 1 < g.nchunk) load_chunk(kc + 1);
+        const int abuf = kc & 1, bbuf = (kc >> 2) & 1, c4 = kc & 3;
+        if (kc + 1 < g.nchunk) {
+            DOE_BIG_LOAD_A(kc + 1);
+        }
+        // this lane's two B rows: scale/min of sub-blocks 2*c4, 2*c4 + 1
+        half2v dsc[2][2], ndmm[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint8_t *hrow = &Braw[bbuf][(wave * 64 + j * 32 + lr) * kRawRow];
+            const u32x2 h01 = *reinterpret_cast<const u32x2 *>(hrow);
+            const u32x2 h23 = *reinterpret_cast<const u32x2 *>(hrow + 8);
+            uint32_t scp, mnp;
+            scale_min_pair(h01.y, h23.x, h23.y, c4, scp, mnp);
+            const float d = doe_half_bits_to_float(h01.x), dmin = doe_half_bits_to_float(h01.x >> 16);
+            const _Float16 s0 = (_Float16)(d * (float)(scp & 0xffu)), s1 = (_Float16)(d * (float)(scp >> 8));
+            const _Float16 z0 = (_Float16)(-(dmin * (float)(mnp & 0xffu)));
+            const _Float16 z1 = (_Float16)(-(dmin * (float)(mnp >> 8)));
+            dsc[j][0] = half2v{s0, s0};
+            dsc[j][1] = half2v{s1, s1};
+            ndmm[j][0] = half2v{z0, z0};
+            ndmm[j][1] = half2v{z1, z1};
+        }
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
-            half8 af[2], bf[2];
+            half8 af[8], bf[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *reinterpret_cast<const half8 *>(&As[buf][(wm * 64 + i * 32 + lr) * kLdsRow + ks * 16 + lk]);
+            for (int i = 0; i < 8; ++i)
+                af[i] = *reinterpret_cast<const half8 *>(&As[abuf][(i * 32 + lr) * kLdsRow + ks * 16 + lk]);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bf[j] = *reinterpret_cast<const half8 *>(&Bs[buf][(wn * 64 + j * 32 + lr) * kLdsRow + ks * 16 + lk]);
+            for (int j = 0; j < 2; ++j) {
+                const u32x2 raw = *reinterpret_cast<const u32x2 *>(
+                    &Braw[bbuf][(wave * 64 + j * 32 + lr) * kRawRow + 16 + 32 * c4 + ((ks * 16 + lk) & 31)]);
+                bf[j] = ks < 2 ? dequant8<false>(raw.x, raw.y, dsc[j][0], ndmm[j][0])
+                               : dequant8<true>(raw.x, raw.y, dsc[j][1], ndmm[j][1]);
+            }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < 8; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        if (kc + 1 < g.nchunk) store_chunk(buf ^ 1, kc + 1);
+        if (kc + 1 < g.nchunk) {
+            DOE_BIG_STORE_A(abuf ^ 1);
+        }
+        if (c4 == 3 && (kc >> 2) + 1 < g.nb) {
+            DOE_BIG_STORE_B(bbuf ^ 1);
+            if ((kc >> 2) + 2 < g.nb) {
+                DOE_BIG_LOAD_B((kc >> 2) + 2);
+            }
+        }
         __syncthreads();
     }
+#undef DOE_BIG_LOAD_A
+#undef DOE_BIG_STORE_A
+#undef DOE_BIG_LOAD_B
+#undef DOE_BIG_STORE_B
 
     // epilogue: D lane l, r: row (r%4) + 8(r/4) + 4(l/32), column l%32
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 8; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m = m0 + wm * 64 + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+            const int m = m0 + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
             if (m >= g.M) continue;
             const float us = __builtin_amdgcn_ldexpf(1.0f, -g.sig[m]);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int n = n0 + wn * 64 + j * 32 + lr;
+                const int n = n0 + wave * 64 + j * 32 + lr;
                 if (n < g.N) g.c[(size_t)m * g.N + n] = acc[i][j][r] * us;
             }
         }
@@ -292,11 +492,17 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
     g.Kp = (int)kp;
     g.nb = (int)((k + 255) / 256);
     g.nchunk = (int)(kp / kBK);
-    g.tiles_m = (int)((m + kBM - 1) / kBM);
-    g.tiles_n = (int)((n + kBN - 1) / kBN);
+    // 256 x 256 tiles once there are enough of them to fill the CUs, else 128 x 128
+    const bool big = m >= 256 && n >= 256 && ((m + 255) / 256) * ((n + 255) / 256) >= 256;
+    const int bm = big ? 256 : 128, bn = big ? 256 : 128;
+    g.tiles_m = (int)((m + bm - 1) / bm);
+    g.tiles_n = (int)((n + bn - 1) / bn);
     const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
     DOE_REQUIRE(tiles <= 0x7fffffff, DOE_E_UNSUPPORTED, "too many tiles");
-    hipLaunchKernelGGL(q4k_gemm_kernel, dim3((unsigned)tiles), dim3(256), 0, st, g);
+    if (big)
+        hipLaunchKernelGGL(q4k_gemm_big_kernel, dim3((unsigned)tiles), dim3(256), 0, st, g);
+    else
+        hipLaunchKernelGGL((q4k_gemm_kernel<2, 2>), dim3((unsigned)tiles), dim3(256), 0, st, g);
     DOE_LAUNCH_CHECK("q4k_gemm_kernel");
     return DOE_OK;
 }

@@ -68,6 +68,28 @@ def test_gemm_prefill_config_sampled(dev, ora):
     assert np.isfinite(got).all()
 
 
+def test_gemm_large_tiles_ragged(dev, ora):
+    # enough tiles for the 256 x 256 path, with M, N and K all off the tile
+    # grid (K tail inside the last Q4_K block): sampled entries, including the
+    # last row and column
+    m, n, k = 2000, 33000, 1000
+    rng = np.random.default_rng(5)
+    a = to_bf16(rng.standard_normal((m, k), dtype=np.float32))
+    b = q4k.random_q4k(rng, n, k)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_q4k_gemm(up(a), up(b), out, m, n, k)
+    got = out.download()
+    mi = np.concatenate([rng.integers(0, m, 1500), [m - 1, m - 1, 0, 1999]]).astype(np.int64)
+    ni = np.concatenate([rng.integers(0, n, 1500), [n - 1, 0, n - 1, 32767]]).astype(np.int64)
+    order = np.argsort(ni, kind="stable")
+    mi, ni = mi[order], ni[order]
+    want = ora.q4k_gemm_sampled(a, b, m, n, k, mi, ni)
+    err = rel_l2(got[mi, ni], want)
+    print(f"[gemm ragged] sampled rel_l2 {err:.2e}", flush=True)
+    assert err <= TOL
+    assert np.isfinite(got).all()
+
+
 def test_gemm_row_scaling_extremes(dev, ora):
     # rows of very different magnitude (2^-60 .. 2^60, a zero row, a row with
     # one non-zero): each row keeps the contract on its own
