@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import sys
@@ -295,6 +296,64 @@ def bench_gemm(args, doe):
     }
 
 
+PF_HQ, PF_HKV, PF_D, PF_S = 32, 16, 128, 2048
+PF_FLOP = PF_HQ * PF_D * 4 * PF_S * (PF_S + 1) // 2  # causal: q.k and p.v over keys 0..i
+
+
+def bench_prefill_attention(args, doe):
+    """Causal GQA prefill attention at the 31B-class shape (32 q / 16 kv heads,
+    head_dim 128, 2048 tokens, bf16 q/K/V N(0,1), f32 out); HIP events around
+    back-to-back calls; oracle parity on sampled rows."""
+    from doe_amd import DeviceBuffer, Event, Stream, ops
+
+    rng = np.random.default_rng(4)
+    q = to_bf16(rng.standard_normal((PF_S, PF_HQ, PF_D), dtype=np.float32))
+    k = to_bf16(rng.standard_normal((PF_HKV, PF_S, PF_D), dtype=np.float32))
+    v = to_bf16(rng.standard_normal((PF_HKV, PF_S, PF_D), dtype=np.float32))
+    dq, dk, dv = DeviceBuffer.from_array(q), DeviceBuffer.from_array(k), DeviceBuffer.from_array(v)
+    out = DeviceBuffer.empty((PF_S, PF_HQ, PF_D), np.float32)
+    s = Stream()
+    scale = 1.0 / math.sqrt(PF_D)
+
+    def call():
+        ops.attention_prefill(dq, dk, dv, out, num_heads=PF_HQ, num_kv_heads=PF_HKV, head_dim=PF_D, q_len=PF_S,
+                              kv_len=PF_S, scale=scale, causal=True, stream=s)
+
+    for _ in range(2):
+        call()
+    s.synchronize()
+    reps = args.gemm_steps
+    e0, e1 = Event(), Event()
+    e0.record(s)
+    for _ in range(reps):
+        call()
+    e1.record(s)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    from oracle import oracle as ora
+
+    f = lambda b: (b.astype(np.uint32) << 16).view(np.float32)
+    got = out.download()
+    errs = []
+    for r0, r1 in ((0, 8), (1024, 1032), (2040, 2048)):
+        want = ora.attn_prefill(f(q), f(k), f(v), PF_HQ, PF_HKV, PF_D, PF_S, PF_S, 0, scale, True, (r0, r1))
+        errs.append(float(np.linalg.norm(got[r0:r1] - want[r0:r1]) / np.linalg.norm(want[r0:r1])))
+    s.destroy()
+    for b in (dq, dk, dv, out):
+        b.free()
+    tflops = PF_FLOP / (ms * 1e-3) / 1e12
+    log(f"prefill attention: {ms * 1e3:.1f} us/call, {tflops:.0f} TFLOP/s "
+        f"({100 * tflops / MFMA_F16_PEAK_TFLOPS:.1f}% of the bf16/f16 MFMA peak), sampled rel_l2 {max(errs):.2e}")
+    return {
+        "workload": f"causal GQA prefill attention Hq={PF_HQ} Hkv={PF_HKV} D={PF_D} S={PF_S}, bf16 q/K/V, f32 out",
+        "us_per_call": round(ms * 1e3, 2),
+        "flop_per_call": PF_FLOP,
+        "achieved_tflops": round(tflops, 1),
+        "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+        "rel_l2_vs_oracle_sampled": max(errs),
+    }
+
+
 def traffic_bytes(summary: str):
     """HBM bytes per launch recorded in a committed rocprofv3 summary
     (line `traffic_bytes_per_launch: <int>`), or None."""
@@ -369,6 +428,7 @@ def main() -> int:
     att = bench_attention(args, doe_amd)
     dec = None if args.no_decode else bench_decode(args, doe_amd)
     gemm = None if args.no_gemm else bench_gemm(args, doe_amd)
+    pfa = None if args.no_gemm else bench_prefill_attention(args, doe_amd)
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of the single-threaded oracle")
@@ -408,6 +468,7 @@ def main() -> int:
         "attention_decode": att,
         "decode": dec,
         "prefill_gemm": gemm,
+        "prefill_attention": pfa,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -88,6 +88,24 @@ def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, out
               sliding_window, _stream_ptr(stream))
 
 
+def attention_prefill(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, output: DeviceBuffer, *, num_heads: int,
+                      num_kv_heads: int, head_dim: int, q_len: int, kv_len: int, kv_stride: int | None = None,
+                      start_pos: int = 0, scale: float, causal: bool = True, out_bf16: bool = False,
+                      stream=None) -> None:
+    """``attention`` op, prefill form (tiled, ``is_causal``): bf16 q
+    [q_len][Hq][D] against bf16 K/V [Hkv][kv_stride][D]; f32 (or bf16) output
+    [q_len][Hq][D]."""
+    kv_stride = kv_len if kv_stride is None else kv_stride
+    if num_kv_heads <= 0 or num_heads % num_kv_heads:
+        raise ValueError(f"num_heads {num_heads} is not a multiple of num_kv_heads {num_kv_heads}")
+    _need(q, q_len * num_heads * head_dim * 2, "q")
+    _need(k, num_kv_heads * kv_stride * head_dim * 2, "k")
+    _need(v, num_kv_heads * kv_stride * head_dim * 2, "v")
+    _need(output, q_len * num_heads * head_dim * (2 if out_bf16 else 4), "output")
+    _lib.call("doe_attn_prefill", _p(q), _p(k), _p(v), _p(output), int(out_bf16), num_heads, num_kv_heads,
+              head_dim, q_len, kv_len, kv_stride, start_pos, scale, int(causal), _stream_ptr(stream))
+
+
 def matmul_q4k_fused(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int, *,
                      norm_weight: DeviceBuffer | None = None, norm_eps: float = 1e-6,
                      norm_weight_offset: bool = True, residual: DeviceBuffer | None = None,
@@ -254,6 +272,7 @@ def tune(key: str, value: int) -> None:
 
 OPS = {
     "attention": attention,
+    "attention_prefill": attention_prefill,
     "dequant": dequant_q4k,
     "embed": embed,
     "gelu_gated": gelu_gated,

@@ -154,6 +154,21 @@ int doe_q4k_gemv_qkv_rope_kv(const void *weight_q4k, const float *activation, fl
                              const int32_t *position_dev, uint16_t *key_cache,
                              uint16_t *val_cache, int64_t max_seq_len, doe_stream_t stream);
 
+/* Causal GQA prefill attention (flash form): out[i][h][:] = softmax over keys
+ * j (j <= start_pos + i when causal) of q[i][h] . k[h/(Hq/Hkv)][j] * scale,
+ * weighting v.  q bf16 [q_len][num_heads][128], k/v bf16
+ * [num_kv_heads][kv_stride][128] (cache layout [kv_head][pos][dim]; keys
+ * [0, kv_len) used), out f32 (out_bf16 = 0) or bf16 [q_len][num_heads][128];
+ * all 16-byte aligned.  Replaces the tiled/causal path of the `attention` op
+ * (attention_head256_f16kv.wgsl:72-267 with is_causal, query blocks of 32;
+ * CPU tiled online softmax run_csl_webgpu_emulator.mjs:646-720).  Q.K^T on
+ * bf16 matrix cores, P.V on f16 matrix cores (V converted exactly for |v| in
+ * [2^-14, 65504]), f32 softmax and accumulation.  head_dim 128 only. */
+int doe_attn_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, void *out,
+                     int out_bf16, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                     int64_t q_len, int64_t kv_len, int64_t kv_stride, int64_t start_pos,
+                     float scale, int causal, doe_stream_t stream);
+
 /* ---- attention ---------------------------------------------------------------
  * GQA decode attention over an f16 KV cache: one query token per sequence.
  * Replaces the `attention` op (emit_csl_exec_v1.zig:117 -> attention_decode;
