@@ -63,6 +63,18 @@ def matmul_q4k_gemm(a_bf16: DeviceBuffer, weight: DeviceBuffer, output: DeviceBu
     _lib.call("doe_q4k_gemm", _p(a_bf16), _p(weight), _p(output), m, n, k, _stream_ptr(stream))
 
 
+def matmul_int4g32(weight_u4: DeviceBuffer, scales_f16: DeviceBuffer, x: DeviceBuffer, output: DeviceBuffer,
+                   m: int, n: int, k: int, stream=None) -> None:
+    """Fused int4 group-32 dequant GEMV (``complex_fused_gemv_dequant``) over a
+    batch of m <= 8 activation rows: output f32[m][n] = x f32[m][k] @
+    ((q - 8) * scale)[n][k]^T."""
+    _need(weight_u4, n * k // 2, "weight")
+    _need(scales_f16, n * (k // 32) * 2, "scales")
+    _need(x, m * k * 4, "x")
+    _need(output, m * n * 4, "output")
+    _lib.call("doe_int4g32_gemv", _p(weight_u4), _p(scales_f16), _p(x), _p(output), m, n, k, _stream_ptr(stream))
+
+
 def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, output: DeviceBuffer, *,
               batch: int, num_heads: int, num_kv_heads: int, head_dim: int, kv_len: int,
               kv_stride: int, scale: float, q_f16: bool = False, out_f16: bool = False,
@@ -280,6 +292,7 @@ OPS = {
     "lm_head": lm_head,
     "matmul_q4k": matmul_q4k,
     "matmul_q4k_gemm": matmul_q4k_gemm,
+    "matmul_int4g32": matmul_int4g32,
     "residual": residual,
     "rmsnorm": rmsnorm,
     "rope": rope,

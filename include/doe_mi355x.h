@@ -116,6 +116,20 @@ int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
 int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m, int64_t n,
                  int64_t k, doe_stream_t stream);
 
+/* Symmetric int4 group-32 GEMV, batch m in 1..8: y[b][i] = sum_k
+ * (q[i][k] - 8) * s[i][k/32] * x[b][k].  w_u4: eight nibbles per u32, element
+ * k of row i at bits 4*(k%8) of word (i*k_dim + k)/8; scales f16 [n][k/32];
+ * x f32 [m][k]; y f32 [m][n]; k a multiple of 256; 16-byte aligned.
+ * Replaces the fused int4 dequant GEMV of
+ * bench/kernels/compilation-corpus/complex_fused_gemv_dequant.wgsl:18-66
+ * (bindings quant_weights, scales, input_vec, output; uniforms rows, cols,
+ * group_size = 32), with f16 scales and an activation batch.  f16 matrix
+ * cores, x split into two f16 halves (~22 bits), f32 accumulation.  Uses a
+ * library-owned workspace (x image and split-K partials), grown on demand
+ * (not during stream capture). */
+int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const float *x, float *y,
+                     int64_t m, int64_t n, int64_t k, doe_stream_t stream);
+
 /* Fused decode GEMV: the plain Q4_K GEMV with the neighbouring steps of the
  * Doppler decode step list folded in (runtime/zig/examples/execution-v1/
  * gemma-3-270m-smoke.json: input_norm -> q/k/v_proj, o_proj ->

@@ -1,0 +1,83 @@
+"""GPU parity of the symmetric int4 group-32 GEMV (batch 1..8, f16 scales)
+against the CPU oracle's f32 left-fold (complex_fused_gemv_dequant.wgsl
+semantics), through the C ABI.  Contract: rel-L2 <= 1e-3; measured ~1e-6."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from doe_amd import DeviceBuffer, _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def random_int4(rng, n, k):
+    """Nibbles q+8 for q uniform in -8..7, eight per u32 (element k at bits
+    4*(k%8)), and f16 scales |N(0, 0.02)| per 32 elements."""
+    nib = rng.integers(0, 16, (n, k), dtype=np.uint32)
+    words = np.zeros((n, k // 8), np.uint32)
+    for j in range(8):
+        words |= nib[:, j::8] << (4 * j)
+    scales = np.abs(rng.normal(0.0, 0.02, (n, k // 32))).astype(np.float16)
+    return words, scales
+
+
+def up(a):
+    return DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 9216, 5120), (1, 64, 256), (3, 1000, 512), (8, 100, 25600),
+                                   (5, 5120, 2048), (8, 17, 256)])
+def test_int4_gemv_matches_oracle(dev, ora, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    w, s = random_int4(rng, n, k)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_int4g32(up(w), up(s), up(x), out, m, n, k)
+    got = out.download()
+    want = ora.int4g32_gemv(w, s, x, m, n, k)
+    err = rel_l2(got, want)
+    print(f"[int4 {m}x{n}x{k}] rel_l2 {err:.2e}", flush=True)
+    assert err <= 1e-5
+
+
+def test_int4_known_answer_and_extremes(dev, ora):
+    # all nibbles 15 (q = 7) with scale 0.5 and x = 1: every output is
+    # 7 * 0.5 * k; all nibbles 0 (q = -8) gives -4 k; then per-row x scales of
+    # 2^60 and 2^-60 keep the contract
+    n, k = 32, 512
+    w = np.full((n, k // 8), 0xFFFFFFFF, np.uint32)
+    w[16:] = 0
+    s = np.full((n, k // 32), 0.5, np.float16)
+    x = np.ones((2, k), np.float32)
+    out = DeviceBuffer.empty((2, n), np.float32)
+    ops.matmul_int4g32(up(w), up(s), up(x), out, 2, n, k)
+    got = out.download()
+    assert np.array_equal(got[:, :16], np.full((2, 16), 3.5 * k, np.float32))
+    assert np.array_equal(got[:, 16:], np.full((2, 16), -4.0 * k, np.float32))
+    rng = np.random.default_rng(5)
+    w, s = random_int4(rng, 256, 1024)
+    x = rng.standard_normal((4, 1024), dtype=np.float32)
+    x[1] *= 2.0 ** 60
+    x[2] *= 2.0 ** -60
+    x[3, ::3] = 0.0
+    out = DeviceBuffer.empty((4, 256), np.float32)
+    ops.matmul_int4g32(up(w), up(s), up(x), out, 4, 256, 1024)
+    got = out.download()
+    want = ora.int4g32_gemv(w, s, x, 4, 256, 1024)
+    for b in range(4):
+        assert rel_l2(got[b], want[b]) <= 1e-5, b
+
+
+def test_int4_rejects_bad_shapes(dev):
+    buf = DeviceBuffer(1 << 16)
+    for m, k in ((9, 256), (0, 256), (1, 100)):
+        with pytest.raises(_lib.DoeError):
+            _lib.call("doe_int4g32_gemv", C.c_void_p(buf.ptr), C.c_void_p(buf.ptr), C.c_void_p(buf.ptr),
+                      C.c_void_p(buf.ptr), m, 4, k, C.c_void_p(None))
