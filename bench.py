@@ -354,6 +354,85 @@ def bench_prefill_attention(args, doe):
     }
 
 
+C4_B, C4_HQ, C4_HKV, C4_D, C4_T = 8, 64, 8, 128, 32768
+C4_GEMVS = (("qkv", 9216, 5120), ("ffn_up", 25600, 5120), ("ffn_down", 5120, 25600))
+
+
+def bench_config4(args, doe):
+    """27B-class long-context decode at batch 8, per layer: GQA attention over
+    32768 cached positions per sequence (64 q / 8 kv heads, head_dim 128, f16
+    K/V = 1 GiB) and the int4 group-32 GEMVs (QKV 5120->9216, FFN 5120->25600
+    ->5120, f16 scales) at M = 8.  HIP events around back-to-back calls; the
+    GEMVs rotate weight copies so the 256 MB Infinity Cache cannot hold them."""
+    import ctypes as C
+
+    from doe_amd import DeviceBuffer, Event, Stream, _lib, ops
+
+    s = Stream()
+    sp = C.c_void_p(s.handle)
+
+    def timed(fn, reps):
+        fn(0)
+        s.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(s)
+        for i in range(reps):
+            fn(i)
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / reps
+
+    res = {}
+    # attention
+    k = DeviceBuffer.empty((C4_B, C4_HKV, C4_T, C4_D), np.float16)
+    v = DeviceBuffer.empty((C4_B, C4_HKV, C4_T, C4_D), np.float16)
+    _lib.call("doe_fill_normal_f16", C.c_void_p(k.ptr), k.nbytes // 2, 41, 0.0, 1.0, sp)
+    _lib.call("doe_fill_normal_f16", C.c_void_p(v.ptr), v.nbytes // 2, 42, 0.0, 1.0, sp)
+    q = DeviceBuffer.empty((C4_B, C4_HQ, C4_D), np.float16)
+    _lib.call("doe_fill_normal_f16", C.c_void_p(q.ptr), q.nbytes // 2, 43, 0.0, 1.0, sp)
+    o = DeviceBuffer.empty((C4_B, C4_HQ, C4_D), np.float16)
+    ms = timed(lambda i: ops.attention(q, k, v, o, batch=C4_B, num_heads=C4_HQ, num_kv_heads=C4_HKV, head_dim=C4_D,
+                                       kv_len=C4_T, kv_stride=C4_T, scale=1.0 / math.sqrt(C4_D), q_f16=True,
+                                       out_f16=True, stream=s), 10)
+    att_bytes = k.nbytes + v.nbytes + q.nbytes + o.nbytes
+    res["attention"] = {"us_per_call": round(ms * 1e3, 2), "bytes_per_call": att_bytes,
+                        "achieved_gbs": round(att_bytes / (ms * 1e-3) / 1e9, 1)}
+    for b in (k, v, q, o):
+        b.free()
+    # int4 GEMVs
+    rng = np.random.default_rng(44)
+    x = DeviceBuffer.from_array(rng.standard_normal((C4_B, 25600), dtype=np.float32))
+    total_us, total_bytes = res["attention"]["us_per_call"], att_bytes
+    for name, n, kdim in C4_GEMVS:
+        wbytes, sbytes = n * kdim // 2, n * (kdim // 32) * 2
+        copies = max(2, -(-768 * 2 ** 20 // (wbytes + sbytes)))
+        ws = [DeviceBuffer(wbytes) for _ in range(copies)]
+        ss = [DeviceBuffer(sbytes) for _ in range(copies)]
+        for i in range(copies):
+            _lib.call("doe_fill_uniform_i32", C.c_void_p(ws[i].ptr), wbytes // 4, 50 + i, -2 ** 31, 2 ** 31 - 1, sp)
+            _lib.call("doe_fill_normal_f16", C.c_void_p(ss[i].ptr), sbytes // 2, 60 + i, 0.0, 0.02, sp)
+        y = DeviceBuffer.empty((C4_B, n), np.float32)
+        ms = timed(lambda i: ops.matmul_int4g32(ws[i % copies], ss[i % copies], x, y, C4_B, n, kdim, stream=s),
+                   4 * copies)
+        byt = wbytes + sbytes + C4_B * kdim * 4 + C4_B * n * 4
+        res[name] = {"m_n_k": [C4_B, n, kdim], "us_per_call": round(ms * 1e3, 2), "bytes_per_call": byt,
+                     "achieved_gbs": round(byt / (ms * 1e-3) / 1e9, 1), "weight_copies": copies}
+        total_us += ms * 1e3
+        total_bytes += byt
+        for b in ws + ss + [y]:
+            b.free()
+    x.free()
+    s.destroy()
+    res["layer_us"] = round(total_us, 2)
+    res["layer_bytes"] = total_bytes
+    res["layer_gbs"] = round(total_bytes / (total_us * 1e-6) / 1e9, 1)
+    log(f"config4 (batch 8, 32k context): attention {res['attention']['us_per_call']} us "
+        f"({res['attention']['achieved_gbs']} GB/s); int4 GEMVs " +
+        ", ".join(f"{nm} {res[nm]['us_per_call']} us ({res[nm]['achieved_gbs']} GB/s)" for nm, _, _ in C4_GEMVS))
+    return {"workload": "27B-class batch-8 long-context decode layer: GQA attention 64q/8kv x 128 over 32768 "
+                        "positions (f16 KV, 1 GiB), int4 group-32 GEMVs with f16 scales at M=8", **res}
+
+
 def traffic_bytes(summary: str):
     """HBM bytes per launch recorded in a committed rocprofv3 summary
     (line `traffic_bytes_per_launch: <int>`), or None."""
@@ -429,6 +508,7 @@ def main() -> int:
     dec = None if args.no_decode else bench_decode(args, doe_amd)
     gemm = None if args.no_gemm else bench_gemm(args, doe_amd)
     pfa = None if args.no_gemm else bench_prefill_attention(args, doe_amd)
+    c4 = None if args.no_gemm else bench_config4(args, doe_amd)
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of the single-threaded oracle")
@@ -469,6 +549,7 @@ def main() -> int:
         "decode": dec,
         "prefill_gemm": gemm,
         "prefill_attention": pfa,
+        "config4_decode_layer": c4,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -9,17 +9,21 @@
 // The batch rides in the N dimension of v_mfma_f32_16x16x32_f16: one MFMA is
 // 16 weight rows x one 32-element group x 16 columns, columns 0..7 carrying
 // x_hi of the eight batch rows and 8..15 their x_lo (x = x_hi + x_lo in f16
-// after a power-of-two scale per batch row), so nothing in the matrix core is
+// after a power-of-two scale per batch row and group), so nothing in the matrix core is
 // wasted at M = 8 and the products carry ~22 bits of x.  (q - 8) is exact in
 // f16 (OR the nibble into the mantissa of 1024, subtract 1032), each group's
 // 16x16 result is scaled by its f16 scale in f32, and the hi/lo halves meet
 // in one lane exchange at the end.
 //
 // A pre-pass writes x as the MFMA's B-operand image ([group][64 lanes][8 f16],
-// 1 KB per group, read by every workgroup from L2).  Each wave owns 16 rows
-// and a K range; K is split over the grid's y dimension when the rows alone
-// do not fill the GPU, and the splits are summed by a small second kernel
-// (deterministic order, no atomics).
+// 1 KB per group, plus one power-of-two unscale factor per group and batch
+// row: x is scaled per 32-element group so max|x| sits near 2^14), read by
+// every workgroup from L2.  A workgroup owns 64 rows (four 16-row MFMA tiles
+// per wave, so each x fragment feeds four MFMAs) and 32 groups of K, eight
+// per wave with every load of a wave issued up front; the
+// four waves' sums meet in LDS.  K is split over the grid's y dimension when
+// the rows alone do not fill the GPU, and the splits are summed by a small
+// second kernel (deterministic order, no atomics).
 #include "common.h"
 
 #include <math.h>
@@ -35,51 +39,50 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMaxBatch = 8;
 
 // x image: lane l of group g holds, for column c = l % 16 (batch c % 8, part
-// c / 8: 0 = hi, 1 = lo), x at k = 32 g + 8 (l / 16) + {0, 4, 1, 5, 2, 6, 3, 7}[j].
+// c / 8: 0 = hi, 1 = lo), x * 2^sig[b][g] at k = 32 g + 8 (l / 16) +
+// {0, 4, 1, 5, 2, 6, 3, 7}[j]; unscale[g][c] = 2^-sig[b][g] (0 past the batch).
+// One thread per (group, batch row, lane group): eight groups per workgroup.
 __global__ __launch_bounds__(256) void int4_x_image_kernel(const float *__restrict__ x,
                                                            _Float16 *__restrict__ img,
                                                            float *__restrict__ unscale, int M,
                                                            int K) {
-    const int b = blockIdx.x;
-    const int G = K / 32;
-    __shared__ float wmax[4];
-    __shared__ int ssig;
-    int sig = 0;
+    const int lg = threadIdx.x & 3, b = (threadIdx.x >> 2) & 7;
+    const int g = blockIdx.x * 8 + (threadIdx.x >> 5);
+    if (g >= K / 32) return;  // whole quads leave together
+    float v[8];
     if (b < M) {
-        float amax = 0.0f;
-        for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(x[(size_t)b * K + k]));
+        const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t)b * K + 32 * g + 8 * lg);
+        const float4 a = xp[0], c = xp[1];
+        v[0] = a.x; v[1] = c.x; v[2] = a.y; v[3] = c.y; v[4] = a.z; v[5] = c.z; v[6] = a.w; v[7] = c.w;
+    } else {
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-        if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const float mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-            int s = 0;
-            if (mx > 0.0f && mx <= 3.0e38f) {
-                s = 14 - __builtin_amdgcn_frexp_expf(mx);
-                s = s < -120 ? -120 : (s > 120 ? 120 : s);
-            }
-            ssig = s;
-            unscale[b] = __builtin_amdgcn_ldexpf(1.0f, -s);
-        }
-        __syncthreads();
-        sig = ssig;
+        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    int sig = 0;
+    if (amax > 0.0f && amax <= 3.0e38f) {
+        sig = 14 - __builtin_amdgcn_frexp_expf(amax);
+        sig = sig < -120 ? -120 : (sig > 120 ? 120 : sig);
     }
     const float sc = __builtin_amdgcn_ldexpf(1.0f, sig);
-    // items: (g, lane group lg, part) -> 8 halves at lane lg*16 + part*8 + b
-    for (int it = threadIdx.x; it < G * 8; it += 256) {
-        const int g = it >> 3, lg = (it >> 1) & 3, part = it & 1;
-        _Float16 v[8];
+    _Float16 hi[8], lo[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int kk = 32 * g + 8 * lg + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
-            float t = b < M ? x[(size_t)b * K + kk] * sc : 0.0f;
-            const _Float16 hi = (_Float16)t;
-            v[j] = part == 0 ? hi : (_Float16)(t - (float)hi);
-        }
-        const int lane = lg * 16 + part * 8 + b;
-        *reinterpret_cast<half8 *>(img + ((size_t)g * 64 + lane) * 8) =
-            half8{v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+    for (int j = 0; j < 8; ++j) {
+        const float t = v[j] * sc;
+        hi[j] = (_Float16)t;
+        lo[j] = (_Float16)(t - (float)hi[j]);
+    }
+    _Float16 *base = img + (size_t)g * 512;
+    *reinterpret_cast<half8 *>(base + (lg * 16 + b) * 8) = half8{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
+    *reinterpret_cast<half8 *>(base + (lg * 16 + 8 + b) * 8) = half8{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
+    if (lg == 0) {
+        const float f = b < M ? __builtin_amdgcn_ldexpf(1.0f, -sig) : 0.0f;
+        unscale[g * 16 + b] = f;
+        unscale[g * 16 + 8 + b] = f;
     }
 }
 
@@ -98,58 +101,116 @@ struct Int4Args {
     const uint16_t *scales;
     const _Float16 *img;
     const float *unscale;
-    float *out;  // y [M][N] (splits == 1) or partials [splits][M][N]
-    int M, N, K, G, gps;  // gps: groups per split (a multiple of 8)
+    float *out;  // y [M][N] (one split) or partials [splits][M][N]
+    int M, N, K, G;
 };
 
+// 64 rows x (4 GPW) groups per workgroup; wave w takes groups
+// [blockIdx.y 4 GPW + w GPW, + GPW).  A row's GPW groups are GPW * 16
+// contiguous bytes: the wave reads them with whole-line 16-byte loads (GPW
+// lanes per row) and regroups them through its own LDS slice into the MFMA
+// lane order (lane (r, j) takes word j of each group of row r).
+template <int GPW>
 __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
+    __shared__ float red[3][4][4][64];
+    __shared__ __attribute__((aligned(16))) uint32_t wl[4][64 * 4 * GPW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int r0 = blockIdx.x * 64 + 16 * wave;
-    if (r0 >= a.N) return;
-    const int g0 = blockIdx.y * a.gps;
-    const int g1 = min(a.G, g0 + a.gps);
-    const int arow = min(r0 + lr, a.N - 1);
-    const uint32_t *qrow = a.q + (size_t)arow * (a.K / 8) + lg;
-    const uint16_t *srow[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) srow[i] = a.scales + (size_t)min(r0 + 4 * lg + i, a.N - 1) * a.G;
-    const _Float16 *ximg = a.img + (size_t)lane * 8;
+    const int r0 = blockIdx.x * 64;
+    const int g0 = (blockIdx.y * 4 + wave) * GPW;
+    const bool active = g0 < a.G;  // a.G is a multiple of GPW
+    const int gb = active ? g0 : 0;
 
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int g = g0; g < g1; g += 8) {
-        // eight groups at a time: weights, x fragments and the scales of this
-        // lane's four D rows, all loads first
-        uint32_t w[8];
-        half8 xb[8];
-        u32x4 sv[4];
+    // all loads first: the 64 rows' weight bytes, GPW x fragments and
+    // unscale factors, and the scales of this lane's 16 D rows
+    constexpr int RPI = 64 / GPW;  // rows per load instruction
+    u32x4 wg[GPW];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) w[u] = __builtin_nontemporal_load(qrow + 4 * (g + u));
+    for (int j = 0; j < GPW; ++j) {
+        const int row = j * RPI + lane / GPW;
+        wg[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
+            a.q + (size_t)min(r0 + row, a.N - 1) * (a.K / 8) + 4 * (gb + lane % GPW)));
+    }
+    half8 xb[GPW];
+    float f[GPW];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) xb[u] = *reinterpret_cast<const half8 *>(ximg + (size_t)(g + u) * 512);
+    for (int u = 0; u < GPW; ++u) {
+        xb[u] = *reinterpret_cast<const half8 *>(a.img + ((size_t)(gb + u) * 64 + lane) * 8);
+        f[u] = a.unscale[(gb + u) * 16 + lr];
+    }
+    u32x4 sv[4][4][GPW / 8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = *reinterpret_cast<const u32x4 *>(srow[i] + g);
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const float4v z = {0.0f, 0.0f, 0.0f, 0.0f};
-            const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_int4(w[u]), xb[u], z, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+            const uint16_t *srow = a.scales + (size_t)min(r0 + 16 * t + 4 * lg + i, a.N - 1) * a.G + gb;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t pair = sv[i][u >> 1];
-                const float s = doe_half_bits_to_float((u & 1) ? (pair >> 16) : pair);
-                acc[i] = fmaf(d[i], s, acc[i]);
+            for (int h = 0; h < GPW / 8; ++h) sv[t][i][h] = *reinterpret_cast<const u32x4 *>(srow + 8 * h);
+        }
+    // regroup: wl[(row * 4 + word) * GPW + group]
+    uint32_t *my = wl[wave];
+#pragma unroll
+    for (int j = 0; j < GPW; ++j) {
+        const int row = j * RPI + lane / GPW, u = lane % GPW;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) my[(row * 4 + e) * GPW + u] = wg[j][e];
+    }
+    // (each wave reads back only its own slice: no workgroup barrier needed)
+    uint32_t w[4][GPW];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(my + ((16 * t + lr) * 4 + lg) * GPW);
+#pragma unroll
+        for (int h = 0; h < GPW / 4; ++h) {
+            const u32x4 v = src[h];
+            w[t][4 * h] = v.x;
+            w[t][4 * h + 1] = v.y;
+            w[t][4 * h + 2] = v.z;
+            w[t][4 * h + 3] = v.w;
+        }
+    }
+
+    float acc[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = 0.0f;
+    if (active) {
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+                const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_int4(w[t][u]), xb[u], z, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t pair = sv[t][i][u >> 3][(u & 7) >> 1];
+                    const float s = doe_half_bits_to_float((u & 1) ? (pair >> 16) : pair);
+                    acc[t][i] = fmaf(d[i] * f[u], s, acc[t][i]);
+                }
             }
         }
     }
-    // D lane l: rows r0 + 4 lg + i, column lr (batch lr % 8; lr / 8: hi / lo)
+    // the four waves' partial sums meet in wave 0
+    if (wave > 0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave - 1][t][i][lane] = acc[t][i];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    // D lane l, tile t: row r0 + 16 t + 4 lg + i, column lr (batch lr % 8; lr / 8: hi / lo)
     const int b = lr & 7;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float v = acc[i] + __shfl_xor(acc[i], 8, 64);
-        const int row = r0 + 4 * lg + i;
-        if (lr < 8 && b < a.M && row < a.N)
-            a.out[((size_t)blockIdx.y * a.M + b) * a.N + row] = v * a.unscale[b];
-    }
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v = acc[t][i] + red[0][t][i][lane] + red[1][t][i][lane] + red[2][t][i][lane];
+            v += __shfl_xor(v, 8, 64);
+            const int row = r0 + 16 * t + 4 * lg + i;
+            if (lr < 8 && b < a.M && row < a.N) a.out[((size_t)blockIdx.y * a.M + b) * a.N + row] = v;
+        }
 }
 
 __global__ __launch_bounds__(256) void int4_split_sum_kernel(const float *__restrict__ part,
@@ -198,18 +259,16 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     }
     const int G = (int)(k / 32);
     const int row_blocks = (int)((n + 63) / 64);
-    // split K until there are ~4 workgroups per CU, keeping >= 8 groups per split
-    int splits = (4 * g_num_cus + row_blocks - 1) / row_blocks;
-    const int max_splits = G / 8;
-    if (splits > max_splits) splits = max_splits;
-    if (splits < 1) splits = 1;
-    int gps = (G + splits - 1) / splits;
-    gps = (gps + 7) / 8 * 8;
-    splits = (G + gps - 1) / gps;
+    // eight groups per wave (every load of a wave in flight at once), K split
+    // over the grid so that the rows times the splits fill the CUs
+    const int gpw = 8;
+    const int per_wg = 4 * gpw;
+    const int splits = (G + per_wg - 1) / per_wg;
 
     const size_t img_bytes = (size_t)G * 64 * 8 * 2;
+    const size_t fac_bytes = (size_t)G * 16 * 4;
     const size_t part_bytes = splits > 1 ? (size_t)splits * m * n * sizeof(float) : 0;
-    const size_t need = img_bytes + 64 + part_bytes;
+    const size_t need = img_bytes + fac_bytes + part_bytes;
     void *ws;
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -224,8 +283,9 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     }
     _Float16 *img = (_Float16 *)ws;
     float *unscale = (float *)((char *)ws + img_bytes);
-    float *part = (float *)((char *)ws + img_bytes + 64);
-    hipLaunchKernelGGL(int4_x_image_kernel, dim3(kMaxBatch), dim3(256), 0, st, x, img, unscale, (int)m, (int)k);
+    float *part = (float *)((char *)ws + img_bytes + fac_bytes);
+    hipLaunchKernelGGL(int4_x_image_kernel, dim3((unsigned)((G + 7) / 8)), dim3(256), 0, st, x, img, unscale, (int)m,
+                       (int)k);
     DOE_LAUNCH_CHECK("int4_x_image_kernel");
     Int4Args a;
     a.q = w_u4;
@@ -237,8 +297,8 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     a.N = (int)n;
     a.K = (int)k;
     a.G = G;
-    a.gps = gps;
-    hipLaunchKernelGGL(int4_gemv_kernel, dim3((unsigned)row_blocks, (unsigned)splits), dim3(256), 0, st, a);
+    const dim3 grid((unsigned)row_blocks, (unsigned)splits);
+    hipLaunchKernelGGL(int4_gemv_kernel<8>, grid, dim3(256), 0, st, a);
     DOE_LAUNCH_CHECK("int4_gemv_kernel");
     if (splits > 1) {
         const int total = (int)(m * n);

@@ -184,3 +184,37 @@ def test_workspace_reuse_after_larger_call(dev, ora):
                        out_f16=False, batch=batch)
         want = oracle_attn(ora, q, k, v, batch=batch, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=t, scale=0.05)
         assert rel_l2(got, want) <= 1e-5, (hq, hkv, d, t, batch)
+
+
+def test_config4_batch8_long_context(dev, ora):
+    # the 27B-class long-context decode: batch 8, 64 query / 8 KV heads,
+    # head_dim 128, 32768 cached positions per sequence (1 GiB of f16 K/V),
+    # generated on the device; oracle on the first and last sequence
+    import ctypes as C
+
+    from doe_amd import _lib
+    b, hq, hkv, d, t = 8, 64, 8, 128, 32768
+    k = DeviceBuffer.empty((b, hkv, t, d), np.float16)
+    v = DeviceBuffer.empty((b, hkv, t, d), np.float16)
+    _lib.call("doe_fill_normal_f16", C.c_void_p(k.ptr), k.nbytes // 2, 41, 0.0, 1.0, C.c_void_p(None))
+    _lib.call("doe_fill_normal_f16", C.c_void_p(v.ptr), v.nbytes // 2, 42, 0.0, 1.0, C.c_void_p(None))
+    rng = np.random.default_rng(43)
+    q = rng.standard_normal((b, hq, d)).astype(np.float16)
+    out = DeviceBuffer.empty((b, hq, d), np.float16)
+    scale = 1 / math.sqrt(d)
+    ops.attention(DeviceBuffer.from_array(q), k, v, out, batch=b, num_heads=hq, num_kv_heads=hkv, head_dim=d,
+                  kv_len=t, kv_stride=t, scale=scale, q_f16=True, out_f16=True)
+    got = out.download().astype(np.float32)
+    assert np.isfinite(got).all()
+    seq_bytes = hkv * t * d * 2
+    for sb in (0, b - 1):
+        kk = np.empty((hkv, t, d), np.float16)
+        vv = np.empty((hkv, t, d), np.float16)
+        _lib.call("doe_memcpy_d2h", kk.ctypes.data_as(C.c_void_p), C.c_void_p(k.ptr + sb * seq_bytes), seq_bytes)
+        _lib.call("doe_memcpy_d2h", vv.ctypes.data_as(C.c_void_p), C.c_void_p(v.ptr + sb * seq_bytes), seq_bytes)
+        want = ora.attn_decode(q[sb].astype(np.float32), kk, vv, hq, hkv, d, t, t, scale)
+        err = rel_l2(got[sb], want)
+        print(f"[attn cfg4] seq {sb} rel_l2={err:.3e}", flush=True)
+        assert err <= ATTN_REL_L2
+    k.free()
+    v.free()
