@@ -44,9 +44,8 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load (weights are read exactly once).
-__device__ __forceinline__ uint4 load_stream16(const uint8_t *p) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
+__device__ __forceinline__ u32x4 load_stream16(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
 
 __device__ __forceinline__ uint32_t pack_half2(_Float16 lo, _Float16 hi) {
@@ -54,10 +53,22 @@ __device__ __forceinline__ uint32_t pack_half2(_Float16 lo, _Float16 hi) {
            ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+// DPP lane exchanges inside 16-lane rows (no LDS round trip): quad_perm
+// [1,0,3,2] and [2,3,0,1] exchange with lane ^ 1 and ^ 2, row_half_mirror
+// with lane 7 - i of each 8-lane half, row_mirror with lane 15 - i.  After
+// the first three, every lane of an 8-lane group holds the group's sum / max;
+// row_mirror then pairs the two groups of a row.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    return v + dpp<kDppHalfMirror>(v);
 }
 
 // Scale/min pair of sub-blocks 2*c4 and 2*c4+1 (doppler_rdrr_q4k.py:56-76),
@@ -119,15 +130,12 @@ __global__ void q4k_dequant_kernel(const uint8_t *__restrict__ w, float *__restr
 // scale exponent, and the scaled x_hi / x_lo halves in dot2 pair order.
 __device__ __forceinline__ void stage_quad(int qd, bool valid, const float *v, uint32_t *xh,
                                            uint32_t *xl, float *sx, int *sig) {
-    float s = (v[0] + v[1]) + (v[2] + v[3]);
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
+    const float s = sum8((v[0] + v[1]) + (v[2] + v[3]));
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 8, 64));
+    amax = fmaxf(amax, dpp<kDppXor1>(amax));
+    amax = fmaxf(amax, dpp<kDppXor2>(amax));
+    amax = fmaxf(amax, dpp<kDppHalfMirror>(amax));
+    amax = fmaxf(amax, dpp<kDppMirror>(amax));
     int sigma = 0;
     if (amax > 0.0f && amax <= 3.0e38f) {
         sigma = 14 - __builtin_amdgcn_frexp_expf(amax);
@@ -252,7 +260,10 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
     }
     // keep the activation loads ahead of the weight loads in issue order
     __builtin_amdgcn_sched_barrier(0);
-    uint4 hdr[R], qa[R], qb[R];
+    // (one 16-byte header load per chunk thread measured faster than one
+    // dword per thread shared across the block's lane quad by DPP, and than
+    // reading the workgroup's rows as consecutive granules through LDS)
+    u32x4 hdr[R], qa[R], qb[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r * rowslots, n - 1);
@@ -316,11 +327,11 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
     // Phase 3: dot products of this thread's chunk for its R rows.
     if (worker) {
         uint32_t xhv[32], xlv[32];
-        const uint4 *xh4 = reinterpret_cast<const uint4 *>(xh + chunk * kLdsChunkDwords);
-        const uint4 *xl4 = reinterpret_cast<const uint4 *>(xl + chunk * kLdsChunkDwords);
+        const u32x4 *xh4 = reinterpret_cast<const u32x4 *>(xh + chunk * kLdsChunkDwords);
+        const u32x4 *xl4 = reinterpret_cast<const u32x4 *>(xl + chunk * kLdsChunkDwords);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint4 a = xh4[i], b = xl4[i];
+            const u32x4 a = xh4[i], b = xl4[i];
             xhv[4 * i] = a.x; xhv[4 * i + 1] = a.y; xhv[4 * i + 2] = a.z; xhv[4 * i + 3] = a.w;
             xlv[4 * i] = b.x; xlv[4 * i + 1] = b.y; xlv[4 * i + 2] = b.z; xlv[4 * i + 3] = b.w;
         }
@@ -367,16 +378,14 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
         const int lr = idx >> 3, l8 = idx & 7;
         float s = 0.0f;
         for (int j = l8; j < nchunk; j += 8) s += red[lr * nchunk + j];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
+        s = sum8(s);
         const int row = blockIdx.x * rows_wg + lr;
         if (fz.gated) {
-            // the partner row (lr ^ 1) is the adjacent 8-lane group of this wave
-            const float other = __shfl_xor(s, 8, 64);
+            // the partner row (lr ^ 1) is the other 8-lane group of this row of 16 lanes
+            const float other = dpp<kDppMirror>(s);
             if (l8 == 0 && (lr & 1) == 0 && row < n) y[row >> 1] = gelu_tanh_clamped(s) * other;
         } else if (fz.rope_kv) {
-            const float other = __shfl_xor(s, 8, 64);
+            const float other = dpp<kDppMirror>(s);
             if (l8 == 0 && (lr & 1) == 0 && row < n) rope_kv_pair(fz, row, s, other, y);
         } else if (l8 == 0 && row < n) {
             y[row] = fz.residual ? s + fz.residual[row] : s;
