@@ -8,9 +8,11 @@
 // window is set and kv_len - 1 >= window; s = (q . k) * scale, optionally
 // softcapped tanh(s / cap) * cap; o = softmax(s) V.
 //
-// Work decomposition: grid (splits, kv heads, batch), 256 threads.  A
+// Work decomposition: grid (splits, kv heads, batch), W waves (4; or, opt-in
+// through doe_tune_set, 16 -- 8 at head_dim 256 -- as one split in one
+// kernel, without the split combine).  A
 // workgroup owns one kv head of one sequence and a contiguous range of
-// 16-position blocks; wave w takes blocks w, w+4, ...  All G = Hq/Hkv query
+// 16-position blocks; wave w takes blocks w, w+W, ...  All G = Hq/Hkv query
 // heads of the group share every K/V byte the workgroup reads.
 //   * q.K^T: v_mfma_f32_16x16x32_f16 with A = the G query rows (rows >= G are
 //     zero; an f32 query is split into f16 hi + lo rows accumulated by a second
@@ -21,7 +23,7 @@
 //   * P.V on the VALU: lane l owns dims l*D/64 .. of every head; the block's
 //     probabilities are broadcast through LDS into f32 FMAs against the f16
 //     V row.  Each wave prefetches its next block while computing this one.
-//   * the four waves combine through LDS; with more than one split, each
+//   * the W waves combine through LDS; with more than one split, each
 //     workgroup writes (m, l, o) partials to the workspace and a second,
 //     small kernel combines them (a kernel boundary orders the partials
 //     across XCDs far cheaper than per-workgroup release fences, which write
@@ -52,7 +54,25 @@ struct AttnArgs {
 };
 
 constexpr int kMaxSplits = 512;
-constexpr int kWaves = 4;
+
+// Max / sum over each 16-lane row with DPP (quad_perm ^1, ^2, row_half_mirror,
+// row_mirror): every lane of the row gets the result, no LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float max16(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    return fmaxf(v, dpp<0x140>(v));
+}
+__device__ __forceinline__ float sum16(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    return v + dpp<0x140>(v);
+}
 
 // K fragment and V rows of one 16-position block, as loaded by one lane.
 template <int D>
@@ -78,8 +98,9 @@ __device__ __forceinline__ void load_block(KVBlock<D> &blk, const uint16_t *kb, 
     }
 }
 
-template <int D, int G>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+template <int D, int G, int W>
+__global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
+    constexpr int kWaves = W, kThreads = 64 * W;
     constexpr int KSTEPS = D / 32;  // MFMA k-steps over the head dimension
     constexpr int DPL = D / 64;     // P.V dims per lane
     constexpr int G4 = (G + 3) / 4; // 4-head groups of the probability broadcast
@@ -120,7 +141,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
 
     // Query fragments (A operand) into LDS: lane l holds row l % 16 (query
     // head hq0 + l % 16 when < G), dims 32 s + 8 (l / 16) .. + 7.
-    for (int idx = tid; idx < KSTEPS * 64; idx += 256) {
+    for (int idx = tid; idx < KSTEPS * 64; idx += kThreads) {
         const int s = idx >> 6, l = idx & 63;
         const int m = l & 15;
         h8 hi, lo;
@@ -182,19 +203,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
                 s *= a.scale_log2e;
             }
             const float sc = valid ? s : -INFINITY;  // score in log2 units
-            float m = sc;
-            m = fmaxf(m, __shfl_xor(m, 1, 16));
-            m = fmaxf(m, __shfl_xor(m, 2, 16));
-            m = fmaxf(m, __shfl_xor(m, 4, 16));
-            m = fmaxf(m, __shfl_xor(m, 8, 16));
+            const float m = max16(sc);
             const float bm = fmaxf(mlane[i], m);
             mlane[i] = bm;
             const float p = valid ? exp2f(sc - bm) : 0.0f;
-            float t = p;
-            t += __shfl_xor(t, 1, 16);
-            t += __shfl_xor(t, 2, 16);
-            t += __shfl_xor(t, 4, 16);
-            t += __shfl_xor(t, 8, 16);
+            const float t = sum16(p);
             const int h = 4 * grp + i;
             if (h < G) {
                 pbw[(lane & 15) * (G4 * 4) + h] = p;
@@ -251,7 +264,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     __syncthreads();
 
     const size_t bh0 = (size_t)b * a.num_heads + hq0;
-    for (int idx = tid; idx < G * D; idx += 256) {
+    for (int idx = tid; idx < G * D; idx += kThreads) {
         const int h = idx / D, d = idx % D;
         float M = -INFINITY;
 #pragma unroll
@@ -368,23 +381,38 @@ size_t g_ws_bytes = 0;
 
 int g_num_cus = 0;
 int g_tune_splits = 0;
+int g_tune_waves = 0;
 
-template <int D>
-int launch_main(int g, dim3 grid, hipStream_t st, const AttnArgs &a) {
-    switch (g) {
-        case 1: hipLaunchKernelGGL((attn_decode_kernel<D, 1>), grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((attn_decode_kernel<D, 2>), grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((attn_decode_kernel<D, 4>), grid, dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL((attn_decode_kernel<D, 8>), grid, dim3(256), 0, st, a); break;
-        default: return doe::set_error(DOE_E_UNSUPPORTED, "query heads per kv head must be 1, 2, 4 or 8 (got %d)", g);
-    }
+// The wide (short-context) workgroup: 16 waves up to head_dim 128, 8 at 256
+// (the head-256 kernel needs more than the 128 VGPRs a 16-wave workgroup
+// leaves), keeping W * G * D <= 8192 floats of wave partials in LDS.
+constexpr int wide_waves(int D, int G) { return D > 256 ? 0 : (D == 256 ? 8 : 16) * (G * D <= 512 ? 1 : 0); }
+
+template <int D, int G>
+int launch_g(bool wide, dim3 grid, hipStream_t st, const AttnArgs &a) {
+    constexpr int WW = wide_waves(D, G);
+    if (wide && WW > 0)
+        hipLaunchKernelGGL((attn_decode_kernel<D, G, (WW > 0 ? WW : 4)>), grid, dim3(64 * WW), 0, st, a);
+    else
+        hipLaunchKernelGGL((attn_decode_kernel<D, G, 4>), grid, dim3(256), 0, st, a);
     DOE_LAUNCH_CHECK("attn_decode_kernel");
     return DOE_OK;
 }
 
 template <int D>
-int launch_d(int g, dim3 grid, hipStream_t st, const AttnArgs &a) {
-    int rc = launch_main<D>(g, grid, st, a);
+int launch_main(int g, bool w, dim3 grid, hipStream_t st, const AttnArgs &a) {
+    switch (g) {
+        case 1: return launch_g<D, 1>(w, grid, st, a);
+        case 2: return launch_g<D, 2>(w, grid, st, a);
+        case 4: return launch_g<D, 4>(w, grid, st, a);
+        case 8: return launch_g<D, 8>(w, grid, st, a);
+        default: return doe::set_error(DOE_E_UNSUPPORTED, "query heads per kv head must be 1, 2, 4 or 8 (got %d)", g);
+    }
+}
+
+template <int D>
+int launch_d(int g, bool w, dim3 grid, hipStream_t st, const AttnArgs &a) {
+    int rc = launch_main<D>(g, w, grid, st, a);
     if (rc || a.splits == 1) return rc;
     const unsigned total_heads = grid.z * (unsigned)a.num_heads;
     hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(total_heads), dim3(256), 0, st, a);
@@ -398,6 +426,10 @@ int launch_d(int g, dim3 grid, hipStream_t st, const AttnArgs &a) {
 namespace doe {
 int attn_set_splits(int v) {
     g_tune_splits = v;
+    return DOE_OK;
+}
+int attn_set_waves(int v) {
+    g_tune_waves = v;
     return DOE_OK;
 }
 }  // namespace doe
@@ -436,11 +468,19 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
         DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         g_num_cus = cus > 0 ? cus : 256;
     }
-    // Splits: about two workgroups per CU, at least four 16-position blocks each.
+    // Four waves and about two workgroups per CU, at least four 16-position
+    // blocks each; or, when tuned so, one wide workgroup per kv head.
     const int64_t len_for_split = kv_len_dev ? kv_stride : kv_len;
     const int64_t nblk = (len_for_split + 15) / 16;
+    const bool wide_ok = head_dim <= 256 && (int64_t)(num_heads / num_kv_heads) * head_dim <= 512;
+    // (the wide workgroup is opt-in: at the 2B-class decode shape, head_dim
+    // 256 over <= 384 positions, four-wave splits plus the combine measured
+    // 767 tok/s against 742 for one eight-wave split)
+    bool wide = false;
+    if (g_tune_waves > 4 && wide_ok) wide = true;
     int64_t splits = (2 * g_num_cus + batch * num_kv_heads - 1) / (batch * num_kv_heads);
     const int64_t max_splits = (nblk + 3) / 4;
+    if (wide) splits = 1;
     if (g_tune_splits > 0) splits = g_tune_splits;
     if (splits > max_splits) splits = max_splits;
     if (splits > kMaxSplits) splits = kMaxSplits;
@@ -482,12 +522,12 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
     const dim3 grid((unsigned)splits, (unsigned)num_kv_heads, (unsigned)batch);
     const hipStream_t st = (hipStream_t)stream;
     switch (head_dim) {
-        case 64: return launch_d<64>(g, grid, st, a);
-        case 128: return launch_d<128>(g, grid, st, a);
-        case 256: return launch_d<256>(g, grid, st, a);
+        case 64: return launch_d<64>(g, wide, grid, st, a);
+        case 128: return launch_d<128>(g, wide, grid, st, a);
+        case 256: return launch_d<256>(g, wide, grid, st, a);
         default:
             DOE_REQUIRE(g <= 2, DOE_E_UNSUPPORTED, "head_dim 512 supports at most 2 query heads per kv head");
-            return launch_d<512>(g, grid, st, a);
+            return launch_d<512>(g, false, grid, st, a);
     }
 }
 

@@ -23,6 +23,7 @@ int hip_fail(hipError_t e, const char *what);
 int require_init();
 // Tuning hooks of individual kernels (0 = automatic).
 int attn_set_splits(int value);
+int attn_set_waves(int value);
 
 }  // namespace doe
 

@@ -71,6 +71,11 @@ __device__ __forceinline__ float sum8(float v) {
     return v + dpp<kDppHalfMirror>(v);
 }
 
+__device__ __forceinline__ float sum16(float v) {
+    v = sum8(v);
+    return v + dpp<kDppMirror>(v);
+}
+
 // Scale/min pair of sub-blocks 2*c4 and 2*c4+1 (doppler_rdrr_q4k.py:56-76),
 // returned as two bytes each: low byte sub-block 2*c4, high byte 2*c4+1.
 __device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int c4,
@@ -274,8 +279,11 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // Fused RMSNorm (the host guarantees Q * nthreads >= nquads): scale the
-    // activation by 1 / sqrt(mean(x^2) + eps) and the norm weight.
+    // Fused RMSNorm (the host guarantees Q * nthreads >= nquads): stage
+    // x * (w or 1 + w) and multiply each row sum by 1 / sqrt(mean(x^2) + eps)
+    // at the end -- the same product, so the sum of squares is reduced in
+    // the shadow of the staging instead of behind a barrier of its own.
+    // Each wave leaves its share in wsum before the staging barrier.
     if (NORM) {
         float ss = 0.0f;
 #pragma unroll
@@ -285,23 +293,16 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
             for (int j = 0; j < 4; ++j) {
                 const float v = (e + j < k) ? xv[it][j] : 0.0f;
                 ss = fmaf(v, v, ss);
-            }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if ((tid & 63) == 0) wsum[tid >> 6] = ss;
-        __syncthreads();
-        float tot = 0.0f;
-        for (int i = 0; i < (nthreads >> 6); ++i) tot += wsum[i];
-        const float inv = 1.0f / sqrtf(tot / (float)k + fz.norm_eps);
-#pragma unroll
-        for (int it = 0; it < Q; ++it) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
                 const float nw = nwv[it][j];
-                xv[it][j] = xv[it][j] * inv * (fz.norm_offset ? 1.0f + nw : nw);
+                xv[it][j] *= fz.norm_offset ? 1.0f + nw : nw;
             }
         }
+        ss = sum16(ss);  // every lane of a 16-lane row holds its row's sum
+        const float wsum_wave = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 0)) +
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 16)) +
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 32)) +
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 48));
+        if ((tid & 63) == 0) wsum[tid >> 6] = wsum_wave;
     }
 
     // Phase 2: stage the activation once per workgroup.  The 16 quads of a
@@ -374,11 +375,18 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
     __syncthreads();
 
     // Phase 4: reduce each row's nchunk partials, eight lanes per row.
+    float inv_rms = 1.0f;
+    if (NORM) {
+        float tot = 0.0f;
+        for (int i = 0; i < (nthreads >> 6); ++i) tot += wsum[i];
+        inv_rms = 1.0f / sqrtf(tot / (float)k + fz.norm_eps);
+    }
     for (int idx = tid; idx < rows_wg * 8; idx += nthreads) {
         const int lr = idx >> 3, l8 = idx & 7;
         float s = 0.0f;
         for (int j = l8; j < nchunk; j += 8) s += red[lr * nchunk + j];
         s = sum8(s);
+        if (NORM) s *= inv_rms;
         const int row = blockIdx.x * rows_wg + lr;
         if (fz.gated) {
             // the partner row (lr ^ 1) is the other 8-lane group of this row of 16 lanes
@@ -599,6 +607,8 @@ int doe_tune_set(const char *key, int value) {
         g_tune_rows = value;
     } else if (!strcmp(key, "attn_decode.splits")) {
         return doe::attn_set_splits(value);
+    } else if (!strcmp(key, "attn_decode.waves")) {
+        return doe::attn_set_waves(value);
     } else {
         return doe::set_error(DOE_E_INVALID, "unknown tuning key '%s'", key);
     }

@@ -292,7 +292,9 @@ int doe_decode_advance(int32_t *state, int32_t *token, int32_t *ids, int64_t max
 
 /* ---- tuning ----------------------------------------------------------------
  * Overrides a kernel launch-shape choice (0 restores the automatic choice).
- * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows", "attn_decode.splits".  No
+ * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows", "attn_decode.splits",
+ * "attn_decode.waves" (4: narrow workgroups; 8 or 16: the wide short-context
+ * workgroup where the head shape allows it).  No
  * reference counterpart:
  * the reference fixes workgroup shapes per WGSL override constant
  * (lm_head_gemv.wgsl:168-169 MULTICOL_* overrides). */

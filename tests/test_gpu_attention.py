@@ -218,3 +218,26 @@ def test_config4_batch8_long_context(dev, ora):
         assert err <= ATTN_REL_L2
     k.free()
     v.free()
+
+
+@pytest.mark.parametrize("waves", [4, 16])
+@pytest.mark.parametrize("d,g", [(64, 8), (128, 4), (256, 2), (256, 1)])
+def test_wide_and_narrow_workgroups_agree_with_oracle(dev, ora, waves, d, g):
+    # short contexts run as one split on a wide workgroup (16 waves, 8 at
+    # head_dim 256); forcing the 4-wave split path must give the same answer
+    from doe_amd import _lib
+    rng = np.random.default_rng(d * 10 + g + waves)
+    hkv, t, stride, batch = 2, 333, 384, 2
+    hq = hkv * g
+    q = rng.standard_normal((batch, hq, d)).astype(np.float32)
+    k = rng.standard_normal((batch, hkv, stride, d)).astype(np.float16)
+    v = rng.standard_normal((batch, hkv, stride, d)).astype(np.float16)
+    scale = 1 / math.sqrt(d)
+    _lib.call("doe_tune_set", b"attn_decode.waves", waves)
+    try:
+        got = run_attn(q, k, v, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=scale, q_f16=False,
+                       out_f16=False, batch=batch)
+    finally:
+        _lib.call("doe_tune_set", b"attn_decode.waves", 0)
+    want = oracle_attn(ora, q, k, v, batch=batch, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=scale)
+    assert rel_l2(got, want) <= 1e-5
