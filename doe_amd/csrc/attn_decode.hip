@@ -48,6 +48,7 @@ struct AttnArgs {
     float *ws_ml;      // [B*Hq][S][2] partial (max, sum)
     int q_f16, out_f16;
     int num_heads, num_kv_heads, kv_len, kv_stride, kv_layout, splits;
+    int partials_only;  // write (m, l, o) partials even for one split; no combine
     float scale_log2e;  // scale * log2(e)
     float softcap;
     int sliding_window;
@@ -278,7 +279,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
                 O += sm.wo[w][h][d] * f;
             }
         }
-        if (a.splits == 1) {
+        if (a.splits == 1 && !a.partials_only) {
             const float r = L > 0.0f ? O / L : 0.0f;
             const size_t oi = (bh0 + h) * D + d;
             if (a.out_f16) reinterpret_cast<_Float16 *>(a.out)[oi] = (_Float16)r;
@@ -413,7 +414,7 @@ int launch_main(int g, bool w, dim3 grid, hipStream_t st, const AttnArgs &a) {
 template <int D>
 int launch_d(int g, bool w, dim3 grid, hipStream_t st, const AttnArgs &a) {
     int rc = launch_main<D>(g, w, grid, st, a);
-    if (rc || a.splits == 1) return rc;
+    if (rc || a.splits == 1 || a.partials_only) return rc;
     const unsigned total_heads = grid.z * (unsigned)a.num_heads;
     hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(total_heads), dim3(256), 0, st, a);
     DOE_LAUNCH_CHECK("attn_combine_kernel");
@@ -434,13 +435,17 @@ int attn_set_waves(int v) {
 }
 }  // namespace doe
 
-extern "C" {
+namespace {
 
-int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uint16_t *v_cache,
-                    void *out, int out_f16, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
-                    int64_t head_dim, int64_t kv_len, const int32_t *kv_len_dev, int64_t kv_stride,
-                    int kv_layout, float scale, float softcap, int64_t sliding_window,
-                    doe_stream_t stream) {
+// parts == NULL: the library workspace and (for several splits) the combine
+// kernel; parts != NULL: (o, m, l) partials into the caller's buffer
+// (o [B*Hq][S][D] then ml [B*Hq][S][2]), at most max_splits splits.
+int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const uint16_t *v_cache,
+                     void *out, int out_f16, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                     int64_t head_dim, int64_t kv_len, const int32_t *kv_len_dev, int64_t kv_stride,
+                     int kv_layout, float scale, float softcap, int64_t sliding_window,
+                     float *parts, int64_t parts_capacity, int64_t max_splits_req, int32_t *splits_out,
+                     doe_stream_t stream) {
     int rc = doe::require_init();
     if (rc) return rc;
     DOE_REQUIRE(batch >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && kv_stride >= 0,
@@ -456,7 +461,7 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
                 "kv_len %lld out of range [0, kv_stride=%lld]", (long long)kv_len, (long long)kv_stride);
     DOE_REQUIRE(sliding_window >= 0 && softcap >= 0.0f, DOE_E_INVALID, "negative window or softcap");
     if (batch == 0) return DOE_OK;
-    DOE_REQUIRE(q && k_cache && v_cache && out, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(q && k_cache && v_cache && (out || parts), DOE_E_INVALID, "null pointer");
     DOE_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0, DOE_E_INVALID,
                 "k/v caches must be 16-byte aligned");
     DOE_REQUIRE(batch * num_kv_heads <= 65535 && kv_stride <= 0x7fffffff, DOE_E_UNSUPPORTED,
@@ -483,6 +488,7 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
     if (wide) splits = 1;
     if (g_tune_splits > 0) splits = g_tune_splits;
     if (splits > max_splits) splits = max_splits;
+    if (parts && splits > max_splits_req) splits = max_splits_req;
     if (splits > kMaxSplits) splits = kMaxSplits;
     if (splits < 1) splits = 1;
 
@@ -503,7 +509,17 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
     a.scale_log2e = scale * 1.4426950408889634f;
     a.softcap = softcap;
     a.sliding_window = (int)sliding_window;
-    if (splits > 1) {
+    if (parts) {
+        const int64_t o_count = batch * num_heads * splits * head_dim;
+        const int64_t need = o_count + batch * num_heads * splits * 2;
+        DOE_REQUIRE(parts_capacity >= need, DOE_E_INVALID,
+                    "partials buffer holds %lld floats, %lld needed for %lld splits",
+                    (long long)parts_capacity, (long long)need, (long long)splits);
+        a.partials_only = 1;
+        a.ws_o = parts;
+        a.ws_ml = parts + o_count;
+        if (splits_out) *splits_out = (int32_t)splits;
+    } else if (splits > 1) {
         const size_t o_bytes = (size_t)batch * num_heads * splits * head_dim * 4;
         const size_t ml_bytes = (size_t)batch * num_heads * splits * 2 * 4;
         const size_t ml_off = (o_bytes + 255) & ~(size_t)255;
@@ -529,6 +545,33 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
             DOE_REQUIRE(g <= 2, DOE_E_UNSUPPORTED, "head_dim 512 supports at most 2 query heads per kv head");
             return launch_d<512>(g, false, grid, st, a);
     }
+}
+
+}  // namespace
+
+extern "C" {
+
+int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uint16_t *v_cache,
+                    void *out, int out_f16, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                    int64_t head_dim, int64_t kv_len, const int32_t *kv_len_dev, int64_t kv_stride,
+                    int kv_layout, float scale, float softcap, int64_t sliding_window,
+                    doe_stream_t stream) {
+    return attn_decode_impl(q, q_f16, k_cache, v_cache, out, out_f16, batch, num_heads, num_kv_heads,
+                            head_dim, kv_len, kv_len_dev, kv_stride, kv_layout, scale, softcap,
+                            sliding_window, nullptr, 0, 0, nullptr, stream);
+}
+
+int doe_attn_decode_partials(const void *q, int q_f16, const uint16_t *k_cache,
+                             const uint16_t *v_cache, int64_t batch, int64_t num_heads,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t kv_len,
+                             const int32_t *kv_len_dev, int64_t kv_stride, int kv_layout, float scale,
+                             float softcap, int64_t sliding_window, float *partials,
+                             int64_t partials_capacity, int64_t max_splits, int32_t *splits,
+                             doe_stream_t stream) {
+    DOE_REQUIRE(partials && max_splits >= 1 && splits, DOE_E_INVALID, "bad partials arguments");
+    return attn_decode_impl(q, q_f16, k_cache, v_cache, nullptr, 0, batch, num_heads, num_kv_heads,
+                            head_dim, kv_len, kv_len_dev, kv_stride, kv_layout, scale, softcap,
+                            sliding_window, partials, partials_capacity, max_splits, splits, stream);
 }
 
 }  // extern "C"

@@ -175,6 +175,12 @@ struct GemvFusion {
     // rotated by freq_cis[pos][i]; k and v rows are also stored as f16 into
     // the caches [kv_heads][max_seq][head_dim] at pos.
     int rope_kv;
+    // Activation = the combine of split-attention partials (o [heads][S][D],
+    // ml [heads][S][2] = (m, l) in log2 units): x[h D + d] =
+    // sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s.
+    const float *attn_o;
+    const float *attn_ml;
+    int attn_splits, attn_head_dim;
     const float *freq_cis;
     const int32_t *pos_dev;
     _Float16 *k_cache, *v_cache;
@@ -216,7 +222,11 @@ __device__ __forceinline__ void rope_kv_pair(const GemvFusion &fz, int row, floa
     }
 }
 
-template <int R, int Q, bool NORM>
+// PRO: activation prologue -- 0 plain f32 load, 1 fused RMSNorm, 2 combine of
+// split-attention partials (S <= kAttnMaxSplits).
+constexpr int kAttnMaxSplits = 8;
+
+template <int R, int Q, int PRO>
 __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restrict__ w,
                                                         const float *__restrict__ x,
                                                         float *__restrict__ y, int n, int k, int nb,
@@ -247,12 +257,31 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
     // Loads are unconditional (indices clamped into range, results masked
     // later) so they stay in straight-line code and the compiler can wait on
     // the activation without waiting on the weights.
+    constexpr bool NORM = PRO == 1, ATTN = PRO == 2;
     float xv[Q][4];
+    float4 ao[ATTN ? Q : 1][ATTN ? kAttnMaxSplits : 1];
+    float2 aml[ATTN ? Q : 1][ATTN ? kAttnMaxSplits : 1];
+    if (ATTN) {
+        // the partials of this thread's quads (a quad never straddles heads)
+        const int S = fz.attn_splits, D = fz.attn_head_dim;
 #pragma unroll
-    for (int it = 0; it < Q; ++it) {
-        const int e = (tid + it * nthreads) * 4;
+        for (int it = 0; it < Q; ++it) {
+            const int e = min((tid + it * nthreads) * 4, k - 4);
+            const int h = e / D, d = e - h * D;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xv[it][j] = x[min(e + j, k - 1)];  // masked when staged
+            for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+                const int ss = min(sp, S - 1);
+                ao[it][sp] = *reinterpret_cast<const float4 *>(fz.attn_o + ((size_t)h * S + ss) * D + d);
+                aml[it][sp] = *reinterpret_cast<const float2 *>(fz.attn_ml + ((size_t)h * S + ss) * 2);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int it = 0; it < Q; ++it) {
+            const int e = (tid + it * nthreads) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xv[it][j] = x[min(e + j, k - 1)];  // masked when staged
+        }
     }
     float nwv[NORM ? Q : 1][4];
     if (NORM) {
@@ -278,6 +307,36 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
         qb[r] = load_stream16(p + 32 + 32 * c4);
     }
     __builtin_amdgcn_sched_barrier(0);
+
+    if (ATTN) {
+        const int S = fz.attn_splits;
+#pragma unroll
+        for (int it = 0; it < Q; ++it) {
+            float M = -INFINITY;
+#pragma unroll
+            for (int sp = 0; sp < kAttnMaxSplits; ++sp)
+                if (sp < S) M = fmaxf(M, aml[it][sp].x);
+            float L = 0.0f, O0 = 0.0f, O1 = 0.0f, O2 = 0.0f, O3 = 0.0f;
+            if (M != -INFINITY) {
+#pragma unroll
+                for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+                    if (sp < S) {
+                        const float f = exp2f(aml[it][sp].x - M);
+                        L = fmaf(aml[it][sp].y, f, L);
+                        O0 = fmaf(ao[it][sp].x, f, O0);
+                        O1 = fmaf(ao[it][sp].y, f, O1);
+                        O2 = fmaf(ao[it][sp].z, f, O2);
+                        O3 = fmaf(ao[it][sp].w, f, O3);
+                    }
+                }
+            }
+            const float r = L > 0.0f ? 1.0f / L : 0.0f;
+            xv[it][0] = O0 * r;
+            xv[it][1] = O1 * r;
+            xv[it][2] = O2 * r;
+            xv[it][3] = O3 * r;
+        }
+    }
 
     // Fused RMSNorm (the host guarantees Q * nthreads >= nquads): stage
     // x * (w or 1 + w) and multiply each row sum by 1 / sqrt(mean(x^2) + eps)
@@ -495,7 +554,7 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         DOE_HIP_CHECK(hipMemsetAsync(output, 0, (size_t)n * sizeof(float), st));
         return DOE_OK;
     }
-    DOE_REQUIRE(weight_q4k && activation, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(weight_q4k && (activation || fz.attn_o), DOE_E_INVALID, "null pointer");
     DOE_REQUIRE(((uintptr_t)weight_q4k & 15) == 0, DOE_E_INVALID, "weight must be 16-byte aligned");
     DOE_REQUIRE(n <= 0x7fffffff && k <= 65536, DOE_E_UNSUPPORTED,
                 "q4k_gemv supports n < 2^31 and k <= 65536 (got n=%lld k=%lld)", (long long)n,
@@ -523,16 +582,19 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     const unsigned grid = (unsigned)((n + rows_wg - 1) / rows_wg);
     const int nquads = nchunk * 16;
     const int q = (nquads + s.threads - 1) / s.threads;
-    DOE_REQUIRE(!fz.norm_w || q <= 4, DOE_E_UNSUPPORTED, "fused RMSNorm needs k <= %d here",
-                4 * s.threads * 4);
+    DOE_REQUIRE((!fz.norm_w && !fz.attn_o) || q <= 4, DOE_E_UNSUPPORTED,
+                "fused RMSNorm / attention combine needs k <= %d here", 4 * s.threads * 4);
     const int qsel = q <= 1 ? 1 : (q <= 2 ? 2 : 4);
     const uint8_t *wp = (const uint8_t *)weight_q4k;
 #define DOE_GEMV_LAUNCH(RR, QQ)                                                                  \
-    if (fz.norm_w)                                                                                \
-        hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ, true>), dim3(grid), dim3(s.threads), s.lds,  \
+    if (fz.attn_o)                                                                                \
+        hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ, 2>), dim3(grid), dim3(s.threads), s.lds,     \
+                           st, wp, activation, output, (int)n, (int)k, nb, nchunk, s.rowslots, fz); \
+    else if (fz.norm_w)                                                                           \
+        hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ, 1>), dim3(grid), dim3(s.threads), s.lds,     \
                            st, wp, activation, output, (int)n, (int)k, nb, nchunk, s.rowslots, fz); \
     else                                                                                          \
-        hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ, false>), dim3(grid), dim3(s.threads), s.lds, \
+        hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ, 0>), dim3(grid), dim3(s.threads), s.lds,     \
                            st, wp, activation, output, (int)n, (int)k, nb, nchunk, s.rowslots, fz)
     switch (s.rows_per_thread * 8 + qsel) {
         case 1 * 8 + 1: DOE_GEMV_LAUNCH(1, 1); break;
@@ -597,6 +659,24 @@ int doe_q4k_gemv_qkv_rope_kv(const void *weight_q4k, const float *activation, fl
     fz.max_seq = (int)max_seq_len;
     const int64_t n = (num_heads + 2 * num_kv_heads) * head_dim;
     return gemv_launch(weight_q4k, activation, output, n, hidden, fz, (hipStream_t)stream);
+}
+
+int doe_q4k_gemv_attn_out(const void *weight_q4k, const float *attn_partials, int64_t splits,
+                          int64_t num_heads, int64_t head_dim, float *output, int64_t n,
+                          const float *residual, doe_stream_t stream) {
+    DOE_REQUIRE(attn_partials, DOE_E_INVALID, "null partials");
+    DOE_REQUIRE(splits >= 1 && splits <= kAttnMaxSplits, DOE_E_UNSUPPORTED,
+                "attention combine prologue supports 1..%d splits (got %lld)", kAttnMaxSplits,
+                (long long)splits);
+    DOE_REQUIRE(num_heads > 0 && head_dim > 0 && head_dim % 4 == 0, DOE_E_INVALID, "bad head shape");
+    DOE_REQUIRE(((uintptr_t)attn_partials & 15) == 0, DOE_E_INVALID, "partials must be 16-byte aligned");
+    GemvFusion fz{};
+    fz.attn_o = attn_partials;
+    fz.attn_ml = attn_partials + num_heads * splits * head_dim;
+    fz.attn_splits = (int)splits;
+    fz.attn_head_dim = (int)head_dim;
+    fz.residual = residual;
+    return gemv_launch(weight_q4k, nullptr, output, n, num_heads * head_dim, fz, (hipStream_t)stream);
 }
 
 int doe_tune_set(const char *key, int value) {

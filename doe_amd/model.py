@@ -10,8 +10,10 @@ an in-kernel grid barrier more), five dispatches per layer:
 
   1. qkv   = Wqkv . rmsnorm(x), RoPE on q/k, k and v stored into the f16
              caches at pos              (q/k rows interleaved rotation pairs)
-  2. attn  = attention(q, K cache, V cache, kv_len = pos + 1)
-  3. x     = Wo . attn + x                (residual epilogue)
+  2. attention(q, K cache, V cache, kv_len = pos + 1) as split partials
+  3. x     = Wo . combine(partials) + x   (the split combine folded into the
+                                           GEMV's activation load; residual
+                                           epilogue)
   4. h     = gelu(Wg . n) * (Wu . n), n = rmsnorm(x)   (gate/up rows
              interleaved, GeGLU epilogue)
   5. x     = Wd . h + x                   (residual epilogue)
@@ -113,7 +115,9 @@ class Decoder:
         self.x = DeviceBuffer.empty((c.hidden,), np.float32)
         self.xn = DeviceBuffer.empty((c.hidden,), np.float32)
         self.qkv = DeviceBuffer.empty((c.qkv_rows,), np.float32)
-        self.attn = DeviceBuffer.empty((c.q_dim,), np.float32)
+        self.max_attn_splits = 8
+        # split-attention partials: o [heads][S][D] then (m, l) [heads][S][2]
+        self.attn_parts = DeviceBuffer.empty((c.heads * self.max_attn_splits * (c.head_dim + 2),), np.float32)
         self.h = DeviceBuffer.empty((c.ffn,), np.float32)
         self.logits = DeviceBuffer.empty((c.vocab,), np.float32)
         self.token = DeviceBuffer.empty((1,), np.int32)
@@ -171,10 +175,13 @@ class Decoder:
                             head_dim=c.head_dim, freq_cis=self.freq_cis, position_buffer=self.pos_view,
                             key_cache=L.k_cache, val_cache=L.v_cache, max_seq_len=c.max_seq,
                             norm_weight=L.norm_attn, norm_eps=c.eps, norm_weight_offset=True, stream=stream)
-            ops.attention(self.q_view, L.k_cache, L.v_cache, self.attn, batch=1, num_heads=c.heads,
-                          num_kv_heads=c.kv_heads, head_dim=c.head_dim, kv_len=0, kv_stride=c.max_seq,
-                          scale=scale, kv_len_buffer=self.kvlen_view, stream=stream)
-            ops.matmul_q4k_fused(L.wo, self.attn, self.x, c.hidden, c.q_dim, residual=self.x, stream=stream)
+            splits = ops.attention_partials(self.q_view, L.k_cache, L.v_cache, self.attn_parts, batch=1,
+                                            num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim,
+                                            kv_len=0, kv_stride=c.max_seq, scale=scale,
+                                            max_splits=self.max_attn_splits, kv_len_buffer=self.kvlen_view,
+                                            stream=stream)
+            ops.matmul_q4k_attn_out(L.wo, self.attn_parts, splits, c.heads, c.head_dim, self.x, c.hidden,
+                                    residual=self.x, stream=stream)
             ops.matmul_q4k_fused(L.wgu, self.x, self.h, 2 * c.ffn, c.hidden, norm_weight=L.norm_ffn,
                                  norm_eps=c.eps, norm_weight_offset=True, gated=True, stream=stream)
             ops.matmul_q4k_fused(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)

@@ -118,6 +118,35 @@ def attention_prefill(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, output:
               head_dim, q_len, kv_len, kv_stride, start_pos, scale, int(causal), _stream_ptr(stream))
 
 
+def attention_partials(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, partials: DeviceBuffer, *,
+                       batch: int, num_heads: int, num_kv_heads: int, head_dim: int, kv_len: int, kv_stride: int,
+                       scale: float, max_splits: int = 8, q_f16: bool = False, softcap: float = 0.0,
+                       sliding_window: int = 0, kv_layout: int = 0, kv_len_buffer: DeviceBuffer | None = None,
+                       stream=None) -> int:
+    """The split half of the ``attention`` op: (o, m, l) partials into
+    ``partials`` for a consumer-side combine; returns the split count."""
+    if num_kv_heads <= 0 or num_heads % num_kv_heads:
+        raise ValueError(f"num_heads {num_heads} is not a multiple of num_kv_heads {num_kv_heads}")
+    splits = C.c_int32()
+    kvl = C.c_void_p(kv_len_buffer.ptr) if kv_len_buffer is not None else C.c_void_p(None)
+    _lib.call("doe_attn_decode_partials", _p(q), int(q_f16), _p(k_cache), _p(v_cache), batch, num_heads,
+              num_kv_heads, head_dim, kv_len, kvl, kv_stride, kv_layout, scale, softcap, sliding_window, _p(partials),
+              partials.nbytes // 4, max_splits, C.byref(splits), _stream_ptr(stream))
+    return int(splits.value)
+
+
+def matmul_q4k_attn_out(weight: DeviceBuffer, partials: DeviceBuffer, splits: int, num_heads: int, head_dim: int,
+                        output: DeviceBuffer, n: int, residual: DeviceBuffer | None = None, stream=None) -> None:
+    """``o_proj`` (+ ``attn_residual``) over the combine of attention partials."""
+    k = num_heads * head_dim
+    _q4k_weight_check(weight, n, k)
+    _need(partials, num_heads * splits * (head_dim + 2) * 4, "partials")
+    _need(output, n * 4, "output")
+    res = C.c_void_p(residual.ptr) if residual is not None else C.c_void_p(None)
+    _lib.call("doe_q4k_gemv_attn_out", _p(weight), _p(partials), splits, num_heads, head_dim, _p(output), n, res,
+              _stream_ptr(stream))
+
+
 def matmul_q4k_fused(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int, *,
                      norm_weight: DeviceBuffer | None = None, norm_eps: float = 1e-6,
                      norm_weight_offset: bool = True, residual: DeviceBuffer | None = None,

@@ -104,6 +104,16 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
 int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
                  int64_t n, int64_t k, doe_stream_t stream);
 
+/* The attention output projection of one sequence with the split-attention
+ * combine folded into its activation load: output[i] = sum_k
+ * dequant(W)[i][k] * attn[k] (+ residual[i]), attn = the combine of the
+ * partials written by doe_attn_decode_partials (batch 1, num_heads x
+ * head_dim = k, 1..8 splits).  Replaces the attention combine + o_proj +
+ * attn_residual steps of a decode step. */
+int doe_q4k_gemv_attn_out(const void *weight_q4k, const float *attn_partials, int64_t splits,
+                          int64_t num_heads, int64_t head_dim, float *output, int64_t n,
+                          const float *residual, doe_stream_t stream);
+
 /* Prefill GEMM c[m][n] = sum_k a[m][k] * dequant(b)[n][k]: a bf16 [m][k]
  * row-major, b row-wise Q4_K_M [n][k] (16-byte aligned), c f32 [m][n]
  * row-major.  Replaces the `matmul_q4k` op at M > 1 (pattern classified in
@@ -208,6 +218,23 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
                     int64_t num_kv_heads, int64_t head_dim, int64_t kv_len,
                     const int32_t *kv_len_dev, int64_t kv_stride, int kv_layout, float scale,
                     float softcap, int64_t sliding_window, doe_stream_t stream);
+
+/* The split-K half of doe_attn_decode without its combine: per query head
+ * and split, the partial output o and (m, l) -- the running max of the
+ * scores in log2 units and the sum of 2^(s - m) -- into the caller's
+ * buffer: o [batch*num_heads][S][head_dim] f32, then ml
+ * [batch*num_heads][S][2] f32 (partials_capacity floats in all).  S (at most
+ * max_splits) is returned in *splits; it depends only on the shapes (the
+ * cache length kv_stride when kv_len_dev is given), so a captured graph
+ * keeps it.  The combine is done by the consumer (doe_q4k_gemv_attn_out):
+ * out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s. */
+int doe_attn_decode_partials(const void *q, int q_f16, const uint16_t *k_cache,
+                             const uint16_t *v_cache, int64_t batch, int64_t num_heads,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t kv_len,
+                             const int32_t *kv_len_dev, int64_t kv_stride, int kv_layout,
+                             float scale, float softcap, int64_t sliding_window, float *partials,
+                             int64_t partials_capacity, int64_t max_splits, int32_t *splits,
+                             doe_stream_t stream);
 
 /* ---- normalisation, position and elementwise ops ---------------------------
  * RMSNorm per row: out = x * 1/sqrt(mean(x^2) + eps) * (w or 1 + w).

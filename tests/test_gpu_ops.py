@@ -282,3 +282,32 @@ def test_lm_head_sample_ties_and_nan(dev, ora):
     b[:] = np.float16(np.nan)
     cnt = ops.lm_head_sample(up(b), up(a), n, k, parts)
     assert _advance_token(parts, cnt)[0] == 0 == ora.argmax(np.full(n, np.nan, np.float32))
+
+
+@pytest.mark.parametrize("kv_len,max_splits", [(200, 8), (384, 8), (17, 8), (300, 1), (300, 3)])
+def test_attention_partials_and_fused_o_projection(dev, ora, kv_len, max_splits):
+    # attention split partials combined inside the Wo GEMV (+ residual), the
+    # 2B-class decode shapes: 8 q / 4 kv heads of 256, Wo 2304 x 2048
+    rng = np.random.default_rng(kv_len + max_splits)
+    hq, hkv, d, maxs, hidden = 8, 4, 256, 384, 2304
+    q = rng.standard_normal((hq, d)).astype(np.float32)
+    kc = rng.standard_normal((hkv, maxs, d)).astype(np.float16)
+    vc = rng.standard_normal((hkv, maxs, d)).astype(np.float16)
+    wo = q4k.random_q4k(rng, hidden, hq * d)
+    res = rng.standard_normal(hidden).astype(np.float32)
+    parts = DeviceBuffer.empty((hq * 8 * (d + 2),), np.float32)
+    scale = 1 / 16
+    splits = ops.attention_partials(up(q), up(kc), up(vc), parts, batch=1, num_heads=hq, num_kv_heads=hkv,
+                                    head_dim=d, kv_len=0, kv_stride=maxs, scale=scale, max_splits=max_splits,
+                                    kv_len_buffer=up(np.array([kv_len], np.int32)))
+    assert 1 <= splits <= max_splits
+    out = DeviceBuffer.empty((hidden,), np.float32)
+    ops.matmul_q4k_attn_out(up(wo), parts, splits, hq, d, out, hidden, residual=up(res))
+    attn = ora.attn_decode(q, kc, vc, hq, hkv, d, kv_len, maxs, scale).reshape(-1)
+    want = ora.residual(ora.q4k_gemv(wo, attn, hidden, hq * d), res)
+    assert rel_l2(out.download(), want) < 1e-5
+    # the same partials through the plain attention op give the same activation
+    full = DeviceBuffer.empty((1, hq, d), np.float32)
+    ops.attention(up(q), up(kc), up(vc), full, batch=1, num_heads=hq, num_kv_heads=hkv, head_dim=d,
+                  kv_len=kv_len, kv_stride=maxs, scale=scale)
+    assert rel_l2(full.download().reshape(-1), attn) < 1e-5
