@@ -112,7 +112,7 @@ def bench_gemv(args, doe):
         "kernel_ms": ms_per_step,
         "kernel_gbs": GEMV_BYTES / (ms_per_step * 1e-3) / 1e9,
         "rel_l2": rel,
-        "kernel": "q4k_gemv_kernel (doe_amd/csrc/q4k_gemv.hip)",
+        "kernel": "q4k_gemv_mfma_kernel<0> (doe_amd/csrc/q4k_gemv.hip)",
         "w": w,
         "x": x,
     }

@@ -460,9 +460,243 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
     }
 }
 
+// ---------------------------------------------------------------------------
+// GEMV on the matrix cores (k <= 16 blocks).  One workgroup owns 16 rows; wave
+// b owns Q4_K block b of those rows and is self-contained up to the final
+// cross-block row sum:
+//   * it reads the 16 rows' 144-byte block b as consecutive 16-byte granules
+//     (lane q -> row q / 9, piece q % 9) and regroups them through its own
+//     LDS slice;
+//   * it stages its own 256 activations (lane 16 g + i holds elements
+//     64 g + 4 i .. +3, i.e. chunk g of the block) into an "A image";
+//   * eight v_mfma_f32_16x16x32_f16 compute D[variant][row] with B = nibbles
+//     as f16 subnormals (q * 2^-24 low, q * 2^-20 high, exact products) and
+//     A = the 16 variants (sub-block 2g + s, x_hi or x_lo) of the staged
+//     activations.  MFMA step j feeds lane group g's nibble dword j (bytes
+//     4j..4j+3 of chunk g: elements 4j..4j+3 of sub-blocks 2g and 2g + 1);
+//     variant m = 4g + 2s + h is nonzero only for lane group g's data of
+//     sub-block 2g + s, so A is zero except in lanes m / 4 == g;
+//   * D lands with lane (g, row) holding variants 4g..4g+3: exactly the four
+//     partial sums the per-chunk scale formula (d*sc, dmin*m of sub-blocks
+//     2g, 2g + 1) needs, in the lane that also loaded that row's header and
+//     staged chunk g's activation sums.
+// The A image of step j is [chunk g][part h][type s] 16-byte slots with the
+// two non-matching halves zero ({pair0, pair1, 0, 0} for s = 0, {0, 0, pair0,
+// pair1} for s = 1), followed by a zero slot that all inactive lanes read.
+// ---------------------------------------------------------------------------
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaMaxBlocks = 16;                 // one wave per block, <= 1024 threads
+constexpr int kMfmaRowBytes = 160;                 // LDS bytes per regrouped row block (144 + 16)
+constexpr int kMfmaAStep = 68;                     // dwords per MFMA step in the A image (64 + 4 zero)
+constexpr int kMfmaWaveLds = 16 * kMfmaRowBytes + 8 * kMfmaAStep * 4;  // 4736 bytes per wave
+
+size_t gemv_mfma_lds_bytes(int nb) { return (size_t)nb * kMfmaWaveLds + (size_t)17 * nb * 4; }
+
+// Sum over the four 16-lane rows of a wave (lanes i, i + 16, i + 32, i + 48)
+// with the gfx950 cross-row swaps; every lane ends with its column's total.
+__device__ __forceinline__ float sum_rows4(float v) {
+    auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+    auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+}
+
+template <int PRO>
+__global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__restrict__ w,
+                                                             const float *__restrict__ x,
+                                                             float *__restrict__ y, int n, int k,
+                                                             int nb, int x_vec4, GemvFusion fz) {
+    constexpr bool NORM = PRO == 1, ATTN = PRO == 2;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, b = tid >> 6;
+    uint8_t *wimg = lds + b * kMfmaWaveLds;
+    uint32_t *aimg = reinterpret_cast<uint32_t *>(wimg + 16 * kMfmaRowBytes);
+    float *red = reinterpret_cast<float *>(lds + nb * kMfmaWaveLds);  // [16][nb] row partials
+    float *ssq = red + 16 * nb;                                       // [nb] sums of squares
+    const int row0 = blockIdx.x * 16;
+    const int e = b * 256 + lane * 4;  // this lane's four activations
+
+    // Activation operands first (vector-memory returns are in order, so the
+    // staging below never waits on the weight stream).
+    float v[4], nwv[4];
+    float4 ao[ATTN ? kAttnMaxSplits : 1];
+    float2 aml[ATTN ? kAttnMaxSplits : 1];
+    if (ATTN) {
+        // a lane's four elements lie in one head (head_dim % 4 == 0)
+        const int S = fz.attn_splits, D = fz.attn_head_dim;
+        const int ec = min(e, k - 4), h = ec / D, d = ec - h * D;
+#pragma unroll
+        for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+            const int ss = min(sp, S - 1);
+            ao[sp] = *reinterpret_cast<const float4 *>(fz.attn_o + ((size_t)h * S + ss) * D + d);
+            aml[sp] = *reinterpret_cast<const float2 *>(fz.attn_ml + ((size_t)h * S + ss) * 2);
+        }
+    } else if (x_vec4 && e + 3 < k) {
+        const float4 f = *reinterpret_cast<const float4 *>(x + e);
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = x[min(e + j, k - 1)];  // masked below
+    }
+    if (NORM) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) nwv[j] = fz.norm_w[min(e + j, k - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Block b of the 16 rows: granule q -> row q / 9, piece q % 9.
+    const size_t rowbytes = (size_t)nb * DOE_Q4K_BLOCK_BYTES;
+    u32x4 wv[3];
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+        const int q = min(lane + 64 * s, 143);
+        const int r = min(row0 + q / 9, n - 1);
+        wv[s] = load_stream16(w + (size_t)r * rowbytes + b * DOE_Q4K_BLOCK_BYTES + (q % 9) * 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (ATTN) {
+        const int S = fz.attn_splits;
+        float M = -INFINITY;
+#pragma unroll
+        for (int sp = 0; sp < kAttnMaxSplits; ++sp)
+            if (sp < S) M = fmaxf(M, aml[sp].x);
+        float L = 0.0f, O0 = 0.0f, O1 = 0.0f, O2 = 0.0f, O3 = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+                if (sp < S) {
+                    const float f = exp2f(aml[sp].x - M);
+                    L = fmaf(aml[sp].y, f, L);
+                    O0 = fmaf(ao[sp].x, f, O0);
+                    O1 = fmaf(ao[sp].y, f, O1);
+                    O2 = fmaf(ao[sp].z, f, O2);
+                    O3 = fmaf(ao[sp].w, f, O3);
+                }
+            }
+        }
+        const float rl = L > 0.0f ? 1.0f / L : 0.0f;
+        v[0] = O0 * rl; v[1] = O1 * rl; v[2] = O2 * rl; v[3] = O3 * rl;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (e + j >= k) v[j] = 0.0f;
+    if (NORM) {
+        // RMSNorm: stage x * (w or 1 + w); the row sums are multiplied by
+        // 1 / sqrt(mean(x^2) + eps) at the end (the same product).
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ss = fmaf(v[j], v[j], ss);
+            v[j] *= fz.norm_offset ? 1.0f + nwv[j] : nwv[j];
+        }
+        ss = sum_rows4(sum16(ss));
+        if (lane == 0) ssq[b] = ss;
+    }
+
+    // Stage this wave's activation image.  Lane 16 g + i: chunk g, quad i;
+    // the 16 lanes of a chunk form one DPP row, the 8 of a sub-block a half.
+    const int g = lane >> 4, i16 = lane & 15;
+    const float ssum = sum8((v[0] + v[1]) + (v[2] + v[3]));
+    const float sother = dpp<kDppMirror>(ssum);  // the other sub-block of the chunk
+    const float sx_lo = i16 < 8 ? ssum : sother, sx_hi = i16 < 8 ? sother : ssum;
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, dpp<kDppXor1>(amax));
+    amax = fmaxf(amax, dpp<kDppXor2>(amax));
+    amax = fmaxf(amax, dpp<kDppHalfMirror>(amax));
+    amax = fmaxf(amax, dpp<kDppMirror>(amax));
+    int sigma = 0;
+    if (amax > 0.0f && amax <= 3.0e38f) {
+        sigma = 14 - __builtin_amdgcn_frexp_expf(amax);
+        sigma = sigma < -100 ? -100 : (sigma > 100 ? 100 : sigma);
+    }
+    {
+        const float xs = __builtin_amdgcn_ldexpf(1.0f, sigma);
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float t = v[j] * xs;
+            hi[j] = (_Float16)t;
+            lo[j] = (_Float16)(t - (float)hi[j]);
+        }
+        const int s = i16 >> 3, jj = i16 & 7;
+        const uint32_t h0 = pack_half2(hi[0], hi[2]), h1 = pack_half2(hi[1], hi[3]);
+        const uint32_t l0 = pack_half2(lo[0], lo[2]), l1 = pack_half2(lo[1], lo[3]);
+        uint32_t *dst = aimg + jj * kMfmaAStep + g * 16 + s * 4;
+        *reinterpret_cast<u32x4 *>(dst) = s ? u32x4{0, 0, h0, h1} : u32x4{h0, h1, 0, 0};
+        *reinterpret_cast<u32x4 *>(dst + 8) = s ? u32x4{0, 0, l0, l1} : u32x4{l0, l1, 0, 0};
+        if (lane < 8) *reinterpret_cast<u32x4 *>(aimg + lane * kMfmaAStep + 64) = u32x4{0, 0, 0, 0};
+    }
+    // LDS operations of one wave complete in order; the wave barrier keeps
+    // the compiler from moving the reads above the writes.
+    __builtin_amdgcn_wave_barrier();
+    const int nchunk = (k + 63) >> 6, c = 4 * b + g, m = lane & 15;
+    const bool act = (m >> 2) == g && c < nchunk;
+    const int abase = act ? g * 16 + (m & 1) * 8 + ((m >> 1) & 1) * 4 : 64;
+    u32x4 areg[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) areg[j] = *reinterpret_cast<const u32x4 *>(aimg + j * kMfmaAStep + abase);
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+        const int q = lane + 64 * s;
+        if (q < 144) *reinterpret_cast<u32x4 *>(wimg + (q / 9) * kMfmaRowBytes + (q % 9) * 16) = wv[s];
+    }
+    __builtin_amdgcn_wave_barrier();
+    const uint8_t *rp = wimg + i16 * kMfmaRowBytes;  // lane (g, row i16)
+    const u32x4 hdr = *reinterpret_cast<const u32x4 *>(rp);
+    const u32x4 qa = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
+    const u32x4 qb = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
+    f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t dw = j < 4 ? qa[j] : qb[j - 4], ew = dw >> 8;
+        const u32x4 bw = {dw & 0x000f000fu, ew & 0x000f000fu, dw & 0x00f000f0u, ew & 0x00f000f0u};
+        acc[j & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, areg[j]),
+                                                            __builtin_bit_cast(half8, bw), acc[j & 1],
+                                                            0, 0, 0);
+    }
+    const f32x4 dsum = acc[0] + acc[1];
+    float part = 0.0f;
+    if (c < nchunk) {
+        uint32_t scp, mnp;
+        q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
+        const float d = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
+        const float qx_lo = (dsum[0] + dsum[1]) * __builtin_amdgcn_ldexpf(1.0f, 24 - sigma);
+        const float qx_hi = (dsum[2] + dsum[3]) * __builtin_amdgcn_ldexpf(1.0f, 20 - sigma);
+        const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
+        const float m_lo = (float)(mnp & 0xffu), m_hi = (float)(mnp >> 8);
+        part = d * (sc_lo * qx_lo + sc_hi * qx_hi) - dmin * (m_lo * sx_lo + m_hi * sx_hi);
+    }
+    part = sum_rows4(part);  // the row's four chunks of block b
+    if (lane < 16) red[lane * nb + b] = part;
+    __syncthreads();
+
+    if (tid < 16) {
+        float s = 0.0f;
+        for (int j = 0; j < nb; ++j) s += red[tid * nb + j];
+        if (NORM) {
+            float tot = 0.0f;
+            for (int j = 0; j < nb; ++j) tot += ssq[j];
+            s *= 1.0f / sqrtf(tot / (float)k + fz.norm_eps);
+        }
+        const int row = row0 + tid;
+        if (fz.gated) {
+            const float other = dpp<kDppXor1>(s);  // row ^ 1
+            if ((tid & 1) == 0 && row < n) y[row >> 1] = gelu_tanh_clamped(s) * other;
+        } else if (fz.rope_kv) {
+            const float other = dpp<kDppXor1>(s);
+            if ((tid & 1) == 0 && row < n) rope_kv_pair(fz, row, s, other, y);
+        } else if (row < n) {
+            y[row] = fz.residual ? s + fz.residual[row] : s;
+        }
+    }
+}
+
 // Tunable launch-shape overrides (0 = automatic), set via doe_tune_set.
 int g_tune_rowslots = 0;
 int g_tune_rows = 0;
+int g_tune_kernel = 0;  // 0 automatic, 1 dot-product kernel, 2 matrix-core kernel
 
 // Launch shape for the GEMV: rowslots * nchunk threads (rounded up to whole
 // waves) and R rows per thread.  The automatic choice spreads the rows over
@@ -561,6 +795,30 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
                 (long long)k);
     const int nb = (int)((k + 255) / 256);
     const int nchunk = (int)((k + 63) / 64);
+    const uint8_t *wp = (const uint8_t *)weight_q4k;
+    if (nb <= kMfmaMaxBlocks && g_tune_kernel != 1) {
+        const size_t lds = gemv_mfma_lds_bytes(nb);
+        const unsigned grid = (unsigned)((n + 15) / 16);
+        const int x_vec4 = activation && ((uintptr_t)activation & 15) == 0;
+#define DOE_GEMV_MFMA_LAUNCH(P)                                                                   \
+    do {                                                                                          \
+        static bool attr_set = false;                                                             \
+        if (!attr_set) {                                                                          \
+            DOE_HIP_CHECK(hipFuncSetAttribute((const void *)q4k_gemv_mfma_kernel<P>,              \
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,         \
+                                              (int)gemv_mfma_lds_bytes(kMfmaMaxBlocks)));         \
+            attr_set = true;                                                                      \
+        }                                                                                         \
+        hipLaunchKernelGGL((q4k_gemv_mfma_kernel<P>), dim3(grid), dim3(64 * nb), lds, st, wp,     \
+                           activation, output, (int)n, (int)k, nb, x_vec4, fz);                   \
+    } while (0)
+        if (fz.attn_o) DOE_GEMV_MFMA_LAUNCH(2);
+        else if (fz.norm_w) DOE_GEMV_MFMA_LAUNCH(1);
+        else DOE_GEMV_MFMA_LAUNCH(0);
+#undef DOE_GEMV_MFMA_LAUNCH
+        DOE_LAUNCH_CHECK("q4k_gemv_mfma_kernel");
+        return DOE_OK;
+    }
     if (g_num_cus == 0) {
         int dev = 0, cus = 0;
         DOE_HIP_CHECK(hipGetDevice(&dev));
@@ -585,7 +843,6 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     DOE_REQUIRE((!fz.norm_w && !fz.attn_o) || q <= 4, DOE_E_UNSUPPORTED,
                 "fused RMSNorm / attention combine needs k <= %d here", 4 * s.threads * 4);
     const int qsel = q <= 1 ? 1 : (q <= 2 ? 2 : 4);
-    const uint8_t *wp = (const uint8_t *)weight_q4k;
 #define DOE_GEMV_LAUNCH(RR, QQ)                                                                  \
     if (fz.attn_o)                                                                                \
         hipLaunchKernelGGL((q4k_gemv_kernel<RR, QQ, 2>), dim3(grid), dim3(s.threads), s.lds,     \
@@ -685,6 +942,9 @@ int doe_tune_set(const char *key, int value) {
         g_tune_rowslots = value;
     } else if (!strcmp(key, "q4k_gemv.rows")) {
         g_tune_rows = value;
+    } else if (!strcmp(key, "q4k_gemv.kernel")) {
+        DOE_REQUIRE(value >= 0 && value <= 2, DOE_E_INVALID, "q4k_gemv.kernel is 0, 1 or 2");
+        g_tune_kernel = value;
     } else if (!strcmp(key, "attn_decode.splits")) {
         return doe::attn_set_splits(value);
     } else if (!strcmp(key, "attn_decode.waves")) {

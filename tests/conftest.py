@@ -37,3 +37,14 @@ def dev():
     info = doe_amd.device_info()
     print(f"[dev] {info}", flush=True)
     return doe_amd
+
+
+@pytest.fixture(params=[1, 2], ids=["dot_kernel", "mfma_kernel"])
+def gemv_kernel(request, dev):
+    """Forces one Q4_K GEMV kernel for k <= 4096 (1: per-chunk dot products,
+    2: matrix cores; larger k always uses the dot-product kernel) and restores
+    the automatic choice afterwards."""
+    from doe_amd import ops
+    ops.tune("q4k_gemv.kernel", request.param)
+    yield request.param
+    ops.tune("q4k_gemv.kernel", 0)

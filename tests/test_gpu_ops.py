@@ -147,7 +147,7 @@ def test_f16_gemv_full_vocab_shape(dev):
     assert rel_l2(got[rows], want) < 1e-5
 
 
-def test_fused_gemv_norm_residual_gated(dev, ora):
+def test_fused_gemv_norm_residual_gated(dev, ora, gemv_kernel):
     rng = np.random.default_rng(8)
     k = 2304
     x = (rng.standard_normal(k) * 5).astype(np.float32)
@@ -179,7 +179,7 @@ def test_fused_gemv_norm_residual_gated(dev, ora):
 
 
 @pytest.mark.parametrize("pos", [0, 17, 63, 64])
-def test_qkv_rope_kv(dev, ora, pos):
+def test_qkv_rope_kv(dev, ora, pos, gemv_kernel):
     # the fused input_norm + q/k/v_proj + rope + cache write, 2B-class head
     # shape (8 q / 4 kv heads of 256 over hidden 2304); pos 64 is outside the
     # 64-position cache: unrotated q/k and no cache write
@@ -285,7 +285,7 @@ def test_lm_head_sample_ties_and_nan(dev, ora):
 
 
 @pytest.mark.parametrize("kv_len,max_splits", [(200, 8), (384, 8), (17, 8), (300, 1), (300, 3)])
-def test_attention_partials_and_fused_o_projection(dev, ora, kv_len, max_splits):
+def test_attention_partials_and_fused_o_projection(dev, ora, kv_len, max_splits, gemv_kernel):
     # attention split partials combined inside the Wo GEMV (+ residual), the
     # 2B-class decode shapes: 8 q / 4 kv heads of 256, Wo 2304 x 2048
     rng = np.random.default_rng(kv_len + max_splits)

@@ -68,7 +68,7 @@ GEMV_SHAPES = [(9216, 2304), (2048, 2304), (1024, 2304), (2304, 2048), (2304, 92
 
 
 @pytest.mark.parametrize("n,k", GEMV_SHAPES)
-def test_gemv_matches_oracle(dev, ora, n, k):
+def test_gemv_matches_oracle(dev, ora, n, k, gemv_kernel):
     rng = np.random.default_rng(n * 7 + k)
     w = q4k.random_q4k(rng, n, k)
     x = rng.standard_normal(k).astype(np.float32)
@@ -81,7 +81,7 @@ def test_gemv_matches_oracle(dev, ora, n, k):
     assert err < 1e-5
 
 
-def test_gemv_reference_block_one_hot(dev, known_answers):
+def test_gemv_reference_block_one_hot(dev, known_answers, gemv_kernel):
     # The reference's known-answer block (test_doppler_rdrr_q4k.py:63-85)
     # through the GEMV: a one-hot activation picks out one dequantized value.
     e = known_answers["q4k_scale_min_block"]
@@ -94,7 +94,7 @@ def test_gemv_reference_block_one_hot(dev, known_answers):
 
 
 @pytest.mark.parametrize("scale", [1e-30, 1e-8, 1e6, 1e30])
-def test_gemv_activation_range(dev, ora, scale):
+def test_gemv_activation_range(dev, ora, scale, gemv_kernel):
     rng = np.random.default_rng(7)
     n, k = 256, 2304
     w = q4k.random_q4k(rng, n, k)
@@ -102,7 +102,7 @@ def test_gemv_activation_range(dev, ora, scale):
     assert rel_l2(_gemv(w, x, n, k), ora.q4k_gemv(w, x, n, k)) < 1e-5
 
 
-def test_gemv_extreme_scales(dev, ora):
+def test_gemv_extreme_scales(dev, ora, gemv_kernel):
     rng = np.random.default_rng(8)
     n, k = 128, 1024
     w = _extreme_q4k(rng, n, k)
@@ -117,7 +117,7 @@ def test_gemv_zero_k_and_zero_n(dev):
     ops.matmul_q4k(DeviceBuffer(0), DeviceBuffer(16), DeviceBuffer(0), 0, 4)
 
 
-def test_gemv_stream_and_graph_replays(dev, ora):
+def test_gemv_stream_and_graph_replays(dev, ora, gemv_kernel):
     rng = np.random.default_rng(9)
     n, k = 2048, 2304
     w = q4k.random_q4k(rng, n, k)
@@ -150,3 +150,21 @@ def test_gemv_rejects_misaligned_weight(dev):
         _lib.call("doe_q4k_gemv", C.c_void_p(dw.ptr), C.c_void_p(dx.ptr), C.c_void_p(dy.ptr), 2, 70000,
                   C.c_void_p(None))
     assert ei.value.status == -4
+
+
+def test_gemv_unaligned_activation(dev, ora, gemv_kernel):
+    # an activation pointer that is 4-byte but not 16-byte aligned takes the
+    # per-element load path
+    import ctypes as C
+
+    from doe_amd import _lib
+    rng = np.random.default_rng(21)
+    n, k = 100, 2304
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    dx = DeviceBuffer.from_array(np.concatenate([np.zeros(1, np.float32), x]))
+    dw = DeviceBuffer.from_array(w)
+    dy = DeviceBuffer.empty((n,), np.float32)
+    _lib.call("doe_q4k_gemv", C.c_void_p(dw.ptr), C.c_void_p(dx.ptr + 4), C.c_void_p(dy.ptr), n, k,
+              C.c_void_p(None))
+    assert rel_l2(dy.download(), ora.q4k_gemv(w, x, n, k)) < 1e-5
