@@ -487,12 +487,18 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMfmaMaxBlocks = 16;                 // one wave per block, <= 1024 threads
+constexpr int kMfmaMaxBlocks = 64;                 // <= 16 waves of <= 4 blocks each
 constexpr int kMfmaRowBytes = 160;                 // LDS bytes per regrouped row block (144 + 16)
 constexpr int kMfmaAStep = 68;                     // dwords per MFMA step in the A image (64 + 4 zero)
-constexpr int kMfmaWaveLds = 16 * kMfmaRowBytes + 8 * kMfmaAStep * 4;  // 4736 bytes per wave
+constexpr int kMfmaAImgDwords = 8 * kMfmaAStep;    // one block's activation image (2176 bytes)
 
-size_t gemv_mfma_lds_bytes(int nb) { return (size_t)nb * kMfmaWaveLds + (size_t)17 * nb * 4; }
+// Activation images per wave: up to three blocks' images are staged ahead.
+constexpr int mfma_images(int bpw) { return bpw < 3 ? bpw : 3; }
+constexpr int mfma_wave_lds(int bpw) { return 16 * kMfmaRowBytes + mfma_images(bpw) * kMfmaAImgDwords * 4; }
+
+size_t gemv_mfma_lds_bytes(int nwaves, int bpw) {
+    return (size_t)nwaves * mfma_wave_lds(bpw) + (size_t)17 * nwaves * 4;
+}
 
 // Sum over the four 16-lane rows of a wave (lanes i, i + 16, i + 32, i + 48)
 // with the gfx950 cross-row swaps; every lane ends with its column's total.
@@ -503,56 +509,75 @@ __device__ __forceinline__ float sum_rows4(float v) {
     return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
 }
 
-template <int PRO>
+// BPW consecutive blocks per wave (BPW = ceil(nb / 16), so a workgroup of at
+// most 16 waves covers the row): the weight loads of all of the wave's blocks
+// are issued up front in block order and the blocks are then processed one
+// after another through the same LDS slice, so the first block's MFMAs run
+// while the later blocks' bytes arrive.
+// XV: the activation is read as one float4 per lane (x 16-byte aligned and
+// k % 4 == 0), else as four clamped dwords.  Both forms are branch-free so the
+// activation loads stay ahead of the weight stream.
+template <int PRO, int BPW, int XV>
 __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__restrict__ w,
-                                                             const float *__restrict__ x,
+                                                             const float *x,
                                                              float *__restrict__ y, int n, int k,
-                                                             int nb, int x_vec4, GemvFusion fz) {
+                                                             int nb, GemvFusion fz) {
     constexpr bool NORM = PRO == 1, ATTN = PRO == 2;
+    constexpr int NA = mfma_images(BPW), WAVE_LDS = mfma_wave_lds(BPW);
+    static_assert(!ATTN || BPW == 1, "the attention-combine prologue is single-block");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63, b = tid >> 6;
-    uint8_t *wimg = lds + b * kMfmaWaveLds;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    uint8_t *wimg = lds + wave * WAVE_LDS;
     uint32_t *aimg = reinterpret_cast<uint32_t *>(wimg + 16 * kMfmaRowBytes);
-    float *red = reinterpret_cast<float *>(lds + nb * kMfmaWaveLds);  // [16][nb] row partials
-    float *ssq = red + 16 * nb;                                       // [nb] sums of squares
-    const int row0 = blockIdx.x * 16;
-    const int e = b * 256 + lane * 4;  // this lane's four activations
+    float *red = reinterpret_cast<float *>(lds + nwaves * WAVE_LDS);  // [16][nwaves] row partials
+    float *ssq = red + 16 * nwaves;                                       // [nwaves] sums of squares
+    const int row0 = blockIdx.x * 16, b0 = wave * BPW;
 
     // Activation operands first (vector-memory returns are in order, so the
     // staging below never waits on the weight stream).
-    float v[4], nwv[4];
+    float v[BPW][4], nwv[NORM ? BPW : 1][4];
     float4 ao[ATTN ? kAttnMaxSplits : 1];
     float2 aml[ATTN ? kAttnMaxSplits : 1];
-    if (ATTN) {
-        // a lane's four elements lie in one head (head_dim % 4 == 0)
-        const int S = fz.attn_splits, D = fz.attn_head_dim;
-        const int ec = min(e, k - 4), h = ec / D, d = ec - h * D;
 #pragma unroll
-        for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
-            const int ss = min(sp, S - 1);
-            ao[sp] = *reinterpret_cast<const float4 *>(fz.attn_o + ((size_t)h * S + ss) * D + d);
-            aml[sp] = *reinterpret_cast<const float2 *>(fz.attn_ml + ((size_t)h * S + ss) * 2);
+    for (int u = 0; u < BPW; ++u) {
+        const int e = (b0 + u) * 256 + lane * 4;  // this lane's four activations of block b0 + u
+        if (ATTN) {
+            // a lane's four elements lie in one head (head_dim % 4 == 0)
+            const int S = fz.attn_splits, D = fz.attn_head_dim;
+            const int ec = min(e, k - 4), h = ec / D, d = ec - h * D;
+#pragma unroll
+            for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+                const int ss = min(sp, S - 1);
+                ao[sp] = *reinterpret_cast<const float4 *>(fz.attn_o + ((size_t)h * S + ss) * D + d);
+                aml[sp] = *reinterpret_cast<const float2 *>(fz.attn_ml + ((size_t)h * S + ss) * 2);
+            }
+        } else if (XV) {
+            const float4 f = *reinterpret_cast<const float4 *>(x + min(e, k - 4));  // masked below
+            v[u][0] = f.x; v[u][1] = f.y; v[u][2] = f.z; v[u][3] = f.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[u][j] = x[min(e + j, k - 1)];  // masked below
         }
-    } else if (x_vec4 && e + 3 < k) {
-        const float4 f = *reinterpret_cast<const float4 *>(x + e);
-        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-    } else {
+        if (NORM) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = x[min(e + j, k - 1)];  // masked below
+            for (int j = 0; j < 4; ++j) nwv[NORM ? u : 0][j] = fz.norm_w[min(e + j, k - 1)];
+        }
     }
-    if (NORM) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) nwv[j] = fz.norm_w[min(e + j, k - 1)];
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    // (x is not __restrict__: with it its loads count as invariant and were
+    // sunk past the weight loads; this memory clobber keeps the order)
+    __asm__ volatile("" ::: "memory");
     // Block b of the 16 rows: granule q -> row q / 9, piece q % 9.
     const size_t rowbytes = (size_t)nb * DOE_Q4K_BLOCK_BYTES;
-    u32x4 wv[3];
+    u32x4 wv[BPW][3];
 #pragma unroll
-    for (int s = 0; s < 3; ++s) {
-        const int q = min(lane + 64 * s, 143);
-        const int r = min(row0 + q / 9, n - 1);
-        wv[s] = load_stream16(w + (size_t)r * rowbytes + b * DOE_Q4K_BLOCK_BYTES + (q % 9) * 16);
+    for (int u = 0; u < BPW; ++u) {
+        const int blk = min(b0 + u, nb - 1);  // past the row end: a valid block, unused
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            const int q = min(lane + 64 * s, 143);
+            const int r = min(row0 + q / 9, n - 1);
+            wv[u][s] = load_stream16(w + (size_t)r * rowbytes + blk * DOE_Q4K_BLOCK_BYTES + (q % 9) * 16);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -577,107 +602,139 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
             }
         }
         const float rl = L > 0.0f ? 1.0f / L : 0.0f;
-        v[0] = O0 * rl; v[1] = O1 * rl; v[2] = O2 * rl; v[3] = O3 * rl;
+        v[0][0] = O0 * rl; v[0][1] = O1 * rl; v[0][2] = O2 * rl; v[0][3] = O3 * rl;
     }
+    float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        if (e + j >= k) v[j] = 0.0f;
-    if (NORM) {
-        // RMSNorm: stage x * (w or 1 + w); the row sums are multiplied by
-        // 1 / sqrt(mean(x^2) + eps) at the end (the same product).
-        float ss = 0.0f;
+    for (int u = 0; u < BPW; ++u) {
+        const int e = (b0 + u) * 256 + lane * 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            ss = fmaf(v[j], v[j], ss);
-            v[j] *= fz.norm_offset ? 1.0f + nwv[j] : nwv[j];
+            if (e + j >= k) v[u][j] = 0.0f;
+            if (NORM) {
+                // RMSNorm: stage x * (w or 1 + w); the row sums are multiplied
+                // by 1 / sqrt(mean(x^2) + eps) at the end (the same product).
+                ss = fmaf(v[u][j], v[u][j], ss);
+                const float nw = nwv[NORM ? u : 0][j];
+                v[u][j] *= fz.norm_offset ? 1.0f + nw : nw;
+            }
         }
+    }
+    if (NORM) {
         ss = sum_rows4(sum16(ss));
-        if (lane == 0) ssq[b] = ss;
+        if (lane == 0) ssq[wave] = ss;
     }
 
-    // Stage this wave's activation image.  Lane 16 g + i: chunk g, quad i;
-    // the 16 lanes of a chunk form one DPP row, the 8 of a sub-block a half.
-    const int g = lane >> 4, i16 = lane & 15;
-    const float ssum = sum8((v[0] + v[1]) + (v[2] + v[3]));
-    const float sother = dpp<kDppMirror>(ssum);  // the other sub-block of the chunk
-    const float sx_lo = i16 < 8 ? ssum : sother, sx_hi = i16 < 8 ? sother : ssum;
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, dpp<kDppXor1>(amax));
-    amax = fmaxf(amax, dpp<kDppXor2>(amax));
-    amax = fmaxf(amax, dpp<kDppHalfMirror>(amax));
-    amax = fmaxf(amax, dpp<kDppMirror>(amax));
-    int sigma = 0;
-    if (amax > 0.0f && amax <= 3.0e38f) {
-        sigma = 14 - __builtin_amdgcn_frexp_expf(amax);
-        sigma = sigma < -100 ? -100 : (sigma > 100 ? 100 : sigma);
-    }
-    {
+    const int g = lane >> 4, i16 = lane & 15, m = lane & 15;
+    const int nchunk = (k + 63) >> 6;
+    // Stage block b0 + u's activation image into image slot u % NA: lane
+    // 16 g + i holds chunk g, quad i (a chunk is one DPP row, a sub-block a
+    // half); returns the chunk's scale exponent and sub-block sums.
+    float sxl[BPW], sxh[BPW];
+    int sgm[BPW];
+    auto stage = [&](int u) __attribute__((always_inline)) {
+        uint32_t *img = aimg + (u % NA) * kMfmaAImgDwords;
+        const float ssum = sum8((v[u][0] + v[u][1]) + (v[u][2] + v[u][3]));
+        const float sother = dpp<kDppMirror>(ssum);  // the other sub-block of the chunk
+        sxl[u] = i16 < 8 ? ssum : sother;
+        sxh[u] = i16 < 8 ? sother : ssum;
+        float amax = fmaxf(fmaxf(fabsf(v[u][0]), fabsf(v[u][1])), fmaxf(fabsf(v[u][2]), fabsf(v[u][3])));
+        amax = fmaxf(amax, dpp<kDppXor1>(amax));
+        amax = fmaxf(amax, dpp<kDppXor2>(amax));
+        amax = fmaxf(amax, dpp<kDppHalfMirror>(amax));
+        amax = fmaxf(amax, dpp<kDppMirror>(amax));
+        int sigma = 0;
+        if (amax > 0.0f && amax <= 3.0e38f) {
+            sigma = 14 - __builtin_amdgcn_frexp_expf(amax);
+            sigma = sigma < -100 ? -100 : (sigma > 100 ? 100 : sigma);
+        }
+        sgm[u] = sigma;
         const float xs = __builtin_amdgcn_ldexpf(1.0f, sigma);
         _Float16 hi[4], lo[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float t = v[j] * xs;
+            const float t = v[u][j] * xs;
             hi[j] = (_Float16)t;
             lo[j] = (_Float16)(t - (float)hi[j]);
         }
         const int s = i16 >> 3, jj = i16 & 7;
         const uint32_t h0 = pack_half2(hi[0], hi[2]), h1 = pack_half2(hi[1], hi[3]);
         const uint32_t l0 = pack_half2(lo[0], lo[2]), l1 = pack_half2(lo[1], lo[3]);
-        uint32_t *dst = aimg + jj * kMfmaAStep + g * 16 + s * 4;
+        uint32_t *dst = img + jj * kMfmaAStep + g * 16 + s * 4;
         *reinterpret_cast<u32x4 *>(dst) = s ? u32x4{0, 0, h0, h1} : u32x4{h0, h1, 0, 0};
         *reinterpret_cast<u32x4 *>(dst + 8) = s ? u32x4{0, 0, l0, l1} : u32x4{l0, l1, 0, 0};
-        if (lane < 8) *reinterpret_cast<u32x4 *>(aimg + lane * kMfmaAStep + 64) = u32x4{0, 0, 0, 0};
-    }
-    // LDS operations of one wave complete in order; the wave barrier keeps
-    // the compiler from moving the reads above the writes.
+        if (u < NA && lane < 8) *reinterpret_cast<u32x4 *>(img + lane * kMfmaAStep + 64) = u32x4{0, 0, 0, 0};
+    };
+    // The first NA blocks' images are staged while the weights are in flight.
+#pragma unroll
+    for (int u = 0; u < NA; ++u)
+        if (b0 + u < nb) stage(u);
+    // LDS operations of one wave complete in order (an image is read before a
+    // later block overwrites it); the wave barriers keep the compiler from
+    // moving reads above writes.
     __builtin_amdgcn_wave_barrier();
-    const int nchunk = (k + 63) >> 6, c = 4 * b + g, m = lane & 15;
-    const bool act = (m >> 2) == g && c < nchunk;
-    const int abase = act ? g * 16 + (m & 1) * 8 + ((m >> 1) & 1) * 4 : 64;
-    u32x4 areg[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) areg[j] = *reinterpret_cast<const u32x4 *>(aimg + j * kMfmaAStep + abase);
-#pragma unroll
-    for (int s = 0; s < 3; ++s) {
-        const int q = lane + 64 * s;
-        if (q < 144) *reinterpret_cast<u32x4 *>(wimg + (q / 9) * kMfmaRowBytes + (q % 9) * 16) = wv[s];
-    }
-    __builtin_amdgcn_wave_barrier();
-    const uint8_t *rp = wimg + i16 * kMfmaRowBytes;  // lane (g, row i16)
-    const u32x4 hdr = *reinterpret_cast<const u32x4 *>(rp);
-    const u32x4 qa = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
-    const u32x4 qb = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
-    f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t dw = j < 4 ? qa[j] : qb[j - 4], ew = dw >> 8;
-        const u32x4 bw = {dw & 0x000f000fu, ew & 0x000f000fu, dw & 0x00f000f0u, ew & 0x00f000f0u};
-        acc[j & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, areg[j]),
-                                                            __builtin_bit_cast(half8, bw), acc[j & 1],
-                                                            0, 0, 0);
-    }
-    const f32x4 dsum = acc[0] + acc[1];
     float part = 0.0f;
-    if (c < nchunk) {
-        uint32_t scp, mnp;
-        q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
-        const float d = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
-        const float qx_lo = (dsum[0] + dsum[1]) * __builtin_amdgcn_ldexpf(1.0f, 24 - sigma);
-        const float qx_hi = (dsum[2] + dsum[3]) * __builtin_amdgcn_ldexpf(1.0f, 20 - sigma);
-        const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
-        const float m_lo = (float)(mnp & 0xffu), m_hi = (float)(mnp >> 8);
-        part = d * (sc_lo * qx_lo + sc_hi * qx_hi) - dmin * (m_lo * sx_lo + m_hi * sx_hi);
+    u32x4 areg[8];
+    auto read_a = [&](int u) __attribute__((always_inline)) {
+        const int c = 4 * (b0 + u) + g;
+        const bool act = (m >> 2) == g && c < nchunk;
+        const uint32_t *img = aimg + (u % NA) * kMfmaAImgDwords;
+        const int abase = act ? g * 16 + (m & 1) * 8 + ((m >> 1) & 1) * 4 : 64;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) areg[j] = *reinterpret_cast<const u32x4 *>(img + j * kMfmaAStep + abase);
+    };
+    read_a(0);  // before the weights arrive
+#pragma unroll
+    for (int u = 0; u < BPW; ++u) {
+        const int b = b0 + u;
+        if (b >= nb) break;  // wave-uniform
+        if (u >= NA) {
+            stage(u);  // slot u % NA: block u - NA is done with it
+            __builtin_amdgcn_wave_barrier();
+        }
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            const int q = lane + 64 * s;
+            if (q < 144) *reinterpret_cast<u32x4 *>(wimg + (q / 9) * kMfmaRowBytes + (q % 9) * 16) = wv[u][s];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (u > 0) read_a(u);
+        const uint8_t *rp = wimg + i16 * kMfmaRowBytes;  // lane (g, row i16)
+        const u32x4 hdr = *reinterpret_cast<const u32x4 *>(rp);
+        const u32x4 qa = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
+        const u32x4 qb = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
+        f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t dw = j < 4 ? qa[j] : qb[j - 4], ew = dw >> 8;
+            const u32x4 bw = {dw & 0x000f000fu, ew & 0x000f000fu, dw & 0x00f000f0u, ew & 0x00f000f0u};
+            acc[j & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, areg[j]),
+                                                                __builtin_bit_cast(half8, bw),
+                                                                acc[j & 1], 0, 0, 0);
+        }
+        const f32x4 dsum = acc[0] + acc[1];
+        if (4 * b + g < nchunk) {
+            uint32_t scp, mnp;
+            q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
+            const float d = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
+            const float qx_lo = (dsum[0] + dsum[1]) * __builtin_amdgcn_ldexpf(1.0f, 24 - sgm[u]);
+            const float qx_hi = (dsum[2] + dsum[3]) * __builtin_amdgcn_ldexpf(1.0f, 20 - sgm[u]);
+            const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
+            const float m_lo = (float)(mnp & 0xffu), m_hi = (float)(mnp >> 8);
+            part += d * (sc_lo * qx_lo + sc_hi * qx_hi) - dmin * (m_lo * sxl[u] + m_hi * sxh[u]);
+        }
+        __builtin_amdgcn_wave_barrier();
     }
-    part = sum_rows4(part);  // the row's four chunks of block b
-    if (lane < 16) red[lane * nb + b] = part;
+    part = sum_rows4(part);  // the row's chunks of this wave's blocks
+    if (lane < 16) red[lane * nwaves + wave] = part;
     __syncthreads();
 
     if (tid < 16) {
         float s = 0.0f;
-        for (int j = 0; j < nb; ++j) s += red[tid * nb + j];
+        for (int j = 0; j < nwaves; ++j) s += red[tid * nwaves + j];
         if (NORM) {
             float tot = 0.0f;
-            for (int j = 0; j < nb; ++j) tot += ssq[j];
+            for (int j = 0; j < nwaves; ++j) tot += ssq[j];
             s *= 1.0f / sqrtf(tot / (float)k + fz.norm_eps);
         }
         const int row = row0 + tid;
@@ -796,25 +853,46 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     const int nb = (int)((k + 255) / 256);
     const int nchunk = (int)((k + 63) / 64);
     const uint8_t *wp = (const uint8_t *)weight_q4k;
-    if (nb <= kMfmaMaxBlocks && g_tune_kernel != 1) {
-        const size_t lds = gemv_mfma_lds_bytes(nb);
+    // Matrix-core kernel up to 64 blocks (up to four per wave; the
+    // attention-combine prologue is single-block); measured faster than the
+    // dot-product kernel on every decode shape.  `q4k_gemv.kernel` = 1 forces
+    // the dot-product kernel where its LDS holds the activation (k <~ 12K).
+    const int bpw = nb <= 16 ? 1 : (nb <= 32 ? 2 : (nb <= 48 ? 3 : 4));
+    const bool mfma_ok = nb <= kMfmaMaxBlocks && (bpw == 1 || !fz.attn_o);
+    const bool dot_ok = gemv_lds_bytes(nchunk, 8) <= 64 * 1024;
+    const bool use_mfma = g_tune_kernel == 1 ? !dot_ok && mfma_ok : mfma_ok;
+    if (use_mfma) {
+        const int nwaves = (nb + bpw - 1) / bpw;
+        const size_t lds = gemv_mfma_lds_bytes(nwaves, bpw);
         const unsigned grid = (unsigned)((n + 15) / 16);
-        const int x_vec4 = activation && ((uintptr_t)activation & 15) == 0;
-#define DOE_GEMV_MFMA_LAUNCH(P)                                                                   \
+        const bool xv = activation && ((uintptr_t)activation & 15) == 0 && (k & 3) == 0;
+#define DOE_GEMV_MFMA_LAUNCH(P, B, X)                                                             \
     do {                                                                                          \
         static bool attr_set = false;                                                             \
         if (!attr_set) {                                                                          \
-            DOE_HIP_CHECK(hipFuncSetAttribute((const void *)q4k_gemv_mfma_kernel<P>,              \
+            DOE_HIP_CHECK(hipFuncSetAttribute((const void *)q4k_gemv_mfma_kernel<P, B, X>,        \
                                               hipFuncAttributeMaxDynamicSharedMemorySize,         \
-                                              (int)gemv_mfma_lds_bytes(kMfmaMaxBlocks)));         \
+                                              (int)gemv_mfma_lds_bytes(16, B)));                  \
             attr_set = true;                                                                      \
         }                                                                                         \
-        hipLaunchKernelGGL((q4k_gemv_mfma_kernel<P>), dim3(grid), dim3(64 * nb), lds, st, wp,     \
-                           activation, output, (int)n, (int)k, nb, x_vec4, fz);                   \
+        hipLaunchKernelGGL((q4k_gemv_mfma_kernel<P, B, X>), dim3(grid), dim3(64 * nwaves), lds,   \
+                           st, wp, activation, output, (int)n, (int)k, nb, fz);                   \
     } while (0)
-        if (fz.attn_o) DOE_GEMV_MFMA_LAUNCH(2);
-        else if (fz.norm_w) DOE_GEMV_MFMA_LAUNCH(1);
-        else DOE_GEMV_MFMA_LAUNCH(0);
+#define DOE_GEMV_MFMA_BPW(P, X)                                                                   \
+    switch (bpw) {                                                                                \
+        case 1: DOE_GEMV_MFMA_LAUNCH(P, 1, X); break;                                             \
+        case 2: DOE_GEMV_MFMA_LAUNCH(P, 2, X); break;                                             \
+        case 3: DOE_GEMV_MFMA_LAUNCH(P, 3, X); break;                                             \
+        default: DOE_GEMV_MFMA_LAUNCH(P, 4, X); break;                                            \
+    }
+        if (fz.attn_o) {
+            DOE_GEMV_MFMA_LAUNCH(2, 1, 0);
+        } else if (fz.norm_w) {
+            if (xv) DOE_GEMV_MFMA_BPW(1, 1) else DOE_GEMV_MFMA_BPW(1, 0)
+        } else {
+            if (xv) DOE_GEMV_MFMA_BPW(0, 1) else DOE_GEMV_MFMA_BPW(0, 0)
+        }
+#undef DOE_GEMV_MFMA_BPW
 #undef DOE_GEMV_MFMA_LAUNCH
         DOE_LAUNCH_CHECK("q4k_gemv_mfma_kernel");
         return DOE_OK;

@@ -64,11 +64,15 @@ def _gemv(w, x, n, k, stream=None):
 
 # config-0 shape, every 2B-class projection shape, 31B prefill K, tails
 GEMV_SHAPES = [(9216, 2304), (2048, 2304), (1024, 2304), (2304, 2048), (2304, 9216),
-               (21504 // 16, 5376), (1, 256), (3, 300), (37, 64 * 3 + 5), (1000, 1024)]
+               (21504 // 16, 5376), (1, 256), (3, 300), (37, 64 * 3 + 5), (1000, 1024),
+               (100, 16384), (50, 12300)]
 
 
 @pytest.mark.parametrize("n,k", GEMV_SHAPES)
 def test_gemv_matches_oracle(dev, ora, n, k, gemv_kernel):
+    if gemv_kernel == 1 and k > 12288:
+        pytest.skip("past k ~ 12K the activation no longer fits the dot-product kernel's LDS; "
+                    "the matrix-core kernel runs instead")
     rng = np.random.default_rng(n * 7 + k)
     w = q4k.random_q4k(rng, n, k)
     x = rng.standard_normal(k).astype(np.float32)
