@@ -547,9 +547,10 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
             const int ec = min(e, k - 4), h = ec / D, d = ec - h * D;
 #pragma unroll
             for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
-                const int ss = min(sp, S - 1);
-                ao[sp] = *reinterpret_cast<const float4 *>(fz.attn_o + ((size_t)h * S + ss) * D + d);
-                aml[sp] = *reinterpret_cast<const float2 *>(fz.attn_ml + ((size_t)h * S + ss) * 2);
+                if (sp < S) {  // S is uniform: only the existing splits are read
+                    ao[sp] = *reinterpret_cast<const float4 *>(fz.attn_o + ((size_t)h * S + sp) * D + d);
+                    aml[sp] = *reinterpret_cast<const float2 *>(fz.attn_ml + ((size_t)h * S + sp) * 2);
+                }
             }
         } else if (XV) {
             const float4 f = *reinterpret_cast<const float4 *>(x + min(e, k - 4));  // masked below
@@ -558,7 +559,11 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
 #pragma unroll
             for (int j = 0; j < 4; ++j) v[u][j] = x[min(e + j, k - 1)];  // masked below
         }
-        if (NORM) {
+        if (NORM && XV) {  // (XV also covers the norm weight's alignment)
+            const float4 f = *reinterpret_cast<const float4 *>(fz.norm_w + min(e, k - 4));
+            nwv[NORM ? u : 0][0] = f.x; nwv[NORM ? u : 0][1] = f.y;
+            nwv[NORM ? u : 0][2] = f.z; nwv[NORM ? u : 0][3] = f.w;
+        } else if (NORM) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) nwv[NORM ? u : 0][j] = fz.norm_w[min(e + j, k - 1)];
         }
@@ -865,7 +870,8 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         const int nwaves = (nb + bpw - 1) / bpw;
         const size_t lds = gemv_mfma_lds_bytes(nwaves, bpw);
         const unsigned grid = (unsigned)((n + 15) / 16);
-        const bool xv = activation && ((uintptr_t)activation & 15) == 0 && (k & 3) == 0;
+        const bool xv = activation && ((uintptr_t)activation & 15) == 0 && (k & 3) == 0 &&
+                        ((uintptr_t)fz.norm_w & 15) == 0;
 #define DOE_GEMV_MFMA_LAUNCH(P, B, X)                                                             \
     do {                                                                                          \
         static bool attr_set = false;                                                             \
