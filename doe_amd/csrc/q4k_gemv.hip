@@ -521,7 +521,7 @@ template <int PRO, int BPW, int XV>
 __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__restrict__ w,
                                                              const float *x,
                                                              float *__restrict__ y, int n, int k,
-                                                             int nb, GemvFusion fz) {
+                                                             int nb, int nbs, GemvFusion fz) {
     constexpr bool NORM = PRO == 1, ATTN = PRO == 2;
     constexpr int NA = mfma_images(BPW), WAVE_LDS = mfma_wave_lds(BPW);
     static_assert(!ATTN || BPW == 1, "the attention-combine prologue is single-block");
@@ -531,7 +531,9 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
     uint32_t *aimg = reinterpret_cast<uint32_t *>(wimg + 16 * kMfmaRowBytes);
     float *red = reinterpret_cast<float *>(lds + nwaves * WAVE_LDS);  // [16][nwaves] row partials
     float *ssq = red + 16 * nwaves;                                       // [nwaves] sums of squares
-    const int row0 = blockIdx.x * 16, b0 = wave * BPW;
+    // K split: workgroup (x, y) owns blocks [y * nbs, min(nb, (y + 1) * nbs)).
+    const int row0 = blockIdx.x * 16, kb1 = min(nb, ((int)blockIdx.y + 1) * nbs);
+    const int b0 = (int)blockIdx.y * nbs + wave * BPW;
 
     // Activation operands first (vector-memory returns are in order, so the
     // staging below never waits on the weight stream).
@@ -576,7 +578,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
     u32x4 wv[BPW][3];
 #pragma unroll
     for (int u = 0; u < BPW; ++u) {
-        const int blk = min(b0 + u, nb - 1);  // past the row end: a valid block, unused
+        const int blk = min(b0 + u, kb1 - 1);  // past the range: a valid block, unused
 #pragma unroll
         for (int s = 0; s < 3; ++s) {
             const int q = min(lane + 64 * s, 143);
@@ -673,7 +675,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
     // The first NA blocks' images are staged while the weights are in flight.
 #pragma unroll
     for (int u = 0; u < NA; ++u)
-        if (b0 + u < nb) stage(u);
+        if (b0 + u < kb1) stage(u);
     // LDS operations of one wave complete in order (an image is read before a
     // later block overwrites it); the wave barriers keep the compiler from
     // moving reads above writes.
@@ -692,7 +694,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
 #pragma unroll
     for (int u = 0; u < BPW; ++u) {
         const int b = b0 + u;
-        if (b >= nb) break;  // wave-uniform
+        if (b >= kb1) break;  // wave-uniform
         if (u >= NA) {
             stage(u);  // slot u % NA: block u - NA is done with it
             __builtin_amdgcn_wave_barrier();
@@ -750,7 +752,8 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
             const float other = dpp<kDppXor1>(s);
             if ((tid & 1) == 0 && row < n) rope_kv_pair(fz, row, s, other, y);
         } else if (row < n) {
-            y[row] = fz.residual ? s + fz.residual[row] : s;
+            if (gridDim.y > 1) atomicAdd(y + row, s);  // K split: y holds the residual already
+            else y[row] = fz.residual ? s + fz.residual[row] : s;
         }
     }
 }
@@ -759,6 +762,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
 int g_tune_rowslots = 0;
 int g_tune_rows = 0;
 int g_tune_kernel = 0;  // 0 automatic, 1 dot-product kernel, 2 matrix-core kernel
+int g_tune_ksplit = 0;  // 0 automatic, 1 never split K over workgroups
 
 // Launch shape for the GEMV: rowslots * nchunk threads (rounded up to whole
 // waves) and R rows per thread.  The automatic choice spreads the rows over
@@ -862,14 +866,30 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     // attention-combine prologue is single-block); measured faster than the
     // dot-product kernel on every decode shape.  `q4k_gemv.kernel` = 1 forces
     // the dot-product kernel where its LDS holds the activation (k <~ 12K).
-    const int bpw = nb <= 16 ? 1 : (nb <= 32 ? 2 : (nb <= 48 ? 3 : 4));
+    if (g_num_cus == 0) {
+        int dev = 0, cus = 0;
+        DOE_HIP_CHECK(hipGetDevice(&dev));
+        DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        g_num_cus = cus > 0 ? cus : 256;
+    }
+    // K split over workgroups (at most 16 blocks, one per wave, each), the
+    // partial row sums added atomically into y: only for an in-place residual
+    // (y already holds it) with a plain activation, when the rows alone give
+    // fewer workgroups than CUs.
+    const int64_t row_groups = (n + 15) / 16;
+    int ksplit = 1;
+    if (nb > 16 && fz.residual == output && !fz.norm_w && !fz.attn_o && !fz.gated && !fz.rope_kv &&
+        row_groups < g_num_cus && g_tune_ksplit != 1)
+        ksplit = (nb + 15) / 16;
+    const int nbs = (nb + ksplit - 1) / ksplit;  // blocks per split
+    const int bpw = nbs <= 16 ? 1 : (nbs <= 32 ? 2 : (nbs <= 48 ? 3 : 4));
     const bool mfma_ok = nb <= kMfmaMaxBlocks && (bpw == 1 || !fz.attn_o);
     const bool dot_ok = gemv_lds_bytes(nchunk, 8) <= 64 * 1024;
     const bool use_mfma = g_tune_kernel == 1 ? !dot_ok && mfma_ok : mfma_ok;
     if (use_mfma) {
-        const int nwaves = (nb + bpw - 1) / bpw;
+        const int nwaves = (nbs + bpw - 1) / bpw;
         const size_t lds = gemv_mfma_lds_bytes(nwaves, bpw);
-        const unsigned grid = (unsigned)((n + 15) / 16);
+        const dim3 grid((unsigned)row_groups, (unsigned)ksplit);
         const bool xv = activation && ((uintptr_t)activation & 15) == 0 && (k & 3) == 0 &&
                         ((uintptr_t)fz.norm_w & 15) == 0;
 #define DOE_GEMV_MFMA_LAUNCH(P, B, X)                                                             \
@@ -881,8 +901,8 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
                                               (int)gemv_mfma_lds_bytes(16, B)));                  \
             attr_set = true;                                                                      \
         }                                                                                         \
-        hipLaunchKernelGGL((q4k_gemv_mfma_kernel<P, B, X>), dim3(grid), dim3(64 * nwaves), lds,   \
-                           st, wp, activation, output, (int)n, (int)k, nb, fz);                   \
+        hipLaunchKernelGGL((q4k_gemv_mfma_kernel<P, B, X>), grid, dim3(64 * nwaves), lds, st, wp, \
+                           activation, output, (int)n, (int)k, nb, nbs, fz);                      \
     } while (0)
 #define DOE_GEMV_MFMA_BPW(P, X)                                                                   \
     switch (bpw) {                                                                                \
@@ -902,12 +922,6 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
 #undef DOE_GEMV_MFMA_LAUNCH
         DOE_LAUNCH_CHECK("q4k_gemv_mfma_kernel");
         return DOE_OK;
-    }
-    if (g_num_cus == 0) {
-        int dev = 0, cus = 0;
-        DOE_HIP_CHECK(hipGetDevice(&dev));
-        DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-        g_num_cus = cus > 0 ? cus : 256;
     }
     GemvShape s = gemv_shape(n, nchunk, g_num_cus);
     if ((fz.gated || fz.rope_kv) && ((s.rowslots * s.rows_per_thread) & 1)) {
@@ -1026,6 +1040,9 @@ int doe_tune_set(const char *key, int value) {
         g_tune_rowslots = value;
     } else if (!strcmp(key, "q4k_gemv.rows")) {
         g_tune_rows = value;
+    } else if (!strcmp(key, "q4k_gemv.ksplit")) {
+        DOE_REQUIRE(value == 0 || value == 1, DOE_E_INVALID, "q4k_gemv.ksplit is 0 or 1");
+        g_tune_ksplit = value;
     } else if (!strcmp(key, "q4k_gemv.kernel")) {
         DOE_REQUIRE(value >= 0 && value <= 2, DOE_E_INVALID, "q4k_gemv.kernel is 0, 1 or 2");
         g_tune_kernel = value;

@@ -172,3 +172,27 @@ def test_gemv_unaligned_activation(dev, ora, gemv_kernel):
     _lib.call("doe_q4k_gemv", C.c_void_p(dw.ptr), C.c_void_p(dx.ptr + 4), C.c_void_p(dy.ptr), n, k,
               C.c_void_p(None))
     assert rel_l2(dy.download(), ora.q4k_gemv(w, x, n, k)) < 1e-5
+
+
+@pytest.mark.parametrize("n,k", [(2304, 9216), (37, 5376), (1000, 4352)])
+def test_gemv_inplace_residual_k_split(dev, ora, n, k):
+    # y <- y + W x with the output buffer as the residual: past 16 blocks and
+    # below one 16-row group per CU the K range is split over workgroups whose
+    # partial sums are added atomically; the unsplit kernel agrees
+    rng = np.random.default_rng(k + n)
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    r = rng.standard_normal(n).astype(np.float32)
+    want = ora.q4k_gemv(w, x, n, k) + r.astype(np.float64)
+    dw, dx = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x)
+    got = {}
+    for split in (0, 1):
+        ops.tune("q4k_gemv.ksplit", split)
+        try:
+            dy = DeviceBuffer.from_array(r)
+            ops.matmul_q4k_fused(dw, dx, dy, n, k, residual=dy)
+            got[split] = dy.download()
+        finally:
+            ops.tune("q4k_gemv.ksplit", 0)
+        assert rel_l2(got[split], want) < 1e-5, split
+    assert rel_l2(got[0], got[1]) < 1e-6
