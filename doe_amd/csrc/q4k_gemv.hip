@@ -874,13 +874,17 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     }
     // K split over workgroups (at most 16 blocks, one per wave, each), the
     // partial row sums added atomically into y: only for an in-place residual
-    // (y already holds it) with a plain activation, when the rows alone give
+    // (y already holds it) and an element-wise activation prologue (not the
+    // RMSNorm, whose scale needs the whole row), when the rows alone give
     // fewer workgroups than CUs.
     const int64_t row_groups = (n + 15) / 16;
     int ksplit = 1;
-    if (nb > 16 && fz.residual == output && !fz.norm_w && !fz.attn_o && !fz.gated && !fz.rope_kv &&
-        row_groups < g_num_cus && g_tune_ksplit != 1)
-        ksplit = (nb + 15) / 16;
+    if (nb > 1 && fz.residual == output && !fz.norm_w && !fz.gated && !fz.rope_kv &&
+        row_groups < g_num_cus && g_tune_ksplit != 1) {
+        const int64_t fill = (g_num_cus + row_groups - 1) / row_groups;
+        ksplit = (int)(fill < nb ? fill : nb);
+        if (ksplit < (nb + 15) / 16) ksplit = (nb + 15) / 16;
+    }
     const int nbs = (nb + ksplit - 1) / ksplit;  // blocks per split
     const int bpw = nbs <= 16 ? 1 : (nbs <= 32 ? 2 : (nbs <= 48 ? 3 : 4));
     const bool mfma_ok = nb <= kMfmaMaxBlocks && (bpw == 1 || !fz.attn_o);

@@ -306,6 +306,11 @@ def test_attention_partials_and_fused_o_projection(dev, ora, kv_len, max_splits,
     attn = ora.attn_decode(q, kc, vc, hq, hkv, d, kv_len, maxs, scale).reshape(-1)
     want = ora.residual(ora.q4k_gemv(wo, attn, hidden, hq * d), res)
     assert rel_l2(out.download(), want) < 1e-5
+    # in place (output = residual, as the decode step calls it): the K range
+    # is split over workgroups that add their row sums atomically
+    inplace = up(res)
+    ops.matmul_q4k_attn_out(up(wo), parts, splits, hq, d, inplace, hidden, residual=inplace)
+    assert rel_l2(inplace.download(), want) < 1e-5
     # the same partials through the plain attention op give the same activation
     full = DeviceBuffer.empty((1, hq, d), np.float32)
     ops.attention(up(q), up(kc), up(vc), full, batch=1, num_heads=hq, num_kv_heads=hkv, head_dim=d,
