@@ -135,30 +135,48 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     const uint16_t *kb = a.k + kv_base;
     const uint16_t *vb = a.v + kv_base;
 
-    // First block's loads go out before the query staging.
+    // Query fragments (A operand) into LDS: lane l holds row l % 16 (query
+    // head hq0 + l % 16 when < G), dims 32 s + 8 (l / 16) .. + 7.  The query
+    // loads go out before the first K/V block's (vector-memory returns are in
+    // order: staging the query then never waits on the K/V stream).
+    constexpr int QITEMS = (KSTEPS * 64 + kThreads - 1) / kThreads;
+    float qv[QITEMS][8];
+#pragma unroll
+    for (int it = 0; it < QITEMS; ++it) {
+        const int idx = tid + it * kThreads;
+        const int s = (idx >> 6) % KSTEPS, l = idx & 63, m = l & 15;
+        // rows >= G (and items past the fragment count) read row 0; zeroed below
+        const size_t qi = ((size_t)b * a.num_heads + hq0 + (m < G ? m : 0)) * D + 32 * s + 8 * (l >> 4);
+        if (a.q_f16) {
+            const h8 t = *reinterpret_cast<const h8 *>(reinterpret_cast<const _Float16 *>(a.q) + qi);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qv[it][j] = (float)t[j];
+        } else {
+            const float4 t0 = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.q) + qi);
+            const float4 t1 = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.q) + qi + 4);
+            qv[it][0] = t0.x; qv[it][1] = t0.y; qv[it][2] = t0.z; qv[it][3] = t0.w;
+            qv[it][4] = t1.x; qv[it][5] = t1.y; qv[it][6] = t1.z; qv[it][7] = t1.w;
+        }
+    }
+    __asm__ volatile("" ::: "memory");
     KVBlock<D> cur;
     int blk = blk_begin + wave;
     if (blk < blk_end) load_block<D>(cur, kb, vb, blk * 16, kv_len, pos_stride, lane);
-
-    // Query fragments (A operand) into LDS: lane l holds row l % 16 (query
-    // head hq0 + l % 16 when < G), dims 32 s + 8 (l / 16) .. + 7.
-    for (int idx = tid; idx < KSTEPS * 64; idx += kThreads) {
-        const int s = idx >> 6, l = idx & 63;
-        const int m = l & 15;
-        h8 hi, lo;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float v = 0.0f;
-            if (m < G) {
-                const size_t qi = ((size_t)b * a.num_heads + hq0 + m) * D + 32 * s + 8 * (l >> 4) + j;
-                v = a.q_f16 ? (float)reinterpret_cast<const _Float16 *>(a.q)[qi]
-                            : reinterpret_cast<const float *>(a.q)[qi];
+    for (int it = 0; it < QITEMS; ++it) {
+        const int idx = tid + it * kThreads;
+        if (idx < KSTEPS * 64) {
+            const int s = idx >> 6, l = idx & 63, m = l & 15;
+            h8 hi, lo;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = m < G ? qv[it][j] : 0.0f;
+                hi[j] = (_Float16)v;
+                lo[j] = (_Float16)(v - (float)hi[j]);
             }
-            hi[j] = (_Float16)v;
-            lo[j] = (_Float16)(v - (float)hi[j]);
+            sm.qfrag[0][s][l] = hi;
+            sm.qfrag[1][s][l] = lo;
         }
-        sm.qfrag[0][s][l] = hi;
-        sm.qfrag[1][s][l] = lo;
     }
     __syncthreads();
 
@@ -177,11 +195,10 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     float *pbw = reinterpret_cast<float *>(&pb[wave][0][0]);  // [17][G4*4]
 
     for (; blk < blk_end; blk += kWaves) {
-        // Prefetch the next block of this wave (clamped to the current one at
-        // the end, which then hits in cache) while this one is computed.
+        // Prefetch the next block of this wave while this one is computed
+        // (only when there is one: a wave retires only once its loads are back).
         KVBlock<D> nxt;
-        const int nb = blk + kWaves < blk_end ? blk + kWaves : blk;
-        load_block<D>(nxt, kb, vb, nb * 16, kv_len, pos_stride, lane);
+        if (blk + kWaves < blk_end) load_block<D>(nxt, kb, vb, (blk + kWaves) * 16, kv_len, pos_stride, lane);
 
         const int p0 = blk * 16;
         const int pk = p0 + (lane & 15);
@@ -462,8 +479,9 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
     DOE_REQUIRE(sliding_window >= 0 && softcap >= 0.0f, DOE_E_INVALID, "negative window or softcap");
     if (batch == 0) return DOE_OK;
     DOE_REQUIRE(q && k_cache && v_cache && (out || parts), DOE_E_INVALID, "null pointer");
-    DOE_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0, DOE_E_INVALID,
-                "k/v caches must be 16-byte aligned");
+    DOE_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)k_cache & 15) == 0 &&
+                    ((uintptr_t)v_cache & 15) == 0,
+                DOE_E_INVALID, "q and the k/v caches must be 16-byte aligned");
     DOE_REQUIRE(batch * num_kv_heads <= 65535 && kv_stride <= 0x7fffffff, DOE_E_UNSUPPORTED,
                 "too many sequences x kv heads");
     const int g = (int)(num_heads / num_kv_heads);

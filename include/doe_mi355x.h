@@ -211,6 +211,7 @@ int doe_attn_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, vo
  *   the query sits at position kv_len - 1; sliding_window > 0 keeps keys
  *   [kv_len - sliding_window, kv_len); softcap > 0 applies tanh(s/cap)*cap.
  * head_dim 64/128/256/512, num_heads / num_kv_heads in {1, 2, 4, 8} (512: <= 2).
+ * q, k_cache and v_cache must be 16-byte aligned.
  * Uses a library-owned workspace for split-K partials: calls on one device
  * must not run concurrently on different streams. */
 int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uint16_t *v_cache,
