@@ -37,6 +37,7 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct AttnArgs {
     const void *q;
@@ -140,7 +141,9 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     // loads go out before the first K/V block's (vector-memory returns are in
     // order: staging the query then never waits on the K/V stream).
     constexpr int QITEMS = (KSTEPS * 64 + kThreads - 1) / kThreads;
-    float qv[QITEMS][8];
+    // raw bytes first: no conversion between the loads, so every query load
+    // and the first K/V block are in flight together
+    u32x4 qraw[QITEMS][2];
 #pragma unroll
     for (int it = 0; it < QITEMS; ++it) {
         const int idx = tid + it * kThreads;
@@ -148,14 +151,10 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         // rows >= G (and items past the fragment count) read row 0; zeroed below
         const size_t qi = ((size_t)b * a.num_heads + hq0 + (m < G ? m : 0)) * D + 32 * s + 8 * (l >> 4);
         if (a.q_f16) {
-            const h8 t = *reinterpret_cast<const h8 *>(reinterpret_cast<const _Float16 *>(a.q) + qi);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qv[it][j] = (float)t[j];
+            qraw[it][0] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const _Float16 *>(a.q) + qi);
         } else {
-            const float4 t0 = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.q) + qi);
-            const float4 t1 = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.q) + qi + 4);
-            qv[it][0] = t0.x; qv[it][1] = t0.y; qv[it][2] = t0.z; qv[it][3] = t0.w;
-            qv[it][4] = t1.x; qv[it][5] = t1.y; qv[it][6] = t1.z; qv[it][7] = t1.w;
+            qraw[it][0] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(a.q) + qi);
+            qraw[it][1] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(a.q) + qi + 4);
         }
     }
     __asm__ volatile("" ::: "memory");
@@ -167,10 +166,22 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         const int idx = tid + it * kThreads;
         if (idx < KSTEPS * 64) {
             const int s = idx >> 6, l = idx & 63, m = l & 15;
+            float qv[8];
+            if (a.q_f16) {
+                const h8 t = __builtin_bit_cast(h8, qraw[it][0]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qv[j] = (float)t[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    qv[j] = __uint_as_float(qraw[it][0][j]);
+                    qv[4 + j] = __uint_as_float(qraw[it][1][j]);
+                }
+            }
             h8 hi, lo;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float v = m < G ? qv[it][j] : 0.0f;
+                const float v = m < G ? qv[j] : 0.0f;
                 hi[j] = (_Float16)v;
                 lo[j] = (_Float16)(v - (float)hi[j]);
             }
