@@ -763,6 +763,7 @@ int g_tune_rowslots = 0;
 int g_tune_rows = 0;
 int g_tune_kernel = 0;  // 0 automatic, 1 dot-product kernel, 2 matrix-core kernel
 int g_tune_ksplit = 0;  // 0 automatic, 1 never split K over workgroups
+int g_tune_bpw = 0;     // 0 automatic, else at least this many blocks per wave (<= 4)
 
 // Launch shape for the GEMV: rowslots * nchunk threads (rounded up to whole
 // waves) and R rows per thread.  The automatic choice spreads the rows over
@@ -886,7 +887,8 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         if (ksplit < (nb + 15) / 16) ksplit = (nb + 15) / 16;
     }
     const int nbs = (nb + ksplit - 1) / ksplit;  // blocks per split
-    const int bpw = nbs <= 16 ? 1 : (nbs <= 32 ? 2 : (nbs <= 48 ? 3 : 4));
+    int bpw = nbs <= 16 ? 1 : (nbs <= 32 ? 2 : (nbs <= 48 ? 3 : 4));
+    if (g_tune_bpw > bpw && g_tune_bpw <= 4 && !fz.attn_o) bpw = g_tune_bpw;
     const bool mfma_ok = nb <= kMfmaMaxBlocks && (bpw == 1 || !fz.attn_o);
     const bool dot_ok = gemv_lds_bytes(nchunk, 8) <= 64 * 1024;
     const bool use_mfma = g_tune_kernel == 1 ? !dot_ok && mfma_ok : mfma_ok;
@@ -1044,6 +1046,9 @@ int doe_tune_set(const char *key, int value) {
         g_tune_rowslots = value;
     } else if (!strcmp(key, "q4k_gemv.rows")) {
         g_tune_rows = value;
+    } else if (!strcmp(key, "q4k_gemv.bpw")) {
+        DOE_REQUIRE(value >= 0 && value <= 4, DOE_E_INVALID, "q4k_gemv.bpw is 0..4");
+        g_tune_bpw = value;
     } else if (!strcmp(key, "q4k_gemv.ksplit")) {
         DOE_REQUIRE(value == 0 || value == 1, DOE_E_INVALID, "q4k_gemv.ksplit is 0 or 1");
         g_tune_ksplit = value;

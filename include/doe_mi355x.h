@@ -100,7 +100,7 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
  * fused_gemv_dequant, runtime/zig/src/doe_wgsl/emit_csl_fused.zig:47-200,
  * exported symbols activation/weight/output) and the reference interpreter's
  * fused_gemv (runtime/zig/src/tsir/reference_interpreter.zig:169-394).
- * activation: f32[k] (16-byte aligned), output: f32[n]. */
+ * activation: f32[k], output: f32[n]. */
 int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
                  int64_t n, int64_t k, doe_stream_t stream);
 
@@ -109,7 +109,8 @@ int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
  * dequant(W)[i][k] * attn[k] (+ residual[i]), attn = the combine of the
  * partials written by doe_attn_decode_partials (batch 1, num_heads x
  * head_dim = k, 1..8 splits).  Replaces the attention combine + o_proj +
- * attn_residual steps of a decode step. */
+ * attn_residual steps of a decode step.  residual == output (in place) may
+ * split K over workgroups that add their partial sums atomically. */
 int doe_q4k_gemv_attn_out(const void *weight_q4k, const float *attn_partials, int64_t splits,
                           int64_t num_heads, int64_t head_dim, float *output, int64_t n,
                           const float *residual, doe_stream_t stream);
@@ -150,6 +151,8 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
  *     norm_eps, weight w (norm_weight_offset 0) or 1 + w (1), as
  *     bench/inference-pipeline/kernels/rmsnorm.wgsl:15-93.
  *   residual != NULL: output[i] = dot_i + residual[i] (residual.wgsl).
+ *     residual == output (in place) may split K over workgroups that add
+ *     their partial sums atomically: the f32 addition order then varies.
  *   gated != 0: rows come as interleaved (gate, up) pairs; output has n/2
  *     values gelu_tanh(dot_2i) * dot_2i+1 (gelu_gated.wgsl:1-14).
  * gated and residual are exclusive; gated needs n even. */
