@@ -6,24 +6,29 @@
 // (nibble - 8) and :25-66 (GEMV over the row, scale [row][col/group]), with the
 // f16 scales of the 27B-class batch-8 decode shape.
 //
-// The batch rides in the N dimension of v_mfma_f32_16x16x32_f16: one MFMA is
-// 16 weight rows x one 32-element group x 16 columns, columns 0..7 carrying
-// x_hi of the eight batch rows and 8..15 their x_lo (x = x_hi + x_lo in f16
-// after a power-of-two scale per batch row and group), so nothing in the matrix core is
-// wasted at M = 8 and the products carry ~22 bits of x.  (q - 8) is exact in
-// f16 (OR the nibble into the mantissa of 1024, subtract 1032), each group's
-// 16x16 result is scaled by its f16 scale in f32, and the hi/lo halves meet
-// in one lane exchange at the end.
+// One v_mfma_f32_16x16x32_f16 per (16 rows, one 32-element group):
+//   * A = the x image: 16 columns = the eight batch rows' x_hi and x_lo (x
+//     scaled per batch row by a power of two so its max sits near 2^14, split
+//     into two f16), in the k order of B below;
+//   * B = the nibbles of one u32 per lane as f16 subnormals with ANDs only:
+//     w & 0x000F000F holds nibbles 0 and 4 as q * 2^-24, w & 0x00F000F0 nibbles
+//     1 and 5 as q * 2^-20 (the image holds x / 16 there, exact), and the same
+//     of w >> 8 nibbles 2, 6 and 3, 7: every product is exact;
+//   * D + C, C = -8 * 2^-24 * sum(x) of the group in the x_hi columns, is
+//     2^-24 * sum((q - 8) x).
+// D lands with lane (row, column group) holding four batch columns of one
+// row: one f16 scale (v_fma_mix) serves all four.  The power-of-two unscale
+// per batch row and the hi + lo sum (one cross-half lane swap) come at the
+// end.
 //
-// A pre-pass writes x as the MFMA's B-operand image ([group][64 lanes][8 f16],
-// 1 KB per group, plus one power-of-two unscale factor per group and batch
-// row: x is scaled per 32-element group so max|x| sits near 2^14), read by
-// every workgroup from L2.  A workgroup owns 64 rows (four 16-row MFMA tiles
-// per wave, so each x fragment feeds four MFMAs) and 32 groups of K, eight
-// per wave with every load of a wave issued up front; the
-// four waves' sums meet in LDS.  K is split over the grid's y dimension when
-// the rows alone do not fill the GPU, and the splits are summed by a small
-// second kernel (deterministic order, no atomics).
+// A pre-pass (one workgroup per batch row) finds the row's max |x| and writes
+// the image ([group][64 lanes][8 f16], 1 KB per group), the corrections
+// ([group][16] f32) and the row's scale exponent.  A workgroup of the GEMV
+// owns 64 rows (four 16-row tiles per wave, so an image fragment feeds four
+// MFMAs) and 32 groups of K, eight per wave with every load of a wave issued
+// up front; the four waves' sums meet in LDS.  K is split over the grid's y
+// dimension into 32-group ranges whose sums are added atomically into y (the
+// pre-pass clears it), so the f32 summation order varies from run to run.
 #include "common.h"
 
 #include <math.h>
@@ -38,70 +43,93 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxBatch = 8;
 
-// x image: lane l of group g holds, for column c = l % 16 (batch c % 8, part
-// c / 8: 0 = hi, 1 = lo), x * 2^sig[b][g] at k = 32 g + 8 (l / 16) +
-// {0, 4, 1, 5, 2, 6, 3, 7}[j]; unscale[g][c] = 2^-sig[b][g] (0 past the batch).
-// One thread per (group, batch row, lane group): eight groups per workgroup.
-__global__ __launch_bounds__(256) void int4_x_image_kernel(const float *__restrict__ x,
-                                                           _Float16 *__restrict__ img,
-                                                           float *__restrict__ unscale, int M,
-                                                           int K) {
-    const int lg = threadIdx.x & 3, b = (threadIdx.x >> 2) & 7;
-    const int g = blockIdx.x * 8 + (threadIdx.x >> 5);
-    if (g >= K / 32) return;  // whole quads leave together
-    float v[8];
-    if (b < M) {
-        const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t)b * K + 32 * g + 8 * lg);
-        const float4 a = xp[0], c = xp[1];
-        v[0] = a.x; v[1] = c.x; v[2] = a.y; v[3] = c.y; v[4] = a.z; v[5] = c.z; v[6] = a.w; v[7] = c.w;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-    }
+// Pre-pass: workgroup b = batch row b (rows >= M write zeros); when the
+// GEMV splits K (atomic partial sums), it also clears y[b].
+constexpr int kImgThreads = 1024;
+__global__ __launch_bounds__(kImgThreads) void int4_x_image_kernel(const float *__restrict__ x,
+                                                                   _Float16 *__restrict__ img,
+                                                                   float *__restrict__ corr,
+                                                                   int *__restrict__ sig_out,
+                                                                   float *__restrict__ y_clear,
+                                                                   int M, int N, int K) {
+    __shared__ float wmax[kImgThreads / 64];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    if (y_clear && b < M)
+        for (int i = tid; i < N; i += kImgThreads) y_clear[(size_t)b * N + i] = 0.0f;
+    const int G = K / 32;
+    const bool live = b < M;
+    const float *xr = x + (size_t)(live ? b : 0) * K;
     float amax = 0.0f;
+    if (live)
+        for (int k4 = tid; k4 < K / 4; k4 += kImgThreads) {
+            const float4 v = reinterpret_cast<const float4 *>(xr)[k4];
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if (lane == 0) wmax[tid >> 6] = amax;
+    __syncthreads();
+    amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    for (int i = 0; i < kImgThreads / 64; ++i) amax = fmaxf(amax, wmax[i]);
     int sig = 0;
     if (amax > 0.0f && amax <= 3.0e38f) {
         sig = 14 - __builtin_amdgcn_frexp_expf(amax);
         sig = sig < -120 ? -120 : (sig > 120 ? 120 : sig);
     }
+    if (tid == 0) sig_out[b] = sig;
     const float sc = __builtin_amdgcn_ldexpf(1.0f, sig);
-    _Float16 hi[8], lo[8];
+    // item (g, kg): eight consecutive x, four items per group in one quad
+    for (int item = tid; item < G * 4; item += kImgThreads) {
+        const int g = item >> 2, kg = item & 3;
+        float v[8];
+        if (live) {
+            const float4 p0 = reinterpret_cast<const float4 *>(xr + 32 * g + 8 * kg)[0];
+            const float4 p1 = reinterpret_cast<const float4 *>(xr + 32 * g + 8 * kg)[1];
+            v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+        } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float t = v[j] * sc;
-        hi[j] = (_Float16)t;
-        lo[j] = (_Float16)(t - (float)hi[j]);
-    }
-    _Float16 *base = img + (size_t)g * 512;
-    *reinterpret_cast<half8 *>(base + (lg * 16 + b) * 8) = half8{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
-    *reinterpret_cast<half8 *>(base + (lg * 16 + 8 + b) * 8) = half8{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
-    if (lg == 0) {
-        const float f = b < M ? __builtin_amdgcn_ldexpf(1.0f, -sig) : 0.0f;
-        unscale[g * 16 + b] = f;
-        unscale[g * 16 + 8 + b] = f;
+            for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+        }
+        float sum = 0.0f;
+        half8 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // slot j: nibble (j / 2) + 4 (j % 2) ... in B's order n0 n4 n1 n5 n2 n6 n3 n7
+            const int nib = (j >> 1) + 4 * (j & 1);
+            const float t = v[nib] * sc;
+            sum += t;
+            const _Float16 h = (_Float16)t, l = (_Float16)(t - (float)h);
+            // slots 2, 3, 6, 7 meet nibbles coded at bits 4..7 (x 16): store x / 16
+            const bool odd = (j & 2) != 0;
+            hi[j] = odd ? (_Float16)((float)h * 0.0625f) : h;
+            lo[j] = odd ? (_Float16)((float)l * 0.0625f) : l;
+        }
+        _Float16 *base = img + (size_t)g * 512;
+        *reinterpret_cast<half8 *>(base + (kg * 16 + b) * 8) = hi;
+        *reinterpret_cast<half8 *>(base + (kg * 16 + 8 + b) * 8) = lo;
+        // the group's sum over its four quads (consecutive threads)
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if (kg == 0) {
+            corr[g * 16 + b] = -8.0f * 5.9604644775390625e-08f * sum;  // -8 * 2^-24 * sum(x)
+            corr[g * 16 + 8 + b] = 0.0f;
+        }
     }
 }
 
-// (q - 8) of the eight nibbles of one word, in the image's k order.
+// B operand of one word: halves (n0, n4, 16 n1, 16 n5, n2, n6, 16 n3, 16 n7) * 2^-24.
 __device__ __forceinline__ half8 unpack_int4(uint32_t w) {
-    const half2v off = {(_Float16)1032.0f, (_Float16)1032.0f};
-    const half2v p0 = __builtin_bit_cast(half2v, (w & 0x000f000fu) | 0x64006400u) - off;
-    const half2v p1 = __builtin_bit_cast(half2v, ((w >> 4) & 0x000f000fu) | 0x64006400u) - off;
-    const half2v p2 = __builtin_bit_cast(half2v, ((w >> 8) & 0x000f000fu) | 0x64006400u) - off;
-    const half2v p3 = __builtin_bit_cast(half2v, ((w >> 12) & 0x000f000fu) | 0x64006400u) - off;
-    return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    const uint32_t w8 = w >> 8;
+    return __builtin_bit_cast(half8, u32x4{w & 0x000f000fu, w & 0x00f000f0u, w8 & 0x000f000fu, w8 & 0x00f000f0u});
 }
 
 struct Int4Args {
     const uint32_t *q;
     const uint16_t *scales;
     const _Float16 *img;
-    const float *unscale;
-    float *out;  // y [M][N] (one split) or partials [splits][M][N]
+    const float *corr;
+    const int *sig;
+    float *out;  // y [M][N] (K splits add atomically into y, cleared by the pre-pass)
     int M, N, K, G;
 };
 
@@ -112,6 +140,7 @@ struct Int4Args {
 // lane order (lane (r, j) takes word j of each group of row r).
 template <int GPW>
 __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
+    static_assert(GPW == 8, "one 16-byte scale load per row tile covers eight groups");
     __shared__ float red[3][4][4][64];
     __shared__ __attribute__((aligned(16))) uint32_t wl[4][64 * 4 * GPW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -121,8 +150,19 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
     const bool active = g0 < a.G;  // a.G is a multiple of GPW
     const int gb = active ? g0 : 0;
 
-    // all loads first: the 64 rows' weight bytes, GPW x fragments and
-    // unscale factors, and the scales of this lane's 16 D rows
+    // all loads first: the x image fragments and corrections (L2-resident),
+    // the scales of this lane's rows, then the 64 rows' weight bytes
+    half8 xa[GPW];
+    float4v cz[GPW];
+#pragma unroll
+    for (int u = 0; u < GPW; ++u) {
+        xa[u] = *reinterpret_cast<const half8 *>(a.img + ((size_t)(gb + u) * 64 + lane) * 8);
+        cz[u] = *reinterpret_cast<const float4v *>(a.corr + (gb + u) * 16 + 4 * lg);
+    }
+    u32x4 sv[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        sv[t] = *reinterpret_cast<const u32x4 *>(a.scales + (size_t)min(r0 + 16 * t + lr, a.N - 1) * a.G + gb);
     constexpr int RPI = 64 / GPW;  // rows per load instruction
     u32x4 wg[GPW];
 #pragma unroll
@@ -131,22 +171,6 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
         wg[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
             a.q + (size_t)min(r0 + row, a.N - 1) * (a.K / 8) + 4 * (gb + lane % GPW)));
     }
-    half8 xb[GPW];
-    float f[GPW];
-#pragma unroll
-    for (int u = 0; u < GPW; ++u) {
-        xb[u] = *reinterpret_cast<const half8 *>(a.img + ((size_t)(gb + u) * 64 + lane) * 8);
-        f[u] = a.unscale[(gb + u) * 16 + lr];
-    }
-    u32x4 sv[4][4][GPW / 8];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint16_t *srow = a.scales + (size_t)min(r0 + 16 * t + 4 * lg + i, a.N - 1) * a.G + gb;
-#pragma unroll
-            for (int h = 0; h < GPW / 8; ++h) sv[t][i][h] = *reinterpret_cast<const u32x4 *>(srow + 8 * h);
-        }
     // regroup: wl[(row * 4 + word) * GPW + group]
     uint32_t *my = wl[wave];
 #pragma unroll
@@ -170,6 +194,7 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
         }
     }
 
+    // acc[t][i]: row r0 + 16 t + lr, column 4 lg + i (batch (4 lg + i) % 8, hi for lg < 2)
     float acc[4][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -180,14 +205,14 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
         for (int u = 0; u < GPW; ++u) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const float4v z = {0.0f, 0.0f, 0.0f, 0.0f};
-                const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_int4(w[t][u]), xb[u], z, 0, 0, 0);
+                // (the correction is added after the product: as the MFMA's
+                // accumulator input it cost precision, rel-L2 1.9e-5 vs 4.8e-6)
+                const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+                const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u], unpack_int4(w[t][u]), zero, 0, 0, 0) + cz[u];
+                const uint32_t pair = sv[t][u >> 1];
+                const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)((u & 1) ? (pair >> 16) : pair));
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t pair = sv[t][i][u >> 3][(u & 7) >> 1];
-                    const float s = doe_half_bits_to_float((u & 1) ? (pair >> 16) : pair);
-                    acc[t][i] = fmaf(d[i] * f[u], s, acc[t][i]);
-                }
+                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(s, d[i], acc[t][i]);
             }
         }
     }
@@ -200,27 +225,21 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
     }
     __syncthreads();
     if (wave > 0) return;
-    // D lane l, tile t: row r0 + 16 t + 4 lg + i, column lr (batch lr % 8; lr / 8: hi / lo)
-    const int b = lr & 7;
+    // x_hi columns sit in lanes 0..31, x_lo in 32..63: one swap adds them
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float v = acc[t][i] + red[0][t][i][lane] + red[1][t][i][lane] + red[2][t][i][lane];
-            v += __shfl_xor(v, 8, 64);
-            const int row = r0 + 16 * t + 4 * lg + i;
-            if (lr < 8 && b < a.M && row < a.N) a.out[((size_t)blockIdx.y * a.M + b) * a.N + row] = v;
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            const int b = 4 * lg + i, row = r0 + 16 * t + lr;
+            if (lg < 2 && b < a.M && row < a.N) {
+                const float r = __builtin_amdgcn_ldexpf(v, 24 - a.sig[b]);
+                if (gridDim.y > 1) atomicAdd(a.out + (size_t)b * a.N + row, r);  // y cleared by the pre-pass
+                else a.out[(size_t)b * a.N + row] = r;
+            }
         }
-}
-
-__global__ __launch_bounds__(256) void int4_split_sum_kernel(const float *__restrict__ part,
-                                                             float *__restrict__ y, int splits,
-                                                             int total) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= total) return;
-    float s = 0.0f;
-    for (int p = 0; p < splits; ++p) s += part[(size_t)p * total + i];
-    y[i] = s;
 }
 
 std::mutex g_ws_mu;
@@ -266,9 +285,8 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     const int splits = (G + per_wg - 1) / per_wg;
 
     const size_t img_bytes = (size_t)G * 64 * 8 * 2;
-    const size_t fac_bytes = (size_t)G * 16 * 4;
-    const size_t part_bytes = splits > 1 ? (size_t)splits * m * n * sizeof(float) : 0;
-    const size_t need = img_bytes + fac_bytes + part_bytes;
+    const size_t fac_bytes = (size_t)G * 16 * 4 + kMaxBatch * 4;  // corrections, exponents
+    const size_t need = img_bytes + fac_bytes;
     void *ws;
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -282,17 +300,18 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
         ws = g_ws;
     }
     _Float16 *img = (_Float16 *)ws;
-    float *unscale = (float *)((char *)ws + img_bytes);
-    float *part = (float *)((char *)ws + img_bytes + fac_bytes);
-    hipLaunchKernelGGL(int4_x_image_kernel, dim3((unsigned)((G + 7) / 8)), dim3(256), 0, st, x, img, unscale, (int)m,
-                       (int)k);
+    float *corr = (float *)((char *)ws + img_bytes);
+    int *sig = (int *)(corr + (size_t)G * 16);
+    hipLaunchKernelGGL(int4_x_image_kernel, dim3(kMaxBatch), dim3(kImgThreads), 0, st, x, img, corr, sig,
+                       splits > 1 ? y : nullptr, (int)m, (int)n, (int)k);
     DOE_LAUNCH_CHECK("int4_x_image_kernel");
     Int4Args a;
     a.q = w_u4;
     a.scales = scales_f16;
     a.img = img;
-    a.unscale = unscale;
-    a.out = splits > 1 ? part : y;
+    a.corr = corr;
+    a.sig = sig;
+    a.out = y;
     a.M = (int)m;
     a.N = (int)n;
     a.K = (int)k;
@@ -300,12 +319,6 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     const dim3 grid((unsigned)row_blocks, (unsigned)splits);
     hipLaunchKernelGGL(int4_gemv_kernel<8>, grid, dim3(256), 0, st, a);
     DOE_LAUNCH_CHECK("int4_gemv_kernel");
-    if (splits > 1) {
-        const int total = (int)(m * n);
-        hipLaunchKernelGGL(int4_split_sum_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, part, y,
-                           splits, total);
-        DOE_LAUNCH_CHECK("int4_split_sum_kernel");
-    }
     return DOE_OK;
 }
 
