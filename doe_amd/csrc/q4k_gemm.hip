@@ -19,11 +19,11 @@
 //     packed fma.  The relative error of w is ~2^-11, far inside the rel-L2
 //     1e-3 contract; a bf16 B (8 bits) would sit at ~1.1e-3.
 //
-// Tiling: 256 x 256 output tile per 256-thread workgroup (2 x 2 waves, each a
-// 128 x 128 block of sixteen 32x32 accumulators; 128 x 128 tiles for small
-// problems), K in steps of one Q4_K chunk
-// (64), A and B tiles double-buffered in LDS with the next chunk's global loads
-// in flight during the current chunk's MFMAs.  Tiles are ordered in groups of
+// Tiling: problems with at least 256 tiles of 256 x 256 use q4k_gemm_pipe_kernel
+// (four waves side by side in N, raw B blocks in LDS dequantised per wave,
+// software-pipelined); smaller ones use 128 x 128 tiles (2 x 2 waves of 64 x 64)
+// with the B chunk dequantised once into LDS.  K runs in steps of one Q4_K
+// chunk (64), A and B double-buffered in LDS.  Tiles are ordered in groups of
 // 8 M-tiles and each XCD (workgroup id mod 8) gets a contiguous range of that
 // order, so the workgroups resident on one XCD share A and B chunks in its L2.
 #include "common.h"
@@ -62,7 +62,8 @@ __device__ __forceinline__ void scale_min_pair(uint32_t s0, uint32_t s1, uint32_
 
 // ---------------------------------------------------------------------------
 // Pre-pass: A bf16 [M][K] -> f16 [M][Kp] (zero padded to Kp, a multiple of
-// 64) scaled by 2^sig[m]; one workgroup per row.
+// 64, or of 256 for the large-tile kernel) scaled by 2^sig[m]; one workgroup
+// per row.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void a_rows_to_f16_kernel(const uint16_t *__restrict__ a,
                                                             _Float16 *__restrict__ a16,
@@ -258,14 +259,30 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// Large-problem GEMM: 256 (M) x 256 (N) tile, the four waves side by side in
-// N (wave w owns columns 64w..64w+63 for all 256 rows: 8 x 2 accumulators).
-// B is staged raw: each Q4_K block (144 bytes) of the tile's 256 rows is
-// loaded once per 256-element K step with line-contiguous 16-byte granules
-// and kept in LDS, and each wave dequantises its MFMA B operands straight
-// from those bytes (8 nibbles -> 8 f16 per lane per 16-k step).  A is staged
-// as f16 per 64-element chunk.  Both are double-buffered; the raw B block
-// for step b + 2 is in flight during the four chunks of step b.
+// Large-problem GEMM: 256 (M) x 256 (N) tile per 256-thread workgroup, the
+// four waves side by side in N (wave w owns columns 64w..64w+63 for all 256
+// rows: 8 x 2 accumulators of v_mfma_f32_32x32x16_f16).  B is staged raw:
+// each Q4_K block (144 bytes) of the tile's 256 rows is loaded once per 256 K
+// with line-contiguous 16-byte granules and kept in LDS, and each wave
+// dequantises its MFMA B operands straight from those bytes (8 nibbles -> 8
+// f16 per lane per 16-k step).  A is staged as f16 per 64-element chunk.
+// Every latency is kept off the MFMA stream (one wave per SIMD issues in
+// order, so anything it waits on idles the matrix core):
+//   * the MFMA operands of 16-k step s + 1 (eight A fragments, two raw B
+//     granules, dequantised in registers) are read and converted while the
+//     sixteen MFMAs of step s run, interleaved one LDS read or a few VALU
+//     operations per MFMA;
+//   * A chunk c + 1 is written to LDS at the start of chunk c (its global
+//     loads were issued one chunk earlier) and B block b + 1 at the start of
+//     block b (loads four chunks earlier), so one barrier per chunk, waiting
+//     on LDS only, separates the writes from the next chunk's reads;
+//   * global loads are buffer loads over the tile's rows with 32-bit offsets:
+//     rows past M or N read as zero, no per-granule 64-bit pointers;
+//   * the four chunks of a Q4_K block are unrolled, so buffer parities and the
+//     sub-block scale selection are compile-time constants;
+//   * the row unscaling factors sit in LDS, so the epilogue's stores never
+//     wait on a global load.
+// A is the f16 copy padded to a whole number of Q4_K blocks (Kp = 256 nb).
 // ---------------------------------------------------------------------------
 constexpr int kRawRow = 152;  // bytes per raw B row: 144 + 8 pad, conflict-free b64 reads
 
@@ -289,10 +306,36 @@ __device__ __forceinline__ half8 dequant8(uint32_t w0, uint32_t w1, half2v dsc, 
     return r;
 }
 
-__global__ __launch_bounds__(256) void q4k_gemm_big_kernel(GemmArgs g) {
+constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit data format
+
+// Scales of chunk c4's two sub-blocks for one B row from its 16 header bytes.
+template <int C4>
+__device__ __forceinline__ void chunk_scales(const u32x4 &h, half2v &dsc_lo, half2v &ndmm_lo, half2v &dsc_hi,
+                                             half2v &ndmm_hi) {
+    uint32_t scp, mnp;
+    scale_min_pair(h.y, h.z, h.w, C4, scp, mnp);
+    const float d = doe_half_bits_to_float(h.x), dmin = doe_half_bits_to_float(h.x >> 16);
+    const _Float16 s0 = (_Float16)(d * (float)(scp & 0xffu)), s1 = (_Float16)(d * (float)(scp >> 8));
+    const _Float16 z0 = (_Float16)(-(dmin * (float)(mnp & 0xffu)));
+    const _Float16 z1 = (_Float16)(-(dmin * (float)(mnp >> 8)));
+    dsc_lo = half2v{s0, s0};
+    dsc_hi = half2v{s1, s1};
+    ndmm_lo = half2v{z0, z0};
+    ndmm_hi = half2v{z1, z1};
+}
+
+// Barrier for LDS hand-offs only: outstanding global loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__global__ __launch_bounds__(256) void q4k_gemm_pipe_kernel(GemmArgs g) {
     constexpr int BM = 256, BN = 256;
     __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLdsRow];
     __shared__ __attribute__((aligned(16))) uint8_t Braw[2][BN * kRawRow];
+    __shared__ float rowscale[BM];  // 2^-sig of the tile's rows (exact unscaling)
 
     const int T = g.tiles_m * g.tiles_n;
     int t = blockIdx.x;
@@ -308,40 +351,35 @@ __global__ __launch_bounds__(256) void q4k_gemm_big_kernel(GemmArgs g) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 31, lk = 8 * (lane >> 5);
 
-    // A granules: gi = tid + 256 i -> row gi >> 3, column (gi & 7) * 8
-    const _Float16 *aptr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int gi = tid + 256 * i;
-        aptr[i] = g.a16 + (size_t)min(m0 + (gi >> 3), g.M - 1) * g.Kp + (gi & 7) * 8;
-    }
-    // raw B granules: gi = tid + 256 i -> row gi / 9, 16-byte piece gi % 9
-    const size_t brow_bytes = (size_t)g.nb * DOE_Q4K_BLOCK_BYTES;
-    const uint8_t *bptr[9];
-    int bdst[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) {
-        const int gi = tid + 256 * i;
-        const int row = gi / 9, piece = gi - 9 * (gi / 9);
-        bptr[i] = g.b + (size_t)min(n0 + row, g.N - 1) * brow_bytes + piece * 16;
-        bdst[i] = row * kRawRow + piece * 16;
-    }
+    const uint32_t a_stride = (uint32_t)g.Kp * 2u;
+    const uint32_t brow_bytes = (uint32_t)g.nb * DOE_Q4K_BLOCK_BYTES;
+    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(g.a16 + (size_t)m0 * g.Kp), (short)0, (int)((uint32_t)min(BM, g.M - m0) * a_stride), kBufFlags);
+    const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(g.b + (size_t)n0 * brow_bytes), (short)0, (int)((uint32_t)min(BN, g.N - n0) * brow_bytes), kBufFlags);
+    // A granule i: row (tid >> 3) + 32 i, bytes 16 (tid & 7) of the chunk
+    const uint32_t a_voff = (uint32_t)(tid >> 3) * a_stride + (uint32_t)(tid & 7) * 16u;
+    const int a_lds = (tid >> 3) * kLdsRow + (tid & 7) * 8;
 
     u32x4 ra[8], rb[9];
-    // (macros, not lambdas: the staging arrays must stay in registers)
-#define DOE_BIG_LOAD_A(KC)                                                                          \
-    _Pragma("unroll") for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(aptr[i] + (KC) * kBK)
-#define DOE_BIG_STORE_A(BUF)                                                                        \
-    _Pragma("unroll") for (int i = 0; i < 8; ++i)                                                   \
-        *reinterpret_cast<u32x4 *>(&As[BUF][((tid + 256 * i) >> 3) * kLdsRow + ((tid + 256 * i) & 7) * 8]) = ra[i]
-#define DOE_BIG_LOAD_B(BLK)                                                                         \
-    _Pragma("unroll") for (int i = 0; i < 9; ++i)                                                   \
-        rb[i] = *reinterpret_cast<const u32x4 *>(bptr[i] + (size_t)(BLK) * DOE_Q4K_BLOCK_BYTES)
-#define DOE_BIG_STORE_B(BUF)                                                                        \
-    _Pragma("unroll") for (int i = 0; i < 9; ++i) {                                                 \
-        u32x2 *d_ = reinterpret_cast<u32x2 *>(&Braw[BUF][bdst[i]]);                                 \
-        d_[0] = u32x2{rb[i].x, rb[i].y};                                                            \
-        d_[1] = u32x2{rb[i].z, rb[i].w};                                                            \
+#define DOE_PIPE_LOAD_A(KC)                                                                            \
+    _Pragma("unroll") for (int i = 0; i < 8; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(         \
+        arsrc, a_voff + (uint32_t)i * 32u * a_stride, (KC) * (kBK * 2), 0)
+#define DOE_PIPE_STORE_A(BUF)                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4 *>(&As[BUF][a_lds + i * 32 * kLdsRow]) = ra[i]
+    // B granule i: gi = tid + 256 i -> row gi / 9, 16-byte piece gi % 9
+#define DOE_PIPE_LOAD_B(BLK)                                                                           \
+    _Pragma("unroll") for (int i = 0; i < 9; ++i) {                                                    \
+        const int gi_ = tid + 256 * i, row_ = gi_ / 9;                                                 \
+        rb[i] = __builtin_amdgcn_raw_buffer_load_b128(                                                 \
+            brsrc, (uint32_t)row_ * brow_bytes + (uint32_t)(gi_ - 9 * row_) * 16u, (BLK) * DOE_Q4K_BLOCK_BYTES, 0); \
+    }
+#define DOE_PIPE_STORE_B(BUF)                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 9; ++i) {                                                    \
+        const int gi_ = tid + 256 * i, row_ = gi_ / 9;                                                 \
+        u32x2 *d_ = reinterpret_cast<u32x2 *>(&Braw[BUF][row_ * kRawRow + (gi_ - 9 * row_) * 16]);     \
+        d_[0] = u32x2{rb[i].x, rb[i].y};                                                               \
+        d_[1] = u32x2{rb[i].z, rb[i].w};                                                               \
     }
 
     float16v acc[8][2];
@@ -352,85 +390,151 @@ __global__ __launch_bounds__(256) void q4k_gemm_big_kernel(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    DOE_BIG_LOAD_A(0);
-    DOE_BIG_LOAD_B(0);
-    DOE_BIG_STORE_A(0);
-    DOE_BIG_STORE_B(0);
-    if (g.nb > 1) {
-        DOE_BIG_LOAD_B(1);
-    }
-    __syncthreads();
+    // this lane's two B rows within the tile
+    int brow[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) brow[j] = (wave * 64 + j * 32 + lr) * kRawRow;
+    const int afrag = lr * kLdsRow + lk;
 
-    for (int kc = 0; kc < g.nchunk; ++kc) {
-        const int abuf = kc & 1, bbuf = (kc >> 2) & 1, c4 = kc & 3;
-        if (kc + 1 < g.nchunk) {
-            DOE_BIG_LOAD_A(kc + 1);
-        }
-        // this lane's two B rows: scale/min of sub-blocks 2*c4, 2*c4 + 1
-        half2v dsc[2][2], ndmm[2][2];
+    const int sig_row = g.sig[min(m0 + tid, g.M - 1)];
+    DOE_PIPE_LOAD_A(0);
+    DOE_PIPE_LOAD_B(0);
+    rowscale[tid] = __builtin_amdgcn_ldexpf(1.0f, -sig_row);
+    DOE_PIPE_STORE_A(0);
+    DOE_PIPE_STORE_B(0);
+    DOE_PIPE_LOAD_A(min(1, g.nchunk - 1));
+    DOE_PIPE_LOAD_B(min(1, g.nb - 1));
+    lds_barrier();
+
+    // operands of step (chunk 0, k-step 0)
+    u32x4 hdr[2];
+    half2v dsc[2][2], ndmm[2][2];
+    half8 af[2][8], bf[2][2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint8_t *hrow = &Braw[bbuf][(wave * 64 + j * 32 + lr) * kRawRow];
-            const u32x2 h01 = *reinterpret_cast<const u32x2 *>(hrow);
-            const u32x2 h23 = *reinterpret_cast<const u32x2 *>(hrow + 8);
-            uint32_t scp, mnp;
-            scale_min_pair(h01.y, h23.x, h23.y, c4, scp, mnp);
-            const float d = doe_half_bits_to_float(h01.x), dmin = doe_half_bits_to_float(h01.x >> 16);
-            const _Float16 s0 = (_Float16)(d * (float)(scp & 0xffu)), s1 = (_Float16)(d * (float)(scp >> 8));
-            const _Float16 z0 = (_Float16)(-(dmin * (float)(mnp & 0xffu)));
-            const _Float16 z1 = (_Float16)(-(dmin * (float)(mnp >> 8)));
-            dsc[j][0] = half2v{s0, s0};
-            dsc[j][1] = half2v{s1, s1};
-            ndmm[j][0] = half2v{z0, z0};
-            ndmm[j][1] = half2v{z1, z1};
-        }
-#pragma unroll
-        for (int ks = 0; ks < kBK / 16; ++ks) {
-            half8 af[8], bf[2];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                af[i] = *reinterpret_cast<const half8 *>(&As[abuf][(i * 32 + lr) * kLdsRow + ks * 16 + lk]);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const u32x2 raw = *reinterpret_cast<const u32x2 *>(
-                    &Braw[bbuf][(wave * 64 + j * 32 + lr) * kRawRow + 16 + 32 * c4 + ((ks * 16 + lk) & 31)]);
-                bf[j] = ks < 2 ? dequant8<false>(raw.x, raw.y, dsc[j][0], ndmm[j][0])
-                               : dequant8<true>(raw.x, raw.y, dsc[j][1], ndmm[j][1]);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (kc + 1 < g.nchunk) {
-            DOE_BIG_STORE_A(abuf ^ 1);
-        }
-        if (c4 == 3 && (kc >> 2) + 1 < g.nb) {
-            DOE_BIG_STORE_B(bbuf ^ 1);
-            if ((kc >> 2) + 2 < g.nb) {
-                DOE_BIG_LOAD_B((kc >> 2) + 2);
-            }
-        }
-        __syncthreads();
+    for (int j = 0; j < 2; ++j) {
+        const u32x2 h01 = *reinterpret_cast<const u32x2 *>(&Braw[0][brow[j]]);
+        const u32x2 h23 = *reinterpret_cast<const u32x2 *>(&Braw[0][brow[j] + 8]);
+        hdr[j] = u32x4{h01.x, h01.y, h23.x, h23.y};
+        chunk_scales<0>(hdr[j], dsc[j][0], ndmm[j][0], dsc[j][1], ndmm[j][1]);
+        const u32x2 raw = *reinterpret_cast<const u32x2 *>(&Braw[0][brow[j] + 16 + lk]);
+        bf[0][j] = dequant8<false>(raw.x, raw.y, dsc[j][0], ndmm[j][0]);
     }
-#undef DOE_BIG_LOAD_A
-#undef DOE_BIG_STORE_A
-#undef DOE_BIG_LOAD_B
-#undef DOE_BIG_STORE_B
+#pragma unroll
+    for (int i = 0; i < 8; ++i) af[0][i] = *reinterpret_cast<const half8 *>(&As[0][afrag + i * 32 * kLdsRow]);
+
+    for (int blk = 0; blk < g.nb; ++blk) {
+        const int bb = blk & 1;
+        const uint8_t *bcur = Braw[bb];
+        const uint8_t *bnext = Braw[bb ^ 1];
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+            const int kc = 4 * blk + c4;
+            const int ab = c4 & 1;  // chunk kc's A buffer (4 blk is even)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int p = ks & 1;
+                // operands of the next step: (chunk kc, step ks + 1) or (chunk kc + 1, step 0)
+                const int abn = ks < 3 ? ab : ab ^ 1;
+                const uint8_t *bsrc = (ks < 3 || c4 < 3) ? bcur : bnext;
+                const int kbyte = ks < 3 ? 32 * c4 + (((ks + 1) * 16 + lk) & 31) : 32 * ((c4 + 1) & 3) + lk;
+                const int acol = ks < 3 ? (ks + 1) * 16 : 0;
+                u32x2 rawn[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    if (ks == 3 && c4 == 3) {
+                        const u32x2 h01 = *reinterpret_cast<const u32x2 *>(&bnext[brow[j]]);
+                        const u32x2 h23 = *reinterpret_cast<const u32x2 *>(&bnext[brow[j] + 8]);
+                        hdr[j] = u32x4{h01.x, h01.y, h23.x, h23.y};
+                    }
+                    rawn[j] = *reinterpret_cast<const u32x2 *>(&bsrc[brow[j] + 16 + kbyte]);
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    af[p ^ 1][i] = *reinterpret_cast<const half8 *>(&As[abn][afrag + i * 32 * kLdsRow + acol]);
+                if (ks == 0) {
+                    // A chunk kc + 1 (and B block blk + 1) to the free buffers, then the next loads
+                    DOE_PIPE_STORE_A(ab ^ 1);
+                    if (c4 == 0) {
+                        DOE_PIPE_STORE_B(bb ^ 1);
+                        DOE_PIPE_LOAD_B(min(blk + 2, g.nb - 1));
+                    }
+                    DOE_PIPE_LOAD_A(min(kc + 2, g.nchunk - 1));
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[p][j], acc[i][j], 0, 0, 0);
+                // first half: the B reads, then one LDS read (or write) per MFMA
+                if (ks == 3 && c4 == 3) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+                else __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (ks == 0) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                }
+                if (ks == 2) {
+                    // every wave's writes of chunk kc + 1 (and block blk + 1) are done, and its
+                    // reads of chunk kc's buffers issued: the next chunk may read / overwrite them
+                    __builtin_amdgcn_sched_barrier(0);
+                    lds_barrier();
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 4; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[p][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    if (ks == 0) {
+                        bf[p ^ 1][j] = dequant8<false>(rawn[j].x, rawn[j].y, dsc[j][0], ndmm[j][0]);
+                    } else if (ks < 3) {
+                        bf[p ^ 1][j] = dequant8<true>(rawn[j].x, rawn[j].y, dsc[j][1], ndmm[j][1]);
+                    } else {
+                        switch (c4) {  // scales of the next chunk
+                            case 0: chunk_scales<1>(hdr[j], dsc[j][0], ndmm[j][0], dsc[j][1], ndmm[j][1]); break;
+                            case 1: chunk_scales<2>(hdr[j], dsc[j][0], ndmm[j][0], dsc[j][1], ndmm[j][1]); break;
+                            case 2: chunk_scales<3>(hdr[j], dsc[j][0], ndmm[j][0], dsc[j][1], ndmm[j][1]); break;
+                            default: chunk_scales<0>(hdr[j], dsc[j][0], ndmm[j][0], dsc[j][1], ndmm[j][1]); break;
+                        }
+                        bf[p ^ 1][j] = dequant8<false>(rawn[j].x, rawn[j].y, dsc[j][0], ndmm[j][0]);
+                    }
+                }
+                // second half: global loads and the dequant VALU between the MFMAs
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (ks == 0) {
+                        __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+                    }
+                    if (ks == 3) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                    else __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+#undef DOE_PIPE_LOAD_A
+#undef DOE_PIPE_STORE_A
+#undef DOE_PIPE_LOAD_B
+#undef DOE_PIPE_STORE_B
 
     // epilogue: D lane l, r: row (r%4) + 8(r/4) + 4(l/32), column l%32
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m = m0 + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+            const int ml = i * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+            const int m = m0 + ml;
             if (m >= g.M) continue;
-            const float us = __builtin_amdgcn_ldexpf(1.0f, -g.sig[m]);
+            const float us = rowscale[ml];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int n = n0 + wave * 64 + j * 32 + lr;
-                if (n < g.N) g.c[(size_t)m * g.N + n] = acc[i][j][r] * us;
+                if (n < g.N) __builtin_nontemporal_store(acc[i][j][r] * us, &g.c[(size_t)m * g.N + n]);
             }
         }
     }
@@ -463,7 +567,10 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
     DOE_REQUIRE(m <= (1 << 24) && n <= (1 << 24) && k <= (1 << 20) && m * n <= ((int64_t)1 << 40),
                 DOE_E_UNSUPPORTED, "q4k_gemm shape too large (m=%lld n=%lld k=%lld)", (long long)m,
                 (long long)n, (long long)k);
-    const int64_t kp = (k + kBK - 1) / kBK * kBK;
+    // 256 x 256 tiles once there are enough of them to fill the CUs, else 128 x 128
+    const bool big = m >= 256 && n >= 256 && ((m + 255) / 256) * ((n + 255) / 256) >= 256;
+    // the large-tile kernel streams whole Q4_K blocks: A padded to 256 nb columns
+    const int64_t kp = big ? (k + 255) / 256 * 256 : (k + kBK - 1) / kBK * kBK;
     const size_t a16_bytes = (size_t)m * (size_t)kp * 2;
     const size_t need = a16_bytes + (size_t)m * 4;
     void *ws;
@@ -492,15 +599,13 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
     g.Kp = (int)kp;
     g.nb = (int)((k + 255) / 256);
     g.nchunk = (int)(kp / kBK);
-    // 256 x 256 tiles once there are enough of them to fill the CUs, else 128 x 128
-    const bool big = m >= 256 && n >= 256 && ((m + 255) / 256) * ((n + 255) / 256) >= 256;
     const int bm = big ? 256 : 128, bn = big ? 256 : 128;
     g.tiles_m = (int)((m + bm - 1) / bm);
     g.tiles_n = (int)((n + bn - 1) / bn);
     const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
     DOE_REQUIRE(tiles <= 0x7fffffff, DOE_E_UNSUPPORTED, "too many tiles");
     if (big)
-        hipLaunchKernelGGL(q4k_gemm_big_kernel, dim3((unsigned)tiles), dim3(256), 0, st, g);
+        hipLaunchKernelGGL(q4k_gemm_pipe_kernel, dim3((unsigned)tiles), dim3(256), 0, st, g);
     else
         hipLaunchKernelGGL((q4k_gemm_kernel<2, 2>), dim3((unsigned)tiles), dim3(256), 0, st, g);
     DOE_LAUNCH_CHECK("q4k_gemm_kernel");
