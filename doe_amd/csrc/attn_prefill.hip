@@ -14,17 +14,26 @@
 //     accumulate).  The transposed product puts one query per lane column, so
 //     the online softmax needs no cross-lane reductions except one exchange
 //     between the two lane halves that hold the same query.
-//   * P = exp2(S*scale*log2e - m) in f32, rounded to f16, and O^T += V^T . P^T
-//     on v_mfma_f32_32x32x16_f16: P's registers are used in place as the B
-//     operand (the key order of the product follows the MFMA's D layout; V^T is
-//     read in the same order).  V is staged transposed in LDS and converted
-//     bf16 -> f16 on the way (exact for |v| in [2^-14, 65504]); f16 P keeps
-//     the output near 1e-4 rel-L2, where a bf16 P would sit at ~1e-3.
+//   * P = exp2(S*scale*log2e - m) in f32 (one fma and one exp per score),
+//     rounded to f16, and O^T += V^T . P^T on v_mfma_f32_32x32x16_f16: P's
+//     registers are used in place as the B operand (the key order of the
+//     product follows the MFMA's D layout; V^T is read in the same order).
+//     The row sum l adds the same f16 P values (v_dot2_f32_f16).
+//   * The running max m is raised (and O, l rescaled) only when some query's
+//     block max exceeds it by more than 2^8: P stays <= 256, well inside f16,
+//     and the O rescale runs on a few blocks instead of every block.
+//   * The causal mask is evaluated only on the blocks that cross the
+//     diagonal (or the end of the keys); blocks every query sees fully skip it.
+// V is converted once per call by a pre-pass into an f16 V^T copy [Hkv][128]
+// [keys] (exact for |v| in [2^-14, 65504]; f16 P keeps the output near 1e-4
+// rel-L2, where a bf16 P would sit at ~1e-3), so the main loop copies V^T
+// tiles straight into LDS.
 // Query blocks are dispatched heavy and light in complementary halves so the
 // two workgroups resident on a CU carry about the same number of key blocks.
 #include "common.h"
 
 #include <math.h>
+#include <mutex>
 
 namespace {
 
@@ -35,15 +44,19 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 128, kBQ = 128, kBKV = 64;
-constexpr int kKRow = kD + 8;     // bf16 per K row in LDS (272 B: b128 reads conflict-free)
-constexpr int kVRow = kBKV + 12;  // f16 per V^T row in LDS (152 B: b64 reads conflict-free)
+constexpr int kKRow = kD + 8;    // bf16 per K row in LDS (272 B: b128 reads conflict-free)
+constexpr int kVRow = kBKV + 8;  // f16 per V^T row in LDS (144 B: 16-byte rows, b64 reads conflict-free)
+constexpr float kLazy = 8.0f;    // the running max is raised only past m + 8 (P <= 2^8)
 
 struct PrefillArgs {
-    const uint16_t *q, *k, *v;
+    const uint16_t *q, *k;
+    const _Float16 *vt;  // f16 V^T [hkv][kD][kv_pad], keys >= kv_len zero
     void *out;
-    int hq, hkv, q_len, kv_len, kv_stride, start_pos, causal, out_bf16, nqb;
+    int hq, hkv, q_len, kv_len, kv_stride, kv_pad, start_pos, causal, out_bf16, nqb;
     float scale_log2;  // softmax scale * log2(e)
 };
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t bf16pair_to_f16pair(uint32_t w) {
     const float lo = __uint_as_float(w << 16), hi = __uint_as_float(w & 0xffff0000u);
@@ -55,6 +68,35 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     const uint32_t u = __float_as_uint(f);
     if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Pre-pass: V bf16 [hkv][kv_stride][128] -> f16 V^T [hkv][128][kv_pad] (keys
+// past kv_len zero); one workgroup per 64 keys of one KV head, transposed
+// through LDS.
+__global__ __launch_bounds__(256) void v_to_f16t_kernel(const uint16_t *__restrict__ v, _Float16 *__restrict__ vt,
+                                                        int kv_len, int kv_stride, int kv_pad) {
+    __shared__ _Float16 tile[kBKV][kD + 2];  // [key][dim], odd dword stride
+    const int kvh = blockIdx.y, key0 = blockIdx.x * kBKV, tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int gi = tid + 256 * i, kl = gi >> 4, d0 = (gi & 15) * 8;
+        u32x4 w = {0, 0, 0, 0};
+        if (key0 + kl < kv_len)
+            w = *reinterpret_cast<const u32x4 *>(v + ((size_t)kvh * kv_stride + key0 + kl) * kD + d0);
+        const uint32_t p[4] = {bf16pair_to_f16pair(w.x), bf16pair_to_f16pair(w.y), bf16pair_to_f16pair(w.z),
+                               bf16pair_to_f16pair(w.w)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) *reinterpret_cast<uint32_t *>(&tile[kl][d0 + 2 * e]) = p[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int gi = tid + 256 * i, d = gi >> 3, k0 = (gi & 7) * 8;
+        half8 r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = tile[k0 + j][d];
+        *reinterpret_cast<half8 *>(vt + ((size_t)kvh * kD + d) * kv_pad + key0 + k0) = r;
+    }
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(PrefillArgs a) {
@@ -88,10 +130,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int limit = qi < a.q_len ? (a.causal ? min(a.kv_len, a.start_pos + qi + 1) : a.kv_len) : kv_end;
 
     const uint16_t *kbase = a.k + (size_t)kvh * a.kv_stride * kD;
-    const uint16_t *vbase = a.v + (size_t)kvh * a.kv_stride * kD;
+    const _Float16 *vtbase = a.vt + (size_t)kvh * kD * a.kv_pad;
     // K staging: granule gi = tid + 256 i -> key gi >> 4, column (gi & 15) * 8
-    // V staging: keys 4 (tid >> 4) .. + 3, dims 8 (tid & 15) .. + 7
-    const int vkg = tid >> 4, vdg = tid & 15;
+    // V^T staging: dim tid >> 1, keys 32 (tid & 1) + 8 i .. + 7 of the block
+    const int vd = tid >> 1, vh = tid & 1;
     u32x4 rk[4], rv[4];
 #define DOE_PF_LOAD(KB)                                                                              \
     do {                                                                                             \
@@ -99,8 +141,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int gi = tid + 256 * i;                                                            \
             const int key = min((KB) * kBKV + (gi >> 4), a.kv_len - 1);                              \
             rk[i] = *reinterpret_cast<const u32x4 *>(kbase + (size_t)key * kD + (gi & 15) * 8);      \
-            const int vkey = min((KB) * kBKV + 4 * vkg + i, a.kv_len - 1);                           \
-            rv[i] = *reinterpret_cast<const u32x4 *>(vbase + (size_t)vkey * kD + 8 * vdg);           \
+            rv[i] = *reinterpret_cast<const u32x4 *>(vtbase + (size_t)vd * a.kv_pad + (KB) * kBKV + 32 * vh + 8 * i); \
         }                                                                                            \
     } while (0)
 #define DOE_PF_STORE(BUF)                                                                            \
@@ -108,23 +149,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                              \
             const int gi = tid + 256 * i;                                                            \
             *reinterpret_cast<u32x4 *>(&Ks[BUF][(gi >> 4) * kKRow + (gi & 15) * 8]) = rk[i];         \
-        }                                                                                            \
-        /* f16 pairs (d 2e, d 2e+1) of each of the 4 keys, then transpose to V^T rows */            \
-        uint32_t hv[4][4];                                                                           \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                              \
-            hv[i][0] = bf16pair_to_f16pair(rv[i].x);                                                 \
-            hv[i][1] = bf16pair_to_f16pair(rv[i].y);                                                 \
-            hv[i][2] = bf16pair_to_f16pair(rv[i].z);                                                 \
-            hv[i][3] = bf16pair_to_f16pair(rv[i].w);                                                 \
-        }                                                                                            \
-        _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                              \
-            /* dims 2e (low halves) and 2e+1 (high halves) over keys 0..3 */                         \
-            const u32x2 lo = {__builtin_amdgcn_perm(hv[1][e], hv[0][e], 0x05040100u),                \
-                              __builtin_amdgcn_perm(hv[3][e], hv[2][e], 0x05040100u)};               \
-            const u32x2 hi = {__builtin_amdgcn_perm(hv[1][e], hv[0][e], 0x07060302u),                \
-                              __builtin_amdgcn_perm(hv[3][e], hv[2][e], 0x07060302u)};               \
-            *reinterpret_cast<u32x2 *>(&Vt[BUF][(8 * vdg + 2 * e) * kVRow + 4 * vkg]) = lo;          \
-            *reinterpret_cast<u32x2 *>(&Vt[BUF][(8 * vdg + 2 * e + 1) * kVRow + 4 * vkg]) = hi;      \
+            *reinterpret_cast<u32x4 *>(&Vt[BUF][vd * kVRow + 32 * vh + 8 * i]) = rv[i];              \
         }                                                                                            \
     } while (0)
 
@@ -140,75 +165,143 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         DOE_PF_STORE(0);
     }
     __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
+    // blocks [0, nkb_full) hold only keys every query of the workgroup sees
+    const int vis_all = a.causal ? min(a.kv_len, a.start_pos + q0 + 1) : a.kv_len;
+    const int nkb_full = min(nkb, vis_all / kBKV);
+    const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+    auto step = [&](const int kb, const bool mask) __attribute__((always_inline)) {
         const int buf = kb & 1;
         if (kb + 1 < nkb) DOE_PF_LOAD(kb + 1);
-        // S^T for keys 64 kb + 32 kb2 + [0, 32): D[i] = key (i%4) + 8(i/4) + 4 lg, query lr
+        // S^T for keys 64 kb + 32 kb2 + [0, 32): D[i] = key (i%4) + 8(i/4) + 4 lg, query lr.
+        // The K fragments of half kb2 + 1 are read under half kb2's MFMAs, and
+        // the max over half 0 runs under half 1's MFMAs.
         float16v st[2];
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) st[kb2][r] = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const bf16x8 kf = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const u32x4 *>(&Ks[buf][(32 * kb2 + lr) * kKRow + 16 * s + 8 * lg]));
-                st[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[kb2], 0, 0, 0);
-            }
-        }
-        // online softmax (base 2), one query per lane column
-        float bmax = -INFINITY;
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kb * kBKV + 32 * kb2 + (r & 3) + 8 * (r >> 2) + 4 * lg;
-                const float x = key < limit ? st[kb2][r] * a.scale_log2 : -INFINITY;
-                st[kb2][r] = x;
-                bmax = fmaxf(bmax, x);
+            for (int r = 0; r < 16; ++r) st[kb2][r] = 0.0f;
+        bf16x8 kf[2][8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            kf[0][s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&Ks[buf][lr * kKRow + 16 * s + 8 * lg]));
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            kf[1][s] = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const u32x4 *>(&Ks[buf][(32 + lr) * kKRow + 16 * s + 8 * lg]));
+            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0][s], qf[s], st[0], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1][s], qf[s], st[1], 0, 0, 0);
+        // block max of the raw scores (the scale is positive: max commutes with it)
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            if (mask) {
+                const int key = kb * kBKV + (r & 3) + 8 * (r >> 2) + 4 * lg;
+                if (key >= limit) st[0][r] = -INFINITY;
             }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-        const float m_new = fmaxf(m_i, bmax);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
-        m_i = m_new;
-        float psum = 0.0f;
+            bmax = fmaxf(bmax, st[0][r]);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (mask) __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            else __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            if (mask) {
+                const int key = kb * kBKV + 32 + (r & 3) + 8 * (r >> 2) + 4 * lg;
+                if (key >= limit) st[1][r] = -INFINITY;
+            }
+            bmax = fmaxf(bmax, st[1][r]);
+        }
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bmax), __float_as_uint(bmax), false, false);
+            bmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // the lane's own value and its partner's
+        }
+        const float mb = bmax * a.scale_log2;
+        if (__builtin_amdgcn_ballot_w64(mb > m_i + kLazy) != 0) {  // wave-uniform
+            const float m_new = fmaxf(m_i, mb);
+            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_i - m_new);
+            m_i = m_new;
+            l_i *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+        }
+        const float nm = m_i == -INFINITY ? 0.0f : -m_i;
+        // P slice by slice; slice s4 + 1's exp / convert runs under slice s4's
+        // four PV MFMAs.  O^T[d][q] += V^T[d][keys] . P^T[keys][q]; slot 8 lg + j
+        // of slice s4 is key 32 (s4/2) + 16 (s4%2) + 4 lg + (j%4) + 8 (j/4) --
+        // the D layout of S^T.
         half8 pf[4];
+        float psum = 0.0f;
+        auto p_slice = [&](const int s4) __attribute__((always_inline)) {
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float p = __builtin_amdgcn_exp2f(st[s4 >> 1][8 * (s4 & 1) + j] - m_use);
-                psum += p;
-                pf[s4][j] = (_Float16)p;
+            for (int j = 0; j < 8; j += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(st[s4 >> 1][8 * (s4 & 1) + j], a.scale_log2, nm));
+                const float p1 = __builtin_amdgcn_exp2f(fmaf(st[s4 >> 1][8 * (s4 & 1) + j + 1], a.scale_log2, nm));
+                const half2v h = {(_Float16)p0, (_Float16)p1};
+                psum = __builtin_amdgcn_fdot2(h, ones, psum, false);
+                pf[s4][j] = h[0];
+                pf[s4][j + 1] = h[1];
             }
-        l_i = l_i * alpha + psum;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-        // O^T[d][q] += V^T[d][keys] . P^T[keys][q]; slot 8 lg + j of slice s4 is key
-        // 32 (s4/2) + 16 (s4%2) + 4 lg + (j%4) + 8 (j/4) -- the D layout of S^T
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
+        };
+        // V^T fragments of slice s4 (four 32-dim blocks), double-buffered
+        half8 vf[2][4];
+        auto read_v = [&](const int s4) __attribute__((always_inline)) {
             const int key0 = 32 * (s4 >> 1) + 16 * (s4 & 1) + 4 * lg;
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const _Float16 *vr = &Vt[buf][(32 * db + lr) * kVRow + key0];
                 const u32x2 v0 = *reinterpret_cast<const u32x2 *>(vr);
                 const u32x2 v1 = *reinterpret_cast<const u32x2 *>(vr + 8);
-                const half8 vf = __builtin_bit_cast(half8, u32x4{v0.x, v0.y, v1.x, v1.y});
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[s4], o[db], 0, 0, 0);
+                vf[s4 & 1][db] = __builtin_bit_cast(half8, u32x4{v0.x, v0.y, v1.x, v1.y});
             }
+        };
+        read_v(0);
+        p_slice(0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            if (s4 < 3) read_v(s4 + 1);
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[s4 & 1][db], pf[s4], o[db], 0, 0, 0);
+            if (s4 < 3) p_slice(s4 + 1);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (s4 < 3) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+        l_i += psum;
         if (kb + 1 < nkb) DOE_PF_STORE(buf ^ 1);
         __syncthreads();
-    }
+    };
+    int kb = 0;
+    for (; kb < nkb_full; ++kb) step(kb, false);
+    for (; kb < nkb; ++kb) step(kb, true);
 #undef DOE_PF_LOAD
 #undef DOE_PF_STORE
 
     if (qi >= a.q_len) return;
-    const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
+    const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_i), __float_as_uint(l_i), false, false);
+    const float l_tot = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     const size_t obase = ((size_t)qi * a.hq + h) * kD;
 #pragma unroll
@@ -227,6 +320,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
         }
 }
+
+// Library-owned workspace (grow-only) for the f16 V^T copy.
+std::mutex g_ws_mu;
+void *g_ws = nullptr;
+size_t g_ws_bytes = 0;
 
 }  // namespace
 
@@ -257,7 +355,6 @@ int doe_attn_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, vo
     PrefillArgs a;
     a.q = q;
     a.k = k;
-    a.v = v;
     a.out = out;
     a.hq = (int)num_heads;
     a.hkv = (int)num_kv_heads;
@@ -278,6 +375,25 @@ int doe_attn_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, vo
     }
     const int64_t blocks = (int64_t)a.nqb * a.hq;
     DOE_REQUIRE(blocks <= 0x7fffffff, DOE_E_UNSUPPORTED, "too many blocks");
+    const int64_t nkb_all = (kv_len + kBKV - 1) / kBKV;
+    a.kv_pad = (int)(nkb_all * kBKV);
+    const size_t need = (size_t)num_kv_heads * kD * (size_t)a.kv_pad * sizeof(_Float16);
+    _Float16 *vt;
+    {
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        if (g_ws_bytes < need) {
+            if (g_ws) DOE_HIP_CHECK(hipFree(g_ws));
+            g_ws = nullptr;
+            g_ws_bytes = 0;
+            DOE_HIP_CHECK(hipMalloc(&g_ws, need));
+            g_ws_bytes = need;
+        }
+        vt = (_Float16 *)g_ws;
+    }
+    a.vt = vt;
+    hipLaunchKernelGGL(v_to_f16t_kernel, dim3((unsigned)nkb_all, (unsigned)num_kv_heads), dim3(256), 0, st, v, vt,
+                       a.kv_len, a.kv_stride, a.kv_pad);
+    DOE_LAUNCH_CHECK("v_to_f16t_kernel");
     hipLaunchKernelGGL(attn_prefill_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
     DOE_LAUNCH_CHECK("attn_prefill_kernel");
     return DOE_OK;
