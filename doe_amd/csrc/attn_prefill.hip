@@ -134,24 +134,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // K staging: granule gi = tid + 256 i -> key gi >> 4, column (gi & 15) * 8
     // V^T staging: dim tid >> 1, keys 32 (tid & 1) + 8 i .. + 7 of the block
     const int vd = tid >> 1, vh = tid & 1;
+    // K runs one block ahead of V: in iteration kb, Ks[(kb + 1) & 1] holds
+    // K(kb + 1) (the next block's scores are computed under this block's
+    // softmax) and Vt[kb & 1] holds V(kb); K(kb + 2) and V(kb + 1) are loaded
+    // during the iteration and written to the buffers freed by the previous
+    // iteration's barrier.  Out-of-range block indices are clamped: their
+    // loads read valid memory and their results are never used.
     u32x4 rk[4], rv[4];
-#define DOE_PF_LOAD(KB)                                                                              \
-    do {                                                                                             \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                              \
-            const int gi = tid + 256 * i;                                                            \
-            const int key = min((KB) * kBKV + (gi >> 4), a.kv_len - 1);                              \
-            rk[i] = *reinterpret_cast<const u32x4 *>(kbase + (size_t)key * kD + (gi & 15) * 8);      \
-            rv[i] = *reinterpret_cast<const u32x4 *>(vtbase + (size_t)vd * a.kv_pad + (KB) * kBKV + 32 * vh + 8 * i); \
-        }                                                                                            \
-    } while (0)
-#define DOE_PF_STORE(BUF)                                                                            \
-    do {                                                                                             \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                              \
-            const int gi = tid + 256 * i;                                                            \
-            *reinterpret_cast<u32x4 *>(&Ks[BUF][(gi >> 4) * kKRow + (gi & 15) * 8]) = rk[i];         \
-            *reinterpret_cast<u32x4 *>(&Vt[BUF][vd * kVRow + 32 * vh + 8 * i]) = rv[i];              \
-        }                                                                                            \
-    } while (0)
+#define DOE_PF_LOAD_K(KB)                                                                            \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                                  \
+        const int gi = tid + 256 * i;                                                                \
+        const int key = min((KB) * kBKV + (gi >> 4), a.kv_len - 1);                                  \
+        rk[i] = *reinterpret_cast<const u32x4 *>(kbase + (size_t)key * kD + (gi & 15) * 8);          \
+    }
+#define DOE_PF_LOAD_V(KB)                                                                            \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) rv[i] =                                            \
+        *reinterpret_cast<const u32x4 *>(vtbase + (size_t)vd * a.kv_pad + (KB) * kBKV + 32 * vh + 8 * i)
+#define DOE_PF_STORE_K(BUF)                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                                  \
+        const int gi = tid + 256 * i;                                                                \
+        *reinterpret_cast<u32x4 *>(&Ks[BUF][(gi >> 4) * kKRow + (gi & 15) * 8]) = rk[i];             \
+    }
+#define DOE_PF_STORE_V(BUF)                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4 *>(&Vt[BUF][vd * kVRow + 32 * vh + 8 * i]) = rv[i]
 
     float16v o[4];
 #pragma unroll
@@ -159,76 +164,64 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
     float m_i = -INFINITY, l_i = 0.0f;
-
-    if (nkb > 0) {
-        DOE_PF_LOAD(0);
-        DOE_PF_STORE(0);
-    }
-    __syncthreads();
+    if (nkb == 0) {
+        // no visible keys (only for rows past q_len): nothing to accumulate
+    } else {
     // blocks [0, nkb_full) hold only keys every query of the workgroup sees
     const int vis_all = a.causal ? min(a.kv_len, a.start_pos + q0 + 1) : a.kv_len;
     const int nkb_full = min(nkb, vis_all / kBKV);
     const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
-    auto step = [&](const int kb, const bool mask) __attribute__((always_inline)) {
-        const int buf = kb & 1;
-        if (kb + 1 < nkb) DOE_PF_LOAD(kb + 1);
-        // S^T for keys 64 kb + 32 kb2 + [0, 32): D[i] = key (i%4) + 8(i/4) + 4 lg, query lr.
-        // The K fragments of half kb2 + 1 are read under half kb2's MFMAs, and
-        // the max over half 0 runs under half 1's MFMAs.
-        float16v st[2];
+
+    // S^T of the block in Ks[buf]: D[i] = key (i%4) + 8(i/4) + 4 lg of half kb2, query lr
+    auto s_mfmas = [&](float16v (&st)[2], const int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) st[kb2][r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const bf16x8 kf = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4 *>(&Ks[buf][(32 * kb2 + lr) * kKRow + 16 * s + 8 * lg]));
+                st[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[kb2], 0, 0, 0);
+            }
+        }
+    };
+    // masks block kbb's scores (keys >= limit -> -inf) and returns their raw max
+    // over the query's two lane halves (the scale is positive: max commutes)
+    auto block_max = [&](float16v (&st)[2], const int kbb, const bool mask) __attribute__((always_inline)) {
+        float bmax = -INFINITY;
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) st[kb2][r] = 0.0f;
-        bf16x8 kf[2][8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s)
-            kf[0][s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&Ks[buf][lr * kKRow + 16 * s + 8 * lg]));
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            kf[1][s] = __builtin_bit_cast(
-                bf16x8, *reinterpret_cast<const u32x4 *>(&Ks[buf][(32 + lr) * kKRow + 16 * s + 8 * lg]));
-            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0][s], qf[s], st[0], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1][s], qf[s], st[1], 0, 0, 0);
-        // block max of the raw scores (the scale is positive: max commutes with it)
-        float bmax = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            if (mask) {
-                const int key = kb * kBKV + (r & 3) + 8 * (r >> 2) + 4 * lg;
-                if (key >= limit) st[0][r] = -INFINITY;
+            for (int r = 0; r < 16; ++r) {
+                if (mask) {
+                    const int key = kbb * kBKV + 32 * kb2 + (r & 3) + 8 * (r >> 2) + 4 * lg;
+                    if (key >= limit) st[kb2][r] = -INFINITY;
+                }
+                bmax = fmaxf(bmax, st[kb2][r]);
             }
-            bmax = fmaxf(bmax, st[0][r]);
-        }
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (mask) __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-            else __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            if (mask) {
-                const int key = kb * kBKV + 32 + (r & 3) + 8 * (r >> 2) + 4 * lg;
-                if (key >= limit) st[1][r] = -INFINITY;
-            }
-            bmax = fmaxf(bmax, st[1][r]);
-        }
-        {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bmax), __float_as_uint(bmax), false, false);
-            bmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // the lane's own value and its partner's
-        }
-        const float mb = bmax * a.scale_log2;
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bmax), __float_as_uint(bmax), false, false);
+        return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    };
+
+    DOE_PF_LOAD_K(0);
+    DOE_PF_LOAD_V(0);
+    DOE_PF_STORE_K(0);
+    DOE_PF_STORE_V(0);
+    DOE_PF_LOAD_K(min(1, nkb - 1));
+    DOE_PF_STORE_K(1);
+    __syncthreads();
+    float16v sc[2];
+    s_mfmas(sc, 0);
+    float bmax_c = block_max(sc, 0, nkb_full == 0);
+    __syncthreads();  // every wave has read K(0) before iteration 0 overwrites Ks[0]
+
+    auto iter = [&](const int kb, const bool mask_next) __attribute__((always_inline)) {
+        const int vb = kb & 1, kn = (kb + 1) & 1;
+        DOE_PF_LOAD_K(min(kb + 2, nkb - 1));
+        DOE_PF_LOAD_V(min(kb + 1, nkb - 1));
+        // running max for block kb (raised only past m + 8: P <= 2^8)
+        const float mb = bmax_c * a.scale_log2;
         if (__builtin_amdgcn_ballot_w64(mb > m_i + kLazy) != 0) {  // wave-uniform
             const float m_new = fmaxf(m_i, mb);
             const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_i - m_new);
@@ -240,64 +233,105 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
         }
         const float nm = m_i == -INFINITY ? 0.0f : -m_i;
-        // P slice by slice; slice s4 + 1's exp / convert runs under slice s4's
-        // four PV MFMAs.  O^T[d][q] += V^T[d][keys] . P^T[keys][q]; slot 8 lg + j
-        // of slice s4 is key 32 (s4/2) + 16 (s4%2) + 4 lg + (j%4) + 8 (j/4) --
-        // the D layout of S^T.
+        // The next block's scores under this block's softmax: MFMA i of S^T
+        // (half i % 2, dims 16 (i / 2)) with the K fragment read four MFMAs
+        // ahead and score pair i of this block turned into f16 P.  Each step is
+        // its own scheduling region, so the exp2s stay between the MFMAs.
+        float16v sn[2];
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sn[kb2][r] = 0.0f;
+        auto kfrag = [&](const int i) __attribute__((always_inline)) {
+            return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
+                                                  &Ks[kn][(32 * (i & 1) + lr) * kKRow + 16 * (i >> 1) + 8 * lg]));
+        };
+        constexpr int kAhead = 4;  // fragment reads this many MFMAs ahead of their use
+        bf16x8 kf[kAhead + 1];
+#pragma unroll
+        for (int i = 0; i < kAhead; ++i) kf[i] = kfrag(i);
         half8 pf[4];
         float psum = 0.0f;
-        auto p_slice = [&](const int s4) __attribute__((always_inline)) {
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(fmaf(st[s4 >> 1][8 * (s4 & 1) + j], a.scale_log2, nm));
-                const float p1 = __builtin_amdgcn_exp2f(fmaf(st[s4 >> 1][8 * (s4 & 1) + j + 1], a.scale_log2, nm));
-                const half2v h = {(_Float16)p0, (_Float16)p1};
-                psum = __builtin_amdgcn_fdot2(h, ones, psum, false);
-                pf[s4][j] = h[0];
-                pf[s4][j + 1] = h[1];
-            }
+        // score pair i: slice i / 4, slots 2 (i % 4), 2 (i % 4) + 1.  Its exp2s
+        // are issued in step i and converted / summed in step i + 1, so no
+        // instruction waits on a just-issued transcendental (the wave issues
+        // in order: such a wait would hold back the next MFMA).
+        float pp0 = 0.0f, pp1 = 0.0f;
+        auto finish_pair = [&](const int i) __attribute__((always_inline)) {
+            const int s4 = i >> 2, j = 2 * (i & 3);
+            const half2v h = {(_Float16)pp0, (_Float16)pp1};
+            psum = __builtin_amdgcn_fdot2(h, ones, psum, false);
+            pf[s4][j] = h[0];
+            pf[s4][j + 1] = h[1];
         };
-        // V^T fragments of slice s4 (four 32-dim blocks), double-buffered
-        half8 vf[2][4];
-        auto read_v = [&](const int s4) __attribute__((always_inline)) {
-            const int key0 = 32 * (s4 >> 1) + 16 * (s4 & 1) + 4 * lg;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const _Float16 *vr = &Vt[buf][(32 * db + lr) * kVRow + key0];
-                const u32x2 v0 = *reinterpret_cast<const u32x2 *>(vr);
-                const u32x2 v1 = *reinterpret_cast<const u32x2 *>(vr + 8);
-                vf[s4 & 1][db] = __builtin_bit_cast(half8, u32x4{v0.x, v0.y, v1.x, v1.y});
-            }
-        };
-        read_v(0);
-        p_slice(0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-            if (s4 < 3) read_v(s4 + 1);
+        for (int i = 0; i < 16; ++i) {
+            sn[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i % (kAhead + 1)], qf[i >> 1], sn[i & 1], 0, 0, 0);
+            if (i + kAhead < 16) kf[(i + kAhead) % (kAhead + 1)] = kfrag(i + kAhead);
+            const int s4 = i >> 2, j = 2 * (i & 3);
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[s4 >> 1][8 * (s4 & 1) + j], a.scale_log2, nm));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[s4 >> 1][8 * (s4 & 1) + j + 1], a.scale_log2, nm));
+            if (i > 0) finish_pair(i - 1);
+            pp0 = p0;
+            pp1 = p1;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        finish_pair(15);
+        l_i += psum;
+        // O^T[d][q] += V^T[d][keys] . P^T[keys][q] (slot 8 lg + j of slice s4 is key
+        // 32 (s4/2) + 16 (s4%2) + 4 lg + (j%4) + 8 (j/4) -- the D layout of S^T),
+        // MFMA i = (slice i / 4, dims 32 (i % 4)) with its V^T fragment read four
+        // MFMAs ahead, under the next block's mask and max.
+        auto vfrag = [&](const int i) __attribute__((always_inline)) {
+            const int s4 = i >> 2, db = i & 3;
+            const _Float16 *vr = &Vt[vb][(32 * db + lr) * kVRow + 32 * (s4 >> 1) + 16 * (s4 & 1) + 4 * lg];
+            const u32x2 v0 = *reinterpret_cast<const u32x2 *>(vr);
+            const u32x2 v1 = *reinterpret_cast<const u32x2 *>(vr + 8);
+            return __builtin_bit_cast(half8, u32x4{v0.x, v0.y, v1.x, v1.y});
+        };
+        half8 vf[kAhead + 1];
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[s4 & 1][db], pf[s4], o[db], 0, 0, 0);
-            if (s4 < 3) p_slice(s4 + 1);
+        for (int i = 0; i < kAhead; ++i) vf[i] = vfrag(i);
+        float bm[2] = {-INFINITY, -INFINITY};  // two independent chains
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (s4 < 3) {
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+        for (int i = 0; i < 16; ++i) {
+            o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i % (kAhead + 1)], pf[i >> 2], o[i & 3], 0, 0, 0);
+            if (i + kAhead < 16) vf[(i + kAhead) % (kAhead + 1)] = vfrag(i + kAhead);
+            // scores 2i, 2i + 1 of the next block: half i / 8, slots 2 (i % 8), + 1
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int kb2 = i >> 3, r = 2 * (i & 7) + e;
+                if (mask_next) {
+                    const int key = (kb + 1) * kBKV + 32 * kb2 + (r & 3) + 8 * (r >> 2) + 4 * lg;
+                    if (key >= limit) sn[kb2][r] = -INFINITY;
                 }
+                bm[e] = fmaxf(bm[e], sn[kb2][r]);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        l_i += psum;
-        if (kb + 1 < nkb) DOE_PF_STORE(buf ^ 1);
+        float bmax_n;
+        {
+            const float bmm = fmaxf(bm[0], bm[1]);
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bmm), __float_as_uint(bmm), false, false);
+            bmax_n = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        DOE_PF_STORE_K(vb);  // K(kb + 2): K(kb) was read before the previous barrier
+        DOE_PF_STORE_V(kn);  // V(kb + 1): V(kb - 1) likewise
         __syncthreads();
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2) sc[kb2] = sn[kb2];
+        bmax_c = bmax_n;
     };
     int kb = 0;
-    for (; kb < nkb_full; ++kb) step(kb, false);
-    for (; kb < nkb; ++kb) step(kb, true);
-#undef DOE_PF_LOAD
-#undef DOE_PF_STORE
+    for (; kb + 1 < nkb_full; ++kb) iter(kb, false);  // the next block needs no mask
+    for (; kb < nkb; ++kb) iter(kb, true);
+    }
+#undef DOE_PF_LOAD_K
+#undef DOE_PF_LOAD_V
+#undef DOE_PF_STORE_K
+#undef DOE_PF_STORE_V
 
     if (qi >= a.q_len) return;
     const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_i), __float_as_uint(l_i), false, false);
