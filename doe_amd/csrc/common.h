@@ -24,6 +24,7 @@ int require_init();
 // Tuning hooks of individual kernels (0 = automatic).
 int attn_set_splits(int value);
 int attn_set_waves(int value);
+int int4_set_kernel(int value);
 
 }  // namespace doe
 
