@@ -129,27 +129,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // keys this lane's query may see: [0, limit)
     const int limit = qi < a.q_len ? (a.causal ? min(a.kv_len, a.start_pos + qi + 1) : a.kv_len) : kv_end;
 
-    const uint16_t *kbase = a.k + (size_t)kvh * a.kv_stride * kD;
-    const _Float16 *vtbase = a.vt + (size_t)kvh * kD * a.kv_pad;
+    // K and V^T of this KV head as buffers: per-lane offsets fixed for the whole
+    // loop, the block offset a scalar; keys past kv_len read as zero (masked)
+    const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.k + (size_t)kvh * a.kv_stride * kD), (short)0, a.kv_len * (kD * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.vt + (size_t)kvh * kD * a.kv_pad), (short)0, a.kv_pad * (kD * 2), 0x00020000);
     // K staging: granule gi = tid + 256 i -> key gi >> 4, column (gi & 15) * 8
     // V^T staging: dim tid >> 1, keys 32 (tid & 1) + 8 i .. + 7 of the block
     const int vd = tid >> 1, vh = tid & 1;
+    const uint32_t k_voff = (uint32_t)((tid >> 4) * kD + (tid & 15) * 8) * 2u;  // + 16 keys per i
+    const uint32_t v_voff = (uint32_t)(vd * a.kv_pad + 32 * vh) * 2u;           // + 8 keys per i
     // K runs one block ahead of V: in iteration kb, Ks[(kb + 1) & 1] holds
     // K(kb + 1) (the next block's scores are computed under this block's
     // softmax) and Vt[kb & 1] holds V(kb); K(kb + 2) and V(kb + 1) are loaded
     // during the iteration and written to the buffers freed by the previous
     // iteration's barrier.  Out-of-range block indices are clamped: their
-    // loads read valid memory and their results are never used.
+    // loads stay inside the buffers and their results are never used.
     u32x4 rk[4], rv[4];
 #define DOE_PF_LOAD_K(KB)                                                                            \
-    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                                  \
-        const int gi = tid + 256 * i;                                                                \
-        const int key = min((KB) * kBKV + (gi >> 4), a.kv_len - 1);                                  \
-        rk[i] = *reinterpret_cast<const u32x4 *>(kbase + (size_t)key * kD + (gi & 15) * 8);          \
-    }
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) rk[i] = __builtin_amdgcn_raw_buffer_load_b128(     \
+        krsrc, k_voff + (uint32_t)i * (16 * kD * 2), (KB) * (kBKV * kD * 2), 0)
 #define DOE_PF_LOAD_V(KB)                                                                            \
-    _Pragma("unroll") for (int i = 0; i < 4; ++i) rv[i] =                                            \
-        *reinterpret_cast<const u32x4 *>(vtbase + (size_t)vd * a.kv_pad + (KB) * kBKV + 32 * vh + 8 * i)
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) rv[i] = __builtin_amdgcn_raw_buffer_load_b128(     \
+        vrsrc, v_voff + (uint32_t)i * 16u, (KB) * (kBKV * 2), 0)
 #define DOE_PF_STORE_K(BUF)                                                                          \
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                                  \
         const int gi = tid + 256 * i;                                                                \
@@ -216,7 +219,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float bmax_c = block_max(sc, 0, nkb_full == 0);
     __syncthreads();  // every wave has read K(0) before iteration 0 overwrites Ks[0]
 
-    auto iter = [&](const int kb, const bool mask_next) __attribute__((always_inline)) {
+    // iteration kb: sc holds block kb's scores, sn receives block kb + 1's
+    auto iter = [&](const int kb, const bool mask_next, float16v(&sc)[2], float16v(&sn)[2]) __attribute__((always_inline)) {
         const int vb = kb & 1, kn = (kb + 1) & 1;
         DOE_PF_LOAD_K(min(kb + 2, nkb - 1));
         DOE_PF_LOAD_V(min(kb + 1, nkb - 1));
@@ -237,7 +241,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // (half i % 2, dims 16 (i / 2)) with the K fragment read four MFMAs
         // ahead and score pair i of this block turned into f16 P.  Each step is
         // its own scheduling region, so the exp2s stay between the MFMAs.
-        float16v sn[2];
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
@@ -320,13 +323,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         DOE_PF_STORE_K(vb);  // K(kb + 2): K(kb) was read before the previous barrier
         DOE_PF_STORE_V(kn);  // V(kb + 1): V(kb - 1) likewise
         __syncthreads();
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2) sc[kb2] = sn[kb2];
         bmax_c = bmax_n;
     };
+    float16v sn[2];
     int kb = 0;
-    for (; kb + 1 < nkb_full; ++kb) iter(kb, false);  // the next block needs no mask
-    for (; kb < nkb; ++kb) iter(kb, true);
+    for (; kb + 2 < nkb_full; kb += 2) {  // two iterations whose next blocks need no mask
+        iter(kb, false, sc, sn);
+        iter(kb + 1, false, sn, sc);
+    }
+    for (; kb < nkb; ++kb) {  // the rest (a mask on blocks every query sees is a no-op)
+        iter(kb, true, sc, sn);
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2) sc[kb2] = sn[kb2];
+    }
     }
 #undef DOE_PF_LOAD_K
 #undef DOE_PF_LOAD_V
@@ -379,7 +388,7 @@ int doe_attn_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, vo
                 (long long)head_dim);
     DOE_REQUIRE(kv_stride >= kv_len, DOE_E_INVALID, "kv_stride %lld < kv_len %lld", (long long)kv_stride,
                 (long long)kv_len);
-    DOE_REQUIRE(num_heads <= 4096 && q_len <= (1 << 24) && kv_stride <= (1 << 24) &&
+    DOE_REQUIRE(num_heads <= 4096 && q_len <= (1 << 24) && kv_stride <= (1 << 24) && kv_len <= (1 << 22) &&
                     num_kv_heads * kv_stride * kD <= ((int64_t)1 << 40),
                 DOE_E_UNSUPPORTED, "prefill attention shape too large");
     if (q_len == 0) return DOE_OK;

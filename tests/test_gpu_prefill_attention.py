@@ -7,7 +7,7 @@ import math
 import numpy as np
 import pytest
 
-from doe_amd import DeviceBuffer, _lib, ops
+from doe_amd import DeviceBuffer, Graph, Stream, _lib, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -99,6 +99,67 @@ def test_prefill_config_rows(dev, ora):
         err = rel_l2(got[r0:r1], want[r0:r1])
         print(f"[prefill config] rows {r0}:{r1} rel_l2 {err:.2e}", flush=True)
         assert err <= TOL
+
+
+@pytest.mark.parametrize("hq,hkv,s", [(4, 2, 1000), (2, 1, 640), (3, 3, 1500)])
+def test_prefill_long_prompts(dev, ora, hq, hkv, s):
+    # longer causal prompts checked per 128-query block (even and odd block
+    # counts, a ragged last block)
+    rng = np.random.default_rng(s + hq)
+    q = to_bf16(rng.standard_normal((s, hq, D), dtype=np.float32))
+    k = to_bf16(rng.standard_normal((hkv, s, D), dtype=np.float32))
+    v = to_bf16(rng.standard_normal((hkv, s, D), dtype=np.float32))
+    scale = 1.0 / math.sqrt(D)
+    got = run(q, k, v, hq, hkv, s, s, s, 0, scale, True)
+    want = oracle(ora, q, k, v, hq, hkv, s, s, s, 0, scale, True)
+    err = rel_l2(got, want)
+    print(f"[prefill {hq}/{hkv} S={s}] rel_l2 {err:.2e}", flush=True)
+    assert err <= TOL
+    for r0 in range(0, s, 128):
+        assert rel_l2(got[r0:r0 + 128], want[r0:r0 + 128]) <= TOL, r0
+
+
+def test_prefill_more_workgroups_than_slots(dev, ora):
+    # 64 heads x 16 query blocks = 1024 workgroups, twice what the CUs hold at once
+    rng = np.random.default_rng(11)
+    hq, hkv, s = 64, 8, 2048
+    q = to_bf16(rng.standard_normal((s, hq, D), dtype=np.float32))
+    k = to_bf16(rng.standard_normal((hkv, s, D), dtype=np.float32))
+    v = to_bf16(rng.standard_normal((hkv, s, D), dtype=np.float32))
+    scale = 1.0 / math.sqrt(D)
+    got = run(q, k, v, hq, hkv, s, s, s, 0, scale, True)
+    assert np.isfinite(got).all()
+    for r0, r1 in ((0, 8), (1020, 1030), (1900, 1910), (2040, 2048)):
+        want = oracle(ora, q, k, v, hq, hkv, s, s, s, 0, scale, True, rows=(r0, r1))
+        assert rel_l2(got[r0:r1], want[r0:r1]) <= TOL, (r0, r1)
+
+
+def test_prefill_graph_replays(dev):
+    # replays of one captured call (the V^T pre-pass and the attention kernel),
+    # with eager calls in between, all reproduce the eager result exactly
+    rng = np.random.default_rng(12)
+    hq, hkv, s = 8, 2, 1024
+    q = up(to_bf16(rng.standard_normal((s, hq, D), dtype=np.float32)))
+    k = up(to_bf16(rng.standard_normal((hkv, s, D), dtype=np.float32)))
+    v = up(to_bf16(rng.standard_normal((hkv, s, D), dtype=np.float32)))
+    out = DeviceBuffer.empty((s, hq, D), np.float32)
+
+    def call(stream=None):
+        ops.attention_prefill(q, k, v, out, num_heads=hq, num_kv_heads=hkv, head_dim=D, q_len=s, kv_len=s,
+                              kv_stride=s, start_pos=0, scale=0.125, causal=True, stream=stream)
+
+    call()
+    want = out.download().copy()
+    st = Stream()
+    g = Graph.capture(st, lambda: call(st))
+    for i in range(4):
+        out.upload(np.zeros((s, hq, D), np.float32))
+        g.launch(st)
+        st.synchronize()
+        np.testing.assert_array_equal(out.download(), want, err_msg=f"replay {i}")
+        call()
+    g.destroy()
+    st.destroy()
 
 
 def test_prefill_softmax_invariants(dev):
