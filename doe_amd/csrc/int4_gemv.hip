@@ -21,7 +21,7 @@
 // per batch row and the hi + lo sum (one cross-half lane swap) come at the
 // end.
 //
-// A pre-pass (one workgroup per batch row) finds the row's max |x| and writes
+// A pre-pass (one workgroup per batch row and 64 groups) finds the row's max |x| and writes
 // the image ([group][64 lanes][8 f16], 1 KB per group), the corrections
 // ([group][16] f32) and the row's scale exponent.  A workgroup of the GEMV
 // owns 64 rows (four 16-row tiles per wave, so an image fragment feeds four
@@ -43,9 +43,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxBatch = 8;
 
-// Pre-pass: workgroup b = batch row b (rows >= M write zeros); when the
-// GEMV splits K (atomic partial sums), it also clears y[b].
-constexpr int kImgThreads = 1024;
+// Pre-pass: workgroup (b, p) = batch row b (rows >= M write zeros), groups
+// [64 p, 64 p + 64); every part of a row finds the row's maximum itself (the
+// same exact value, so the same exponent).  When the GEMV splits K (atomic
+// partial sums), the parts also clear y[b].
+constexpr int kImgThreads = 256;
+constexpr int kImgGroups = 64;  // groups per workgroup: one item per thread
 __global__ __launch_bounds__(kImgThreads) void int4_x_image_kernel(const float *__restrict__ x,
                                                                    _Float16 *__restrict__ img,
                                                                    float *__restrict__ corr,
@@ -53,10 +56,13 @@ __global__ __launch_bounds__(kImgThreads) void int4_x_image_kernel(const float *
                                                                    float *__restrict__ y_clear,
                                                                    int M, int N, int K) {
     __shared__ float wmax[kImgThreads / 64];
-    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-    if (y_clear && b < M)
-        for (int i = tid; i < N; i += kImgThreads) y_clear[(size_t)b * N + i] = 0.0f;
+    const int b = blockIdx.x, part = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    if (y_clear && b < M) {
+        const int chunk = (N + (int)gridDim.y - 1) / (int)gridDim.y, i1 = min(N, (part + 1) * chunk);
+        for (int i = part * chunk + tid; i < i1; i += kImgThreads) y_clear[(size_t)b * N + i] = 0.0f;
+    }
     const int G = K / 32;
+    const int g0 = part * kImgGroups, g1 = min(G, g0 + kImgGroups);
     const bool live = b < M;
     const float *xr = x + (size_t)(live ? b : 0) * K;
     float amax = 0.0f;
@@ -76,10 +82,10 @@ __global__ __launch_bounds__(kImgThreads) void int4_x_image_kernel(const float *
         sig = 14 - __builtin_amdgcn_frexp_expf(amax);
         sig = sig < -120 ? -120 : (sig > 120 ? 120 : sig);
     }
-    if (tid == 0) sig_out[b] = sig;
+    if (tid == 0 && part == 0) sig_out[b] = sig;
     const float sc = __builtin_amdgcn_ldexpf(1.0f, sig);
     // item (g, kg): eight consecutive x, four items per group in one quad
-    for (int item = tid; item < G * 4; item += kImgThreads) {
+    for (int item = g0 * 4 + tid; item < g1 * 4; item += kImgThreads) {
         const int g = item >> 2, kg = item & 3;
         float v[8];
         if (live) {
@@ -422,7 +428,8 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     _Float16 *img = (_Float16 *)ws;
     float *corr = (float *)((char *)ws + img_bytes);
     int *sig = (int *)(corr + (size_t)G * 16);
-    hipLaunchKernelGGL(int4_x_image_kernel, dim3(kMaxBatch), dim3(kImgThreads), 0, st, x, img, corr, sig,
+    const int img_parts = G > 0 ? (G + kImgGroups - 1) / kImgGroups : 1;
+    hipLaunchKernelGGL(int4_x_image_kernel, dim3(kMaxBatch, (unsigned)img_parts), dim3(kImgThreads), 0, st, x, img, corr, sig,
                        splits > 1 ? y : nullptr, (int)m, (int)n, (int)k);
     DOE_LAUNCH_CHECK("int4_x_image_kernel");
     Int4Args a;
