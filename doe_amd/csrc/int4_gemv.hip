@@ -67,7 +67,8 @@ __global__ __launch_bounds__(kImgThreads) void int4_x_image_kernel(const float *
     const float *xr = x + (size_t)(live ? b : 0) * K;
     float amax = 0.0f;
     if (live)
-        for (int k4 = tid; k4 < K / 4; k4 += kImgThreads) {
+#pragma unroll 8
+        for (int k4 = tid; k4 < K / 4; k4 += kImgThreads) {  // eight loads in flight per thread
             const float4 v = reinterpret_cast<const float4 *>(xr)[k4];
             amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
