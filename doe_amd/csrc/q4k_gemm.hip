@@ -70,8 +70,23 @@ __global__ __launch_bounds__(256) void a_rows_to_f16_kernel(const uint16_t *__re
                                                             int *__restrict__ sig, int K, int Kp) {
     const int m = blockIdx.x;
     const uint16_t *row = a + (size_t)m * K;
+    _Float16 *out = a16 + (size_t)m * Kp;
+    // 16-byte granules of eight elements when the row allows (K % 8 == 0 and an
+    // aligned base), several loads in flight per thread; else element by element
+    const bool vec = (K & 7) == 0 && ((uintptr_t)row & 15) == 0;
+    const int ng = K >> 3;
     float amax = 0.0f;
-    for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(__uint_as_float((uint32_t)row[k] << 16)));
+    if (vec) {
+#pragma unroll 4
+        for (int gi = threadIdx.x; gi < ng; gi += 256) {
+            const u32x4 w = *reinterpret_cast<const u32x4 *>(row + 8 * gi);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(w[e] << 16)), fabsf(__uint_as_float(w[e] & 0xffff0000u))));
+        }
+    } else {
+        for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(__uint_as_float((uint32_t)row[k] << 16)));
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
     __shared__ float wmax[4];
@@ -90,9 +105,23 @@ __global__ __launch_bounds__(256) void a_rows_to_f16_kernel(const uint16_t *__re
     }
     __syncthreads();
     const float scale = __builtin_amdgcn_ldexpf(1.0f, ssig);
-    _Float16 *out = a16 + (size_t)m * Kp;
-    for (int k = threadIdx.x; k < Kp; k += 256)
-        out[k] = k < K ? (_Float16)(__uint_as_float((uint32_t)row[k] << 16) * scale) : (_Float16)0.0f;
+    if (vec) {
+#pragma unroll 4
+        for (int gi = threadIdx.x; gi < (Kp >> 3); gi += 256) {
+            u32x4 w = {0u, 0u, 0u, 0u};
+            if (gi < ng) w = *reinterpret_cast<const u32x4 *>(row + 8 * gi);
+            half8 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h[2 * e] = (_Float16)(__uint_as_float(w[e] << 16) * scale);
+                h[2 * e + 1] = (_Float16)(__uint_as_float(w[e] & 0xffff0000u) * scale);
+            }
+            *reinterpret_cast<half8 *>(out + 8 * gi) = h;
+        }
+    } else {
+        for (int k = threadIdx.x; k < Kp; k += 256)
+            out[k] = k < K ? (_Float16)(__uint_as_float((uint32_t)row[k] << 16) * scale) : (_Float16)0.0f;
+    }
 }
 
 // ---------------------------------------------------------------------------
