@@ -185,16 +185,17 @@ def bench_attention(args, doe):
     }
 
 
-def bench_decode(args, doe):
+def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
     """2B-class decode loop at batch 1 (26 layers, hidden 2304, 8/4 heads of
     256, FFN 9216 GeGLU, Q4_K projections, f16 lm_head over 256000): a
     128-token prompt then `--decode-steps` greedy steps, each step a replay of
-    a captured HIP graph; tokens/s over the decode steps (HIP events)."""
+    a captured HIP graph; tokens/s over the decode steps (HIP events).  cfg /
+    plan: another model shape and its execution-v1 decode plan."""
     from doe_amd import Stream
     from doe_amd.model import Decoder, DecoderConfig
 
-    cfg = DecoderConfig()
-    dec = Decoder(cfg)
+    cfg = cfg or DecoderConfig()
+    dec = Decoder(cfg, plan=plan)
     dec.init_random(seed=2)
     rng = np.random.default_rng(2)
     prompt = rng.integers(0, cfg.vocab, args.prompt_len, dtype=np.int64).astype(np.int32)
@@ -213,10 +214,10 @@ def bench_decode(args, doe):
     mean_len = args.prompt_len + (args.decode_steps + 1) / 2.0
     bpt = cfg.decode_bytes_per_token(mean_len)
     gbs = bpt * tok_s / 1e9
-    log(f"decode: {tok_s:.1f} tok/s ({timing['decode_s'] * 1e3 / args.decode_steps:.3f} ms/token), "
+    log(f"decode ({label}): {tok_s:.1f} tok/s ({timing['decode_s'] * 1e3 / args.decode_steps:.3f} ms/token), "
         f"prompt {timing['prompt_s']:.3f} s, {gbs:.0f} GB/s of algorithmic bytes")
     return {
-        "workload": f"2B-class decoder bs=1: {cfg.layers} layers, hidden {cfg.hidden}, {cfg.heads}/{cfg.kv_heads} "
+        "workload": f"{label} bs=1: {cfg.layers} layers, hidden {cfg.hidden}, {cfg.heads}/{cfg.kv_heads} "
                     f"heads x {cfg.head_dim}, FFN {cfg.ffn} GeGLU, vocab {cfg.vocab}; Q4_K projections, f16 "
                     f"lm_head, f16 KV; prompt {args.prompt_len} then {args.decode_steps} greedy steps; "
                     f"random-init weights; " + (f"{spg} steps per HIP graph" if spg > 0 else "eager launches"),
@@ -229,6 +230,22 @@ def bench_decode(args, doe):
         "prompt_s": round(timing["prompt_s"], 4),
         "last_tokens": [int(t) for t in ids[-4:]],
     }
+
+
+def bench_decode_graph(args, doe):
+    """The decode loop planned from the reference's gemma-3-270m execution-v1
+    manifest graph (runtime/zig/examples/execution-v1/gemma-3-270m-manifest-
+    smoke.json, kept as a test fixture) at that model's shapes: 18 layers,
+    hidden 640, 4/1 heads of 256, FFN 2048, vocab 262144; random weights."""
+    from doe_amd import execution as ex
+    from doe_amd.model import DecoderConfig
+
+    graph = ex.load_step_graph(ROOT / "tests" / "golden" / "execution_v1" / "gemma-3-270m-manifest-smoke.json")
+    cfg = DecoderConfig(layers=18, hidden=640, heads=4, kv_heads=1, head_dim=256, ffn=2048, vocab=262144,
+                        max_seq=384)
+    res = bench_decode(args, doe, cfg, ex.plan_decode(graph, cfg.layers),
+                       label=f"{graph.model_id} (execution-v1 manifest graph)")
+    return res
 
 
 GEMM_M, GEMM_N, GEMM_K = 2048, 21504, 5376
@@ -506,6 +523,7 @@ def main() -> int:
     g = bench_gemv(args, doe_amd)
     att = bench_attention(args, doe_amd)
     dec = None if args.no_decode else bench_decode(args, doe_amd)
+    dec_graph = None if args.no_decode else bench_decode_graph(args, doe_amd)
     gemm = None if args.no_gemm else bench_gemm(args, doe_amd)
     pfa = None if args.no_gemm else bench_prefill_attention(args, doe_amd)
     c4 = None if args.no_gemm else bench_config4(args, doe_amd)
@@ -547,6 +565,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "attention_decode": att,
         "decode": dec,
+        "decode_graph_gemma3_270m": dec_graph,
         "prefill_gemm": gemm,
         "prefill_attention": pfa,
         "config4_decode_layer": c4,

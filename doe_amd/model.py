@@ -67,6 +67,25 @@ class DecoderConfig:
         return (self.qkv_rows * rb(self.hidden) + self.hidden * rb(self.q_dim)
                 + 2 * self.ffn * rb(self.hidden) + self.hidden * rb(self.ffn))
 
+    @classmethod
+    def from_model_config(cls, mc: dict, **overrides) -> "DecoderConfig":
+        """From a step graph's modelConfig (hiddenDim, numHeads, headDim,
+        numKeyValueHeads, numLayers, vocabSize, maxSeqLen, ffnExpansionFactor);
+        a separate globalHeadDim or a non-Q4_K quantFormat is not supported."""
+        from .execution import UnsupportedStep
+
+        if mc.get("quantFormat", "q4k") != "q4k":
+            raise UnsupportedStep(f"quantFormat {mc.get('quantFormat')!r}")
+        if mc.get("globalHeadDim", mc["headDim"]) != mc["headDim"]:
+            raise UnsupportedStep(f"globalHeadDim {mc['globalHeadDim']} != headDim {mc['headDim']}")
+        kw = dict(layers=mc["numLayers"], hidden=mc["hiddenDim"], heads=mc["numHeads"],
+                  kv_heads=mc["numKeyValueHeads"], head_dim=mc["headDim"], vocab=mc["vocabSize"],
+                  ffn=mc["hiddenDim"] * mc.get("ffnExpansionFactor", 4))
+        if "maxSeqLen" in mc:
+            kw["max_seq"] = mc["maxSeqLen"]
+        kw.update(overrides)
+        return cls(**kw)
+
     def decode_bytes_per_token(self, kv_len: float) -> float:
         """Algorithmic HBM bytes of one decode step: every weight once, the
         KV cache up to kv_len, plus the embedding row."""
@@ -103,9 +122,14 @@ class LayerWeights:
 class Decoder:
     """Device-resident weights, KV cache and activations of one decoder."""
 
-    def __init__(self, cfg: DecoderConfig, keep_logits: bool = False):
+    def __init__(self, cfg: DecoderConfig, keep_logits: bool = False, plan=None):
+        """plan: an execution.DecodePlan (per-layer attention windows); None =
+        global attention in every layer."""
         self.cfg = cfg
         self.keep_logits = keep_logits  # also write the logits (tests); the sample does not need them
+        self.attn_windows = tuple(plan.windows) if plan is not None else (0,) * cfg.layers
+        if len(self.attn_windows) != cfg.layers:
+            raise ValueError(f"plan covers {len(self.attn_windows)} layers, the model has {cfg.layers}")
         c = cfg
         self.layers = [LayerWeights(c) for _ in range(c.layers)]
         self.embed = DeviceBuffer.empty((c.vocab, c.hidden), np.float16)
@@ -170,7 +194,7 @@ class Decoder:
         c = self.cfg
         ops.embed(self.embed, self.tok_view, self.x, 1, c.vocab, c.hidden, c.embed_scale, stream=stream)
         scale = 1.0 / math.sqrt(c.head_dim)
-        for L in self.layers:
+        for li, L in enumerate(self.layers):
             ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads, num_kv_heads=c.kv_heads,
                             head_dim=c.head_dim, freq_cis=self.freq_cis, position_buffer=self.pos_view,
                             key_cache=L.k_cache, val_cache=L.v_cache, max_seq_len=c.max_seq,
@@ -179,7 +203,7 @@ class Decoder:
                                             num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim,
                                             kv_len=0, kv_stride=c.max_seq, scale=scale,
                                             max_splits=self.max_attn_splits, kv_len_buffer=self.kvlen_view,
-                                            stream=stream)
+                                            sliding_window=self.attn_windows[li], stream=stream)
             ops.matmul_q4k_attn_out(L.wo, self.attn_parts, splits, c.heads, c.head_dim, self.x, c.hidden,
                                     residual=self.x, stream=stream)
             ops.matmul_q4k_fused(L.wgu, self.x, self.h, 2 * c.ffn, c.hidden, norm_weight=L.norm_ffn,

@@ -31,12 +31,13 @@ class OracleDecoder:
         self.lm_head = dec.lm_head.download()
         self.nf = dec.norm_final.download()
         self.table = dec.freq_cis.download()
+        self.windows = dec.attn_windows
 
     def step(self, pos: int, token: int) -> np.ndarray:
         c = self.cfg
         x = ora.embed_gather(self.embed, np.array([token], np.int32), c.embed_scale)[0]
         scale = 1.0 / math.sqrt(c.head_dim)
-        for L in self.layers:
+        for li, L in enumerate(self.layers):
             xn = ora.rmsnorm(x, L["n1"], c.eps, True)
             qkv = ora.q4k_gemv(L["wqkv"], xn, c.qkv_rows, c.hidden)
             qk = ora.rope(qkv[: c.q_dim + c.kv_dim], self.table, 1, c.heads + c.kv_heads, c.head_dim, pos)
@@ -44,7 +45,7 @@ class OracleDecoder:
             v = qkv[c.q_dim + c.kv_dim:]
             ora.kv_write(k, v, L["kc"], L["vc"], c.kv_heads, c.max_seq, c.head_dim, pos)
             attn = ora.attn_decode(qk[: c.q_dim], L["kc"], L["vc"], c.heads, c.kv_heads, c.head_dim, pos + 1,
-                                   c.max_seq, scale).reshape(-1)
+                                   c.max_seq, scale, sliding_window=self.windows[li]).reshape(-1)
             x = ora.residual(ora.q4k_gemv(L["wo"], attn, c.hidden, c.q_dim), x)
             xn2 = ora.rmsnorm(x, L["n2"], c.eps, True)
             gu = ora.q4k_gemv(L["wgu"], xn2, 2 * c.ffn, c.hidden)

@@ -1,6 +1,9 @@
 """GPU parity of the decode loop against the CPU oracle decoder, teacher
 forced on the GPU's own tokens: per-step logits within rel-L2 1e-3 and the
 greedy token equal to the oracle's argmax."""
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -80,4 +83,57 @@ def test_full_size_first_steps(dev, ora):
     prompt = np.array([12345, 200000], np.int32)
     ids, errs = run_teacher_forced(dec, oracle, prompt, 1, s)
     print(f"[decode 2B] logits rel_l2 per step {errs}", flush=True)
+    assert max(errs) <= 1e-3
+
+
+def test_step_graph_plan_with_sliding_layers(dev, ora):
+    # The decode loop driven by the reference's gemma-3-270m step graph with a
+    # layerPattern added: layer 0 attends through an 8-key sliding window,
+    # layer 1 globally.  Teacher-forced past the window against the oracle
+    # decoder; a global-attention decoder on the same weights must differ.
+    from doe_amd import execution as ex
+
+    g = json.loads((Path(__file__).parent / "golden" / "execution_v1" / "gemma-3-270m-smoke.json").read_text())
+    g["layerPattern"] = {"type": "every_n", "period": 2, "offset": 1}
+    g["slidingWindowSize"] = 8
+    plan = ex.plan_decode(ex.load_step_graph(g), SMALL.layers)
+    assert plan.windows == (8, 0)
+    s = Stream()
+    dec = Decoder(SMALL, keep_logits=True, plan=plan)
+    dec.init_random(seed=4)
+    oracle = OracleDecoder(dec)
+    prompt = np.array([9, 400, 4000, 12, 12, 700, 31, 2], np.int32)
+    ids, errs = run_teacher_forced(dec, oracle, prompt, 16, s)
+    print(f"[decode windowed] max logits rel_l2 {max(errs):.2e}", flush=True)
+    assert max(errs) <= 1e-3
+    glob = Decoder(SMALL, keep_logits=True)
+    glob.init_random(seed=4)
+    glob.reset(np.array(ids, np.int32))
+    dec.reset(np.array(ids, np.int32))
+    for _ in range(len(ids)):
+        glob.step(s)
+        dec.step(s)
+    s.synchronize()
+    assert rel_l2(dec.logits.download(), glob.logits.download()) > 1e-3
+
+
+def test_gemma3_270m_manifest_graph_first_steps(dev, ora):
+    # The reference's gemma-3-270m manifest graph planned onto the decode loop
+    # at that model's shapes (hidden 640: Q4_K rows with a 128-element tail;
+    # 4 query heads on 1 KV head of 256; FFN 2048; vocab 262144), random
+    # weights, teacher-forced against the oracle decoder.
+    from doe_amd import execution as ex
+
+    graph = ex.load_step_graph(Path(__file__).parent / "golden" / "execution_v1" /
+                               "gemma-3-270m-manifest-smoke.json")
+    cfg = DecoderConfig(layers=18, hidden=640, heads=4, kv_heads=1, head_dim=256, ffn=2048, vocab=262144,
+                        max_seq=32)
+    plan = ex.plan_decode(graph, cfg.layers)
+    s = Stream()
+    dec = Decoder(cfg, keep_logits=True, plan=plan)
+    dec.init_random(seed=5)
+    oracle = OracleDecoder(dec)
+    prompt = np.array([2, 105, 262143, 818], np.int32)
+    ids, errs = run_teacher_forced(dec, oracle, prompt, 3, s)
+    print(f"[decode gemma-3-270m graph] max logits rel_l2 {max(errs):.2e}", flush=True)
     assert max(errs) <= 1e-3
