@@ -137,3 +137,80 @@ def test_gemma3_270m_manifest_graph_first_steps(dev, ora):
     ids, errs = run_teacher_forced(dec, oracle, prompt, 3, s)
     print(f"[decode gemma-3-270m graph] max logits rel_l2 {max(errs):.2e}", flush=True)
     assert max(errs) <= 1e-3
+
+
+def _write_rdrr(dec, root):
+    """An RDRR artifact (manifest + two shards, HF tensor names) holding a
+    decoder's weights in the plain row order of the checkpoint files."""
+    from doe_amd import q4k as _q4k
+    from doe_amd.ops import deinterleave_rope_rows
+
+    c = dec.cfg
+    rb = _q4k.row_bytes
+    tensors, blobs = {}, [bytearray(), bytearray()]
+
+    def put(name, arr, dtype, shape, layout=None, split=False):
+        raw = np.ascontiguousarray(arr).tobytes()
+        meta = {"dtype": dtype, "shape": list(shape), "size": len(raw)}
+        if layout:
+            meta["layout"] = layout
+        if split:  # this tensor's bytes span both shards
+            h = len(raw) // 3
+            meta["spans"] = [{"shardIndex": 0, "offset": len(blobs[0]), "size": h},
+                             {"shardIndex": 1, "offset": len(blobs[1]), "size": len(raw) - h}]
+            blobs[0].extend(raw[:h])
+            blobs[1].extend(raw[h:])
+        else:
+            meta.update(shard=0, offset=len(blobs[0]))
+            blobs[0].extend(raw)
+        tensors[name] = meta
+
+    for i, L in enumerate(dec.layers):
+        p = f"model.layers.{i}"
+        wqkv = L.wqkv.download().reshape(c.qkv_rows, rb(c.hidden))
+        q, k, v = wqkv[:c.q_dim], wqkv[c.q_dim:c.q_dim + c.kv_dim], wqkv[c.q_dim + c.kv_dim:]
+        put(f"{p}.self_attn.q_proj.weight", deinterleave_rope_rows(q, c.head_dim), "Q4_K_M", (c.q_dim, c.hidden), "row")
+        put(f"{p}.self_attn.k_proj.weight", deinterleave_rope_rows(k, c.head_dim), "Q4_K_M", (c.kv_dim, c.hidden), "row")
+        put(f"{p}.self_attn.v_proj.weight", v, "Q4_K_M", (c.kv_dim, c.hidden), "row")
+        put(f"{p}.self_attn.o_proj.weight", L.wo.download(), "Q4_K_M", (c.hidden, c.q_dim), "row")
+        gu = L.wgu.download().reshape(2 * c.ffn, rb(c.hidden))
+        put(f"{p}.mlp.gate_proj.weight", gu[0::2], "Q4_K_M", (c.ffn, c.hidden), "row")
+        put(f"{p}.mlp.up_proj.weight", gu[1::2], "Q4_K_M", (c.ffn, c.hidden), "row")
+        put(f"{p}.mlp.down_proj.weight", L.wd.download(), "Q4_K_M", (c.hidden, c.ffn), "row", split=(i == 1))
+        put(f"{p}.input_layernorm.weight", L.norm_attn.download(), "F32", (c.hidden,))
+        put(f"{p}.post_attention_layernorm.weight", L.norm_ffn.download(), "F32", (c.hidden,))
+    put("model.embed_tokens.weight", dec.embed.download(), "F16", (c.vocab, c.hidden))
+    put("lm_head.weight", dec.lm_head.download(), "F16", (c.vocab, c.hidden), split=True)
+    put("model.norm.weight", dec.norm_final.download(), "F32", (c.hidden,))
+    for idx, b in enumerate(blobs):
+        (root / f"shard_{idx:05d}.bin").write_bytes(bytes(b))
+    manifest = {"shards": [{"index": 0, "filename": "shard_00000.bin"}, {"index": 1, "filename": "shard_00001.bin"}],
+                "tensors": tensors}
+    (root / "manifest.json").write_text(json.dumps(manifest))
+
+
+def test_rdrr_artifact_loads_byte_identical(dev, tmp_path):
+    # Q4_K_M rows move unchanged from the artifact into the decoder's layout;
+    # a decoder loaded from it holds the same bytes and decodes the same logits
+    from doe_amd import rdrr
+
+    src = Decoder(SMALL, keep_logits=True)
+    src.init_random(seed=6)
+    _write_rdrr(src, tmp_path)
+    dst = Decoder(SMALL, keep_logits=True)
+    rdrr.load_decoder_weights(rdrr.RdrrArtifact(tmp_path), dst)
+    pairs = [(src.embed, dst.embed), (src.lm_head, dst.lm_head), (src.norm_final, dst.norm_final)]
+    for a, b in zip(src.layers, dst.layers):
+        pairs += [(a.wqkv, b.wqkv), (a.wo, b.wo), (a.wgu, b.wgu), (a.wd, b.wd), (a.norm_attn, b.norm_attn),
+                  (a.norm_ffn, b.norm_ffn)]
+    for a, b in pairs:
+        assert a.download().tobytes() == b.download().tobytes()
+    s = Stream()
+    prompt = np.array([3, 1000, 7], np.int32)
+    for d in (src, dst):
+        d.reset(prompt)
+        for _ in range(4):
+            d.step(s)
+    s.synchronize()
+    assert rel_l2(dst.logits.download(), src.logits.download()) <= 1e-6
+    assert src.ids.download()[:7].tolist() == dst.ids.download()[:7].tolist()
