@@ -53,6 +53,7 @@ struct AttnArgs {
     float scale_log2e;  // scale * log2(e)
     float softcap;
     int sliding_window;
+    int head_groups;  // workgroups per kv head, each over G of its query heads
 };
 
 constexpr int kMaxSplits = 512;
@@ -116,9 +117,10 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     __shared__ float4 pb[kWaves][17][G4];  // per wave: probabilities [position][head], row 16: max/sum
     __shared__ float wm[kWaves][G], wl[kWaves][G];
 
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    // blockIdx.y = kv head * head_groups + group: G query heads per workgroup
+    const int split = blockIdx.x, kvh = (int)blockIdx.y / a.head_groups, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int hq0 = kvh * G;  // first query head of this group
+    const int hq0 = (int)blockIdx.y * G;  // first query head of this group
 
     int kv_len = a.kv_len_dev ? a.kv_len_dev[0] : a.kv_len;
     kv_len = kv_len < 0 ? 0 : (kv_len > a.kv_stride ? a.kv_stride : kv_len);
@@ -569,15 +571,19 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
         a.ws_o = (float *)g_ws;
         a.ws_ml = (float *)((char *)g_ws + ml_off);
     }
-    const dim3 grid((unsigned)splits, (unsigned)num_kv_heads, (unsigned)batch);
+    // head_dim 512 holds at most two query heads per workgroup (a 16-position
+    // K/V block is 64 registers per lane, double-buffered): larger groups are
+    // split over g / 2 workgroups per kv head, each reading the kv head's K/V
+    a.head_groups = head_dim == 512 && g > 2 ? g / 2 : 1;
+    DOE_REQUIRE(num_kv_heads * a.head_groups <= 65535, DOE_E_UNSUPPORTED, "too many kv heads");
+    const dim3 grid((unsigned)splits, (unsigned)(num_kv_heads * a.head_groups), (unsigned)batch);
     const hipStream_t st = (hipStream_t)stream;
     switch (head_dim) {
         case 64: return launch_d<64>(g, wide, grid, st, a);
         case 128: return launch_d<128>(g, wide, grid, st, a);
         case 256: return launch_d<256>(g, wide, grid, st, a);
         default:
-            DOE_REQUIRE(g <= 2, DOE_E_UNSUPPORTED, "head_dim 512 supports at most 2 query heads per kv head");
-            return launch_d<512>(g, false, grid, st, a);
+            return launch_d<512>(g / a.head_groups, false, grid, st, a);
     }
 }
 

@@ -49,6 +49,7 @@ class DecoderConfig:
     rope_base: float = 10000.0
     max_seq: int = 384
     embed_scale: float = 1.0
+    attn_softcap: float = 0.0  # > 0: scores s -> softcap * tanh(s / softcap) (attention_head256_f16kv.wgsl:197-199)
 
     @property
     def q_dim(self) -> int:
@@ -203,7 +204,8 @@ class Decoder:
                                             num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim,
                                             kv_len=0, kv_stride=c.max_seq, scale=scale,
                                             max_splits=self.max_attn_splits, kv_len_buffer=self.kvlen_view,
-                                            sliding_window=self.attn_windows[li], stream=stream)
+                                            sliding_window=self.attn_windows[li], softcap=c.attn_softcap,
+                                            stream=stream)
             ops.matmul_q4k_attn_out(L.wo, self.attn_parts, splits, c.heads, c.head_dim, self.x, c.hidden,
                                     residual=self.x, stream=stream)
             ops.matmul_q4k_fused(L.wgu, self.x, self.h, 2 * c.ffn, c.hidden, norm_weight=L.norm_ffn,

@@ -45,7 +45,8 @@ class OracleDecoder:
             v = qkv[c.q_dim + c.kv_dim:]
             ora.kv_write(k, v, L["kc"], L["vc"], c.kv_heads, c.max_seq, c.head_dim, pos)
             attn = ora.attn_decode(qk[: c.q_dim], L["kc"], L["vc"], c.heads, c.kv_heads, c.head_dim, pos + 1,
-                                   c.max_seq, scale, sliding_window=self.windows[li]).reshape(-1)
+                                   c.max_seq, scale, softcap=c.attn_softcap,
+                                   sliding_window=self.windows[li]).reshape(-1)
             x = ora.residual(ora.q4k_gemv(L["wo"], attn, c.hidden, c.q_dim), x)
             xn2 = ora.rmsnorm(x, L["n2"], c.eps, True)
             gu = ora.q4k_gemv(L["wgu"], xn2, 2 * c.ffn, c.hidden)

@@ -57,8 +57,8 @@ def test_config1_gqa_decode(dev, ora):
 @pytest.mark.parametrize("d", [64, 128, 256, 512])
 @pytest.mark.parametrize("g", [1, 2, 4, 8])
 def test_head_dims_and_groups(dev, ora, d, g):
-    if d == 512 and g > 2:
-        pytest.skip("head_dim 512 supports at most 2 query heads per kv head")
+    # (head_dim 512 with more than two query heads per kv head runs as g / 2
+    # workgroups per kv head)
     rng = np.random.default_rng(d + g)
     hkv = 2
     hq = hkv * g
@@ -71,6 +71,22 @@ def test_head_dims_and_groups(dev, ora, d, g):
                    out_f16=False, batch=batch)
     want = oracle_attn(ora, q, k, v, batch=batch, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=scale)
     assert rel_l2(got, want) <= 1e-5  # f32 query (hi/lo split), f32 output
+
+
+def test_head512_global_layer_shape(dev, ora):
+    # a 512-wide global attention layer: 8 query heads on one kv head, the
+    # [pos][kv_head][dim] layout, a score softcap and a sliding window
+    rng = np.random.default_rng(512)
+    hq, hkv, d, t, stride = 8, 1, 512, 700, 768
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    k = rng.standard_normal((1, stride, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((1, stride, hkv, d)).astype(np.float16)
+    for softcap, window in ((0.0, 0), (50.0, 0), (0.0, 256)):
+        got = run_attn(q, k, v, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=1 / 16, q_f16=False,
+                       out_f16=False, softcap=softcap, window=window, layout=1)
+        want = oracle_attn(ora, q, k, v, batch=1, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=1 / 16,
+                           softcap=softcap, window=window, layout=1)
+        assert rel_l2(got, want) <= 1e-5, (softcap, window)
 
 
 @pytest.mark.parametrize("t", [1, 15, 16, 17, 63, 64, 65, 1000])

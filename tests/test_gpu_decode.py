@@ -214,3 +214,26 @@ def test_rdrr_artifact_loads_byte_identical(dev, tmp_path):
     s.synchronize()
     assert rel_l2(dst.logits.download(), src.logits.download()) <= 1e-6
     assert src.ids.download()[:7].tolist() == dst.ids.download()[:7].tolist()
+
+
+def test_attention_softcap_in_the_decode_loop(dev, ora):
+    # attn_softcap (the reference attention's attn_softcap uniform) caps the
+    # scores in every layer; a small softcap changes the logits measurably
+    cfg = DecoderConfig(layers=2, hidden=512, heads=4, kv_heads=2, head_dim=128, ffn=1024, vocab=4096, max_seq=64,
+                        attn_softcap=0.5)
+    s = Stream()
+    dec = Decoder(cfg, keep_logits=True)
+    dec.init_random(seed=7)
+    oracle = OracleDecoder(dec)
+    prompt = np.array([11, 22, 3333, 44], np.int32)
+    ids, errs = run_teacher_forced(dec, oracle, prompt, 8, s)
+    print(f"[decode softcap] max logits rel_l2 {max(errs):.2e}", flush=True)
+    assert max(errs) <= 1e-3
+    plain = Decoder(SMALL, keep_logits=True)
+    plain.init_random(seed=7)
+    for d in (dec, plain):
+        d.reset(np.array(ids, np.int32))
+        for _ in range(len(ids)):
+            d.step(s)
+    s.synchronize()
+    assert rel_l2(dec.logits.download(), plain.logits.download()) > 1e-3
