@@ -54,6 +54,16 @@ struct AttnArgs {
     float softcap;
     int sliding_window;
     int head_groups;  // workgroups per kv head, each over G of its query heads
+    // Logical key p -> cache row (attention_head256_f16kv.wgsl:51-63):
+    // kv_map 0: kv_start + p; 1: (kv_start + p) % ring; 2: paged, the page
+    // table entry of (kv_start + p) / page_size times page_size plus the
+    // offset in the page.  Rows are clamped into [0, kv_stride).
+    int kv_map, kv_start, ring, page_size;
+    const uint32_t *page_table;
+    int page_table_len;
+    // The query's absolute position: kv_start + kv_len - 1 (query_at_end) or
+    // start_pos; causal keeps keys <= it, a sliding window the last `window`.
+    int query_at_end, start_pos, causal;
 };
 
 constexpr int kMaxSplits = 512;
@@ -84,18 +94,34 @@ struct KVBlock {
     _Float16 vv[16][D / 64];
 };
 
+// Cache row of logical key p (see AttnArgs), clamped into the cache.
+__device__ __forceinline__ int kv_row(const AttnArgs &a, int p) {
+    const int64_t abs_key = (int64_t)a.kv_start + p;
+    int64_t r = abs_key;
+    if (a.kv_map == 1) {
+        r = abs_key % a.ring;
+    } else if (a.kv_map == 2) {
+        int64_t pg = abs_key / a.page_size;
+        pg = pg < a.page_table_len ? pg : a.page_table_len - 1;
+        r = (int64_t)a.page_table[pg] * a.page_size + (abs_key - (abs_key / a.page_size) * a.page_size);
+    }
+    return (int)(r < 0 ? 0 : (r >= a.kv_stride ? a.kv_stride - 1 : r));
+}
+
+// rowk: this lane's key row (lane l holds key p0 + l % 16); lanes 0..15 give
+// the 16 rows every lane's V loads need.
 template <int D>
 __device__ __forceinline__ void load_block(KVBlock<D> &blk, const uint16_t *kb, const uint16_t *vb,
-                                           int p0, int kv_len, size_t pos_stride, int lane) {
+                                           int rowk, size_t pos_stride, int lane) {
     constexpr int KSTEPS = D / 32, DPL = D / 64;
-    // key p0 + lane % 16, dims 8 (lane / 16) + 32 s (clamped into range, masked later)
-    const uint16_t *krow = kb + (size_t)min(p0 + (lane & 15), kv_len - 1) * pos_stride + 8 * (lane >> 4);
+    // dims 8 (lane / 16) + 32 s of the lane's key
+    const uint16_t *krow = kb + (size_t)rowk * pos_stride + 8 * (lane >> 4);
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) blk.kf[s] = *reinterpret_cast<const h8 *>(krow + 32 * s);
 #pragma unroll
     for (int n = 0; n < 16; ++n) {
         const _Float16 *vrow = reinterpret_cast<const _Float16 *>(
-            vb + (size_t)min(p0 + n, kv_len - 1) * pos_stride + lane * DPL);
+            vb + (size_t)__builtin_amdgcn_readlane(rowk, n) * pos_stride + lane * DPL);
 #pragma unroll
         for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
     }
@@ -123,10 +149,17 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     const int hq0 = (int)blockIdx.y * G;  // first query head of this group
 
     int kv_len = a.kv_len_dev ? a.kv_len_dev[0] : a.kv_len;
-    kv_len = kv_len < 0 ? 0 : (kv_len > a.kv_stride ? a.kv_stride : kv_len);
-    const int min_key = (a.sliding_window > 0 && kv_len - 1 >= a.sliding_window)
-                            ? kv_len - a.sliding_window : 0;
-    const int nblk = (kv_len + 15) >> 4;
+    kv_len = kv_len < 0 ? 0 : kv_len;
+    if (a.kv_map == 0 && a.kv_start == 0 && kv_len > a.kv_stride) kv_len = a.kv_stride;
+    // visible keys [min_key, key_hi) (attention_head256_f16kv.wgsl:115-131)
+    const int qpos = a.query_at_end ? a.kv_start + kv_len - 1 : a.start_pos;
+    int key_hi = kv_len, min_key = 0;
+    if (a.causal) key_hi = qpos < a.kv_start ? 0 : min(kv_len, qpos - a.kv_start + 1);
+    if (a.sliding_window > 0 && qpos >= a.sliding_window) {
+        const int min_abs = qpos - a.sliding_window + 1;
+        min_key = min_abs > a.kv_start ? min(min_abs - a.kv_start, kv_len) : 0;
+    }
+    const int nblk = (key_hi + 15) >> 4;
     const int bps = (nblk + a.splits - 1) / a.splits;
     const int blk_begin = split * bps;
     const int blk_end = min(nblk, blk_begin + bps);
@@ -162,7 +195,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     __asm__ volatile("" ::: "memory");
     KVBlock<D> cur;
     int blk = blk_begin + wave;
-    if (blk < blk_end) load_block<D>(cur, kb, vb, blk * 16, kv_len, pos_stride, lane);
+    if (blk < blk_end) load_block<D>(cur, kb, vb, kv_row(a, min(blk * 16 + (lane & 15), key_hi - 1)), pos_stride, lane);
 #pragma unroll
     for (int it = 0; it < QITEMS; ++it) {
         const int idx = tid + it * kThreads;
@@ -211,7 +244,9 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         // Prefetch the next block of this wave while this one is computed
         // (only when there is one: a wave retires only once its loads are back).
         KVBlock<D> nxt;
-        if (blk + kWaves < blk_end) load_block<D>(nxt, kb, vb, (blk + kWaves) * 16, kv_len, pos_stride, lane);
+        if (blk + kWaves < blk_end)
+            load_block<D>(nxt, kb, vb, kv_row(a, min((blk + kWaves) * 16 + (lane & 15), key_hi - 1)), pos_stride,
+                          lane);
 
         const int p0 = blk * 16;
         const int pk = p0 + (lane & 15);
@@ -224,7 +259,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
             for (int s = 0; s < KSTEPS; ++s)
                 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(sm.qfrag[1][s][lane], cur.kf[s], c, 0, 0, 0);
         }
-        const bool valid = pk < kv_len && pk >= min_key;
+        const bool valid = pk < key_hi && pk >= min_key;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float s = c[i];
@@ -467,6 +502,15 @@ int attn_set_waves(int v) {
 
 namespace {
 
+// The reference attention's cache addressing and key range (defaults: the
+// rows kv_start + p from 0, causal, the query at the last key).
+struct KvMap {
+    int kv_map = 0, kv_start = 0, ring = 0, page_size = 0;
+    const uint32_t *page_table = nullptr;
+    int64_t page_table_len = 0;
+    int query_at_end = 1, start_pos = 0, causal = 1;
+};
+
 // parts == NULL: the library workspace and (for several splits) the combine
 // kernel; parts != NULL: (o, m, l) partials into the caller's buffer
 // (o [B*Hq][S][D] then ml [B*Hq][S][2]), at most max_splits splits.
@@ -475,7 +519,7 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
                      int64_t head_dim, int64_t kv_len, const int32_t *kv_len_dev, int64_t kv_stride,
                      int kv_layout, float scale, float softcap, int64_t sliding_window,
                      float *parts, int64_t parts_capacity, int64_t max_splits_req, int32_t *splits_out,
-                     doe_stream_t stream) {
+                     doe_stream_t stream, const KvMap &map = KvMap()) {
     int rc = doe::require_init();
     if (rc) return rc;
     DOE_REQUIRE(batch >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && kv_stride >= 0,
@@ -487,8 +531,10 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
                 "kv_layout %d unsupported (0: [kv_head][pos][dim], 1: [pos][kv_head][dim])", kv_layout);
     DOE_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512,
                 DOE_E_UNSUPPORTED, "head_dim %lld unsupported (64, 128, 256, 512)", (long long)head_dim);
-    DOE_REQUIRE(kv_len_dev != nullptr || (kv_len >= 0 && kv_len <= kv_stride), DOE_E_INVALID,
-                "kv_len %lld out of range [0, kv_stride=%lld]", (long long)kv_len, (long long)kv_stride);
+    const bool plain = map.kv_map == 0 && map.kv_start == 0;  // logical key p is cache row p
+    DOE_REQUIRE(kv_len_dev != nullptr || (kv_len >= 0 && (!plain || kv_len <= kv_stride) && kv_len < (1 << 30)),
+                DOE_E_INVALID, "kv_len %lld out of range [0, kv_stride=%lld]", (long long)kv_len,
+                (long long)kv_stride);
     DOE_REQUIRE(sliding_window >= 0 && softcap >= 0.0f, DOE_E_INVALID, "negative window or softcap");
     if (batch == 0) return DOE_OK;
     DOE_REQUIRE(q && k_cache && v_cache && (out || parts), DOE_E_INVALID, "null pointer");
@@ -545,6 +591,15 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
     a.scale_log2e = scale * 1.4426950408889634f;
     a.softcap = softcap;
     a.sliding_window = (int)sliding_window;
+    a.kv_map = map.kv_map;
+    a.kv_start = map.kv_start;
+    a.ring = map.ring;
+    a.page_size = map.page_size;
+    a.page_table = map.page_table;
+    a.page_table_len = (int)map.page_table_len;
+    a.query_at_end = map.query_at_end;
+    a.start_pos = map.start_pos;
+    a.causal = map.causal;
     if (parts) {
         const int64_t o_count = batch * num_heads * splits * head_dim;
         const int64_t need = o_count + batch * num_heads * splits * 2;
@@ -599,6 +654,46 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
     return attn_decode_impl(q, q_f16, k_cache, v_cache, out, out_f16, batch, num_heads, num_kv_heads,
                             head_dim, kv_len, kv_len_dev, kv_stride, kv_layout, scale, softcap,
                             sliding_window, nullptr, 0, 0, nullptr, stream);
+}
+
+int doe_attention_dispatch(const doe_attention_uniforms *u, const float *q, const uint16_t *k,
+                           const uint16_t *v, float *output, const uint32_t *kv_len_buffer,
+                           const uint32_t *page_table, int64_t page_table_len, int64_t kv_capacity,
+                           doe_stream_t stream) {
+    DOE_REQUIRE(u, DOE_E_INVALID, "null uniforms");
+    DOE_REQUIRE(u->query_len == 1, DOE_E_UNSUPPORTED,
+                "query_len %u: this dispatch is the decode form (query_len 1); prompts go to doe_attn_prefill",
+                u->query_len);
+    DOE_REQUIRE(u->kv_layout <= 2, DOE_E_INVALID, "kv_layout %u (0 contiguous, 1 ring, 2 paged)", u->kv_layout);
+    DOE_REQUIRE(kv_capacity > 0 && kv_capacity < (1 << 30), DOE_E_INVALID, "kv_capacity %lld",
+                (long long)kv_capacity);
+    DOE_REQUIRE(u->kv_len_source == 0 || kv_len_buffer, DOE_E_INVALID, "kv_len_source 1 needs kv_len_buffer");
+    DOE_REQUIRE(u->seq_len < (1u << 30) && u->kv_start < (1u << 30) && u->start_pos < (1u << 30), DOE_E_INVALID,
+                "seq_len / kv_start / start_pos out of range");
+    KvMap m;
+    m.kv_start = (int)u->kv_start;
+    if (u->kv_layout == 1 && u->sliding_window > 0) {  // ring of sliding_window rows
+        DOE_REQUIRE(u->sliding_window <= kv_capacity, DOE_E_INVALID, "ring of %u rows in a %lld-row cache",
+                    u->sliding_window, (long long)kv_capacity);
+        m.kv_map = 1;
+        m.ring = (int)u->sliding_window;
+    } else if (u->kv_layout == 2) {
+        DOE_REQUIRE(u->page_size > 0 && page_table && page_table_len > 0 && page_table_len < (1 << 30),
+                    DOE_E_INVALID, "paged KV needs page_size > 0 and a page table");
+        m.kv_map = 2;
+        m.page_size = (int)u->page_size;
+        m.page_table = page_table;
+        m.page_table_len = page_table_len;
+    }
+    m.query_at_end = 0;
+    m.start_pos = (int)u->start_pos;
+    m.causal = u->is_causal != 0;
+    // K/V in the reference's [pos][kv_head][head_dim] order; f32 q and output
+    return attn_decode_impl(q, 0, k, v, output, 0, 1, u->num_heads, u->num_kv_heads, u->head_dim,
+                            u->kv_len_source ? 0 : (int64_t)u->seq_len,
+                            u->kv_len_source ? reinterpret_cast<const int32_t *>(kv_len_buffer) : nullptr,
+                            kv_capacity, 1, u->scale, u->attn_softcap, (int64_t)u->sliding_window, nullptr, 0, 0,
+                            nullptr, stream, m);
 }
 
 int doe_attn_decode_partials(const void *q, int q_f16, const uint16_t *k_cache,

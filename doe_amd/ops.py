@@ -100,6 +100,37 @@ def attention(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, out
               sliding_window, _stream_ptr(stream))
 
 
+class AttentionUniforms(C.Structure):
+    """The reference attention kernel's Uniforms block
+    (attention_head256_f16kv.wgsl:14-30), field for field."""
+    _fields_ = [("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("seq_len", C.c_uint32), ("query_len", C.c_uint32), ("scale", C.c_float),
+                ("is_causal", C.c_uint32), ("start_pos", C.c_uint32), ("attn_softcap", C.c_float),
+                ("sliding_window", C.c_uint32), ("kv_len_source", C.c_uint32), ("kv_start", C.c_uint32),
+                ("page_size", C.c_uint32), ("kv_layout", C.c_uint32), ("pad", C.c_uint32)]
+
+
+def attention_dispatch(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, output: DeviceBuffer, *,
+                       kv_capacity: int, kv_len_buffer: DeviceBuffer | None = None,
+                       page_table: DeviceBuffer | None = None, stream=None, **uniforms) -> None:
+    """``attention`` as the reference dispatches it: the Uniforms fields as
+    keywords (query_len 1), K/V f16 [kv_capacity][num_kv_heads][head_dim],
+    f32 q and output [num_heads][head_dim]."""
+    u = AttentionUniforms(**{"query_len": 1, **uniforms})
+    hd, hq, hkv = u.head_dim, u.num_heads, u.num_kv_heads
+    _need(q, hq * hd * 4, "q")
+    _need(output, hq * hd * 4, "output")
+    _need(k, kv_capacity * hkv * hd * 2, "k")
+    _need(v, kv_capacity * hkv * hd * 2, "v")
+    pt_len = 0
+    if page_table is not None:
+        pt_len = page_table.nbytes // 4
+    _lib.call("doe_attention_dispatch", C.byref(u), C.c_void_p(q.ptr), C.c_void_p(k.ptr), C.c_void_p(v.ptr),
+              C.c_void_p(output.ptr), C.c_void_p(kv_len_buffer.ptr if kv_len_buffer is not None else None),
+              C.c_void_p(page_table.ptr if page_table is not None else None), pt_len, kv_capacity,
+              _stream_ptr(stream))
+
+
 def attention_prefill(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, output: DeviceBuffer, *, num_heads: int,
                       num_kv_heads: int, head_dim: int, q_len: int, kv_len: int, kv_stride: int | None = None,
                       start_pos: int = 0, scale: float, causal: bool = True, out_bf16: bool = False,

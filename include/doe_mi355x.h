@@ -213,8 +213,11 @@ int doe_attn_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, vo
  *            with a growing cache.
  *   the query sits at position kv_len - 1; sliding_window > 0 keeps keys
  *   [kv_len - sliding_window, kv_len); softcap > 0 applies tanh(s/cap)*cap.
- * head_dim 64/128/256/512, num_heads / num_kv_heads in {1, 2, 4, 8} (512: <= 2).
+ * head_dim 64/128/256/512, num_heads / num_kv_heads in {1, 2, 4, 8}.
  * q, k_cache and v_cache must be 16-byte aligned.
+ * This entry point's kv_layout is the memory order; the reference's own
+ * kv_layout uniform (contiguous / ring / paged positions) is taken by
+ * doe_attention_dispatch below.
  * Uses a library-owned workspace for split-K partials: calls on one device
  * must not run concurrently on different streams. */
 int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uint16_t *v_cache,
@@ -222,6 +225,35 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
                     int64_t num_kv_heads, int64_t head_dim, int64_t kv_len,
                     const int32_t *kv_len_dev, int64_t kv_stride, int kv_layout, float scale,
                     float softcap, int64_t sliding_window, doe_stream_t stream);
+
+/* The reference attention dispatch itself: its Uniforms block field for
+ * field (attention_head256_f16kv.wgsl:14-30) and its bindings Q (1), K (2),
+ * V (3), output (4), kv_len_buffer (5), page_table (6), in the decode form
+ * (query_len 1; prompts: doe_attn_prefill).
+ *   q        f32 [num_heads][head_dim]; output f32 [num_heads][head_dim]
+ *   k/v      f16 [kv_capacity][num_kv_heads][head_dim] (the reference's order)
+ *   keys     key_pos in [0, L), L = seq_len or kv_len_buffer[0]
+ *            (kv_len_source 1); cache row of key_pos (:51-63): kv_start +
+ *            key_pos; kv_layout 1 with sliding_window > 0: that modulo
+ *            sliding_window (a ring); kv_layout 2: page_table[abs / page_size]
+ *            * page_size + abs % page_size (page_table_len entries, clamped).
+ *            Rows are clamped into [0, kv_capacity).
+ *   visible  (:115-131) is_causal: key_pos <= start_pos - kv_start;
+ *            sliding_window > 0: key_pos >= start_pos - sliding_window + 1 -
+ *            kv_start; scores scaled by scale, softcapped by attn_softcap.
+ * q, k and v must be 16-byte aligned. */
+typedef struct {
+    uint32_t num_heads, num_kv_heads, head_dim, seq_len, query_len;
+    float scale;
+    uint32_t is_causal, start_pos;
+    float attn_softcap;
+    uint32_t sliding_window, kv_len_source, kv_start, page_size, kv_layout, pad;
+} doe_attention_uniforms;
+
+int doe_attention_dispatch(const doe_attention_uniforms *u, const float *q, const uint16_t *k,
+                           const uint16_t *v, float *output, const uint32_t *kv_len_buffer,
+                           const uint32_t *page_table, int64_t page_table_len, int64_t kv_capacity,
+                           doe_stream_t stream);
 
 /* The split-K half of doe_attn_decode without its combine: per query head
  * and split, the partial output o and (m, l) -- the running max of the

@@ -5,7 +5,7 @@ import math
 import numpy as np
 import pytest
 
-from doe_amd import DeviceBuffer, Graph, Stream, ops
+from doe_amd import DeviceBuffer, DoeError, Graph, Stream, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -257,3 +257,88 @@ def test_wide_and_narrow_workgroups_agree_with_oracle(dev, ora, waves, d, g):
         _lib.call("doe_tune_set", b"attn_decode.waves", 0)
     want = oracle_attn(ora, q, k, v, batch=batch, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=scale)
     assert rel_l2(got, want) <= 1e-5
+
+
+def _dispatch(q, kc, vc, *, cap, page_table=None, kv_len_buffer=None, **uni):
+    """doe_attention_dispatch on host arrays: q f32 [hq][d], K/V f16 [cap][hkv][d]."""
+    out = DeviceBuffer.empty((uni["num_heads"], uni["head_dim"]), np.float32)
+    ops.attention_dispatch(DeviceBuffer.from_array(q), DeviceBuffer.from_array(kc), DeviceBuffer.from_array(vc),
+                           out, kv_capacity=cap,
+                           page_table=None if page_table is None else DeviceBuffer.from_array(page_table),
+                           kv_len_buffer=kv_len_buffer, **uni)
+    return out.download()
+
+
+def test_reference_dispatch_cache_addressing(dev, ora):
+    # The reference attention's own Uniforms and bindings (decode form).  Its
+    # cache addressing is pinned by storage invariants: a paged cache (rows
+    # scattered over pages by a random page table), a ring of the last
+    # `window` rows and a kv_start offset each hold the same keys as a
+    # contiguous cache, so they give the same output; the contiguous form
+    # matches doe_attn_decode and the oracle.
+    rng = np.random.default_rng(21)
+    hq, hkv, d, L, ps = 8, 2, 128, 300, 32
+    q = rng.standard_normal((hq, d)).astype(np.float32)
+    kc = rng.standard_normal((L, hkv, d)).astype(np.float16)
+    vc = rng.standard_normal((L, hkv, d)).astype(np.float16)
+    base = dict(num_heads=hq, num_kv_heads=hkv, head_dim=d, seq_len=L, scale=1 / math.sqrt(d), is_causal=1,
+                start_pos=L - 1)
+    ref = _dispatch(q, kc, vc, cap=L, **base)
+    want = oracle_attn(ora, q[None], kc[None], vc[None], batch=1, hq=hq, hkv=hkv, d=d, kv_len=L, kv_stride=L,
+                       scale=1 / math.sqrt(d), layout=1)[0]
+    assert rel_l2(ref, want) <= 1e-5
+    same = run_attn(q[None], kc[None], vc[None], hq=hq, hkv=hkv, d=d, kv_len=L, kv_stride=L, scale=1 / math.sqrt(d),
+                    q_f16=False, out_f16=False, layout=1)[0]
+    assert rel_l2(ref, same) <= 1e-6
+    # paged: logical page p lives in physical page perm[p] of a larger pool
+    npg = -(-L // ps)
+    perm = rng.permutation(npg + 5)[:npg].astype(np.uint32)
+    pool_k = rng.standard_normal(((npg + 5) * ps, hkv, d)).astype(np.float16)
+    pool_v = rng.standard_normal(((npg + 5) * ps, hkv, d)).astype(np.float16)
+    for pg in range(npg):
+        n = min(ps, L - pg * ps)
+        pool_k[perm[pg] * ps:perm[pg] * ps + n] = kc[pg * ps:pg * ps + n]
+        pool_v[perm[pg] * ps:perm[pg] * ps + n] = vc[pg * ps:pg * ps + n]
+    paged = _dispatch(q, pool_k, pool_v, cap=(npg + 5) * ps, page_table=perm, kv_layout=2, page_size=ps, **base)
+    assert rel_l2(paged, ref) <= 1e-6
+    # kv_start: the same keys stored 40 rows further in
+    shift_k = np.concatenate([rng.standard_normal((40, hkv, d)).astype(np.float16), kc])
+    shift_v = np.concatenate([rng.standard_normal((40, hkv, d)).astype(np.float16), vc])
+    shifted = _dispatch(q, shift_k, shift_v, cap=L + 40, **{**base, "kv_start": 40, "start_pos": L - 1 + 40})
+    assert rel_l2(shifted, ref) <= 1e-6
+    # ring of the last W rows at (abs % W) == contiguous with a W-key window
+    W = 64
+    ring_k = np.zeros((W, hkv, d), np.float16)
+    ring_v = np.zeros((W, hkv, d), np.float16)
+    for pos in range(L - W, L):
+        ring_k[pos % W], ring_v[pos % W] = kc[pos], vc[pos]
+    ring = _dispatch(q, ring_k, ring_v, cap=W, kv_layout=1, **{**base, "sliding_window": W})
+    windowed = _dispatch(q, kc, vc, cap=L, **{**base, "sliding_window": W})
+    assert rel_l2(ring, windowed) <= 1e-6
+    assert rel_l2(windowed, ref) > 1e-3
+    # causal at an earlier query position == a cache holding only keys <= it
+    early = _dispatch(q, kc, vc, cap=L, **{**base, "start_pos": 100})
+    short = _dispatch(q, kc[:101].copy(), vc[:101].copy(), cap=101, **{**base, "seq_len": 101, "start_pos": 100})
+    assert rel_l2(early, short) <= 1e-6
+    # the length from the device buffer (kv_len_source 1)
+    klen = DeviceBuffer.from_array(np.array([L], np.uint32))
+    dev_len = _dispatch(q, kc, vc, cap=L, kv_len_buffer=klen, **{**base, "seq_len": 0, "kv_len_source": 1})
+    assert rel_l2(dev_len, ref) <= 1e-6
+    # page table entries past the pool are clamped into it: finite output, no fault
+    bad = perm.copy()
+    bad[0] = 1 << 20
+    clamped = _dispatch(q, pool_k, pool_v, cap=(npg + 5) * ps, page_table=bad, kv_layout=2, page_size=ps, **base)
+    assert np.isfinite(clamped).all()
+
+
+def test_reference_dispatch_rejects_unsupported(dev):
+    buf = DeviceBuffer(1 << 16)
+    kw = dict(num_heads=2, num_kv_heads=1, head_dim=64, seq_len=4, scale=1.0, is_causal=1, start_pos=3)
+    with pytest.raises(DoeError, match="query_len"):
+        ops.attention_dispatch(buf, buf, buf, buf, kv_capacity=8, **{**kw, "query_len": 4})
+    with pytest.raises(DoeError, match="kv_layout"):
+        ops.attention_dispatch(buf, buf, buf, buf, kv_capacity=8, kv_layout=3, **kw)
+    with pytest.raises(DoeError, match="page"):
+        ops.attention_dispatch(buf, buf, buf, buf, kv_capacity=8, kv_layout=2, **kw)
+    with pytest.raises(DoeError, match="kv_len_buffer"):
+        ops.attention_dispatch(buf, buf, buf, buf, kv_capacity=8, kv_len_source=1, **kw)
