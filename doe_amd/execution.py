@@ -229,6 +229,12 @@ def load_step_graph(src) -> StepGraph:
         steps = [_flat_step(v) for v in root["steps"]]
     else:
         raise StepGraphError("step graph has neither 'execution' nor 'steps'")
+    # a decode step needs a prefill step before it (the reference lowering's
+    # MalformedStep for a decode-first list)
+    first_prefill = next((i for i, st in enumerate(steps) if st.phase == "prefill"), None)
+    first_decode = next((i for i, st in enumerate(steps) if st.phase == "decode"), None)
+    if first_decode is not None and (first_prefill is None or first_decode < first_prefill):
+        raise StepGraphError(f"{steps[first_decode].label()} comes before any prefill step")
     pattern = None
     if root.get("layerPattern") is not None:
         lp = root["layerPattern"]

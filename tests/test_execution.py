@@ -117,3 +117,28 @@ def test_model_config_maps_to_decoder_config():
         (18, 640, 4, 1, 256, 262144, 2560, 64)
     with pytest.raises(ex.UnsupportedStep, match="quantFormat"):
         DecoderConfig.from_model_config({**mc, "quantFormat": "q6k"})
+
+
+def test_reference_lowering_known_answers():
+    # the cases of runtime/zig/tests/wgsl/emit_csl_exec_v1_test.zig, as data
+    with pytest.raises(ex.StepGraphError, match="kind"):  # embed declared as a sample step
+        ex.load_step_graph({"grid": {"width": 8, "height": 1}, "steps": [
+            {"phase": "prefill", "op": "embed", "kernelKey": "embed_gather", "kind": "sample"}]})
+    with pytest.raises(ex.StepGraphError, match="before any prefill"):  # decode before prefill
+        ex.load_step_graph({"grid": {"width": 8, "height": 1}, "steps": [
+            {"phase": "decode", "op": "attention", "kernelKey": "attn_0"}]})
+    with pytest.raises(ex.StepGraphError, match="attentionType"):  # "local" is not an attention type
+        ex.load_step_graph({"grid": {"width": 8, "height": 1}, "steps": [
+            {"phase": "prefill", "op": "embed", "kernelKey": "embed_gather"},
+            {"phase": "decode", "op": "attention", "kernelKey": "attn_0", "attentionType": "local"}]})
+    # Gemma 4 routing from layerPattern: decode attention 0 is sliding (512),
+    # attention 1 global
+    g = ex.load_step_graph({"grid": {"width": 8, "height": 1}, "slidingWindowSize": 512,
+                            "layerPattern": {"type": "every_n", "period": 2, "offset": 1}, "steps": [
+                                {"phase": "prefill", "op": "embed", "kernelKey": "embed_gather"},
+                                {"phase": "decode", "op": "attention", "kernelKey": "attn_local"},
+                                {"phase": "decode", "op": "kv_write", "kernelKey": "kv_write"},
+                                {"phase": "decode", "op": "attention", "kernelKey": "attn_global"},
+                                {"phase": "decode", "op": "sample", "kernelKey": "sampler", "kind": "sample"}]})
+    attns = [s for s in g.phase("decode") if s.op == "attention"]
+    assert [ex._window(g, a, i) for i, a in enumerate(attns)] == [512, 0]
