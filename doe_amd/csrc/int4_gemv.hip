@@ -418,7 +418,11 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
         if (g_ws_bytes < need) {
-            if (g_ws) DOE_HIP_CHECK(hipFree(g_ws));
+            if (g_ws) {
+                // queued kernels (any stream) may still read the old workspace
+                DOE_HIP_CHECK(hipDeviceSynchronize());
+                DOE_HIP_CHECK(hipFree(g_ws));
+            }
             g_ws = nullptr;
             g_ws_bytes = 0;
             DOE_HIP_CHECK(hipMalloc(&g_ws, need));

@@ -606,7 +606,11 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
         if (g_ws_bytes < need) {
-            if (g_ws) DOE_HIP_CHECK(hipFree(g_ws));
+            if (g_ws) {
+                // queued kernels (any stream) may still read the old workspace
+                DOE_HIP_CHECK(hipDeviceSynchronize());
+                DOE_HIP_CHECK(hipFree(g_ws));
+            }
             g_ws = nullptr;
             g_ws_bytes = 0;
             DOE_HIP_CHECK(hipMalloc(&g_ws, need));

@@ -900,13 +900,11 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
                         ((uintptr_t)fz.norm_w & 15) == 0;
 #define DOE_GEMV_MFMA_LAUNCH(P, B, X)                                                             \
     do {                                                                                          \
-        static bool attr_set = false;                                                             \
-        if (!attr_set) {                                                                          \
-            DOE_HIP_CHECK(hipFuncSetAttribute((const void *)q4k_gemv_mfma_kernel<P, B, X>,        \
-                                              hipFuncAttributeMaxDynamicSharedMemorySize,         \
-                                              (int)gemv_mfma_lds_bytes(16, B)));                  \
-            attr_set = true;                                                                      \
-        }                                                                                         \
+        /* set once per process; a static's initialisation is thread-safe */                    \
+        static const hipError_t attr_rc = hipFuncSetAttribute(                                    \
+            (const void *)q4k_gemv_mfma_kernel<P, B, X>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+            (int)gemv_mfma_lds_bytes(16, B));                                                     \
+        DOE_HIP_CHECK(attr_rc);                                                                   \
         hipLaunchKernelGGL((q4k_gemv_mfma_kernel<P, B, X>), grid, dim3(64 * nwaves), lds, st, wp, \
                            activation, output, (int)n, (int)k, nb, nbs, fz);                      \
     } while (0)
