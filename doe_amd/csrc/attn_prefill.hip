@@ -413,8 +413,7 @@ int doe_attn_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, vo
     if (kv_len == 0) {
         // no keys: the empty softmax contributes nothing (zero output)
         const size_t bytes = (size_t)q_len * num_heads * kD * (out_bf16 ? 2 : 4);
-        DOE_HIP_CHECK(hipMemsetAsync(out, 0, bytes, st));
-        return DOE_OK;
+        return doe::fill_bytes_async(out, 0, bytes, st);
     }
     const int64_t blocks = (int64_t)a.nqb * a.hq;
     DOE_REQUIRE(blocks <= 0x7fffffff, DOE_E_UNSUPPORTED, "too many blocks");

@@ -21,6 +21,9 @@ void clear_error();
 int hip_fail(hipError_t e, const char *what);
 // Checks that the library was initialised on the calling thread's device.
 int require_init();
+// Fills bytes [dst, dst + bytes) with `value` on a stream with a kernel
+// (capturable into a HIP graph; no memset node).  Returns a DOE status.
+int fill_bytes_async(void *dst, int value, size_t bytes, hipStream_t st);
 // Tuning hooks of individual kernels (0 = automatic).
 int attn_set_splits(int value);
 int attn_set_waves(int value);

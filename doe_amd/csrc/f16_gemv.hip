@@ -194,8 +194,7 @@ int f16_launch(const uint16_t *b_f16, const float *a, float *c, int64_t n, int64
     DOE_REQUIRE(c || fz.argmax_part, DOE_E_INVALID, "null output");
     if (k == 0) {
         DOE_REQUIRE(c && !fz.argmax_part, DOE_E_UNSUPPORTED, "k == 0 with argmax");
-        DOE_HIP_CHECK(hipMemsetAsync(c, 0, (size_t)n * 4, st));
-        return DOE_OK;
+        return doe::fill_bytes_async(c, 0, (size_t)n * 4, st);
     }
     DOE_REQUIRE(b_f16 && a, DOE_E_INVALID, "null pointer");
     DOE_REQUIRE((k % 8) == 0 && k <= 64 * 8 * 16, DOE_E_UNSUPPORTED,

@@ -389,8 +389,7 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     DOE_REQUIRE(y, DOE_E_INVALID, "null output");
     hipStream_t st = (hipStream_t)stream;
     if (k == 0) {
-        DOE_HIP_CHECK(hipMemsetAsync(y, 0, (size_t)m * n * sizeof(float), st));
-        return DOE_OK;
+        return doe::fill_bytes_async(y, 0, (size_t)m * n * sizeof(float), st);
     }
     DOE_REQUIRE(w_u4 && scales_f16 && x, DOE_E_INVALID, "null pointer");
     DOE_REQUIRE(k % 256 == 0, DOE_E_UNSUPPORTED, "int4g32_gemv needs k %% 256 == 0 (got %lld)", (long long)k);

@@ -588,8 +588,7 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
     hipStream_t st = (hipStream_t)stream;
     if (k == 0) {
         // empty reduction: the sum identity
-        DOE_HIP_CHECK(hipMemsetAsync(c, 0, (size_t)m * (size_t)n * sizeof(float), st));
-        return DOE_OK;
+        return doe::fill_bytes_async(c, 0, (size_t)m * (size_t)n * sizeof(float), st);
     }
     DOE_REQUIRE(a_bf16 && b_q4k, DOE_E_INVALID, "null pointer");
     DOE_REQUIRE(((uintptr_t)b_q4k & 15) == 0, DOE_E_INVALID, "weight must be 16-byte aligned");

@@ -852,8 +852,7 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     if (k == 0) {
         // Empty reduction: the sum identity (reference_interpreter.zig:323-327).
         DOE_REQUIRE(!fz.residual && !fz.gated, DOE_E_UNSUPPORTED, "fused epilogues need k > 0");
-        DOE_HIP_CHECK(hipMemsetAsync(output, 0, (size_t)n * sizeof(float), st));
-        return DOE_OK;
+        return doe::fill_bytes_async(output, 0, (size_t)n * sizeof(float), st);
     }
     DOE_REQUIRE(weight_q4k && (activation || fz.attn_o), DOE_E_INVALID, "null pointer");
     DOE_REQUIRE(((uintptr_t)weight_q4k & 15) == 0, DOE_E_INVALID, "weight must be 16-byte aligned");

@@ -31,6 +31,36 @@ int require_init() {
     return DOE_OK;
 }
 
+// byte fill: the unaligned head and tail byte by byte, the middle 16 bytes
+// per store
+__global__ __launch_bounds__(256) void fill_bytes_kernel(uint8_t *dst, size_t head, size_t n16, size_t total,
+                                                         uint32_t v4) {
+    const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
+    const uint4 v = make_uint4(v4, v4, v4, v4);
+    uint4 *mid = reinterpret_cast<uint4 *>(dst + head);
+    for (size_t i = tid; i < n16; i += stride) mid[i] = v;
+    const size_t tail0 = head + n16 * 16;
+    for (size_t i = tid; i < head + (total - tail0); i += stride) {
+        const size_t at = i < head ? i : tail0 + (i - head);
+        dst[at] = (uint8_t)v4;
+    }
+}
+
+int fill_bytes_async(void *dst, int value, size_t bytes, hipStream_t st) {
+    if (bytes == 0) return DOE_OK;
+    uint8_t *p = static_cast<uint8_t *>(dst);
+    size_t head = (16 - ((uintptr_t)p & 15)) & 15;
+    if (head > bytes) head = bytes;
+    const size_t n16 = (bytes - head) / 16;
+    const uint32_t b = (uint32_t)(value & 0xff);
+    size_t blocks = (n16 + 255) / 256;
+    blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
+    hipLaunchKernelGGL(fill_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p, head, n16, bytes,
+                       b * 0x01010101u);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? DOE_OK : hip_fail(e, "fill_bytes_kernel launch");
+}
+
 }  // namespace doe
 
 extern "C" {
@@ -135,8 +165,7 @@ int doe_memset(void *dst, int value, size_t bytes, doe_stream_t stream) {
     if (rc) return rc;
     if (bytes == 0) return DOE_OK;
     DOE_REQUIRE(dst, DOE_E_INVALID, "null pointer");
-    DOE_HIP_CHECK(hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
-    return DOE_OK;
+    return doe::fill_bytes_async(dst, value, bytes, (hipStream_t)stream);
 }
 
 int doe_stream_create(doe_stream_t *stream) {

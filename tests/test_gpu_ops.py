@@ -316,3 +316,44 @@ def test_attention_partials_and_fused_o_projection(dev, ora, kv_len, max_splits,
     ops.attention(up(q), up(kc), up(vc), full, batch=1, num_heads=hq, num_kv_heads=hkv, head_dim=d,
                   kv_len=kv_len, kv_stride=maxs, scale=scale)
     assert rel_l2(full.download().reshape(-1), attn) < 1e-5
+
+
+def test_fills_replay_in_graphs(dev):
+    # Empty reductions clear their outputs and doe_memset fills bytes with a
+    # kernel (no memset node): captured once, replayed with garbage written
+    # in between, every replay rewrites the outputs.
+    import ctypes as C
+
+    from doe_amd import Graph, Stream, _lib
+
+    s = Stream()
+    sp = C.c_void_p(s.handle)
+    m, n = 37, 300
+    c = DeviceBuffer.empty((m, n), np.float32)
+    y = DeviceBuffer.empty((n,), np.float32)
+    raw = DeviceBuffer(4096)
+    dummy = DeviceBuffer(1 << 12)
+
+    def body():
+        _lib.call("doe_q4k_gemm", C.c_void_p(dummy.ptr), C.c_void_p(dummy.ptr), C.c_void_p(c.ptr), m, n, 0, sp)
+        _lib.call("doe_q4k_gemv", C.c_void_p(dummy.ptr), C.c_void_p(dummy.ptr), C.c_void_p(y.ptr), n, 0, sp)
+        _lib.call("doe_memset", C.c_void_p(raw.ptr + 3), 0x5A, 1001, sp)   # unaligned head and tail
+        _lib.call("doe_memset", C.c_void_p(raw.ptr + 2048), 0x00, 1024, sp)  # aligned
+
+    g = Graph.capture(s, body)
+    rng = np.random.default_rng(5)
+    for i in range(4):
+        c.upload(rng.standard_normal((m, n)).astype(np.float32))
+        y.upload(rng.standard_normal(n).astype(np.float32))
+        before = rng.integers(0, 256, 4096, dtype=np.uint8)
+        raw.upload(before)
+        g.launch(s)
+        s.synchronize()
+        assert not c.download().any() and not y.download().any(), i
+        got = raw.download().view(np.uint8)
+        want = before.copy()
+        want[3:1004] = 0x5A
+        want[2048:3072] = 0
+        assert np.array_equal(got, want), i
+    g.destroy()
+    s.destroy()
