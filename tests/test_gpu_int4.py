@@ -81,3 +81,36 @@ def test_int4_rejects_bad_shapes(dev):
         with pytest.raises(_lib.DoeError):
             _lib.call("doe_int4g32_gemv", C.c_void_p(buf.ptr), C.c_void_p(buf.ptr), C.c_void_p(buf.ptr),
                       C.c_void_p(buf.ptr), m, 4, k, C.c_void_p(None))
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 25600, 5120), (8, 5120, 25600)])
+def test_int4_ffn_shapes_streaming(dev, ora, m, n, k):
+    # the config-4 FFN projections: enough (row block, K range) items that the
+    # automatic choice is the streaming kernel (workgroups walk row blocks)
+    rng = np.random.default_rng(n + k)
+    w, s = random_int4(rng, n, k)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_int4g32(up(w), up(s), up(x), out, m, n, k)
+    err = rel_l2(out.download(), ora.int4g32_gemv(w, s, x, m, n, k))
+    print(f"[int4 ffn {m}x{n}x{k}] rel_l2 {err:.2e}", flush=True)
+    assert err <= 1e-5
+
+
+@pytest.mark.parametrize("kernel", [1, 2])
+@pytest.mark.parametrize("m,n,k", [(8, 3000, 2048), (3, 1000, 7168), (1, 64 * 97 + 5, 1024)])
+def test_int4_both_kernels_match_oracle(dev, ora, kernel, m, n, k):
+    # one-shot (1) and streaming (2) workgroups forced on the same shapes,
+    # ragged row counts and batches below 8 included
+    rng = np.random.default_rng(m * n + k)
+    w, s = random_int4(rng, n, k)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    _lib.call("doe_tune_set", b"int4_gemv.kernel", kernel)
+    try:
+        ops.matmul_int4g32(up(w), up(s), up(x), out, m, n, k)
+        got = out.download()
+    finally:
+        _lib.call("doe_tune_set", b"int4_gemv.kernel", 0)
+    err = rel_l2(got, ora.int4g32_gemv(w, s, x, m, n, k))
+    assert err <= 1e-5, (kernel, err)
