@@ -862,10 +862,11 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     const int nb = (int)((k + 255) / 256);
     const int nchunk = (int)((k + 63) / 64);
     const uint8_t *wp = (const uint8_t *)weight_q4k;
-    // Matrix-core kernel up to 64 blocks (up to four per wave; the
-    // attention-combine prologue is single-block); measured faster than the
-    // dot-product kernel on every decode shape.  `q4k_gemv.kernel` = 1 forces
-    // the dot-product kernel where its LDS holds the activation (k <~ 12K).
+    // Matrix-core kernel, up to 64 blocks per workgroup (up to four per wave;
+    // the attention-combine prologue is single-block) and K split beyond;
+    // measured faster than the dot-product kernel on every decode shape.
+    // `q4k_gemv.kernel` = 1 forces the dot-product kernel where its LDS holds
+    // the activation (k <~ 12K).
     if (g_num_cus == 0) {
         int dev = 0, cus = 0;
         DOE_HIP_CHECK(hipGetDevice(&dev));
@@ -879,8 +880,23 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     // fewer workgroups than CUs.
     const int64_t row_groups = (n + 15) / 16;
     int ksplit = 1;
-    if (nb > 1 && fz.residual == output && !fz.norm_w && !fz.gated && !fz.rope_kv &&
-        row_groups < g_num_cus && g_tune_ksplit != 1) {
+    if (nb > kMfmaMaxBlocks) {
+        // Past 64 blocks a row no longer fits one workgroup: K ranges of at
+        // most 16 blocks (one per wave) add their row sums atomically into y,
+        // which starts at the residual (or zero).  The fused prologues and
+        // epilogues need whole rows.
+        DOE_REQUIRE(!fz.norm_w && !fz.gated && !fz.rope_kv && !fz.attn_o, DOE_E_UNSUPPORTED,
+                    "k=%lld (%d Q4_K blocks > %d): only the plain and residual forms", (long long)k, nb,
+                    kMfmaMaxBlocks);
+        if (fz.residual && fz.residual != output) {
+            DOE_HIP_CHECK(hipMemcpyAsync(output, fz.residual, (size_t)n * sizeof(float), hipMemcpyDeviceToDevice, st));
+        } else if (!fz.residual) {
+            rc = doe::fill_bytes_async(output, 0, (size_t)n * sizeof(float), st);
+            if (rc) return rc;
+        }
+        ksplit = (nb + 15) / 16;
+    } else if (nb > 1 && fz.residual == output && !fz.norm_w && !fz.gated && !fz.rope_kv &&
+               row_groups < g_num_cus && g_tune_ksplit != 1) {
         const int64_t fill = (g_num_cus + row_groups - 1) / row_groups;
         ksplit = (int)(fill < nb ? fill : nb);
         if (ksplit < (nb + 15) / 16) ksplit = (nb + 15) / 16;
@@ -888,7 +904,7 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     const int nbs = (nb + ksplit - 1) / ksplit;  // blocks per split
     int bpw = nbs <= 16 ? 1 : (nbs <= 32 ? 2 : (nbs <= 48 ? 3 : 4));
     if (g_tune_bpw > bpw && g_tune_bpw <= 4 && !fz.attn_o) bpw = g_tune_bpw;
-    const bool mfma_ok = nb <= kMfmaMaxBlocks && (bpw == 1 || !fz.attn_o);
+    const bool mfma_ok = nbs <= kMfmaMaxBlocks && (bpw == 1 || !fz.attn_o);
     const bool dot_ok = gemv_lds_bytes(nchunk, 8) <= 64 * 1024;
     const bool use_mfma = g_tune_kernel == 1 ? !dot_ok && mfma_ok : mfma_ok;
     if (use_mfma) {

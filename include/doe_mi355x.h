@@ -100,7 +100,8 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
  * fused_gemv_dequant, runtime/zig/src/doe_wgsl/emit_csl_fused.zig:47-200,
  * exported symbols activation/weight/output) and the reference interpreter's
  * fused_gemv (runtime/zig/src/tsir/reference_interpreter.zig:169-394).
- * activation: f32[k], output: f32[n]. */
+ * activation: f32[k], output: f32[n]; k <= 65536 (past 16384 the K ranges
+ * add into output atomically: the f32 summation order varies run to run). */
 int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
                  int64_t n, int64_t k, doe_stream_t stream);
 

@@ -196,3 +196,37 @@ def test_gemv_inplace_residual_k_split(dev, ora, n, k):
             ops.tune("q4k_gemv.ksplit", 0)
         assert rel_l2(got[split], want) < 1e-5, split
     assert rel_l2(got[0], got[1]) < 1e-6
+
+
+@pytest.mark.parametrize("k", [21504, 25600, 65536])
+def test_gemv_large_k_splits(dev, ora, k):
+    # past 64 Q4_K blocks per row the K ranges add into y: plain (y cleared),
+    # residual into a separate output (y starts as the residual) and in place
+    rng = np.random.default_rng(k)
+    n = 333
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k, dtype=np.float32)
+    r = rng.standard_normal(n, dtype=np.float32)
+    want = ora.q4k_gemv(w, x, n, k)
+    dw, dx = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x)
+    y = DeviceBuffer.from_array(np.full(n, 7.0, np.float32))  # stale contents are overwritten
+    ops.matmul_q4k(dw, dx, y, n, k)
+    assert rel_l2(y.download(), want) <= 1e-5
+    res = DeviceBuffer.from_array(r)
+    out = DeviceBuffer.from_array(np.full(n, -3.0, np.float32))
+    ops.matmul_q4k_fused(dw, dx, out, n, k, residual=res)
+    assert rel_l2(out.download(), want + r) <= 1e-5
+    ops.matmul_q4k_fused(dw, dx, res, n, k, residual=res)  # in place
+    assert rel_l2(res.download(), want + r) <= 1e-5
+    # captured: the clear / residual copy replay with the GEMV
+    s = Stream()
+    g = Graph.capture(s, lambda: ops.matmul_q4k(dw, dx, y, n, k, s))
+    for i in range(3):
+        y.upload(np.full(n, float(i + 1), np.float32))
+        g.launch(s)
+        s.synchronize()
+        assert rel_l2(y.download(), want) <= 1e-5, i
+    g.destroy()
+    s.destroy()
+    with pytest.raises(DoeError, match="plain and residual"):
+        ops.matmul_q4k_fused(dw, dx, out, n, k, norm_weight=DeviceBuffer.from_array(np.ones(k, np.float32)))
