@@ -450,6 +450,55 @@ def bench_config4(args, doe):
                         "positions (f16 KV, 1 GiB), int4 group-32 GEMVs with f16 scales at M=8", **res}
 
 
+Q8_N, Q8_K = 9216, 2304
+
+
+def bench_q8_0(args, doe):
+    """The Q8_0 GEMV at the headline GEMV's shape (9216 x 2304, 34-byte
+    blocks): rotating weight copies (more bytes than the 256 MB Infinity
+    Cache) replayed in a HIP graph, HIP events around the replays."""
+    from doe_amd import DeviceBuffer, Event, Graph, Stream, ops, q8_0
+    from oracle import oracle as ora
+
+    rng = np.random.default_rng(7)
+    w = q8_0.random_q8_0(rng, Q8_N, Q8_K)
+    x = rng.standard_normal(Q8_K, dtype=np.float32)
+    copies = max(2, -(-384 * 2 ** 20 // w.nbytes))
+    bufs = [DeviceBuffer.from_array(w)]
+    for _ in range(copies - 1):
+        b = DeviceBuffer(w.nbytes)
+        b.copy_from(bufs[0])
+        bufs.append(b)
+    dx = DeviceBuffer.from_array(x)
+    dy = DeviceBuffer.empty((Q8_N,), np.float32)
+    s = Stream()
+    graph = Graph.capture(s, lambda: [ops.matmul_q8_0(c, dx, dy, Q8_N, Q8_K, stream=s) for c in bufs])
+    graph.launch(s)
+    s.synchronize()
+    reps = max(1, -(-args.steps // copies))
+    e0, e1 = Event(), Event()
+    e0.record(s)
+    for _ in range(reps):
+        graph.launch(s)
+    e1.record(s)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / (reps * copies)
+    rel = float(np.linalg.norm(dy.download().astype(np.float64) - ora.q8_0_gemv(w, x, Q8_N, Q8_K)) /
+                np.linalg.norm(ora.q8_0_gemv(w, x, Q8_N, Q8_K)))
+    graph.destroy()
+    s.destroy()
+    for b in bufs:
+        b.free()
+    byt = w.nbytes + Q8_K * 4 + Q8_N * 4
+    gbs = byt / (ms * 1e-3) / 1e9
+    log(f"q8_0 gemv {Q8_N}x{Q8_K}: {ms * 1e3:.2f} us, {gbs:.1f} GB/s, rel_l2 {rel:.2e}")
+    return {"workload": f"q8_0_gemv M=1 N={Q8_N} K={Q8_K} (Q8_0 weights, f32 activation/output), "
+                        f"{copies} rotating weight copies, HIP-graph replay",
+            "kernel": "q8_0_gemv_kernel<4> (doe_amd/csrc/q8_0_gemv.hip)",
+            "us_per_call": round(ms * 1e3, 3), "bytes_per_call": byt, "achieved_gbs": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "rel_l2_vs_oracle": rel}
+
+
 def traffic_bytes(summary: str):
     """HBM bytes per launch recorded in a committed rocprofv3 summary
     (line `traffic_bytes_per_launch: <int>`), or None."""
@@ -527,6 +576,7 @@ def main() -> int:
     gemm = None if args.no_gemm else bench_gemm(args, doe_amd)
     pfa = None if args.no_gemm else bench_prefill_attention(args, doe_amd)
     c4 = None if args.no_gemm else bench_config4(args, doe_amd)
+    q8 = bench_q8_0(args, doe_amd)
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of the single-threaded oracle")
@@ -569,6 +619,7 @@ def main() -> int:
         "prefill_gemm": gemm,
         "prefill_attention": pfa,
         "config4_decode_layer": c4,
+        "q8_0_gemv": q8,
     }
     print(json.dumps(out), flush=True)
     return 0

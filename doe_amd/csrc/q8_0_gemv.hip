@@ -1,0 +1,214 @@
+// q8_0_gemv.hip -- Q8_0-weight GEMV for gfx950.
+//
+// y[i] = sum_k dequant(W)[i][k] * x[k] (+ residual[i]).  Q8_0 blocks
+// (runtime/zig/src/doe_wgsl/csl_spec.zig:122-152, the `q8_0` quant format of
+// emit_csl_host.zig:62) hold 32 weights in 34 bytes: an f16 scale d, then 32
+// int8 quants q; weight = d * q.  Weights are row-wise: each row is
+// nb = ceil(k / 32) blocks (the tail block zero padded), so a row is nb * 34
+// bytes and blocks are only 2-byte aligned.
+//
+// Decomposition: a workgroup of four waves first issues the loads of its first
+// blocks, then stages x into LDS as 36-float rows per block (32 values + 4 of
+// padding: lanes on consecutive blocks hit distinct banks) together with the
+// per-block sums sx[b].  A wave owns groups of R consecutive rows; the R * nb
+// (row, block) units of a group are spread over its lanes (unit u = lane +
+// 64 t), so short rows still fill the wave.  A unit is three buffer loads
+// (16 + 16 + 4 bytes from the block's dword-aligned start: no 64-bit address
+// registers, and bytes past the matrix read as zero), one v_perm per quant
+// dword to undo the 2-byte misalignment, and 32 FMAs of u = q + 128 (the
+// sign bit flipped, so each byte converts with one v_cvt_f32_ubyte) against x:
+// block dot = d * (sum u * x - 128 * sx[b]).  The next unit's loads are issued
+// before the current unit is computed.  Bound: HBM (34 bytes per 32 weights).
+#include "common.h"
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;               // waves per workgroup
+constexpr int kXStride = 36;            // floats per staged x block (32 + pad)
+constexpr int kMaxBlocks = 1024;        // k <= 32768: 1024 * 148 bytes of LDS
+constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads zero
+
+struct Blk {
+    u32x4 a, b;
+    uint32_t c;
+};
+
+__device__ __forceinline__ Blk load_blk(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    const uint32_t al = off & ~3u;
+    Blk r;
+    r.a = __builtin_amdgcn_raw_buffer_load_b128(rs, al, 0, 0);
+    r.b = __builtin_amdgcn_raw_buffer_load_b128(rs, al + 16, 0, 0);
+    r.c = __builtin_amdgcn_raw_buffer_load_b32(rs, al + 32, 0, 0);
+    return r;
+}
+
+// d * sum_j q_j * x_j for the block whose 34 bytes start at byte (off & 3)
+// of the loaded dwords; xb = the block's staged x, sxb = their sum.
+__device__ __forceinline__ float blk_dot(const Blk &bk, uint32_t off, const float *xb, float sxb) {
+    const uint32_t dw[9] = {bk.a.x, bk.a.y, bk.a.z, bk.a.w, bk.b.x, bk.b.y, bk.b.z, bk.b.w, bk.c};
+    const uint32_t sh = (off & 2u) << 3;                    // 0 or 16
+    const uint32_t sel = sh ? 0x07060504u : 0x05040302u;   // quant bytes at 4 or 2
+    const float d = doe_half_bits_to_float(__builtin_amdgcn_ubfe(dw[0], sh, 16));
+    const float4 *x4 = reinterpret_cast<const float4 *>(xb);
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t u = __builtin_amdgcn_perm(dw[j + 1], dw[j], sel) ^ 0x80808080u;
+        const float4 xv = x4[j];
+        s0 = fmaf((float)(u & 0xffu), xv.x, s0);
+        s1 = fmaf((float)((u >> 8) & 0xffu), xv.y, s1);
+        s0 = fmaf((float)((u >> 16) & 0xffu), xv.z, s0);
+        s1 = fmaf((float)(u >> 24), xv.w, s1);
+    }
+    return d * fmaf(-128.0f, sxb, s0 + s1);
+}
+
+template <int R>
+__global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
+    const uint8_t *__restrict__ w, const float *__restrict__ x, float *y, const float *res, int n,
+    int k, int nb, int q64, int r64) {
+    extern __shared__ float lds[];
+    float *xs = lds;                          // [nb][kXStride]
+    float *sx = lds + (size_t)nb * kXStride;  // [nb]
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * kWaves;
+    const int ngroups = (n + R - 1) / R;
+    const uint32_t rb = (uint32_t)nb * 34u;  // row bytes
+    // first unit of every group: row lane / nb, block lane % nb
+    const int rl0 = lane / nb, b0 = lane - rl0 * nb;
+
+    auto group_rsrc = [&](int g, int &rows, uint32_t &s0) {
+        rows = min(R, n - g * R);
+        const size_t base = (size_t)g * R * rb;
+        s0 = (uint32_t)(base & 3u);
+        return __builtin_amdgcn_make_buffer_rsrc((void *)(w + base - s0), (short)0,
+                                                 (int)((s0 + (uint32_t)rows * rb + 3u) & ~3u),
+                                                 0x00020000);
+    };
+
+    // issue this wave's first block loads before staging x
+    // (a wave without a group reads out of range: zeros, no access)
+    int g = wave, rows = 0;
+    uint32_t s0 = 0;
+    __amdgpu_buffer_rsrc_t rs = group_rsrc(min(g, ngroups - 1), rows, s0);
+    uint32_t cur_off =
+        (g < ngroups && rl0 < rows) ? s0 + (uint32_t)rl0 * rb + 34u * (uint32_t)b0 : kOutOfRange;
+    Blk cur = load_blk(rs, cur_off);
+
+    for (int i = threadIdx.x; i < nb * 32; i += kWaves * 64)
+        xs[(i >> 5) * kXStride + (i & 31)] = i < k ? x[i] : 0.0f;
+    __syncthreads();
+    for (int b = threadIdx.x; b < nb; b += kWaves * 64) {
+        const float4 *p = reinterpret_cast<const float4 *>(xs + b * kXStride);
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float4 v = p[j];
+            s += v.x + v.y + v.z + v.w;
+        }
+        sx[b] = s;
+    }
+    __syncthreads();
+
+    for (; g < ngroups; g += nwaves) {
+        if (g != wave) {
+            rs = group_rsrc(g, rows, s0);
+            cur_off = rl0 < rows ? s0 + (uint32_t)rl0 * rb + 34u * (uint32_t)b0 : kOutOfRange;
+            cur = load_blk(rs, cur_off);
+        }
+        const int rounds = (rows * nb + 63) >> 6;
+        int rl = rl0, b = b0;
+        float acc[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) acc[j] = 0.0f;
+        for (int t = 0; t < rounds; ++t) {
+            int nrl = rl + q64, nbk = b + r64;
+            if (nbk >= nb) {
+                nbk -= nb;
+                ++nrl;
+            }
+            const uint32_t nxt_off =
+                (t + 1 < rounds && nrl < rows) ? s0 + (uint32_t)nrl * rb + 34u * (uint32_t)nbk : kOutOfRange;
+            const Blk nxt = load_blk(rs, nxt_off);
+            const float v = blk_dot(cur, cur_off, xs + b * kXStride, sx[b]);
+#pragma unroll
+            for (int j = 0; j < R; ++j) acc[j] += (rl == j) ? v : 0.0f;
+            cur = nxt;
+            cur_off = nxt_off;
+            rl = nrl;
+            b = nbk;
+        }
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            float s = acc[j];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+            if (lane == 0 && j < rows) {
+                const int row = g * R + j;
+                y[row] = res ? s + res[row] : s;
+            }
+        }
+    }
+}
+
+int g_num_cus = 0;
+
+template <int R>
+int q8_0_launch(const uint8_t *w, const float *x, float *y, const float *res, int n, int k, int nb,
+                hipStream_t st) {
+    static const hipError_t attr_rc = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&q8_0_gemv_kernel<R>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxBlocks * (kXStride + 1) * 4);
+    DOE_HIP_CHECK(attr_rc);
+    const long ngroups = (n + R - 1) / R;
+    long blocks = (ngroups + kWaves - 1) / kWaves;
+    const long cap = (long)g_num_cus * 8;
+    if (blocks > cap) blocks = cap;
+    const size_t lds = (size_t)nb * (kXStride + 1) * 4;
+    hipLaunchKernelGGL(q8_0_gemv_kernel<R>, dim3((unsigned)blocks), dim3(kWaves * 64), lds, st, w,
+                       x, y, res, n, k, nb, 64 / nb, 64 % nb);
+    DOE_LAUNCH_CHECK("q8_0_gemv_kernel");
+    return DOE_OK;
+}
+
+}  // namespace
+
+extern "C" int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, float *output,
+                             int64_t n, int64_t k, const float *residual, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    const hipStream_t st = (hipStream_t)stream;
+    DOE_REQUIRE(n >= 0 && k >= 0 && n <= 0x7fffffff, DOE_E_INVALID, "bad q8_0_gemv shape");
+    if (n == 0) return DOE_OK;
+    DOE_REQUIRE(output, DOE_E_INVALID, "null output");
+    if (k == 0) {  // empty reductions: the residual, or zeros
+        if (!residual) return doe::fill_bytes_async(output, 0, (size_t)n * 4, st);
+        if (residual != output)
+            DOE_HIP_CHECK(hipMemcpyAsync(output, residual, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
+        return DOE_OK;
+    }
+    DOE_REQUIRE(weight_q8_0 && activation, DOE_E_INVALID, "null pointer");
+    const int64_t nb = (k + 31) / 32;
+    DOE_REQUIRE(nb <= kMaxBlocks, DOE_E_UNSUPPORTED,
+                "q8_0_gemv needs k <= %d (got %lld)", kMaxBlocks * 32, (long long)k);
+    DOE_REQUIRE(((uintptr_t)weight_q8_0 & 3) == 0, DOE_E_INVALID, "Q8_0 weights must be 4-byte aligned");
+    DOE_REQUIRE(((uintptr_t)activation & 3) == 0 && ((uintptr_t)output & 3) == 0 &&
+                    ((uintptr_t)residual & 3) == 0,
+                DOE_E_INVALID, "activation, output and residual must be 4-byte aligned");
+    if (g_num_cus == 0) {
+        int dev = 0, cus = 0;
+        DOE_HIP_CHECK(hipGetDevice(&dev));
+        DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        g_num_cus = cus > 0 ? cus : 256;
+    }
+    const uint8_t *w = (const uint8_t *)weight_q8_0;
+    // four-row groups once they still give two workgroups per CU, else fewer
+    if (n >= (int64_t)g_num_cus * 2 * kWaves * 4)
+        return q8_0_launch<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
+    if (n >= (int64_t)g_num_cus * 2 * kWaves * 2)
+        return q8_0_launch<2>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
+    return q8_0_launch<1>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
+}

@@ -16,6 +16,7 @@ import numpy as np
 
 from . import _lib
 from . import q4k as _q4k
+from . import q8_0 as _q8_0
 from .device import DeviceBuffer, _stream_ptr
 
 
@@ -61,6 +62,22 @@ def matmul_q4k_gemm(a_bf16: DeviceBuffer, weight: DeviceBuffer, output: DeviceBu
     _need(a_bf16, m * k * 2, "a")
     _need(output, m * n * 4, "output")
     _lib.call("doe_q4k_gemm", _p(a_bf16), _p(weight), _p(output), m, n, k, _stream_ptr(stream))
+
+
+def matmul_q8_0(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int,
+                residual: DeviceBuffer | None = None, stream=None) -> None:
+    """``matmul`` with quantFormat ``q8_0`` at M = 1: output f32[n] =
+    dequant(weight)[n][k] @ activation f32[k] (+ residual f32[n]); weight
+    row-wise Q8_0 (34-byte blocks: f16 scale, 32 int8 quants)."""
+    expected = n * _q8_0.row_bytes(k)
+    if weight.nbytes != expected:
+        raise ValueError(f"Q8_0 rowwise byte length {weight.nbytes} != expected {expected}")
+    _need(activation, k * 4, "activation")
+    _need(output, n * 4, "output")
+    if residual is not None:
+        _need(residual, n * 4, "residual")
+    _lib.call("doe_q8_0_gemv", _p(weight), _p(activation), _p(output), n, k,
+              None if residual is None else _p(residual), _stream_ptr(stream))
 
 
 def matmul_int4g32(weight_u4: DeviceBuffer, scales_f16: DeviceBuffer, x: DeviceBuffer, output: DeviceBuffer,

@@ -11,7 +11,8 @@ An RDRR artifact is a directory holding ``manifest.json`` and shard files
     shard, ``"shard"``, ``"offset"``, ``"size"`` on the tensor itself.  A
     tensor's bytes are its spans concatenated in order.
 
-``Q4_K_M`` tensors are row-wise: ``shape [rows, cols...]``, each row
+``Q4_K_M`` and ``Q8_0`` tensors are row-wise (Q8_0: ``ceil(cols / 32)``
+blocks of 34 bytes per row).  ``Q4_K_M`` tensors are row-wise: ``shape [rows, cols...]``, each row
 ``ceil(cols / 256)`` blocks of 144 bytes (the tail block zero-padded), which
 is the layout the GEMV and GEMM kernels read.  Step-graph weight keys
 (``layer.3.self_attn.q_proj``, ``embed_tokens``, ``norm``, ...) resolve to the
@@ -27,6 +28,7 @@ from pathlib import Path
 import numpy as np
 
 from . import q4k as _q4k
+from . import q8_0 as _q8_0
 from .ops import interleave_rope_rows
 
 
@@ -158,6 +160,29 @@ class RdrrArtifact:
         data = self.read(name)
         if data.size != rows * rb:
             raise RdrrError(f"{name}: {data.size} bytes, a {rows} x {cols} Q4_K_M matrix has {rows * rb}")
+        return data.reshape(rows, rb)
+
+    def q8_0_rows(self, name: str) -> np.ndarray:
+        """A row-wise Q8_0 tensor as its row bytes [rows][ceil(cols/32)*34]
+        (RDRR dtype "Q8_0": blockSizeElements 32, blockSizeBytes 34,
+        bench/tools/run_doe_csl_int4ple_transcript.py:1559-1565).  The byte
+        count must also pass the reference's Q8_0 size check (a nonzero whole
+        number of blocks, runtime/zig/src/doe_wgsl/csl_spec.zig:135-140)."""
+        t = self.meta(name)
+        if t.get("dtype") != "Q8_0":
+            raise RdrrError(f"{name}: dtype {t.get('dtype')!r} is not Q8_0")
+        if t.get("layout", "row") != "row":
+            raise RdrrError(f"{name}: Q8_0 layout {t.get('layout')!r} is not row")
+        shape = [int(v) for v in t.get("shape", [])]
+        if len(shape) < 2:
+            raise RdrrError(f"{name}: shape {shape} is not a matrix")
+        rows, cols = shape[0], math.prod(shape[1:])
+        rb = _q8_0.row_bytes(cols)
+        data = self.read(name)
+        if data.size == 0 or data.size % _q8_0.BLOCK_BYTES:
+            raise RdrrError(f"{name}: {data.size} bytes is not a whole number of Q8_0 blocks")
+        if data.size != rows * rb:
+            raise RdrrError(f"{name}: {data.size} bytes, a {rows} x {cols} Q8_0 matrix has {rows * rb}")
         return data.reshape(rows, rb)
 
     def dense(self, name: str, dtype) -> np.ndarray:

@@ -105,6 +105,20 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
 int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
                  int64_t n, int64_t k, doe_stream_t stream);
 
+/* Q8_0 GEMV: output[i] = sum_k dequant(W)[i][k] * activation[k] (+
+ * residual[i] when residual != NULL; residual == output is allowed).  W is
+ * row-wise Q8_0: each row ceil(k / 32) blocks of 34 bytes, an f16 scale d then
+ * 32 int8 quants q, weight = d * q (the block of
+ * runtime/zig/src/doe_wgsl/csl_spec.zig:122-152, Q8_0_BLOCK_BYTES = 34; the
+ * `q8_0` matmul quant format of emit_csl_host.zig:62 / emit_csl_exec_v1.zig:
+ * 279-284; RDRR dtype "Q8_0", blockSizeElements 32, blockSizeBytes 34,
+ * bench/tools/run_doe_csl_int4ple_transcript.py:1532-1565), the tail block
+ * zero padded.  Replaces the decode `matmul` step at M = 1 when the model's
+ * quantFormat is q8_0.  Weights 4-byte aligned (rows and blocks are only
+ * 2-byte aligned), k <= 32768, f32 accumulation. */
+int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, float *output, int64_t n,
+                  int64_t k, const float *residual, doe_stream_t stream);
+
 /* The attention output projection of one sequence with the split-attention
  * combine folded into its activation load: output[i] = sum_k
  * dequant(W)[i][k] * attn[k] (+ residual[i]), attn = the combine of the

@@ -309,6 +309,45 @@ int ora_int4g32_gemv(const uint32_t *q, const uint16_t *scales, const float *x, 
     return 0;
 }
 
+int64_t ora_q8_0_element_count(int64_t bytes) {
+    /* runtime/zig/src/doe_wgsl/csl_spec.zig:135-153: a zero size or one that
+     * is not a whole number of 34-byte blocks is invalid; else 32 elements per
+     * block. */
+    if (bytes <= 0 || bytes % 34 != 0) return -1;
+    return bytes / 34 * 32;
+}
+
+/* Weight (row, col) of row-wise Q8_0: block col / 32 of the row, whose bytes
+ * are the f16 scale d (little-endian) then 32 int8 quants
+ * (csl_spec.zig:121-125); weight = f32(q) * d. */
+static float q8_0_weight(const uint8_t *w, int64_t row, int64_t col, int64_t nb) {
+    const uint8_t *blk = w + (row * nb + col / 32) * 34;
+    float d = ora_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    return (float)(int8_t)blk[2 + col % 32] * d;
+}
+
+int ora_q8_0_dequant(const uint8_t *w, float *out, int64_t n, int64_t k) {
+    if (n < 0 || k < 0) return -1;
+    int64_t nb = (k + 31) / 32;
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t c = 0; c < k; ++c) out[r * k + c] = q8_0_weight(w, r, c, nb);
+    return 0;
+}
+
+int ora_q8_0_gemv(const uint8_t *w, const float *x, const float *residual, float *y, int64_t n,
+                  int64_t k) {
+    /* y[r] = f32 left-fold over k of weight * x, then + residual[r]: the
+     * accumulation of ora_int4g32_gemv, so equal weights give equal sums. */
+    if (n < 0 || k < 0) return -1;
+    int64_t nb = (k + 31) / 32;
+    for (int64_t r = 0; r < n; ++r) {
+        float acc = 0.0f;
+        for (int64_t c = 0; c < k; ++c) acc += q8_0_weight(w, r, c, nb) * x[c];
+        y[r] = residual ? acc + residual[r] : acc;
+    }
+    return 0;
+}
+
 /* ------------------------------------------------------------------------- */
 /* Normalisation and elementwise ops.                                         */
 /* ------------------------------------------------------------------------- */

@@ -48,6 +48,14 @@ int ora_f16_gemv(const uint16_t *b, const float *a, float *c, int64_t n, int64_t
                  float alpha);
 int ora_int4g32_gemv(const uint32_t *q, const uint16_t *scales, const float *x, float *y,
                      int64_t m, int64_t n, int64_t k);
+/* Q8_0 (34-byte blocks: f16 scale, 32 int8 quants).  element_count returns
+ * the dequantised element count of a buffer, or -1 where the reference's
+ * validator rejects its size; dequant and gemv read row-wise Q8_0 rows of
+ * ceil(k / 32) blocks. */
+int64_t ora_q8_0_element_count(int64_t bytes);
+int ora_q8_0_dequant(const uint8_t *w, float *out, int64_t n, int64_t k);
+int ora_q8_0_gemv(const uint8_t *w, const float *x, const float *residual, float *y, int64_t n,
+                  int64_t k);
 
 /* ---- elementwise / normalisation ---------------------------------------- */
 int ora_rmsnorm(const float *x, const float *w, float *out, int64_t rows, int64_t h,

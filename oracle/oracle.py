@@ -46,6 +46,9 @@ def lib() -> C.CDLL:
             "ora_f32_gemv": ([vp, vp, vp, i64, i64], i32),
             "ora_f16_gemv": ([vp, vp, vp, i64, i64, f32], i32),
             "ora_int4g32_gemv": ([vp, vp, vp, vp, i64, i64, i64], i32),
+            "ora_q8_0_element_count": ([i64], i64),
+            "ora_q8_0_dequant": ([vp, vp, i64, i64], i32),
+            "ora_q8_0_gemv": ([vp, vp, vp, vp, i64, i64], i32),
             "ora_rmsnorm": ([vp, vp, vp, i64, i64, f32, i32], i32),
             "ora_rope_table": ([vp, i64, i64, C.c_double], i32),
             "ora_rope": ([vp, vp, i64, i64, i64, i64], i32),
@@ -157,6 +160,31 @@ def int4g32_gemv(q_u32: np.ndarray, scales_f16: np.ndarray, x: np.ndarray, m: in
     x = _c(x, np.float32)
     y = np.zeros((m, n), np.float32)
     _ok(lib().ora_int4g32_gemv(_ptr(q), _ptr(s), _ptr(x), _ptr(y), m, n, k), "int4g32_gemv")
+    return y
+
+
+def q8_0_element_count(nbytes: int) -> int | None:
+    v = lib().ora_q8_0_element_count(nbytes)
+    return None if v < 0 else int(v)
+
+
+def q8_0_dequant(w: np.ndarray, n: int, k: int) -> np.ndarray:
+    w = _c(w, np.uint8)
+    if w.size != n * ((k + 31) // 32) * 34:
+        raise ValueError("Q8_0 byte count does not match n x k")
+    out = np.zeros((n, k), np.float32)
+    _ok(lib().ora_q8_0_dequant(_ptr(w), _ptr(out), n, k), "q8_0_dequant")
+    return out
+
+
+def q8_0_gemv(w: np.ndarray, x: np.ndarray, n: int, k: int, residual: np.ndarray | None = None) -> np.ndarray:
+    w = _c(w, np.uint8)
+    if w.size != n * ((k + 31) // 32) * 34:
+        raise ValueError("Q8_0 byte count does not match n x k")
+    x = _c(x, np.float32)
+    r = None if residual is None else _c(residual, np.float32)
+    y = np.zeros(n, np.float32)
+    _ok(lib().ora_q8_0_gemv(_ptr(w), _ptr(x), None if r is None else _ptr(r), _ptr(y), n, k), "q8_0_gemv")
     return y
 
 

@@ -1,0 +1,111 @@
+"""GPU parity of the Q8_0 GEMV (doe_q8_0_gemv) against the CPU oracle's f32
+left-fold (ora_q8_0_gemv), through the C ABI.  Contract: rel-L2 <= 1e-3.
+Shapes cover one-block rows, ragged tails, odd block counts (rows that start
+2 bytes off a dword), the 1-, 2- and 4-row wave groups, more groups than the
+persistent grid and the largest k; plus residuals, empty reductions, extreme
+quants and the argument checks."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from doe_amd import DeviceBuffer, DoeError, Graph, Stream, _lib, ops, q8_0
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+@pytest.mark.parametrize("n,k", [(1, 32), (3, 40), (5, 1000), (64, 2048), (2304, 2304), (9216, 2304),
+                                 (2304, 9216), (5000, 96), (10000, 320), (65539, 256), (64, 32768),
+                                 (7, 32767), (130, 7)])
+def test_q8_0_gemv_matches_oracle(dev, ora, n, k):
+    print(f"q8_0_gemv n={n} k={k}", flush=True)
+    rng = np.random.default_rng(n * 7 + k)
+    w = q8_0.random_q8_0(rng, n, k)
+    x = rng.standard_normal(k, dtype=np.float32)
+    out = DeviceBuffer.empty((n,), np.float32)
+    ops.matmul_q8_0(DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), out, n, k)
+    err = rel_l2(out.download(), ora.q8_0_gemv(w, x, n, k))
+    assert err <= 1e-3, err
+    assert err <= 1e-5, err  # f32 sums of exact products: ~1e-7 expected
+
+
+def test_q8_0_gemv_residual_in_place_and_separate(dev, ora):
+    rng = np.random.default_rng(11)
+    n, k = 3000, 544
+    w = q8_0.random_q8_0(rng, n, k)
+    x = rng.standard_normal(k, dtype=np.float32)
+    r = rng.standard_normal(n, dtype=np.float32)
+    want = ora.q8_0_gemv(w, x, n, k, residual=r)
+    dw, dx = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x)
+    dr = DeviceBuffer.from_array(r)
+    out = DeviceBuffer.empty((n,), np.float32)
+    ops.matmul_q8_0(dw, dx, out, n, k, residual=dr)
+    assert rel_l2(out.download(), want) <= 1e-5
+    ops.matmul_q8_0(dw, dx, dr, n, k, residual=dr)  # y += W x in place
+    assert rel_l2(dr.download(), want) <= 1e-5
+
+
+def test_q8_0_gemv_extreme_quants_and_negative_scales(dev, ora):
+    rng = np.random.default_rng(12)
+    n, k = 256, 1024
+    nb = k // 32
+    q = rng.choice(np.array([-128, 127, -1, 0]), (n, nb, 32))
+    d = rng.choice(np.array([-2.0, 0.5, -6.1e-5, 1024.0]), (n, nb))
+    w = q8_0.pack_rows(d, q)
+    x = (rng.standard_normal(k) * 100).astype(np.float32)
+    out = DeviceBuffer.empty((n,), np.float32)
+    ops.matmul_q8_0(DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), out, n, k)
+    assert rel_l2(out.download(), ora.q8_0_gemv(w, x, n, k)) <= 1e-5
+
+
+def test_q8_0_gemv_empty_reduction(dev):
+    n = 100
+    r = np.arange(n, dtype=np.float32)
+    out = DeviceBuffer.from_array(np.full(n, 7.0, np.float32))
+    dr = DeviceBuffer.from_array(r)
+    # no weights or activation are read at k = 0
+    _lib.call("doe_q8_0_gemv", None, None, C.c_void_p(out.ptr), n, 0, None, None)
+    assert not out.download().any()
+    _lib.call("doe_q8_0_gemv", None, None, C.c_void_p(out.ptr), n, 0, C.c_void_p(dr.ptr), None)
+    assert np.array_equal(out.download(), r)
+
+
+def test_q8_0_gemv_graph_replays(dev, ora):
+    rng = np.random.default_rng(13)
+    n, k = 1024, 2304
+    w = q8_0.random_q8_0(rng, n, k)
+    xs = [rng.standard_normal(k, dtype=np.float32) for _ in range(3)]
+    dw, dx = DeviceBuffer.from_array(w), DeviceBuffer.from_array(xs[0])
+    out = DeviceBuffer.empty((n,), np.float32)
+    s = Stream()
+    g = Graph.capture(s, lambda: ops.matmul_q8_0(dw, dx, out, n, k, stream=s))
+    for x in xs:
+        dx.upload(x)
+        out.fill_zero(s)
+        g.launch(s)
+        s.synchronize()
+        assert rel_l2(out.download(), ora.q8_0_gemv(w, x, n, k)) <= 1e-5
+    g.destroy()
+    s.destroy()
+
+
+def test_q8_0_gemv_rejects(dev):
+    n, k = 4, 64
+    dw = DeviceBuffer(n * q8_0.row_bytes(k) + 4)
+    dx = DeviceBuffer.empty((32800,), np.float32)
+    out = DeviceBuffer.empty((n,), np.float32)
+    with pytest.raises(DoeError, match="4-byte aligned"):
+        _lib.call("doe_q8_0_gemv", C.c_void_p(dw.ptr + 2), C.c_void_p(dx.ptr), C.c_void_p(out.ptr), n, k,
+                  None, None)
+    big = DeviceBuffer(q8_0.row_bytes(32800))
+    with pytest.raises(DoeError, match="k <= 32768"):
+        _lib.call("doe_q8_0_gemv", C.c_void_p(big.ptr), C.c_void_p(dx.ptr), C.c_void_p(out.ptr), 1, 32800,
+                  None, None)
+    with pytest.raises(ValueError, match="byte length"):
+        ops.matmul_q8_0(dw, dx, out, n, k)
