@@ -494,7 +494,7 @@ def bench_q8_0(args, doe):
     log(f"q8_0 gemv {Q8_N}x{Q8_K}: {ms * 1e3:.2f} us, {gbs:.1f} GB/s, rel_l2 {rel:.2e}")
     return {"workload": f"q8_0_gemv M=1 N={Q8_N} K={Q8_K} (Q8_0 weights, f32 activation/output), "
                         f"{copies} rotating weight copies, HIP-graph replay",
-            "kernel": "q8_0_gemv_kernel<4> (doe_amd/csrc/q8_0_gemv.hip)",
+            "kernel": "q8_0_gemv_kernel<2, 1> (doe_amd/csrc/q8_0_gemv.hip)",
             "us_per_call": round(ms * 1e3, 3), "bytes_per_call": byt, "achieved_gbs": round(gbs, 1),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "rel_l2_vs_oracle": rel}
 

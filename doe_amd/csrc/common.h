@@ -28,6 +28,7 @@ int fill_bytes_async(void *dst, int value, size_t bytes, hipStream_t st);
 int attn_set_splits(int value);
 int attn_set_waves(int value);
 int int4_set_kernel(int value);
+int q8_0_set_tune(const char *key, int value);  // "q8_0_gemv.rows" / ".depth"
 
 }  // namespace doe
 

@@ -1068,6 +1068,8 @@ int doe_tune_set(const char *key, int value) {
     } else if (!strcmp(key, "q4k_gemv.kernel")) {
         DOE_REQUIRE(value >= 0 && value <= 2, DOE_E_INVALID, "q4k_gemv.kernel is 0, 1 or 2");
         g_tune_kernel = value;
+    } else if (!strcmp(key, "q8_0_gemv.rows") || !strcmp(key, "q8_0_gemv.depth")) {
+        return doe::q8_0_set_tune(key, value);
     } else if (!strcmp(key, "int4_gemv.kernel")) {
         return doe::int4_set_kernel(value);
     } else if (!strcmp(key, "attn_decode.splits")) {

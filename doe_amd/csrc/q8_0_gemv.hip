@@ -21,6 +21,8 @@
 // before the current unit is computed.  Bound: HBM (34 bytes per 32 weights).
 #include "common.h"
 
+#include <string.h>
+
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -65,10 +67,11 @@ __device__ __forceinline__ float blk_dot(const Blk &bk, uint32_t off, const floa
     return d * fmaf(-128.0f, sxb, s0 + s1);
 }
 
-template <int R>
+template <int R, int D>
 __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
     const uint8_t *__restrict__ w, const float *__restrict__ x, float *y, const float *res, int n,
     int k, int nb, int q64, int r64) {
+    static_assert(D == 1 || D == 2, "one or two units in flight ahead");
     extern __shared__ float lds[];
     float *xs = lds;                          // [nb][kXStride]
     float *sx = lds + (size_t)nb * kXStride;  // [nb]
@@ -77,26 +80,45 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
     const int nwaves = gridDim.x * kWaves;
     const int ngroups = (n + R - 1) / R;
     const uint32_t rb = (uint32_t)nb * 34u;  // row bytes
-    // first unit of every group: row lane / nb, block lane % nb
+    // first unit of every group: row lane / nb, block lane % nb; each round
+    // moves a lane 64 units on: q64 rows and r64 blocks
     const int rl0 = lane / nb, b0 = lane - rl0 * nb;
-
-    auto group_rsrc = [&](int g, int &rows, uint32_t &s0) {
-        rows = min(R, n - g * R);
-        const size_t base = (size_t)g * R * rb;
-        s0 = (uint32_t)(base & 3u);
-        return __builtin_amdgcn_make_buffer_rsrc((void *)(w + base - s0), (short)0,
-                                                 (int)((s0 + (uint32_t)rows * rb + 3u) & ~3u),
-                                                 0x00020000);
+    auto adv = [&](int &r, int &bb) {
+        r += q64;
+        bb += r64;
+        if (bb >= nb) {
+            bb -= nb;
+            ++r;
+        }
     };
 
-    // issue this wave's first block loads before staging x
-    // (a wave without a group reads out of range: zeros, no access)
-    int g = wave, rows = 0;
+    int g = wave, rows = 0, rounds = 0, lrl = 0, lb = 0;
     uint32_t s0 = 0;
-    __amdgpu_buffer_rsrc_t rs = group_rsrc(min(g, ngroups - 1), rows, s0);
-    uint32_t cur_off =
-        (g < ngroups && rl0 < rows) ? s0 + (uint32_t)rl0 * rb + 34u * (uint32_t)b0 : kOutOfRange;
-    Blk cur = load_blk(rs, cur_off);
+    __amdgpu_buffer_rsrc_t rs;
+    Blk c0, c1;
+    uint32_t o0 = kOutOfRange, o1 = kOutOfRange;
+    // group g's buffer and its first D units' loads (a wave without a group
+    // reads out of range: zeros, no access)
+    auto start_group = [&]() {
+        const int gg = min(g, ngroups - 1);
+        rows = min(R, n - gg * R);
+        rounds = g < ngroups ? (rows * nb + 63) >> 6 : 0;
+        const size_t base = (size_t)gg * R * rb;
+        s0 = (uint32_t)(base & 3u);
+        rs = __builtin_amdgcn_make_buffer_rsrc((void *)(w + base - s0), (short)0,
+                                               (int)((s0 + (uint32_t)rows * rb + 3u) & ~3u), 0x00020000);
+        lrl = rl0;
+        lb = b0;
+        o0 = (0 < rounds && lrl < rows) ? s0 + (uint32_t)lrl * rb + 34u * (uint32_t)lb : kOutOfRange;
+        c0 = load_blk(rs, o0);
+        adv(lrl, lb);
+        if (D == 2) {
+            o1 = (1 < rounds && lrl < rows) ? s0 + (uint32_t)lrl * rb + 34u * (uint32_t)lb : kOutOfRange;
+            c1 = load_blk(rs, o1);
+            adv(lrl, lb);
+        }
+    };
+    start_group();  // issued before x is staged
 
     for (int i = threadIdx.x; i < nb * 32; i += kWaves * 64)
         xs[(i >> 5) * kXStride + (i & 31)] = i < k ? x[i] : 0.0f;
@@ -114,32 +136,29 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
     __syncthreads();
 
     for (; g < ngroups; g += nwaves) {
-        if (g != wave) {
-            rs = group_rsrc(g, rows, s0);
-            cur_off = rl0 < rows ? s0 + (uint32_t)rl0 * rb + 34u * (uint32_t)b0 : kOutOfRange;
-            cur = load_blk(rs, cur_off);
-        }
-        const int rounds = (rows * nb + 63) >> 6;
+        if (g != wave) start_group();
         int rl = rl0, b = b0;
         float acc[R];
 #pragma unroll
         for (int j = 0; j < R; ++j) acc[j] = 0.0f;
         for (int t = 0; t < rounds; ++t) {
-            int nrl = rl + q64, nbk = b + r64;
-            if (nbk >= nb) {
-                nbk -= nb;
-                ++nrl;
-            }
-            const uint32_t nxt_off =
-                (t + 1 < rounds && nrl < rows) ? s0 + (uint32_t)nrl * rb + 34u * (uint32_t)nbk : kOutOfRange;
-            const Blk nxt = load_blk(rs, nxt_off);
-            const float v = blk_dot(cur, cur_off, xs + b * kXStride, sx[b]);
+            const uint32_t on =
+                (t + D < rounds && lrl < rows) ? s0 + (uint32_t)lrl * rb + 34u * (uint32_t)lb : kOutOfRange;
+            const Blk cn = load_blk(rs, on);
+            adv(lrl, lb);
+            const float v = blk_dot(c0, o0, xs + b * kXStride, sx[b]);
 #pragma unroll
             for (int j = 0; j < R; ++j) acc[j] += (rl == j) ? v : 0.0f;
-            cur = nxt;
-            cur_off = nxt_off;
-            rl = nrl;
-            b = nbk;
+            adv(rl, b);
+            if (D == 2) {
+                c0 = c1;
+                o0 = o1;
+                c1 = cn;
+                o1 = on;
+            } else {
+                c0 = cn;
+                o0 = on;
+            }
         }
 #pragma unroll
         for (int j = 0; j < R; ++j) {
@@ -156,11 +175,14 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
 
 int g_num_cus = 0;
 
-template <int R>
+int g_tune_rows = 0;   // 0 = automatic, else 1, 2 or 4 rows per wave group
+int g_tune_depth = 0;  // 0 = automatic, else 1 or 2 units in flight ahead
+
+template <int R, int D>
 int q8_0_launch(const uint8_t *w, const float *x, float *y, const float *res, int n, int k, int nb,
                 hipStream_t st) {
     static const hipError_t attr_rc = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&q8_0_gemv_kernel<R>),
+        reinterpret_cast<const void *>(&q8_0_gemv_kernel<R, D>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxBlocks * (kXStride + 1) * 4);
     DOE_HIP_CHECK(attr_rc);
     const long ngroups = (n + R - 1) / R;
@@ -168,10 +190,17 @@ int q8_0_launch(const uint8_t *w, const float *x, float *y, const float *res, in
     const long cap = (long)g_num_cus * 8;
     if (blocks > cap) blocks = cap;
     const size_t lds = (size_t)nb * (kXStride + 1) * 4;
-    hipLaunchKernelGGL(q8_0_gemv_kernel<R>, dim3((unsigned)blocks), dim3(kWaves * 64), lds, st, w,
-                       x, y, res, n, k, nb, 64 / nb, 64 % nb);
+    hipLaunchKernelGGL((q8_0_gemv_kernel<R, D>), dim3((unsigned)blocks), dim3(kWaves * 64), lds, st,
+                       w, x, y, res, n, k, nb, 64 / nb, 64 % nb);
     DOE_LAUNCH_CHECK("q8_0_gemv_kernel");
     return DOE_OK;
+}
+
+template <int R>
+int q8_0_launch_depth(const uint8_t *w, const float *x, float *y, const float *res, int n, int k,
+                      int nb, hipStream_t st) {
+    if (g_tune_depth == 2) return q8_0_launch<R, 2>(w, x, y, res, n, k, nb, st);
+    return q8_0_launch<R, 1>(w, x, y, res, n, k, nb, st);
 }
 
 }  // namespace
@@ -205,10 +234,31 @@ extern "C" int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, f
         g_num_cus = cus > 0 ? cus : 256;
     }
     const uint8_t *w = (const uint8_t *)weight_q8_0;
-    // four-row groups once they still give two workgroups per CU, else fewer
-    if (n >= (int64_t)g_num_cus * 2 * kWaves * 4)
-        return q8_0_launch<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
-    if (n >= (int64_t)g_num_cus * 2 * kWaves * 2)
-        return q8_0_launch<2>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
-    return q8_0_launch<1>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
+    // rows per wave group: the fewest that give a wave two full rounds of
+    // units (a partly filled last round idles lanes), more only where the
+    // persistent grid is full anyway (fewer groups, same occupancy)
+    int r = g_tune_rows;
+    if (r == 0) {
+        r = 1;
+        while (r < 4 && (int64_t)r * nb < 128) r *= 2;
+        while (r < 4 && (n + r - 1) / r > (int64_t)g_num_cus * 8 * kWaves) r *= 2;
+    }
+    if (r == 4) return q8_0_launch_depth<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
+    if (r == 2) return q8_0_launch_depth<2>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
+    return q8_0_launch_depth<1>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
 }
+
+namespace doe {
+
+int q8_0_set_tune(const char *key, int v) {
+    if (!strcmp(key, "q8_0_gemv.rows")) {
+        DOE_REQUIRE(v == 0 || v == 1 || v == 2 || v == 4, DOE_E_INVALID, "q8_0_gemv.rows is 0, 1, 2 or 4");
+        g_tune_rows = v;
+    } else {
+        DOE_REQUIRE(v >= 0 && v <= 2, DOE_E_INVALID, "q8_0_gemv.depth is 0, 1 or 2");
+        g_tune_depth = v;
+    }
+    return DOE_OK;
+}
+
+}  // namespace doe

@@ -370,7 +370,9 @@ int doe_decode_advance(int32_t *state, int32_t *token, int32_t *ids, int64_t max
 
 /* ---- tuning ----------------------------------------------------------------
  * Overrides a kernel launch-shape choice (0 restores the automatic choice).
- * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows", "attn_decode.splits",
+ * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows", "q8_0_gemv.rows" (1, 2 or 4
+ * rows per wave group), "q8_0_gemv.depth" (1 or 2 blocks loaded ahead),
+ * "attn_decode.splits",
  * "attn_decode.waves" (4: narrow workgroups; 8 or 16: the wide short-context
  * workgroup where the head shape allows it).  No
  * reference counterpart:

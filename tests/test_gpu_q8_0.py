@@ -35,6 +35,26 @@ def test_q8_0_gemv_matches_oracle(dev, ora, n, k):
     assert err <= 1e-5, err  # f32 sums of exact products: ~1e-7 expected
 
 
+@pytest.mark.parametrize("rows,depth", [(1, 1), (1, 2), (2, 1), (2, 2), (4, 1), (4, 2)])
+def test_q8_0_gemv_every_variant(dev, ora, rows, depth):
+    # wave groups of 1, 2 or 4 rows, one or two units loaded ahead
+    rng = np.random.default_rng(rows * 10 + depth)
+    try:
+        ops.tune("q8_0_gemv.rows", rows)
+        ops.tune("q8_0_gemv.depth", depth)
+        for n, k in ((777, 1000), (70, 3000), (9, 33)):
+            w = q8_0.random_q8_0(rng, n, k)
+            x = rng.standard_normal(k, dtype=np.float32)
+            r = rng.standard_normal(n, dtype=np.float32)
+            out = DeviceBuffer.empty((n,), np.float32)
+            ops.matmul_q8_0(DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), out, n, k,
+                            residual=DeviceBuffer.from_array(r))
+            assert rel_l2(out.download(), ora.q8_0_gemv(w, x, n, k, residual=r)) <= 1e-5, (n, k)
+    finally:
+        ops.tune("q8_0_gemv.rows", 0)
+        ops.tune("q8_0_gemv.depth", 0)
+
+
 def test_q8_0_gemv_residual_in_place_and_separate(dev, ora):
     rng = np.random.default_rng(11)
     n, k = 3000, 544
