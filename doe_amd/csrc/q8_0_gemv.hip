@@ -9,8 +9,9 @@
 //
 // Decomposition: a workgroup of four waves first issues the loads of its first
 // blocks, then stages x into LDS as 36-float rows per block (32 values + 4 of
-// padding: lanes on consecutive blocks hit distinct banks) together with the
-// per-block sums sx[b].  A wave owns groups of R consecutive rows; the R * nb
+// padding: lanes on consecutive blocks hit distinct banks; 16-byte loads when
+// x is 16-byte aligned) together with the per-block sums sx[b], reduced in
+// registers on the way.  A wave owns groups of R consecutive rows; the R * nb
 // (row, block) units of a group are spread over its lanes (unit u = lane +
 // 64 t), so short rows still fill the wave.  A unit is three buffer loads
 // (16 + 16 + 4 bytes from the block's dword-aligned start: no 64-bit address
@@ -70,7 +71,7 @@ __device__ __forceinline__ float blk_dot(const Blk &bk, uint32_t off, const floa
 template <int R, int D>
 __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
     const uint8_t *__restrict__ w, const float *__restrict__ x, float *y, const float *res, int n,
-    int k, int nb, int q64, int r64) {
+    int k, int nb, int q64, int r64, bool x_vec) {
     static_assert(D == 1 || D == 2, "one or two units in flight ahead");
     extern __shared__ float lds[];
     float *xs = lds;                          // [nb][kXStride]
@@ -120,18 +121,28 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
     };
     start_group();  // issued before x is staged
 
-    for (int i = threadIdx.x; i < nb * 32; i += kWaves * 64)
-        xs[(i >> 5) * kXStride + (i & 31)] = i < k ? x[i] : 0.0f;
-    __syncthreads();
-    for (int b = threadIdx.x; b < nb; b += kWaves * 64) {
-        const float4 *p = reinterpret_cast<const float4 *>(xs + b * kXStride);
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float4 v = p[j];
-            s += v.x + v.y + v.z + v.w;
+    // x in 4-float pieces (piece i = elements 4i..4i+3 of block i / 8); the
+    // eight lanes holding a block's pieces sum it with three shuffles
+    for (int i0 = 0; i0 < nb * 8; i0 += kWaves * 64) {
+        const int i = i0 + threadIdx.x;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < nb * 8) {
+            const int e = 4 * i;
+            if (x_vec && e + 3 < k) {
+                v = *reinterpret_cast<const float4 *>(x + e);
+            } else {
+                if (e < k) v.x = x[e];
+                if (e + 1 < k) v.y = x[e + 1];
+                if (e + 2 < k) v.z = x[e + 2];
+                if (e + 3 < k) v.w = x[e + 3];
+            }
+            *reinterpret_cast<float4 *>(xs + (i >> 3) * kXStride + (i & 7) * 4) = v;
         }
-        sx[b] = s;
+        float s = (v.x + v.y) + (v.z + v.w);
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        if (i < nb * 8 && (i & 7) == 0) sx[i >> 3] = s;
     }
     __syncthreads();
 
@@ -191,7 +202,7 @@ int q8_0_launch(const uint8_t *w, const float *x, float *y, const float *res, in
     if (blocks > cap) blocks = cap;
     const size_t lds = (size_t)nb * (kXStride + 1) * 4;
     hipLaunchKernelGGL((q8_0_gemv_kernel<R, D>), dim3((unsigned)blocks), dim3(kWaves * 64), lds, st,
-                       w, x, y, res, n, k, nb, 64 / nb, 64 % nb);
+                       w, x, y, res, n, k, nb, 64 / nb, 64 % nb, ((uintptr_t)x & 15) == 0);
     DOE_LAUNCH_CHECK("q8_0_gemv_kernel");
     return DOE_OK;
 }
@@ -235,12 +246,15 @@ extern "C" int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, f
     }
     const uint8_t *w = (const uint8_t *)weight_q8_0;
     // rows per wave group: the fewest that give a wave two full rounds of
-    // units (a partly filled last round idles lanes), more only where the
-    // persistent grid is full anyway (fewer groups, same occupancy)
+    // units (a partly filled last round idles lanes) while two workgroups per
+    // CU remain, more where the persistent grid is full anyway (fewer groups,
+    // same occupancy)
     int r = g_tune_rows;
     if (r == 0) {
         r = 1;
-        while (r < 4 && (int64_t)r * nb < 128) r *= 2;
+        while (r < 4 && (int64_t)r * nb < 128 &&
+               (n + 2 * r - 1) / (2 * r) >= (int64_t)g_num_cus * 2 * kWaves)
+            r *= 2;
         while (r < 4 && (n + r - 1) / r > (int64_t)g_num_cus * 8 * kWaves) r *= 2;
     }
     if (r == 4) return q8_0_launch_depth<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
