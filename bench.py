@@ -218,7 +218,8 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
         f"prompt {timing['prompt_s']:.3f} s, {gbs:.0f} GB/s of algorithmic bytes")
     return {
         "workload": f"{label} bs=1: {cfg.layers} layers, hidden {cfg.hidden}, {cfg.heads}/{cfg.kv_heads} "
-                    f"heads x {cfg.head_dim}, FFN {cfg.ffn} GeGLU, vocab {cfg.vocab}; Q4_K projections, f16 "
+                    f"heads x {cfg.head_dim}, FFN {cfg.ffn} GeGLU, vocab {cfg.vocab}; "
+                    f"{'Q8_0' if cfg.weight_format == 'q8_0' else 'Q4_K'} projections, f16 "
                     f"lm_head, f16 KV; prompt {args.prompt_len} then {args.decode_steps} greedy steps; "
                     f"random-init weights; " + (f"{spg} steps per HIP graph" if spg > 0 else "eager launches"),
         "tok_s": round(tok_s, 2),
@@ -573,6 +574,12 @@ def main() -> int:
     att = bench_attention(args, doe_amd)
     dec = None if args.no_decode else bench_decode(args, doe_amd)
     dec_graph = None if args.no_decode else bench_decode_graph(args, doe_amd)
+    dec_q8 = None
+    if not args.no_decode:
+        from doe_amd.model import DecoderConfig
+
+        dec_q8 = bench_decode(args, doe_amd, cfg=DecoderConfig(weight_format="q8_0"),
+                              label="2B-class decoder, Q8_0 weights")
     gemm = None if args.no_gemm else bench_gemm(args, doe_amd)
     pfa = None if args.no_gemm else bench_prefill_attention(args, doe_amd)
     c4 = None if args.no_gemm else bench_config4(args, doe_amd)
@@ -616,6 +623,7 @@ def main() -> int:
         "attention_decode": att,
         "decode": dec,
         "decode_graph_gemma3_270m": dec_graph,
+        "decode_q8_0": dec_q8,
         "prefill_gemm": gemm,
         "prefill_attention": pfa,
         "config4_decode_layer": c4,

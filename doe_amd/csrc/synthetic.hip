@@ -67,6 +67,23 @@ __global__ void fill_q4k_kernel(uint8_t *w, int64_t nblocks, uint64_t seed, floa
     }
 }
 
+// Q8_0 blocks (34 bytes: f16 scale d = |N(0, d_sigma)|, 32 uniform int8
+// quants), written with 2-byte stores (blocks are only 2-byte aligned).
+__global__ void fill_q8_0_kernel(uint8_t *w, int64_t nblocks, uint64_t seed, float d_sigma) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblocks;
+         b += (int64_t)gridDim.x * blockDim.x) {
+        uint16_t *p = reinterpret_cast<uint16_t *>(w + b * 34);
+        const _Float16 d = (_Float16)fabsf(d_sigma * normal_at(seed ^ 0xd1b54a32d192ed03ull, (uint64_t)b));
+        p[0] = __builtin_bit_cast(uint16_t, d);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint64_t r = mix64(seed * 0x632be59bd9b4e019ull + (uint64_t)b * 4 + j);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) p[1 + 4 * j + h] = (uint16_t)(r >> (16 * h));
+        }
+    }
+}
+
 // Decode-loop bookkeeping after a step: state = [pos, kv_len, prompt_len,
 // current token].  With argmax partials (one key per workgroup of the fused
 // lm_head) the sampled token is their reduction (largest logit, lowest index)
@@ -157,6 +174,19 @@ int doe_fill_random_q4k(void *weight_q4k, int64_t nblocks, uint64_t seed, float 
     hipLaunchKernelGGL(fill_q4k_kernel, dim3(grid_for(nblocks * 9)), dim3(256), 0, (hipStream_t)stream,
                        (uint8_t *)weight_q4k, nblocks, seed, d_sigma, dmin_sigma);
     DOE_LAUNCH_CHECK("fill_q4k_kernel");
+    return DOE_OK;
+}
+
+int doe_fill_random_q8_0(void *weight_q8_0, int64_t nblocks, uint64_t seed, float d_sigma,
+                         doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(nblocks >= 0 && (nblocks == 0 || weight_q8_0), DOE_E_INVALID, "bad fill arguments");
+    DOE_REQUIRE(((uintptr_t)weight_q8_0 & 1) == 0, DOE_E_INVALID, "weight must be 2-byte aligned");
+    if (nblocks == 0) return DOE_OK;
+    hipLaunchKernelGGL(fill_q8_0_kernel, dim3(grid_for(nblocks)), dim3(256), 0, (hipStream_t)stream,
+                       (uint8_t *)weight_q8_0, nblocks, seed, d_sigma);
+    DOE_LAUNCH_CHECK("fill_q8_0_kernel");
     return DOE_OK;
 }
 

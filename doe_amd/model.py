@@ -33,6 +33,7 @@ import numpy as np
 
 from . import _lib, ops
 from . import q4k as _q4k
+from . import q8_0 as _q8_0
 from .device import DeviceBuffer, Event, Graph, Stream, _stream_ptr
 
 
@@ -50,6 +51,10 @@ class DecoderConfig:
     max_seq: int = 384
     embed_scale: float = 1.0
     attn_softcap: float = 0.0  # > 0: scores s -> softcap * tanh(s / softcap) (attention_head256_f16kv.wgsl:197-199)
+    # projection weights: "q4k" (Q4_K_M, fused kernels) or "q8_0" (Q8_0 GEMVs
+    # between the unfused norm / RoPE / KV-write / attention / GeGLU ops): the
+    # modelConfig quantFormat of emit_csl_exec_v1.zig:279-284
+    weight_format: str = "q4k"
 
     @property
     def q_dim(self) -> int:
@@ -63,8 +68,16 @@ class DecoderConfig:
     def qkv_rows(self) -> int:
         return self.q_dim + 2 * self.kv_dim
 
-    def q4k_bytes_per_layer(self) -> int:
-        rb = _q4k.row_bytes
+    def row_bytes(self, k: int) -> int:
+        """Bytes of one projection row of k weights in this model's format."""
+        if self.weight_format == "q4k":
+            return _q4k.row_bytes(k)
+        if self.weight_format == "q8_0":
+            return _q8_0.row_bytes(k)
+        raise ValueError(f"weight_format {self.weight_format!r} is not q4k or q8_0")
+
+    def weight_bytes_per_layer(self) -> int:
+        rb = self.row_bytes
         return (self.qkv_rows * rb(self.hidden) + self.hidden * rb(self.q_dim)
                 + 2 * self.ffn * rb(self.hidden) + self.hidden * rb(self.ffn))
 
@@ -72,16 +85,18 @@ class DecoderConfig:
     def from_model_config(cls, mc: dict, **overrides) -> "DecoderConfig":
         """From a step graph's modelConfig (hiddenDim, numHeads, headDim,
         numKeyValueHeads, numLayers, vocabSize, maxSeqLen, ffnExpansionFactor);
-        a separate globalHeadDim or a non-Q4_K quantFormat is not supported."""
+        quantFormat q4k or q8_0; a separate globalHeadDim or quantFormat f16 is
+        not supported."""
         from .execution import UnsupportedStep
 
-        if mc.get("quantFormat", "q4k") != "q4k":
-            raise UnsupportedStep(f"quantFormat {mc.get('quantFormat')!r}")
+        fmt = mc.get("quantFormat", "q4k")
+        if fmt not in ("q4k", "q8_0"):
+            raise UnsupportedStep(f"quantFormat {fmt!r}")
         if mc.get("globalHeadDim", mc["headDim"]) != mc["headDim"]:
             raise UnsupportedStep(f"globalHeadDim {mc['globalHeadDim']} != headDim {mc['headDim']}")
         kw = dict(layers=mc["numLayers"], hidden=mc["hiddenDim"], heads=mc["numHeads"],
                   kv_heads=mc["numKeyValueHeads"], head_dim=mc["headDim"], vocab=mc["vocabSize"],
-                  ffn=mc["hiddenDim"] * mc.get("ffnExpansionFactor", 4))
+                  ffn=mc["hiddenDim"] * mc.get("ffnExpansionFactor", 4), weight_format=fmt)
         if "maxSeqLen" in mc:
             kw["max_seq"] = mc["maxSeqLen"]
         kw.update(overrides)
@@ -90,7 +105,7 @@ class DecoderConfig:
     def decode_bytes_per_token(self, kv_len: float) -> float:
         """Algorithmic HBM bytes of one decode step: every weight once, the
         KV cache up to kv_len, plus the embedding row."""
-        w = self.layers * self.q4k_bytes_per_layer() + self.vocab * self.hidden * 2
+        w = self.layers * self.weight_bytes_per_layer() + self.vocab * self.hidden * 2
         kv = self.layers * 2 * self.kv_heads * kv_len * self.head_dim * 2
         return float(w + kv + self.hidden * 2)
 
@@ -109,10 +124,13 @@ def rope_table(max_pos: int, head_dim: int, base: float) -> np.ndarray:
 
 class LayerWeights:
     def __init__(self, cfg: DecoderConfig):
-        rb = _q4k.row_bytes
+        rb = cfg.row_bytes
+        # q4k: q/k rows as interleaved rotation pairs, gate/up rows interleaved
+        # (gate_0, up_0, gate_1, ...) for the fused kernels; q8_0: plain q/k
+        # rows (rotate-half RoPE op), gate rows then up rows
         self.wqkv = DeviceBuffer(cfg.qkv_rows * rb(cfg.hidden))
         self.wo = DeviceBuffer(cfg.hidden * rb(cfg.q_dim))
-        self.wgu = DeviceBuffer(2 * cfg.ffn * rb(cfg.hidden))  # rows: gate_0, up_0, gate_1, up_1, ...
+        self.wgu = DeviceBuffer(2 * cfg.ffn * rb(cfg.hidden))
         self.wd = DeviceBuffer(cfg.hidden * rb(cfg.ffn))
         self.norm_attn = DeviceBuffer.empty((cfg.hidden,), np.float32)
         self.norm_ffn = DeviceBuffer.empty((cfg.hidden,), np.float32)
@@ -144,6 +162,11 @@ class Decoder:
         # split-attention partials: o [heads][S][D] then (m, l) [heads][S][2]
         self.attn_parts = DeviceBuffer.empty((c.heads * self.max_attn_splits * (c.head_dim + 2),), np.float32)
         self.h = DeviceBuffer.empty((c.ffn,), np.float32)
+        if c.weight_format == "q8_0":  # unfused step: attention output, gate/up
+            self.attn_out = DeviceBuffer.empty((c.q_dim,), np.float32)
+            self.gu = DeviceBuffer.empty((2 * c.ffn,), np.float32)
+            self.gate_view = self.gu.view(0, c.ffn * 4, np.float32)
+            self.up_view = self.gu.view(c.ffn * 4, c.ffn * 4, np.float32)
         self.logits = DeviceBuffer.empty((c.vocab,), np.float32)
         self.token = DeviceBuffer.empty((1,), np.int32)
         self.state = DeviceBuffer.empty((4,), np.int32)  # pos, kv_len, prompt_len, token
@@ -169,6 +192,10 @@ class Decoder:
         s = seed * 1000
 
         def q4k(buf, tag):
+            if c.weight_format == "q8_0":  # d ~ |N(0, 0.001)|: weights of ~0.06 like the Q4_K ones
+                _lib.call("doe_fill_random_q8_0", C.c_void_p(buf.ptr), buf.nbytes // _q8_0.BLOCK_BYTES, s + tag,
+                          0.001, sp)
+                return
             _lib.call("doe_fill_random_q4k", C.c_void_p(buf.ptr), buf.nbytes // _q4k.BLOCK_BYTES, s + tag, 0.02,
                       0.01, sp)
 
@@ -196,6 +223,9 @@ class Decoder:
         ops.embed(self.embed, self.tok_view, self.x, 1, c.vocab, c.hidden, c.embed_scale, stream=stream)
         scale = 1.0 / math.sqrt(c.head_dim)
         for li, L in enumerate(self.layers):
+            if c.weight_format == "q8_0":
+                self._layer_q8_0(li, L, scale, stream)
+                continue
             ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads, num_kv_heads=c.kv_heads,
                             head_dim=c.head_dim, freq_cis=self.freq_cis, position_buffer=self.pos_view,
                             key_cache=L.k_cache, val_cache=L.v_cache, max_seq_len=c.max_seq,
@@ -217,6 +247,28 @@ class Decoder:
         _lib.call("doe_decode_advance", C.c_void_p(self.state.ptr), C.c_void_p(self.token.ptr),
                   C.c_void_p(self.ids.ptr), c.max_seq, C.c_void_p(self.argmax_parts.ptr), nparts,
                   _stream_ptr(stream))
+
+    def _layer_q8_0(self, li: int, L: LayerWeights, scale: float, stream) -> None:
+        """One layer with Q8_0 projections: the step graph's ops one by one
+        (input_norm, q/k/v_proj, rope_q/rope_k, the cache write, attention,
+        o_proj + attn_residual, post_attn_norm, gate/up_proj, activation,
+        down_proj + ffn_residual)."""
+        c = self.cfg
+        ops.rmsnorm(self.x, L.norm_attn, self.xn, 1, c.hidden, c.eps, weight_offset=True, stream=stream)
+        ops.matmul_q8_0(L.wqkv, self.xn, self.qkv, c.qkv_rows, c.hidden, stream=stream)
+        ops.rope(self.qk_view, self.freq_cis, 1, c.heads + c.kv_heads, c.head_dim, position_buffer=self.pos_view,
+                 stream=stream)
+        ops.kv_write(self.k_view, self.v_view, L.k_cache, L.v_cache, c.kv_heads, c.max_seq, c.head_dim,
+                     position_buffer=self.pos_view, stream=stream)
+        ops.attention(self.q_view, L.k_cache, L.v_cache, self.attn_out, batch=1, num_heads=c.heads,
+                      num_kv_heads=c.kv_heads, head_dim=c.head_dim, kv_len=0, kv_stride=c.max_seq, scale=scale,
+                      softcap=c.attn_softcap, sliding_window=self.attn_windows[li], kv_len_buffer=self.kvlen_view,
+                      stream=stream)
+        ops.matmul_q8_0(L.wo, self.attn_out, self.x, c.hidden, c.q_dim, residual=self.x, stream=stream)
+        ops.rmsnorm(self.x, L.norm_ffn, self.xn, 1, c.hidden, c.eps, weight_offset=True, stream=stream)
+        ops.matmul_q8_0(L.wgu, self.xn, self.gu, 2 * c.ffn, c.hidden, stream=stream)
+        ops.gelu_gated(self.gate_view, self.up_view, self.h, c.ffn, stream=stream)
+        ops.matmul_q8_0(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)
 
     # ---- generation ----------------------------------------------------------
     def reset(self, prompt: np.ndarray) -> None:

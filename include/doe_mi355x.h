@@ -356,6 +356,9 @@ int doe_fill_uniform_i32(int32_t *out, int64_t n, uint64_t seed, int32_t lo, int
                          doe_stream_t stream);
 int doe_fill_random_q4k(void *weight_q4k, int64_t nblocks, uint64_t seed, float d_sigma,
                         float dmin_sigma, doe_stream_t stream);
+/* Q8_0 blocks: f16 scale |N(0, d_sigma)|, 32 uniform int8 quants. */
+int doe_fill_random_q8_0(void *weight_q8_0, int64_t nblocks, uint64_t seed, float d_sigma,
+                         doe_stream_t stream);
 /* After a decode step, on the device: state = {pos, kv_len, prompt_len,
  * token}; pos += 1, kv_len = pos + 1, and the next token is ids[pos] inside
  * the prompt or the sampled *token (also stored to ids[pos]) after it.  With

@@ -115,8 +115,17 @@ def test_model_config_maps_to_decoder_config():
     c = DecoderConfig.from_model_config(mc, max_seq=64)
     assert (c.layers, c.hidden, c.heads, c.kv_heads, c.head_dim, c.vocab, c.ffn, c.max_seq) == \
         (18, 640, 4, 1, 256, 262144, 2560, 64)
-    with pytest.raises(ex.UnsupportedStep, match="quantFormat"):
-        DecoderConfig.from_model_config({**mc, "quantFormat": "q6k"})
+    assert c.weight_format == "q4k"
+    q8 = DecoderConfig.from_model_config({**mc, "quantFormat": "q8_0"})
+    assert q8.weight_format == "q8_0"
+    # 640-wide rows are 20 Q8_0 blocks of 34 bytes, 3 Q4_K blocks of 144; per
+    # layer: qkv 1536 and gate/up 2 x 2560 rows of 640, o_proj 640 rows of
+    # 1024 (32 blocks), down 640 rows of 2560 (80 blocks)
+    assert q8.row_bytes(640) == 680 and c.row_bytes(640) == 432
+    assert q8.weight_bytes_per_layer() == (1536 + 2 * 2560) * 680 + 640 * 32 * 34 + 640 * 80 * 34
+    for bad in ("q6k", "f16"):
+        with pytest.raises(ex.UnsupportedStep, match="quantFormat"):
+            DecoderConfig.from_model_config({**mc, "quantFormat": bad})
 
 
 def test_reference_lowering_known_answers():

@@ -1,6 +1,7 @@
 """GPU parity of the decode loop against the CPU oracle decoder, teacher
 forced on the GPU's own tokens: per-step logits within rel-L2 1e-3 and the
 greedy token equal to the oracle's argmax."""
+import dataclasses
 import json
 from pathlib import Path
 
@@ -54,6 +55,42 @@ def test_small_decoder_matches_oracle(dev, ora):
     # the device-side token record matches
     dev_ids = dec.ids.download()[: len(ids)]
     assert dev_ids.tolist() == ids
+
+
+SMALL_Q8 = dataclasses.replace(SMALL, weight_format="q8_0")
+
+
+def test_q8_0_decoder_matches_oracle(dev, ora):
+    # Q8_0 projections through the unfused ops, against the oracle decoder
+    # with Q8_0 GEMVs; a sliding window on layer 0 and a softcap included
+    from doe_amd import execution
+
+    cfg = dataclasses.replace(SMALL_Q8, attn_softcap=30.0)
+    plan = execution.DecodePlan(layer=(), post=(), windows=(4, 0), eos_token_id=None)
+    dec = Decoder(cfg, keep_logits=True, plan=plan)
+    dec.init_random(seed=9)
+    s = Stream()
+    oracle = OracleDecoder(dec)
+    prompt = np.array([9, 4000, 12, 12, 300], np.int32)
+    ids, errs = run_teacher_forced(dec, oracle, prompt, 10, s)
+    print(f"[decode q8_0] max logits rel_l2 {max(errs):.2e}", flush=True)
+    assert max(errs) <= 1e-3
+    assert dec.ids.download()[: len(ids)].tolist() == ids
+
+
+def test_q8_0_decoder_graph_replay_equals_eager(dev):
+    dec = Decoder(SMALL_Q8)
+    dec.init_random(seed=10)
+    s = Stream()
+    prompt = np.arange(1, 7, dtype=np.int32) * 51
+    eager = dec.generate(prompt, 12, s)
+    dec.reset(prompt)
+    dec.step(s)
+    s.synchronize()
+    g = dec.capture(s, 2)
+    out = dec.generate(prompt, 12, s, graph=g, steps_per_graph=2)
+    g.destroy()
+    assert out.tolist() == eager.tolist()
 
 
 def test_graph_replay_equals_eager(dev):
@@ -142,11 +179,13 @@ def test_gemma3_270m_manifest_graph_first_steps(dev, ora):
 def _write_rdrr(dec, root):
     """An RDRR artifact (manifest + two shards, HF tensor names) holding a
     decoder's weights in the plain row order of the checkpoint files."""
-    from doe_amd import q4k as _q4k
     from doe_amd.ops import deinterleave_rope_rows
 
     c = dec.cfg
-    rb = _q4k.row_bytes
+    rb = c.row_bytes
+    q8 = c.weight_format == "q8_0"
+    wdt = "Q8_0" if q8 else "Q4_K_M"
+    plain = (lambda rows, hd: rows) if q8 else deinterleave_rope_rows  # Q8_0 q/k rows are stored plain
     tensors, blobs = {}, [bytearray(), bytearray()]
 
     def put(name, arr, dtype, shape, layout=None, split=False):
@@ -169,14 +208,15 @@ def _write_rdrr(dec, root):
         p = f"model.layers.{i}"
         wqkv = L.wqkv.download().reshape(c.qkv_rows, rb(c.hidden))
         q, k, v = wqkv[:c.q_dim], wqkv[c.q_dim:c.q_dim + c.kv_dim], wqkv[c.q_dim + c.kv_dim:]
-        put(f"{p}.self_attn.q_proj.weight", deinterleave_rope_rows(q, c.head_dim), "Q4_K_M", (c.q_dim, c.hidden), "row")
-        put(f"{p}.self_attn.k_proj.weight", deinterleave_rope_rows(k, c.head_dim), "Q4_K_M", (c.kv_dim, c.hidden), "row")
-        put(f"{p}.self_attn.v_proj.weight", v, "Q4_K_M", (c.kv_dim, c.hidden), "row")
-        put(f"{p}.self_attn.o_proj.weight", L.wo.download(), "Q4_K_M", (c.hidden, c.q_dim), "row")
+        put(f"{p}.self_attn.q_proj.weight", plain(q, c.head_dim), wdt, (c.q_dim, c.hidden), "row")
+        put(f"{p}.self_attn.k_proj.weight", plain(k, c.head_dim), wdt, (c.kv_dim, c.hidden), "row")
+        put(f"{p}.self_attn.v_proj.weight", v, wdt, (c.kv_dim, c.hidden), "row")
+        put(f"{p}.self_attn.o_proj.weight", L.wo.download(), wdt, (c.hidden, c.q_dim), "row")
         gu = L.wgu.download().reshape(2 * c.ffn, rb(c.hidden))
-        put(f"{p}.mlp.gate_proj.weight", gu[0::2], "Q4_K_M", (c.ffn, c.hidden), "row")
-        put(f"{p}.mlp.up_proj.weight", gu[1::2], "Q4_K_M", (c.ffn, c.hidden), "row")
-        put(f"{p}.mlp.down_proj.weight", L.wd.download(), "Q4_K_M", (c.hidden, c.ffn), "row", split=(i == 1))
+        gate, up = (gu[:c.ffn], gu[c.ffn:]) if q8 else (gu[0::2], gu[1::2])
+        put(f"{p}.mlp.gate_proj.weight", gate, wdt, (c.ffn, c.hidden), "row")
+        put(f"{p}.mlp.up_proj.weight", up, wdt, (c.ffn, c.hidden), "row")
+        put(f"{p}.mlp.down_proj.weight", L.wd.download(), wdt, (c.hidden, c.ffn), "row", split=(i == 1))
         put(f"{p}.input_layernorm.weight", L.norm_attn.download(), "F32", (c.hidden,))
         put(f"{p}.post_attention_layernorm.weight", L.norm_ffn.download(), "F32", (c.hidden,))
     put("model.embed_tokens.weight", dec.embed.download(), "F16", (c.vocab, c.hidden))
@@ -189,15 +229,18 @@ def _write_rdrr(dec, root):
     (root / "manifest.json").write_text(json.dumps(manifest))
 
 
-def test_rdrr_artifact_loads_byte_identical(dev, tmp_path):
-    # Q4_K_M rows move unchanged from the artifact into the decoder's layout;
-    # a decoder loaded from it holds the same bytes and decodes the same logits
+@pytest.mark.parametrize("fmt", ["q4k", "q8_0"])
+def test_rdrr_artifact_loads_byte_identical(dev, tmp_path, fmt):
+    # Q4_K_M (or Q8_0) rows move unchanged from the artifact into the
+    # decoder's layout; a decoder loaded from it holds the same bytes and
+    # decodes the same logits
     from doe_amd import rdrr
 
-    src = Decoder(SMALL, keep_logits=True)
+    cfg = dataclasses.replace(SMALL, weight_format=fmt)
+    src = Decoder(cfg, keep_logits=True)
     src.init_random(seed=6)
     _write_rdrr(src, tmp_path)
-    dst = Decoder(SMALL, keep_logits=True)
+    dst = Decoder(cfg, keep_logits=True)
     rdrr.load_decoder_weights(rdrr.RdrrArtifact(tmp_path), dst)
     pairs = [(src.embed, dst.embed), (src.lm_head, dst.lm_head), (src.norm_final, dst.norm_final)]
     for a, b in zip(src.layers, dst.layers):
