@@ -71,11 +71,12 @@ __device__ __forceinline__ float blk_dot(const Blk &bk, uint32_t off, const floa
 template <int R, int D>
 __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
     const uint8_t *__restrict__ w, const float *__restrict__ x, float *y, const float *res, int n,
-    int k, int nb, int q64, int r64, bool x_vec) {
+    int k, int nb, int q64, int r64, bool x_vec, const float *norm_w, float norm_eps, int norm_offset) {
     static_assert(D == 1 || D == 2, "one or two units in flight ahead");
     extern __shared__ float lds[];
     float *xs = lds;                          // [nb][kXStride]
     float *sx = lds + (size_t)nb * kXStride;  // [nb]
+    float *ss = sx + nb;                      // [kWaves] sums of squares (norm)
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const int nwaves = gridDim.x * kWaves;
@@ -122,7 +123,10 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
     start_group();  // issued before x is staged
 
     // x in 4-float pieces (piece i = elements 4i..4i+3 of block i / 8); the
-    // eight lanes holding a block's pieces sum it with three shuffles
+    // eight lanes holding a block's pieces sum it with three shuffles.  With
+    // an RMSNorm, x * w' is staged (w' = w or 1 + w) and the row sums are
+    // scaled by 1 / sqrt(mean(x^2) + eps) at the end: W (r x w') = r W (x w').
+    float sq = 0.0f;
     for (int i0 = 0; i0 < nb * 8; i0 += kWaves * 64) {
         const int i = i0 + threadIdx.x;
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -136,6 +140,14 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
                 if (e + 2 < k) v.z = x[e + 2];
                 if (e + 3 < k) v.w = x[e + 3];
             }
+            if (norm_w) {
+                sq += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+                const float o = norm_offset ? 1.0f : 0.0f;
+                v.x *= o + (e < k ? norm_w[e] : 0.0f);
+                v.y *= o + (e + 1 < k ? norm_w[e + 1] : 0.0f);
+                v.z *= o + (e + 2 < k ? norm_w[e + 2] : 0.0f);
+                v.w *= o + (e + 3 < k ? norm_w[e + 3] : 0.0f);
+            }
             *reinterpret_cast<float4 *>(xs + (i >> 3) * kXStride + (i & 7) * 4) = v;
         }
         float s = (v.x + v.y) + (v.z + v.w);
@@ -144,7 +156,19 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
         s += __shfl_xor(s, 4, 64);
         if (i < nb * 8 && (i & 7) == 0) sx[i >> 3] = s;
     }
+    if (norm_w) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+        if (lane == 0) ss[threadIdx.x >> 6] = sq;
+    }
     __syncthreads();
+    float rms_inv = 1.0f;
+    if (norm_w) {
+        float t = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kWaves; ++j) t += ss[j];
+        rms_inv = 1.0f / sqrtf(t / (float)k + norm_eps);
+    }
 
     for (; g < ngroups; g += nwaves) {
         if (g != wave) start_group();
@@ -178,7 +202,7 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
             for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
             if (lane == 0 && j < rows) {
                 const int row = g * R + j;
-                y[row] = res ? s + res[row] : s;
+                y[row] = res ? fmaf(rms_inv, s, res[row]) : rms_inv * s;
             }
         }
     }
@@ -189,35 +213,44 @@ int g_num_cus = 0;
 int g_tune_rows = 0;   // 0 = automatic, else 1, 2 or 4 rows per wave group
 int g_tune_depth = 0;  // 0 = automatic, else 1 or 2 units in flight ahead
 
+struct Q8Norm {
+    const float *norm_w;  // nullptr: no RMSNorm of the activation
+    float norm_eps;
+    int norm_offset;
+};
+
 template <int R, int D>
 int q8_0_launch(const uint8_t *w, const float *x, float *y, const float *res, int n, int k, int nb,
-                hipStream_t st) {
+                const Q8Norm &fz, hipStream_t st) {
     static const hipError_t attr_rc = hipFuncSetAttribute(
         reinterpret_cast<const void *>(&q8_0_gemv_kernel<R, D>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxBlocks * (kXStride + 1) * 4);
+        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxBlocks * (kXStride + 1) * 4 + kWaves * 4);
     DOE_HIP_CHECK(attr_rc);
     const long ngroups = (n + R - 1) / R;
     long blocks = (ngroups + kWaves - 1) / kWaves;
     const long cap = (long)g_num_cus * 8;
     if (blocks > cap) blocks = cap;
-    const size_t lds = (size_t)nb * (kXStride + 1) * 4;
+    const size_t lds = (size_t)nb * (kXStride + 1) * 4 + kWaves * 4;
     hipLaunchKernelGGL((q8_0_gemv_kernel<R, D>), dim3((unsigned)blocks), dim3(kWaves * 64), lds, st,
-                       w, x, y, res, n, k, nb, 64 / nb, 64 % nb, ((uintptr_t)x & 15) == 0);
+                       w, x, y, res, n, k, nb, 64 / nb, 64 % nb, ((uintptr_t)x & 15) == 0, fz.norm_w,
+                       fz.norm_eps, fz.norm_offset);
     DOE_LAUNCH_CHECK("q8_0_gemv_kernel");
     return DOE_OK;
 }
 
 template <int R>
 int q8_0_launch_depth(const uint8_t *w, const float *x, float *y, const float *res, int n, int k,
-                      int nb, hipStream_t st) {
-    if (g_tune_depth == 2) return q8_0_launch<R, 2>(w, x, y, res, n, k, nb, st);
-    return q8_0_launch<R, 1>(w, x, y, res, n, k, nb, st);
+                      int nb, const Q8Norm &fz, hipStream_t st) {
+    if (g_tune_depth == 2) return q8_0_launch<R, 2>(w, x, y, res, n, k, nb, fz, st);
+    return q8_0_launch<R, 1>(w, x, y, res, n, k, nb, fz, st);
 }
 
 }  // namespace
 
-extern "C" int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, float *output,
-                             int64_t n, int64_t k, const float *residual, doe_stream_t stream) {
+namespace {
+
+int q8_0_gemv_impl(const void *weight_q8_0, const float *activation, float *output, int64_t n,
+                   int64_t k, const float *residual, const Q8Norm &fz, doe_stream_t stream) {
     int rc = doe::require_init();
     if (rc) return rc;
     const hipStream_t st = (hipStream_t)stream;
@@ -236,8 +269,8 @@ extern "C" int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, f
                 "q8_0_gemv needs k <= %d (got %lld)", kMaxBlocks * 32, (long long)k);
     DOE_REQUIRE(((uintptr_t)weight_q8_0 & 3) == 0, DOE_E_INVALID, "Q8_0 weights must be 4-byte aligned");
     DOE_REQUIRE(((uintptr_t)activation & 3) == 0 && ((uintptr_t)output & 3) == 0 &&
-                    ((uintptr_t)residual & 3) == 0,
-                DOE_E_INVALID, "activation, output and residual must be 4-byte aligned");
+                    ((uintptr_t)residual & 3) == 0 && ((uintptr_t)fz.norm_w & 3) == 0,
+                DOE_E_INVALID, "activation, output, residual and norm weight must be 4-byte aligned");
     if (g_num_cus == 0) {
         int dev = 0, cus = 0;
         DOE_HIP_CHECK(hipGetDevice(&dev));
@@ -257,9 +290,25 @@ extern "C" int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, f
             r *= 2;
         while (r < 4 && (n + r - 1) / r > (int64_t)g_num_cus * 8 * kWaves) r *= 2;
     }
-    if (r == 4) return q8_0_launch_depth<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
-    if (r == 2) return q8_0_launch_depth<2>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
-    return q8_0_launch_depth<1>(w, activation, output, residual, (int)n, (int)k, (int)nb, st);
+    if (r == 4) return q8_0_launch_depth<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, st);
+    if (r == 2) return q8_0_launch_depth<2>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, st);
+    return q8_0_launch_depth<1>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, st);
+}
+
+}  // namespace
+
+extern "C" int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, float *output,
+                             int64_t n, int64_t k, const float *residual, doe_stream_t stream) {
+    return q8_0_gemv_impl(weight_q8_0, activation, output, n, k, residual, Q8Norm{nullptr, 0.0f, 0},
+                          stream);
+}
+
+extern "C" int doe_q8_0_gemv_norm(const void *weight_q8_0, const float *activation, float *output,
+                                  int64_t n, int64_t k, const float *norm_weight, float norm_eps,
+                                  int norm_weight_offset, const float *residual, doe_stream_t stream) {
+    DOE_REQUIRE(norm_weight, DOE_E_INVALID, "null norm weight");
+    return q8_0_gemv_impl(weight_q8_0, activation, output, n, k, residual,
+                          Q8Norm{norm_weight, norm_eps, norm_weight_offset ? 1 : 0}, stream);
 }
 
 namespace doe {

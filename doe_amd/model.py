@@ -249,13 +249,13 @@ class Decoder:
                   _stream_ptr(stream))
 
     def _layer_q8_0(self, li: int, L: LayerWeights, scale: float, stream) -> None:
-        """One layer with Q8_0 projections: the step graph's ops one by one
-        (input_norm, q/k/v_proj, rope_q/rope_k, the cache write, attention,
-        o_proj + attn_residual, post_attn_norm, gate/up_proj, activation,
-        down_proj + ffn_residual)."""
+        """One layer with Q8_0 projections: the step graph's ops, the norms and
+        residuals folded into the GEMVs (input_norm + q/k/v_proj, rope_q /
+        rope_k, the cache write, attention, o_proj + attn_residual,
+        post_attn_norm + gate/up_proj, activation, down_proj + ffn_residual)."""
         c = self.cfg
-        ops.rmsnorm(self.x, L.norm_attn, self.xn, 1, c.hidden, c.eps, weight_offset=True, stream=stream)
-        ops.matmul_q8_0(L.wqkv, self.xn, self.qkv, c.qkv_rows, c.hidden, stream=stream)
+        ops.matmul_q8_0(L.wqkv, self.x, self.qkv, c.qkv_rows, c.hidden, stream=stream, norm_weight=L.norm_attn,
+                        norm_eps=c.eps, norm_weight_offset=True)
         ops.rope(self.qk_view, self.freq_cis, 1, c.heads + c.kv_heads, c.head_dim, position_buffer=self.pos_view,
                  stream=stream)
         ops.kv_write(self.k_view, self.v_view, L.k_cache, L.v_cache, c.kv_heads, c.max_seq, c.head_dim,
@@ -265,8 +265,8 @@ class Decoder:
                       softcap=c.attn_softcap, sliding_window=self.attn_windows[li], kv_len_buffer=self.kvlen_view,
                       stream=stream)
         ops.matmul_q8_0(L.wo, self.attn_out, self.x, c.hidden, c.q_dim, residual=self.x, stream=stream)
-        ops.rmsnorm(self.x, L.norm_ffn, self.xn, 1, c.hidden, c.eps, weight_offset=True, stream=stream)
-        ops.matmul_q8_0(L.wgu, self.xn, self.gu, 2 * c.ffn, c.hidden, stream=stream)
+        ops.matmul_q8_0(L.wgu, self.x, self.gu, 2 * c.ffn, c.hidden, stream=stream, norm_weight=L.norm_ffn,
+                        norm_eps=c.eps, norm_weight_offset=True)
         ops.gelu_gated(self.gate_view, self.up_view, self.h, c.ffn, stream=stream)
         ops.matmul_q8_0(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)
 

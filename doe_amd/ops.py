@@ -65,10 +65,13 @@ def matmul_q4k_gemm(a_bf16: DeviceBuffer, weight: DeviceBuffer, output: DeviceBu
 
 
 def matmul_q8_0(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int,
-                residual: DeviceBuffer | None = None, stream=None) -> None:
+                residual: DeviceBuffer | None = None, stream=None, *, norm_weight: DeviceBuffer | None = None,
+                norm_eps: float = 1e-6, norm_weight_offset: bool = False) -> None:
     """``matmul`` with quantFormat ``q8_0`` at M = 1: output f32[n] =
     dequant(weight)[n][k] @ activation f32[k] (+ residual f32[n]); weight
-    row-wise Q8_0 (34-byte blocks: f16 scale, 32 int8 quants)."""
+    row-wise Q8_0 (34-byte blocks: f16 scale, 32 int8 quants).  With
+    ``norm_weight`` the activation is RMS-normalised first (the
+    ``input_norm`` / ``post_attn_norm`` step folded in)."""
     expected = n * _q8_0.row_bytes(k)
     if weight.nbytes != expected:
         raise ValueError(f"Q8_0 rowwise byte length {weight.nbytes} != expected {expected}")
@@ -76,8 +79,13 @@ def matmul_q8_0(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBu
     _need(output, n * 4, "output")
     if residual is not None:
         _need(residual, n * 4, "residual")
-    _lib.call("doe_q8_0_gemv", _p(weight), _p(activation), _p(output), n, k,
-              None if residual is None else _p(residual), _stream_ptr(stream))
+    res = None if residual is None else _p(residual)
+    if norm_weight is not None:
+        _need(norm_weight, k * 4, "norm_weight")
+        _lib.call("doe_q8_0_gemv_norm", _p(weight), _p(activation), _p(output), n, k, _p(norm_weight), norm_eps,
+                  int(norm_weight_offset), res, _stream_ptr(stream))
+        return
+    _lib.call("doe_q8_0_gemv", _p(weight), _p(activation), _p(output), n, k, res, _stream_ptr(stream))
 
 
 def matmul_int4g32(weight_u4: DeviceBuffer, scales_f16: DeviceBuffer, x: DeviceBuffer, output: DeviceBuffer,

@@ -118,6 +118,13 @@ int doe_q4k_gemv(const void *weight_q4k, const float *activation, float *output,
  * 2-byte aligned), k <= 32768, f32 accumulation. */
 int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, float *output, int64_t n,
                   int64_t k, const float *residual, doe_stream_t stream);
+/* doe_q8_0_gemv of rmsnorm(activation): activation * 1/sqrt(mean(a^2) +
+ * norm_eps) * (norm_weight, or 1 + norm_weight when norm_weight_offset) --
+ * the `input_norm` / `post_attn_norm` step before q/k/v_proj or gate/up_proj
+ * (rmsnorm.wgsl; reference_interpreter.zig:510-526) folded into the GEMV. */
+int doe_q8_0_gemv_norm(const void *weight_q8_0, const float *activation, float *output, int64_t n,
+                       int64_t k, const float *norm_weight, float norm_eps, int norm_weight_offset,
+                       const float *residual, doe_stream_t stream);
 
 /* The attention output projection of one sequence with the split-attention
  * combine folded into its activation load: output[i] = sum_k

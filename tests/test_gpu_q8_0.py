@@ -55,6 +55,21 @@ def test_q8_0_gemv_every_variant(dev, ora, rows, depth):
         ops.tune("q8_0_gemv.depth", 0)
 
 
+@pytest.mark.parametrize("n,k,offset", [(4096, 2304, True), (300, 1000, False), (9, 33, True)])
+def test_q8_0_gemv_with_rmsnorm(dev, ora, n, k, offset):
+    # the input_norm / post_attn_norm step folded in: oracle rmsnorm, then the GEMV
+    rng = np.random.default_rng(n + k)
+    w = q8_0.random_q8_0(rng, n, k)
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    nw = (rng.standard_normal(k) * 0.1).astype(np.float32)
+    r = rng.standard_normal(n, dtype=np.float32)
+    want = ora.q8_0_gemv(w, ora.rmsnorm(x, nw, 1e-6, offset), n, k, residual=r)
+    out = DeviceBuffer.from_array(r)
+    ops.matmul_q8_0(DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), out, n, k, residual=out,
+                    norm_weight=DeviceBuffer.from_array(nw), norm_eps=1e-6, norm_weight_offset=offset)
+    assert rel_l2(out.download(), want) <= 1e-5
+
+
 def test_q8_0_gemv_residual_in_place_and_separate(dev, ora):
     rng = np.random.default_rng(11)
     n, k = 3000, 544
