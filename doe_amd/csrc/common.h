@@ -54,6 +54,14 @@ int q8_0_set_tune(const char *key, int value);  // "q8_0_gemv.rows" / ".depth"
 #define DOE_Q4K_BLOCK_BYTES 144
 #define DOE_Q4K_BLOCK_ELEMS 256
 
+// gelu_tanh with the reference's clamp of the tanh argument
+// (gelu_gated.wgsl:5-8, reference_interpreter.zig:1027-1045).
+__device__ __forceinline__ float doe_gelu_tanh_clamped(float x) {
+    float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    inner = fminf(fmaxf(inner, -15.0f), 15.0f);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
 __device__ __forceinline__ float doe_half_bits_to_float(uint32_t bits16) {
     return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
 }

@@ -68,18 +68,11 @@ __global__ __launch_bounds__(256) void rope_kernel(float *__restrict__ qk,
     }
 }
 
-__device__ __forceinline__ float gelu_tanh_clamped(float x) {
-    // gelu_gated.wgsl:5-8, reference_interpreter.zig:1027-1045
-    float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    inner = fminf(fmaxf(inner, -15.0f), 15.0f);
-    return 0.5f * x * (1.0f + tanhf(inner));
-}
-
 __global__ __launch_bounds__(256) void geglu_kernel(const float *__restrict__ gate,
                                                     const float *__restrict__ up,
                                                     float *__restrict__ out, long n) {
     for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
-        out[i] = gelu_tanh_clamped(gate[i]) * up[i];
+        out[i] = doe_gelu_tanh_clamped(gate[i]) * up[i];
 }
 
 __global__ __launch_bounds__(256) void residual_kernel(const float *__restrict__ a,

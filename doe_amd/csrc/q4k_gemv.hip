@@ -187,12 +187,6 @@ struct GemvFusion {
     int q_rows, kv_rows, head_dim, max_seq;
 };
 
-__device__ __forceinline__ float gelu_tanh_clamped(float v) {
-    float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-    inner = fminf(fmaxf(inner, -15.0f), 15.0f);
-    return 0.5f * v * (1.0f + tanhf(inner));
-}
-
 // Epilogue of one (even row, odd row) pair of a fused q/k/v projection.
 __device__ __forceinline__ void rope_kv_pair(const GemvFusion &fz, int row, float s0, float s1,
                                              float *__restrict__ y) {
@@ -450,7 +444,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_kernel(const uint8_t *__restric
         if (fz.gated) {
             // the partner row (lr ^ 1) is the other 8-lane group of this row of 16 lanes
             const float other = dpp<kDppMirror>(s);
-            if (l8 == 0 && (lr & 1) == 0 && row < n) y[row >> 1] = gelu_tanh_clamped(s) * other;
+            if (l8 == 0 && (lr & 1) == 0 && row < n) y[row >> 1] = doe_gelu_tanh_clamped(s) * other;
         } else if (fz.rope_kv) {
             const float other = dpp<kDppMirror>(s);
             if (l8 == 0 && (lr & 1) == 0 && row < n) rope_kv_pair(fz, row, s, other, y);
@@ -747,7 +741,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
         const int row = row0 + tid;
         if (fz.gated) {
             const float other = dpp<kDppXor1>(s);  // row ^ 1
-            if ((tid & 1) == 0 && row < n) y[row >> 1] = gelu_tanh_clamped(s) * other;
+            if ((tid & 1) == 0 && row < n) y[row >> 1] = doe_gelu_tanh_clamped(s) * other;
         } else if (fz.rope_kv) {
             const float other = dpp<kDppXor1>(s);
             if ((tid & 1) == 0 && row < n) rope_kv_pair(fz, row, s, other, y);
