@@ -428,17 +428,6 @@ int ora_rope_pairs(float *x, const float *cos_t, const float *sin_t, int64_t hea
     return 0;
 }
 
-int ora_gelu(const float *x, float *out, int64_t n) {
-    /* run_csl_webgpu_emulator.mjs:499-507 (tanh form, no clamp). */
-    if (n < 0) return -1;
-    for (int64_t i = 0; i < n; ++i) {
-        float v = x[i];
-        float t = 0.7978845608f * (v + 0.044715f * v * v * v);
-        out[i] = 0.5f * v * (1.0f + tanhf(t));
-    }
-    return 0;
-}
-
 int ora_geglu(const float *gate, const float *up, float *out, int64_t n) {
     /* reference_interpreter.zig:1027-1045 (gelu arm of tryGated) and
      * gelu_gated.wgsl:5-14: inner = a*(x + b*x*x*x) clamped to [-15, 15],

@@ -65,7 +65,6 @@ int ora_rope(float *qk, const float *freq_cis, int64_t seq_len, int64_t num_head
              int64_t head_dim, int64_t position_offset);
 int ora_rope_pairs(float *x, const float *cos_t, const float *sin_t, int64_t head_dim,
                    int64_t num_pairs, int interleaved);
-int ora_gelu(const float *x, float *out, int64_t n);
 int ora_geglu(const float *gate, const float *up, float *out, int64_t n);
 int ora_residual(const float *a, const float *b, float *out, int64_t n);
 int64_t ora_argmax(const float *logits, int64_t n);

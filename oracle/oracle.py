@@ -53,7 +53,6 @@ def lib() -> C.CDLL:
             "ora_rope_table": ([vp, i64, i64, C.c_double], i32),
             "ora_rope": ([vp, vp, i64, i64, i64, i64], i32),
             "ora_rope_pairs": ([vp, vp, vp, i64, i64, i32], i32),
-            "ora_gelu": ([vp, vp, i64], i32),
             "ora_geglu": ([vp, vp, vp, i64], i32),
             "ora_residual": ([vp, vp, vp, i64], i32),
             "ora_argmax": ([vp, i64], i64),
@@ -218,13 +217,6 @@ def rope_pairs(x: np.ndarray, cos_t: np.ndarray, sin_t: np.ndarray, head_dim: in
     c = _c(cos_t, np.float32)
     s = _c(sin_t, np.float32)
     _ok(lib().ora_rope_pairs(_ptr(out), _ptr(c), _ptr(s), head_dim, num_pairs, int(interleaved)), "rope_pairs")
-    return out
-
-
-def gelu(x: np.ndarray) -> np.ndarray:
-    x = _c(x, np.float32)
-    out = np.zeros_like(x)
-    _ok(lib().ora_gelu(_ptr(x), _ptr(out), x.size), "gelu")
     return out
 
 

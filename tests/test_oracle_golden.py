@@ -377,3 +377,120 @@ def test_q4k_gemm_matches_float64_and_sampled(ora):
     mi = np.array([0, 4, 2])
     ni = np.array([6, 0, 3])
     assert np.array_equal(ora.q4k_gemm_sampled(a_bf16, b, m, n, k, mi, ni), c[mi, ni])
+
+
+def test_f16_gemv_matches_float64_dense(ora):
+    # lm_head_gemv.wgsl:78-180 (transpose_b = 1): C[n] = alpha * sum_k A[k] *
+    # f32(B[n][k]).  float64 dense at the decode widths (2304, 5120) and an
+    # odd K; alpha != 1 on both signs.
+    rng = np.random.default_rng(15)
+    for n, k, alpha in [(37, 2304, 0.37), (19, 5120, -2.5), (23, 777, 1.0), (5, 1, 0.125)]:
+        b = (0.02 * rng.standard_normal((n, k))).astype(np.float16)
+        a = rng.standard_normal(k).astype(np.float32)
+        c = ora.f16_gemv(b, a, alpha)
+        ref = alpha * (b.astype(np.float64) @ a.astype(np.float64))
+        # f32 left-fold rounding: ~sqrt(k) ulps; one dropped term would cost ~1e-2
+        assert np.linalg.norm(c - ref) / np.linalg.norm(ref) < 1e-5, (n, k, alpha)
+        # alpha scales the finished sum once (f32 product), not each term
+        c1 = ora.f16_gemv(b, a, 1.0)
+        assert np.array_equal(c, (c1 * np.float32(alpha)).astype(np.float32))
+
+
+def test_f16_gemv_one_hot_and_zero(ora):
+    rng = np.random.default_rng(16)
+    n, k = 9, 300
+    b = rng.standard_normal((n, k)).astype(np.float16)
+    for col in (0, 1, 150, 299):
+        a = np.zeros(k, np.float32)
+        a[col] = 1.0
+        # a one-hot activation selects column `col` exactly (power-of-two alpha)
+        assert np.array_equal(ora.f16_gemv(b, a, 0.25), b[:, col].astype(np.float32) * np.float32(0.25))
+    # the reference transcript's all-zero lm_head input gives all-zero logits
+    assert not ora.f16_gemv(b, np.zeros(k, np.float32), 1.0).any()
+    # rows are independent: row j only reads B[j]
+    a = rng.standard_normal(k).astype(np.float32)
+    assert np.array_equal(ora.f16_gemv(b[3:5], a), ora.f16_gemv(b, a)[3:5])
+
+
+def test_residual_is_ieee_f32_addition(ora):
+    # run_csl_webgpu_emulator.mjs:482-489 / residual.wgsl: out = a + b, one f32
+    # addition per element: bit-equal to numpy's IEEE float32 add, including
+    # signed zeros, infinities, overflow, subnormals and NaN.
+    rng = np.random.default_rng(17)
+    special = np.array([0.0, -0.0, -0.0, np.inf, -np.inf, np.inf, np.nan, 3e38, -3e38, 1e-45, -1e-45,
+                        2.0 ** -126, 1.0, 1.0], np.float32)
+    other = np.array([-0.0, 0.0, -0.0, 1.0, -np.inf, -np.inf, 1.0, 3e38, -3e38, 1e-45, 1e-45,
+                      -2.0 ** -127, 2.0 ** -24, 2.0 ** -23], np.float32)
+    a = np.concatenate([special, rng.standard_normal(4000).astype(np.float32) * 1e3])
+    b = np.concatenate([other, rng.standard_normal(4000).astype(np.float32)])
+    out = ora.residual(a, b)
+    want = np.add(a, b, dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(out), nan)
+    assert np.array_equal(out[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    # the cases that separate a correct add from a plausible slip
+    assert np.signbit(out[0]) == False and np.signbit(out[2]) == True  # +0 + -0 = +0; -0 + -0 = -0
+    assert np.isnan(out[5]) and out[7] == np.inf and out[8] == -np.inf  # inf - inf; overflow
+    assert out[12] == 1.0 and out[13] == np.float32(1.0 + 2.0 ** -23)  # a tie rounds to even
+
+
+# Every function the oracle header declares and the tests above that pin it
+# against something other than its own formula (golden vectors, exact
+# arithmetic, float64 library routines, invariants).
+PINS = {
+    "ora_f16_to_f32": ["test_f16_bf16_conversions"],
+    "ora_f32_to_f16": ["test_f16_bf16_conversions"],
+    "ora_bf16_to_f32": ["test_f16_bf16_conversions"],
+    "ora_f32_to_bf16": ["test_f16_bf16_conversions"],
+    "ora_q4k_unpack_scale_min": ["test_q4k_unpack_known_answer", "test_q4k_scale_min_exhaustive_roundtrip"],
+    "ora_q4k_dequant_block": ["test_q4k_dequant_known_answers", "test_q4k_dequant_is_one_rounding_of_the_exact_value"],
+    "ora_q4k_dequant_rowwise": ["test_q4k_rowwise_tail_padding"],
+    "ora_q4k_gemv": ["test_q4k_gemv_matches_float64_dense", "test_q4k_gemv_one_hot_selects_a_column"],
+    "ora_q4k_gemv_rows": ["test_q4k_gemv_matches_float64_dense"],
+    "ora_q4k_gemm_sampled": ["test_q4k_gemm_matches_float64_and_sampled"],
+    "ora_q4k_gemm": ["test_q4k_gemm_matches_float64_and_sampled"],
+    "ora_f32_gemv": ["test_interp_gemv_known_answer", "test_fixture_fused_gemv"],
+    "ora_f16_gemv": ["test_f16_gemv_matches_float64_dense", "test_f16_gemv_one_hot_and_zero"],
+    "ora_int4g32_gemv": ["test_int4g32_gemv_closed_form"],
+    "ora_q8_0_element_count": ["test_q8_0.py::test_reference_size_checks"],
+    "ora_q8_0_dequant": ["test_q8_0.py::test_known_block_bytes", "test_q8_0.py::test_matches_int4_group32_oracle"],
+    "ora_q8_0_gemv": ["test_q8_0.py::test_tail_block_residual_and_brute_force"],
+    "ora_rmsnorm": ["test_interp_rmsnorm_known_answer", "test_fixture_rmsnorm_transcript",
+                    "test_rmsnorm_weight_offset_and_float64"],
+    "ora_rope_table": ["test_rope_rotate_half_properties"],
+    "ora_rope": ["test_rope_rotate_half_properties"],
+    "ora_rope_pairs": ["test_emulator_rope_known_answer"],
+    "ora_geglu": ["test_geglu_matches_closed_form"],
+    "ora_residual": ["test_residual_is_ieee_f32_addition"],
+    "ora_argmax": ["test_argmax_known_answers"],
+    "ora_embed_gather": ["test_kv_write_and_gather"],
+    "ora_kv_write": ["test_kv_write_and_gather"],
+    "ora_attn_decode": ["test_emulator_attention_known_answer", "test_attention_invariants_and_gqa"],
+    "ora_attn_prefill": ["test_attention_prefill_causal_matches_float64"],
+}
+
+
+def test_every_oracle_function_has_a_pinning_test():
+    import ast
+    import re
+
+    from conftest import ROOT
+
+    header = (ROOT / "oracle" / "doe_oracle.h").read_text()
+    header = re.sub(r"/\*.*?\*/", "", header, flags=re.S)
+    declared = set(re.findall(r"\b(ora_[a-z0-9_]+)\s*\(", header))
+    assert declared == set(PINS), (sorted(declared - set(PINS)), sorted(set(PINS) - declared))
+
+    def test_names(path):
+        tree = ast.parse(path.read_text())
+        return {n.name for n in tree.body if isinstance(n, ast.FunctionDef) and n.name.startswith("test_")}
+
+    here = test_names(ROOT / "tests" / "test_oracle_golden.py")
+    for fn, tests in PINS.items():
+        assert tests, fn
+        for t in tests:
+            if "::" in t:
+                mod, name = t.split("::")
+                assert name in test_names(ROOT / "tests" / mod), (fn, t)
+            else:
+                assert t in here, (fn, t)
