@@ -53,69 +53,98 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def bench_gemv(args, doe):
+def timed_gemv_replays(doe, n, k, steps, warmup, copies, seed):
+    """Q4_K GEMVs over `copies` distinct weight copies, replayed from HIP
+    graphs: exactly `steps` launches in the timed region (full replays of one
+    launch per copy, then a partial replay for the remainder), HIP events on
+    the kernel's stream after every replay.  Returns the per-launch times."""
     from doe_amd import DeviceBuffer, Event, Graph, Stream, ops, q4k
 
-    rng = np.random.default_rng(0)
-    w = q4k.random_q4k(rng, N, K)
-    x = rng.standard_normal(K, dtype=np.float32)
-    log(f"gemv: N={N} K={K}, {args.copies} weight copies of {w.nbytes} B")
-    copies = [DeviceBuffer.from_array(w)]
-    for _ in range(args.copies - 1):
+    rng = np.random.default_rng(seed)
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k, dtype=np.float32)
+    copies = max(1, min(copies, steps))
+    bufs = [DeviceBuffer.from_array(w)]
+    for _ in range(copies - 1):
         b = DeviceBuffer(w.nbytes)
-        b.copy_from(copies[0])
-        copies.append(b)
+        b.copy_from(bufs[0])
+        bufs.append(b)
     dx = DeviceBuffer.from_array(x)
-    dy = DeviceBuffer.empty((N,), np.float32)
+    dy = DeviceBuffer.empty((n,), np.float32)
     doe.synchronize()
-
     s = Stream()
-    per_graph = args.copies
-    graph = Graph.capture(s, lambda: [ops.matmul_q4k(c, dx, dy, N, K, s) for c in copies])
-    # warmup
-    reps_w = max(1, -(-args.warmup // per_graph))
-    for _ in range(reps_w):
+    full, rest = divmod(steps, copies)
+    graph = Graph.capture(s, lambda: [ops.matmul_q4k(c, dx, dy, n, k, s) for c in bufs])
+    tail = Graph.capture(s, lambda: [ops.matmul_q4k(c, dx, dy, n, k, s) for c in bufs[:rest]]) if rest else None
+    for _ in range(max(1, -(-warmup // copies))):
         graph.launch(s)
     s.synchronize()
-
-    # timed region: whole-job throughput over K steps (graph replays)
-    reps = max(1, -(-args.steps // per_graph))
-    steps = reps * per_graph
-    e0, e1 = Event(), Event()
+    ev = [Event() for _ in range(full + 2)]
     doe.synchronize()
     t0 = time.perf_counter()
-    e0.record(s)
-    for _ in range(reps):
+    ev[0].record(s)
+    for i in range(full):
         graph.launch(s)
-    e1.record(s)
-    e1.synchronize()
+        ev[i + 1].record(s)
+    if tail is not None:
+        tail.launch(s)
+    ev[full + 1].record(s)
+    ev[full + 1].synchronize()
     wall = time.perf_counter() - t0
-    total_ms = e0.elapsed_ms(e1)
-    ms_per_step = total_ms / steps
-
-    # correctness of the timed kernel on these inputs
-    from oracle import oracle as ora
+    total_ms = ev[0].elapsed_ms(ev[full + 1])
+    per_replay = [ev[i].elapsed_ms(ev[i + 1]) / copies for i in range(full)]
+    from oracle import oracle as ora  # the checker, outside the timed region
 
     got = dy.download()
-    want = ora.q4k_gemv(w, x, N, K)
+    want = ora.q4k_gemv(w, x, n, k)
     rel = float(np.linalg.norm(got.astype(np.float64) - want) / np.linalg.norm(want))
-    log(f"gemv: rel_l2 vs oracle {rel:.3e}; {ms_per_step * 1e3:.2f} us/launch over the timed "
-        f"region, wall {wall:.3f}s")
-    graph.destroy()
+    for g in (graph, tail):
+        if g is not None:
+            g.destroy()
     s.destroy()
-    for c in copies:
+    for c in bufs:
         c.free()
     return {
         "steps": steps,
-        "ms_per_step": ms_per_step,
-        "value_gbs": GEMV_BYTES / (ms_per_step * 1e-3) / 1e9,
-        "kernel_ms": ms_per_step,
-        "kernel_gbs": GEMV_BYTES / (ms_per_step * 1e-3) / 1e9,
+        "copies": copies,
+        "replays": full + (1 if rest else 0),
+        "ms_per_step": total_ms / steps,
+        "median_ms_per_launch": float(np.median(per_replay)) if per_replay else total_ms / steps,
+        "wall_s": wall,
         "rel_l2": rel,
-        "kernel": "q4k_gemv_mfma_kernel<0> (doe_amd/csrc/q4k_gemv.hip)",
         "w": w,
         "x": x,
     }
+
+
+def bench_gemv(args, doe):
+    log(f"gemv: N={N} K={K}, {args.steps} launches over {args.copies} weight copies")
+    r = timed_gemv_replays(doe, N, K, args.steps, args.warmup, args.copies, seed=0)
+    log(f"gemv: rel_l2 vs oracle {r['rel_l2']:.3e}; {r['ms_per_step'] * 1e3:.3f} us/launch over "
+        f"{r['steps']} launches ({r['replays']} graph replays, median {r['median_ms_per_launch'] * 1e3:.3f} "
+        f"us/launch), wall {r['wall_s']:.3f}s")
+    r["value_gbs"] = GEMV_BYTES / (r["ms_per_step"] * 1e-3) / 1e9
+    r["kernel"] = "q4k_gemv_mfma_kernel<0> (doe_amd/csrc/q4k_gemv.hip)"
+    return r
+
+
+GL_N = 65536
+
+
+def bench_gemv_large(args, doe):
+    """The same Q4_K GEMV kernel at N=65536, K=2304 (85 MB of weights per
+    launch), where the per-dispatch latency is amortised over more bytes."""
+    byt = GL_N * (K // 256) * 144 + 4 * K + 4 * GL_N
+    copies = max(2, -(-768 * 2 ** 20 // (GL_N * (K // 256) * 144)))
+    r = timed_gemv_replays(doe, GL_N, K, max(args.large_steps, 5 * copies), 2 * copies, copies, seed=5)
+    gbs = byt / (r["ms_per_step"] * 1e-3) / 1e9
+    log(f"gemv N={GL_N} K={K}: {r['ms_per_step'] * 1e3:.2f} us/launch, {gbs:.0f} GB/s "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of peak), rel_l2 {r['rel_l2']:.2e}")
+    return {"workload": f"q4k_gemv M=1 N={GL_N} K={K}, {copies} rotating weight copies, HIP-graph replay",
+            "launches": r["steps"], "us_per_launch": round(r["ms_per_step"] * 1e3, 3),
+            "median_us_per_launch": round(r["median_ms_per_launch"] * 1e3, 3), "bytes_per_launch": byt,
+            "achieved_gbs": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "rel_l2_vs_oracle": r["rel_l2"]}
 
 
 ATT_HQ, ATT_HKV, ATT_D, ATT_T = 8, 4, 256, 4096
@@ -210,6 +239,7 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
     ids = dec.generate(prompt, args.decode_steps, s, graph=graph, steps_per_graph=max(spg, 1), timing=timing)
     if graph is not None:
         graph.destroy()
+    parity, cpu = decode_parity_and_cpu(dec, prompt, s)
     tok_s = args.decode_steps / timing["decode_s"]
     mean_len = args.prompt_len + (args.decode_steps + 1) / 2.0
     bpt = cfg.decode_bytes_per_token(mean_len)
@@ -230,7 +260,41 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
         "ceiling_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
         "prompt_s": round(timing["prompt_s"], 4),
         "last_tokens": [int(t) for t in ids[-4:]],
+        "parity": parity,
+        "cpu_baseline": cpu,
     }
+
+
+def decode_parity_and_cpu(dec, prompt, s):
+    """Outside the timed region: one eager decode step at position 0 with the
+    logits kept, against the oracle decoder (the CPU restatement composed from
+    the oracle's kernels, on the device's weights); the oracle step's own
+    single-threaded time is the decode CPU baseline."""
+    from oracle.decoder import OracleDecoder
+
+    dec.keep_logits = True
+    dec.reset(prompt)
+    dec.step(s)
+    s.synchronize()
+    got = dec.logits.download().astype(np.float64)
+    tok = int(dec.token.download()[0])
+    dec.keep_logits = False
+    oracle = OracleDecoder(dec)
+    t0 = time.perf_counter()
+    want = oracle.step(0, int(prompt[0]))
+    el = time.perf_counter() - t0
+    rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    del oracle
+    log(f"  decode parity: step-0 logits rel_l2 {rel:.2e}, token {tok} vs oracle {int(np.argmax(want))}; "
+        f"oracle step {el:.2f} s")
+    parity = {"step0_logits_rel_l2_vs_oracle": rel, "step0_token_equal": tok == int(np.argmax(want)),
+              "tolerance": 1e-3}
+    cpu = {"value": round(1.0 / el, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+           "sample": f"one full-size decode step (position 0, every weight of every layer and the lm_head) of "
+                     f"the single-threaded C oracle decoder (f32 left-fold, -O2 -ffp-contract=off) in {el:.2f} s "
+                     f"on {cpu_model()} ({os.cpu_count()} logical cores on host); attention at position 0 "
+                     f"reads 1 key (< 1% of a token's bytes at the benchmarked lengths)"}
+    return parity, cpu
 
 
 def bench_decode_graph(args, doe):
@@ -549,6 +613,7 @@ def main() -> int:
     ap.add_argument("--steps-per-graph", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--gemm-steps", type=int, default=20)
+    ap.add_argument("--large-steps", type=int, default=45)
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -571,6 +636,7 @@ def main() -> int:
     log(f"device {info}")
 
     g = bench_gemv(args, doe_amd)
+    gl = None if args.no_gemm else bench_gemv_large(args, doe_amd)
     att = bench_attention(args, doe_amd)
     dec = None if args.no_decode else bench_decode(args, doe_amd)
     dec_graph = None if args.no_decode else bench_decode_graph(args, doe_amd)
@@ -604,22 +670,26 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": f"q4k_gemv M=1 N={N} K={K} (Q4_K_M weights, f32 activation/output), "
-                        f"{args.copies} rotating weight copies, HIP-graph replay",
+                        f"{g['copies']} rotating weight copies, HIP-graph replay",
             "bytes_per_step": GEMV_BYTES,
             "pct_of_hbm_peak": round(100.0 * g["value_gbs"] / HBM_PEAK_GBS, 2),
             "rel_l2_vs_oracle": g["rel_l2"],
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(g["kernel_gbs"], 2),
+            "achieved": round(g["value_gbs"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(g["kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "frac": round(g["value_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic_bytes("q4k_gemv_n9216_k2304.md"),
             "kernel": g["kernel"],
-            "kernel_us": round(g["kernel_ms"] * 1e3, 3),
+            "kernel_us": round(g["ms_per_step"] * 1e3, 3),
+            "median_kernel_us": round(g["median_ms_per_launch"] * 1e3, 3),
+            "launches": g["steps"],
+            "graph_replays": g["replays"],
         },
         "cpu_baseline": cpu,
+        "gemv_n65536": gl,
         "attention_decode": att,
         "decode": dec,
         "decode_graph_gemma3_270m": dec_graph,

@@ -68,10 +68,54 @@ __device__ __forceinline__ float blk_dot(const Blk &bk, uint32_t off, const floa
     return d * fmaf(-128.0f, sxb, s0 + s1);
 }
 
+// The activation as split-attention partials (doe_attn_decode_partials):
+// x[h * D + d] = sum_s o[h][s][d] 2^(m_s - M) / sum_s l_s 2^(m_s - M),
+// M = max_s m_s, with o [heads][S][D] then (m, l) [heads][S][2].
+constexpr int kAttnMaxSplits = 8;
+
+struct Q8Attn {
+    const float *o;   // nullptr: x is a plain f32 vector
+    const float *ml;
+    int splits, head_dim;
+};
+
+__device__ __forceinline__ float4 attn_combine4(const Q8Attn &at, int e) {
+    const int S = at.splits, D = at.head_dim;
+    const int h = e / D, d = e - h * D;  // e % 4 == 0 and D % 4 == 0: one head
+    float2 ml[kAttnMaxSplits];
+    float M = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+        if (sp < S) {
+            ml[sp] = *reinterpret_cast<const float2 *>(at.ml + ((size_t)h * S + sp) * 2);
+            M = fmaxf(M, ml[sp].x);
+        }
+    }
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float L = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+        for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+            if (sp < S) {
+                const float f = exp2f(ml[sp].x - M);
+                const float4 o = *reinterpret_cast<const float4 *>(at.o + ((size_t)h * S + sp) * D + d);
+                L = fmaf(ml[sp].y, f, L);
+                acc.x = fmaf(o.x, f, acc.x);
+                acc.y = fmaf(o.y, f, acc.y);
+                acc.z = fmaf(o.z, f, acc.z);
+                acc.w = fmaf(o.w, f, acc.w);
+            }
+        }
+    }
+    const float rl = L > 0.0f ? 1.0f / L : 0.0f;
+    return make_float4(acc.x * rl, acc.y * rl, acc.z * rl, acc.w * rl);
+}
+
 template <int R, int D>
 __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
     const uint8_t *__restrict__ w, const float *__restrict__ x, float *y, const float *res, int n,
-    int k, int nb, int q64, int r64, bool x_vec, const float *norm_w, float norm_eps, int norm_offset) {
+    int k, int nb, int q64, int r64, bool x_vec, const float *norm_w, float norm_eps, int norm_offset,
+    Q8Attn at) {
     static_assert(D == 1 || D == 2, "one or two units in flight ahead");
     extern __shared__ float lds[];
     float *xs = lds;                          // [nb][kXStride]
@@ -132,7 +176,9 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (i < nb * 8) {
             const int e = 4 * i;
-            if (x_vec && e + 3 < k) {
+            if (at.o) {
+                if (e < k) v = attn_combine4(at, e);  // k % 4 == 0 in this form
+            } else if (x_vec && e + 3 < k) {
                 v = *reinterpret_cast<const float4 *>(x + e);
             } else {
                 if (e < k) v.x = x[e];
@@ -221,7 +267,7 @@ struct Q8Norm {
 
 template <int R, int D>
 int q8_0_launch(const uint8_t *w, const float *x, float *y, const float *res, int n, int k, int nb,
-                const Q8Norm &fz, hipStream_t st) {
+                const Q8Norm &fz, const Q8Attn &at, hipStream_t st) {
     static const hipError_t attr_rc = hipFuncSetAttribute(
         reinterpret_cast<const void *>(&q8_0_gemv_kernel<R, D>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxBlocks * (kXStride + 1) * 4 + kWaves * 4);
@@ -233,16 +279,16 @@ int q8_0_launch(const uint8_t *w, const float *x, float *y, const float *res, in
     const size_t lds = (size_t)nb * (kXStride + 1) * 4 + kWaves * 4;
     hipLaunchKernelGGL((q8_0_gemv_kernel<R, D>), dim3((unsigned)blocks), dim3(kWaves * 64), lds, st,
                        w, x, y, res, n, k, nb, 64 / nb, 64 % nb, ((uintptr_t)x & 15) == 0, fz.norm_w,
-                       fz.norm_eps, fz.norm_offset);
+                       fz.norm_eps, fz.norm_offset, at);
     DOE_LAUNCH_CHECK("q8_0_gemv_kernel");
     return DOE_OK;
 }
 
 template <int R>
 int q8_0_launch_depth(const uint8_t *w, const float *x, float *y, const float *res, int n, int k,
-                      int nb, const Q8Norm &fz, hipStream_t st) {
-    if (g_tune_depth == 2) return q8_0_launch<R, 2>(w, x, y, res, n, k, nb, fz, st);
-    return q8_0_launch<R, 1>(w, x, y, res, n, k, nb, fz, st);
+                      int nb, const Q8Norm &fz, const Q8Attn &at, hipStream_t st) {
+    if (g_tune_depth == 2) return q8_0_launch<R, 2>(w, x, y, res, n, k, nb, fz, at, st);
+    return q8_0_launch<R, 1>(w, x, y, res, n, k, nb, fz, at, st);
 }
 
 }  // namespace
@@ -250,7 +296,8 @@ int q8_0_launch_depth(const uint8_t *w, const float *x, float *y, const float *r
 namespace {
 
 int q8_0_gemv_impl(const void *weight_q8_0, const float *activation, float *output, int64_t n,
-                   int64_t k, const float *residual, const Q8Norm &fz, doe_stream_t stream) {
+                   int64_t k, const float *residual, const Q8Norm &fz, doe_stream_t stream,
+                   const Q8Attn &at = Q8Attn{nullptr, nullptr, 0, 0}) {
     int rc = doe::require_init();
     if (rc) return rc;
     const hipStream_t st = (hipStream_t)stream;
@@ -263,7 +310,11 @@ int q8_0_gemv_impl(const void *weight_q8_0, const float *activation, float *outp
             DOE_HIP_CHECK(hipMemcpyAsync(output, residual, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
         return DOE_OK;
     }
-    DOE_REQUIRE(weight_q8_0 && activation, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(weight_q8_0 && (activation || at.o), DOE_E_INVALID, "null pointer");
+    // every workgroup stages the whole activation while others already write
+    // output rows: only the residual may alias the output
+    DOE_REQUIRE(activation != output && fz.norm_w != output && (!at.o || (at.o != output && at.ml != output)),
+                DOE_E_INVALID, "the activation and norm weight must not alias the output (only the residual may)");
     const int64_t nb = (k + 31) / 32;
     DOE_REQUIRE(nb <= kMaxBlocks, DOE_E_UNSUPPORTED,
                 "q8_0_gemv needs k <= %d (got %lld)", kMaxBlocks * 32, (long long)k);
@@ -290,9 +341,9 @@ int q8_0_gemv_impl(const void *weight_q8_0, const float *activation, float *outp
             r *= 2;
         while (r < 4 && (n + r - 1) / r > (int64_t)g_num_cus * 8 * kWaves) r *= 2;
     }
-    if (r == 4) return q8_0_launch_depth<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, st);
-    if (r == 2) return q8_0_launch_depth<2>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, st);
-    return q8_0_launch_depth<1>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, st);
+    if (r == 4) return q8_0_launch_depth<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, at, st);
+    if (r == 2) return q8_0_launch_depth<2>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, at, st);
+    return q8_0_launch_depth<1>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, at, st);
 }
 
 }  // namespace
@@ -309,6 +360,20 @@ extern "C" int doe_q8_0_gemv_norm(const void *weight_q8_0, const float *activati
     DOE_REQUIRE(norm_weight, DOE_E_INVALID, "null norm weight");
     return q8_0_gemv_impl(weight_q8_0, activation, output, n, k, residual,
                           Q8Norm{norm_weight, norm_eps, norm_weight_offset ? 1 : 0}, stream);
+}
+
+extern "C" int doe_q8_0_gemv_attn_out(const void *weight_q8_0, const float *attn_partials, int64_t splits,
+                                      int64_t num_heads, int64_t head_dim, float *output, int64_t n,
+                                      const float *residual, doe_stream_t stream) {
+    DOE_REQUIRE(attn_partials, DOE_E_INVALID, "null partials");
+    DOE_REQUIRE(splits >= 1 && splits <= kAttnMaxSplits, DOE_E_UNSUPPORTED,
+                "attention combine prologue supports 1..%d splits (got %lld)", kAttnMaxSplits, (long long)splits);
+    DOE_REQUIRE(num_heads > 0 && head_dim > 0 && head_dim % 4 == 0 && num_heads * head_dim <= 0x7fffffff,
+                DOE_E_INVALID, "bad head shape");
+    DOE_REQUIRE(((uintptr_t)attn_partials & 15) == 0, DOE_E_INVALID, "partials must be 16-byte aligned");
+    const Q8Attn at{attn_partials, attn_partials + num_heads * splits * head_dim, (int)splits, (int)head_dim};
+    return q8_0_gemv_impl(weight_q8_0, nullptr, output, n, num_heads * head_dim, residual,
+                          Q8Norm{nullptr, 0.0f, 0}, stream, at);
 }
 
 namespace doe {

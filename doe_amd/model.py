@@ -162,8 +162,7 @@ class Decoder:
         # split-attention partials: o [heads][S][D] then (m, l) [heads][S][2]
         self.attn_parts = DeviceBuffer.empty((c.heads * self.max_attn_splits * (c.head_dim + 2),), np.float32)
         self.h = DeviceBuffer.empty((c.ffn,), np.float32)
-        if c.weight_format == "q8_0":  # unfused step: attention output, gate/up
-            self.attn_out = DeviceBuffer.empty((c.q_dim,), np.float32)
+        if c.weight_format == "q8_0":  # unfused step: gate/up
             self.gu = DeviceBuffer.empty((2 * c.ffn,), np.float32)
             self.gate_view = self.gu.view(0, c.ffn * 4, np.float32)
             self.up_view = self.gu.view(c.ffn * 4, c.ffn * 4, np.float32)
@@ -249,10 +248,13 @@ class Decoder:
                   _stream_ptr(stream))
 
     def _layer_q8_0(self, li: int, L: LayerWeights, scale: float, stream) -> None:
-        """One layer with Q8_0 projections: the step graph's ops, the norms and
-        residuals folded into the GEMVs (input_norm + q/k/v_proj, rope_q /
-        rope_k, the cache write, attention, o_proj + attn_residual,
-        post_attn_norm + gate/up_proj, activation, down_proj + ffn_residual)."""
+        """One layer with Q8_0 projections: the step graph's ops, the norms,
+        residuals and the attention combine folded into the GEMVs (input_norm +
+        q/k/v_proj, rope_q / rope_k, the cache write, attention as split
+        partials into the decoder's own buffer, combine + o_proj +
+        attn_residual, post_attn_norm + gate/up_proj, activation, down_proj +
+        ffn_residual): eight dispatches, no library workspace, so a captured
+        graph stays valid whatever other attention calls the process makes."""
         c = self.cfg
         ops.matmul_q8_0(L.wqkv, self.x, self.qkv, c.qkv_rows, c.hidden, stream=stream, norm_weight=L.norm_attn,
                         norm_eps=c.eps, norm_weight_offset=True)
@@ -260,11 +262,13 @@ class Decoder:
                  stream=stream)
         ops.kv_write(self.k_view, self.v_view, L.k_cache, L.v_cache, c.kv_heads, c.max_seq, c.head_dim,
                      position_buffer=self.pos_view, stream=stream)
-        ops.attention(self.q_view, L.k_cache, L.v_cache, self.attn_out, batch=1, num_heads=c.heads,
-                      num_kv_heads=c.kv_heads, head_dim=c.head_dim, kv_len=0, kv_stride=c.max_seq, scale=scale,
-                      softcap=c.attn_softcap, sliding_window=self.attn_windows[li], kv_len_buffer=self.kvlen_view,
-                      stream=stream)
-        ops.matmul_q8_0(L.wo, self.attn_out, self.x, c.hidden, c.q_dim, residual=self.x, stream=stream)
+        splits = ops.attention_partials(self.q_view, L.k_cache, L.v_cache, self.attn_parts, batch=1,
+                                        num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim, kv_len=0,
+                                        kv_stride=c.max_seq, scale=scale, max_splits=self.max_attn_splits,
+                                        kv_len_buffer=self.kvlen_view, sliding_window=self.attn_windows[li],
+                                        softcap=c.attn_softcap, stream=stream)
+        ops.matmul_q8_0_attn_out(L.wo, self.attn_parts, splits, c.heads, c.head_dim, self.x, c.hidden,
+                                 residual=self.x, stream=stream)
         ops.matmul_q8_0(L.wgu, self.x, self.gu, 2 * c.ffn, c.hidden, stream=stream, norm_weight=L.norm_ffn,
                         norm_eps=c.eps, norm_weight_offset=True)
         ops.gelu_gated(self.gate_view, self.up_view, self.h, c.ffn, stream=stream)

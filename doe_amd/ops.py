@@ -88,6 +88,24 @@ def matmul_q8_0(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBu
     _lib.call("doe_q8_0_gemv", _p(weight), _p(activation), _p(output), n, k, res, _stream_ptr(stream))
 
 
+def matmul_q8_0_attn_out(weight: DeviceBuffer, partials: DeviceBuffer, splits: int, num_heads: int,
+                         head_dim: int, output: DeviceBuffer, n: int, residual: DeviceBuffer | None = None,
+                         stream=None) -> None:
+    """Q8_0 ``o_proj`` (+ ``attn_residual``) over the combine of the attention
+    partials of ``attention_partials`` (the caller's buffer)."""
+    k = num_heads * head_dim
+    expected = n * _q8_0.row_bytes(k)
+    if weight.nbytes != expected:
+        raise ValueError(f"Q8_0 rowwise byte length {weight.nbytes} != expected {expected}")
+    _need(partials, num_heads * splits * (head_dim + 2) * 4, "partials")
+    _need(output, n * 4, "output")
+    if residual is not None:
+        _need(residual, n * 4, "residual")
+    res = None if residual is None else _p(residual)
+    _lib.call("doe_q8_0_gemv_attn_out", _p(weight), _p(partials), splits, num_heads, head_dim, _p(output), n, res,
+              _stream_ptr(stream))
+
+
 def matmul_int4g32(weight_u4: DeviceBuffer, scales_f16: DeviceBuffer, x: DeviceBuffer, output: DeviceBuffer,
                    m: int, n: int, k: int, stream=None) -> None:
     """Fused int4 group-32 dequant GEMV (``complex_fused_gemv_dequant``) over a

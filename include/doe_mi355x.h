@@ -125,6 +125,15 @@ int doe_q8_0_gemv(const void *weight_q8_0, const float *activation, float *outpu
 int doe_q8_0_gemv_norm(const void *weight_q8_0, const float *activation, float *output, int64_t n,
                        int64_t k, const float *norm_weight, float norm_eps, int norm_weight_offset,
                        const float *residual, doe_stream_t stream);
+/* doe_q8_0_gemv whose activation is the combine of the split-attention
+ * partials written by doe_attn_decode_partials (batch 1, k = num_heads x
+ * head_dim, 1..8 splits; the combine formula is given there): the attention
+ * combine + o_proj + attn_residual steps of a Q8_0 decode step in one
+ * dispatch, reading the caller's partials buffer (no library workspace).
+ * In every Q8_0 entry point only the residual may alias the output. */
+int doe_q8_0_gemv_attn_out(const void *weight_q8_0, const float *attn_partials, int64_t splits,
+                           int64_t num_heads, int64_t head_dim, float *output, int64_t n,
+                           const float *residual, doe_stream_t stream);
 
 /* The attention output projection of one sequence with the split-attention
  * combine folded into its activation load: output[i] = sum_k

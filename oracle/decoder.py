@@ -1,4 +1,5 @@
-"""CPU oracle of the decode step (test infrastructure): the same step the
+"""CPU oracle of the decode step (TEST INFRASTRUCTURE ONLY: the checker of
+the decode loop in tests/ and bench.py, never on the product path): the same step the
 Decoder runs, composed from the oracle's kernel restatements, on weights
 downloaded from the device."""
 import math
@@ -7,7 +8,7 @@ import numpy as np
 
 from doe_amd import q4k
 from doe_amd.ops import deinterleave_rope_rows
-from oracle import oracle as ora
+from . import oracle as ora
 
 
 class OracleDecoder:

@@ -41,9 +41,11 @@ def dev():
 
 @pytest.fixture(params=[1, 2], ids=["dot_kernel", "mfma_kernel"])
 def gemv_kernel(request, dev):
-    """Forces one Q4_K GEMV kernel for k <= 4096 (1: per-chunk dot products,
-    2: matrix cores; larger k always uses the dot-product kernel) and restores
-    the automatic choice afterwards."""
+    """Forces one Q4_K GEMV kernel (1: per-chunk dot products, 2: matrix
+    cores) and restores the automatic choice afterwards.  The automatic choice
+    is the matrix-core kernel (K split over workgroups past k = 16384); the
+    dot-product kernel runs only when forced, where its LDS holds the
+    activation."""
     from doe_amd import ops
     ops.tune("q4k_gemv.kernel", request.param)
     yield request.param

@@ -11,7 +11,7 @@ import pytest
 from doe_amd import Stream
 from doe_amd.model import Decoder, DecoderConfig
 
-from decode_oracle import OracleDecoder
+from oracle.decoder import OracleDecoder
 
 pytestmark = pytest.mark.gpu
 
@@ -109,17 +109,50 @@ def test_graph_replay_equals_eager(dev):
         assert out.tolist() == eager.tolist(), steps_per_graph
 
 
-def test_full_size_first_steps(dev, ora):
+def test_q8_0_graph_survives_a_larger_attention_call(dev):
+    # The Q8_0 layer keeps its attention partials in the decoder's own buffer:
+    # a later attention call that needs a larger library workspace (which is
+    # freed and reallocated) leaves a captured step graph valid.
+    from doe_amd import DeviceBuffer, ops
+
+    dec = Decoder(SMALL_Q8)
+    dec.init_random(seed=11)
+    s = Stream()
+    prompt = np.arange(1, 6, dtype=np.int32) * 77
+    eager = dec.generate(prompt, 10, s)
+    dec.reset(prompt)
+    dec.step(s)
+    s.synchronize()
+    g = dec.capture(s, 1)
+    hq, hkv, d, t = 32, 8, 128, 8192  # many splits: a workspace larger than any before
+    q = DeviceBuffer.empty((1, hq, d), np.float32)
+    kc = DeviceBuffer.empty((1, hkv, t, d), np.float16)
+    vc = DeviceBuffer.empty((1, hkv, t, d), np.float16)
+    for b in (q, kc, vc):
+        b.upload(np.zeros(b.nbytes, np.uint8))
+    o = DeviceBuffer.empty((1, hq, d), np.float32)
+    ops.attention(q, kc, vc, o, batch=1, num_heads=hq, num_kv_heads=hkv, head_dim=d, kv_len=t, kv_stride=t,
+                  scale=0.1, stream=s)
+    s.synchronize()
+    out = dec.generate(prompt, 10, s, graph=g, steps_per_graph=1)
+    g.destroy()
+    assert out.tolist() == eager.tolist()
+
+
+@pytest.mark.parametrize("weight_format", ["q4k", "q8_0"])
+def test_full_size_first_steps(dev, ora, weight_format):
     # the 2B-class shape itself: 26 layers, hidden 2304, 8/4 heads of 256,
-    # FFN 9216, vocab 256000; two teacher-forced steps against the oracle.
-    cfg = DecoderConfig()
+    # FFN 9216, vocab 256000, Q4_K or Q8_0 projections (the Q8_0 form runs
+    # the 6-split attention into the decoder's partials); two teacher-forced
+    # steps against the oracle.
+    cfg = DecoderConfig(weight_format=weight_format)
     dec = Decoder(cfg, keep_logits=True)
     dec.init_random(seed=2)
     s = Stream()
     oracle = OracleDecoder(dec)
     prompt = np.array([12345, 200000], np.int32)
     ids, errs = run_teacher_forced(dec, oracle, prompt, 1, s)
-    print(f"[decode 2B] logits rel_l2 per step {errs}", flush=True)
+    print(f"[decode 2B {weight_format}] logits rel_l2 per step {errs}", flush=True)
     assert max(errs) <= 1e-3
 
 

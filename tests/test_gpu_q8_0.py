@@ -144,3 +144,45 @@ def test_q8_0_gemv_rejects(dev):
                   None, None)
     with pytest.raises(ValueError, match="byte length"):
         ops.matmul_q8_0(dw, dx, out, n, k)
+
+
+@pytest.mark.parametrize("heads,kv_heads,d,t,n", [(8, 4, 256, 300, 2304), (4, 1, 128, 37, 640), (2, 2, 64, 1, 100)])
+def test_q8_0_gemv_attn_out_matches_oracle(dev, ora, heads, kv_heads, d, t, n):
+    # split-attention partials (doe_attn_decode_partials) combined in the
+    # Q8_0 GEMV's activation staging, against the oracle attention followed by
+    # the oracle Q8_0 GEMV with the residual
+    print(f"q8_0 attn_out heads={heads}/{kv_heads} d={d} t={t} n={n}", flush=True)
+    rng = np.random.default_rng(heads * 1000 + t)
+    q = rng.standard_normal((heads, d)).astype(np.float32)
+    kc = rng.standard_normal((kv_heads, t, d)).astype(np.float16)
+    vc = rng.standard_normal((kv_heads, t, d)).astype(np.float16)
+    w = q8_0.random_q8_0(rng, n, heads * d)
+    res = rng.standard_normal(n).astype(np.float32)
+    parts = DeviceBuffer.empty((heads * 8 * (d + 2),), np.float32)
+    scale = 1.0 / np.sqrt(d)
+    splits = ops.attention_partials(DeviceBuffer.from_array(q), DeviceBuffer.from_array(kc),
+                                    DeviceBuffer.from_array(vc), parts, batch=1, num_heads=heads,
+                                    num_kv_heads=kv_heads, head_dim=d, kv_len=t, kv_stride=t, scale=scale)
+    out = DeviceBuffer.from_array(res)
+    ops.matmul_q8_0_attn_out(DeviceBuffer.from_array(w), parts, splits, heads, d, out, n, residual=out)
+    attn = ora.attn_decode(q, kc, vc, heads, kv_heads, d, t, t, scale).reshape(-1)
+    want = ora.q8_0_gemv(w, attn, n, heads * d, residual=res)
+    err = rel_l2(out.download(), want)
+    print(f"  splits {splits} rel_l2 {err:.2e}", flush=True)
+    assert err <= 1e-3, err
+
+
+def test_q8_0_gemv_rejects_aliased_activation(dev):
+    n = k = 64
+    dw = DeviceBuffer(n * q8_0.row_bytes(k))
+    x = DeviceBuffer.empty((k,), np.float32)
+    with pytest.raises(DoeError, match="alias"):
+        _lib.call("doe_q8_0_gemv", C.c_void_p(dw.ptr), C.c_void_p(x.ptr), C.c_void_p(x.ptr), n, k, None, None)
+    nw = DeviceBuffer.empty((k,), np.float32)
+    out = DeviceBuffer.empty((n,), np.float32)
+    with pytest.raises(DoeError, match="alias"):
+        _lib.call("doe_q8_0_gemv_norm", C.c_void_p(dw.ptr), C.c_void_p(x.ptr), C.c_void_p(nw.ptr), n, k,
+                  C.c_void_p(nw.ptr), C.c_float(1e-6), 0, None, None)
+    with pytest.raises(DoeError, match="splits"):
+        _lib.call("doe_q8_0_gemv_attn_out", C.c_void_p(dw.ptr), C.c_void_p(out.ptr), 9, 1, 64, C.c_void_p(x.ptr),
+                  n, None, None)
