@@ -79,6 +79,8 @@ SIGNATURES: dict[str, list] = {
     "doe_attention_dispatch": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "doe_attn_decode": [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i32,
                         _f32, _f32, _i64, _vp],
+    "doe_attn_decode_noalloc": [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i32,
+                                _f32, _f32, _i64, _vp],
     "doe_q4k_gemv_fused": [_vp, _vp, _vp, _i64, _i64, _vp, _f32, _i32, _vp, _i32, _vp],
     "doe_q4k_gemv_qkv_rope_kv": [_vp, _vp, _vp, _i64, _vp, _f32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64,
                                  _vp],

@@ -33,6 +33,18 @@
 #include <math.h>
 #include <mutex>
 
+// The allocation-free form's split partials (doe_attn_decode_noalloc): a
+// file-scope device array of kScratchBytes, one copy per GPU at its own
+// address, looked up once per device by doe_init with that device current.
+// Host code uses only that looked-up address (g_scratch_dev), never the
+// array's name.  Every split workgroup writes its (m, l, o) partial
+// unconditionally before the combine reads it, so nothing needs clearing;
+// calls that overlap on one GPU share the array and race.
+static constexpr size_t kScratchBytes = (size_t)16 << 20;
+static constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+static float *g_scratch_dev[kMaxDevices] = {};
+
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -445,6 +457,7 @@ std::mutex g_ws_mu;
 void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
 
+
 int g_num_cus = 0;
 int g_tune_splits = 0;
 int g_tune_waves = 0;
@@ -490,6 +503,15 @@ int launch_d(int g, bool w, dim3 grid, hipStream_t st, const AttnArgs &a) {
 }  // namespace
 
 namespace doe {
+int attn_scratch_setup(int device) {
+    DOE_REQUIRE(device >= 0 && device < kMaxDevices, DOE_E_UNSUPPORTED, "device %d >= %d", device, kMaxDevices);
+    if (g_scratch_dev[device]) return DOE_OK;
+    void *p = nullptr;
+    DOE_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    DOE_REQUIRE(p != nullptr, DOE_E_HIP, "hipGetSymbolAddress returned a null scratch address");
+    g_scratch_dev[device] = static_cast<float *>(p);
+    return DOE_OK;
+}
 int attn_set_splits(int v) {
     g_tune_splits = v;
     return DOE_OK;
@@ -519,7 +541,8 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
                      int64_t head_dim, int64_t kv_len, const int32_t *kv_len_dev, int64_t kv_stride,
                      int kv_layout, float scale, float softcap, int64_t sliding_window,
                      float *parts, int64_t parts_capacity, int64_t max_splits_req, int32_t *splits_out,
-                     doe_stream_t stream, const KvMap &map = KvMap()) {
+                     doe_stream_t stream, const KvMap &map = KvMap(), float *fixed_ws = nullptr,
+                     size_t fixed_ws_bytes = 0) {
     int rc = doe::require_init();
     if (rc) return rc;
     DOE_REQUIRE(batch >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && kv_stride >= 0,
@@ -610,6 +633,16 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
         a.ws_o = parts;
         a.ws_ml = parts + o_count;
         if (splits_out) *splits_out = (int32_t)splits;
+    } else if (splits > 1 && fixed_ws) {  // allocation-free: the caller-supplied fixed array
+        const size_t o_bytes = (size_t)batch * num_heads * splits * head_dim * 4;
+        const size_t ml_off = (o_bytes + 255) & ~(size_t)255;
+        const size_t need = ml_off + (size_t)batch * num_heads * splits * 2 * 4;
+        DOE_REQUIRE(need <= fixed_ws_bytes, DOE_E_UNSUPPORTED,
+                    "split partials of %zu bytes (%lld sequences x %lld heads x %lld splits x head_dim %lld) "
+                    "exceed the %zu-byte allocation-free scratch", need, (long long)batch, (long long)num_heads,
+                    (long long)splits, (long long)head_dim, fixed_ws_bytes);
+        a.ws_o = fixed_ws;
+        a.ws_ml = (float *)((char *)fixed_ws + ml_off);
     } else if (splits > 1) {
         const size_t o_bytes = (size_t)batch * num_heads * splits * head_dim * 4;
         const size_t ml_bytes = (size_t)batch * num_heads * splits * 2 * 4;
@@ -658,6 +691,23 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
     return attn_decode_impl(q, q_f16, k_cache, v_cache, out, out_f16, batch, num_heads, num_kv_heads,
                             head_dim, kv_len, kv_len_dev, kv_stride, kv_layout, scale, softcap,
                             sliding_window, nullptr, 0, 0, nullptr, stream);
+}
+
+int doe_attn_decode_noalloc(const void *q, int q_f16, const uint16_t *k_cache, const uint16_t *v_cache,
+                            void *out, int out_f16, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                            int64_t head_dim, int64_t kv_len, const int32_t *kv_len_dev, int64_t kv_stride,
+                            int kv_layout, float scale, float softcap, int64_t sliding_window,
+                            doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    int dev = -1;
+    DOE_HIP_CHECK(hipGetDevice(&dev));
+    DOE_REQUIRE(dev >= 0 && dev < kMaxDevices && g_scratch_dev[dev], DOE_E_NOT_INIT,
+                "doe_init(%d) was not called: the allocation-free scratch of device %d is not set up", dev, dev);
+    return attn_decode_impl(q, q_f16, k_cache, v_cache, out, out_f16, batch, num_heads, num_kv_heads,
+                            head_dim, kv_len, kv_len_dev, kv_stride, kv_layout, scale, softcap,
+                            sliding_window, nullptr, 0, 0, nullptr, stream, KvMap(), g_scratch_dev[dev],
+                            kScratchBytes);
 }
 
 int doe_attention_dispatch(const doe_attention_uniforms *u, const float *q, const uint16_t *k,

@@ -24,6 +24,8 @@ int require_init();
 // Fills bytes [dst, dst + bytes) with `value` on a stream with a kernel
 // (capturable into a HIP graph; no memset node).  Returns a DOE status.
 int fill_bytes_async(void *dst, int value, size_t bytes, hipStream_t st);
+// Looks up the allocation-free attention scratch of `device` (current).
+int attn_scratch_setup(int device);
 // Tuning hooks of individual kernels (0 = automatic).
 int attn_set_splits(int value);
 int attn_set_waves(int value);

@@ -77,6 +77,9 @@ int doe_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return doe::set_error(DOE_E_UNSUPPORTED, "device %d is %s; this library is built for gfx950",
                               device, prop.gcnArchName);
+    // per-device address of the allocation-free entry point's scratch array
+    const int src = doe::attn_scratch_setup(device);
+    if (src) return src;
     doe::g_device = device;
     doe::clear_error();
     return DOE_OK;

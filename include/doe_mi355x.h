@@ -257,6 +257,25 @@ int doe_attn_decode(const void *q, int q_f16, const uint16_t *k_cache, const uin
                     const int32_t *kv_len_dev, int64_t kv_stride, int kv_layout, float scale,
                     float softcap, int64_t sliding_window, doe_stream_t stream);
 
+/* doe_attn_decode for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference, whose attention dispatch computes its
+ * online softmax in one workgroup pass and so has no split partials.  Same
+ * arguments, split choice and results as doe_attn_decode, but the split
+ * partials live in a fixed 16 MiB device array per GPU (set up by doe_init;
+ * DOE_E_NOT_INIT before that on the current device) instead of the library's
+ * grow-only workspace: the call makes no hipMalloc / hipFree / synchronising
+ * call.  Shapes whose partials exceed the array (batch x num_heads x splits x
+ * (head_dim + 2) floats, 256-byte aligned halves) are rejected with
+ * DOE_E_UNSUPPORTED.  Every call on one GPU shares that GPU's array: calls
+ * that overlap in time on one GPU (different streams) race. */
+int doe_attn_decode_noalloc(const void *q, int q_f16, const uint16_t *k_cache,
+                            const uint16_t *v_cache, void *out, int out_f16, int64_t batch,
+                            int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                            int64_t kv_len, const int32_t *kv_len_dev, int64_t kv_stride,
+                            int kv_layout, float scale, float softcap, int64_t sliding_window,
+                            doe_stream_t stream);
+
 /* The reference attention dispatch itself: its Uniforms block field for
  * field (attention_head256_f16kv.wgsl:14-30) and its bindings Q (1), K (2),
  * V (3), output (4), kv_len_buffer (5), page_table (6), in the decode form
