@@ -88,6 +88,7 @@ SIGNATURES: dict[str, list] = {
     "doe_rope": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp],
     "doe_geglu": [_vp, _vp, _vp, _i64, _vp],
     "doe_residual_add": [_vp, _vp, _vp, _i64, _vp],
+    "doe_ple_modulate": [_vp, _vp, _vp, _i64, _f32, _vp],
     "doe_argmax": [_vp, _i64, _vp, _vp, _vp],
     "doe_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _vp],
     "doe_embed_gather": [_vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp],

@@ -75,11 +75,19 @@ __global__ __launch_bounds__(256) void geglu_kernel(const float *__restrict__ ga
         out[i] = doe_gelu_tanh_clamped(gate[i]) * up[i];
 }
 
-__global__ __launch_bounds__(256) void residual_kernel(const float *__restrict__ a,
-                                                       const float *__restrict__ b,
-                                                       float *__restrict__ out, long n) {
+// out may be a or b: each element is read before it is written
+__global__ __launch_bounds__(256) void residual_kernel(const float *a, const float *b, float *out, long n) {
     for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
         out[i] = a[i] + b[i];
+}
+
+// (projected + gathered) * scale: one f32 add, then one f32 multiply (no fma)
+__global__ __launch_bounds__(256) void ple_modulate_kernel(const float *__restrict__ a,
+                                                           const float *__restrict__ b,
+                                                           float *__restrict__ out, long n, float scale) {
+#pragma clang fp contract(off)
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+        out[i] = (a[i] + b[i]) * scale;
 }
 
 // Argmax keys: ordered float bits in the high word, inverted index in the low
@@ -224,6 +232,19 @@ int doe_residual_add(const float *input, const float *residual, float *output, i
     hipLaunchKernelGGL(residual_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, input,
                        residual, output, (long)n);
     DOE_LAUNCH_CHECK("residual_kernel");
+    return DOE_OK;
+}
+
+int doe_ple_modulate(const float *projected, const float *gathered, float *output, int64_t n, float scale,
+                     doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n >= 0, DOE_E_INVALID, "negative size");
+    if (n == 0) return DOE_OK;
+    DOE_REQUIRE(projected && gathered && output, DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(ple_modulate_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, projected,
+                       gathered, output, (long)n, scale);
+    DOE_LAUNCH_CHECK("ple_modulate_kernel");
     return DOE_OK;
 }
 

@@ -1008,10 +1008,13 @@ int doe_q4k_gemv_qkv_rope_kv(const void *weight_q4k, const float *activation, fl
                              int64_t head_dim, const float *freq_cis, const int32_t *position_dev,
                              uint16_t *key_cache, uint16_t *val_cache, int64_t max_seq_len,
                              doe_stream_t stream) {
-    DOE_REQUIRE(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && (head_dim % 2) == 0 &&
+    DOE_REQUIRE(num_heads > 0 && num_kv_heads >= 0 && head_dim > 0 && (head_dim % 2) == 0 &&
                     max_seq_len > 0,
                 DOE_E_INVALID, "bad qkv shape");
-    DOE_REQUIRE(freq_cis && position_dev && key_cache && val_cache, DOE_E_INVALID, "null pointer");
+    // num_kv_heads 0: the q rows alone (a layer that reads another layer's
+    // KV cache), no cache row is written and the caches may be NULL
+    DOE_REQUIRE(freq_cis && position_dev && (num_kv_heads == 0 || (key_cache && val_cache)), DOE_E_INVALID,
+                "null pointer");
     GemvFusion fz{};
     fz.norm_w = norm_weight;
     fz.norm_eps = norm_eps;

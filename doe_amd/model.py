@@ -55,6 +55,16 @@ class DecoderConfig:
     # between the unfused norm / RoPE / KV-write / attention / GeGLU ops): the
     # modelConfig quantFormat of emit_csl_exec_v1.zig:279-284
     weight_format: str = "q4k"
+    # RMSNorm weights used as 1 + w (Gemma 2/3) or as w (Gemma 4)
+    norm_weight_offset: bool = True
+    # Gemma 4 (modelConfig globalHeadDim, pleWidth, pleVocabSize;
+    # emit_csl_exec_v1.zig:296-305): the head_dim of global-attention layers
+    # (0: head_dim) with its rotary base (0: rope_base), and the width and
+    # table rows of the per-layer embeddings (0: none; rows 0: vocab)
+    global_head_dim: int = 0
+    rope_base_global: float = 0.0
+    ple_width: int = 0
+    ple_vocab: int = 0
 
     @property
     def q_dim(self) -> int:
@@ -81,22 +91,27 @@ class DecoderConfig:
         return (self.qkv_rows * rb(self.hidden) + self.hidden * rb(self.q_dim)
                 + 2 * self.ffn * rb(self.hidden) + self.hidden * rb(self.ffn))
 
+    @property
+    def ple_dim(self) -> int:
+        """Per-layer embedding values per token: layers x ple_width."""
+        return self.layers * self.ple_width
+
     @classmethod
     def from_model_config(cls, mc: dict, **overrides) -> "DecoderConfig":
         """From a step graph's modelConfig (hiddenDim, numHeads, headDim,
-        numKeyValueHeads, numLayers, vocabSize, maxSeqLen, ffnExpansionFactor);
-        quantFormat q4k or q8_0; a separate globalHeadDim or quantFormat f16 is
-        not supported."""
+        numKeyValueHeads, numLayers, vocabSize, maxSeqLen, ffnExpansionFactor,
+        globalHeadDim, pleWidth, pleVocabSize); quantFormat q4k or q8_0
+        (f16 is not supported)."""
         from .execution import UnsupportedStep
 
         fmt = mc.get("quantFormat", "q4k")
         if fmt not in ("q4k", "q8_0"):
             raise UnsupportedStep(f"quantFormat {fmt!r}")
-        if mc.get("globalHeadDim", mc["headDim"]) != mc["headDim"]:
-            raise UnsupportedStep(f"globalHeadDim {mc['globalHeadDim']} != headDim {mc['headDim']}")
         kw = dict(layers=mc["numLayers"], hidden=mc["hiddenDim"], heads=mc["numHeads"],
                   kv_heads=mc["numKeyValueHeads"], head_dim=mc["headDim"], vocab=mc["vocabSize"],
-                  ffn=mc["hiddenDim"] * mc.get("ffnExpansionFactor", 4), weight_format=fmt)
+                  ffn=mc["hiddenDim"] * mc.get("ffnExpansionFactor", 4), weight_format=fmt,
+                  global_head_dim=mc.get("globalHeadDim") or 0, ple_width=mc.get("pleWidth") or 0,
+                  ple_vocab=mc.get("pleVocabSize") or 0)
         if "maxSeqLen" in mc:
             kw["max_seq"] = mc["maxSeqLen"]
         kw.update(overrides)
@@ -123,44 +138,106 @@ def rope_table(max_pos: int, head_dim: int, base: float) -> np.ndarray:
 
 
 class LayerWeights:
-    def __init__(self, cfg: DecoderConfig):
+    def __init__(self, cfg: DecoderConfig, head_dim: int | None = None, shared_kv: bool = False):
+        """head_dim: this layer's (a global layer's may differ); shared_kv: the
+        layer projects q only and its attention reads an earlier layer's cache,
+        so it has no k/v rows and no cache of its own."""
         rb = cfg.row_bytes
+        self.head_dim = hd = head_dim or cfg.head_dim
+        self.shared_kv = shared_kv
+        self.q_dim = cfg.heads * hd
+        self.kv_dim = 0 if shared_kv else cfg.kv_heads * hd
+        self.qkv_rows = self.q_dim + 2 * self.kv_dim
         # q4k: q/k rows as interleaved rotation pairs, gate/up rows interleaved
         # (gate_0, up_0, gate_1, ...) for the fused kernels; q8_0: plain q/k
         # rows (rotate-half RoPE op), gate rows then up rows
-        self.wqkv = DeviceBuffer(cfg.qkv_rows * rb(cfg.hidden))
-        self.wo = DeviceBuffer(cfg.hidden * rb(cfg.q_dim))
+        self.wqkv = DeviceBuffer(self.qkv_rows * rb(cfg.hidden))
+        self.wo = DeviceBuffer(cfg.hidden * rb(self.q_dim))
         self.wgu = DeviceBuffer(2 * cfg.ffn * rb(cfg.hidden))
         self.wd = DeviceBuffer(cfg.hidden * rb(cfg.ffn))
         self.norm_attn = DeviceBuffer.empty((cfg.hidden,), np.float32)
         self.norm_ffn = DeviceBuffer.empty((cfg.hidden,), np.float32)
-        self.k_cache = DeviceBuffer.empty((cfg.kv_heads, cfg.max_seq, cfg.head_dim), np.float16)
-        self.v_cache = DeviceBuffer.empty((cfg.kv_heads, cfg.max_seq, cfg.head_dim), np.float16)
+        self.k_cache = self.v_cache = None
+        if not shared_kv:
+            self.k_cache = DeviceBuffer.empty((cfg.kv_heads, cfg.max_seq, hd), np.float16)
+            self.v_cache = DeviceBuffer.empty((cfg.kv_heads, cfg.max_seq, hd), np.float16)
+        if cfg.ple_width:
+            # the per-layer input block: gate [P][hidden], projection [hidden][P]
+            # (Q4_K) and the norm of the projection
+            self.w_ple_gate = DeviceBuffer(cfg.ple_width * rb(cfg.hidden))
+            self.w_ple_out = DeviceBuffer(cfg.hidden * rb(cfg.ple_width))
+            self.norm_ple = DeviceBuffer.empty((cfg.hidden,), np.float32)
+
+    def weight_bytes(self) -> int:
+        b = self.wqkv.nbytes + self.wo.nbytes + self.wgu.nbytes + self.wd.nbytes
+        if hasattr(self, "w_ple_gate"):
+            b += self.w_ple_gate.nbytes + self.w_ple_out.nbytes
+        return b
 
 
 class Decoder:
     """Device-resident weights, KV cache and activations of one decoder."""
 
     def __init__(self, cfg: DecoderConfig, keep_logits: bool = False, plan=None):
-        """plan: an execution.DecodePlan (per-layer attention windows); None =
-        global attention in every layer."""
+        """plan: an execution.DecodePlan (per-layer attention windows, head
+        dims, KV-cache sources, per-layer embeddings); None = global attention
+        in every layer at the model's head_dim, every layer its own cache."""
+        from .execution import UnsupportedStep
+
         self.cfg = cfg
         self.keep_logits = keep_logits  # also write the logits (tests); the sample does not need them
-        self.attn_windows = tuple(plan.windows) if plan is not None else (0,) * cfg.layers
-        if len(self.attn_windows) != cfg.layers:
-            raise ValueError(f"plan covers {len(self.attn_windows)} layers, the model has {cfg.layers}")
         c = cfg
-        self.layers = [LayerWeights(c) for _ in range(c.layers)]
+        L = c.layers
+        self.attn_windows = tuple(plan.windows) if plan is not None else (0,) * L
+        self.head_dims = tuple(plan.head_dims) if plan is not None and plan.head_dims else (c.head_dim,) * L
+        self.kv_sources = tuple(plan.kv_sources) if plan is not None and plan.kv_sources else tuple(range(L))
+        for name, v in (("windows", self.attn_windows), ("head dims", self.head_dims),
+                        ("KV sources", self.kv_sources)):
+            if len(v) != L:
+                raise ValueError(f"plan {name} cover {len(v)} layers, the model has {L}")
+        if any(self.kv_sources[s] != s or s >= li for li, s in enumerate(self.kv_sources) if s != li):
+            raise ValueError(f"KV sources {self.kv_sources}: a shared layer must read an earlier owning layer")
+        if plan is not None and plan.ple is not None and not c.ple_width:
+            raise UnsupportedStep("per-layer embedding steps in a model without pleWidth")
+        self.ple = bool(c.ple_width)
+        gemma4 = self.ple or any(s != li for li, s in enumerate(self.kv_sources)) or len(set(self.head_dims)) > 1
+        if gemma4 and c.weight_format != "q4k":
+            raise UnsupportedStep("per-layer embeddings, shared-KV layers and a global head_dim need q4k weights")
+        self.layers = [LayerWeights(c, self.head_dims[li], self.kv_sources[li] != li) for li in range(L)]
         self.embed = DeviceBuffer.empty((c.vocab, c.hidden), np.float16)
         self.lm_head = DeviceBuffer.empty((c.vocab, c.hidden), np.float16)
         self.norm_final = DeviceBuffer.empty((c.hidden,), np.float32)
-        self.freq_cis = DeviceBuffer.from_array(rope_table(c.max_seq, c.head_dim, c.rope_base))
+        # rotary tables per (head_dim, base): a global layer may differ in both
+        self._tables = {}
+        self.freq_by_layer = []
+        for li in range(L):
+            key = (self.head_dims[li], c.rope_base_global or c.rope_base if self.attn_windows[li] == 0 else c.rope_base)
+            if key not in self._tables:
+                self._tables[key] = DeviceBuffer.from_array(rope_table(c.max_seq, key[0], key[1]))
+            self.freq_by_layer.append(self._tables[key])
+        self.freq_cis = self.freq_by_layer[0]
         self.x = DeviceBuffer.empty((c.hidden,), np.float32)
         self.xn = DeviceBuffer.empty((c.hidden,), np.float32)
-        self.qkv = DeviceBuffer.empty((c.qkv_rows,), np.float32)
+        max_rows = max(Lw.qkv_rows for Lw in self.layers)
+        self.qkv = DeviceBuffer.empty((max_rows,), np.float32)
         self.max_attn_splits = 8
         # split-attention partials: o [heads][S][D] then (m, l) [heads][S][2]
-        self.attn_parts = DeviceBuffer.empty((c.heads * self.max_attn_splits * (c.head_dim + 2),), np.float32)
+        self.attn_parts = DeviceBuffer.empty((c.heads * self.max_attn_splits * (max(self.head_dims) + 2),),
+                                             np.float32)
+        if self.ple:
+            P, PD = c.ple_width, c.ple_dim
+            self.ple_table = DeviceBuffer.empty((c.ple_vocab or c.vocab, PD), np.float16)
+            self.ple_proj = DeviceBuffer.empty((PD, c.hidden), np.float16)
+            self.ple_norm = DeviceBuffer.empty((P,), np.float32)
+            self.ple_e = DeviceBuffer.empty((PD,), np.float32)   # gathered rows
+            self.ple_p = DeviceBuffer.empty((PD,), np.float32)   # projected
+            self.ple_pn = DeviceBuffer.empty((PD,), np.float32)  # projected, normalised per layer
+            self.ple_u = DeviceBuffer.empty((PD,), np.float32)   # per-layer inputs
+            self.ple_g = DeviceBuffer.empty((P,), np.float32)
+            self.ple_h = DeviceBuffer.empty((P,), np.float32)
+            self.ple_y = DeviceBuffer.empty((c.hidden,), np.float32)
+            self.ple_yn = DeviceBuffer.empty((c.hidden,), np.float32)
+            self.ple_u_views = [self.ple_u.view(li * P * 4, P * 4, np.float32) for li in range(L)]
         self.h = DeviceBuffer.empty((c.ffn,), np.float32)
         if c.weight_format == "q8_0":  # unfused step: gate/up
             self.gu = DeviceBuffer.empty((2 * c.ffn,), np.float32)
@@ -171,12 +248,14 @@ class Decoder:
         self.state = DeviceBuffer.empty((4,), np.int32)  # pos, kv_len, prompt_len, token
         self.ids = DeviceBuffer.empty((c.max_seq,), np.int32)
         self.argmax_parts = DeviceBuffer(1024 * 8)
-        # views of the fused QKV output
+        # views of the fused QKV output (the uniform model's shapes; per-layer
+        # q views for layers of another head_dim)
         f4 = 4
         self.q_view = self.qkv.view(0, c.q_dim * f4, np.float32)
         self.qk_view = self.qkv.view(0, (c.q_dim + c.kv_dim) * f4, np.float32)
         self.k_view = self.qkv.view(c.q_dim * f4, c.kv_dim * f4, np.float32)
         self.v_view = self.qkv.view((c.q_dim + c.kv_dim) * f4, c.kv_dim * f4, np.float32)
+        self.q_views = [self.qkv.view(0, Lw.q_dim * f4, np.float32) for Lw in self.layers]
         self.pos_view = self.state.view(0, 4, np.int32)
         self.kvlen_view = self.state.view(4, 4, np.int32)
         self.tok_view = self.state.view(12, 4, np.int32)
@@ -198,10 +277,13 @@ class Decoder:
             _lib.call("doe_fill_random_q4k", C.c_void_p(buf.ptr), buf.nbytes // _q4k.BLOCK_BYTES, s + tag, 0.02,
                       0.01, sp)
 
-        def nrm(buf, tag, sigma, dtype_f16=False):
+        # norm weights: N(0, 0.1) used as 1 + w, or 1 + N(0, 0.1) used as w
+        nmean = 0.0 if c.norm_weight_offset else 1.0
+
+        def nrm(buf, tag, sigma, dtype_f16=False, mean=0.0):
             fn = "doe_fill_normal_f16" if dtype_f16 else "doe_fill_normal_f32"
             n = buf.nbytes // (2 if dtype_f16 else 4)
-            _lib.call(fn, C.c_void_p(buf.ptr), n, s + tag, 0.0, sigma, sp)
+            _lib.call(fn, C.c_void_p(buf.ptr), n, s + tag, mean, sigma, sp)
 
         for i, L in enumerate(self.layers):
             base = 100 * (i + 1)
@@ -209,43 +291,88 @@ class Decoder:
             q4k(L.wo, base + 2)
             q4k(L.wgu, base + 3)
             q4k(L.wd, base + 4)
-            nrm(L.norm_attn, base + 5, 0.1)
-            nrm(L.norm_ffn, base + 6, 0.1)
+            nrm(L.norm_attn, base + 5, 0.1, mean=nmean)
+            nrm(L.norm_ffn, base + 6, 0.1, mean=nmean)
+            if self.ple:
+                q4k(L.w_ple_gate, base + 10)
+                q4k(L.w_ple_out, base + 11)
+                nrm(L.norm_ple, base + 12, 0.1, mean=nmean)
         nrm(self.embed, 7, 0.02, True)
         nrm(self.lm_head, 8, 0.02, True)
-        nrm(self.norm_final, 9, 0.1)
+        nrm(self.norm_final, 9, 0.1, mean=nmean)
+        if self.ple:
+            nrm(self.ple_table, 13, 0.02, True)
+            nrm(self.ple_proj, 14, 0.02, True)
+            nrm(self.ple_norm, 15, 0.1, mean=nmean)
 
     # ---- one decode step -------------------------------------------------------
     def step(self, stream=None) -> None:
         """Enqueues one decode step at position state.pos on `stream`."""
         c = self.cfg
         ops.embed(self.embed, self.tok_view, self.x, 1, c.vocab, c.hidden, c.embed_scale, stream=stream)
-        scale = 1.0 / math.sqrt(c.head_dim)
+        if self.ple:
+            self._ple_inputs(stream)
         for li, L in enumerate(self.layers):
             if c.weight_format == "q8_0":
-                self._layer_q8_0(li, L, scale, stream)
+                self._layer_q8_0(li, L, 1.0 / math.sqrt(c.head_dim), stream)
                 continue
-            ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads, num_kv_heads=c.kv_heads,
-                            head_dim=c.head_dim, freq_cis=self.freq_cis, position_buffer=self.pos_view,
-                            key_cache=L.k_cache, val_cache=L.v_cache, max_seq_len=c.max_seq,
-                            norm_weight=L.norm_attn, norm_eps=c.eps, norm_weight_offset=True, stream=stream)
-            splits = ops.attention_partials(self.q_view, L.k_cache, L.v_cache, self.attn_parts, batch=1,
-                                            num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim,
-                                            kv_len=0, kv_stride=c.max_seq, scale=scale,
+            hd = L.head_dim
+            src = self.layers[self.kv_sources[li]]  # the layer whose KV cache this one reads
+            ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads,
+                            num_kv_heads=0 if L.shared_kv else c.kv_heads, head_dim=hd,
+                            freq_cis=self.freq_by_layer[li], position_buffer=self.pos_view, key_cache=L.k_cache,
+                            val_cache=L.v_cache, max_seq_len=c.max_seq, norm_weight=L.norm_attn, norm_eps=c.eps,
+                            norm_weight_offset=c.norm_weight_offset, stream=stream)
+            splits = ops.attention_partials(self.q_views[li], src.k_cache, src.v_cache, self.attn_parts, batch=1,
+                                            num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=hd,
+                                            kv_len=0, kv_stride=c.max_seq, scale=1.0 / math.sqrt(hd),
                                             max_splits=self.max_attn_splits, kv_len_buffer=self.kvlen_view,
                                             sliding_window=self.attn_windows[li], softcap=c.attn_softcap,
                                             stream=stream)
-            ops.matmul_q4k_attn_out(L.wo, self.attn_parts, splits, c.heads, c.head_dim, self.x, c.hidden,
+            ops.matmul_q4k_attn_out(L.wo, self.attn_parts, splits, c.heads, hd, self.x, c.hidden,
                                     residual=self.x, stream=stream)
             ops.matmul_q4k_fused(L.wgu, self.x, self.h, 2 * c.ffn, c.hidden, norm_weight=L.norm_ffn,
-                                 norm_eps=c.eps, norm_weight_offset=True, gated=True, stream=stream)
+                                 norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset, gated=True, stream=stream)
             ops.matmul_q4k_fused(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)
+            if self.ple:
+                self._ple_block(li, L, stream)
         nparts = ops.lm_head_sample(self.lm_head, self.x, c.vocab, c.hidden, self.argmax_parts,
                                     logits=self.logits if self.keep_logits else None, norm_weight=self.norm_final,
-                                    norm_eps=c.eps, norm_weight_offset=True, stream=stream)
+                                    norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset, stream=stream)
         _lib.call("doe_decode_advance", C.c_void_p(self.state.ptr), C.c_void_p(self.token.ptr),
                   C.c_void_p(self.ids.ptr), c.max_seq, C.c_void_p(self.argmax_parts.ptr), nparts,
                   _stream_ptr(stream))
+
+    def _ple_inputs(self, stream) -> None:
+        """The step graph's ple_gather, ple_project, ple_norm and ple_modulate
+        steps (emit_csl_exec_v1.zig:167-172: gather + matmul + reduction +
+        element_wise), once per token, for every layer at once: the token's
+        row of the per-layer embedding table scaled by sqrt(P), the embedding
+        projected by the f16 model projection (scaled by hidden^-1/2) and
+        RMS-normalised per layer, then (projected + gathered) / sqrt(2) -- the
+        per-layer inputs of the Gemma 4 architecture (pleWidth P, every layer's
+        P values side by side)."""
+        c = self.cfg
+        P, PD = c.ple_width, c.ple_dim
+        ops.embed(self.ple_table, self.tok_view, self.ple_e, 1, c.ple_vocab or c.vocab, PD, math.sqrt(P),
+                  stream=stream)
+        ops.lm_head(self.ple_proj, self.x, self.ple_p, PD, c.hidden, alpha=c.hidden ** -0.5, stream=stream)
+        ops.rmsnorm(self.ple_p, self.ple_norm, self.ple_pn, c.layers, P, c.eps,
+                    weight_offset=c.norm_weight_offset, stream=stream)
+        ops.ple_modulate(self.ple_pn, self.ple_e, self.ple_u, PD, 2.0 ** -0.5, stream=stream)
+
+    def _ple_block(self, li: int, L: LayerWeights, stream) -> None:
+        """A layer's use of its per-layer input u (after ffn_residual): x +=
+        rmsnorm(W_out . (gelu(W_gate . x) * u)) -- the Gemma 4 decoder layer's
+        per-layer input block, which the step graph's PLE composite feeds."""
+        c = self.cfg
+        P = c.ple_width
+        ops.matmul_q4k(L.w_ple_gate, self.x, self.ple_g, P, c.hidden, stream=stream)
+        ops.gelu_gated(self.ple_g, self.ple_u_views[li], self.ple_h, P, stream=stream)
+        ops.matmul_q4k(L.w_ple_out, self.ple_h, self.ple_y, c.hidden, P, stream=stream)
+        ops.rmsnorm(self.ple_y, L.norm_ple, self.ple_yn, 1, c.hidden, c.eps, weight_offset=c.norm_weight_offset,
+                    stream=stream)
+        ops.residual(self.ple_yn, self.x, self.x, c.hidden, stream=stream)
 
     def _layer_q8_0(self, li: int, L: LayerWeights, scale: float, stream) -> None:
         """One layer with Q8_0 projections: the step graph's ops, the norms,
@@ -257,7 +384,7 @@ class Decoder:
         graph stays valid whatever other attention calls the process makes."""
         c = self.cfg
         ops.matmul_q8_0(L.wqkv, self.x, self.qkv, c.qkv_rows, c.hidden, stream=stream, norm_weight=L.norm_attn,
-                        norm_eps=c.eps, norm_weight_offset=True)
+                        norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset)
         ops.rope(self.qk_view, self.freq_cis, 1, c.heads + c.kv_heads, c.head_dim, position_buffer=self.pos_view,
                  stream=stream)
         ops.kv_write(self.k_view, self.v_view, L.k_cache, L.v_cache, c.kv_heads, c.max_seq, c.head_dim,
@@ -270,7 +397,7 @@ class Decoder:
         ops.matmul_q8_0_attn_out(L.wo, self.attn_parts, splits, c.heads, c.head_dim, self.x, c.hidden,
                                  residual=self.x, stream=stream)
         ops.matmul_q8_0(L.wgu, self.x, self.gu, 2 * c.ffn, c.hidden, stream=stream, norm_weight=L.norm_ffn,
-                        norm_eps=c.eps, norm_weight_offset=True)
+                        norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset)
         ops.gelu_gated(self.gate_view, self.up_view, self.h, c.ffn, stream=stream)
         ops.matmul_q8_0(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)
 

@@ -256,14 +256,17 @@ def qkv_rope_kv(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBu
     _need(activation, hidden * 4, "activation")
     _need(output, n * 4, "output")
     cache = num_kv_heads * max_seq_len * head_dim * 2
-    _need(key_cache, cache, "key_cache")
-    _need(val_cache, cache, "val_cache")
+    if num_kv_heads:  # 0: q rows only, no cache (a shared-KV layer)
+        _need(key_cache, cache, "key_cache")
+        _need(val_cache, cache, "val_cache")
     _need(freq_cis, max_seq_len * head_dim * 4, "freq_cis")
     _need(position_buffer, 4, "position_buffer")
     nw = C.c_void_p(norm_weight.ptr) if norm_weight is not None else C.c_void_p(None)
+    kc = _p(key_cache) if num_kv_heads else C.c_void_p(None)
+    vc = _p(val_cache) if num_kv_heads else C.c_void_p(None)
     _lib.call("doe_q4k_gemv_qkv_rope_kv", _p(weight), _p(activation), _p(output), hidden, nw, norm_eps,
               int(norm_weight_offset), num_heads, num_kv_heads, head_dim, _p(freq_cis), _p(position_buffer),
-              _p(key_cache), _p(val_cache), max_seq_len, _stream_ptr(stream))
+              kc, vc, max_seq_len, _stream_ptr(stream))
 
 
 def interleave_rope_rows(rows: np.ndarray, head_dim: int) -> np.ndarray:
@@ -317,6 +320,14 @@ def residual(input: DeviceBuffer, residual_in: DeviceBuffer, output: DeviceBuffe
     for buf, role in ((input, "input"), (residual_in, "residual"), (output, "output")):
         _need(buf, n * 4, role)
     _lib.call("doe_residual_add", _p(input), _p(residual_in), _p(output), n, _stream_ptr(stream))
+
+
+def ple_modulate(projected: DeviceBuffer, gathered: DeviceBuffer, output: DeviceBuffer, n: int, scale: float,
+                 stream=None) -> None:
+    """``ple_modulate`` step: output = (projected + gathered) * scale."""
+    for b, role in ((projected, "projected"), (gathered, "gathered"), (output, "output")):
+        _need(b, n * 4, role)
+    _lib.call("doe_ple_modulate", _p(projected), _p(gathered), _p(output), n, scale, _stream_ptr(stream))
 
 
 def sample(logits: DeviceBuffer, n: int, token: DeviceBuffer, workspace: DeviceBuffer, stream=None) -> None:

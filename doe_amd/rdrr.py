@@ -214,6 +214,10 @@ def load_decoder_weights(art: RdrrArtifact, dec) -> None:
     dtype).  input_layernorm feeds attention, post_attention_layernorm the
     FFN (the step graph's post_attn_norm before gate_proj)."""
     c = dec.cfg
+    if dec.ple or len(set(dec.head_dims)) > 1 or dec.kv_sources != tuple(range(c.layers)):
+        from .execution import UnsupportedStep
+
+        raise UnsupportedStep("loading per-layer embeddings, shared-KV layers or a global head_dim from RDRR")
     q8 = c.weight_format == "q8_0"
     rb_h, rb_q, rb_f = c.row_bytes(c.hidden), c.row_bytes(c.q_dim), c.row_bytes(c.ffn)
     for i, L in enumerate(dec.layers):

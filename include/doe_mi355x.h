@@ -204,7 +204,10 @@ int doe_q4k_gemv_fused(const void *weight_q4k, const float *activation, float *o
  * time; q . k is unchanged because q and k share it, and k is cached in the
  * same order).  norm_weight may be NULL (no norm).  freq_cis holds
  * max_seq_len positions; a position outside [0, max_seq_len) leaves q/k
- * unrotated and writes no cache row. */
+ * unrotated and writes no cache row.  num_kv_heads 0 projects and rotates the
+ * q rows only (a shared-KV layer, whose attention reads an earlier layer's
+ * cache: numKvSharedLayers, emit_csl_exec_v1.zig:720-723); the caches may
+ * then be NULL. */
 int doe_q4k_gemv_qkv_rope_kv(const void *weight_q4k, const float *activation, float *output,
                              int64_t hidden, const float *norm_weight, float norm_eps,
                              int norm_weight_offset, int64_t num_heads, int64_t num_kv_heads,
@@ -338,9 +341,17 @@ int doe_rope(float *qk, const float *freq_cis, int64_t seq_len, int64_t num_head
              doe_stream_t stream);
 /* out = gelu_tanh(gate) * up (clamped inner, gelu_gated.wgsl:1-14). */
 int doe_geglu(const float *gate, const float *up, float *output, int64_t n, doe_stream_t stream);
-/* out = input + residual (residual.wgsl; run_csl_webgpu_emulator.mjs:482-489). */
+/* out = input + residual (residual.wgsl; run_csl_webgpu_emulator.mjs:482-489);
+ * output may be input or residual (in place). */
 int doe_residual_add(const float *input, const float *residual, float *output, int64_t n,
                      doe_stream_t stream);
+/* Per-layer-embedding combine: out = (projected + gathered) * scale, one f32
+ * add then one f32 multiply per element -- the `ple_modulate` step
+ * (emit_csl_exec_v1.zig:167-172: the element_wise part of the PLE composite,
+ * kernelKey ple_residual) that joins the projected, normalised per-layer
+ * inputs with the gathered per-layer embedding rows. */
+int doe_ple_modulate(const float *projected, const float *gathered, float *output, int64_t n,
+                     float scale, doe_stream_t stream);
 /* Greedy sample: token = argmax(logits), lowest index on ties (sample.wgsl:
  * 17-55, run_csl_webgpu_emulator.mjs:841-878).  workspace: >= 8192 device
  * bytes. */

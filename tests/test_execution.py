@@ -38,17 +38,164 @@ def test_both_forms_of_the_270m_graph_plan_alike():
 
 
 def test_graphs_this_library_does_not_execute_are_refused_by_step():
-    with pytest.raises(ex.UnsupportedStep, match="numKvSharedLayers"):
-        ex.plan_decode(ex.load_step_graph(GOLD / "gemma-4-e2b-smoke.json"), 35)
     with pytest.raises(ex.UnsupportedStep, match="conv1d_depthwise"):
         ex.plan_decode(ex.load_step_graph(GOLD / "qwen-3-6-27b-smoke.json"), 64)
+    # per-layer embedding steps out of their order
     e2b = graph_json("gemma-4-e2b-smoke.json")
-    with pytest.raises(ex.UnsupportedStep, match="globalHeadDim"):
-        DecoderConfig.from_model_config(e2b["modelConfig"])
-    # without the shared-KV layers the per-layer embedding steps are what stops it
-    e2b.pop("numKvSharedLayers")
+    dec = [s for s in e2b["steps"] if s["phase"] == "decode"]
+    dec[0], dec[1] = dec[1], dec[0]
+    e2b["steps"] = [s for s in e2b["steps"] if s["phase"] == "prefill"] + dec
     with pytest.raises(ex.UnsupportedStep, match="ple_"):
         ex.plan_decode(ex.load_step_graph(e2b), 35)
+
+
+def test_gemma4_e2b_graph_plans_per_layer():
+    # gemma-4-e2b-smoke.json: 35 layers, layerPattern every 5 offset 4 (global
+    # layers 4, 9, ..., 34 at globalHeadDim 512, the others sliding over 512
+    # keys at headDim 256), the last 20 layers (15..34) sharing KV: a sliding
+    # one reads the cache of layer 13 (the last sliding layer before 15), a
+    # global one that of layer 14.
+    g = ex.load_step_graph(GOLD / "gemma-4-e2b-smoke.json")
+    mc = g.model_config
+    plan = ex.plan_decode(g, mc["numLayers"], mc["headDim"], mc["globalHeadDim"])
+    glob = {4, 9, 14, 19, 24, 29, 34}
+    assert plan.windows == tuple(0 if i in glob else 512 for i in range(35))
+    assert plan.head_dims == tuple(512 if i in glob else 256 for i in range(35))
+    assert plan.kv_sources == tuple(range(15)) + tuple(14 if i in glob else 13 for i in range(15, 35))
+    assert plan.ple.steps == ("ple_gather", "ple_project", "ple_norm", "ple_modulate")
+    assert [d.kind for d in plan.layer] == ["qkv_rope_kv", "attention", "attn_out", "gate_up", "down"]
+    # every decode step is carried out: the layer template, the PLE steps, the
+    # variant steps (kv_write_shared, attention_global) and the sample
+    covered = [n for d in plan.layer + plan.post + (plan.ple,) for n in d.steps]
+    names = [s.name for s in g.phase("decode")]
+    assert set(names) - set(covered) == {"kv_write_shared", "attention_global"}
+    c = DecoderConfig.from_model_config(mc)
+    assert (c.global_head_dim, c.ple_width, c.ple_vocab, c.ffn) == (512, 256, 262144, 6144)
+    # a shared-KV count that leaves a type without an owner is an error
+    e2b = graph_json("gemma-4-e2b-smoke.json")
+    e2b["numKvSharedLayers"] = 31  # layers 4..34 shared: no earlier global layer owns a cache
+    with pytest.raises(ex.StepGraphError, match="no earlier global layer"):
+        ex.plan_decode(ex.load_step_graph(e2b), 35, 256, 512)
+
+
+def test_golden_host_plans():
+    # the reference's lowering goldens (runtime/zig/examples/doe-wgsl-host-plan.
+    # *.json, checked at emit_csl_exec_v1_test.zig:352-447): launch lists with
+    # attention type, window, decode-position source and KV alias, kernels in
+    # order of first use with counts, EOS token.  The goldens name rmsnorm's
+    # pattern "reduction"; the op table and its own test
+    # (emit_csl_exec_v1_test.zig:8-17) map rmsnorm to "rms_norm", which is
+    # followed here.  The PE grid is a Cerebras placement and not derived.
+    for graph, golden in [("gemma-3-270m-smoke.json", "doe-wgsl-host-plan.gemma-3-270m-smoke.json"),
+                          ("gemma-3-270m-manifest-smoke.json", "doe-wgsl-host-plan.gemma-3-270m-manifest-smoke.json"),
+                          ("gemma-4-e2b-smoke.json", "doe-wgsl-host-plan.gemma-4-e2b-smoke.json")]:
+        got = ex.lower_host_plan(ex.load_step_graph(GOLD / graph))
+        want = graph_json("host_plan/" + golden)["hostPlan"]
+        assert got["phases"] == want["phases"], graph
+        assert got["eosTokenId"] == want["eosTokenId"]
+        assert [(k["name"], k["count"]) for k in got["kernels"]] == [(k["name"], k["count"]) for k in want["kernels"]]
+        for a, b in zip(got["kernels"], want["kernels"]):
+            assert a["pattern"] == b["pattern"] or (a["name"], a["pattern"], b["pattern"]) == (
+                "rmsnorm", "rms_norm", "reduction"), (graph, a, b)
+
+
+def test_reference_shared_kv_and_validation_cases():
+    # emit_csl_exec_v1_test.zig:268-299: shared KV launch metadata
+    g = ex.load_step_graph({"grid": {"width": 8, "height": 1}, "slidingWindowSize": 512, "numKvSharedLayers": 4,
+                            "steps": [
+                                {"phase": "prefill", "op": "embed", "kernelKey": "embed_gather"},
+                                {"phase": "decode", "op": "attention_sliding", "kernelKey": "attn_local",
+                                 "attentionType": "sliding"},
+                                {"phase": "decode", "op": "kv_write_shared", "kernelKey": "kv_shared",
+                                 "kvCacheAlias": "layer.0.kv"},
+                                {"phase": "decode", "op": "sample", "kernelKey": "sampler", "kind": "sample"}]})
+    plan = ex.lower_host_plan(g)
+    assert len(plan["kernels"]) == 4 and len(plan["phases"]["prefill"]) == 1
+    d = plan["phases"]["decode"]
+    assert len(d) == 3
+    assert (d[0]["attentionType"], d[0]["slidingWindowSize"], d[0]["currentPosSource"]) == (
+        "sliding", 512, "decode_position")
+    assert d[1]["currentPosSource"] == "decode_position" and d[1]["kvCacheAlias"] == "layer.0.kv"
+    # :301-320: kv_write_shared without numKvSharedLayers
+    with pytest.raises(ex.StepGraphError, match="numKvSharedLayers"):
+        ex.load_step_graph({"grid": {"width": 8, "height": 1}, "steps": [
+            {"phase": "prefill", "op": "embed", "kernelKey": "embed_gather"},
+            {"phase": "decode", "op": "kv_write_shared", "kernelKey": "kv_shared", "kvCacheAlias": "layer.0.kv"},
+            {"phase": "decode", "op": "sample", "kernelKey": "sampler", "kind": "sample"}]})
+    # :46-64, :82-110, :112-137: valid plans from steps, objects and tuples
+    g = ex.load_step_graph({"grid": {"width": 16, "height": 2}, "eosTokenId": 7, "steps": [
+        {"phase": "prefill", "op": "embed", "kernelKey": "embed_gather"},
+        {"phase": "prefill", "op": "rmsnorm", "kernelKey": "norm_0"},
+        {"phase": "decode", "op": "attention", "kernelKey": "attn_0"},
+        {"phase": "decode", "op": "sample", "kernelKey": "sampler", "kind": "sample"}]})
+    plan = ex.lower_host_plan(g)
+    assert (len(plan["kernels"]), len(plan["phases"]["prefill"]), len(plan["phases"]["decode"]),
+            plan["eosTokenId"]) == (4, 2, 2, 7)
+    g = ex.load_step_graph({"grid": {"width": 8, "height": 1}, "steps": [
+        ["prefill", "embed", "embed_gather"], ["decode", "attention", "attn_0"],
+        ["decode", "sample", "sampler", None, "sample"]]})
+    plan = ex.lower_host_plan(g)
+    assert (len(plan["phases"]["prefill"]), len(plan["phases"]["decode"]), plan["eosTokenId"]) == (1, 2, None)
+    # :197-229: layerPattern routing; both decode attention launches carry the
+    # sliding/global type, the sliding one and kv_write read the decode position
+    g = ex.load_step_graph({"grid": {"width": 8, "height": 1}, "slidingWindowSize": 512,
+                            "layerPattern": {"type": "every_n", "period": 2, "offset": 1}, "steps": [
+                                {"phase": "prefill", "op": "embed", "kernelKey": "embed_gather"},
+                                {"phase": "decode", "op": "attention", "kernelKey": "attn_local"},
+                                {"phase": "decode", "op": "kv_write", "kernelKey": "kv_write"},
+                                {"phase": "decode", "op": "attention", "kernelKey": "attn_global"},
+                                {"phase": "decode", "op": "sample", "kernelKey": "sampler", "kind": "sample"}]})
+    d = ex.lower_host_plan(g)["phases"]["decode"]
+    assert len(d) == 4
+    assert (d[0]["attentionType"], d[0]["slidingWindowSize"], d[0]["currentPosSource"]) == (
+        "sliding", 512, "decode_position")
+    assert d[1]["currentPosSource"] == "decode_position"
+    assert d[2]["attentionType"] == "global" and "slidingWindowSize" not in d[2]
+
+
+def test_step_validation_rules():
+    # emit_csl_exec_v1.zig:527-559 (validateStep), 335-389 (parseStepObject)
+    base = [{"phase": "prefill", "op": "embed", "kernelKey": "e"}]
+    tail = [{"phase": "decode", "op": "sample", "kernelKey": "s"}]
+
+    def graph(*decode, **root):
+        return {**root, "steps": base + list(decode) + tail}
+
+    cases = [
+        ({"phase": "decode", "op": "kv_write", "kernelKey": "k", "kvCacheAlias": "layer.0.kv"}, "kvCacheAlias"),
+        ({"phase": "decode", "op": "kv_write_shared", "kernelKey": "k"}, "kvCacheAlias"),
+        ({"phase": "decode", "op": "attention", "kernelKey": "a", "slidingWindowSize": 0}, "slidingWindowSize"),
+        ({"phase": "decode", "op": "rmsnorm", "kernelKey": "n", "slidingWindowSize": 64}, "slidingWindowSize"),
+        ({"phase": "decode", "op": "rmsnorm", "kernelKey": "n", "attentionType": "global"}, "attentionType"),
+        ({"phase": "decode", "op": "attention_sliding", "kernelKey": "a", "attentionType": "global"},
+         "attentionType"),
+        ({"phase": "decode", "op": "rmsnorm", "kernelKey": "n", "repeat": 0}, "repeat"),
+        ({"phase": "decode", "op": "gelu_gated", "kernelKey": "g"}, "inputsFrom"),
+        ({"phase": "decode", "op": "gelu_gated", "kernelKey": "g", "inputsFrom": ["gate_proj"]}, "inputsFrom"),
+    ]
+    for step, msg in cases:
+        with pytest.raises(ex.StepGraphError, match=msg):
+            ex.load_step_graph(graph(step, numKvSharedLayers=4))
+    with pytest.raises(ex.StepGraphError, match="weightsKey"):  # a sample step with weights
+        ex.load_step_graph({"steps": base + [{"phase": "decode", "op": "sample", "kernelKey": "s",
+                                               "weightsKey": "lm_head"}]})
+    ok = ex.load_step_graph(graph({"phase": "decode", "op": "gelu_gated", "kernelKey": "g",
+                                   "inputsFrom": ["gate_proj", "up_proj"], "repeat": 3}))
+    assert ok.phase("decode")[0].repeat == 3 and ok.phase("decode")[0].inputs_from == ("gate_proj", "up_proj")
+    # ordering (emit_csl_exec_v1.zig:683-706, 786-787)
+    with pytest.raises(ex.StepGraphError, match="after a decode step"):
+        ex.load_step_graph({"steps": base + tail + [{"phase": "prefill", "op": "rmsnorm", "kernelKey": "n"}]})
+    with pytest.raises(ex.StepGraphError, match="sample step"):
+        ex.load_step_graph({"steps": base + [{"phase": "decode", "op": "rmsnorm", "kernelKey": "n"}] + tail +
+                            [{"phase": "decode", "op": "rmsnorm", "kernelKey": "n"}]})
+    with pytest.raises(ex.StepGraphError, match="computes nothing"):
+        ex.load_step_graph({"steps": base + tail})
+    # the lm_head matmul lowers as dense_gemv, the 31B prefill GEMV as prefill_q4k_gemv
+    g = ex.load_step_graph({"steps": [
+        {"phase": "prefill", "op": "matmul", "kernelKey": "tiled_31b"},
+        {"phase": "decode", "op": "matmul", "kernelKey": "lm_head_f16", "name": "lm_head"},
+        {"phase": "decode", "op": "sample", "kernelKey": "s"}]})
+    assert [k["pattern"] for k in ex.lower_host_plan(g)["kernels"]] == ["prefill_q4k_gemv", "dense_gemv", "sample"]
 
 
 def test_layer_pattern_windows_follow_the_reference_rule():
@@ -126,6 +273,9 @@ def test_model_config_maps_to_decoder_config():
     for bad in ("q6k", "f16"):
         with pytest.raises(ex.UnsupportedStep, match="quantFormat"):
             DecoderConfig.from_model_config({**mc, "quantFormat": bad})
+    # Gemma 4 fields: a global-layer head_dim and per-layer embeddings
+    g4 = DecoderConfig.from_model_config({**mc, "globalHeadDim": 512, "pleWidth": 256, "pleVocabSize": 1000})
+    assert (g4.global_head_dim, g4.ple_width, g4.ple_vocab) == (512, 256, 1000)
 
 
 def test_reference_lowering_known_answers():

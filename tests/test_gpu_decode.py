@@ -313,3 +313,59 @@ def test_attention_softcap_in_the_decode_loop(dev, ora):
             d.step(s)
     s.synchronize()
     assert rel_l2(dec.logits.download(), plain.logits.download()) > 1e-3
+
+
+def _e2b_small():
+    """The reference's gemma-4-e2b-smoke.json graph (per-layer embeddings,
+    sliding layers at headDim and global layers every 5th at globalHeadDim
+    512, shared-KV layers, kv_write_shared / attention_global variants) at
+    small shapes: 10 layers (global: 4, 9), the last 4 sharing KV (6, 7, 8
+    read layer 5's cache, 9 reads layer 4's), an 8-key window, hidden 512,
+    4 query heads on 1 KV head of 256 (512 in global layers), PLE width 256."""
+    from doe_amd import execution as ex
+
+    g = json.loads((Path(__file__).parent / "golden" / "execution_v1" / "gemma-4-e2b-smoke.json").read_text())
+    g["slidingWindowSize"] = 8
+    g["numKvSharedLayers"] = 4
+    mc = {**g["modelConfig"], "numLayers": 10, "hiddenDim": 512, "numHeads": 4, "vocabSize": 4096,
+          "pleVocabSize": 4096}
+    g["modelConfig"] = mc
+    graph = ex.load_step_graph(g)
+    cfg = DecoderConfig.from_model_config(mc, max_seq=64, norm_weight_offset=False, rope_base_global=1e6)
+    plan = ex.plan_decode(graph, cfg.layers, cfg.head_dim, cfg.global_head_dim)
+    assert plan.windows == (8, 8, 8, 8, 0, 8, 8, 8, 8, 0)
+    assert plan.head_dims == (256,) * 4 + (512,) + (256,) * 4 + (512,)
+    assert plan.kv_sources == (0, 1, 2, 3, 4, 5, 5, 5, 5, 4)
+    return cfg, plan
+
+
+def test_gemma4_e2b_graph_decodes_against_oracle(dev, ora):
+    # Teacher-forced past the sliding window against the oracle decoder (the
+    # same per-layer plan composed from the oracle's kernels): logits within
+    # 1e-3, tokens equal.
+    cfg, plan = _e2b_small()
+    dec = Decoder(cfg, keep_logits=True, plan=plan)
+    dec.init_random(seed=12)
+    s = Stream()
+    oracle = OracleDecoder(dec)
+    prompt = np.array([7, 4000, 123, 123, 2048], np.int32)
+    ids, errs = run_teacher_forced(dec, oracle, prompt, 12, s)
+    print(f"[decode e2b] max logits rel_l2 {max(errs):.2e}", flush=True)
+    assert max(errs) <= 1e-3
+    assert dec.ids.download()[: len(ids)].tolist() == ids
+
+
+def test_gemma4_e2b_graph_replay_equals_eager(dev):
+    cfg, plan = _e2b_small()
+    dec = Decoder(cfg, plan=plan)
+    dec.init_random(seed=13)
+    s = Stream()
+    prompt = np.arange(1, 6, dtype=np.int32) * 61
+    eager = dec.generate(prompt, 14, s)
+    dec.reset(prompt)
+    dec.step(s)
+    s.synchronize()
+    g = dec.capture(s, 2)
+    out = dec.generate(prompt, 14, s, graph=g, steps_per_graph=2)
+    g.destroy()
+    assert out.tolist() == eager.tolist()
