@@ -752,12 +752,208 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
     }
 }
 
+// Streaming form of the matrix-core kernel, for GEMVs of more 16-row groups
+// than one resident round: a persistent workgroup of one wave per Q4_K block
+// (nb <= 16) walks row groups blockIdx.x, + gridDim.x, ...  A wave's block,
+// and so its activation image, is the same in every group: it is staged once.
+// Two groups' weight loads stay in flight (the next one's and the one after,
+// issued as soon as a group's bytes are regrouped into LDS), and the row sums
+// wait in LDS until the walk ends: the loop issues no global store, so no
+// write sits in the in-order vmcnt queue ahead of a weight load.  Per group:
+// regroup, 8 MFMAs, the scale formula, one barrier for the cross-wave sum.
+constexpr int kStreamMaxGroups = 32;  // row groups per workgroup (LDS row sums)
+constexpr int kStreamWaveLds = 16 * kMfmaRowBytes + kMfmaAImgDwords * 4;
+
+size_t gemv_stream_lds_bytes(int nwaves) {
+    return (size_t)nwaves * kStreamWaveLds + (size_t)(2 * 16 + 1) * nwaves * 4 + (size_t)kStreamMaxGroups * 16 * 4;
+}
+
+template <int PRO, int XV>
+__global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__restrict__ w, const float *x,
+                                                               float *__restrict__ y, int n, int k, int nb,
+                                                               int ngroups, GemvFusion fz) {
+    constexpr bool NORM = PRO == 1;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    uint8_t *wimg = lds + wave * kStreamWaveLds;
+    uint32_t *aimg = reinterpret_cast<uint32_t *>(wimg + 16 * kMfmaRowBytes);
+    float *red = reinterpret_cast<float *>(lds + nwaves * kStreamWaveLds);  // [2][16][nwaves]
+    float *ssq = red + 2 * 16 * nwaves;                                      // [nwaves]
+    float *rsum = ssq + nwaves;                                              // [kStreamMaxGroups][16]
+    const int b = wave, G = gridDim.x;
+
+    // Activation (and norm weight) loads first.
+    float v[4], nwv[4];
+    const int e = b * 256 + lane * 4;
+    if (XV) {
+        const float4 f = *reinterpret_cast<const float4 *>(x + min(e, k - 4));  // masked below
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = x[min(e + j, k - 1)];
+    }
+    if (NORM && XV) {
+        const float4 f = *reinterpret_cast<const float4 *>(fz.norm_w + min(e, k - 4));
+        nwv[0] = f.x; nwv[1] = f.y; nwv[2] = f.z; nwv[3] = f.w;
+    } else if (NORM) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) nwv[j] = fz.norm_w[min(e + j, k - 1)];
+    }
+    __asm__ volatile("" ::: "memory");  // keep the activation loads ahead of the weights
+    const size_t rowbytes = (size_t)nb * DOE_Q4K_BLOCK_BYTES;
+    // group gi's 16 rows of block b: granule q -> row q / 9, piece q % 9
+    auto load_group = [&](int gi, u32x4 (&dst)[3]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            const int q = min(lane + 64 * s, 143);
+            const int r = min(gi * 16 + q / 9, n - 1);
+            dst[s] = load_stream16(w + (size_t)r * rowbytes + (size_t)b * DOE_Q4K_BLOCK_BYTES + (q % 9) * 16);
+        }
+    };
+    u32x4 wa[3], wb[3];
+    int gi = blockIdx.x;  // the grid never exceeds the group count
+    load_group(gi, wa);
+    if (gi + G < ngroups) load_group(gi + G, wb);
+    __builtin_amdgcn_sched_barrier(0);
+
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (e + j >= k) v[j] = 0.0f;
+        if (NORM) {
+            ss = fmaf(v[j], v[j], ss);
+            v[j] *= fz.norm_offset ? 1.0f + nwv[j] : nwv[j];
+        }
+    }
+    if (NORM) {
+        ss = sum_rows4(sum16(ss));
+        if (lane == 0) ssq[wave] = ss;
+    }
+    // The block's activation image, staged once (as the one-shot kernel's
+    // stage(): lane 16 g + i holds chunk g, quad i).
+    const int g = lane >> 4, i16 = lane & 15, m = lane & 15;
+    const int nchunk = (k + 63) >> 6;
+    float sxl, sxh;
+    int sgm = 0;
+    {
+        const float ssum = sum8((v[0] + v[1]) + (v[2] + v[3]));
+        const float sother = dpp<kDppMirror>(ssum);
+        sxl = i16 < 8 ? ssum : sother;
+        sxh = i16 < 8 ? sother : ssum;
+        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        amax = fmaxf(amax, dpp<kDppXor1>(amax));
+        amax = fmaxf(amax, dpp<kDppXor2>(amax));
+        amax = fmaxf(amax, dpp<kDppHalfMirror>(amax));
+        amax = fmaxf(amax, dpp<kDppMirror>(amax));
+        if (amax > 0.0f && amax <= 3.0e38f) {
+            sgm = 14 - __builtin_amdgcn_frexp_expf(amax);
+            sgm = sgm < -100 ? -100 : (sgm > 100 ? 100 : sgm);
+        }
+        const float xs = __builtin_amdgcn_ldexpf(1.0f, sgm);
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float t = v[j] * xs;
+            hi[j] = (_Float16)t;
+            lo[j] = (_Float16)(t - (float)hi[j]);
+        }
+        const int s = i16 >> 3, jj = i16 & 7;
+        const uint32_t h0 = pack_half2(hi[0], hi[2]), h1 = pack_half2(hi[1], hi[3]);
+        const uint32_t l0 = pack_half2(lo[0], lo[2]), l1 = pack_half2(lo[1], lo[3]);
+        uint32_t *dst = aimg + jj * kMfmaAStep + g * 16 + s * 4;
+        *reinterpret_cast<u32x4 *>(dst) = s ? u32x4{0, 0, h0, h1} : u32x4{h0, h1, 0, 0};
+        *reinterpret_cast<u32x4 *>(dst + 8) = s ? u32x4{0, 0, l0, l1} : u32x4{l0, l1, 0, 0};
+        if (lane < 8) *reinterpret_cast<u32x4 *>(aimg + lane * kMfmaAStep + 64) = u32x4{0, 0, 0, 0};
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int c = 4 * b + g;
+    const bool act = (m >> 2) == g && c < nchunk;
+    const int abase = act ? g * 16 + (m & 1) * 8 + ((m >> 1) & 1) * 4 : 64;
+    const float lo_scale = __builtin_amdgcn_ldexpf(1.0f, 24 - sgm), hi_scale = __builtin_amdgcn_ldexpf(1.0f, 20 - sgm);
+
+    int j = 0;
+    for (; gi < ngroups; gi += G, ++j) {
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            const int q = lane + 64 * s;
+            if (q < 144) *reinterpret_cast<u32x4 *>(wimg + (q / 9) * kMfmaRowBytes + (q % 9) * 16) = wa[s];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (gi + 2 * G < ngroups) load_group(gi + 2 * G, wa);  // wa's bytes are in LDS now
+        u32x4 areg[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) areg[jj] = *reinterpret_cast<const u32x4 *>(aimg + jj * kMfmaAStep + abase);
+        const uint8_t *rp = wimg + i16 * kMfmaRowBytes;
+        const u32x4 hdr = *reinterpret_cast<const u32x4 *>(rp);
+        const u32x4 qa = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
+        const u32x4 qb = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
+        f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const uint32_t dw = jj < 4 ? qa[jj] : qb[jj - 4], ew = dw >> 8;
+            const u32x4 bw = {dw & 0x000f000fu, ew & 0x000f000fu, dw & 0x00f000f0u, ew & 0x00f000f0u};
+            acc[jj & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, areg[jj]),
+                                                                 __builtin_bit_cast(half8, bw), acc[jj & 1], 0, 0, 0);
+        }
+        const f32x4 dsum = acc[0] + acc[1];
+        float part = 0.0f;
+        if (c < nchunk) {
+            uint32_t scp, mnp;
+            q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
+            const float d = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
+            const float qx_lo = (dsum[0] + dsum[1]) * lo_scale;
+            const float qx_hi = (dsum[2] + dsum[3]) * hi_scale;
+            const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
+            const float m_lo = (float)(mnp & 0xffu), m_hi = (float)(mnp >> 8);
+            part = d * (sc_lo * qx_lo + sc_hi * qx_hi) - dmin * (m_lo * sxl + m_hi * sxh);
+        }
+        __builtin_amdgcn_wave_barrier();
+        part = sum_rows4(part);
+        float *rd = red + (j & 1) * 16 * nwaves;
+        if (lane < 16) rd[lane * nwaves + wave] = part;
+        __syncthreads();
+        if (tid < 16) {
+            float sm = 0.0f;
+            for (int ww = 0; ww < nwaves; ++ww) sm += rd[tid * nwaves + ww];
+            rsum[j * 16 + tid] = sm;
+        }
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            const u32x4 t = wa[s];
+            wa[s] = wb[s];
+            wb[s] = t;
+        }
+    }
+    __syncthreads();
+    float inv = 1.0f;
+    if (NORM) {
+        float tot = 0.0f;
+        for (int ww = 0; ww < nwaves; ++ww) tot += ssq[ww];
+        inv = 1.0f / sqrtf(tot / (float)k + fz.norm_eps);
+    }
+    for (int t = tid; t < j * 16; t += blockDim.x) {
+        const int r16 = t & 15;
+        const int row = ((int)blockIdx.x + (t >> 4) * G) * 16 + r16;
+        const float sv = NORM ? rsum[t] * inv : rsum[t];
+        if (fz.gated) {
+            const float other = NORM ? rsum[t ^ 1] * inv : rsum[t ^ 1];
+            if ((r16 & 1) == 0 && row < n) y[row >> 1] = doe_gelu_tanh_clamped(sv) * other;
+        } else if (fz.rope_kv) {
+            const float other = NORM ? rsum[t ^ 1] * inv : rsum[t ^ 1];
+            if ((r16 & 1) == 0 && row < n) rope_kv_pair(fz, row, sv, other, y);
+        } else if (row < n) {
+            y[row] = fz.residual ? sv + fz.residual[row] : sv;
+        }
+    }
+}
+
 // Tunable launch-shape overrides (0 = automatic), set via doe_tune_set.
 int g_tune_rowslots = 0;
 int g_tune_rows = 0;
 int g_tune_kernel = 0;  // 0 automatic, 1 dot-product kernel, 2 matrix-core kernel
 int g_tune_ksplit = 0;  // 0 automatic, 1 never split K over workgroups
 int g_tune_bpw = 0;     // 0 automatic, else at least this many blocks per wave (<= 4)
+int g_tune_stream = 0;  // 0 automatic, -1 never stream, g > 0: stream g row groups per workgroup
 
 // Launch shape for the GEMV: rowslots * nchunk threads (rounded up to whole
 // waves) and R rows per thread.  The automatic choice spreads the rows over
@@ -901,6 +1097,58 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     const bool mfma_ok = nbs <= kMfmaMaxBlocks && (bpw == 1 || !fz.attn_o);
     const bool dot_ok = gemv_lds_bytes(nchunk, 8) <= 64 * 1024;
     const bool use_mfma = g_tune_kernel == 1 ? !dot_ok && mfma_ok : mfma_ok;
+    // Streaming kernel (opt-in, q4k_gemv.stream = groups per workgroup): one
+    // wave per block, whole rows, no attention prologue.  Measured slower
+    // than the one-shot kernel on every shape tried (9216, 18432 and 65536
+    // rows of 2304; 4096 and 2304 rows): 96 VGPRs leave two workgroups per
+    // CU, and the per-group barrier chain bounds a workgroup to about two
+    // groups in flight.
+    if (use_mfma && bpw == 1 && ksplit == 1 && !fz.attn_o && g_tune_stream > 0) {
+        const int nwaves = nb;
+        const size_t lds = gemv_stream_lds_bytes(nwaves);
+        const bool xv = ((uintptr_t)activation & 15) == 0 && (k & 3) == 0 && ((uintptr_t)fz.norm_w & 15) == 0;
+        const void *fn = fz.norm_w ? (xv ? (const void *)q4k_gemv_stream_kernel<1, 1> : (const void *)q4k_gemv_stream_kernel<1, 0>)
+                                   : (xv ? (const void *)q4k_gemv_stream_kernel<0, 1> : (const void *)q4k_gemv_stream_kernel<0, 0>);
+        static const hipError_t attr_all = [] {
+            hipError_t e = hipSuccess;
+            for (const void *f : {(const void *)q4k_gemv_stream_kernel<0, 0>, (const void *)q4k_gemv_stream_kernel<0, 1>,
+                                  (const void *)q4k_gemv_stream_kernel<1, 0>, (const void *)q4k_gemv_stream_kernel<1, 1>})
+                if (e == hipSuccess)
+                    e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemv_stream_lds_bytes(16));
+            return e;
+        }();
+        DOE_HIP_CHECK(attr_all);
+        // stream when the one-shot kernel needs more than one round of
+        // resident workgroups, with as few groups per workgroup as the
+        // streaming kernel's own residency allows
+        int per_cu = 0, per_cu_once = 0;
+        DOE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * nwaves, lds));
+        const void *once = fz.norm_w ? (const void *)q4k_gemv_mfma_kernel<1, 1, 1> : (const void *)q4k_gemv_mfma_kernel<0, 1, 1>;
+        DOE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_once, once, 64 * nwaves,
+                                                                   gemv_mfma_lds_bytes(nwaves, 1)));
+        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * g_num_cus;
+        const int64_t resident_once = (int64_t)(per_cu_once > 0 ? per_cu_once : 1) * g_num_cus;
+        (void)resident_once;
+        int64_t per_wg = g_tune_stream > 0 ? g_tune_stream
+                                           : (row_groups > resident_once ? (row_groups + resident - 1) / resident : 0);
+        if (per_wg > kStreamMaxGroups) per_wg = 0;  // too many groups per workgroup for the LDS row sums
+        if (per_wg > 0) {
+            const int64_t grid = (row_groups + per_wg - 1) / per_wg;
+#define DOE_GEMV_STREAM_LAUNCH(P, X)                                                                   \
+    do {                                                                                               \
+        hipLaunchKernelGGL((q4k_gemv_stream_kernel<P, X>), dim3((unsigned)grid), dim3(64 * nwaves), lds, st, wp, \
+                           activation, output, (int)n, (int)k, nb, (int)row_groups, fz);               \
+    } while (0)
+            if (fz.norm_w) {
+                if (xv) DOE_GEMV_STREAM_LAUNCH(1, 1); else DOE_GEMV_STREAM_LAUNCH(1, 0);
+            } else {
+                if (xv) DOE_GEMV_STREAM_LAUNCH(0, 1); else DOE_GEMV_STREAM_LAUNCH(0, 0);
+            }
+#undef DOE_GEMV_STREAM_LAUNCH
+            DOE_LAUNCH_CHECK("q4k_gemv_stream_kernel");
+            return DOE_OK;
+        }
+    }
     if (use_mfma) {
         const int nwaves = (nbs + bpw - 1) / bpw;
         const size_t lds = gemv_mfma_lds_bytes(nwaves, bpw);
@@ -1059,6 +1307,10 @@ int doe_tune_set(const char *key, int value) {
     } else if (!strcmp(key, "q4k_gemv.bpw")) {
         DOE_REQUIRE(value >= 0 && value <= 4, DOE_E_INVALID, "q4k_gemv.bpw is 0..4");
         g_tune_bpw = value;
+    } else if (!strcmp(key, "q4k_gemv.stream")) {
+        DOE_REQUIRE(value >= -1 && value <= kStreamMaxGroups, DOE_E_INVALID, "q4k_gemv.stream is -1..%d",
+                    kStreamMaxGroups);
+        g_tune_stream = value;
     } else if (!strcmp(key, "q4k_gemv.ksplit")) {
         DOE_REQUIRE(value == 0 || value == 1, DOE_E_INVALID, "q4k_gemv.ksplit is 0 or 1");
         g_tune_ksplit = value;

@@ -419,7 +419,8 @@ int doe_decode_advance(int32_t *state, int32_t *token, int32_t *ids, int64_t max
 
 /* ---- tuning ----------------------------------------------------------------
  * Overrides a kernel launch-shape choice (0 restores the automatic choice).
- * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows", "q8_0_gemv.rows" (1, 2 or 4
+ * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows", "q4k_gemv.stream" (v > 0: the
+ * streaming GEMV walking v row groups per workgroup), "q8_0_gemv.rows" (1, 2 or 4
  * rows per wave group), "q8_0_gemv.depth" (1 or 2 blocks loaded ahead),
  * "attn_decode.splits",
  * "attn_decode.waves" (4: narrow workgroups; 8 or 16: the wide short-context

@@ -230,3 +230,72 @@ def test_gemv_large_k_splits(dev, ora, k):
     s.destroy()
     with pytest.raises(DoeError, match="plain and residual"):
         ops.matmul_q4k_fused(dw, dx, out, n, k, norm_weight=DeviceBuffer.from_array(np.ones(k, np.float32)))
+
+
+@pytest.fixture
+def stream_groups(request, dev):
+    """Forces the streaming GEMV kernel to walk `param` row groups per
+    workgroup (q4k_gemv.stream) and restores the automatic choice."""
+    ops.tune("q4k_gemv.stream", request.param)
+    yield request.param
+    ops.tune("q4k_gemv.stream", 0)
+
+
+@pytest.mark.parametrize("stream_groups", [1, 2, 3, 7, 32], indirect=True)
+@pytest.mark.parametrize("n,k", [(9216, 2304), (1000, 2304), (77, 300), (4096, 4096), (18432, 2304), (33, 256)])
+def test_gemv_streaming_kernel(dev, ora, n, k, stream_groups):
+    # the persistent streaming form: each workgroup walks `stream_groups` row
+    # groups (the last one partial where n % 16 != 0), one wave per block
+    print(f"[gemv stream {stream_groups}] {n}x{k}", flush=True)
+    rng = np.random.default_rng(n + k + stream_groups)
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    err = rel_l2(_gemv(w, x, n, k), ora.q4k_gemv(w, x, n, k))
+    assert err < 1e-5, err
+
+
+@pytest.mark.parametrize("stream_groups", [2, 5], indirect=True)
+def test_gemv_streaming_fused_forms(dev, ora, stream_groups):
+    # RMSNorm prologue, residual epilogue, gated epilogue and the RoPE + KV
+    # cache epilogue through the streaming kernel
+    rng = np.random.default_rng(40 + stream_groups)
+    up = DeviceBuffer.from_array
+    k = 2304
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    nw = (0.1 * rng.standard_normal(k)).astype(np.float32)
+    xn = ora.rmsnorm(x, nw, 1e-6, True)
+    n = 3000
+    w = q4k.random_q4k(rng, n, k)
+    out = DeviceBuffer.empty((n,), np.float32)
+    ops.matmul_q4k_fused(up(w), up(x), out, n, k, norm_weight=up(nw), norm_eps=1e-6, norm_weight_offset=True)
+    assert rel_l2(out.download(), ora.q4k_gemv(w, xn, n, k)) < 1e-5
+    res = rng.standard_normal(n).astype(np.float32)
+    out2 = DeviceBuffer.empty((n,), np.float32)
+    ops.matmul_q4k_fused(up(w), up(x), out2, n, k, residual=up(res))
+    assert rel_l2(out2.download(), ora.residual(ora.q4k_gemv(w, x, n, k), res)) < 1e-5
+    wg = q4k.random_q4k(rng, 2 * 1500, k)
+    out3 = DeviceBuffer.empty((1500,), np.float32)
+    ops.matmul_q4k_fused(up(wg), up(x), out3, 3000, k, norm_weight=up(nw), norm_eps=1e-6, gated=True)
+    y = ora.q4k_gemv(wg, xn, 3000, k)
+    assert rel_l2(out3.download(), ora.geglu(y[0::2], y[1::2])) < 1e-5
+    # RoPE + cache write: 8 q / 4 kv heads of 256 at position 5
+    hq, hkv, d, maxs, pos = 8, 4, 256, 16, 5
+    qd, kd = hq * d, hkv * d
+    nq = qd + 2 * kd
+    w_plain = q4k.random_q4k(rng, nq, k).reshape(nq, -1)
+    w_dev = w_plain.copy()
+    w_dev[: qd + kd] = ops.interleave_rope_rows(w_plain[: qd + kd], d)
+    table = ora.rope_table(maxs, d, 10000.0)
+    kc = up(np.zeros((hkv, maxs, d), np.float16))
+    vc = up(np.zeros((hkv, maxs, d), np.float16))
+    out4 = DeviceBuffer.empty((nq,), np.float32)
+    ops.qkv_rope_kv(up(w_dev), up(x), out4, hidden=k, num_heads=hq, num_kv_heads=hkv, head_dim=d,
+                    freq_cis=up(table), position_buffer=up(np.array([pos], np.int32)), key_cache=kc,
+                    val_cache=vc, max_seq_len=maxs, norm_weight=up(nw), norm_eps=1e-6, norm_weight_offset=True)
+    qkv = ora.q4k_gemv(w_plain, xn, nq, k)
+    qk = ora.rope(qkv[: qd + kd], table, 1, hq + hkv, d, pos)
+    want = np.concatenate([ops.interleave_rope_rows(qk, d), qkv[qd + kd:]])
+    assert rel_l2(out4.download(), want) < 1e-5
+    kg = kc.download()
+    assert rel_l2(kg[:, pos].astype(np.float32),
+                  ops.interleave_rope_rows(qk[qd:], d).reshape(hkv, d).astype(np.float32)) < 1e-3
