@@ -70,6 +70,7 @@ SIGNATURES: dict[str, list] = {
     "doe_int4g32_gemv": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "doe_q4k_gemv_attn_out": [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
     "doe_q4k_gemm": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "doe_q4k_gemm_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "doe_q4k_gemv": [_vp, _vp, _vp, _i64, _i64, _vp],
     "doe_q8_0_gemv": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
     "doe_q8_0_gemv_norm": [_vp, _vp, _vp, _i64, _i64, _vp, _f32, _i32, _vp, _vp],
@@ -77,6 +78,8 @@ SIGNATURES: dict[str, list] = {
     "doe_attn_prefill": [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp],
     "doe_attn_decode_partials": [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i32, _f32, _f32, _i64, _vp, _i64, _i64, C.POINTER(_i32), _vp],
     "doe_attention_dispatch": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp],
+    "doe_attn_prefill_f16kv": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64,
+                               _f32, _f32, _i64, _vp],
     "doe_attn_decode": [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i32,
                         _f32, _f32, _i64, _vp],
     "doe_attn_decode_noalloc": [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i32,
@@ -89,6 +92,8 @@ SIGNATURES: dict[str, list] = {
     "doe_geglu": [_vp, _vp, _vp, _i64, _vp],
     "doe_residual_add": [_vp, _vp, _vp, _i64, _vp],
     "doe_ple_modulate": [_vp, _vp, _vp, _i64, _f32, _vp],
+    "doe_qkv_rope_kv_rows": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
+    "doe_geglu_pairs": [_vp, _vp, _i64, _vp],
     "doe_argmax": [_vp, _i64, _vp, _vp, _vp],
     "doe_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _vp],
     "doe_embed_gather": [_vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp],

@@ -715,9 +715,6 @@ int doe_attention_dispatch(const doe_attention_uniforms *u, const float *q, cons
                            const uint32_t *page_table, int64_t page_table_len, int64_t kv_capacity,
                            doe_stream_t stream) {
     DOE_REQUIRE(u, DOE_E_INVALID, "null uniforms");
-    DOE_REQUIRE(u->query_len == 1, DOE_E_UNSUPPORTED,
-                "query_len %u: this dispatch is the decode form (query_len 1); prompts go to doe_attn_prefill",
-                u->query_len);
     DOE_REQUIRE(u->kv_layout <= 2, DOE_E_INVALID, "kv_layout %u (0 contiguous, 1 ring, 2 paged)", u->kv_layout);
     DOE_REQUIRE(kv_capacity > 0 && kv_capacity < (1 << 30), DOE_E_INVALID, "kv_capacity %lld",
                 (long long)kv_capacity);
@@ -738,6 +735,11 @@ int doe_attention_dispatch(const doe_attention_uniforms *u, const float *q, cons
         m.page_size = (int)u->page_size;
         m.page_table = page_table;
         m.page_table_len = page_table_len;
+    }
+    if (u->query_len != 1) {  // prompts: the multi-query kernel (attn_mq.hip)
+        DOE_REQUIRE(u->query_len < (1u << 30), DOE_E_INVALID, "query_len %u", u->query_len);
+        return doe::attention_dispatch_mq(u, q, k, v, output, kv_len_buffer, page_table, page_table_len, kv_capacity,
+                                          stream);
     }
     m.query_at_end = 0;
     m.start_pos = (int)u->start_pos;

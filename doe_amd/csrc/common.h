@@ -24,6 +24,10 @@ int require_init();
 // Fills bytes [dst, dst + bytes) with `value` on a stream with a kernel
 // (capturable into a HIP graph; no memset node).  Returns a DOE status.
 int fill_bytes_async(void *dst, int value, size_t bytes, hipStream_t st);
+// The query_len > 1 form of doe_attention_dispatch (attn_mq.hip).
+int attention_dispatch_mq(const doe_attention_uniforms *u, const float *q, const uint16_t *k, const uint16_t *v,
+                          float *output, const uint32_t *kv_len_buffer, const uint32_t *page_table,
+                          int64_t page_table_len, int64_t kv_capacity, doe_stream_t stream);
 // Looks up the allocation-free attention scratch of `device` (current).
 int attn_scratch_setup(int device);
 // Tuning hooks of individual kernels (0 = automatic).

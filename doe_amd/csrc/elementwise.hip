@@ -81,6 +81,54 @@ __global__ __launch_bounds__(256) void residual_kernel(const float *a, const flo
         out[i] = a[i] + b[i];
 }
 
+// Prompt rows of a fused [q; k; v] projection whose q and k rows are
+// interleaved rotation pairs (row 2i = dim i, 2i + 1 = dim i + D/2 of the
+// rotate-half form): token t (position start_pos + t) has its q/k pairs
+// rotated by freq_cis[pos][i] and its k and v rows stored as f16 into the
+// caches [kv_heads][max_seq][D] at pos -- the decode epilogue's arithmetic,
+// one thread per row pair.
+__global__ __launch_bounds__(256) void rope_kv_rows_kernel(float *qkv, long row_stride, int tokens, int q_rows,
+                                                           int kv_rows, int head_dim, const float *__restrict__ freq,
+                                                           int start_pos, _Float16 *kc, _Float16 *vc, int max_seq) {
+#pragma clang fp contract(off)
+    const int npairs = (q_rows + 2 * kv_rows) >> 1;
+    const long total = (long)tokens * npairs;
+    for (long gi = (long)blockIdx.x * 256 + threadIdx.x; gi < total; gi += (long)gridDim.x * 256) {
+        const int t = (int)(gi / npairs), row = 2 * (int)(gi % npairs);
+        const int pos = start_pos + t;
+        float *r = qkv + (size_t)t * row_stride;
+        const float s0 = r[row], s1 = r[row + 1];
+        float r0 = s0, r1 = s1;
+        const int dim = row % head_dim;
+        if (row < q_rows + kv_rows) {
+            const int i = dim >> 1, half = head_dim >> 1;
+            const float c = freq[((size_t)pos * half + i) * 2], sn = freq[((size_t)pos * half + i) * 2 + 1];
+            r0 = s0 * c - s1 * sn;
+            r1 = s0 * sn + s1 * c;
+            r[row] = r0;
+            r[row + 1] = r1;
+        }
+        if (row >= q_rows) {
+            const int kvr = row - q_rows;
+            const bool is_v = kvr >= kv_rows;
+            const int h = (is_v ? kvr - kv_rows : kvr) / head_dim;
+            _Float16 *cache = is_v ? vc : kc;
+            const size_t ci = ((size_t)h * max_seq + pos) * head_dim + dim;
+            cache[ci] = (_Float16)r0;
+            cache[ci + 1] = (_Float16)r1;
+        }
+    }
+}
+
+// GeGLU over interleaved (gate, up) columns: out[i] = gelu(gu[2i]) * gu[2i+1]
+__global__ __launch_bounds__(256) void geglu_pairs_kernel(const float2 *__restrict__ gu, float *__restrict__ out,
+                                                          long n) {
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        const float2 p = gu[i];
+        out[i] = doe_gelu_tanh_clamped(p.x) * p.y;
+    }
+}
+
 // (projected + gathered) * scale: one f32 add, then one f32 multiply (no fma)
 __global__ __launch_bounds__(256) void ple_modulate_kernel(const float *__restrict__ a,
                                                            const float *__restrict__ b,
@@ -232,6 +280,40 @@ int doe_residual_add(const float *input, const float *residual, float *output, i
     hipLaunchKernelGGL(residual_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream, input,
                        residual, output, (long)n);
     DOE_LAUNCH_CHECK("residual_kernel");
+    return DOE_OK;
+}
+
+int doe_qkv_rope_kv_rows(float *qkv, int64_t tokens, int64_t row_stride, int64_t num_heads, int64_t num_kv_heads,
+                         int64_t head_dim, const float *freq_cis, int64_t start_pos, uint16_t *key_cache,
+                         uint16_t *val_cache, int64_t max_seq_len, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(tokens >= 0 && num_heads > 0 && num_kv_heads >= 0 && head_dim > 0 && (head_dim % 2) == 0 &&
+                    start_pos >= 0 && max_seq_len > 0 && start_pos + tokens <= max_seq_len &&
+                    row_stride >= (num_heads + 2 * num_kv_heads) * head_dim && max_seq_len < (1 << 30),
+                DOE_E_INVALID, "bad prompt q/k/v shape (positions %lld..%lld in a %lld-row cache)",
+                (long long)start_pos, (long long)(start_pos + tokens - 1), (long long)max_seq_len);
+    if (tokens == 0) return DOE_OK;
+    DOE_REQUIRE(qkv && freq_cis && (num_kv_heads == 0 || (key_cache && val_cache)), DOE_E_INVALID, "null pointer");
+    const long total = (long)tokens * ((num_heads + 2 * num_kv_heads) * head_dim / 2);
+    hipLaunchKernelGGL(rope_kv_rows_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, qkv,
+                       (long)row_stride, (int)tokens, (int)(num_heads * head_dim), (int)(num_kv_heads * head_dim),
+                       (int)head_dim, freq_cis, (int)start_pos, (_Float16 *)key_cache, (_Float16 *)val_cache,
+                       (int)max_seq_len);
+    DOE_LAUNCH_CHECK("rope_kv_rows_kernel");
+    return DOE_OK;
+}
+
+int doe_geglu_pairs(const float *gate_up, float *output, int64_t n, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n >= 0, DOE_E_INVALID, "negative size");
+    if (n == 0) return DOE_OK;
+    DOE_REQUIRE(gate_up && output && ((uintptr_t)gate_up & 7) == 0, DOE_E_INVALID,
+                "null or misaligned pointer (gate_up 8-byte aligned)");
+    hipLaunchKernelGGL(geglu_pairs_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t)stream,
+                       (const float2 *)gate_up, output, (long)n);
+    DOE_LAUNCH_CHECK("geglu_pairs_kernel");
     return DOE_OK;
 }
 

@@ -124,6 +124,37 @@ __global__ __launch_bounds__(256) void a_rows_to_f16_kernel(const uint16_t *__re
     }
 }
 
+// The same pre-pass for f32 A: each row scaled by 2^sig[m] (max|A[m]| just
+// under 2^14) and rounded once to f16 (11 significant bits).
+__global__ __launch_bounds__(256) void a_rows_f32_to_f16_kernel(const float *__restrict__ a,
+                                                                _Float16 *__restrict__ a16,
+                                                                int *__restrict__ sig, int K, int Kp) {
+    const int m = blockIdx.x;
+    const float *row = a + (size_t)m * K;
+    _Float16 *out = a16 + (size_t)m * Kp;
+    float amax = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(row[k]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    __shared__ float wmax[4];
+    __shared__ int ssig;
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        int s = 0;
+        if (mx > 0.0f && mx <= 3.0e38f) {
+            s = 14 - __builtin_amdgcn_frexp_expf(mx);
+            s = s < -120 ? -120 : (s > 120 ? 120 : s);
+        }
+        ssig = s;
+        sig[m] = s;
+    }
+    __syncthreads();
+    const float scale = __builtin_amdgcn_ldexpf(1.0f, ssig);
+    for (int k = threadIdx.x; k < Kp; k += 256) out[k] = k < K ? (_Float16)(row[k] * scale) : (_Float16)0.0f;
+}
+
 // ---------------------------------------------------------------------------
 // GEMM.
 // ---------------------------------------------------------------------------
@@ -574,12 +605,9 @@ std::mutex g_ws_mu;
 void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
 
-}  // namespace
-
-extern "C" {
-
-int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m, int64_t n,
-                 int64_t k, doe_stream_t stream) {
+int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m, int64_t n, int64_t k,
+              doe_stream_t stream) {
+    const uint16_t *a_bf16 = a_f32 ? nullptr : (const uint16_t *)a;
     int rc = doe::require_init();
     if (rc) return rc;
     DOE_REQUIRE(m >= 0 && n >= 0 && k >= 0, DOE_E_INVALID, "negative shape");
@@ -590,7 +618,7 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
         // empty reduction: the sum identity
         return doe::fill_bytes_async(c, 0, (size_t)m * (size_t)n * sizeof(float), st);
     }
-    DOE_REQUIRE(a_bf16 && b_q4k, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(a && b_q4k, DOE_E_INVALID, "null pointer");
     DOE_REQUIRE(((uintptr_t)b_q4k & 15) == 0, DOE_E_INVALID, "weight must be 16-byte aligned");
     DOE_REQUIRE(m <= (1 << 24) && n <= (1 << 24) && k <= (1 << 20) && m * n <= ((int64_t)1 << 40),
                 DOE_E_UNSUPPORTED, "q4k_gemm shape too large (m=%lld n=%lld k=%lld)", (long long)m,
@@ -619,7 +647,12 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
     }
     _Float16 *a16 = (_Float16 *)ws;
     int *sig = (int *)((char *)ws + a16_bytes);
-    hipLaunchKernelGGL(a_rows_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, a_bf16, a16, sig, (int)k, (int)kp);
+    if (a_f32)
+        hipLaunchKernelGGL(a_rows_f32_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, (const float *)a, a16, sig,
+                           (int)k, (int)kp);
+    else
+        hipLaunchKernelGGL(a_rows_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, a_bf16, a16, sig, (int)k,
+                           (int)kp);
     DOE_LAUNCH_CHECK("a_rows_to_f16_kernel");
     GemmArgs g;
     g.a16 = a16;
@@ -642,6 +675,20 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
         hipLaunchKernelGGL((q4k_gemm_kernel<2, 2>), dim3((unsigned)tiles), dim3(256), 0, st, g);
     DOE_LAUNCH_CHECK("q4k_gemm_kernel");
     return DOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m, int64_t n,
+                 int64_t k, doe_stream_t stream) {
+    return gemm_impl(a_bf16, false, b_q4k, c, m, n, k, stream);
+}
+
+int doe_q4k_gemm_f32(const float *a, const void *b_q4k, float *c, int64_t m, int64_t n, int64_t k,
+                     doe_stream_t stream) {
+    return gemm_impl(a, true, b_q4k, c, m, n, k, stream);
 }
 
 }  // extern "C"

@@ -401,6 +401,78 @@ class Decoder:
         ops.gelu_gated(self.gate_view, self.up_view, self.h, c.ffn, stream=stream)
         ops.matmul_q8_0(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)
 
+    # ---- prompt ----------------------------------------------------------------
+    def can_prefill(self) -> bool:
+        """Batched prompts run for uniform Q4_K models (no per-layer
+        embeddings, shared-KV layers or second head_dim)."""
+        return (self.cfg.weight_format == "q4k" and not self.ple and len(set(self.head_dims)) == 1
+                and self.kv_sources == tuple(range(self.cfg.layers)))
+
+    def _prefill_buffers(self):
+        if getattr(self, "_pf", None) is None:
+            c, S = self.cfg, self.cfg.max_seq
+            self._pf = {
+                "x": DeviceBuffer.empty((S, c.hidden), np.float32),
+                "xn": DeviceBuffer.empty((S, c.hidden), np.float32),
+                "t": DeviceBuffer.empty((S, c.hidden), np.float32),
+                "qkv": DeviceBuffer.empty((S, c.qkv_rows), np.float32),
+                "att": DeviceBuffer.empty((S, c.q_dim), np.float32),
+                "gu": DeviceBuffer.empty((S, 2 * c.ffn), np.float32),
+                "h": DeviceBuffer.empty((S, c.ffn), np.float32),
+            }
+        return self._pf
+
+    def prefill(self, prompt: np.ndarray, stream=None) -> None:
+        """The prompt in one batched pass -- the step graph's prefill phase
+        (gemma-3-270m-smoke.json prefill steps: embed, then per layer
+        input_norm, q/k/v_proj as one M-row GEMM, rope_q / rope_k with the
+        cache write, causal attention of the whole prompt, o_proj +
+        attn_residual, post_attn_norm, gate/up_proj, activation, down_proj +
+        ffn_residual), then the last token's final norm + lm_head + sample.
+        Leaves the decoder where teacher-forced decode steps over the prompt
+        would: cache rows 0..P-1 written, the first new token in ids[P],
+        state = (P, P + 1, P, token)."""
+        from .execution import UnsupportedStep
+
+        if not self.can_prefill():
+            raise UnsupportedStep("batched prompts need a uniform Q4_K model")
+        c = self.cfg
+        prompt = np.asarray(prompt, np.int32)
+        P = int(prompt.size)
+        if not 1 <= P < c.max_seq:
+            raise ValueError(f"prompt of {P} tokens for max_seq {c.max_seq}")
+        self.reset(prompt)
+        self.state.upload(np.array([P - 1, P, P, prompt[-1]], np.int32))
+        b = self._prefill_buffers()
+        hd = c.head_dim
+        off = c.norm_weight_offset
+        ids = self.ids.view(0, P * 4, np.int32)
+        ops.embed(self.embed, ids, b["x"], P, c.vocab, c.hidden, c.embed_scale, stream=stream)
+        for li, L in enumerate(self.layers):
+            ops.rmsnorm(b["x"], L.norm_attn, b["xn"], P, c.hidden, c.eps, weight_offset=off, stream=stream)
+            ops.matmul_q4k_gemm_f32(b["xn"], L.wqkv, b["qkv"], P, c.qkv_rows, c.hidden, stream=stream)
+            ops.qkv_rope_kv_rows(b["qkv"], P, c.qkv_rows, c.heads, c.kv_heads, hd, self.freq_by_layer[li], 0,
+                                 L.k_cache, L.v_cache, c.max_seq, stream=stream)
+            ops.attention_prefill_f16kv(b["qkv"], L.k_cache, L.v_cache, b["att"], num_heads=c.heads,
+                                        num_kv_heads=c.kv_heads, head_dim=hd, query_len=P, kv_len=P,
+                                        kv_stride=c.max_seq, start_pos=0, scale=1.0 / math.sqrt(hd),
+                                        softcap=c.attn_softcap, sliding_window=self.attn_windows[li],
+                                        q_row_stride=c.qkv_rows, stream=stream)
+            ops.matmul_q4k_gemm_f32(b["att"], L.wo, b["t"], P, c.hidden, c.q_dim, stream=stream)
+            ops.residual(b["t"], b["x"], b["x"], P * c.hidden, stream=stream)
+            ops.rmsnorm(b["x"], L.norm_ffn, b["xn"], P, c.hidden, c.eps, weight_offset=off, stream=stream)
+            ops.matmul_q4k_gemm_f32(b["xn"], L.wgu, b["gu"], P, 2 * c.ffn, c.hidden, stream=stream)
+            ops.geglu_pairs(b["gu"], b["h"], P * c.ffn, stream=stream)
+            ops.matmul_q4k_gemm_f32(b["h"], L.wd, b["t"], P, c.hidden, c.ffn, stream=stream)
+            ops.residual(b["t"], b["x"], b["x"], P * c.hidden, stream=stream)
+        last = b["x"].view((P - 1) * c.hidden * 4, c.hidden * 4, np.float32)
+        nparts = ops.lm_head_sample(self.lm_head, last, c.vocab, c.hidden, self.argmax_parts,
+                                    logits=self.logits if self.keep_logits else None, norm_weight=self.norm_final,
+                                    norm_eps=c.eps, norm_weight_offset=off, stream=stream)
+        _lib.call("doe_decode_advance", C.c_void_p(self.state.ptr), C.c_void_p(self.token.ptr),
+                  C.c_void_p(self.ids.ptr), c.max_seq, C.c_void_p(self.argmax_parts.ptr), nparts,
+                  _stream_ptr(stream))
+
     # ---- generation ----------------------------------------------------------
     def reset(self, prompt: np.ndarray) -> None:
         """Loads a prompt: ids[0:len] = prompt, state = (0, 1, len, prompt[0])."""
@@ -423,17 +495,27 @@ class Decoder:
         return Graph.capture(stream, body)
 
     def generate(self, prompt: np.ndarray, n_new: int, stream: Stream, graph: Graph | None = None,
-                 steps_per_graph: int = 1, timing: dict | None = None) -> np.ndarray:
-        """Prompt (teacher-forced decode steps), then `n_new` greedy tokens.
-        Returns ids[0 : len(prompt) + n_new].  With `timing`, records the
+                 steps_per_graph: int = 1, timing: dict | None = None, prefill: bool = False) -> np.ndarray:
+        """Prompt, then `n_new` greedy tokens; returns ids[0 : len(prompt) +
+        n_new].  The prompt runs as teacher-forced decode steps, or with
+        `prefill` as one batched pass that also samples the first new token
+        (then n_new - 1 decode steps follow).  With `timing`, records the
         seconds spent in the prompt and in the decode steps (HIP events)."""
         prompt = np.asarray(prompt, np.int32)
         total = prompt.size + n_new
         if total > self.cfg.max_seq:
             raise ValueError("prompt + n_new exceeds max_seq")
-        self.reset(prompt)
-        n_prompt_steps = prompt.size - 1
         e0, e1, e2 = Event(), Event(), Event()
+        if prefill:
+            if n_new < 1:
+                raise ValueError("a batched prompt samples one token: n_new >= 1")
+            e0.record(stream)
+            self.prefill(prompt, stream)
+            e1.record(stream)
+            n_prompt_steps, n_new = 0, n_new - 1
+        else:
+            self.reset(prompt)
+            n_prompt_steps = prompt.size - 1
 
         def run(n):
             if graph is None:
@@ -446,9 +528,10 @@ class Decoder:
                 for _ in range(rest):
                     self.step(stream)
 
-        e0.record(stream)
-        run(n_prompt_steps)
-        e1.record(stream)
+        if not prefill:
+            e0.record(stream)
+            run(n_prompt_steps)
+            e1.record(stream)
         run(n_new)
         e2.record(stream)
         e2.synchronize()

@@ -64,6 +64,40 @@ def matmul_q4k_gemm(a_bf16: DeviceBuffer, weight: DeviceBuffer, output: DeviceBu
     _lib.call("doe_q4k_gemm", _p(a_bf16), _p(weight), _p(output), m, n, k, _stream_ptr(stream))
 
 
+def matmul_q4k_gemm_f32(a: DeviceBuffer, weight: DeviceBuffer, output: DeviceBuffer, m: int, n: int, k: int,
+                        stream=None) -> None:
+    """``matmul_q4k`` at M > 1 with f32 activations a [m][k] (rounded to f16
+    per row by the GEMM's pre-pass): output f32 [m][n]."""
+    _q4k_weight_check(weight, n, k)
+    _need(a, m * k * 4, "a")
+    _need(output, m * n * 4, "output")
+    _lib.call("doe_q4k_gemm_f32", _p(a), _p(weight), _p(output), m, n, k, _stream_ptr(stream))
+
+
+def qkv_rope_kv_rows(qkv: DeviceBuffer, tokens: int, row_stride: int, num_heads: int, num_kv_heads: int,
+                     head_dim: int, freq_cis: DeviceBuffer, start_pos: int, key_cache: DeviceBuffer | None,
+                     val_cache: DeviceBuffer | None, max_seq_len: int, stream=None) -> None:
+    """Prompt rope_q / rope_k + cache write over `tokens` fused q/k/v rows."""
+    if tokens:
+        _need(qkv, ((tokens - 1) * row_stride + (num_heads + 2 * num_kv_heads) * head_dim) * 4, "qkv")
+    _need(freq_cis, max_seq_len * head_dim * 4, "freq_cis")
+    kc = vc = C.c_void_p(None)
+    if num_kv_heads:
+        _need(key_cache, num_kv_heads * max_seq_len * head_dim * 2, "key_cache")
+        _need(val_cache, num_kv_heads * max_seq_len * head_dim * 2, "val_cache")
+        kc, vc = _p(key_cache), _p(val_cache)
+    _lib.call("doe_qkv_rope_kv_rows", _p(qkv), tokens, row_stride, num_heads, num_kv_heads, head_dim, _p(freq_cis),
+              start_pos, kc, vc, max_seq_len, _stream_ptr(stream))
+
+
+def geglu_pairs(gate_up: DeviceBuffer, output: DeviceBuffer, n: int, stream=None) -> None:
+    """``gelu_gated`` over interleaved (gate, up) pairs: output[i] =
+    gelu(gate_up[2i]) * gate_up[2i + 1]."""
+    _need(gate_up, 2 * n * 4, "gate_up")
+    _need(output, n * 4, "output")
+    _lib.call("doe_geglu_pairs", _p(gate_up), _p(output), n, _stream_ptr(stream))
+
+
 def matmul_q8_0(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int,
                 residual: DeviceBuffer | None = None, stream=None, *, norm_weight: DeviceBuffer | None = None,
                 norm_eps: float = 1e-6, norm_weight_offset: bool = False) -> None:
@@ -157,12 +191,12 @@ def attention_dispatch(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, output
                        kv_capacity: int, kv_len_buffer: DeviceBuffer | None = None,
                        page_table: DeviceBuffer | None = None, stream=None, **uniforms) -> None:
     """``attention`` as the reference dispatches it: the Uniforms fields as
-    keywords (query_len 1), K/V f16 [kv_capacity][num_kv_heads][head_dim],
-    f32 q and output [num_heads][head_dim]."""
+    keywords (query_len defaults to 1), K/V f16 [kv_capacity][num_kv_heads]
+    [head_dim], f32 q and output [query_len][num_heads][head_dim]."""
     u = AttentionUniforms(**{"query_len": 1, **uniforms})
-    hd, hq, hkv = u.head_dim, u.num_heads, u.num_kv_heads
-    _need(q, hq * hd * 4, "q")
-    _need(output, hq * hd * 4, "output")
+    hd, hq, hkv, ql = u.head_dim, u.num_heads, u.num_kv_heads, u.query_len
+    _need(q, ql * hq * hd * 4, "q")
+    _need(output, ql * hq * hd * 4, "output")
     _need(k, kv_capacity * hkv * hd * 2, "k")
     _need(v, kv_capacity * hkv * hd * 2, "v")
     pt_len = 0
@@ -171,6 +205,26 @@ def attention_dispatch(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, output
     _lib.call("doe_attention_dispatch", C.byref(u), C.c_void_p(q.ptr), C.c_void_p(k.ptr), C.c_void_p(v.ptr),
               C.c_void_p(output.ptr), C.c_void_p(kv_len_buffer.ptr if kv_len_buffer is not None else None),
               C.c_void_p(page_table.ptr if page_table is not None else None), pt_len, kv_capacity,
+              _stream_ptr(stream))
+
+
+def attention_prefill_f16kv(q: DeviceBuffer, k_cache: DeviceBuffer, v_cache: DeviceBuffer, output: DeviceBuffer, *,
+                            num_heads: int, num_kv_heads: int, head_dim: int, query_len: int, kv_len: int,
+                            kv_stride: int, start_pos: int, scale: float, softcap: float = 0.0,
+                            sliding_window: int = 0, kv_layout: int = 0, q_row_stride: int | None = None,
+                            out_row_stride: int | None = None, stream=None) -> None:
+    """Causal multi-query ``attention`` of a prompt (queries at start_pos +
+    i) over an f16 cache in the decoder's layout; f32 q / output rows."""
+    hd = num_heads * head_dim
+    qs = hd if q_row_stride is None else q_row_stride
+    os_ = hd if out_row_stride is None else out_row_stride
+    if query_len:
+        _need(q, ((query_len - 1) * qs + hd) * 4, "q")
+        _need(output, ((query_len - 1) * os_ + hd) * 4, "output")
+    _need(k_cache, num_kv_heads * kv_stride * head_dim * 2, "k_cache")
+    _need(v_cache, num_kv_heads * kv_stride * head_dim * 2, "v_cache")
+    _lib.call("doe_attn_prefill_f16kv", _p(q), qs, _p(k_cache), _p(v_cache), _p(output), os_, num_heads, num_kv_heads,
+              head_dim, query_len, kv_len, kv_stride, kv_layout, start_pos, scale, softcap, sliding_window,
               _stream_ptr(stream))
 
 

@@ -158,6 +158,13 @@ int doe_q4k_gemv_attn_out(const void *weight_q4k, const float *attn_partials, in
 int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m, int64_t n,
                  int64_t k, doe_stream_t stream);
 
+/* doe_q4k_gemm with f32 activations a [m][k] (a prompt's f32 hidden states,
+ * the step graphs' af32 activation format): each row is scaled by a power of
+ * two and rounded once to f16 (11 significant bits) by the pre-pass, then
+ * the same matrix-core GEMM; the same workspace rule. */
+int doe_q4k_gemm_f32(const float *a, const void *b_q4k, float *c, int64_t m, int64_t n, int64_t k,
+                     doe_stream_t stream);
+
 /* Symmetric int4 group-32 GEMV, batch m in 1..8: y[b][i] = sum_k
  * (q[i][k] - 8) * s[i][k/32] * x[b][k].  w_u4: eight nibbles per u32, element
  * k of row i at bits 4*(k%8) of word (i*k_dim + k)/8; scales f16 [n][k/32];
@@ -281,9 +288,9 @@ int doe_attn_decode_noalloc(const void *q, int q_f16, const uint16_t *k_cache,
 
 /* The reference attention dispatch itself: its Uniforms block field for
  * field (attention_head256_f16kv.wgsl:14-30) and its bindings Q (1), K (2),
- * V (3), output (4), kv_len_buffer (5), page_table (6), in the decode form
- * (query_len 1; prompts: doe_attn_prefill).
- *   q        f32 [num_heads][head_dim]; output f32 [num_heads][head_dim]
+ * V (3), output (4), kv_len_buffer (5), page_table (6), for any query_len
+ * (:72-267; query i at absolute position start_pos + i).
+ *   q        f32 [query_len][num_heads][head_dim]; output the same shape
  *   k/v      f16 [kv_capacity][num_kv_heads][head_dim] (the reference's order)
  *   keys     key_pos in [0, L), L = seq_len or kv_len_buffer[0]
  *            (kv_len_source 1); cache row of key_pos (:51-63): kv_start +
@@ -291,9 +298,14 @@ int doe_attn_decode_noalloc(const void *q, int q_f16, const uint16_t *k_cache,
  *            sliding_window (a ring); kv_layout 2: page_table[abs / page_size]
  *            * page_size + abs % page_size (page_table_len entries, clamped).
  *            Rows are clamped into [0, kv_capacity).
- *   visible  (:115-131) is_causal: key_pos <= start_pos - kv_start;
- *            sliding_window > 0: key_pos >= start_pos - sliding_window + 1 -
- *            kv_start; scores scaled by scale, softcapped by attn_softcap.
+ *   visible  (:115-131) for query i, abs = start_pos + i: is_causal:
+ *            key_pos <= abs - kv_start; sliding_window > 0 and abs >=
+ *            sliding_window: key_pos >= abs - sliding_window + 1 - kv_start;
+ *            scores scaled by scale, softcapped by attn_softcap; a query with
+ *            no visible key writes zeros.
+ * query_len 1 runs the split-K decode kernel; query_len > 1 an MFMA flash
+ * kernel (16 queries x the query heads of one KV head per workgroup, f32 q
+ * as f16 hi + lo, P in f16, f32 accumulation).  head_dim 64/128/256/512.
  * q, k and v must be 16-byte aligned. */
 typedef struct {
     uint32_t num_heads, num_kv_heads, head_dim, seq_len, query_len;
@@ -306,6 +318,23 @@ typedef struct {
 int doe_attention_dispatch(const doe_attention_uniforms *u, const float *q, const uint16_t *k,
                            const uint16_t *v, float *output, const uint32_t *kv_len_buffer,
                            const uint32_t *page_table, int64_t page_table_len, int64_t kv_capacity,
+                           doe_stream_t stream);
+
+/* The multi-query form of the dispatch above over a decoder's cache: causal
+ * attention of query_len prompt queries at positions start_pos + i over keys
+ * [0, kv_len) of an f16 cache in either memory order (kv_layout 0
+ * [num_kv_heads][kv_stride][head_dim], 1 [kv_stride][num_kv_heads]
+ * [head_dim]), q f32 rows of q_row_stride floats ([num_heads][head_dim] at
+ * the start of each row, e.g. the q part of a fused q/k/v projection),
+ * output f32 rows of out_row_stride floats; sliding_window > 0 keeps the
+ * last sliding_window keys of each query, softcap > 0 caps the scores.  The
+ * prefill `attention` step of a step graph's prompt (gemma-3-270m-smoke.json
+ * prefill; attention_head256_f16kv.wgsl:72-267 with is_causal). */
+int doe_attn_prefill_f16kv(const float *q, int64_t q_row_stride, const uint16_t *k_cache,
+                           const uint16_t *v_cache, float *output, int64_t out_row_stride,
+                           int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                           int64_t query_len, int64_t kv_len, int64_t kv_stride, int kv_layout,
+                           int64_t start_pos, float scale, float softcap, int64_t sliding_window,
                            doe_stream_t stream);
 
 /* The split-K half of doe_attn_decode without its combine: per query head
@@ -345,6 +374,22 @@ int doe_geglu(const float *gate, const float *up, float *output, int64_t n, doe_
  * output may be input or residual (in place). */
 int doe_residual_add(const float *input, const float *residual, float *output, int64_t n,
                      doe_stream_t stream);
+/* The prompt form of doe_q4k_gemv_qkv_rope_kv's epilogue, over `tokens` rows
+ * of row_stride floats of a fused [q; k; v] projection (q/k rows interleaved
+ * rotation pairs): token t at position start_pos + t has its q and k pairs
+ * rotated by freq_cis[pos] in place and its k and v rows written as f16 into
+ * the caches [num_kv_heads][max_seq_len][head_dim] -- the prefill rope_q /
+ * rope_k steps (rope.wgsl with seq_len = the prompt) and the cache write of
+ * the prompt (run_csl_webgpu_emulator.mjs:615-644).  Positions must lie in
+ * the cache; num_kv_heads 0 rotates q only. */
+int doe_qkv_rope_kv_rows(float *qkv, int64_t tokens, int64_t row_stride, int64_t num_heads,
+                         int64_t num_kv_heads, int64_t head_dim, const float *freq_cis,
+                         int64_t start_pos, uint16_t *key_cache, uint16_t *val_cache,
+                         int64_t max_seq_len, doe_stream_t stream);
+/* GeGLU over interleaved (gate, up) pairs: out[i] = gelu_tanh(gate_up[2i]) *
+ * gate_up[2i + 1] (gelu_gated.wgsl:1-14; the activation step of a prompt
+ * whose gate/up projection rows are interleaved). */
+int doe_geglu_pairs(const float *gate_up, float *output, int64_t n, doe_stream_t stream);
 /* Per-layer-embedding combine: out = (projected + gathered) * scale, one f32
  * add then one f32 multiply per element -- the `ple_modulate` step
  * (emit_csl_exec_v1.zig:167-172: the element_wise part of the PLE composite,

@@ -369,3 +369,60 @@ def test_gemma4_e2b_graph_replay_equals_eager(dev):
     out = dec.generate(prompt, 14, s, graph=g, steps_per_graph=2)
     g.destroy()
     assert out.tolist() == eager.tolist()
+
+
+def _prefill_then_decode(dec, oracle, prompt, n_after, s):
+    """Batched prompt, then decode steps; every logits vector against the
+    oracle decoder stepping through the same tokens.  Returns the errors."""
+    dec.prefill(prompt, s)
+    s.synchronize()
+    want = None
+    for pos, t in enumerate(prompt):
+        want = oracle.step(pos, int(t))
+    errs = [rel_l2(dec.logits.download(), want)]
+    tok = int(dec.token.download()[0])
+    assert tok == int(np.argmax(want))
+    ids = list(prompt) + [tok]
+    assert dec.ids.download()[: len(ids)].tolist() == ids
+    assert dec.state.download().tolist() == [len(prompt), len(prompt) + 1, len(prompt), tok]
+    for pos in range(len(prompt), len(prompt) + n_after):
+        dec.step(s)
+        s.synchronize()
+        want = oracle.step(pos, ids[pos])
+        errs.append(rel_l2(dec.logits.download(), want))
+        tok = int(dec.token.download()[0])
+        assert tok == int(np.argmax(want)), pos
+        ids.append(tok)
+    return errs
+
+
+def test_prefill_matches_oracle_decoder(dev, ora):
+    # the prompt as one batched pass (Q4_K GEMMs of 20 rows, the multi-query
+    # attention with an 8-key window on layer 0 and a softcap), against the
+    # oracle decoder run token by token; then 6 decode steps on its cache
+    from doe_amd import execution as ex
+
+    cfg = dataclasses.replace(SMALL, attn_softcap=30.0)
+    plan = ex.DecodePlan(layer=(), post=(), windows=(8, 0), eos_token_id=None)
+    dec = Decoder(cfg, keep_logits=True, plan=plan)
+    dec.init_random(seed=21)
+    s = Stream()
+    oracle = OracleDecoder(dec)
+    prompt = np.array([3, 900, 4001, 17, 17, 256, 1024, 5, 77, 3000, 12, 1, 2, 3, 999, 64, 128, 4095, 0, 8], np.int32)
+    errs = _prefill_then_decode(dec, oracle, prompt, 6, s)
+    print(f"[prefill small] logits rel_l2 {['%.1e' % e for e in errs]}", flush=True)
+    assert max(errs) <= 1e-3
+
+
+def test_prefill_full_size(dev, ora):
+    # the 2B-class shape: a 12-token prompt through the batched pass, the last
+    # token's logits against 12 oracle decode steps, then 2 decode steps
+    cfg = DecoderConfig()
+    dec = Decoder(cfg, keep_logits=True)
+    dec.init_random(seed=2)
+    s = Stream()
+    oracle = OracleDecoder(dec)
+    prompt = np.array([12345, 200000, 7, 7, 99999, 1, 250000, 31337, 42, 100, 65535, 3], np.int32)
+    errs = _prefill_then_decode(dec, oracle, prompt, 2, s)
+    print(f"[prefill 2B] logits rel_l2 {['%.1e' % e for e in errs]}", flush=True)
+    assert max(errs) <= 1e-3
