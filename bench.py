@@ -234,9 +234,13 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
     s.synchronize()
     spg = args.steps_per_graph  # 0: eager launches (no graph), e.g. under a profiler
     graph = dec.capture(s, spg) if spg > 0 else None
-    dec.generate(prompt, min(16, args.decode_steps), s, graph=graph, steps_per_graph=max(spg, 1))  # warm
+    # the prompt as one batched pass (uniform Q4_K models), then exactly
+    # --decode-steps decode steps; else the prompt as teacher-forced steps
+    pf = dec.can_prefill() and not args.no_prefill
+    n_new = args.decode_steps + (1 if pf else 0)
+    dec.generate(prompt, min(16, n_new), s, graph=graph, steps_per_graph=max(spg, 1), prefill=pf)  # warm
     timing = {}
-    ids = dec.generate(prompt, args.decode_steps, s, graph=graph, steps_per_graph=max(spg, 1), timing=timing)
+    ids = dec.generate(prompt, n_new, s, graph=graph, steps_per_graph=max(spg, 1), timing=timing, prefill=pf)
     if graph is not None:
         graph.destroy()
     parity, cpu = decode_parity_and_cpu(dec, prompt, s)
@@ -244,8 +248,10 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
     mean_len = args.prompt_len + (args.decode_steps + 1) / 2.0
     bpt = cfg.decode_bytes_per_token(mean_len)
     gbs = bpt * tok_s / 1e9
+    prompt_mode = "one batched prefill pass" if pf else f"{args.prompt_len - 1} teacher-forced decode steps"
     log(f"decode ({label}): {tok_s:.1f} tok/s ({timing['decode_s'] * 1e3 / args.decode_steps:.3f} ms/token), "
-        f"prompt {timing['prompt_s']:.3f} s, {gbs:.0f} GB/s of algorithmic bytes")
+        f"prompt {timing['prompt_s'] * 1e3:.2f} ms ({prompt_mode}, {args.prompt_len / timing['prompt_s']:.0f} "
+        f"prompt tok/s), {gbs:.0f} GB/s of algorithmic bytes")
     return {
         "workload": f"{label} bs=1: {cfg.layers} layers, hidden {cfg.hidden}, {cfg.heads}/{cfg.kv_heads} "
                     f"heads x {cfg.head_dim}, FFN {cfg.ffn} GeGLU, vocab {cfg.vocab}; "
@@ -258,7 +264,9 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
         "achieved_gbs": round(gbs, 1),
         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
         "ceiling_tok_s_at_peak": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
-        "prompt_s": round(timing["prompt_s"], 4),
+        "prompt_s": round(timing["prompt_s"], 5),
+        "prompt_tok_s": round(args.prompt_len / timing["prompt_s"], 1),
+        "prompt_mode": prompt_mode,
         "last_tokens": [int(t) for t in ids[-4:]],
         "parity": parity,
         "cpu_baseline": cpu,
@@ -612,6 +620,7 @@ def main() -> int:
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--steps-per-graph", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="run prompts as teacher-forced decode steps")
     ap.add_argument("--gemm-steps", type=int, default=20)
     ap.add_argument("--large-steps", type=int, default=45)
     ap.add_argument("--no-gemm", action="store_true")
