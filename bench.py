@@ -20,6 +20,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -224,6 +225,11 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
     from doe_amd.model import Decoder, DecoderConfig
 
     cfg = cfg or DecoderConfig()
+    # a batched prompt samples one token before the first decode step: room
+    # for prompt + 1 + decode_steps ids (the KV cache uses one row fewer)
+    need = args.prompt_len + args.decode_steps + 1
+    if cfg.max_seq < need:
+        cfg = dataclasses.replace(cfg, max_seq=need)
     dec = Decoder(cfg, plan=plan)
     dec.init_random(seed=2)
     rng = np.random.default_rng(2)

@@ -97,7 +97,9 @@ SIGNATURES: dict[str, list] = {
     "doe_argmax": [_vp, _i64, _vp, _vp, _vp],
     "doe_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _vp],
     "doe_embed_gather": [_vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp],
+    "doe_gather_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp],
     "doe_f16_gemv": [_vp, _vp, _vp, _i64, _i64, _f32, _vp],
+    "doe_lm_head_gemv": [_vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
     "doe_f16_gemv_argmax": [_vp, _vp, _vp, _i64, _i64, _f32, _vp, _f32, _i32, _vp, _i64, C.POINTER(_i32), _vp],
     "doe_fill_normal_f16": [_vp, _i64, C.c_uint64, _f32, _f32, _vp],
     "doe_fill_normal_f32": [_vp, _i64, C.c_uint64, _f32, _f32, _vp],

@@ -217,6 +217,30 @@ __global__ __launch_bounds__(256) void embed_kernel(const _Float16 *__restrict__
     }
 }
 
+// Strict f32 gather (reference_interpreter.zig:4143-4276): out[t] =
+// table[ids[t]] for u32 ids; an id outside the table zero-fills its row and
+// is counted in *bad (the interpreter rejects such a run).  VEC = 4 moves
+// float4 runs when hidden % 4 == 0.
+template <int VEC>
+__global__ __launch_bounds__(256) void gather_f32_kernel(const uint32_t *__restrict__ ids,
+                                                         const float *__restrict__ table,
+                                                         float *__restrict__ out, int n_ids,
+                                                         uint32_t vocab, int hidden, int *bad) {
+    typedef float fv __attribute__((ext_vector_type(VEC)));
+    const int per_row = hidden / VEC;
+    const long total = (long)n_ids * per_row;
+    for (long g = (long)blockIdx.x * 256 + threadIdx.x; g < total; g += (long)gridDim.x * 256) {
+        const int t = (int)(g / per_row), d = (int)(g % per_row);
+        const uint32_t id = ids[t];
+        fv v = (fv)0.0f;
+        if (id < vocab)
+            v = *reinterpret_cast<const fv *>(table + (size_t)id * hidden + (size_t)d * VEC);
+        else if (d == 0 && bad)
+            atomicAdd(bad, 1);
+        *reinterpret_cast<fv *>(out + (size_t)t * hidden + (size_t)d * VEC) = v;
+    }
+}
+
 unsigned grid_for(long n, unsigned cap = 4096) {
     long b = (n + 255) / 256;
     if (b < 1) b = 1;
@@ -365,6 +389,34 @@ int doe_kv_write(const float *key_proj, const float *val_proj, uint16_t *key_cac
                        (int)num_kv_heads, (int)max_seq_len, (int)head_dim, (int)position,
                        position_dev, kv_layout);
     DOE_LAUNCH_CHECK("kv_write_kernel");
+    return DOE_OK;
+}
+
+int doe_gather_f32(const uint32_t *ids, const float *table, float *output, int64_t n_ids,
+                   int64_t vocab, int64_t hidden, int32_t *bad_ids, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(n_ids >= 0 && vocab >= 0 && hidden >= 0 && vocab <= 0xffffffffL &&
+                    n_ids <= 0x7fffffff && hidden <= 0x7fffffff,
+                DOE_E_INVALID, "bad gather shape");
+    hipStream_t st = (hipStream_t)stream;
+    if (bad_ids) {
+        DOE_REQUIRE(((uintptr_t)bad_ids & 3) == 0, DOE_E_INVALID, "bad_ids must be 4-byte aligned");
+        rc = doe::fill_bytes_async(bad_ids, 0, 4, st);
+        if (rc) return rc;
+    }
+    const long total = (long)n_ids * hidden;
+    if (total == 0) return DOE_OK;
+    DOE_REQUIRE(table || vocab == 0, DOE_E_INVALID, "null table");
+    DOE_REQUIRE(ids && output, DOE_E_INVALID, "null pointer");
+    const bool v4 = (hidden % 4) == 0 && ((uintptr_t)table & 15) == 0 && ((uintptr_t)output & 15) == 0;
+    if (v4)
+        hipLaunchKernelGGL(gather_f32_kernel<4>, dim3(grid_for(total / 4)), dim3(256), 0, st, ids, table,
+                           output, (int)n_ids, (uint32_t)vocab, (int)hidden, (int *)bad_ids);
+    else
+        hipLaunchKernelGGL(gather_f32_kernel<1>, dim3(grid_for(total)), dim3(256), 0, st, ids, table,
+                           output, (int)n_ids, (uint32_t)vocab, (int)hidden, (int *)bad_ids);
+    DOE_LAUNCH_CHECK("gather_f32_kernel");
     return DOE_OK;
 }
 

@@ -4,6 +4,9 @@
 // (runtime/zig/tests/tsir/real/lm_head_gemv/lm_head_gemv.wgsl:78-180,
 // transpose_b = 1), A and C f32.
 //
+// doe_lm_head_gemv is the full form: m activation rows, either layout of B
+// (transpose_b), any k; one row against [N][K] takes the kernel below.
+//
 // Decomposition: persistent waves; a wave owns whole rows (row = wave id +
 // i * total waves) and each lane a fixed set of 16-byte pieces of the row
 // (pieces lane, lane + 64, ...), so its 8-element activation slices stay in
@@ -183,6 +186,169 @@ __global__ __launch_bounds__(256) void f16_gemv_kernel(const uint16_t *__restric
     }
 }
 
+// ---- general forms: any k, B in either layout, m activation rows -----------
+//
+// c[r][j] = alpha * sum_k a[r][k] * B(j, k) for r < m, with B(j, k) =
+// b[j*K + k] (transpose_b = 1) or b[k*N + j] (transpose_b = 0).  Products
+// are plain f32 FMAs of the exact f16 -> f32 weight; each launch covers MT
+// activation rows, so the weights are read ceil(m / MT) times.
+
+template <int VEC>
+__device__ __forceinline__ void load_f16(const uint16_t *p, float (&v)[VEC]) {
+    if constexpr (VEC == 8) {
+        const u32x4 w = load16(p);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // copy the element out first: a bit_cast of the element
+            // expression itself reads element 0 of w
+            const uint32_t word = w[j];
+            const half2v h = __builtin_bit_cast(half2v, word);
+            v[2 * j] = (float)h[0];
+            v[2 * j + 1] = (float)h[1];
+        }
+    } else {
+        v[0] = (float)__builtin_bit_cast(_Float16, *p);
+    }
+}
+
+// transpose_b = 0, b [K][N]: a lane owns VEC adjacent columns, the four
+// waves of a workgroup take the k rows w, w + 4, ... (each row a contiguous
+// 64 * VEC * 2-byte run) and fold their partial sums through LDS.
+template <int MT, int VEC>
+__global__ __launch_bounds__(256) void lm_head_kn_kernel(const float *__restrict__ a,
+                                                         const uint16_t *__restrict__ b,
+                                                         float *__restrict__ c, int m, int n,
+                                                         int k, float alpha) {
+    __shared__ float red[3][MT * VEC][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = (blockIdx.x * 64 + lane) * VEC;
+    const int row0 = blockIdx.y * MT;
+    const bool live = col < n;
+    const uint16_t *bc = b + (live ? col : 0);
+    float acc[MT][VEC];
+#pragma unroll
+    for (int r = 0; r < MT; ++r)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[r][v] = 0.0f;
+    int kk = wave;
+    for (; kk + 12 < k; kk += 16) {
+        float w[4][VEC];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load_f16<VEC>(bc + (size_t)(kk + 4 * u) * n, w[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int r = 0; r < MT; ++r) {
+                const float x = row0 + r < m ? a[(size_t)(row0 + r) * k + kk + 4 * u] : 0.0f;
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) acc[r][v] = fmaf(x, w[u][v], acc[r][v]);
+            }
+    }
+    for (; kk < k; kk += 4) {
+        float w[VEC];
+        load_f16<VEC>(bc + (size_t)kk * n, w);
+#pragma unroll
+        for (int r = 0; r < MT; ++r) {
+            const float x = row0 + r < m ? a[(size_t)(row0 + r) * k + kk] : 0.0f;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) acc[r][v] = fmaf(x, w[v], acc[r][v]);
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < MT; ++r)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) red[wave - 1][r * VEC + v][lane] = acc[r][v];
+    }
+    __syncthreads();
+    if (wave == 0 && live) {
+#pragma unroll
+        for (int r = 0; r < MT; ++r) {
+            if (row0 + r >= m) break;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+                const float s = ((acc[r][v] + red[0][r * VEC + v][lane]) + red[1][r * VEC + v][lane]) +
+                                red[2][r * VEC + v][lane];
+                c[(size_t)(row0 + r) * n + col + v] = s * alpha;
+            }
+        }
+    }
+}
+
+// transpose_b = 1, b [N][K], any k: a wave owns two rows of b at a time and
+// its lanes stride along k, VEC elements per lane per step.
+template <int MT, int VEC>
+__global__ __launch_bounds__(256) void lm_head_nk_kernel(const float *__restrict__ a,
+                                                         const uint16_t *__restrict__ b,
+                                                         float *__restrict__ c, int m, int n,
+                                                         int k, float alpha) {
+    const int lane = threadIdx.x & 63;
+    const int j0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
+    if (j0 >= n) return;
+    const int j1 = min(j0 + 1, n - 1);
+    const int row0 = blockIdx.y * MT;
+    const uint16_t *b0 = b + (size_t)j0 * k, *b1 = b + (size_t)j1 * k;
+    float acc[MT][2];
+#pragma unroll
+    for (int r = 0; r < MT; ++r) acc[r][0] = acc[r][1] = 0.0f;
+    for (int kk = lane * VEC; kk < k; kk += 64 * VEC) {
+        float w0[VEC], w1[VEC];
+        load_f16<VEC>(b0 + kk, w0);
+        load_f16<VEC>(b1 + kk, w1);
+#pragma unroll
+        for (int r = 0; r < MT; ++r) {
+            if (row0 + r >= m) break;
+            const float *ar = a + (size_t)(row0 + r) * k + kk;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+                acc[r][0] = fmaf(ar[v], w0[v], acc[r][0]);
+                acc[r][1] = fmaf(ar[v], w1[v], acc[r][1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < MT; ++r) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            acc[r][0] += __shfl_xor(acc[r][0], o, 64);
+            acc[r][1] += __shfl_xor(acc[r][1], o, 64);
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < MT; ++r) {
+            if (row0 + r >= m) break;
+            c[(size_t)(row0 + r) * n + j0] = acc[r][0] * alpha;
+            if (j0 + 1 < n) c[(size_t)(row0 + r) * n + j0 + 1] = acc[r][1] * alpha;
+        }
+    }
+}
+
+template <int MT>
+int lm_head_general(const float *a, const uint16_t *b, float *c, int m, int n, int k, float alpha,
+                    int transpose_b, hipStream_t st) {
+    const unsigned mtiles = (unsigned)((m + MT - 1) / MT);
+    if (transpose_b) {
+        const bool v8 = (k % 8) == 0 && ((uintptr_t)b & 15) == 0;
+        const dim3 grid((unsigned)((n + 7) / 8), mtiles), blk(256);
+        if (v8)
+            hipLaunchKernelGGL((lm_head_nk_kernel<MT, 8>), grid, blk, 0, st, a, b, c, m, n, k, alpha);
+        else
+            hipLaunchKernelGGL((lm_head_nk_kernel<MT, 1>), grid, blk, 0, st, a, b, c, m, n, k, alpha);
+        DOE_LAUNCH_CHECK("lm_head_nk_kernel");
+    } else {
+        const bool v8 = (n % 8) == 0 && ((uintptr_t)b & 15) == 0;
+        const int cols = v8 ? 512 : 64;
+        const dim3 grid((unsigned)((n + cols - 1) / cols), mtiles), blk(256);
+        if (v8)
+            hipLaunchKernelGGL((lm_head_kn_kernel<MT, 8>), grid, blk, 0, st, a, b, c, m, n, k, alpha);
+        else
+            hipLaunchKernelGGL((lm_head_kn_kernel<MT, 1>), grid, blk, 0, st, a, b, c, m, n, k, alpha);
+        DOE_LAUNCH_CHECK("lm_head_kn_kernel");
+    }
+    return DOE_OK;
+}
+
 int g_num_cus = 0;
 
 int f16_launch(const uint16_t *b_f16, const float *a, float *c, int64_t n, int64_t k, float alpha,
@@ -253,6 +419,33 @@ int doe_f16_gemv_argmax(const uint16_t *b_f16, const float *a, float *logits, in
     int rc = f16_launch(b_f16, a, logits, n, k, alpha, fz, (hipStream_t)stream, cap, &blocks);
     if (num_partials) *num_partials = (int32_t)blocks;
     return rc;
+}
+
+int doe_lm_head_gemv(const float *a, const uint16_t *b_f16, float *c, int64_t m, int64_t n,
+                     int64_t k, float alpha, int transpose_b, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(m >= 0 && n >= 0 && k >= 0 && n <= 0x7fffffff && k <= (1L << 30), DOE_E_INVALID,
+                "bad lm_head_gemv shape");
+    DOE_REQUIRE(transpose_b == 0 || transpose_b == 1, DOE_E_INVALID, "transpose_b must be 0 or 1");
+    DOE_REQUIRE(m <= 65535L * 8, DOE_E_UNSUPPORTED, "lm_head_gemv takes at most 524280 rows");
+    DOE_REQUIRE((uint64_t)m * (uint64_t)n < (1ull << 40), DOE_E_INVALID, "output too large");
+    hipStream_t st = (hipStream_t)stream;
+    if (m == 0 || n == 0) return DOE_OK;
+    DOE_REQUIRE(c, DOE_E_INVALID, "null output");
+    if (k == 0) return doe::fill_bytes_async(c, 0, (size_t)m * (size_t)n * 4, st);
+    DOE_REQUIRE(a && b_f16, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(((uintptr_t)a & 3) == 0 && ((uintptr_t)c & 3) == 0 && ((uintptr_t)b_f16 & 1) == 0,
+                DOE_E_INVALID, "a and c must be 4-byte aligned, b 2-byte aligned");
+    // one activation row against the [N][K] layout: the persistent hi/lo kernel
+    if (m == 1 && transpose_b == 1 && (k % 8) == 0 && k <= 64 * 8 * 16 &&
+        ((uintptr_t)b_f16 & 15) == 0 && ((uintptr_t)a & 15) == 0) {
+        const F16Fusion fz{nullptr, 0.0f, 0, nullptr};
+        return f16_launch(b_f16, a, c, n, k, alpha, fz, st, 0, nullptr);
+    }
+    if (m == 1) return lm_head_general<1>(a, b_f16, c, 1, (int)n, (int)k, alpha, transpose_b, st);
+    if (m <= 4) return lm_head_general<4>(a, b_f16, c, (int)m, (int)n, (int)k, alpha, transpose_b, st);
+    return lm_head_general<8>(a, b_f16, c, (int)m, (int)n, (int)k, alpha, transpose_b, st);
 }
 
 }  // extern "C"

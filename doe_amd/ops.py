@@ -417,6 +417,30 @@ def embed(table: DeviceBuffer, ids: DeviceBuffer, output: DeviceBuffer, n_ids: i
               _stream_ptr(stream))
 
 
+def gather_f32(table: DeviceBuffer, ids: DeviceBuffer, output: DeviceBuffer, n_ids: int, vocab: int,
+               hidden: int, *, strict: bool = True, bad_ids: DeviceBuffer | None = None, stream=None) -> None:
+    """The interpreter's ``gather``: output[t] = table[ids[t]], u32 ids, f32
+    table.  ``strict`` mirrors the reference's rejection of an id outside the
+    table: the call waits for the stream and raises ValueError naming the
+    count (the rows are zero-filled).  ``strict=False`` does not wait; pass
+    ``bad_ids`` (one device int32) to collect the count."""
+    _need(table, vocab * hidden * 4, "table")
+    _need(ids, n_ids * 4, "ids")
+    _need(output, n_ids * hidden * 4, "output")
+    if strict and bad_ids is None:
+        bad_ids = DeviceBuffer.empty((1,), np.int32)
+    if bad_ids is not None:
+        _need(bad_ids, 4, "bad_ids")
+    _lib.call("doe_gather_f32", _p(ids), _p(table), _p(output), n_ids, vocab, hidden,
+              C.c_void_p(bad_ids.ptr) if bad_ids is not None else C.c_void_p(None), _stream_ptr(stream))
+    if strict:
+        if stream is not None:
+            _lib.call("doe_stream_synchronize", _stream_ptr(stream))
+        bad = int(bad_ids.download()[0])
+        if bad:
+            raise ValueError(f"gather rejects {bad} token index(es) outside the {vocab}-row table")
+
+
 def lm_head(weight_f16: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int,
             alpha: float = 1.0, stream=None) -> None:
     """f16-weight GEMV (lm_head_gemv): output[n] = alpha * weight[n][k] @ activation[k]."""
@@ -424,6 +448,18 @@ def lm_head(weight_f16: DeviceBuffer, activation: DeviceBuffer, output: DeviceBu
     _need(activation, k * 4, "activation")
     _need(output, n * 4, "output")
     _lib.call("doe_f16_gemv", _p(weight_f16), _p(activation), _p(output), n, k, alpha, _stream_ptr(stream))
+
+
+def lm_head_gemv(activation: DeviceBuffer, weight_f16: DeviceBuffer, output: DeviceBuffer, m: int, n: int,
+                 k: int, alpha: float = 1.0, transpose_b: int = 1, stream=None) -> None:
+    """lm_head_gemv with its uniforms (M, N, K, alpha, transpose_b):
+    output[r][j] = alpha * sum_k activation[r][k] * B(j, k), B(j, k) =
+    weight[j][k] (transpose_b 1) or weight[k][j] (transpose_b 0)."""
+    _need(weight_f16, n * k * 2, "weight")
+    _need(activation, m * k * 4, "activation")
+    _need(output, m * n * 4, "output")
+    _lib.call("doe_lm_head_gemv", _p(activation), _p(weight_f16), _p(output), m, n, k, alpha, int(transpose_b),
+              _stream_ptr(stream))
 
 
 def lm_head_sample(weight_f16: DeviceBuffer, activation: DeviceBuffer, n: int, k: int, partials: DeviceBuffer, *,

@@ -414,6 +414,13 @@ int doe_kv_write(const float *key_proj, const float *val_proj, uint16_t *key_cac
 int doe_embed_gather(const uint16_t *table_f16, const int32_t *ids, float *output,
                      int64_t n_ids, int64_t vocab, int64_t hidden, float scale,
                      doe_stream_t stream);
+/* The interpreter's gather (reference_interpreter.zig:4143-4276): out[t][:] =
+ * table[ids[t]][:], u32 ids, f32 table.  The reference rejects a run with an
+ * id >= vocab; here such a row is zero-filled and, when bad_ids != NULL, the
+ * device int *bad_ids (cleared by this call) counts those ids, so the caller
+ * can reject the result (the Python mirror does). */
+int doe_gather_f32(const uint32_t *ids, const float *table, float *output, int64_t n_ids,
+                   int64_t vocab, int64_t hidden, int32_t *bad_ids, doe_stream_t stream);
 
 /* ---- f16-weight GEMV (lm_head) -----------------------------------------------
  * c[n] = alpha * sum_k a[k] * f32(b[n][k]); b f16 row-major (transpose_b = 1).
@@ -422,6 +429,15 @@ int doe_embed_gather(const uint16_t *table_f16, const int32_t *ids, float *outpu
  * Uniforms M, N, K, alpha, transpose_b).  k % 8 == 0, k <= 8192. */
 int doe_f16_gemv(const uint16_t *b_f16, const float *a, float *c, int64_t n, int64_t k,
                  float alpha, doe_stream_t stream);
+/* The same GEMV with all of the shader's uniforms: c[r][j] = alpha *
+ * sum_i a[r][i] * B(j, i) for r < m, B(j, i) = b[j*k + i] (transpose_b = 1,
+ * [N][K]) or b[i*n + j] (transpose_b = 0, [K][N]), any k (lm_head_gemv.wgsl
+ * :105-143; main reads activation row 0, i.e. m = 1).  m = 1 against [N][K]
+ * with k % 8 == 0, k <= 8192 and 16-byte aligned a and b runs the
+ * doe_f16_gemv kernel; other shapes read b ceil(m / 8) times (ceil(m / 4)
+ * for m <= 4).  m <= 524280, k <= 2^30. */
+int doe_lm_head_gemv(const float *a, const uint16_t *b_f16, float *c, int64_t m, int64_t n,
+                     int64_t k, float alpha, int transpose_b, doe_stream_t stream);
 /* The lm_head with the final norm and the greedy sample folded in: a =
  * rmsnorm(a) when norm_weight != NULL; logits written when non-NULL; every
  * workgroup writes its best argmax key (see doe_decode_advance) to

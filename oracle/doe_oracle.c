@@ -270,19 +270,35 @@ int ora_f32_gemv(const float *w, const float *x, float *y, int64_t m, int64_t k)
     return 0;
 }
 
-int ora_f16_gemv(const uint16_t *b, const float *a, float *c, int64_t n, int64_t k,
-                 float alpha) {
-    /* lm_head_gemv.wgsl:78-180 with transpose_b = 1: C[n] = alpha *
-     * sum_k A[k] * f32(B[n*K + k]); the sum is restated as an f32 left-fold
-     * (reference_interpreter.zig:333-339). */
-    if (n < 0 || k < 0) return -1;
-    for (int64_t j = 0; j < n; ++j) {
-        const uint16_t *row = b + (size_t)j * (size_t)k;
-        float acc = 0.0f;
-        for (int64_t kk = 0; kk < k; ++kk) acc += a[kk] * ora_f16_to_f32(row[kk]);
-        c[j] = acc * alpha;
+int ora_lm_head_gemv(const float *a, const uint16_t *b, float *c, int64_t m, int64_t n,
+                     int64_t k, float alpha, int transpose_b) {
+    /* lm_head_gemv.wgsl:79-168 (main; main_multicol :188-274 is the same
+     * sum): C[col] = alpha * sum_k A[k] * f32(B(col, k)), B(col, k) =
+     * B[col*K + k] when transpose_b == 1 (:105-116), B[k*N + col] otherwise
+     * (:117-143).  The shader reads activation row 0 only; row r of a here
+     * is computed the same way into row r of c.  Each sum is an f32
+     * left-fold (reference_interpreter.zig:333-339) and alpha scales the
+     * finished sum (:167). */
+    if (m < 0 || n < 0 || k < 0 || (transpose_b != 0 && transpose_b != 1)) return -1;
+    for (int64_t r = 0; r < m; ++r) {
+        const float *ar = a + (size_t)r * (size_t)k;
+        for (int64_t j = 0; j < n; ++j) {
+            float acc = 0.0f;
+            for (int64_t kk = 0; kk < k; ++kk) {
+                const size_t at = transpose_b ? (size_t)j * (size_t)k + (size_t)kk
+                                              : (size_t)kk * (size_t)n + (size_t)j;
+                acc += ar[kk] * ora_f16_to_f32(b[at]);
+            }
+            c[(size_t)r * (size_t)n + j] = acc * alpha;
+        }
     }
     return 0;
+}
+
+int ora_f16_gemv(const uint16_t *b, const float *a, float *c, int64_t n, int64_t k,
+                 float alpha) {
+    /* lm_head_gemv.wgsl:78-180 with transpose_b = 1 and one activation row. */
+    return ora_lm_head_gemv(a, b, c, 1, n, k, alpha, 1);
 }
 
 int ora_int4g32_gemv(const uint32_t *q, const uint16_t *scales, const float *x, float *y,
@@ -481,6 +497,21 @@ int ora_embed_gather(const uint16_t *table_f16, const int32_t *ids, float *out,
                                       : 0.0f;
         }
     }
+    return 0;
+}
+
+int ora_gather_f32(const uint32_t *ids, const float *table, float *out, int64_t n_ids,
+                   int64_t vocab, int64_t hidden) {
+    /* reference_interpreter.zig:4143-4219 (gather: out[t][h] = table[ids[t]][h],
+     * u32 indices, f32 table) and :4221-4276 (an index outside the table
+     * rejects the whole run, nothing is clamped): returns -2 then, with out
+     * untouched. */
+    if (n_ids < 0 || vocab < 0 || hidden < 0) return -1;
+    for (int64_t t = 0; t < n_ids; ++t)
+        if ((int64_t)ids[t] >= vocab) return -2;
+    for (int64_t t = 0; t < n_ids; ++t)
+        for (int64_t h = 0; h < hidden; ++h)
+            out[t * hidden + h] = table[(int64_t)ids[t] * hidden + h];
     return 0;
 }
 

@@ -44,6 +44,8 @@ int ora_q4k_gemm(const uint16_t *a_bf16, const uint8_t *b, float *c, int64_t m, 
 
 /* ---- dense GEMVs --------------------------------------------------------- */
 int ora_f32_gemv(const float *w, const float *x, float *y, int64_t m, int64_t k);
+int ora_lm_head_gemv(const float *a, const uint16_t *b, float *c, int64_t m, int64_t n,
+                     int64_t k, float alpha, int transpose_b);
 int ora_f16_gemv(const uint16_t *b, const float *a, float *c, int64_t n, int64_t k,
                  float alpha);
 int ora_int4g32_gemv(const uint32_t *q, const uint16_t *scales, const float *x, float *y,
@@ -70,6 +72,8 @@ int ora_residual(const float *a, const float *b, float *out, int64_t n);
 int64_t ora_argmax(const float *logits, int64_t n);
 int ora_embed_gather(const uint16_t *table_f16, const int32_t *ids, float *out,
                      int64_t n_ids, int64_t vocab, int64_t hidden, float scale);
+int ora_gather_f32(const uint32_t *ids, const float *table, float *out, int64_t n_ids,
+                   int64_t vocab, int64_t hidden);
 int ora_kv_write(const float *k_proj, const float *v_proj, uint16_t *k_cache,
                  uint16_t *v_cache, int64_t num_kv_heads, int64_t max_seq, int64_t head_dim,
                  int64_t pos, int kv_layout);

@@ -45,6 +45,7 @@ def lib() -> C.CDLL:
             "ora_q4k_gemm": ([vp, vp, vp, i64, i64, i64], i32),
             "ora_f32_gemv": ([vp, vp, vp, i64, i64], i32),
             "ora_f16_gemv": ([vp, vp, vp, i64, i64, f32], i32),
+            "ora_lm_head_gemv": ([vp, vp, vp, i64, i64, i64, f32, i32], i32),
             "ora_int4g32_gemv": ([vp, vp, vp, vp, i64, i64, i64], i32),
             "ora_q8_0_element_count": ([i64], i64),
             "ora_q8_0_dequant": ([vp, vp, i64, i64], i32),
@@ -57,6 +58,7 @@ def lib() -> C.CDLL:
             "ora_residual": ([vp, vp, vp, i64], i32),
             "ora_argmax": ([vp, i64], i64),
             "ora_embed_gather": ([vp, vp, vp, i64, i64, i64, f32], i32),
+            "ora_gather_f32": ([vp, vp, vp, i64, i64, i64], i32),
             "ora_kv_write": ([vp, vp, vp, vp, i64, i64, i64, i64, i32], i32),
             "ora_attn_decode": ([vp, vp, vp, vp, i64, i64, i64, i64, i64, f32, f32, i64, i32], i32),
             "ora_attn_prefill": ([vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, f32, i32, i64, i64], i32),
@@ -153,6 +155,18 @@ def f16_gemv(b_f16: np.ndarray, a: np.ndarray, alpha: float = 1.0) -> np.ndarray
     return c
 
 
+def lm_head_gemv(a: np.ndarray, b_f16: np.ndarray, alpha: float = 1.0, transpose_b: int = 1) -> np.ndarray:
+    """a [m][k] f32; b f16 [n][k] (transpose_b 1) or [k][n] (0); returns c [m][n]."""
+    a = np.atleast_2d(_c(a, np.float32))
+    b = _c(b_f16, np.float16).view(np.uint16)
+    m, k = a.shape
+    n = b.shape[0] if transpose_b else b.shape[1]
+    assert b.shape == ((n, k) if transpose_b else (k, n))
+    c = np.zeros((m, n), np.float32)
+    _ok(lib().ora_lm_head_gemv(_ptr(a), _ptr(b), _ptr(c), m, n, k, alpha, transpose_b), "lm_head_gemv")
+    return c
+
+
 def int4g32_gemv(q_u32: np.ndarray, scales_f16: np.ndarray, x: np.ndarray, m: int, n: int, k: int) -> np.ndarray:
     q = _c(q_u32, np.uint32)
     s = _c(scales_f16, np.float16).view(np.uint16)
@@ -239,6 +253,17 @@ def residual(a: np.ndarray, b: np.ndarray) -> np.ndarray:
 def argmax(logits: np.ndarray) -> int:
     x = _c(logits, np.float32)
     return int(lib().ora_argmax(_ptr(x), x.size))
+
+
+def gather_f32(table: np.ndarray, ids: np.ndarray) -> np.ndarray:
+    """The interpreter's gather: f32 table [vocab][hidden], u32 ids; raises
+    ValueError for an id outside the table (nothing is clamped)."""
+    t = _c(table, np.float32)
+    i = _c(ids, np.uint32)
+    vocab, hidden = t.shape
+    out = np.zeros((i.size, hidden), np.float32)
+    _ok(lib().ora_gather_f32(_ptr(i), _ptr(t), _ptr(out), i.size, vocab, hidden), "gather_f32")
+    return out
 
 
 def embed_gather(table_f16: np.ndarray, ids: np.ndarray, scale: float = 1.0) -> np.ndarray:

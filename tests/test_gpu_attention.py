@@ -334,8 +334,9 @@ def test_reference_dispatch_cache_addressing(dev, ora):
 def test_reference_dispatch_rejects_unsupported(dev):
     buf = DeviceBuffer(1 << 16)
     kw = dict(num_heads=2, num_kv_heads=1, head_dim=64, seq_len=4, scale=1.0, is_causal=1, start_pos=3)
-    with pytest.raises(DoeError, match="query_len"):
-        ops.attention_dispatch(buf, buf, buf, buf, kv_capacity=8, **{**kw, "query_len": 4})
+    # several queries run the multi-query kernel, whose head widths are 64 .. 512
+    with pytest.raises(DoeError, match="head_dim"):
+        ops.attention_dispatch(buf, buf, buf, buf, kv_capacity=8, **{**kw, "query_len": 4, "head_dim": 96})
     with pytest.raises(DoeError, match="kv_layout"):
         ops.attention_dispatch(buf, buf, buf, buf, kv_capacity=8, kv_layout=3, **kw)
     with pytest.raises(DoeError, match="page"):

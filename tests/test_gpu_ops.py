@@ -1,5 +1,6 @@
 """GPU parity of the decode-loop ops (RMSNorm, RoPE, GeGLU, residual, argmax,
-KV write, embed gather, f16 lm_head GEMV, fused Q4_K GEMVs) against the CPU
+KV write, embed gather, f16 lm_head GEMV in both layouts and with several
+activation rows, fused Q4_K GEMVs) against the CPU
 oracle, through the C ABI.  Byte/index work and exactly-rounded elementwise
 ops are compared bit-exactly; reductions and transcendentals by rel-L2."""
 import math
@@ -123,6 +124,45 @@ def test_embed_gather_bit_exact(dev, ora):
     assert np.array_equal(out.download(), ora.embed_gather(table, ids, 48.0))
 
 
+def test_gather_f32_interpreter_known_answer(dev, known_answers):
+    # reference_interpreter.zig:4143-4219: rows [2, 0, 3] of a 4x2 table
+    e = known_answers["interp_gather"]
+    table = np.array(e["table_f32"], np.float32)
+    ids = np.array(e["indices_u32"], np.uint32)
+    out = DeviceBuffer.empty((3, 2), np.float32)
+    ops.gather_f32(up(table), up(ids), out, 3, 4, 2)
+    assert np.array_equal(out.download(), np.array(e["output"], np.float32))
+    # :4221-4276: an index outside the table is rejected, not clamped
+    e = known_answers["interp_gather_oob"]
+    out1 = DeviceBuffer.empty((1, 1), np.float32)
+    with pytest.raises(ValueError):
+        ops.gather_f32(up(np.array(e["table_f32"], np.float32)), up(np.array(e["indices_u32"], np.uint32)),
+                       out1, 1, 2, 1)
+
+
+@pytest.mark.parametrize("n_ids,vocab,hidden", [(40, 50, 7), (128, 262144 // 64, 2304), (3, 9, 1), (0, 4, 8)])
+def test_gather_f32_bit_exact(dev, ora, n_ids, vocab, hidden):
+    rng = np.random.default_rng(n_ids + vocab + hidden)
+    table = rng.standard_normal((vocab, hidden)).astype(np.float32)
+    table.view(np.uint32)[0, 0] = 0x7FC01234  # NaN payloads move unchanged
+    ids = rng.integers(0, vocab, n_ids).astype(np.uint32)
+    if n_ids:
+        ids[0] = 0
+    out = DeviceBuffer.empty((max(n_ids, 1), hidden), np.float32)
+    ops.gather_f32(up(table), up(ids if n_ids else np.zeros(1, np.uint32)), out, n_ids, vocab, hidden)
+    if n_ids:
+        assert np.array_equal(out.download()[:n_ids].view(np.uint32), ora.gather_f32(table, ids).view(np.uint32))
+    # non-strict: out-of-range rows zero-filled and counted on the device
+    bad = DeviceBuffer.from_array(np.array([77], np.int32))
+    ids2 = np.array([1, vocab, 0xFFFFFFFF, 0], np.uint32)
+    out2 = DeviceBuffer.empty((4, hidden), np.float32)
+    ops.gather_f32(up(table), up(ids2), out2, 4, vocab, hidden, strict=False, bad_ids=bad)
+    got = out2.download()
+    assert bad.download()[0] == 2
+    assert np.array_equal(got[[0, 3]].view(np.uint32), table[[1, 0]].view(np.uint32))
+    assert not got[1:3].any()
+
+
 @pytest.mark.parametrize("n,k", [(256000 // 8, 2304), (1000, 2304), (7, 8), (100, 5120), (33, 512)])
 def test_f16_gemv(dev, ora, n, k):
     rng = np.random.default_rng(n + k)
@@ -145,6 +185,60 @@ def test_f16_gemv_full_vocab_shape(dev):
     rows = rng.integers(0, n, 2000)
     want = b[rows].astype(np.float64) @ a.astype(np.float64)
     assert rel_l2(got[rows], want) < 1e-5
+
+
+@pytest.mark.parametrize("m,n,k,tb", [
+    (1, 1000, 2304, 0), (1, 999, 777, 0), (3, 4096, 2304, 0), (4, 37, 5120, 0), (9, 1032, 300, 0),
+    (17, 513, 64, 0), (1, 1000, 777, 1), (1, 333, 10000, 1), (2, 1000, 2304, 1), (5, 77, 129, 1),
+    (12, 1001, 5120, 1), (1, 8, 1, 0), (1, 3, 1, 1)])
+def test_lm_head_gemv_layouts_and_rows(dev, ora, m, n, k, tb):
+    # lm_head_gemv.wgsl:105-143: both layouts of B, odd and large K, and
+    # several activation rows, against the oracle (f32 sums, rel-L2 1e-5)
+    rng = np.random.default_rng(m * 7 + n + k + tb)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = (rng.standard_normal((n, k) if tb else (k, n)) * 0.02).astype(np.float16)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.lm_head_gemv(up(a), up(b), out, m, n, k, alpha=-0.75, transpose_b=tb)
+    assert rel_l2(out.download(), ora.lm_head_gemv(a, b, -0.75, tb)) < 1e-5
+
+
+def test_lm_head_gemv_one_row_is_doe_f16_gemv(dev):
+    # one row against [N][K] runs the same kernel as doe_f16_gemv: identical bits
+    rng = np.random.default_rng(21)
+    n, k = 3000, 2304
+    a = rng.standard_normal(k).astype(np.float32)
+    b = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    o1 = DeviceBuffer.empty((n,), np.float32)
+    o2 = DeviceBuffer.empty((n,), np.float32)
+    ops.lm_head(up(b), up(a), o1, n, k, alpha=0.5)
+    ops.lm_head_gemv(up(a), up(b), o2, 1, n, k, alpha=0.5, transpose_b=1)
+    assert np.array_equal(o1.download(), o2.download())
+
+
+def test_lm_head_gemv_full_vocab_column_major(dev):
+    # 256000 x 2304 stored [K][N] (transpose_b = 0), two rows: float64 on sampled columns
+    rng = np.random.default_rng(22)
+    m, n, k = 2, 256000, 2304
+    b = (rng.standard_normal((k, n), dtype=np.float32) * 0.02).astype(np.float16)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.lm_head_gemv(up(a), up(b), out, m, n, k, transpose_b=0)
+    got = out.download()
+    cols = rng.integers(0, n, 2000)
+    want = a.astype(np.float64) @ b[:, cols].astype(np.float64)
+    assert rel_l2(got[:, cols], want) < 1e-5
+
+
+def test_lm_head_gemv_edges(dev):
+    from doe_amd import DoeError
+    out = DeviceBuffer.from_array(np.full((2, 5), 7.0, np.float32))
+    a = DeviceBuffer.empty((2, 1), np.float32)
+    b = DeviceBuffer.empty((5, 1), np.float16)
+    ops.lm_head_gemv(a, b, out, 2, 5, 0)  # k = 0: all-zero output
+    assert not out.download().any()
+    ops.lm_head_gemv(a, b, out, 0, 5, 1)  # m = 0: nothing written
+    with pytest.raises(DoeError):
+        ops.lm_head_gemv(a, b, out, 1, 5, 1, transpose_b=2)
 
 
 def test_fused_gemv_norm_residual_gated(dev, ora, gemv_kernel):

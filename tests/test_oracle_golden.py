@@ -412,6 +412,64 @@ def test_f16_gemv_one_hot_and_zero(ora):
     assert np.array_equal(ora.f16_gemv(b[3:5], a), ora.f16_gemv(b, a)[3:5])
 
 
+def test_lm_head_gemv_layouts_and_rows_match_float64(ora):
+    # lm_head_gemv.wgsl:105-143: transpose_b = 1 reads B[col*K + k], 0 reads
+    # B[k*N + col].  float64 dense for both layouts, odd and decode-width K,
+    # several activation rows; alpha != 1.
+    rng = np.random.default_rng(17)
+    for m, n, k, alpha in [(1, 29, 2304, 0.5), (3, 17, 777, -1.25), (5, 8, 1, 2.0), (2, 40, 5120, 1.0)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = (0.02 * rng.standard_normal((n, k))).astype(np.float16)
+        ref = alpha * (a.astype(np.float64) @ b.astype(np.float64).T)
+        c1 = ora.lm_head_gemv(a, b, alpha, transpose_b=1)
+        c0 = ora.lm_head_gemv(a, np.ascontiguousarray(b.T), alpha, transpose_b=0)
+        assert c1.shape == c0.shape == (m, n)
+        assert np.linalg.norm(c1 - ref) / np.linalg.norm(ref) < 1e-5, (m, n, k)
+        # the two layouts name the same matrix: same sums in the same order
+        assert np.array_equal(c0, c1), (m, n, k)
+        # a transposed index (B[k*K + col]) would only agree for square B
+        if n != k and m == 1:
+            assert np.array_equal(c1[0], ora.f16_gemv(b, a[0], alpha))
+
+
+def test_lm_head_gemv_rows_are_independent(ora):
+    rng = np.random.default_rng(18)
+    m, n, k = 6, 11, 300
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float16)
+    c = ora.lm_head_gemv(a, b, 1.0, transpose_b=0)
+    for r in range(m):
+        assert np.array_equal(ora.lm_head_gemv(a[r], b, 1.0, transpose_b=0)[0], c[r])
+    # a one-hot row selects row k of the [K][N] matrix exactly
+    e = np.zeros((1, k), np.float32)
+    e[0, 123] = 1.0
+    assert np.array_equal(ora.lm_head_gemv(e, b, 1.0, transpose_b=0)[0], b[123].astype(np.float32))
+    # transpose_b is a flag: other values are rejected before any access
+    assert ora.lib().ora_lm_head_gemv(None, None, None, 1, 1, 1, 1.0, 2) == -1
+
+
+def test_gather_f32_interpreter_known_answers(ora, known_answers):
+    e = known_answers["interp_gather"]
+    out = ora.gather_f32(np.array(e["table_f32"], np.float32), np.array(e["indices_u32"], np.uint32))
+    assert np.array_equal(out, np.array(e["output"], np.float32))
+    # an index one past the table rejects the run instead of clamping to the last row
+    e = known_answers["interp_gather_oob"]
+    with pytest.raises(ValueError):
+        ora.gather_f32(np.array(e["table_f32"], np.float32), np.array(e["indices_u32"], np.uint32))
+    # the largest u32 is not read as -1
+    with pytest.raises(ValueError):
+        ora.gather_f32(np.ones((3, 2), np.float32), np.array([0, 0xFFFFFFFF], np.uint32))
+    # in range: a row copy, bit for bit (NaN payloads and -0.0 included)
+    rng = np.random.default_rng(19)
+    table = rng.standard_normal((50, 7)).astype(np.float32)
+    table[3, 1] = -0.0
+    table.view(np.uint32)[4, 2] = 0x7FC01234
+    ids = rng.integers(0, 50, 40).astype(np.uint32)
+    ids[:2] = [3, 4]
+    got = ora.gather_f32(table, ids)
+    assert np.array_equal(got.view(np.uint32), table[ids].view(np.uint32))
+
+
 def test_residual_is_ieee_f32_addition(ora):
     # run_csl_webgpu_emulator.mjs:482-489 / residual.wgsl: out = a + b, one f32
     # addition per element: bit-equal to numpy's IEEE float32 add, including
@@ -451,6 +509,7 @@ PINS = {
     "ora_q4k_gemm": ["test_q4k_gemm_matches_float64_and_sampled"],
     "ora_f32_gemv": ["test_interp_gemv_known_answer", "test_fixture_fused_gemv"],
     "ora_f16_gemv": ["test_f16_gemv_matches_float64_dense", "test_f16_gemv_one_hot_and_zero"],
+    "ora_lm_head_gemv": ["test_lm_head_gemv_layouts_and_rows_match_float64", "test_lm_head_gemv_rows_are_independent"],
     "ora_int4g32_gemv": ["test_int4g32_gemv_closed_form"],
     "ora_q8_0_element_count": ["test_q8_0.py::test_reference_size_checks"],
     "ora_q8_0_dequant": ["test_q8_0.py::test_known_block_bytes", "test_q8_0.py::test_matches_int4_group32_oracle"],
@@ -464,6 +523,7 @@ PINS = {
     "ora_residual": ["test_residual_is_ieee_f32_addition"],
     "ora_argmax": ["test_argmax_known_answers"],
     "ora_embed_gather": ["test_kv_write_and_gather"],
+    "ora_gather_f32": ["test_gather_f32_interpreter_known_answers"],
     "ora_kv_write": ["test_kv_write_and_gather"],
     "ora_attn_decode": ["test_emulator_attention_known_answer", "test_attention_invariants_and_gqa"],
     "ora_attn_prefill": ["test_attention_prefill_causal_matches_float64"],
