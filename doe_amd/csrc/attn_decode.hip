@@ -372,60 +372,69 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     }
 }
 
-// Combine of the split partials, one workgroup per query head:
-// out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s.
-// Thread (column c4, phase ph) sums splits ph, ph + PH, ...; every load of a
-// 16-split batch is issued before the first is used, the phases fold in LDS.
+// Combine of the split partials: out = sum_s o_s 2^(m_s - M) / sum_s l_s
+// 2^(m_s - M), M = max_s m_s.  One workgroup per (query head, 64-column
+// slice of the head): thread (column quad c4, phase ph) sums splits ph,
+// ph + 16, ...; its first eight splits' loads are issued before the (m, l)
+// pass, and M and L are block reductions (wave shuffles, then LDS).
+constexpr int kCombineCols = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    constexpr int C4 = D / 4;
-    constexpr int PH = 256 / C4;
+    constexpr int SL = D < kCombineCols ? D : kCombineCols;  // columns per workgroup
+    constexpr int C4 = SL / 4, PH = 256 / C4;
+    constexpr int NS = D / SL;                                 // slices per head
     __shared__ float wts[kMaxSplits];
-    __shared__ float red_l[kMaxSplits];
     __shared__ float4 fold[256];
-    __shared__ float sM, sL;
-    const int bh = blockIdx.x, tid = threadIdx.x;
+    __shared__ float red[4];
+    const int bh = blockIdx.x / NS, col0 = (blockIdx.x % NS) * SL, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
     const int S = a.splits;
     const float *ml = a.ws_ml + (size_t)bh * S * 2;
     const int c4 = tid % C4, ph = tid / C4;
-    const float4 *po = reinterpret_cast<const float4 *>(a.ws_o + (size_t)bh * S * D) + c4;
+    const float4 *po = reinterpret_cast<const float4 *>(a.ws_o + (size_t)bh * S * D + col0) + c4;
+    constexpr int DC4 = D / 4;  // float4 stride between splits
 
-    // first batch of partial outputs in flight before the (m, l) pass
-    float4 v[16];
+    float4 v[8];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] = po[(size_t)min(ph + u * PH, S - 1) * C4];
-    for (int sp = tid; sp < S; sp += 256) {
-        wts[sp] = ml[2 * sp];
-        red_l[sp] = ml[2 * sp + 1];
-    }
+    for (int u = 0; u < 8; ++u) v[u] = po[(size_t)min(ph + u * PH, S - 1) * DC4];
+    // (m, l) of splits tid and tid + 256 (S <= kMaxSplits = 512)
+    float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
+    if (tid < S) { m0 = ml[2 * tid]; l0 = ml[2 * tid + 1]; }
+    if (tid + 256 < S) { m1 = ml[2 * (tid + 256)]; l1 = ml[2 * (tid + 256) + 1]; }
+    float mx = wave_max(fmaxf(m0, m1));
+    if (lane == 0) red[wave] = mx;
     __syncthreads();
-    if (tid == 0) {
-        float M = -INFINITY;
-        for (int sp = 0; sp < S; ++sp) M = fmaxf(M, wts[sp]);
-        sM = M;
-    }
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float f0 = (m0 == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(m0 - M);
+    const float f1 = (m1 == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(m1 - M);
+    if (tid < S) wts[tid] = f0;
+    if (tid + 256 < S) wts[tid + 256] = f1;
+    const float ls = wave_sum(l0 * f0 + l1 * f1);
+    __syncthreads();  // every wave has read red (M) and written wts
+    if (lane == 0) red[wave] = ls;
     __syncthreads();
-    const float M = sM;
-    for (int sp = tid; sp < S; sp += 256) {
-        const float m = wts[sp];
-        const float f = (m == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(m - M);
-        wts[sp] = f;
-        red_l[sp] *= f;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float L = 0.0f;
-        for (int sp = 0; sp < S; ++sp) L += red_l[sp];
-        sL = L;
-    }
+    const float L = (red[0] + red[1]) + (red[2] + red[3]);
+
     float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int base = 0; base < S; base += 16 * PH) {
+    for (int base = 0; base < S; base += 8 * PH) {
         if (base > 0) {
 #pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = po[(size_t)min(base + ph + u * PH, S - 1) * C4];
+            for (int u = 0; u < 8; ++u) v[u] = po[(size_t)min(base + ph + u * PH, S - 1) * DC4];
         }
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+        for (int u = 0; u < 8; ++u) {
             const int sp = base + ph + u * PH;
             const float f = sp < S ? wts[sp] : 0.0f;
             t.x = fmaf(v[u].x, f, t.x); t.y = fmaf(v[u].y, f, t.y);
@@ -440,10 +449,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
             const float4 u = fold[p2 * C4 + tid];
             r.x += u.x; r.y += u.y; r.z += u.z; r.w += u.w;
         }
-        const float L = sL;
         const float inv = L > 0.0f ? 1.0f / L : 0.0f;
         const float rv[4] = {r.x * inv, r.y * inv, r.z * inv, r.w * inv};
-        const size_t oi = (size_t)bh * D + 4 * tid;
+        const size_t oi = (size_t)bh * D + col0 + 4 * tid;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             if (a.out_f16) reinterpret_cast<_Float16 *>(a.out)[oi + j] = (_Float16)rv[j];
@@ -493,8 +501,9 @@ template <int D>
 int launch_d(int g, bool w, dim3 grid, hipStream_t st, const AttnArgs &a) {
     int rc = launch_main<D>(g, w, grid, st, a);
     if (rc || a.splits == 1 || a.partials_only) return rc;
+    const unsigned slices = D < kCombineCols ? 1u : (unsigned)(D / kCombineCols);
     const unsigned total_heads = grid.z * (unsigned)a.num_heads;
-    hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(total_heads), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(total_heads * slices), dim3(256), 0, st, a);
     DOE_LAUNCH_CHECK("attn_combine_kernel");
     return DOE_OK;
 }
