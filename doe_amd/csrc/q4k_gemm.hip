@@ -164,6 +164,10 @@ struct GemmArgs {
     const uint8_t *b;
     float *c;
     int M, N, Kp, nb, nchunk, tiles_m, tiles_n;
+    // K split of the small-tile kernel (gridDim.y > 1): split y runs chunks
+    // [y kps, (y + 1) kps) and writes its partial tile to part + y M N
+    float *part;
+    int kps;
 };
 
 // Four halves from the low nibbles and four from the high nibbles of one
@@ -273,13 +277,15 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    DOE_GEMM_LOAD_CHUNK(0);
-    DOE_GEMM_STORE_CHUNK(0, 0);
+    const int kc0 = (int)blockIdx.y * g.kps, kc1 = min(g.nchunk, kc0 + g.kps);
+    float *cout = gridDim.y > 1 ? g.part + (size_t)blockIdx.y * g.M * g.N : g.c;
+    DOE_GEMM_LOAD_CHUNK(kc0);
+    DOE_GEMM_STORE_CHUNK(0, kc0);
     __syncthreads();
     const int lr = lane & 31, lk = 8 * (lane >> 5);
-    for (int kc = 0; kc < g.nchunk; ++kc) {
-        const int buf = kc & 1;
-        if (kc + 1 < g.nchunk) DOE_GEMM_LOAD_CHUNK(kc + 1);
+    for (int kc = kc0; kc < kc1; ++kc) {
+        const int buf = (kc - kc0) & 1;
+        if (kc + 1 < kc1) DOE_GEMM_LOAD_CHUNK(kc + 1);
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
             half8 af[TM], bf[TN];
@@ -295,7 +301,7 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        if (kc + 1 < g.nchunk) DOE_GEMM_STORE_CHUNK(buf ^ 1, kc + 1);
+        if (kc + 1 < kc1) DOE_GEMM_STORE_CHUNK(buf ^ 1, kc + 1);
         __syncthreads();
     }
 #undef DOE_GEMM_LOAD_CHUNK
@@ -312,7 +318,7 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int n = n0 + wn * 32 * TN + j * 32 + lr;
-                if (n < g.N) g.c[(size_t)m * g.N + n] = acc[i][j][r] * us;
+                if (n < g.N) cout[(size_t)m * g.N + n] = acc[i][j][r] * us;
             }
         }
     }
@@ -600,10 +606,33 @@ __global__ __launch_bounds__(256) void q4k_gemm_pipe_kernel(GemmArgs g) {
     }
 }
 
+// c = sum of the K splits' partial tiles (split order, so the result is
+// the same on every run).
+__global__ __launch_bounds__(256) void sum_splits_kernel(const float *__restrict__ part, float *__restrict__ c,
+                                                         size_t mn, int splits) {
+    const size_t n4 = mn / 4;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        float4 acc = reinterpret_cast<const float4 *>(part)[i];
+        for (int s = 1; s < splits; ++s) {
+            const float4 v = reinterpret_cast<const float4 *>(part + (size_t)s * mn)[i];
+            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        }
+        reinterpret_cast<float4 *>(c)[i] = acc;
+    }
+    // the last mn % 4 elements
+    const size_t i = 4 * n4 + (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (blockIdx.x == 0 && i < mn) {
+        float acc = part[i];
+        for (int s = 1; s < splits; ++s) acc += part[(size_t)s * mn + i];
+        c[i] = acc;
+    }
+}
+
 // Library-owned workspace (grow-only) for the f16 copy of A and its row scales.
 std::mutex g_ws_mu;
 void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
+int g_num_cus = 0;
 
 int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m, int64_t n, int64_t k,
               doe_stream_t stream) {
@@ -628,7 +657,29 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     // the large-tile kernel streams whole Q4_K blocks: A padded to 256 nb columns
     const int64_t kp = big ? (k + 255) / 256 * 256 : (k + kBK - 1) / kBK * kBK;
     const size_t a16_bytes = (size_t)m * (size_t)kp * 2;
-    const size_t need = a16_bytes + (size_t)m * 4;
+    if (g_num_cus == 0) {
+        int dev = 0, cus = 0;
+        DOE_HIP_CHECK(hipGetDevice(&dev));
+        DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        g_num_cus = cus > 0 ? cus : 256;
+    }
+    // Short prompts (few 128 x 128 tiles): K split over the grid so that
+    // tiles x splits reach about two workgroups per CU, at most 8 splits
+    // (their partial tiles are written and summed once more), each at least
+    // one Q4_K block of K.
+    const int64_t nchunk = kp / kBK;
+    const int64_t small_tiles = ((m + 127) / 128) * ((n + 127) / 128);
+    int64_t splits = 1;
+    if (!big && small_tiles < 2 * g_num_cus) {
+        splits = (2 * g_num_cus + small_tiles - 1) / small_tiles;
+        if (splits > 8) splits = 8;
+        if (splits > nchunk / 4) splits = nchunk / 4;
+        if (splits < 1) splits = 1;
+    }
+    const int64_t kps = (nchunk + splits - 1) / splits;
+    splits = (nchunk + kps - 1) / kps;
+    const size_t part_off = (a16_bytes + (size_t)m * 4 + 255) & ~(size_t)255;
+    const size_t need = splits > 1 ? part_off + (size_t)splits * m * n * 4 : a16_bytes + (size_t)m * 4;
     void *ws;
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -664,6 +715,8 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     g.Kp = (int)kp;
     g.nb = (int)((k + 255) / 256);
     g.nchunk = (int)(kp / kBK);
+    g.kps = (int)kps;
+    g.part = splits > 1 ? (float *)((char *)ws + part_off) : nullptr;
     const int bm = big ? 256 : 128, bn = big ? 256 : 128;
     g.tiles_m = (int)((m + bm - 1) / bm);
     g.tiles_n = (int)((n + bn - 1) / bn);
@@ -672,8 +725,15 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     if (big)
         hipLaunchKernelGGL(q4k_gemm_pipe_kernel, dim3((unsigned)tiles), dim3(256), 0, st, g);
     else
-        hipLaunchKernelGGL((q4k_gemm_kernel<2, 2>), dim3((unsigned)tiles), dim3(256), 0, st, g);
+        hipLaunchKernelGGL((q4k_gemm_kernel<2, 2>), dim3((unsigned)tiles, (unsigned)splits), dim3(256), 0, st, g);
     DOE_LAUNCH_CHECK("q4k_gemm_kernel");
+    if (splits > 1) {
+        const size_t mn = (size_t)m * (size_t)n;
+        size_t blocks = (mn / 4 + 255) / 256;
+        blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
+        hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g.part, c, mn, (int)splits);
+        DOE_LAUNCH_CHECK("sum_splits_kernel");
+    }
     return DOE_OK;
 }
 

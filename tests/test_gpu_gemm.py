@@ -47,6 +47,28 @@ def test_gemm_matches_oracle(dev, ora, m, n, k):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("m,n,k", [(128, 2304, 9216), (128, 4096, 2304), (17, 300, 2048), (128, 18432, 2304),
+                                   (3, 64, 1024)])
+def test_gemm_f32_prompt_shapes(dev, ora, m, n, k):
+    # the decoder's batched prompt: f32 activations, few 128 x 128 tiles, so K
+    # runs split over the grid (up to 8 partial tiles summed in split order);
+    # float64 reference over the dequantised weights
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    b = q4k.random_q4k(rng, n, k)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_q4k_gemm_f32(up(a), up(b), out, m, n, k)
+    got = out.download()
+    want = a.astype(np.float64) @ ora.q4k_dequant_rowwise(b, n, k).astype(np.float64).T
+    err = rel_l2(got, want)
+    print(f"[gemm f32 {m}x{n}x{k}] rel_l2 {err:.2e}", flush=True)
+    assert err <= TOL
+    # the same call twice gives the same bits (fixed split order, no atomics)
+    out2 = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_q4k_gemm_f32(up(a), up(b), out2, m, n, k)
+    assert np.array_equal(out2.download(), got)
+
+
 def test_gemm_prefill_config_sampled(dev, ora):
     # the 31B-class prefill shape: M=2048 tokens, K=5376, N=21504; the oracle
     # evaluates 2048 sampled entries (every row once, at a random column)
