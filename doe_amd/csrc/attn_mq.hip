@@ -97,9 +97,16 @@ struct MqLds {
     }
 };
 
-template <int D>
-__global__ __launch_bounds__(512) void attn_mq_kernel(MqArgs a) {
+// NTH = 64 HG threads.  A key block is staged as 16-byte pieces c = tid +
+// NTH i (key c % 32, dims 8 (c / 32) ..): up to eight pieces per thread are
+// fetched into registers for the next block while the current one is
+// computed, the rest (head_dim 512) just before it is staged.
+template <int D, int NTH>
+__global__ __launch_bounds__(NTH) void attn_mq_kernel(MqArgs a) {
     using Lds = MqLds<D>;
+    constexpr int PIECES = kKeys * (D / 8);
+    constexpr int PPT = (PIECES + NTH - 1) / NTH;
+    constexpr int PF = PPT < 8 ? PPT : 8;
     constexpr int QROW = Lds::QROW, KROW = Lds::KROW, VROW = Lds::VROW, PROW = Lds::PROW;
     constexpr int NT = D / 16;  // O tiles of 16 dims
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
@@ -110,7 +117,7 @@ __global__ __launch_bounds__(512) void attn_mq_kernel(MqArgs a) {
     _Float16 *ps = vt + (size_t)D * VROW;                     // [HG][16][PROW]
     float *qinv = reinterpret_cast<float *>(ps + (size_t)HG * 16 * PROW);  // [HG][16]
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthreads = blockDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g4 = lane >> 4, c16 = lane & 15;
     const int q0 = blockIdx.x * 16;
     const int kvh = blockIdx.y / (a.num_heads / a.num_kv_heads / HG);
@@ -202,23 +209,54 @@ __global__ __launch_bounds__(512) void attn_mq_kernel(MqArgs a) {
     const _Float16 *ql = qs + (size_t)(wave * 2 + 1) * 16 * QROW;
     _Float16 *pw = ps + (size_t)wave * 16 * PROW;
 
-    for (int p0 = (ulo / kKeys) * kKeys; p0 < uhi; p0 += kKeys) {
-        __syncthreads();  // every wave is done with the previous block
-        // stage K [32][D] and V^T [D][32]: 16-byte pieces of 8 dims
-        for (int c = tid; c < kKeys * (D / 8); c += nthreads) {
-            const int key = c / (D / 8), d0 = (c % (D / 8)) * 8;
+    // pieces [i0, i0 + n) of the block at p0: global -> registers -> LDS
+    auto fetch = [&](int p0, int i0, int n, h8 *kd, h8 *vd) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+            const int c = tid + (i0 + i) * NTH;
+            const int key = c % kKeys, d0 = (c / kKeys) * 8;
             const int p = p0 + key;
             h8 kv = h8{0, 0, 0, 0, 0, 0, 0, 0}, vv = kv;
-            if (p < L) {
+            if (c < PIECES && p < L) {
                 const long row = cache_row(a, p);
                 kv = *reinterpret_cast<const h8 *>(kb + row * a.row_stride + d0);
                 vv = *reinterpret_cast<const h8 *>(vb + row * a.row_stride + d0);
             }
-            *reinterpret_cast<h8 *>(ks + (size_t)key * KROW + d0) = kv;
+            kd[i] = kv;
+            vd[i] = vv;
+        }
+    };
+    auto put = [&](int i0, int n, const h8 *kd, const h8 *vd) __attribute__((always_inline)) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vt[(size_t)(d0 + e) * VROW + key] = vv[e];
+        for (int i = 0; i < n; ++i) {
+            const int c = tid + (i0 + i) * NTH;
+            if (c < PIECES) {
+                const int key = c % kKeys, d0 = (c / kKeys) * 8;
+                *reinterpret_cast<h8 *>(ks + (size_t)key * KROW + d0) = kd[i];
+                // consecutive lanes hold consecutive keys: each V^T row's
+                // writes land in consecutive halves
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vt[(size_t)(d0 + e) * VROW + key] = vd[i][e];
+            }
+        }
+    };
+    h8 kr[PF], vr[PF];
+    int p0 = (ulo / kKeys) * kKeys;
+    if (p0 < uhi) fetch(p0, 0, PF, kr, vr);
+    for (; p0 < uhi; p0 += kKeys) {
+        __syncthreads();  // every wave is done with the previous block
+        put(0, PF, kr, vr);
+        if constexpr (PPT > PF) {
+            // the rest in chunks of eight pieces (eight loads in flight each)
+#pragma unroll 1
+            for (int i0 = PF; i0 < PPT; i0 += 8) {
+                h8 k2[8], v2[8];
+                fetch(p0, i0, 8, k2, v2);
+                put(i0, 8, k2, v2);
+            }
         }
         __syncthreads();
+        if (p0 + kKeys < uhi) fetch(p0 + kKeys, 0, PF, kr, vr);  // in flight during this block
 
         // S = Q K^T: two 16-key tiles, Q hi and lo
         f32x4 s[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -291,12 +329,22 @@ int launch_mq(const MqArgs &a0, hipStream_t st) {
     if (hg > G) hg = G;
     a.heads_per_wg = hg;
     const size_t lds = MqLds<D>::bytes(hg);
-    static const hipError_t attr_rc = hipFuncSetAttribute((const void *)attn_mq_kernel<D>,
-                                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static const hipError_t attr_rc = [] {
+        hipError_t e = hipSuccess;
+        for (const void *f : {(const void *)attn_mq_kernel<D, 64>, (const void *)attn_mq_kernel<D, 128>,
+                              (const void *)attn_mq_kernel<D, 256>, (const void *)attn_mq_kernel<D, 512>})
+            if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        return e;
+    }();
     DOE_HIP_CHECK(attr_rc);
     DOE_REQUIRE(lds <= 160 * 1024, DOE_E_UNSUPPORTED, "attention needs %zu bytes of LDS", lds);
     const dim3 grid((unsigned)((a.query_len + 15) / 16), (unsigned)(a.num_kv_heads * (G / hg)), 1);
-    hipLaunchKernelGGL(attn_mq_kernel<D>, grid, dim3(64 * hg), lds, st, a);
+    switch (hg) {
+        case 1: hipLaunchKernelGGL((attn_mq_kernel<D, 64>), grid, dim3(64), lds, st, a); break;
+        case 2: hipLaunchKernelGGL((attn_mq_kernel<D, 128>), grid, dim3(128), lds, st, a); break;
+        case 4: hipLaunchKernelGGL((attn_mq_kernel<D, 256>), grid, dim3(256), lds, st, a); break;
+        default: hipLaunchKernelGGL((attn_mq_kernel<D, 512>), grid, dim3(512), lds, st, a); break;
+    }
     DOE_LAUNCH_CHECK("attn_mq_kernel");
     return DOE_OK;
 }
