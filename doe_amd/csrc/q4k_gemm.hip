@@ -200,6 +200,10 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
     constexpr int NQ = NBY / 16;     // 16-byte nibble loads per thread
     __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLdsRow];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * kLdsRow];
+    // 2^-sig of the tile's rows: the epilogue's stores never wait on a
+    // global load (cout may alias sig as far as the compiler knows, so each
+    // row's load would otherwise wait for the stores before it)
+    __shared__ float rowscale[BM];
 
     // tile order: XCD-contiguous ranges of an M-grouped raster
     const int T = g.tiles_m * g.tiles_n;
@@ -277,6 +281,7 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+    for (int r = tid; r < BM; r += 256) rowscale[r] = __builtin_amdgcn_ldexpf(1.0f, -g.sig[min(m0 + r, g.M - 1)]);
     const int kc0 = (int)blockIdx.y * g.kps, kc1 = min(g.nchunk, kc0 + g.kps);
     float *cout = gridDim.y > 1 ? g.part + (size_t)blockIdx.y * g.M * g.N : g.c;
     DOE_GEMM_LOAD_CHUNK(kc0);
@@ -312,9 +317,10 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m = m0 + wm * 32 * TM + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+            const int mt = wm * 32 * TM + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+            const int m = m0 + mt;
             if (m >= g.M) continue;
-            const float us = __builtin_amdgcn_ldexpf(1.0f, -g.sig[m]);
+            const float us = rowscale[mt];
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int n = n0 + wn * 32 * TN + j * 32 + lr;
