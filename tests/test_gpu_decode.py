@@ -426,3 +426,23 @@ def test_prefill_full_size(dev, ora):
     errs = _prefill_then_decode(dec, oracle, prompt, 2, s)
     print(f"[prefill 2B] logits rel_l2 {['%.1e' % e for e in errs]}", flush=True)
     assert max(errs) <= 1e-3
+
+
+def test_full_size_graph_trajectory_equals_eager(dev):
+    # the trajectory the bench times, at the 2B-class shape: a 128-token
+    # prompt as one batched pass, then 64 greedy steps replayed from graphs of
+    # 8 steps, token for token equal to the same steps launched eagerly
+    cfg = DecoderConfig(max_seq=128 + 64 + 1)
+    dec = Decoder(cfg)
+    dec.init_random(seed=2)
+    s = Stream()
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab, 128).astype(np.int32)
+    eager = dec.generate(prompt, 65, s, prefill=True)
+    dec.reset(prompt)
+    dec.step(s)  # allocates the attention workspace outside capture
+    s.synchronize()
+    g = dec.capture(s, 8)
+    out = dec.generate(prompt, 65, s, graph=g, steps_per_graph=8, prefill=True)
+    g.destroy()
+    assert out.tolist() == eager.tolist()
+    assert out[:128].tolist() == prompt.tolist()
