@@ -71,6 +71,7 @@ SIGNATURES: dict[str, list] = {
     "doe_q4k_gemv_attn_out": [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
     "doe_q4k_gemm": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "doe_q4k_gemm_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "doe_q8_0_gemm_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "doe_q4k_gemv": [_vp, _vp, _vp, _i64, _i64, _vp],
     "doe_q8_0_gemv": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
     "doe_q8_0_gemv_norm": [_vp, _vp, _vp, _i64, _i64, _vp, _f32, _i32, _vp, _vp],
@@ -93,7 +94,9 @@ SIGNATURES: dict[str, list] = {
     "doe_residual_add": [_vp, _vp, _vp, _i64, _vp],
     "doe_ple_modulate": [_vp, _vp, _vp, _i64, _f32, _vp],
     "doe_qkv_rope_kv_rows": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
+    "doe_qkv_rope_half_kv_rows": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
     "doe_geglu_pairs": [_vp, _vp, _i64, _vp],
+    "doe_geglu_halves": [_vp, _vp, _i64, _i64, _vp],
     "doe_argmax": [_vp, _i64, _vp, _vp, _vp],
     "doe_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i32, _vp],
     "doe_embed_gather": [_vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp],

@@ -120,6 +120,51 @@ __global__ __launch_bounds__(256) void rope_kv_rows_kernel(float *qkv, long row_
     }
 }
 
+// Rotate-half form of rope_kv_rows (the doe_rope pairing, i and i + D/2 of
+// each head): q and k heads rotated in place, k and v rows into the caches.
+__global__ __launch_bounds__(256) void rope_half_kv_rows_kernel(float *qkv, long row_stride, int tokens, int q_heads,
+                                                                int kv_heads, int head_dim,
+                                                                const float *__restrict__ freq, int start_pos,
+                                                                _Float16 *kc, _Float16 *vc, int max_seq) {
+#pragma clang fp contract(off)
+    const int half = head_dim >> 1, heads = q_heads + 2 * kv_heads;
+    const long total = (long)tokens * heads * half;
+    for (long gi = (long)blockIdx.x * 256 + threadIdx.x; gi < total; gi += (long)gridDim.x * 256) {
+        const int i = (int)(gi % half);
+        const long th = gi / half;
+        const int t = (int)(th / heads), hh = (int)(th % heads);
+        const int pos = start_pos + t;
+        float *base = qkv + (size_t)t * row_stride + (size_t)hh * head_dim;
+        const float x0 = base[i], x1 = base[i + half];
+        float r0 = x0, r1 = x1;
+        if (hh < q_heads + kv_heads) {
+            const float c = freq[((size_t)pos * half + i) * 2], sn = freq[((size_t)pos * half + i) * 2 + 1];
+            r0 = x0 * c - x1 * sn;
+            r1 = x0 * sn + x1 * c;
+            base[i] = r0;
+            base[i + half] = r1;
+        }
+        if (hh >= q_heads) {
+            const bool is_v = hh >= q_heads + kv_heads;
+            const int h = is_v ? hh - q_heads - kv_heads : hh - q_heads;
+            _Float16 *cache = is_v ? vc : kc;
+            const size_t ci = ((size_t)h * max_seq + pos) * head_dim + i;
+            cache[ci] = (_Float16)r0;
+            cache[ci + half] = (_Float16)r1;
+        }
+    }
+}
+
+// GeGLU over rows of [gate (n) | up (n)]: out[t][i] = gelu(gu[t][i]) * gu[t][n + i]
+__global__ __launch_bounds__(256) void geglu_halves_kernel(const float *__restrict__ gu, float *__restrict__ out,
+                                                           int rows, int n) {
+    const long total = (long)rows * n;
+    for (long g = (long)blockIdx.x * 256 + threadIdx.x; g < total; g += (long)gridDim.x * 256) {
+        const long t = g / n, i = g % n;
+        out[g] = doe_gelu_tanh_clamped(gu[t * 2 * n + i]) * gu[t * 2 * n + n + i];
+    }
+}
+
 // GeGLU over interleaved (gate, up) columns: out[i] = gelu(gu[2i]) * gu[2i+1]
 __global__ __launch_bounds__(256) void geglu_pairs_kernel(const float2 *__restrict__ gu, float *__restrict__ out,
                                                           long n) {
@@ -325,6 +370,40 @@ int doe_qkv_rope_kv_rows(float *qkv, int64_t tokens, int64_t row_stride, int64_t
                        (int)head_dim, freq_cis, (int)start_pos, (_Float16 *)key_cache, (_Float16 *)val_cache,
                        (int)max_seq_len);
     DOE_LAUNCH_CHECK("rope_kv_rows_kernel");
+    return DOE_OK;
+}
+
+int doe_qkv_rope_half_kv_rows(float *qkv, int64_t tokens, int64_t row_stride, int64_t num_heads,
+                              int64_t num_kv_heads, int64_t head_dim, const float *freq_cis, int64_t start_pos,
+                              uint16_t *key_cache, uint16_t *val_cache, int64_t max_seq_len, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(tokens >= 0 && num_heads >= 0 && num_kv_heads >= 0 && head_dim > 0 && (head_dim % 2) == 0 &&
+                    start_pos >= 0 && max_seq_len > 0,
+                DOE_E_INVALID, "bad rope rows shape");
+    DOE_REQUIRE(row_stride >= (num_heads + 2 * num_kv_heads) * head_dim, DOE_E_INVALID,
+                "row_stride %lld shorter than the q/k/v rows", (long long)row_stride);
+    DOE_REQUIRE(start_pos + tokens <= max_seq_len, DOE_E_INVALID, "positions %lld..%lld outside the %lld-row cache",
+                (long long)start_pos, (long long)(start_pos + tokens - 1), (long long)max_seq_len);
+    const long total = (long)tokens * (num_heads + 2 * num_kv_heads) * (head_dim / 2);
+    if (total == 0) return DOE_OK;
+    DOE_REQUIRE(qkv && freq_cis && (num_kv_heads == 0 || (key_cache && val_cache)), DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(rope_half_kv_rows_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, qkv,
+                       (long)row_stride, (int)tokens, (int)num_heads, (int)num_kv_heads, (int)head_dim, freq_cis,
+                       (int)start_pos, (_Float16 *)key_cache, (_Float16 *)val_cache, (int)max_seq_len);
+    DOE_LAUNCH_CHECK("rope_half_kv_rows_kernel");
+    return DOE_OK;
+}
+
+int doe_geglu_halves(const float *gate_up, float *output, int64_t rows, int64_t n, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(rows >= 0 && n >= 0 && n <= 0x3fffffff && rows <= 0x7fffffff, DOE_E_INVALID, "bad geglu shape");
+    if (rows == 0 || n == 0) return DOE_OK;
+    DOE_REQUIRE(gate_up && output, DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(geglu_halves_kernel, dim3(grid_for(rows * n)), dim3(256), 0, (hipStream_t)stream, gate_up,
+                       output, (int)rows, (int)n);
+    DOE_LAUNCH_CHECK("geglu_halves_kernel");
     return DOE_OK;
 }
 

@@ -19,6 +19,9 @@
 //     packed fma.  The relative error of w is ~2^-11, far inside the rel-L2
 //     1e-3 contract; a bf16 B (8 bits) would sit at ~1.1e-3.
 //
+// doe_q8_0_gemm_f32 runs the 128 x 128 kernel over Q8_0 rows (34-byte blocks
+// of an f16 scale and 32 int8 quants), dequantised to f16 the same way.
+//
 // Tiling: problems with at least 256 tiles of 256 x 256 use q4k_gemm_pipe_kernel
 // (four waves side by side in N, raw B blocks in LDS dequantised per wave,
 // software-pipelined); smaller ones use 128 x 128 tiles (2 x 2 waves of 64 x 64)
@@ -191,13 +194,18 @@ __device__ __forceinline__ void dequant_dword(uint32_t w, half2v dsc_lo, half2v 
 }
 
 // TM x TN 32x32 accumulators per wave, 2 x 2 waves: a (64 TM) x (64 TN) tile.
-template <int TM, int TN>
-__global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
+// FMT 0: B is row-wise Q4_K_M; FMT 1: B is row-wise Q8_0 (nb = ceil(K / 32)
+// blocks of 34 bytes: f16 d, 32 int8 q, weight d * q; blocks only 2-byte
+// aligned): the two threads of a B row each dequantise one block of the
+// chunk, w = RN_f16(d * q) (d * q is exact in f32).
+template <int TM, int TN, int FMT>
+__global__ __launch_bounds__(256) void quant_gemm_kernel(GemmArgs g) {
     constexpr int BM = 64 * TM, BN = 64 * TN;
     constexpr int GA = BM / 32;      // 16-byte A granules per thread per chunk
     constexpr int TPR = 256 / BN;    // threads per B row (1 or 2)
     constexpr int NBY = 32 / TPR;    // nibble bytes per thread per chunk (32 or 16)
     constexpr int NQ = NBY / 16;     // 16-byte nibble loads per thread
+    static_assert(FMT == 0 || TPR == 2, "Q8_0 staging: two threads per B row, one block each");
     __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLdsRow];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * kLdsRow];
     // 2^-sig of the tile's rows: the epilogue's stores never wait on a
@@ -226,6 +234,14 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
     // B: row tid / TPR, nibble bytes [boff, boff + NBY) of the chunk
     const int brow = tid / TPR, boff = (tid % TPR) * NBY;
     const uint8_t *brow_ptr = g.b + (size_t)min(n0 + brow, g.N - 1) * g.nb * DOE_Q4K_BLOCK_BYTES;
+    // Q8_0: buffer loads over the whole matrix, its size rounded up to a whole
+    // dword (the range check is per dword: the last block's last quants share
+    // a dword with up to two bytes past the matrix, which a 4-byte-aligned
+    // weight keeps on the same page); a block's 36-byte dword-aligned window
+    // read from an offset past the end reads zero
+    const __amdgpu_buffer_rsrc_t b8rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)g.b, (short)0, FMT == 1 ? (int)(((uint32_t)g.N * (uint32_t)g.nb * 34u + 3u) & ~3u) : 0, 0x00020000);
+    const uint32_t b8row = (uint32_t)min(n0 + brow, g.N - 1) * (uint32_t)g.nb;
     const _Float16 *arow_ptr[GA];
 #pragma unroll
     for (int i = 0; i < GA; ++i) {
@@ -234,21 +250,54 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs g) {
     }
 
     u32x4 ra[GA], rh, rq[NQ];
+    u32x4 r8a, r8b;  // Q8_0: the block's dword-aligned 36-byte window
+    uint32_t r8c, r8sh;
     // (macros, not lambdas: the staging arrays must stay in registers)
 #define DOE_GEMM_LOAD_CHUNK(KC)                                                                        \
     do {                                                                                               \
         _Pragma("unroll") for (int i = 0; i < GA; ++i)                                                 \
             ra[i] = *reinterpret_cast<const u32x4 *>(arow_ptr[i] + (KC) * kBK);                        \
-        const uint8_t *blk_ = brow_ptr + (size_t)((KC) >> 2) * DOE_Q4K_BLOCK_BYTES;                    \
-        rh = *reinterpret_cast<const u32x4 *>(blk_);                                                   \
-        _Pragma("unroll") for (int j = 0; j < NQ; ++j)                                                 \
-            rq[j] = *reinterpret_cast<const u32x4 *>(blk_ + 16 + 32 * ((KC) & 3) + boff + 16 * j);     \
+        if constexpr (FMT == 0) {                                                                      \
+            const uint8_t *blk_ = brow_ptr + (size_t)((KC) >> 2) * DOE_Q4K_BLOCK_BYTES;                \
+            rh = *reinterpret_cast<const u32x4 *>(blk_);                                               \
+            _Pragma("unroll") for (int j = 0; j < NQ; ++j)                                             \
+                rq[j] = *reinterpret_cast<const u32x4 *>(blk_ + 16 + 32 * ((KC) & 3) + boff + 16 * j); \
+        } else {                                                                                       \
+            const int bi_ = 2 * (KC) + (tid & 1);                                                      \
+            const uint32_t o_ = bi_ < g.nb ? (b8row + (uint32_t)bi_) * 34u : 0x80000000u;              \
+            const uint32_t al_ = o_ & ~3u;                                                             \
+            r8a = __builtin_amdgcn_raw_buffer_load_b128(b8rsrc, al_, 0, 0);                           \
+            r8b = __builtin_amdgcn_raw_buffer_load_b128(b8rsrc, al_ + 16u, 0, 0);                     \
+            r8c = __builtin_amdgcn_raw_buffer_load_b32(b8rsrc, al_ + 32u, 0, 0);                      \
+            r8sh = o_ & 2u;                                                                            \
+        }                                                                                              \
     } while (0)
 #define DOE_GEMM_STORE_CHUNK(BUF, KC)                                                                  \
     do {                                                                                               \
         _Pragma("unroll") for (int i = 0; i < GA; ++i) {                                               \
             const int gi = tid + 256 * i;                                                              \
             *reinterpret_cast<u32x4 *>(&As[BUF][(gi >> 3) * kLdsRow + (gi & 7) * 8]) = ra[i];          \
+        }                                                                                              \
+        if constexpr (FMT == 1) {                                                                      \
+            const uint32_t dw_[9] = {r8a.x, r8a.y, r8a.z, r8a.w, r8b.x, r8b.y, r8b.z, r8b.w, r8c};     \
+            const uint32_t sh_ = r8sh << 3; /* the block starts at byte 0 or 2 of the window */       \
+            const uint32_t sel_ = sh_ ? 0x07060504u : 0x05040302u;                                     \
+            const float d8_ = doe_half_bits_to_float(__builtin_amdgcn_ubfe(dw_[0], sh_, 16));          \
+            uint32_t hv_[16];                                                                          \
+            _Pragma("unroll") for (int j = 0; j < 8; ++j) {                                            \
+                const uint32_t u_ = __builtin_amdgcn_perm(dw_[j + 1], dw_[j], sel_);                   \
+                const half2v w01 = {(_Float16)(d8_ * (float)(int8_t)(u_ & 0xffu)),                     \
+                                    (_Float16)(d8_ * (float)(int8_t)((u_ >> 8) & 0xffu))};             \
+                const half2v w23 = {(_Float16)(d8_ * (float)(int8_t)((u_ >> 16) & 0xffu)),             \
+                                    (_Float16)(d8_ * (float)(int8_t)(u_ >> 24))};                      \
+                hv_[2 * j] = as_u32(w01);                                                              \
+                hv_[2 * j + 1] = as_u32(w23);                                                          \
+            }                                                                                          \
+            _Float16 *bl8_ = &Bs[BUF][brow * kLdsRow + (tid & 1) * 32];                                \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j)                                              \
+                *reinterpret_cast<u32x4 *>(bl8_ + 8 * j) =                                             \
+                    u32x4{hv_[4 * j], hv_[4 * j + 1], hv_[4 * j + 2], hv_[4 * j + 3]};                 \
+            break;                                                                                     \
         }                                                                                              \
         uint32_t scp_, mnp_;                                                                           \
         scale_min_pair(rh.y, rh.z, rh.w, (KC) & 3, scp_, mnp_);                                        \
@@ -640,8 +689,9 @@ void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
 int g_num_cus = 0;
 
+// fmt 0: B Q4_K_M rows; fmt 1: B Q8_0 rows (small-tile kernel only)
 int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m, int64_t n, int64_t k,
-              doe_stream_t stream) {
+              doe_stream_t stream, int fmt = 0) {
     const uint16_t *a_bf16 = a_f32 ? nullptr : (const uint16_t *)a;
     int rc = doe::require_init();
     if (rc) return rc;
@@ -654,12 +704,15 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
         return doe::fill_bytes_async(c, 0, (size_t)m * (size_t)n * sizeof(float), st);
     }
     DOE_REQUIRE(a && b_q4k, DOE_E_INVALID, "null pointer");
-    DOE_REQUIRE(((uintptr_t)b_q4k & 15) == 0, DOE_E_INVALID, "weight must be 16-byte aligned");
+    DOE_REQUIRE(((uintptr_t)b_q4k & (fmt ? 3 : 15)) == 0, DOE_E_INVALID, "weight must be %d-byte aligned",
+                fmt ? 4 : 16);
+    DOE_REQUIRE(!fmt || (uint64_t)n * (uint64_t)((k + 31) / 32) * 34u < (1ull << 31), DOE_E_UNSUPPORTED,
+                "Q8_0 weight of %lld rows x %lld columns exceeds 2 GiB", (long long)n, (long long)k);
     DOE_REQUIRE(m <= (1 << 24) && n <= (1 << 24) && k <= (1 << 20) && m * n <= ((int64_t)1 << 40),
                 DOE_E_UNSUPPORTED, "q4k_gemm shape too large (m=%lld n=%lld k=%lld)", (long long)m,
                 (long long)n, (long long)k);
     // 256 x 256 tiles once there are enough of them to fill the CUs, else 128 x 128
-    const bool big = m >= 256 && n >= 256 && ((m + 255) / 256) * ((n + 255) / 256) >= 256;
+    const bool big = fmt == 0 && m >= 256 && n >= 256 && ((m + 255) / 256) * ((n + 255) / 256) >= 256;
     // the large-tile kernel streams whole Q4_K blocks: A padded to 256 nb columns
     const int64_t kp = big ? (k + 255) / 256 * 256 : (k + kBK - 1) / kBK * kBK;
     const size_t a16_bytes = (size_t)m * (size_t)kp * 2;
@@ -719,7 +772,7 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     g.M = (int)m;
     g.N = (int)n;
     g.Kp = (int)kp;
-    g.nb = (int)((k + 255) / 256);
+    g.nb = (int)(fmt ? (k + 31) / 32 : (k + 255) / 256);
     g.nchunk = (int)(kp / kBK);
     g.kps = (int)kps;
     g.part = splits > 1 ? (float *)((char *)ws + part_off) : nullptr;
@@ -730,9 +783,11 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     DOE_REQUIRE(tiles <= 0x7fffffff, DOE_E_UNSUPPORTED, "too many tiles");
     if (big)
         hipLaunchKernelGGL(q4k_gemm_pipe_kernel, dim3((unsigned)tiles), dim3(256), 0, st, g);
+    else if (fmt)
+        hipLaunchKernelGGL((quant_gemm_kernel<2, 2, 1>), dim3((unsigned)tiles, (unsigned)splits), dim3(256), 0, st, g);
     else
-        hipLaunchKernelGGL((q4k_gemm_kernel<2, 2>), dim3((unsigned)tiles, (unsigned)splits), dim3(256), 0, st, g);
-    DOE_LAUNCH_CHECK("q4k_gemm_kernel");
+        hipLaunchKernelGGL((quant_gemm_kernel<2, 2, 0>), dim3((unsigned)tiles, (unsigned)splits), dim3(256), 0, st, g);
+    DOE_LAUNCH_CHECK("quant_gemm_kernel");
     if (splits > 1) {
         const size_t mn = (size_t)m * (size_t)n;
         size_t blocks = (mn / 4 + 255) / 256;
@@ -755,6 +810,11 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
 int doe_q4k_gemm_f32(const float *a, const void *b_q4k, float *c, int64_t m, int64_t n, int64_t k,
                      doe_stream_t stream) {
     return gemm_impl(a, true, b_q4k, c, m, n, k, stream);
+}
+
+int doe_q8_0_gemm_f32(const float *a, const void *b_q8_0, float *c, int64_t m, int64_t n, int64_t k,
+                      doe_stream_t stream) {
+    return gemm_impl(a, true, b_q8_0, c, m, n, k, stream, 1);
 }
 
 }  // extern "C"

@@ -403,9 +403,9 @@ class Decoder:
 
     # ---- prompt ----------------------------------------------------------------
     def can_prefill(self) -> bool:
-        """Batched prompts run for uniform Q4_K models (no per-layer
+        """Batched prompts run for uniform Q4_K and Q8_0 models (no per-layer
         embeddings, shared-KV layers or second head_dim)."""
-        return (self.cfg.weight_format == "q4k" and not self.ple and len(set(self.head_dims)) == 1
+        return (self.cfg.weight_format in ("q4k", "q8_0") and not self.ple and len(set(self.head_dims)) == 1
                 and self.kv_sources == tuple(range(self.cfg.layers)))
 
     def _prefill_buffers(self):
@@ -429,13 +429,15 @@ class Decoder:
         cache write, causal attention of the whole prompt, o_proj +
         attn_residual, post_attn_norm, gate/up_proj, activation, down_proj +
         ffn_residual), then the last token's final norm + lm_head + sample.
+        Q4_K layers run the Q4_K GEMM and the interleaved-pair RoPE, Q8_0
+        layers the Q8_0 GEMM and the rotate-half RoPE of their decode step.
         Leaves the decoder where teacher-forced decode steps over the prompt
         would: cache rows 0..P-1 written, the first new token in ids[P],
         state = (P, P + 1, P, token)."""
         from .execution import UnsupportedStep
 
         if not self.can_prefill():
-            raise UnsupportedStep("batched prompts need a uniform Q4_K model")
+            raise UnsupportedStep("batched prompts need a uniform Q4_K or Q8_0 model")
         c = self.cfg
         prompt = np.asarray(prompt, np.int32)
         P = int(prompt.size)
@@ -448,22 +450,32 @@ class Decoder:
         off = c.norm_weight_offset
         ids = self.ids.view(0, P * 4, np.int32)
         ops.embed(self.embed, ids, b["x"], P, c.vocab, c.hidden, c.embed_scale, stream=stream)
+        # Q4_K layers hold q/k rows as interleaved rotation pairs and gate/up
+        # rows interleaved; Q8_0 layers hold heads in order (rotate-half
+        # RoPE) and the gate rows before the up rows
+        q8 = c.weight_format == "q8_0"
+        gemm = ops.matmul_q8_0_gemm_f32 if q8 else ops.matmul_q4k_gemm_f32
+        rope_rows = ops.qkv_rope_half_kv_rows if q8 else ops.qkv_rope_kv_rows
         for li, L in enumerate(self.layers):
             ops.rmsnorm(b["x"], L.norm_attn, b["xn"], P, c.hidden, c.eps, weight_offset=off, stream=stream)
-            ops.matmul_q4k_gemm_f32(b["xn"], L.wqkv, b["qkv"], P, c.qkv_rows, c.hidden, stream=stream)
-            ops.qkv_rope_kv_rows(b["qkv"], P, c.qkv_rows, c.heads, c.kv_heads, hd, self.freq_by_layer[li], 0,
-                                 L.k_cache, L.v_cache, c.max_seq, stream=stream)
+            gemm(b["xn"], L.wqkv, b["qkv"], P, c.qkv_rows, c.hidden, stream=stream)
+            freq = self.freq_cis if q8 else self.freq_by_layer[li]  # the Q8_0 decode step's table
+            rope_rows(b["qkv"], P, c.qkv_rows, c.heads, c.kv_heads, hd, freq, 0, L.k_cache, L.v_cache, c.max_seq,
+                      stream=stream)
             ops.attention_prefill_f16kv(b["qkv"], L.k_cache, L.v_cache, b["att"], num_heads=c.heads,
                                         num_kv_heads=c.kv_heads, head_dim=hd, query_len=P, kv_len=P,
                                         kv_stride=c.max_seq, start_pos=0, scale=1.0 / math.sqrt(hd),
                                         softcap=c.attn_softcap, sliding_window=self.attn_windows[li],
                                         q_row_stride=c.qkv_rows, stream=stream)
-            ops.matmul_q4k_gemm_f32(b["att"], L.wo, b["t"], P, c.hidden, c.q_dim, stream=stream)
+            gemm(b["att"], L.wo, b["t"], P, c.hidden, c.q_dim, stream=stream)
             ops.residual(b["t"], b["x"], b["x"], P * c.hidden, stream=stream)
             ops.rmsnorm(b["x"], L.norm_ffn, b["xn"], P, c.hidden, c.eps, weight_offset=off, stream=stream)
-            ops.matmul_q4k_gemm_f32(b["xn"], L.wgu, b["gu"], P, 2 * c.ffn, c.hidden, stream=stream)
-            ops.geglu_pairs(b["gu"], b["h"], P * c.ffn, stream=stream)
-            ops.matmul_q4k_gemm_f32(b["h"], L.wd, b["t"], P, c.hidden, c.ffn, stream=stream)
+            gemm(b["xn"], L.wgu, b["gu"], P, 2 * c.ffn, c.hidden, stream=stream)
+            if q8:
+                ops.geglu_halves(b["gu"], b["h"], P, c.ffn, stream=stream)
+            else:
+                ops.geglu_pairs(b["gu"], b["h"], P * c.ffn, stream=stream)
+            gemm(b["h"], L.wd, b["t"], P, c.hidden, c.ffn, stream=stream)
             ops.residual(b["t"], b["x"], b["x"], P * c.hidden, stream=stream)
         last = b["x"].view((P - 1) * c.hidden * 4, c.hidden * 4, np.float32)
         nparts = ops.lm_head_sample(self.lm_head, last, c.vocab, c.hidden, self.argmax_parts,

@@ -98,6 +98,41 @@ def geglu_pairs(gate_up: DeviceBuffer, output: DeviceBuffer, n: int, stream=None
     _lib.call("doe_geglu_pairs", _p(gate_up), _p(output), n, _stream_ptr(stream))
 
 
+def qkv_rope_half_kv_rows(qkv: DeviceBuffer, tokens: int, row_stride: int, num_heads: int, num_kv_heads: int,
+                          head_dim: int, freq_cis: DeviceBuffer, start_pos: int, key_cache: DeviceBuffer | None,
+                          val_cache: DeviceBuffer | None, max_seq_len: int, stream=None) -> None:
+    """Prompt rope_q / rope_k (rotate-half pairs, as ``rope``) + cache write
+    over `tokens` rows of [q heads | k heads | v heads]."""
+    if tokens:
+        _need(qkv, ((tokens - 1) * row_stride + (num_heads + 2 * num_kv_heads) * head_dim) * 4, "qkv")
+    _need(freq_cis, max_seq_len * head_dim * 4, "freq_cis")
+    kc = vc = C.c_void_p(None)
+    if num_kv_heads:
+        _need(key_cache, num_kv_heads * max_seq_len * head_dim * 2, "key_cache")
+        _need(val_cache, num_kv_heads * max_seq_len * head_dim * 2, "val_cache")
+        kc, vc = _p(key_cache), _p(val_cache)
+    _lib.call("doe_qkv_rope_half_kv_rows", _p(qkv), tokens, row_stride, num_heads, num_kv_heads, head_dim,
+              _p(freq_cis), start_pos, kc, vc, max_seq_len, _stream_ptr(stream))
+
+
+def geglu_halves(gate_up: DeviceBuffer, output: DeviceBuffer, rows: int, n: int, stream=None) -> None:
+    """``gelu_gated`` over rows of [gate (n) | up (n)]: output[t][i] =
+    gelu(gate_up[t][i]) * gate_up[t][n + i]."""
+    _need(gate_up, rows * 2 * n * 4, "gate_up")
+    _need(output, rows * n * 4, "output")
+    _lib.call("doe_geglu_halves", _p(gate_up), _p(output), rows, n, _stream_ptr(stream))
+
+
+def matmul_q8_0_gemm_f32(a: DeviceBuffer, weight: DeviceBuffer, output: DeviceBuffer, m: int, n: int, k: int,
+                         stream=None) -> None:
+    """``matmul`` with quantFormat ``q8_0`` at M > 1: output f32 [m][n] =
+    a f32 [m][k] @ dequant(weight)[n][k]^T (weights rounded to f16 once)."""
+    _need(weight, n * _q8_0.row_bytes(k), "weight")
+    _need(a, m * k * 4, "a")
+    _need(output, m * n * 4, "output")
+    _lib.call("doe_q8_0_gemm_f32", _p(a), _p(weight), _p(output), m, n, k, _stream_ptr(stream))
+
+
 def matmul_q8_0(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int,
                 residual: DeviceBuffer | None = None, stream=None, *, norm_weight: DeviceBuffer | None = None,
                 norm_eps: float = 1e-6, norm_weight_offset: bool = False) -> None:

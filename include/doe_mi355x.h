@@ -164,6 +164,12 @@ int doe_q4k_gemm(const uint16_t *a_bf16, const void *b_q4k, float *c, int64_t m,
  * the same matrix-core GEMM; the same workspace rule. */
 int doe_q4k_gemm_f32(const float *a, const void *b_q4k, float *c, int64_t m, int64_t n, int64_t k,
                      doe_stream_t stream);
+/* The same GEMM over Q8_0 rows (the `matmul` op with quantFormat q8_0 at
+ * M > 1, emit_csl_exec_v1.zig:279-284; block csl_spec.zig:121-153: 34 bytes
+ * of f16 d and 32 int8 q, weight d * q, rows of ceil(k / 32) blocks, the
+ * weight 4-byte aligned and under 2 GiB). */
+int doe_q8_0_gemm_f32(const float *a, const void *b_q8_0, float *c, int64_t m, int64_t n, int64_t k,
+                      doe_stream_t stream);
 
 /* Symmetric int4 group-32 GEMV, batch m in 1..8: y[b][i] = sum_k
  * (q[i][k] - 8) * s[i][k/32] * x[b][k].  w_u4: eight nibbles per u32, element
@@ -386,6 +392,18 @@ int doe_qkv_rope_kv_rows(float *qkv, int64_t tokens, int64_t row_stride, int64_t
                          int64_t num_kv_heads, int64_t head_dim, const float *freq_cis,
                          int64_t start_pos, uint16_t *key_cache, uint16_t *val_cache,
                          int64_t max_seq_len, doe_stream_t stream);
+/* doe_qkv_rope_kv_rows for projections in head order (rows [q heads | k heads
+ * | v heads], each head_dim wide): the rotate-half pairs (i, i + head_dim/2)
+ * of doe_rope, with the same arithmetic, for every prompt row; k and v rows
+ * into the caches [num_kv_heads][max_seq_len][head_dim]. */
+int doe_qkv_rope_half_kv_rows(float *qkv, int64_t tokens, int64_t row_stride, int64_t num_heads,
+                              int64_t num_kv_heads, int64_t head_dim, const float *freq_cis,
+                              int64_t start_pos, uint16_t *key_cache, uint16_t *val_cache,
+                              int64_t max_seq_len, doe_stream_t stream);
+/* GeGLU over rows of [gate (n) | up (n)] (the `activation` step of a prompt):
+ * out[t][i] = gelu_tanh(gate[t][i]) * up[t][i], gelu_gated.wgsl per row. */
+int doe_geglu_halves(const float *gate_up, float *output, int64_t rows, int64_t n,
+                     doe_stream_t stream);
 /* GeGLU over interleaved (gate, up) pairs: out[i] = gelu_tanh(gate_up[2i]) *
  * gate_up[2i + 1] (gelu_gated.wgsl:1-14; the activation step of a prompt
  * whose gate/up projection rows are interleaved). */

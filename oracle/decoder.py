@@ -47,6 +47,8 @@ class OracleDecoder:
         self.lm_head = dec.lm_head.download()
         self.nf = dec.norm_final.download()
         self.windows = dec.attn_windows
+        self.f16_operands = False
+        self._f16w = {}
         self.ple = dec.ple
         if self.ple:
             self.ple_table = dec.ple_table.download()
@@ -54,9 +56,43 @@ class OracleDecoder:
             self.ple_norm = dec.ple_norm.download()
 
     def gemv(self, w, x, n, k):
+        if self.f16_operands:
+            # the batched prompt's GEMM (q4k_gemm.hip): activation and
+            # dequantized weight each rounded to f16 (round to nearest even),
+            # their products exact in f32, accumulated in f32
+            wh = self._f16_weights(w, n, k).astype(np.float32)
+            return wh @ np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
         if self.cfg.weight_format == "q8_0":
             return ora.q8_0_gemv(w, x, n, k)
         return ora.q4k_gemv(w, x, n, k)
+
+    def _attn_p_f16(self, q, kc, vc, hd, n, window):
+        """The batched prompt's attention (attn_mq.hip) for a prompt within
+        one 32-key block: exact scores (Q is split hi/lo there), the
+        probabilities exp2(x - max) rounded to f16 and normalised by their
+        own sum; the window and softcap of ora_attn_decode."""
+        c = self.cfg
+        G = c.heads // c.kv_heads
+        lo = n - window if 0 < window <= n - 1 else 0
+        out = np.zeros((c.heads, hd), np.float32)
+        qh = np.asarray(q, np.float64).reshape(c.heads, hd)
+        for h in range(c.heads):
+            kk = kc[h // G, lo:n].astype(np.float64)
+            vv = vc[h // G, lo:n].astype(np.float64)
+            sc = (kk @ qh[h]) / math.sqrt(hd)
+            if c.attn_softcap > 0:
+                sc = np.tanh(sc / c.attn_softcap) * c.attn_softcap
+            x = sc * math.log2(math.e)
+            p = np.exp2(x - x.max()).astype(np.float16).astype(np.float64)
+            out[h] = (p @ vv) / p.sum()
+        return out.reshape(-1)
+
+    def _f16_weights(self, w, n, k):
+        key = id(w)
+        if key not in self._f16w:
+            deq = ora.q8_0_dequant(w, n, k) if self.cfg.weight_format == "q8_0" else ora.q4k_dequant_rowwise(w, n, k)
+            self._f16w[key] = deq.astype(np.float16)
+        return self._f16w[key]
 
     def ple_inputs(self, token: int, x: np.ndarray) -> np.ndarray:
         """Per-layer inputs [layers][P]: (rmsnorm_P(W_proj x / sqrt(hidden)) +
@@ -70,7 +106,19 @@ class OracleDecoder:
         u = np.add(pn, e, dtype=np.float32) * np.float32(2.0 ** -0.5)
         return u.astype(np.float32).reshape(c.layers, P)
 
-    def step(self, pos: int, token: int) -> np.ndarray:
+    def step(self, pos: int, token: int, f16_operands: bool = False) -> np.ndarray:
+        """One decode step.  With `f16_operands` the step models the batched
+        prompt's precision: the layer projections round their operands to f16
+        as its GEMMs do, and attention rounds its probabilities to f16 (for a
+        prompt of at most 32 tokens, one key block); the lm_head and
+        per-layer-embedding GEMVs stay f32."""
+        self.f16_operands = f16_operands
+        try:
+            return self._step(pos, token)
+        finally:
+            self.f16_operands = False
+
+    def _step(self, pos: int, token: int) -> np.ndarray:
         c = self.cfg
         off = c.norm_weight_offset
         x = ora.embed_gather(self.embed, np.array([token], np.int32), c.embed_scale)[0]
@@ -86,9 +134,12 @@ class OracleDecoder:
                 k = qk[L["q_dim"]:]
                 v = qkv[L["q_dim"] + L["kv_dim"]:]
                 ora.kv_write(k, v, L["kc"], L["vc"], c.kv_heads, c.max_seq, hd, pos)
-            attn = ora.attn_decode(qk[: L["q_dim"]], src["kc"], src["vc"], c.heads, c.kv_heads, hd, pos + 1,
-                                   c.max_seq, 1.0 / math.sqrt(hd), softcap=c.attn_softcap,
-                                   sliding_window=self.windows[li]).reshape(-1)
+            if self.f16_operands:
+                attn = self._attn_p_f16(qk[: L["q_dim"]], src["kc"], src["vc"], hd, pos + 1, self.windows[li])
+            else:
+                attn = ora.attn_decode(qk[: L["q_dim"]], src["kc"], src["vc"], c.heads, c.kv_heads, hd, pos + 1,
+                                       c.max_seq, 1.0 / math.sqrt(hd), softcap=c.attn_softcap,
+                                       sliding_window=self.windows[li]).reshape(-1)
             x = ora.residual(self.gemv(L["wo"], attn, c.hidden, L["q_dim"]), x)
             xn2 = ora.rmsnorm(x, L["n2"], c.eps, off)
             gu = self.gemv(L["wgu"], xn2, 2 * c.ffn, c.hidden)

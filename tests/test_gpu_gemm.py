@@ -69,6 +69,29 @@ def test_gemm_f32_prompt_shapes(dev, ora, m, n, k):
     assert np.array_equal(out2.download(), got)
 
 
+@pytest.mark.parametrize("m,n,k", [(5, 77, 129), (128, 2304, 9216), (17, 300, 2048), (64, 1000, 64),
+                                   (130, 257, 2304), (1, 3, 32)])
+def test_q8_0_gemm_f32(dev, ora, m, n, k):
+    # Q8_0 rows (34-byte blocks, 2-byte aligned; a K that is no multiple of 32
+    # zero-pads the last block) through the 128 x 128 kernel with its K split;
+    # float64 reference over the oracle's dequantised rows
+    from doe_amd import q8_0
+
+    rng = np.random.default_rng(m * 3 + n + k)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    b = q8_0.random_q8_0(rng, n, k)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_q8_0_gemm_f32(up(a), up(b), out, m, n, k)
+    got = out.download()
+    want = a.astype(np.float64) @ ora.q8_0_dequant(b, n, k).astype(np.float64).T
+    err = rel_l2(got, want)
+    print(f"[q8_0 gemm {m}x{n}x{k}] rel_l2 {err:.2e}", flush=True)
+    assert err <= TOL
+    # rows of the GEMM are the M = 1 GEMV's rows (same blocks, f16-rounded weights)
+    y0 = ora.q8_0_gemv(b, a[0], n, k)
+    assert rel_l2(got[0], y0) <= TOL
+
+
 def test_gemm_prefill_config_sampled(dev, ora):
     # the 31B-class prefill shape: M=2048 tokens, K=5376, N=21504; the oracle
     # evaluates 2048 sampled entries (every row once, at a random column)

@@ -69,6 +69,47 @@ def test_geglu_and_residual(dev, ora):
     assert np.array_equal(out.download(), ora.residual(g, u))
 
 
+def test_rope_half_kv_rows_equals_rope_and_kv_write(dev, ora):
+    # the prompt-row form in head order against doe_rope (same rotate-half
+    # pairing and arithmetic) token by token and doe_kv_write: bit-exact
+    rng = np.random.default_rng(31)
+    tokens, hq, hkv, d, max_seq, start = 5, 4, 2, 64, 16, 3
+    table = ora.rope_table(max_seq, d, 10000.0)
+    stride = (hq + 2 * hkv) * d + 8
+    qkv = rng.standard_normal((tokens, stride)).astype(np.float32)
+    buf = up(qkv)
+    kc = DeviceBuffer.from_array(np.zeros((hkv, max_seq, d), np.float16))
+    vc = DeviceBuffer.from_array(np.zeros((hkv, max_seq, d), np.float16))
+    ops.qkv_rope_half_kv_rows(buf, tokens, stride, hq, hkv, d, up(table), start, kc, vc, max_seq)
+    got = buf.download()
+    kref = np.zeros((hkv, max_seq, d), np.float16)
+    vref = np.zeros((hkv, max_seq, d), np.float16)
+    for t in range(tokens):
+        qk = qkv[t, : (hq + hkv) * d]
+        want = ora.rope(qk, table, 1, hq + hkv, d, start + t)
+        assert np.array_equal(got[t, : (hq + hkv) * d], want), t
+        assert np.array_equal(got[t, (hq + hkv) * d:], qkv[t, (hq + hkv) * d:]), t  # v and padding untouched
+        kref[:, start + t] = want[hq * d:].reshape(hkv, d).astype(np.float16)
+        vref[:, start + t] = qkv[t, (hq + hkv) * d: (hq + 2 * hkv) * d].reshape(hkv, d).astype(np.float16)
+    assert np.array_equal(kc.download(), kref)
+    assert np.array_equal(vc.download(), vref)
+
+
+def test_geglu_halves(dev, ora):
+    rng = np.random.default_rng(32)
+    rows, n = 7, 1000
+    gu = (rng.standard_normal((rows, 2 * n)) * 4).astype(np.float32)
+    out = DeviceBuffer.empty((rows, n), np.float32)
+    ops.geglu_halves(up(gu), out, rows, n)
+    want = np.stack([ora.geglu(gu[t, :n], gu[t, n:]) for t in range(rows)])
+    # the kernel runs the per-row gelu_gated kernel's arithmetic
+    single = DeviceBuffer.empty((n,), np.float32)
+    ops.gelu_gated(up(gu[3, :n]), up(gu[3, n:]), single, n)
+    got = out.download()
+    assert np.array_equal(got[3], single.download())
+    assert rel_l2(got, want) < 1e-6
+
+
 def test_argmax(dev, ora, known_answers):
     ws = DeviceBuffer(8192)
     tok = DeviceBuffer.empty((1,), np.int32)
