@@ -752,37 +752,68 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
     }
 }
 
-// Streaming form of the matrix-core kernel, for GEMVs of more 16-row groups
-// than one resident round: a persistent workgroup of one wave per Q4_K block
-// (nb <= 16) walks row groups blockIdx.x, + gridDim.x, ...  A wave's block,
-// and so its activation image, is the same in every group: it is staged once.
-// Two groups' weight loads stay in flight (the next one's and the one after,
-// issued as soon as a group's bytes are regrouped into LDS), and the row sums
-// wait in LDS until the walk ends: the loop issues no global store, so no
-// write sits in the in-order vmcnt queue ahead of a weight load.  Per group:
-// regroup, 8 MFMAs, the scale formula, one barrier for the cross-wave sum.
-constexpr int kStreamMaxGroups = 32;  // row groups per workgroup (LDS row sums)
-constexpr int kStreamWaveLds = 16 * kMfmaRowBytes + kMfmaAImgDwords * 4;
+// Streaming form of the matrix-core kernel, for GEMVs of many more 16-row
+// groups than CUs: a persistent workgroup of one wave per Q4_K block (nb <=
+// 16) walks a contiguous range of row groups.  A wave's block, and so its
+// activation image, is the same in every group: it is staged once.  The
+// weights go straight from memory into a ring of D LDS slots per wave
+// (global_load_lds_dwordx4: lane i's 16 bytes land at slot + 16 i, so granule
+// q of a unit -- row q / 9, piece q % 9 -- sits at row * 144 + piece * 16,
+// the row layout the MFMA operands are read from, bank-conflict free at that
+// stride), so D units per wave stay in flight without holding registers.
+// The compiler does not order LDS reads after these loads: each slot is read
+// after an explicit vmcnt wait for its three loads (every unit is exactly
+// three load instructions, issued unconditionally -- past the range, the last
+// group again -- and nothing else reads memory in the walk).  No wave waits
+// for another inside the walk: each writes its per-group row partials to
+// LDS, and one barrier at the end precedes the cross-wave sums and the
+// epilogues.  Measured at 65536 x 2304: 22.8 us against 27.8 for the
+// one-shot kernel on the same box, whose workgroups leave their slot empty
+// for 1.3-2 us between one workgroup's end and the next one's start.  (One
+// ring slot per workgroup, filled with linear 1 KB loads and read after a
+// per-group barrier, measured 25.0 us.)
+constexpr int kStreamMaxGroups = 16;  // row groups per workgroup (LDS row partials)
+constexpr int kStreamMinGroupsPerCu = 8;  // automatic choice: at least 8 row groups per CU
+constexpr int kStreamUnitBytes = 16 * DOE_Q4K_BLOCK_BYTES;  // 16 rows x one block
+constexpr int kStreamLdsMax = 160 * 1024;                  // one workgroup per CU
 
-size_t gemv_stream_lds_bytes(int nwaves) {
-    return (size_t)nwaves * kStreamWaveLds + (size_t)(2 * 16 + 1) * nwaves * 4 + (size_t)kStreamMaxGroups * 16 * 4;
+size_t gemv_stream_lds_bytes(int nwaves, int depth) {
+    return (size_t)nwaves * ((size_t)depth * kStreamUnitBytes + kMfmaAImgDwords * 4) +
+           (size_t)kStreamMaxGroups * 16 * nwaves * 4 + (size_t)nwaves * 4;
 }
 
-template <int PRO, int XV>
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    // vmcnt N (low 4 bits at [3:0], high 2 at [15:14]), expcnt and lgkmcnt
+    // not waited on; the builtin (unlike inline asm) updates the compiler's
+    // own count, and the empty asm keeps LDS reads from moving above it
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+    __asm__ volatile("" ::: "memory");
+}
+
+template <int PRO, int XV, int D>
 __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__restrict__ w, const float *x,
                                                                float *__restrict__ y, int n, int k, int nb,
                                                                int ngroups, GemvFusion fz) {
     constexpr bool NORM = PRO == 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-    uint8_t *wimg = lds + wave * kStreamWaveLds;
-    uint32_t *aimg = reinterpret_cast<uint32_t *>(wimg + 16 * kMfmaRowBytes);
-    float *red = reinterpret_cast<float *>(lds + nwaves * kStreamWaveLds);  // [2][16][nwaves]
-    float *ssq = red + 2 * 16 * nwaves;                                      // [nwaves]
-    float *rsum = ssq + nwaves;                                              // [kStreamMaxGroups][16]
-    const int b = wave, G = gridDim.x;
+    uint8_t *ring = lds + (size_t)wave * D * kStreamUnitBytes;                        // [D][16 rows][144]
+    uint32_t *aimg = reinterpret_cast<uint32_t *>(lds + (size_t)nwaves * D * kStreamUnitBytes +
+                                                  (size_t)wave * kMfmaAImgDwords * 4);
+    float *rpart = reinterpret_cast<float *>(lds + (size_t)nwaves * (D * kStreamUnitBytes + kMfmaAImgDwords * 4));
+    float *ssq = rpart + kStreamMaxGroups * 16 * nwaves;  // [nwaves]
+    const int b = wave;
+    // this workgroup's groups [g0, g1): a balanced contiguous split (the host
+    // keeps g1 - g0 <= kStreamMaxGroups)
+    const int g0 = (int)(((int64_t)blockIdx.x * ngroups) / gridDim.x);
+    const int g1 = (int)(((int64_t)blockIdx.x + 1) * ngroups / gridDim.x);
+    const int my = g1 - g0;
+    const int glast = min(max(g1 - 1, g0), ngroups - 1);
 
-    // Activation (and norm weight) loads first.
+    // Activation (and norm weight) loads first; they are waited on (vmcnt 0)
+    // before the ring's first loads are issued.
     float v[4], nwv[4];
     const int e = b * 256 + lane * 4;
     if (XV) {
@@ -799,22 +830,25 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
 #pragma unroll
         for (int j = 0; j < 4; ++j) nwv[j] = fz.norm_w[min(e + j, k - 1)];
     }
-    __asm__ volatile("" ::: "memory");  // keep the activation loads ahead of the weights
+    wait_vmcnt<0>();
     const size_t rowbytes = (size_t)nb * DOE_Q4K_BLOCK_BYTES;
-    // group gi's 16 rows of block b: granule q -> row q / 9, piece q % 9
-    auto load_group = [&](int gi, u32x4 (&dst)[3]) __attribute__((always_inline)) {
+    // group gi (clamped to the range), block b, into ring slot d: three load
+    // instructions (lanes 0..63, 64..127 and 128..143 of the 144 granules)
+    auto load_unit = [&](int gi, int d) __attribute__((always_inline)) {
+        gi = min(gi, glast);
+        uint8_t *slot = ring + d * kStreamUnitBytes;
 #pragma unroll
         for (int s = 0; s < 3; ++s) {
             const int q = min(lane + 64 * s, 143);
             const int r = min(gi * 16 + q / 9, n - 1);
-            dst[s] = load_stream16(w + (size_t)r * rowbytes + (size_t)b * DOE_Q4K_BLOCK_BYTES + (q % 9) * 16);
+            const uint8_t *src = w + (size_t)r * rowbytes + (size_t)b * DOE_Q4K_BLOCK_BYTES + (q % 9) * 16;
+            if (s < 2 || lane < 16)
+                __builtin_amdgcn_global_load_lds((const void *)src,
+                                                 (__attribute__((address_space(3))) void *)(slot + s * 1024), 16, 0, 0);
         }
     };
-    u32x4 wa[3], wb[3];
-    int gi = blockIdx.x;  // the grid never exceeds the group count
-    load_group(gi, wa);
-    if (gi + G < ngroups) load_group(gi + G, wb);
-    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_unit(g0 + d, d);
 
     float ss = 0.0f;
 #pragma unroll
@@ -870,60 +904,51 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
     const bool act = (m >> 2) == g && c < nchunk;
     const int abase = act ? g * 16 + (m & 1) * 8 + ((m >> 1) & 1) * 4 : 64;
     const float lo_scale = __builtin_amdgcn_ldexpf(1.0f, 24 - sgm), hi_scale = __builtin_amdgcn_ldexpf(1.0f, 20 - sgm);
+    u32x4 areg[8];  // the block's A operands: the same in every group
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) areg[jj] = *reinterpret_cast<const u32x4 *>(aimg + jj * kMfmaAStep + abase);
 
-    int j = 0;
-    for (; gi < ngroups; gi += G, ++j) {
+    for (int j0 = 0; j0 < my; j0 += D) {
 #pragma unroll
-        for (int s = 0; s < 3; ++s) {
-            const int q = lane + 64 * s;
-            if (q < 144) *reinterpret_cast<u32x4 *>(wimg + (q / 9) * kMfmaRowBytes + (q % 9) * 16) = wa[s];
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (gi + 2 * G < ngroups) load_group(gi + 2 * G, wa);  // wa's bytes are in LDS now
-        u32x4 areg[8];
+        for (int d = 0; d < D; ++d) {
+            const int j = j0 + d;
+            // slot d's three loads are the oldest of the 3 D in flight
+            wait_vmcnt<3 * (D - 1)>();
+            if (j < my) {  // wave-uniform; LDS and arithmetic only
+                const uint8_t *rp = ring + d * kStreamUnitBytes + i16 * DOE_Q4K_BLOCK_BYTES;  // lane (g, row i16)
+                const u32x4 hdr = *reinterpret_cast<const u32x4 *>(rp);
+                const u32x4 qa = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
+                const u32x4 qb = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
+                f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) areg[jj] = *reinterpret_cast<const u32x4 *>(aimg + jj * kMfmaAStep + abase);
-        const uint8_t *rp = wimg + i16 * kMfmaRowBytes;
-        const u32x4 hdr = *reinterpret_cast<const u32x4 *>(rp);
-        const u32x4 qa = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
-        const u32x4 qb = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
-        f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            const uint32_t dw = jj < 4 ? qa[jj] : qb[jj - 4], ew = dw >> 8;
-            const u32x4 bw = {dw & 0x000f000fu, ew & 0x000f000fu, dw & 0x00f000f0u, ew & 0x00f000f0u};
-            acc[jj & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, areg[jj]),
-                                                                 __builtin_bit_cast(half8, bw), acc[jj & 1], 0, 0, 0);
-        }
-        const f32x4 dsum = acc[0] + acc[1];
-        float part = 0.0f;
-        if (c < nchunk) {
-            uint32_t scp, mnp;
-            q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
-            const float d = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
-            const float qx_lo = (dsum[0] + dsum[1]) * lo_scale;
-            const float qx_hi = (dsum[2] + dsum[3]) * hi_scale;
-            const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
-            const float m_lo = (float)(mnp & 0xffu), m_hi = (float)(mnp >> 8);
-            part = d * (sc_lo * qx_lo + sc_hi * qx_hi) - dmin * (m_lo * sxl + m_hi * sxh);
-        }
-        __builtin_amdgcn_wave_barrier();
-        part = sum_rows4(part);
-        float *rd = red + (j & 1) * 16 * nwaves;
-        if (lane < 16) rd[lane * nwaves + wave] = part;
-        __syncthreads();
-        if (tid < 16) {
-            float sm = 0.0f;
-            for (int ww = 0; ww < nwaves; ++ww) sm += rd[tid * nwaves + ww];
-            rsum[j * 16 + tid] = sm;
-        }
-#pragma unroll
-        for (int s = 0; s < 3; ++s) {
-            const u32x4 t = wa[s];
-            wa[s] = wb[s];
-            wb[s] = t;
+                for (int jj = 0; jj < 8; ++jj) {
+                    const uint32_t dw = jj < 4 ? qa[jj] : qb[jj - 4], ew = dw >> 8;
+                    const u32x4 bw = {dw & 0x000f000fu, ew & 0x000f000fu, dw & 0x00f000f0u, ew & 0x00f000f0u};
+                    acc[jj & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, areg[jj]),
+                                                                         __builtin_bit_cast(half8, bw), acc[jj & 1], 0, 0, 0);
+                }
+                const f32x4 dsum = acc[0] + acc[1];
+                float part = 0.0f;
+                if (c < nchunk) {
+                    uint32_t scp, mnp;
+                    q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
+                    const float d_ = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
+                    const float qx_lo = (dsum[0] + dsum[1]) * lo_scale;
+                    const float qx_hi = (dsum[2] + dsum[3]) * hi_scale;
+                    const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
+                    const float m_lo = (float)(mnp & 0xffu), m_hi = (float)(mnp >> 8);
+                    part = d_ * (sc_lo * qx_lo + sc_hi * qx_hi) - dmin * (m_lo * sxl + m_hi * sxh);
+                }
+                part = sum_rows4(part);
+                if (lane < 16) rpart[(j * 16 + lane) * nwaves + wave] = part;
+            }
+            // the slot's reads have returned (the arithmetic above used them)
+            // before the next unit's bytes may land in it
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            load_unit(g0 + j + D, d);
         }
     }
+    wait_vmcnt<0>();  // the dropped loads past the range land before the LDS is released
     __syncthreads();
     float inv = 1.0f;
     if (NORM) {
@@ -931,17 +956,20 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
         for (int ww = 0; ww < nwaves; ++ww) tot += ssq[ww];
         inv = 1.0f / sqrtf(tot / (float)k + fz.norm_eps);
     }
-    for (int t = tid; t < j * 16; t += blockDim.x) {
+    auto row_sum = [&](int t) __attribute__((always_inline)) {
+        float sm = 0.0f;
+        for (int ww = 0; ww < nwaves; ++ww) sm += rpart[t * nwaves + ww];
+        return NORM ? sm * inv : sm;
+    };
+    for (int t = tid; t < my * 16; t += blockDim.x) {
         const int r16 = t & 15;
-        const int row = ((int)blockIdx.x + (t >> 4) * G) * 16 + r16;
-        const float sv = NORM ? rsum[t] * inv : rsum[t];
+        const int row = (g0 + (t >> 4)) * 16 + r16;
         if (fz.gated) {
-            const float other = NORM ? rsum[t ^ 1] * inv : rsum[t ^ 1];
-            if ((r16 & 1) == 0 && row < n) y[row >> 1] = doe_gelu_tanh_clamped(sv) * other;
+            if ((r16 & 1) == 0 && row < n) y[row >> 1] = doe_gelu_tanh_clamped(row_sum(t)) * row_sum(t + 1);
         } else if (fz.rope_kv) {
-            const float other = NORM ? rsum[t ^ 1] * inv : rsum[t ^ 1];
-            if ((r16 & 1) == 0 && row < n) rope_kv_pair(fz, row, sv, other, y);
+            if ((r16 & 1) == 0 && row < n) rope_kv_pair(fz, row, row_sum(t), row_sum(t + 1), y);
         } else if (row < n) {
+            const float sv = row_sum(t);
             y[row] = fz.residual ? sv + fz.residual[row] : sv;
         }
     }
@@ -1097,57 +1125,47 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     const bool mfma_ok = nbs <= kMfmaMaxBlocks && (bpw == 1 || !fz.attn_o);
     const bool dot_ok = gemv_lds_bytes(nchunk, 8) <= 64 * 1024;
     const bool use_mfma = g_tune_kernel == 1 ? !dot_ok && mfma_ok : mfma_ok;
-    // Streaming kernel (opt-in, q4k_gemv.stream = groups per workgroup): one
-    // wave per block, whole rows, no attention prologue.  Measured slower
-    // than the one-shot kernel on every shape tried (9216, 18432 and 65536
-    // rows of 2304; 4096 and 2304 rows): 96 VGPRs leave two workgroups per
-    // CU, and the per-group barrier chain bounds a workgroup to about two
-    // groups in flight.
-    if (use_mfma && bpw == 1 && ksplit == 1 && !fz.attn_o && g_tune_stream > 0) {
+    // Streaming kernel: one wave per block, whole rows, no attention
+    // prologue; automatic from kStreamMinGroupsPerCu row groups per CU
+    // (q4k_gemv.stream: -1 never, g > 0 forces g row groups per workgroup).
+    const bool stream_ok = use_mfma && bpw == 1 && ksplit == 1 && !fz.attn_o;
+    if (stream_ok && (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups >= kStreamMinGroupsPerCu * g_num_cus))) {
         const int nwaves = nb;
-        const size_t lds = gemv_stream_lds_bytes(nwaves);
+        // ring depth: the deepest that fits one workgroup's LDS
+        const int depth = gemv_stream_lds_bytes(nwaves, 4) <= kStreamLdsMax ? 4 : 2;
+        const size_t lds = gemv_stream_lds_bytes(nwaves, depth);
         const bool xv = ((uintptr_t)activation & 15) == 0 && (k & 3) == 0 && ((uintptr_t)fz.norm_w & 15) == 0;
-        const void *fn = fz.norm_w ? (xv ? (const void *)q4k_gemv_stream_kernel<1, 1> : (const void *)q4k_gemv_stream_kernel<1, 0>)
-                                   : (xv ? (const void *)q4k_gemv_stream_kernel<0, 1> : (const void *)q4k_gemv_stream_kernel<0, 0>);
         static const hipError_t attr_all = [] {
             hipError_t e = hipSuccess;
-            for (const void *f : {(const void *)q4k_gemv_stream_kernel<0, 0>, (const void *)q4k_gemv_stream_kernel<0, 1>,
-                                  (const void *)q4k_gemv_stream_kernel<1, 0>, (const void *)q4k_gemv_stream_kernel<1, 1>})
-                if (e == hipSuccess)
-                    e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemv_stream_lds_bytes(16));
+            for (const void *f : {(const void *)q4k_gemv_stream_kernel<0, 0, 2>, (const void *)q4k_gemv_stream_kernel<0, 1, 2>,
+                                  (const void *)q4k_gemv_stream_kernel<1, 0, 2>, (const void *)q4k_gemv_stream_kernel<1, 1, 2>,
+                                  (const void *)q4k_gemv_stream_kernel<0, 0, 4>, (const void *)q4k_gemv_stream_kernel<0, 1, 4>,
+                                  (const void *)q4k_gemv_stream_kernel<1, 0, 4>, (const void *)q4k_gemv_stream_kernel<1, 1, 4>})
+                if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kStreamLdsMax);
             return e;
         }();
         DOE_HIP_CHECK(attr_all);
-        // stream when the one-shot kernel needs more than one round of
-        // resident workgroups, with as few groups per workgroup as the
-        // streaming kernel's own residency allows
-        int per_cu = 0, per_cu_once = 0;
-        DOE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64 * nwaves, lds));
-        const void *once = fz.norm_w ? (const void *)q4k_gemv_mfma_kernel<1, 1, 1> : (const void *)q4k_gemv_mfma_kernel<0, 1, 1>;
-        DOE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_once, once, 64 * nwaves,
-                                                                   gemv_mfma_lds_bytes(nwaves, 1)));
-        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * g_num_cus;
-        const int64_t resident_once = (int64_t)(per_cu_once > 0 ? per_cu_once : 1) * g_num_cus;
-        (void)resident_once;
-        int64_t per_wg = g_tune_stream > 0 ? g_tune_stream
-                                           : (row_groups > resident_once ? (row_groups + resident - 1) / resident : 0);
-        if (per_wg > kStreamMaxGroups) per_wg = 0;  // too many groups per workgroup for the LDS row sums
-        if (per_wg > 0) {
-            const int64_t grid = (row_groups + per_wg - 1) / per_wg;
-#define DOE_GEMV_STREAM_LAUNCH(P, X)                                                                   \
-    do {                                                                                               \
-        hipLaunchKernelGGL((q4k_gemv_stream_kernel<P, X>), dim3((unsigned)grid), dim3(64 * nwaves), lds, st, wp, \
-                           activation, output, (int)n, (int)k, nb, (int)row_groups, fz);               \
+        // groups per workgroup: forced, or one workgroup per CU (LDS-bound)
+        // with at most kStreamMaxGroups each
+        int64_t per_wg = g_tune_stream > 0 ? g_tune_stream : (row_groups + g_num_cus - 1) / g_num_cus;
+        if (per_wg > kStreamMaxGroups) per_wg = kStreamMaxGroups;
+        const int64_t grid = (row_groups + per_wg - 1) / per_wg;
+#define DOE_GEMV_STREAM_LAUNCH(P, X, D)                                                                   \
+    hipLaunchKernelGGL((q4k_gemv_stream_kernel<P, X, D>), dim3((unsigned)grid), dim3(64 * nwaves), lds, st, wp, \
+                       activation, output, (int)n, (int)k, nb, (int)row_groups, fz)
+#define DOE_GEMV_STREAM_DEPTH(P, X)                                                                       \
+    do {                                                                                                  \
+        if (depth == 4) DOE_GEMV_STREAM_LAUNCH(P, X, 4); else DOE_GEMV_STREAM_LAUNCH(P, X, 2);           \
     } while (0)
-            if (fz.norm_w) {
-                if (xv) DOE_GEMV_STREAM_LAUNCH(1, 1); else DOE_GEMV_STREAM_LAUNCH(1, 0);
-            } else {
-                if (xv) DOE_GEMV_STREAM_LAUNCH(0, 1); else DOE_GEMV_STREAM_LAUNCH(0, 0);
-            }
-#undef DOE_GEMV_STREAM_LAUNCH
-            DOE_LAUNCH_CHECK("q4k_gemv_stream_kernel");
-            return DOE_OK;
+        if (fz.norm_w) {
+            if (xv) DOE_GEMV_STREAM_DEPTH(1, 1); else DOE_GEMV_STREAM_DEPTH(1, 0);
+        } else {
+            if (xv) DOE_GEMV_STREAM_DEPTH(0, 1); else DOE_GEMV_STREAM_DEPTH(0, 0);
         }
+#undef DOE_GEMV_STREAM_DEPTH
+#undef DOE_GEMV_STREAM_LAUNCH
+        DOE_LAUNCH_CHECK("q4k_gemv_stream_kernel");
+        return DOE_OK;
     }
     if (use_mfma) {
         const int nwaves = (nbs + bpw - 1) / bpw;

@@ -241,13 +241,25 @@ def stream_groups(request, dev):
     ops.tune("q4k_gemv.stream", 0)
 
 
-@pytest.mark.parametrize("stream_groups", [1, 2, 3, 7, 32], indirect=True)
+@pytest.mark.parametrize("stream_groups", [1, 2, 3, 7, 16], indirect=True)
 @pytest.mark.parametrize("n,k", [(9216, 2304), (1000, 2304), (77, 300), (4096, 4096), (18432, 2304), (33, 256)])
 def test_gemv_streaming_kernel(dev, ora, n, k, stream_groups):
     # the persistent streaming form: each workgroup walks `stream_groups` row
     # groups (the last one partial where n % 16 != 0), one wave per block
     print(f"[gemv stream {stream_groups}] {n}x{k}", flush=True)
     rng = np.random.default_rng(n + k + stream_groups)
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    err = rel_l2(_gemv(w, x, n, k), ora.q4k_gemv(w, x, n, k))
+    assert err < 1e-5, err
+
+
+@pytest.mark.parametrize("n,k", [(40000, 2304), (65536, 2304), (70001, 512)])
+def test_gemv_streaming_automatic(dev, ora, n, k):
+    # the automatic choice streams from 8 row groups per CU (one persistent
+    # workgroup per CU, up to 16 groups each; past that, several rounds)
+    print(f"[gemv stream auto] {n}x{k}", flush=True)
+    rng = np.random.default_rng(n + k)
     w = q4k.random_q4k(rng, n, k)
     x = rng.standard_normal(k).astype(np.float32)
     err = rel_l2(_gemv(w, x, n, k), ora.q4k_gemv(w, x, n, k))
