@@ -982,6 +982,7 @@ int g_tune_kernel = 0;  // 0 automatic, 1 dot-product kernel, 2 matrix-core kern
 int g_tune_ksplit = 0;  // 0 automatic, 1 never split K over workgroups
 int g_tune_bpw = 0;     // 0 automatic, else at least this many blocks per wave (<= 4)
 int g_tune_stream = 0;  // 0 automatic, -1 never stream, g > 0: stream g row groups per workgroup
+int g_tune_stream_depth = 0;  // 0 automatic, else 2, 4 or 6 units in flight per wave (if the LDS allows)
 
 // Launch shape for the GEMV: rowslots * nchunk threads (rounded up to whole
 // waves) and R rows per thread.  The automatic choice spreads the rows over
@@ -1131,8 +1132,13 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     const bool stream_ok = use_mfma && bpw == 1 && ksplit == 1 && !fz.attn_o;
     if (stream_ok && (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups >= kStreamMinGroupsPerCu * g_num_cus))) {
         const int nwaves = nb;
-        // ring depth: the deepest that fits one workgroup's LDS
-        const int depth = gemv_stream_lds_bytes(nwaves, 4) <= kStreamLdsMax ? 4 : 2;
+        // ring depth 2: deeper rings measured slower (65536 x 2304: 21.4 us
+        // at 2, 23.0 at 3, 23.4 at 4, 25.8 at 6) -- the more units each wave
+        // has in flight, the further a workgroup's waves drift apart over
+        // the groups and the less DRAM row locality their reads keep
+        int depth = 2;
+        if (g_tune_stream_depth > 0 && gemv_stream_lds_bytes(nwaves, g_tune_stream_depth) <= kStreamLdsMax)
+            depth = g_tune_stream_depth;
         const size_t lds = gemv_stream_lds_bytes(nwaves, depth);
         const bool xv = ((uintptr_t)activation & 15) == 0 && (k & 3) == 0 && ((uintptr_t)fz.norm_w & 15) == 0;
         static const hipError_t attr_all = [] {
@@ -1140,7 +1146,11 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
             for (const void *f : {(const void *)q4k_gemv_stream_kernel<0, 0, 2>, (const void *)q4k_gemv_stream_kernel<0, 1, 2>,
                                   (const void *)q4k_gemv_stream_kernel<1, 0, 2>, (const void *)q4k_gemv_stream_kernel<1, 1, 2>,
                                   (const void *)q4k_gemv_stream_kernel<0, 0, 4>, (const void *)q4k_gemv_stream_kernel<0, 1, 4>,
-                                  (const void *)q4k_gemv_stream_kernel<1, 0, 4>, (const void *)q4k_gemv_stream_kernel<1, 1, 4>})
+                                  (const void *)q4k_gemv_stream_kernel<1, 0, 4>, (const void *)q4k_gemv_stream_kernel<1, 1, 4>,
+                                  (const void *)q4k_gemv_stream_kernel<0, 0, 6>, (const void *)q4k_gemv_stream_kernel<0, 1, 6>,
+                                  (const void *)q4k_gemv_stream_kernel<1, 0, 6>, (const void *)q4k_gemv_stream_kernel<1, 1, 6>,
+                                  (const void *)q4k_gemv_stream_kernel<0, 0, 3>, (const void *)q4k_gemv_stream_kernel<0, 1, 3>,
+                                  (const void *)q4k_gemv_stream_kernel<1, 0, 3>, (const void *)q4k_gemv_stream_kernel<1, 1, 3>})
                 if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kStreamLdsMax);
             return e;
         }();
@@ -1155,7 +1165,10 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
                        activation, output, (int)n, (int)k, nb, (int)row_groups, fz)
 #define DOE_GEMV_STREAM_DEPTH(P, X)                                                                       \
     do {                                                                                                  \
-        if (depth == 4) DOE_GEMV_STREAM_LAUNCH(P, X, 4); else DOE_GEMV_STREAM_LAUNCH(P, X, 2);           \
+        if (depth == 4) DOE_GEMV_STREAM_LAUNCH(P, X, 4);                                                 \
+        else if (depth == 6) DOE_GEMV_STREAM_LAUNCH(P, X, 6);                                            \
+        else if (depth == 3) DOE_GEMV_STREAM_LAUNCH(P, X, 3);                                            \
+        else DOE_GEMV_STREAM_LAUNCH(P, X, 2);                                                            \
     } while (0)
         if (fz.norm_w) {
             if (xv) DOE_GEMV_STREAM_DEPTH(1, 1); else DOE_GEMV_STREAM_DEPTH(1, 0);
@@ -1329,6 +1342,10 @@ int doe_tune_set(const char *key, int value) {
         DOE_REQUIRE(value >= -1 && value <= kStreamMaxGroups, DOE_E_INVALID, "q4k_gemv.stream is -1..%d",
                     kStreamMaxGroups);
         g_tune_stream = value;
+    } else if (!strcmp(key, "q4k_gemv.stream_depth")) {
+        DOE_REQUIRE(value == 0 || value == 2 || value == 3 || value == 4 || value == 6, DOE_E_INVALID,
+                    "q4k_gemv.stream_depth is 0, 2, 3, 4 or 6");
+        g_tune_stream_depth = value;
     } else if (!strcmp(key, "q4k_gemv.ksplit")) {
         DOE_REQUIRE(value == 0 || value == 1, DOE_E_INVALID, "q4k_gemv.ksplit is 0 or 1");
         g_tune_ksplit = value;
