@@ -72,6 +72,7 @@ SIGNATURES: dict[str, list] = {
     "doe_q4k_gemm": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "doe_q4k_gemm_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "doe_q8_0_gemm_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "doe_quant_gemm_f32_fused": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _f32, _i32, _vp, _i32, _vp],
     "doe_q4k_gemv": [_vp, _vp, _vp, _i64, _i64, _vp],
     "doe_q8_0_gemv": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
     "doe_q8_0_gemv_norm": [_vp, _vp, _vp, _i64, _i64, _vp, _f32, _i32, _vp, _vp],

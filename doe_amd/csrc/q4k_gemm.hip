@@ -158,6 +158,63 @@ __global__ __launch_bounds__(256) void a_rows_f32_to_f16_kernel(const float *__r
     for (int k = threadIdx.x; k < Kp; k += 256) out[k] = k < K ? (_Float16)(row[k] * scale) : (_Float16)0.0f;
 }
 
+// The same copy of RMSNorm(a) rows (the input_norm / post_attn_norm step
+// folded into the projection that consumes it): the normalised values are
+// those of the rmsnorm op bit for bit -- the same per-thread f32 sums of
+// squares over k = t, t + 256, ..., the same four-wave sum, inv = 1 /
+// sqrt(ss / K + eps), y = x * inv * (w or 1 + w) -- then scaled and rounded
+// as a_rows_f32_to_f16_kernel does.
+__global__ __launch_bounds__(256) void a_rows_norm_f32_to_f16_kernel(const float *__restrict__ a,
+                                                                     const float *__restrict__ w, float eps,
+                                                                     int weight_offset, _Float16 *__restrict__ a16,
+                                                                     int *__restrict__ sig, int K, int Kp) {
+    const int m = blockIdx.x;
+    const float *row = a + (size_t)m * K;
+    _Float16 *out = a16 + (size_t)m * Kp;
+    __shared__ float sh[4];
+    __shared__ int ssig;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float ss = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) ss = fmaf(row[k], row[k], ss);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) sh[wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int j = 0; j < 4; ++j) tot += sh[j];
+    const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+    float amax = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const float y = row[k] * inv * (weight_offset ? 1.0f + w[k] : w[k]);
+        amax = fmaxf(amax, fabsf(y));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    __syncthreads();  // every thread has read sh
+    if (lane == 0) sh[wave] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float mx = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+        int s = 0;
+        if (mx > 0.0f && mx <= 3.0e38f) {
+            s = 14 - __builtin_amdgcn_frexp_expf(mx);
+            s = s < -120 ? -120 : (s > 120 ? 120 : s);
+        }
+        ssig = s;
+        sig[m] = s;
+    }
+    __syncthreads();
+    const float scale = __builtin_amdgcn_ldexpf(1.0f, ssig);
+    for (int k = threadIdx.x; k < Kp; k += 256) {
+        if (k < K) {
+            const float y = row[k] * inv * (weight_offset ? 1.0f + w[k] : w[k]);
+            out[k] = (_Float16)(y * scale);
+        } else {
+            out[k] = (_Float16)0.0f;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // GEMM.
 // ---------------------------------------------------------------------------
@@ -663,14 +720,20 @@ __global__ __launch_bounds__(256) void q4k_gemm_pipe_kernel(GemmArgs g) {
 
 // c = sum of the K splits' partial tiles (split order, so the result is
 // the same on every run).
-__global__ __launch_bounds__(256) void sum_splits_kernel(const float *__restrict__ part, float *__restrict__ c,
-                                                         size_t mn, int splits) {
+// c = the split sum (+ res: the attn_residual / ffn_residual step, c may
+// be res), the splits added in order, then the residual.
+__global__ __launch_bounds__(256) void sum_splits_kernel(const float *__restrict__ part, float *c, size_t mn,
+                                                         int splits, const float *res) {
     const size_t n4 = mn / 4;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
         float4 acc = reinterpret_cast<const float4 *>(part)[i];
         for (int s = 1; s < splits; ++s) {
             const float4 v = reinterpret_cast<const float4 *>(part + (size_t)s * mn)[i];
             acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        }
+        if (res) {
+            const float4 r = reinterpret_cast<const float4 *>(res)[i];
+            acc.x += r.x; acc.y += r.y; acc.z += r.z; acc.w += r.w;
         }
         reinterpret_cast<float4 *>(c)[i] = acc;
     }
@@ -679,7 +742,27 @@ __global__ __launch_bounds__(256) void sum_splits_kernel(const float *__restrict
     if (blockIdx.x == 0 && i < mn) {
         float acc = part[i];
         for (int s = 1; s < splits; ++s) acc += part[(size_t)s * mn + i];
+        if (res) acc += res[i];
         c[i] = acc;
+    }
+}
+
+// c[row][j] = gelu(gate) * up over the split sums of the gate/up projection
+// (the activation step folded in): gate and up columns (2j, 2j + 1) for
+// interleaved rows (halves 0) or (j, j + n/2) for [gate | up] (halves 1).
+__global__ __launch_bounds__(256) void sum_splits_geglu_kernel(const float *__restrict__ part, float *__restrict__ c,
+                                                               int m, int n, int splits, int halves) {
+    const int h = n >> 1;
+    const size_t mn = (size_t)m * n, total = (size_t)m * h;
+    for (size_t o = (size_t)blockIdx.x * 256 + threadIdx.x; o < total; o += (size_t)gridDim.x * 256) {
+        const size_t row = o / h, j = o - row * h;
+        const size_t gc = row * n + (halves ? j : 2 * j), uc = row * n + (halves ? j + h : 2 * j + 1);
+        float g = part[gc], u = part[uc];
+        for (int s = 1; s < splits; ++s) {
+            g += part[(size_t)s * mn + gc];
+            u += part[(size_t)s * mn + uc];
+        }
+        c[o] = doe_gelu_tanh_clamped(g) * u;
     }
 }
 
@@ -689,9 +772,20 @@ void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
 int g_num_cus = 0;
 
+// Steps folded around the prompt GEMM (f32 activations only): RMSNorm of
+// A's rows in the f16 pre-pass, and a residual add or a GeGLU over gate/up
+// column pairs in the pass that sums the K splits.
+struct GemmFusion {
+    const float *norm_w = nullptr;
+    float norm_eps = 0.0f;
+    int norm_offset = 0;
+    const float *residual = nullptr;  // c += residual (may be c)
+    int act = 0;                      // 1: GeGLU over (2j, 2j + 1), 2: over (j, j + n/2); c is [m][n/2]
+};
+
 // fmt 0: B Q4_K_M rows; fmt 1: B Q8_0 rows (small-tile kernel only)
 int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m, int64_t n, int64_t k,
-              doe_stream_t stream, int fmt = 0) {
+              doe_stream_t stream, int fmt = 0, const GemmFusion &fu = GemmFusion()) {
     const uint16_t *a_bf16 = a_f32 ? nullptr : (const uint16_t *)a;
     int rc = doe::require_init();
     if (rc) return rc;
@@ -699,8 +793,16 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     if (m == 0 || n == 0) return DOE_OK;
     DOE_REQUIRE(c, DOE_E_INVALID, "null output");
     hipStream_t st = (hipStream_t)stream;
+    const bool epi = fu.residual || fu.act;  // the split-sum pass writes c
+    DOE_REQUIRE(a_f32 || (!fu.norm_w && !epi), DOE_E_UNSUPPORTED, "fused steps need f32 activations");
+    DOE_REQUIRE(fu.act >= 0 && fu.act <= 2 && !(fu.act && fu.residual), DOE_E_INVALID,
+                "activation 0, 1 or 2, and not with a residual");
+    DOE_REQUIRE(!fu.act || n % 2 == 0, DOE_E_INVALID, "GeGLU needs an even column count");
+    DOE_REQUIRE(!fu.norm_w || (fu.norm_w != c && a != c), DOE_E_INVALID,
+                "the norm weight and the activation must not alias the output");
     if (k == 0) {
-        // empty reduction: the sum identity
+        // empty reduction: the sum identity (the fused steps need k > 0)
+        DOE_REQUIRE(!fu.norm_w && !epi, DOE_E_UNSUPPORTED, "fused steps need k > 0");
         return doe::fill_bytes_async(c, 0, (size_t)m * (size_t)n * sizeof(float), st);
     }
     DOE_REQUIRE(a && b_q4k, DOE_E_INVALID, "null pointer");
@@ -738,7 +840,8 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     const int64_t kps = (nchunk + splits - 1) / splits;
     splits = (nchunk + kps - 1) / kps;
     const size_t part_off = (a16_bytes + (size_t)m * 4 + 255) & ~(size_t)255;
-    const size_t need = splits > 1 ? part_off + (size_t)splits * m * n * 4 : a16_bytes + (size_t)m * 4;
+    const bool use_part = splits > 1 || epi;  // the GEMM writes partial tiles, a second pass writes c
+    const size_t need = use_part ? part_off + (size_t)splits * m * n * 4 : a16_bytes + (size_t)m * 4;
     void *ws;
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -757,7 +860,10 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     }
     _Float16 *a16 = (_Float16 *)ws;
     int *sig = (int *)((char *)ws + a16_bytes);
-    if (a_f32)
+    if (a_f32 && fu.norm_w)
+        hipLaunchKernelGGL(a_rows_norm_f32_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, (const float *)a,
+                           fu.norm_w, fu.norm_eps, fu.norm_offset, a16, sig, (int)k, (int)kp);
+    else if (a_f32)
         hipLaunchKernelGGL(a_rows_f32_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, (const float *)a, a16, sig,
                            (int)k, (int)kp);
     else
@@ -768,14 +874,15 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     g.a16 = a16;
     g.sig = sig;
     g.b = (const uint8_t *)b_q4k;
-    g.c = c;
+    float *part = use_part ? (float *)((char *)ws + part_off) : nullptr;
+    g.c = use_part && splits == 1 ? part : c;  // one split: the tile goes to the workspace for the second pass
     g.M = (int)m;
     g.N = (int)n;
     g.Kp = (int)kp;
     g.nb = (int)(fmt ? (k + 31) / 32 : (k + 255) / 256);
     g.nchunk = (int)(kp / kBK);
     g.kps = (int)kps;
-    g.part = splits > 1 ? (float *)((char *)ws + part_off) : nullptr;
+    g.part = splits > 1 ? part : nullptr;
     const int bm = big ? 256 : 128, bn = big ? 256 : 128;
     g.tiles_m = (int)((m + bm - 1) / bm);
     g.tiles_n = (int)((n + bn - 1) / bn);
@@ -788,11 +895,19 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     else
         hipLaunchKernelGGL((quant_gemm_kernel<2, 2, 0>), dim3((unsigned)tiles, (unsigned)splits), dim3(256), 0, st, g);
     DOE_LAUNCH_CHECK("quant_gemm_kernel");
-    if (splits > 1) {
+    if (use_part && fu.act) {
+        const size_t total = (size_t)m * (size_t)(n / 2);
+        size_t blocks = (total + 255) / 256;
+        blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
+        hipLaunchKernelGGL(sum_splits_geglu_kernel, dim3((unsigned)blocks), dim3(256), 0, st, part, c, (int)m, (int)n,
+                           (int)splits, fu.act == 2 ? 1 : 0);
+        DOE_LAUNCH_CHECK("sum_splits_geglu_kernel");
+    } else if (use_part) {
         const size_t mn = (size_t)m * (size_t)n;
         size_t blocks = (mn / 4 + 255) / 256;
         blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
-        hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g.part, c, mn, (int)splits);
+        hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)blocks), dim3(256), 0, st, part, c, mn, (int)splits,
+                           fu.residual);
         DOE_LAUNCH_CHECK("sum_splits_kernel");
     }
     return DOE_OK;
@@ -815,6 +930,19 @@ int doe_q4k_gemm_f32(const float *a, const void *b_q4k, float *c, int64_t m, int
 int doe_q8_0_gemm_f32(const float *a, const void *b_q8_0, float *c, int64_t m, int64_t n, int64_t k,
                       doe_stream_t stream) {
     return gemm_impl(a, true, b_q8_0, c, m, n, k, stream, 1);
+}
+
+int doe_quant_gemm_f32_fused(const float *a, const void *b, float *c, int64_t m, int64_t n, int64_t k,
+                             int weight_format, const float *norm_weight, float norm_eps, int norm_weight_offset,
+                             const float *residual, int activation, doe_stream_t stream) {
+    DOE_REQUIRE(weight_format == 0 || weight_format == 1, DOE_E_INVALID, "weight_format is 0 (Q4_K) or 1 (Q8_0)");
+    GemmFusion fu;
+    fu.norm_w = norm_weight;
+    fu.norm_eps = norm_eps;
+    fu.norm_offset = norm_weight_offset;
+    fu.residual = residual;
+    fu.act = activation;
+    return gemm_impl(a, true, b, c, m, n, k, stream, weight_format, fu);
 }
 
 }  // extern "C"

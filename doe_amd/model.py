@@ -413,11 +413,8 @@ class Decoder:
             c, S = self.cfg, self.cfg.max_seq
             self._pf = {
                 "x": DeviceBuffer.empty((S, c.hidden), np.float32),
-                "xn": DeviceBuffer.empty((S, c.hidden), np.float32),
-                "t": DeviceBuffer.empty((S, c.hidden), np.float32),
                 "qkv": DeviceBuffer.empty((S, c.qkv_rows), np.float32),
                 "att": DeviceBuffer.empty((S, c.q_dim), np.float32),
-                "gu": DeviceBuffer.empty((S, 2 * c.ffn), np.float32),
                 "h": DeviceBuffer.empty((S, c.ffn), np.float32),
             }
         return self._pf
@@ -425,10 +422,12 @@ class Decoder:
     def prefill(self, prompt: np.ndarray, stream=None) -> None:
         """The prompt in one batched pass -- the step graph's prefill phase
         (gemma-3-270m-smoke.json prefill steps: embed, then per layer
-        input_norm, q/k/v_proj as one M-row GEMM, rope_q / rope_k with the
+        input_norm + q/k/v_proj as one M-row GEMM, rope_q / rope_k with the
         cache write, causal attention of the whole prompt, o_proj +
-        attn_residual, post_attn_norm, gate/up_proj, activation, down_proj +
-        ffn_residual), then the last token's final norm + lm_head + sample.
+        attn_residual, post_attn_norm + gate/up_proj + activation, down_proj +
+        ffn_residual -- each "+" folded into the GEMM's pre-pass or the pass
+        that sums its K splits), then the last token's final norm + lm_head +
+        sample.
         Q4_K layers run the Q4_K GEMM and the interleaved-pair RoPE, Q8_0
         layers the Q8_0 GEMM and the rotate-half RoPE of their decode step.
         Leaves the decoder where teacher-forced decode steps over the prompt
@@ -454,11 +453,13 @@ class Decoder:
         # rows interleaved; Q8_0 layers hold heads in order (rotate-half
         # RoPE) and the gate rows before the up rows
         q8 = c.weight_format == "q8_0"
-        gemm = ops.matmul_q8_0_gemm_f32 if q8 else ops.matmul_q4k_gemm_f32
+        fmt = c.weight_format
         rope_rows = ops.qkv_rope_half_kv_rows if q8 else ops.qkv_rope_kv_rows
+        act = ops.GEGLU_HALVES if q8 else ops.GEGLU_PAIRS
+        gemm = ops.matmul_gemm_f32_fused  # the norms, residuals and GeGLU ride on the GEMMs
         for li, L in enumerate(self.layers):
-            ops.rmsnorm(b["x"], L.norm_attn, b["xn"], P, c.hidden, c.eps, weight_offset=off, stream=stream)
-            gemm(b["xn"], L.wqkv, b["qkv"], P, c.qkv_rows, c.hidden, stream=stream)
+            gemm(b["x"], L.wqkv, b["qkv"], P, c.qkv_rows, c.hidden, fmt, norm_weight=L.norm_attn, norm_eps=c.eps,
+                 norm_weight_offset=off, stream=stream)
             freq = self.freq_cis if q8 else self.freq_by_layer[li]  # the Q8_0 decode step's table
             rope_rows(b["qkv"], P, c.qkv_rows, c.heads, c.kv_heads, hd, freq, 0, L.k_cache, L.v_cache, c.max_seq,
                       stream=stream)
@@ -467,16 +468,10 @@ class Decoder:
                                         kv_stride=c.max_seq, start_pos=0, scale=1.0 / math.sqrt(hd),
                                         softcap=c.attn_softcap, sliding_window=self.attn_windows[li],
                                         q_row_stride=c.qkv_rows, stream=stream)
-            gemm(b["att"], L.wo, b["t"], P, c.hidden, c.q_dim, stream=stream)
-            ops.residual(b["t"], b["x"], b["x"], P * c.hidden, stream=stream)
-            ops.rmsnorm(b["x"], L.norm_ffn, b["xn"], P, c.hidden, c.eps, weight_offset=off, stream=stream)
-            gemm(b["xn"], L.wgu, b["gu"], P, 2 * c.ffn, c.hidden, stream=stream)
-            if q8:
-                ops.geglu_halves(b["gu"], b["h"], P, c.ffn, stream=stream)
-            else:
-                ops.geglu_pairs(b["gu"], b["h"], P * c.ffn, stream=stream)
-            gemm(b["h"], L.wd, b["t"], P, c.hidden, c.ffn, stream=stream)
-            ops.residual(b["t"], b["x"], b["x"], P * c.hidden, stream=stream)
+            gemm(b["att"], L.wo, b["x"], P, c.hidden, c.q_dim, fmt, residual=b["x"], stream=stream)
+            gemm(b["x"], L.wgu, b["h"], P, 2 * c.ffn, c.hidden, fmt, norm_weight=L.norm_ffn, norm_eps=c.eps,
+                 norm_weight_offset=off, activation=act, stream=stream)
+            gemm(b["h"], L.wd, b["x"], P, c.hidden, c.ffn, fmt, residual=b["x"], stream=stream)
         last = b["x"].view((P - 1) * c.hidden * 4, c.hidden * 4, np.float32)
         nparts = ops.lm_head_sample(self.lm_head, last, c.vocab, c.hidden, self.argmax_parts,
                                     logits=self.logits if self.keep_logits else None, norm_weight=self.norm_final,

@@ -133,6 +133,39 @@ def matmul_q8_0_gemm_f32(a: DeviceBuffer, weight: DeviceBuffer, output: DeviceBu
     _lib.call("doe_q8_0_gemm_f32", _p(a), _p(weight), _p(output), m, n, k, _stream_ptr(stream))
 
 
+GEGLU_PAIRS, GEGLU_HALVES = 1, 2
+
+
+def matmul_gemm_f32_fused(a: DeviceBuffer, weight: DeviceBuffer, output: DeviceBuffer, m: int, n: int, k: int,
+                          weight_format: str = "q4k", *, norm_weight: DeviceBuffer | None = None,
+                          norm_eps: float = 1e-6, norm_weight_offset: bool = False,
+                          residual: DeviceBuffer | None = None, activation: int = 0, stream=None) -> None:
+    """A prompt projection with its neighbouring steps folded in: optional
+    RMSNorm of a's rows (``input_norm`` / ``post_attn_norm``), then ``matmul``
+    over Q4_K or Q8_0 rows, then an optional residual add (``attn_residual``
+    / ``ffn_residual``; residual may be output) or GeGLU over the gate/up
+    columns (GEGLU_PAIRS: (2j, 2j + 1), GEGLU_HALVES: (j, j + n/2); output
+    [m][n/2]).  Equals the unfused ops bit for bit."""
+    if weight_format == "q4k":
+        _q4k_weight_check(weight, n, k)
+        fmt = 0
+    elif weight_format == "q8_0":
+        _need(weight, n * _q8_0.row_bytes(k), "weight")
+        fmt = 1
+    else:
+        raise ValueError(f"weight_format {weight_format!r} is not q4k or q8_0")
+    _need(a, m * k * 4, "a")
+    _need(output, m * (n // 2 if activation else n) * 4, "output")
+    if norm_weight is not None:
+        _need(norm_weight, k * 4, "norm_weight")
+    if residual is not None:
+        _need(residual, m * n * 4, "residual")
+    _lib.call("doe_quant_gemm_f32_fused", _p(a), _p(weight), _p(output), m, n, k, fmt,
+              C.c_void_p(norm_weight.ptr) if norm_weight is not None else C.c_void_p(None), norm_eps,
+              int(norm_weight_offset), C.c_void_p(residual.ptr) if residual is not None else C.c_void_p(None),
+              activation, _stream_ptr(stream))
+
+
 def matmul_q8_0(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int,
                 residual: DeviceBuffer | None = None, stream=None, *, norm_weight: DeviceBuffer | None = None,
                 norm_eps: float = 1e-6, norm_weight_offset: bool = False) -> None:

@@ -170,6 +170,19 @@ int doe_q4k_gemm_f32(const float *a, const void *b_q4k, float *c, int64_t m, int
  * weight 4-byte aligned and under 2 GiB). */
 int doe_q8_0_gemm_f32(const float *a, const void *b_q8_0, float *c, int64_t m, int64_t n, int64_t k,
                       doe_stream_t stream);
+/* doe_q4k_gemm_f32 (weight_format 0) or doe_q8_0_gemm_f32 (1) with the
+ * prefill steps around a projection folded in (gemma-3-270m-smoke.json:
+ * 10-25): input_norm / post_attn_norm (norm_weight non-NULL: a's rows go
+ * through RMSNorm, bit for bit the doe_rmsnorm op, before the f16 pre-pass),
+ * attn_residual / ffn_residual (residual non-NULL: c = a W^T + residual,
+ * residual may be c), or the GeGLU activation over the gate/up projection
+ * (activation 1: columns (2j, 2j + 1) as doe_geglu_pairs; 2: columns (j, j +
+ * n/2) as doe_geglu_halves; c is then [m][n/2]).  A residual and an
+ * activation are exclusive; a and norm_weight must not alias c.  Each fused
+ * result equals the unfused op sequence bit for bit. */
+int doe_quant_gemm_f32_fused(const float *a, const void *b, float *c, int64_t m, int64_t n, int64_t k,
+                             int weight_format, const float *norm_weight, float norm_eps, int norm_weight_offset,
+                             const float *residual, int activation, doe_stream_t stream);
 
 /* Symmetric int4 group-32 GEMV, batch m in 1..8: y[b][i] = sum_k
  * (q[i][k] - 8) * s[i][k/32] * x[b][k].  w_u4: eight nibbles per u32, element

@@ -180,3 +180,80 @@ def test_gemm_rejects_misaligned_weight(dev):
     with pytest.raises(_lib.DoeError):
         _lib.call("doe_q4k_gemm", C.c_void_p(a.ptr), C.c_void_p(buf.ptr + 8), C.c_void_p(out.ptr), 1, 1, 256,
                   C.c_void_p(None))
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q8_0"])
+@pytest.mark.parametrize("m,n,k", [(128, 4096, 2304), (5, 78, 300), (130, 512, 2304), (1, 2, 256)])
+def test_fused_gemm_equals_the_op_sequence(dev, fmt, m, n, k):
+    # input_norm + q/k/v_proj, o_proj + attn_residual (in place) and
+    # post_attn_norm + gate/up_proj + GeGLU: bit for bit the unfused ops
+    from doe_amd import q8_0
+
+    rng = np.random.default_rng(m + n + k + (fmt == "q8_0"))
+    a = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    nw = (0.1 * rng.standard_normal(k)).astype(np.float32)
+    w = q4k.random_q4k(rng, n, k) if fmt == "q4k" else q8_0.random_q8_0(rng, n, k)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    gemm = ops.matmul_q4k_gemm_f32 if fmt == "q4k" else ops.matmul_q8_0_gemm_f32
+    da, dw, dnw = up(a), up(w), up(nw)
+    for offset in (False, True):
+        xn = DeviceBuffer.empty((m, k), np.float32)
+        ops.rmsnorm(da, dnw, xn, m, k, 1e-6, weight_offset=offset)
+        want = DeviceBuffer.empty((m, n), np.float32)
+        gemm(xn, dw, want, m, n, k)
+        got = DeviceBuffer.empty((m, n), np.float32)
+        ops.matmul_gemm_f32_fused(da, dw, got, m, n, k, fmt, norm_weight=dnw, norm_eps=1e-6,
+                                  norm_weight_offset=offset)
+        assert np.array_equal(got.download(), want.download()), ("norm", offset)
+        # GeGLU over the gate/up columns in either layout
+        for act in (ops.GEGLU_PAIRS, ops.GEGLU_HALVES):
+            h_want = DeviceBuffer.empty((m, n // 2), np.float32)
+            if act == ops.GEGLU_PAIRS:
+                ops.geglu_pairs(want, h_want, m * (n // 2))
+            else:
+                ops.geglu_halves(want, h_want, m, n // 2)
+            h_got = DeviceBuffer.empty((m, n // 2), np.float32)
+            ops.matmul_gemm_f32_fused(da, dw, h_got, m, n, k, fmt, norm_weight=dnw, norm_eps=1e-6,
+                                      norm_weight_offset=offset, activation=act)
+            assert np.array_equal(h_got.download(), h_want.download()), ("geglu", act, offset)
+    # residual, in place: x = a W^T + x
+    t = DeviceBuffer.empty((m, n), np.float32)
+    gemm(da, dw, t, m, n, k)
+    x_want = up(res)
+    ops.residual(t, x_want, x_want, m * n)
+    x_got = up(res)
+    ops.matmul_gemm_f32_fused(da, dw, x_got, m, n, k, fmt, residual=x_got)
+    assert np.array_equal(x_got.download(), x_want.download())
+
+
+def test_fused_gemm_large_tiles(dev):
+    # the 256 x 256 tile kernel (no K split) writes its tiles to the workspace
+    # and the second pass adds the residual
+    m, n, k = 1024, 16384, 256
+    rng = np.random.default_rng(9)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = q4k.random_q4k(rng, n, k)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    da, dw = up(a), up(w)
+    t = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_q4k_gemm_f32(da, dw, t, m, n, k)
+    x_want = up(res)
+    ops.residual(t, x_want, x_want, m * n)
+    x_got = up(res)
+    ops.matmul_gemm_f32_fused(da, dw, x_got, m, n, k, "q4k", residual=x_got)
+    assert np.array_equal(x_got.download(), x_want.download())
+
+
+def test_fused_gemm_rejects(dev):
+    a = DeviceBuffer.empty((4, 256), np.float32)
+    w = up(q4k.random_q4k(np.random.default_rng(1), 8, 256))
+    out = DeviceBuffer.empty((4, 8), np.float32)
+    with pytest.raises(_lib.DoeError, match="not with a residual"):
+        ops.matmul_gemm_f32_fused(a, w, out, 4, 8, 256, residual=out, activation=ops.GEGLU_PAIRS)
+    w7 = up(q4k.random_q4k(np.random.default_rng(2), 7, 256))
+    with pytest.raises(_lib.DoeError, match="even column count"):
+        ops.matmul_gemm_f32_fused(a, w7, out, 4, 7, 256, activation=ops.GEGLU_PAIRS)
+    with pytest.raises(_lib.DoeError, match="alias the output"):
+        ops.matmul_gemm_f32_fused(a, w, a, 4, 8, 256, norm_weight=up(np.ones(256, np.float32)))
+    with pytest.raises(ValueError):
+        ops.matmul_gemm_f32_fused(a, w, out, 4, 8, 256, "q6_k")
