@@ -129,71 +129,71 @@ __global__ __launch_bounds__(256) void a_rows_to_f16_kernel(const uint16_t *__re
 
 // The same pre-pass for f32 A: each row scaled by 2^sig[m] (max|A[m]| just
 // under 2^14) and rounded once to f16 (11 significant bits).
-__global__ __launch_bounds__(256) void a_rows_f32_to_f16_kernel(const float *__restrict__ a,
-                                                                _Float16 *__restrict__ a16,
-                                                                int *__restrict__ sig, int K, int Kp) {
-    const int m = blockIdx.x;
-    const float *row = a + (size_t)m * K;
-    _Float16 *out = a16 + (size_t)m * Kp;
-    float amax = 0.0f;
-    for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(row[k]));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    __shared__ float wmax[4];
-    __shared__ int ssig;
-    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const float mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-        int s = 0;
-        if (mx > 0.0f && mx <= 3.0e38f) {
-            s = 14 - __builtin_amdgcn_frexp_expf(mx);
-            s = s < -120 ? -120 : (s > 120 ? 120 : s);
-        }
-        ssig = s;
-        sig[m] = s;
-    }
-    __syncthreads();
-    const float scale = __builtin_amdgcn_ldexpf(1.0f, ssig);
-    for (int k = threadIdx.x; k < Kp; k += 256) out[k] = k < K ? (_Float16)(row[k] * scale) : (_Float16)0.0f;
-}
-
-// The same copy of RMSNorm(a) rows (the input_norm / post_attn_norm step
-// folded into the projection that consumes it): the normalised values are
-// those of the rmsnorm op bit for bit -- the same per-thread f32 sums of
-// squares over k = t, t + 256, ..., the same four-wave sum, inv = 1 /
-// sqrt(ss / K + eps), y = x * inv * (w or 1 + w) -- then scaled and rounded
-// as a_rows_f32_to_f16_kernel does.
-__global__ __launch_bounds__(256) void a_rows_norm_f32_to_f16_kernel(const float *__restrict__ a,
-                                                                     const float *__restrict__ w, float eps,
-                                                                     int weight_offset, _Float16 *__restrict__ a16,
-                                                                     int *__restrict__ sig, int K, int Kp) {
-    const int m = blockIdx.x;
+// f32 rows to f16 with a per-row power-of-two scale (as a_rows_to_f16_kernel
+// for bf16), optionally through RMSNorm first (the input_norm /
+// post_attn_norm step folded into the projection that consumes it; the
+// normalised values are those of the rmsnorm op bit for bit: the same
+// per-thread f32 sums of squares over k = t, t + 256, ..., the same
+// four-wave sum, inv = 1 / sqrt(ss / K + eps), y = x * inv * (w or 1 + w)).
+// R > 0: each thread holds its R elements of the row in registers (K <= 256
+// R), so the row is read from memory once; R = 0: the general form re-reads it.
+template <int R, bool NORM>
+__global__ __launch_bounds__(256) void a_rows_f32_kernel(const float *__restrict__ a, const float *__restrict__ w,
+                                                         float eps, int weight_offset, _Float16 *__restrict__ a16,
+                                                         int *__restrict__ sig, int K, int Kp) {
+    const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float *row = a + (size_t)m * K;
     _Float16 *out = a16 + (size_t)m * Kp;
     __shared__ float sh[4];
     __shared__ int ssig;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float ss = 0.0f;
-    for (int k = threadIdx.x; k < K; k += 256) ss = fmaf(row[k], row[k], ss);
+    float xv[R > 0 ? R : 1];
+    if (R > 0) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if (lane == 0) sh[wave] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-    for (int j = 0; j < 4; ++j) tot += sh[j];
-    const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+        for (int j = 0; j < R; ++j) xv[j] = t + 256 * j < K ? row[t + 256 * j] : 0.0f;
+    }
+    auto x_at = [&](int j, int k) __attribute__((always_inline)) { return R > 0 ? xv[R > 0 ? j : 0] : row[k]; };
+    float inv = 1.0f;
+    if (NORM) {
+        float ss = 0.0f;
+        if (R > 0) {
+#pragma unroll
+            for (int j = 0; j < R; ++j)
+                if (t + 256 * j < K) ss = fmaf(xv[R > 0 ? j : 0], xv[R > 0 ? j : 0], ss);
+        } else {
+            for (int k = t; k < K; k += 256) ss = fmaf(row[k], row[k], ss);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) sh[wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int j = 0; j < 4; ++j) tot += sh[j];
+        inv = 1.0f / sqrtf(tot / (float)K + eps);
+        __syncthreads();  // every thread has read sh
+    }
+    auto y_at = [&](int j, int k) __attribute__((always_inline)) {
+        const float x = x_at(j, k);
+        return NORM ? x * inv * (weight_offset ? 1.0f + w[k] : w[k]) : x;
+    };
     float amax = 0.0f;
-    for (int k = threadIdx.x; k < K; k += 256) {
-        const float y = row[k] * inv * (weight_offset ? 1.0f + w[k] : w[k]);
-        amax = fmaxf(amax, fabsf(y));
+    if (R > 0) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int k = t + 256 * j;
+            if (k < K) {
+                const float y = y_at(j, k);
+                if (NORM) xv[R > 0 ? j : 0] = y;  // keep the normalised value
+                amax = fmaxf(amax, fabsf(y));
+            }
+        }
+    } else {
+        for (int k = t; k < K; k += 256) amax = fmaxf(amax, fabsf(y_at(0, k)));
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    __syncthreads();  // every thread has read sh
     if (lane == 0) sh[wave] = amax;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (t == 0) {
         const float mx = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
         int s = 0;
         if (mx > 0.0f && mx <= 3.0e38f) {
@@ -205,14 +205,37 @@ __global__ __launch_bounds__(256) void a_rows_norm_f32_to_f16_kernel(const float
     }
     __syncthreads();
     const float scale = __builtin_amdgcn_ldexpf(1.0f, ssig);
-    for (int k = threadIdx.x; k < Kp; k += 256) {
-        if (k < K) {
-            const float y = row[k] * inv * (weight_offset ? 1.0f + w[k] : w[k]);
-            out[k] = (_Float16)(y * scale);
-        } else {
-            out[k] = (_Float16)0.0f;
+    if (R > 0) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int k = t + 256 * j;
+            if (k < K) out[k] = (_Float16)(xv[R > 0 ? j : 0] * scale);
         }
+        for (int k = K + t; k < Kp; k += 256) out[k] = (_Float16)0.0f;  // K padding
+    } else {
+        for (int k = t; k < Kp; k += 256) out[k] = k < K ? (_Float16)(y_at(0, k) * scale) : (_Float16)0.0f;
     }
+}
+
+// Launch of the f32 pre-pass: the register form up to K = 256 x 48.
+void launch_a_rows_f32(const float *a, const float *w, float eps, int offset, _Float16 *a16, int *sig, int64_t m,
+                       int64_t k, int64_t kp, hipStream_t st) {
+    const int r = (int)((k + 255) / 256);
+#define DOE_A_ROWS(R)                                                                                          \
+    do {                                                                                                       \
+        if (w)                                                                                                 \
+            hipLaunchKernelGGL((a_rows_f32_kernel<R, true>), dim3((unsigned)m), dim3(256), 0, st, a, w, eps, offset, \
+                               a16, sig, (int)k, (int)kp);                                                     \
+        else                                                                                                   \
+            hipLaunchKernelGGL((a_rows_f32_kernel<R, false>), dim3((unsigned)m), dim3(256), 0, st, a, w, eps, offset, \
+                               a16, sig, (int)k, (int)kp);                                                     \
+    } while (0)
+    if (r <= 4) DOE_A_ROWS(4);
+    else if (r <= 12) DOE_A_ROWS(12);
+    else if (r <= 24) DOE_A_ROWS(24);
+    else if (r <= 48) DOE_A_ROWS(48);
+    else DOE_A_ROWS(0);
+#undef DOE_A_ROWS
 }
 
 // ---------------------------------------------------------------------------
@@ -863,12 +886,8 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     }
     _Float16 *a16 = (_Float16 *)ws;
     int *sig = (int *)((char *)ws + a16_bytes);
-    if (a_f32 && fu.norm_w)
-        hipLaunchKernelGGL(a_rows_norm_f32_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, (const float *)a,
-                           fu.norm_w, fu.norm_eps, fu.norm_offset, a16, sig, (int)k, (int)kp);
-    else if (a_f32)
-        hipLaunchKernelGGL(a_rows_f32_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, (const float *)a, a16, sig,
-                           (int)k, (int)kp);
+    if (a_f32)
+        launch_a_rows_f32((const float *)a, fu.norm_w, fu.norm_eps, fu.norm_offset, a16, sig, m, k, kp, st);
     else
         hipLaunchKernelGGL(a_rows_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, a_bf16, a16, sig, (int)k,
                            (int)kp);
