@@ -25,6 +25,7 @@
 #include "common.h"
 
 #include <math.h>
+#include <mutex>
 
 namespace {
 
@@ -60,6 +61,12 @@ struct MqArgs {
     int num_heads, num_kv_heads, heads_per_wg, query_len, seq_len, capacity;
     int start_pos, kv_start, causal, window, kv_map, ring, page_size, page_table_len;
     float scale, softcap;
+    // key split (splits > 1, grid z): split z walks its share of the query
+    // block's key blocks and writes the unnormalised (o, m, l) of each row to
+    // ws_o [z][query][head][D] and ws_ml [z][query][head][2]; a second kernel
+    // merges them
+    int splits;
+    float *ws_o, *ws_ml;
 };
 
 constexpr int kKeys = 32;  // keys per block
@@ -129,6 +136,72 @@ __global__ __launch_bounds__(NTH) void attn_mq_kernel(MqArgs a) {
                                     : (a.kv_map == 2 ? (long)a.page_table_len * a.page_size : (1L << 24));
     const int L = (int)min(lmax, (long)(a.kv_len_dev ? a.kv_len_dev[0] : (uint32_t)a.seq_len));
 
+    // Per-row key ranges of this lane's four rows, and the union over the 16
+    // queries (the same for every head of the workgroup).
+    int rlo[4], rhi[4];
+    int ulo = 1 << 30, uhi = 0;
+    for (int i = 0; i < 16; ++i) {
+        int lo, hi;
+        key_range(a, L, (long)a.start_pos + q0 + i, lo, hi);
+        const bool valid = q0 + i < a.query_len;
+        if (valid && hi > lo) {
+            ulo = min(ulo, lo);
+            uhi = max(uhi, hi);
+        }
+        if ((i >> 2) == g4) {
+            rlo[i & 3] = valid ? lo : 0;
+            rhi[i & 3] = valid ? hi : 0;
+        }
+    }
+    const float log2e = 1.4426950408889634f;
+    const _Float16 *kb = a.k + (size_t)kvh * a.head_stride;
+    const _Float16 *vb = a.v + (size_t)kvh * a.head_stride;
+    const _Float16 *qh = qs + (size_t)(wave * 2 + 0) * 16 * QROW;
+    const _Float16 *ql = qs + (size_t)(wave * 2 + 1) * 16 * QROW;
+    _Float16 *pw = ps + (size_t)wave * 16 * PROW;
+
+    // pieces [i0, i0 + n) of the block at p0: global -> registers -> LDS
+    auto fetch = [&](int p0, int i0, int n, h8 *kd, h8 *vd) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+            const int c = tid + (i0 + i) * NTH;
+            const int key = c % kKeys, d0 = (c / kKeys) * 8;
+            const int p = p0 + key;
+            h8 kv = h8{0, 0, 0, 0, 0, 0, 0, 0}, vv = kv;
+            if (c < PIECES && p < L) {
+                const long row = cache_row(a, p);
+                kv = *reinterpret_cast<const h8 *>(kb + row * a.row_stride + d0);
+                vv = *reinterpret_cast<const h8 *>(vb + row * a.row_stride + d0);
+            }
+            kd[i] = kv;
+            vd[i] = vv;
+        }
+    };
+    auto put = [&](int i0, int n, const h8 *kd, const h8 *vd) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+            const int c = tid + (i0 + i) * NTH;
+            if (c < PIECES) {
+                const int key = c % kKeys, d0 = (c / kKeys) * 8;
+                *reinterpret_cast<h8 *>(ks + (size_t)key * KROW + d0) = kd[i];
+                // consecutive lanes hold consecutive keys: each V^T row's
+                // writes land in consecutive halves
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vt[(size_t)(d0 + e) * VROW + key] = vd[i][e];
+            }
+        }
+    };
+    // this split's key blocks: a contiguous share of the union's blocks
+    int p0 = (ulo / kKeys) * kKeys;
+    if (a.splits > 1 && p0 < uhi) {
+        const int nblk = (uhi - p0 + kKeys - 1) / kKeys, per = (nblk + a.splits - 1) / a.splits;
+        const int b0 = (int)blockIdx.z * per;
+        uhi = min(uhi, p0 + (b0 + per) * kKeys);
+        p0 += b0 * kKeys;
+    }
+    // the first block's loads go out before Q is read and staged
+    h8 kr[PF], vr[PF];
+    if (p0 < uhi) fetch(p0, 0, PF, kr, vr);
     // Q: 4 lanes per query, D / 4 dims each; per-row power-of-two scale, hi/lo.
     {
         const int i = lane >> 2, part = lane & 3;
@@ -171,23 +244,6 @@ __global__ __launch_bounds__(NTH) void attn_mq_kernel(MqArgs a) {
         if (part == 0) qinv[wave * 16 + i] = __builtin_amdgcn_ldexpf(1.0f, -sg);
     }
 
-    // Per-row key ranges of this lane's four rows, and the union over the 16
-    // queries (the same for every head of the workgroup).
-    int rlo[4], rhi[4];
-    int ulo = 1 << 30, uhi = 0;
-    for (int i = 0; i < 16; ++i) {
-        int lo, hi;
-        key_range(a, L, (long)a.start_pos + q0 + i, lo, hi);
-        const bool valid = q0 + i < a.query_len;
-        if (valid && hi > lo) {
-            ulo = min(ulo, lo);
-            uhi = max(uhi, hi);
-        }
-        if ((i >> 2) == g4) {
-            rlo[i & 3] = valid ? lo : 0;
-            rhi[i & 3] = valid ? hi : 0;
-        }
-    }
     __syncthreads();
     float rowf[4];  // score scale of each row: scale / (the row's Q scale)
 #pragma unroll
@@ -202,47 +258,6 @@ __global__ __launch_bounds__(NTH) void attn_mq_kernel(MqArgs a) {
         m[r] = -INFINITY;
         l[r] = 0.0f;
     }
-    const float log2e = 1.4426950408889634f;
-    const _Float16 *kb = a.k + (size_t)kvh * a.head_stride;
-    const _Float16 *vb = a.v + (size_t)kvh * a.head_stride;
-    const _Float16 *qh = qs + (size_t)(wave * 2 + 0) * 16 * QROW;
-    const _Float16 *ql = qs + (size_t)(wave * 2 + 1) * 16 * QROW;
-    _Float16 *pw = ps + (size_t)wave * 16 * PROW;
-
-    // pieces [i0, i0 + n) of the block at p0: global -> registers -> LDS
-    auto fetch = [&](int p0, int i0, int n, h8 *kd, h8 *vd) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < n; ++i) {
-            const int c = tid + (i0 + i) * NTH;
-            const int key = c % kKeys, d0 = (c / kKeys) * 8;
-            const int p = p0 + key;
-            h8 kv = h8{0, 0, 0, 0, 0, 0, 0, 0}, vv = kv;
-            if (c < PIECES && p < L) {
-                const long row = cache_row(a, p);
-                kv = *reinterpret_cast<const h8 *>(kb + row * a.row_stride + d0);
-                vv = *reinterpret_cast<const h8 *>(vb + row * a.row_stride + d0);
-            }
-            kd[i] = kv;
-            vd[i] = vv;
-        }
-    };
-    auto put = [&](int i0, int n, const h8 *kd, const h8 *vd) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < n; ++i) {
-            const int c = tid + (i0 + i) * NTH;
-            if (c < PIECES) {
-                const int key = c % kKeys, d0 = (c / kKeys) * 8;
-                *reinterpret_cast<h8 *>(ks + (size_t)key * KROW + d0) = kd[i];
-                // consecutive lanes hold consecutive keys: each V^T row's
-                // writes land in consecutive halves
-#pragma unroll
-                for (int e = 0; e < 8; ++e) vt[(size_t)(d0 + e) * VROW + key] = vd[i][e];
-            }
-        }
-    };
-    h8 kr[PF], vr[PF];
-    int p0 = (ulo / kKeys) * kKeys;
-    if (p0 < uhi) fetch(p0, 0, PF, kr, vr);
     for (; p0 < uhi; p0 += kKeys) {
         __syncthreads();  // every wave is done with the previous block
         put(0, PF, kr, vr);
@@ -313,12 +328,47 @@ __global__ __launch_bounds__(NTH) void attn_mq_kernel(MqArgs a) {
     for (int r = 0; r < 4; ++r) {
         const int qi = q0 + 4 * g4 + r;
         if (qi >= a.query_len) continue;
+        if (a.splits > 1) {
+            const size_t pr = ((size_t)blockIdx.z * a.query_len + qi) * a.num_heads + head;
+            float *dst = a.ws_o + pr * D + c16;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) dst[16 * t] = o[t][r];
+            if (c16 == 0) *reinterpret_cast<float2 *>(a.ws_ml + 2 * pr) = make_float2(m[r], l[r]);
+            continue;
+        }
         const float inv = l[r] > 0.0f ? 1.0f / l[r] : 0.0f;
         float *dst = a.out + (size_t)qi * a.out_row_stride + (size_t)head * D + c16;
 #pragma unroll
         for (int t = 0; t < NT; ++t) dst[16 * t] = o[t][r] * inv;
     }
 }
+
+// The key splits of one (query, head) row merged: M = max m_s, L = sum l_s
+// 2^(m_s - M), out = sum o_s 2^(m_s - M) / L (zero where no key was visible).
+__global__ __launch_bounds__(512) void attn_mq_combine_kernel(MqArgs a, int D) {
+    const int row = blockIdx.x, qi = row / a.num_heads, head = row - qi * a.num_heads, d = threadIdx.x;
+    const size_t stride = (size_t)a.query_len * a.num_heads;
+    float M = -INFINITY;
+    for (int z = 0; z < a.splits; ++z) M = fmaxf(M, a.ws_ml[2 * (z * stride + row)]);
+    float L = 0.0f, O = 0.0f;
+    if (M != -INFINITY) {
+        for (int z = 0; z < a.splits; ++z) {
+            const float2 ml = *reinterpret_cast<const float2 *>(a.ws_ml + 2 * (z * stride + row));
+            const float f = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - M);
+            L = fmaf(ml.y, f, L);
+            O = fmaf(a.ws_o[(z * stride + row) * D + d], f, O);
+        }
+    }
+    a.out[(size_t)qi * a.out_row_stride + (size_t)head * D + d] = L > 0.0f ? O / L : 0.0f;
+}
+
+// Key-split partials: a library-owned grow-only workspace (see the header's
+// workspace rule), and the split count (0 automatic, n > 0 forced).
+std::mutex g_mq_mu;
+void *g_mq_ws = nullptr;
+size_t g_mq_ws_bytes = 0;
+int g_mq_cus = 0;
+int g_mq_splits = 0;
 
 template <int D>
 int launch_mq(const MqArgs &a0, hipStream_t st) {
@@ -328,6 +378,47 @@ int launch_mq(const MqArgs &a0, hipStream_t st) {
     while (hg > 1 && G % hg) hg >>= 1;
     if (hg > G) hg = G;
     a.heads_per_wg = hg;
+    // Key split: a short prompt gives few workgroups (a 128-token prompt of
+    // 4 kv heads: 32), whose last query blocks walk every key block in turn;
+    // split the key blocks over the grid until about two workgroups per CU
+    // (host-known key counts only: a device length keeps one split).
+    const int qblocks = (a.query_len + 15) / 16, ygrid = a.num_kv_heads * (G / hg);
+    if (g_mq_cus == 0) {
+        int dev = 0, cus = 0;
+        DOE_HIP_CHECK(hipGetDevice(&dev));
+        DOE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        g_mq_cus = cus > 0 ? cus : 256;
+    }
+    int splits = 1;
+    if (g_mq_splits > 0) {
+        splits = g_mq_splits;
+    } else if (!a.kv_len_dev) {
+        const long nkb = ((long)min(a.seq_len, a.capacity) + kKeys - 1) / kKeys;
+        const long base = (long)qblocks * ygrid;
+        if (nkb > 1 && base < g_mq_cus) {
+            long sp = 2L * g_mq_cus / base;
+            sp = sp < nkb ? sp : nkb;
+            splits = (int)(sp < 16 ? sp : 16);
+        }
+    }
+    a.splits = splits;
+    if (splits > 1) {
+        const size_t rows = (size_t)a.query_len * a.num_heads;
+        const size_t o_bytes = (size_t)splits * rows * D * 4, need = o_bytes + (size_t)splits * rows * 8;
+        std::lock_guard<std::mutex> lk(g_mq_mu);
+        if (g_mq_ws_bytes < need) {
+            if (g_mq_ws) {
+                DOE_HIP_CHECK(hipDeviceSynchronize());  // queued kernels may still use the old one
+                DOE_HIP_CHECK(hipFree(g_mq_ws));
+            }
+            g_mq_ws = nullptr;
+            g_mq_ws_bytes = 0;
+            DOE_HIP_CHECK(hipMalloc(&g_mq_ws, need));
+            g_mq_ws_bytes = need;
+        }
+        a.ws_o = (float *)g_mq_ws;
+        a.ws_ml = (float *)((char *)g_mq_ws + o_bytes);
+    }
     const size_t lds = MqLds<D>::bytes(hg);
     static const hipError_t attr_rc = [] {
         hipError_t e = hipSuccess;
@@ -338,7 +429,7 @@ int launch_mq(const MqArgs &a0, hipStream_t st) {
     }();
     DOE_HIP_CHECK(attr_rc);
     DOE_REQUIRE(lds <= 160 * 1024, DOE_E_UNSUPPORTED, "attention needs %zu bytes of LDS", lds);
-    const dim3 grid((unsigned)((a.query_len + 15) / 16), (unsigned)(a.num_kv_heads * (G / hg)), 1);
+    const dim3 grid((unsigned)qblocks, (unsigned)ygrid, (unsigned)splits);
     switch (hg) {
         case 1: hipLaunchKernelGGL((attn_mq_kernel<D, 64>), grid, dim3(64), lds, st, a); break;
         case 2: hipLaunchKernelGGL((attn_mq_kernel<D, 128>), grid, dim3(128), lds, st, a); break;
@@ -346,6 +437,10 @@ int launch_mq(const MqArgs &a0, hipStream_t st) {
         default: hipLaunchKernelGGL((attn_mq_kernel<D, 512>), grid, dim3(512), lds, st, a); break;
     }
     DOE_LAUNCH_CHECK("attn_mq_kernel");
+    if (splits > 1) {
+        hipLaunchKernelGGL(attn_mq_combine_kernel, dim3((unsigned)(a.query_len * a.num_heads)), dim3(D), 0, st, a, D);
+        DOE_LAUNCH_CHECK("attn_mq_combine_kernel");
+    }
     return DOE_OK;
 }
 
@@ -375,6 +470,12 @@ int mq_impl(MqArgs a, int64_t head_dim, hipStream_t st) {
 }  // namespace
 
 namespace doe {
+
+int mq_set_splits(int value) {
+    DOE_REQUIRE(value >= 0 && value <= 16, DOE_E_INVALID, "attn_mq.splits is 0..16");
+    g_mq_splits = value;
+    return DOE_OK;
+}
 
 // The query_len > 1 form of doe_attention_dispatch (the reference's own
 // uniforms; K/V [capacity][num_kv_heads][head_dim]).

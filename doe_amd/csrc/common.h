@@ -32,6 +32,7 @@ int attention_dispatch_mq(const doe_attention_uniforms *u, const float *q, const
 int attn_scratch_setup(int device);
 // Tuning hooks of individual kernels (0 = automatic).
 int attn_set_splits(int value);
+int mq_set_splits(int value);
 int attn_set_waves(int value);
 int int4_set_kernel(int value);
 int q8_0_set_tune(const char *key, int value);  // "q8_0_gemv.rows" / ".depth"

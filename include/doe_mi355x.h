@@ -348,7 +348,10 @@ int doe_attention_dispatch(const doe_attention_uniforms *u, const float *q, cons
  * output f32 rows of out_row_stride floats; sliding_window > 0 keeps the
  * last sliding_window keys of each query, softcap > 0 caps the scores.  The
  * prefill `attention` step of a step graph's prompt (gemma-3-270m-smoke.json
- * prefill; attention_head256_f16kv.wgsl:72-267 with is_causal). */
+ * prefill; attention_head256_f16kv.wgsl:72-267 with is_causal).  A short
+ * prompt splits its key blocks over the grid and merges the splits in a
+ * second kernel, through a library-owned grow-only workspace (the workspace
+ * rule of doe_attn_decode). */
 int doe_attn_prefill_f16kv(const float *q, int64_t q_row_stride, const uint16_t *k_cache,
                            const uint16_t *v_cache, float *output, int64_t out_row_stride,
                            int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
@@ -512,9 +515,11 @@ int doe_decode_advance(int32_t *state, int32_t *token, int32_t *ids, int64_t max
 /* ---- tuning ----------------------------------------------------------------
  * Overrides a kernel launch-shape choice (0 restores the automatic choice).
  * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows", "q4k_gemv.stream" (v > 0: the
- * streaming GEMV walking v row groups per workgroup), "q8_0_gemv.rows" (1, 2 or 4
- * rows per wave group), "q8_0_gemv.depth" (1 or 2 blocks loaded ahead),
- * "attn_decode.splits",
+ * streaming GEMV walking v row groups per workgroup, -1: never streaming),
+ * "q4k_gemv.stream_depth" (2, 3, 4 or 6 units in flight per wave),
+ * "q8_0_gemv.rows" (1, 2 or 4 rows per wave group), "q8_0_gemv.depth" (1 or
+ * 2 blocks loaded ahead), "attn_mq.splits" (1..16 key splits of the
+ * multi-query attention), "attn_decode.splits",
  * "attn_decode.waves" (4: narrow workgroups; 8 or 16: the wide short-context
  * workgroup where the head shape allows it).  No
  * reference counterpart:

@@ -155,11 +155,22 @@ def test_dispatch_ring_and_pages_are_storage_invariant(dev):
     assert rel_l2(o_last.download()[0], o_flat.download()[-1]) < 1e-3
 
 
+@pytest.fixture
+def mq_splits(request, dev):
+    """Forces the multi-query attention's key split (attn_mq.splits; 0 the
+    automatic choice, 1 none) and restores the automatic choice."""
+    ops.tune("attn_mq.splits", request.param)
+    yield request.param
+    ops.tune("attn_mq.splits", 0)
+
+
+@pytest.mark.parametrize("mq_splits", [0, 1, 2, 3, 5], indirect=True)
 @pytest.mark.parametrize("hq,hkv,d", [(8, 4, 256), (4, 1, 512), (2, 1, 64)])
-def test_prefill_f16kv_decoder_layout(dev, ora, hq, hkv, d):
+def test_prefill_f16kv_decoder_layout(dev, ora, hq, hkv, d, mq_splits):
     # the decoder's cache ([kv_head][max_seq][dim]) and the q part of fused
     # q/k/v rows (row stride q + 2 kv dims): a prompt continuing at position
-    # 10, window 12, softcap 30
+    # 10, window 12, softcap 30; the key blocks split 1..5 ways over the grid
+    # (5: more splits than key blocks, some empty) and merged
     rng = np.random.default_rng(d + hq)
     ql, start, maxs, window, softcap = 33, 10, 64, 12, 30.0
     L = start + ql
@@ -178,5 +189,5 @@ def test_prefill_f16kv_decoder_layout(dev, ora, hq, hkv, d):
     want = oracle_rows(ora, q, krows, vrows, hq, hkv, d, L, start, 0, 1, window, scale, softcap)
     got = out.download()[:, : hq * d].reshape(ql, hq, d)
     err = rel_l2(got, want)
-    print(f"[mq decoder layout {hq}/{hkv}x{d}] rel_l2 {err:.2e}", flush=True)
+    print(f"[mq decoder layout {hq}/{hkv}x{d} splits {mq_splits}] rel_l2 {err:.2e}", flush=True)
     assert err <= 1e-3, err
