@@ -32,8 +32,15 @@ COMMON_FLAGS = [
 ]
 
 
+# per-source additions: the int4 GEMV keeps its MFMA results in VGPRs (no
+# accumulator-register reads between each MFMA and the scale FMAs that use it)
+FILE_FLAGS = {
+    "int4_gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path, obj: Path) -> tuple[Path, str]:
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{proc.stdout}{proc.stderr}")

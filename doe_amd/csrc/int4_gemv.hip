@@ -8,27 +8,31 @@
 //
 // One v_mfma_f32_16x16x32_f16 per (16 rows, one 32-element group):
 //   * A = the x image: 16 columns = the eight batch rows' x_hi and x_lo (x
-//     scaled per batch row by a power of two so its max sits near 2^14, split
-//     into two f16), in the k order of B below;
+//     scaled per batch row by a power of two so its max over the wave's K
+//     range sits near 2^14, split into two f16), in the k order of B below;
 //   * B = the nibbles of one u32 per lane as f16 subnormals with ANDs only:
-//     w & 0x000F000F holds nibbles 0 and 4 as q * 2^-24, w & 0x00F000F0 nibbles
-//     1 and 5 as q * 2^-20 (the image holds x / 16 there, exact), and the same
-//     of w >> 8 nibbles 2, 6 and 3, 7: every product is exact;
-//   * D + C, C = -8 * 2^-24 * sum(x) of the group in the x_hi columns, is
-//     2^-24 * sum((q - 8) x).
+//     w & 0x000F000F holds nibbles 0 and 4 as q * 2^-24, w & 0x00F000F0
+//     nibbles 1 and 5 as q * 2^-20 (the image holds x / 16 there), and the
+//     same of w >> 8 nibbles 2, 6 and 3, 7: every product is exact and
+//     D = 2^-24 * sum(q x) of the group.
 // D lands with lane (row, column group) holding four batch columns of one
-// row: one f16 scale (v_fma_mix) serves all four.  The power-of-two unscale
-// per batch row and the hi + lo sum (one cross-half lane swap) come at the
-// end.
+// row: one f16 scale (v_fma_mix) serves all four.  The -8 of (q - 8) is one
+// more MFMA per 16-row tile over the wave's eight groups: A = the group sums
+// of each image column (from an MFMA of the image against ones, split into
+// f16 hi and lo parts), B = the rows' f16 scales, so D_c = sum_g s * sum(x)
+// and y = 2^-24 (sum_g s D_g - 8 D_c).  The power-of-two unscale per (wave,
+// batch row) and the hi + lo sum (one cross-half lane swap) come at the end.
 //
-// A pre-pass (one workgroup per batch row and 64 groups) finds the row's max |x| and writes
-// the image ([group][64 lanes][8 f16], 1 KB per group), the corrections
-// ([group][16] f32) and the row's scale exponent.  A workgroup of the GEMV
-// owns 64 rows (four 16-row tiles per wave, so an image fragment feeds four
-// MFMAs) and 32 groups of K, eight per wave with every load of a wave issued
-// up front; the four waves' sums meet in LDS.  K is split over the grid's y
-// dimension into 32-group ranges whose sums are added atomically into y (the
-// pre-pass clears it), so the f32 summation order varies from run to run.
+// Each wave builds the image of its own K range from x in its prologue (lane
+// (column c, quarter kg) loads the eight x of its batch row c % 8 and group
+// quarter, the max over the range meets in two lane swaps): the x loads go
+// out first, then the weight loads, and the image is built while those are in
+// flight.  A workgroup of the one-shot kernel owns 64 rows (four 16-row tiles
+// per wave, so an image fragment feeds four MFMAs) and 32 groups of K, eight
+// per wave with every load of a wave issued up front; the four waves' sums
+// meet in LDS.  When K spans more than one workgroup's 32 groups, the grid
+// splits K: each range writes its partial sums to a workspace and a second
+// kernel adds the ranges in order, so y is the same bit for bit on every run.
 #include "common.h"
 
 #include <math.h>
@@ -42,87 +46,7 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxBatch = 8;
-
-// Pre-pass: workgroup (b, p) = batch row b (rows >= M write zeros), groups
-// [64 p, 64 p + 64); every part of a row finds the row's maximum itself (the
-// same exact value, so the same exponent).  When the GEMV splits K (atomic
-// partial sums), the parts also clear y[b].
-constexpr int kImgThreads = 256;
-constexpr int kImgGroups = 64;  // groups per workgroup: one item per thread
-__global__ __launch_bounds__(kImgThreads) void int4_x_image_kernel(const float *__restrict__ x,
-                                                                   _Float16 *__restrict__ img,
-                                                                   float *__restrict__ corr,
-                                                                   int *__restrict__ sig_out,
-                                                                   float *__restrict__ y_clear,
-                                                                   int M, int N, int K) {
-    __shared__ float wmax[kImgThreads / 64];
-    const int b = blockIdx.x, part = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
-    if (y_clear && b < M) {
-        const int chunk = (N + (int)gridDim.y - 1) / (int)gridDim.y, i1 = min(N, (part + 1) * chunk);
-        for (int i = part * chunk + tid; i < i1; i += kImgThreads) y_clear[(size_t)b * N + i] = 0.0f;
-    }
-    const int G = K / 32;
-    const int g0 = part * kImgGroups, g1 = min(G, g0 + kImgGroups);
-    const bool live = b < M;
-    const float *xr = x + (size_t)(live ? b : 0) * K;
-    float amax = 0.0f;
-    if (live)
-#pragma unroll 8
-        for (int k4 = tid; k4 < K / 4; k4 += kImgThreads) {  // eight loads in flight per thread
-            const float4 v = reinterpret_cast<const float4 *>(xr)[k4];
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        }
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    if (lane == 0) wmax[tid >> 6] = amax;
-    __syncthreads();
-    amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kImgThreads / 64; ++i) amax = fmaxf(amax, wmax[i]);
-    int sig = 0;
-    if (amax > 0.0f && amax <= 3.0e38f) {
-        sig = 14 - __builtin_amdgcn_frexp_expf(amax);
-        sig = sig < -120 ? -120 : (sig > 120 ? 120 : sig);
-    }
-    if (tid == 0 && part == 0) sig_out[b] = sig;
-    const float sc = __builtin_amdgcn_ldexpf(1.0f, sig);
-    // item (g, kg): eight consecutive x, four items per group in one quad
-    for (int item = g0 * 4 + tid; item < g1 * 4; item += kImgThreads) {
-        const int g = item >> 2, kg = item & 3;
-        float v[8];
-        if (live) {
-            const float4 p0 = reinterpret_cast<const float4 *>(xr + 32 * g + 8 * kg)[0];
-            const float4 p1 = reinterpret_cast<const float4 *>(xr + 32 * g + 8 * kg)[1];
-            v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-        }
-        float sum = 0.0f;
-        half8 hi, lo;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            // slot j: nibble (j / 2) + 4 (j % 2) ... in B's order n0 n4 n1 n5 n2 n6 n3 n7
-            const int nib = (j >> 1) + 4 * (j & 1);
-            const float t = v[nib] * sc;
-            sum += t;
-            const _Float16 h = (_Float16)t, l = (_Float16)(t - (float)h);
-            // slots 2, 3, 6, 7 meet nibbles coded at bits 4..7 (x 16): store x / 16
-            const bool odd = (j & 2) != 0;
-            hi[j] = odd ? (_Float16)((float)h * 0.0625f) : h;
-            lo[j] = odd ? (_Float16)((float)l * 0.0625f) : l;
-        }
-        _Float16 *base = img + (size_t)g * 512;
-        *reinterpret_cast<half8 *>(base + (kg * 16 + b) * 8) = hi;
-        *reinterpret_cast<half8 *>(base + (kg * 16 + 8 + b) * 8) = lo;
-        // the group's sum over its four quads (consecutive threads)
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        if (kg == 0) {
-            corr[g * 16 + b] = -8.0f * 5.9604644775390625e-08f * sum;  // -8 * 2^-24 * sum(x)
-            corr[g * 16 + 8 + b] = 0.0f;
-        }
-    }
-}
+constexpr int kGpw = 8;  // groups per wave: one 16-byte scale load per row covers them
 
 // B operand of one word: halves (n0, n4, 16 n1, 16 n5, n2, n6, 16 n3, 16 n7) * 2^-24.
 __device__ __forceinline__ half8 unpack_int4(uint32_t w) {
@@ -130,69 +54,167 @@ __device__ __forceinline__ half8 unpack_int4(uint32_t w) {
     return __builtin_bit_cast(half8, u32x4{w & 0x000f000fu, w & 0x00f000f0u, w8 & 0x000f000fu, w8 & 0x00f000f0u});
 }
 
+// f16 hi / lo split of two floats, packed: hi = RTZ(t), lo = RTZ(t - hi);
+// |t - hi| is below one f16 ulp of t, so hi + lo carries 21+ bits of t.
+__device__ __forceinline__ void split_pair(const float t0, const float t1, uint32_t &hi, uint32_t &lo) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(t0, t1);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(t0 - (float)h[0], t1 - (float)h[1]));
+}
+
 struct Int4Args {
     const uint32_t *q;
     const uint16_t *scales;
-    const _Float16 *img;
-    const float *corr;
-    const int *sig;
-    float *out;  // y [M][N] (K splits add atomically into y, cleared by the pre-pass)
+    const float *x;  // [M][K]
+    float *out;      // one K range: y [M][N]; else the ranges' partial sums
+    float *y;        // [M][N]
+    unsigned *cnt;   // one-shot kernel, K split: ranges done per row block (zero between calls)
     int M, N, K, G;
 };
 
-// 64 rows x (4 GPW) groups per workgroup; wave w takes groups
-// [blockIdx.y 4 GPW + w GPW, + GPW).  A row's GPW groups are GPW * 16
-// contiguous bytes: the wave reads them with whole-line 16-byte loads (GPW
+// s_waitcnt vmcnt(0) (every load and store of the wave complete), as the
+// compiler's own wait so that it tracks it; the empty asm keeps memory
+// operations on their side of it.
+__device__ __forceinline__ void wait_memory() {
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8) | (0 << 14));
+    asm volatile("" ::: "memory");
+}
+
+// The x image of the wave's kGpw groups from group gb: lane (c = lane & 15,
+// kg = lane >> 4) holds the A fragment of column c -- batch row c % 8, x_hi
+// for c < 8 and x_lo for c >= 8 -- over elements 8 kg .. 8 kg + 7 of each
+// group, in B's slot order n0 n4 n1 n5 n2 n6 n3 n7 (slots 2, 3, 6, 7 meet
+// nibbles coded at bits 4..7 (x 16): they hold x / 16).  Rows past M and
+// inactive waves hold zeros.  x_load issues the lane's loads (before the
+// weights', so that the image is built while those are in flight); x_image
+// builds the fragments and returns the lane's batch-row exponent: x was
+// scaled by 2^sig.
+__device__ __forceinline__ void x_load(const Int4Args &a, const int gb, const int lane, float v[kGpw][8]) {
+    const int c = lane & 15, kg = lane >> 4, b = c & 7;
+    const float *xr = a.x + (size_t)(b < a.M ? b : 0) * a.K + 32 * gb + 8 * kg;
+#pragma unroll
+    for (int u = 0; u < kGpw; ++u) {
+        const float4 p0 = reinterpret_cast<const float4 *>(xr + 32 * u)[0];
+        const float4 p1 = reinterpret_cast<const float4 *>(xr + 32 * u)[1];
+        v[u][0] = p0.x; v[u][1] = p0.y; v[u][2] = p0.z; v[u][3] = p0.w;
+        v[u][4] = p1.x; v[u][5] = p1.y; v[u][6] = p1.z; v[u][7] = p1.w;
+    }
+}
+
+__device__ __forceinline__ int x_image(const Int4Args &a, const bool active, const int lane,
+                                       const float v[kGpw][8], half8 xa[kGpw], half8 &ac) {
+    const int c = lane & 15, kg = lane >> 4;
+    const bool live = active && (c & 7) < a.M;
+    float amax = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kGpw; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[u][j]));
+    // the four quarters of the range hold batch row c % 8 in lanes c, c + 16, ...
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    int sig = 0;
+    if (live && amax > 0.0f && amax <= 3.0e38f) {
+        sig = 14 - __builtin_amdgcn_frexp_expf(amax);
+        sig = sig < -120 ? -120 : (sig > 120 ? 120 : sig);
+    }
+    // columns of rows past M are zero (or NaN from x * 0 where row 0 holds an
+    // infinity): every later step keeps columns apart, and they are never stored
+    const float sc = live ? __builtin_amdgcn_ldexpf(1.0f, sig) : 0.0f, sc16 = sc * 0.0625f;
+    const bool lo = c >= 8;
+#pragma unroll
+    for (int u = 0; u < kGpw; ++u) {
+        uint32_t d[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            // slots 2p, 2p + 1 hold nibbles p and p + 4; pairs 1 and 3 take x / 16
+            uint32_t h, l;
+            const float s_ = (p & 1) ? sc16 : sc;
+            split_pair(v[u][p] * s_, v[u][p + 4] * s_, h, l);
+            d[p] = lo ? l : h;
+        }
+        xa[u] = __builtin_bit_cast(half8, u32x4{d[0], d[1], d[2], d[3]});
+    }
+    // A of the correction MFMA: lane (c, kg) holds, for groups u = 0..7, the
+    // image column c's group sum times 2^-8 (f16 hi parts in quarter 0, lo
+    // parts in quarter 1, zeros in quarters 2 and 3).  The sums come from
+    // D[m][c] = sum_k ones[m][k] img[c][k] (ones = 16 on the x / 16 slots),
+    // which lands column c in lanes c, c + 16, ...
+    const half8 ones = {1, 1, 16, 16, 1, 1, 16, 16};
+    float sx[kGpw];
+#pragma unroll
+    for (int u = 0; u < kGpw; ++u) {
+        const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        sx[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, xa[u], zero, 0, 0, 0)[0] * 0.00390625f;
+    }
+    uint32_t hc[4], lc[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) split_pair(sx[2 * p], sx[2 * p + 1], hc[p], lc[p]);
+    const u32x4 zw = {0u, 0u, 0u, 0u};
+    ac = __builtin_bit_cast(half8, kg == 0 ? u32x4{hc[0], hc[1], hc[2], hc[3]}
+                                          : (kg == 1 ? u32x4{lc[0], lc[1], lc[2], lc[3]} : zw));
+    return sig;
+}
+
+// Exponents of the four batch columns 4 lg + i (i < 4) a lane's D holds:
+// batch 4 (lg & 1) + i, whose exponent lane c = batch of the image holds.
+__device__ __forceinline__ void column_exponents(const int sig, const int lg, int e[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = 24 - __shfl(sig, 4 * (lg & 1) + i, 64);
+}
+
+// 64 rows x (4 kGpw) groups per workgroup: workgroup i takes row block
+// i / ranges and K range sp = i % ranges (the ranges of one row block run
+// side by side, so the row's bytes are read together), wave w the groups
+// [sp 4 kGpw + w kGpw, + kGpw).  A row's kGpw groups are kGpw * 16
+// contiguous bytes: the wave reads them with whole-line 16-byte loads (kGpw
 // lanes per row) and regroups them through its own LDS slice into the MFMA
-// lane order (lane (r, j) takes word j of each group of row r).
-template <int GPW>
-__global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
-    static_assert(GPW == 8, "one 16-byte scale load per row tile covers eight groups");
+// lane order (lane (r, j) takes word j of each group of row r).  More than
+// one range: the range's sums go to out[sp][M][N].
+__global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a, int ranges) {
     __shared__ float red[3][4][4][64];
-    __shared__ __attribute__((aligned(16))) uint32_t wl[4][64 * 4 * GPW];
+    __shared__ __attribute__((aligned(16))) uint32_t wl[4][64 * 4 * kGpw];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int r0 = blockIdx.x * 64;
-    const int g0 = (blockIdx.y * 4 + wave) * GPW;
-    const bool active = g0 < a.G;  // a.G is a multiple of GPW
+    const int rb = blockIdx.x / ranges, sp = blockIdx.x - rb * ranges;
+    const int r0 = rb * 64;
+    const int g0 = (sp * 4 + wave) * kGpw;
+    const bool active = g0 < a.G;  // a.G is a multiple of kGpw
     const int gb = active ? g0 : 0;
 
-    // all loads first: the x image fragments and corrections (L2-resident),
-    // the scales of this lane's rows, then the 64 rows' weight bytes
-    half8 xa[GPW];
-    float4v cz[GPW];
-#pragma unroll
-    for (int u = 0; u < GPW; ++u) {
-        xa[u] = *reinterpret_cast<const half8 *>(a.img + ((size_t)(gb + u) * 64 + lane) * 8);
-        cz[u] = *reinterpret_cast<const float4v *>(a.corr + (gb + u) * 16 + 4 * lg);
-    }
+    // x (L2-resident after the first workgroups), then the scales and weight
+    // bytes (HBM); the image is built while the weights are in flight
+    float xv[kGpw][8];
+    x_load(a, gb, lane, xv);
     u32x4 sv[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
         sv[t] = *reinterpret_cast<const u32x4 *>(a.scales + (size_t)min(r0 + 16 * t + lr, a.N - 1) * a.G + gb);
-    constexpr int RPI = 64 / GPW;  // rows per load instruction
-    u32x4 wg[GPW];
+    constexpr int RPI = 64 / kGpw;  // rows per load instruction
+    u32x4 wg[kGpw];
 #pragma unroll
-    for (int j = 0; j < GPW; ++j) {
-        const int row = j * RPI + lane / GPW;
+    for (int j = 0; j < kGpw; ++j) {
+        const int row = j * RPI + lane / kGpw;
         wg[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
-            a.q + (size_t)min(r0 + row, a.N - 1) * (a.K / 8) + 4 * (gb + lane % GPW)));
+            a.q + (size_t)min(r0 + row, a.N - 1) * (a.K / 8) + 4 * (gb + lane % kGpw)));
     }
-    // regroup: wl[(row * 4 + word) * GPW + group]
+    half8 xa[kGpw], ac;
+    const int sig = x_image(a, active, lane, xv, xa, ac);
+    // regroup: wl[(row * 4 + word) * kGpw + group]
     uint32_t *my = wl[wave];
 #pragma unroll
-    for (int j = 0; j < GPW; ++j) {
-        const int row = j * RPI + lane / GPW, u = lane % GPW;
+    for (int j = 0; j < kGpw; ++j) {
+        const int row = j * RPI + lane / kGpw, u = lane % kGpw;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) my[(row * 4 + e) * GPW + u] = wg[j][e];
+        for (int e = 0; e < 4; ++e) my[(row * 4 + e) * kGpw + u] = wg[j][e];
     }
     // (each wave reads back only its own slice: no workgroup barrier needed)
-    uint32_t w[4][GPW];
+    uint32_t w[4][kGpw];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(my + ((16 * t + lr) * 4 + lg) * GPW);
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(my + ((16 * t + lr) * 4 + lg) * kGpw);
 #pragma unroll
-        for (int h = 0; h < GPW / 4; ++h) {
+        for (int h = 0; h < kGpw / 4; ++h) {
             const u32x4 v = src[h];
             w[t][4 * h] = v.x;
             w[t][4 * h + 1] = v.y;
@@ -209,21 +231,33 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
         for (int i = 0; i < 4; ++i) acc[t][i] = 0.0f;
     if (active) {
 #pragma unroll
-        for (int u = 0; u < GPW; ++u) {
+        for (int u = 0; u < kGpw; ++u) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                // (the correction is added after the product: as the MFMA's
-                // accumulator input it cost precision, rel-L2 1.9e-5 vs 4.8e-6)
                 const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
-                const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u], unpack_int4(w[t][u]), zero, 0, 0, 0) + cz[u];
+                const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u], unpack_int4(w[t][u]), zero, 0, 0, 0);
                 const uint32_t pair = sv[t][u >> 1];
                 const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)((u & 1) ? (pair >> 16) : pair));
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(s, d[i], acc[t][i]);
             }
         }
+        // the -8: sum_g s * sum(x) of the tile's rows, times -8 * 2^-24 * 2^8
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+            const float4v dc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac, __builtin_bit_cast(half8, sv[t]), zero, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(-0.0001220703125f, dc[i], acc[t][i]);
+        }
     }
-    // the four waves' partial sums meet in wave 0
+    // every wave unscales its own range (exact), then the four meet in wave 0
+    int e[4];
+    column_exponents(sig, lg, e);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = __builtin_amdgcn_ldexpf(acc[t][i], e[i]);
     if (wave > 0) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -233,20 +267,66 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a) {
     __syncthreads();
     if (wave > 0) return;
     // x_hi columns sit in lanes 0..31, x_lo in 32..63: one swap adds them
+    float yv[4][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float v = acc[t][i] + red[0][t][i][lane] + red[1][t][i][lane] + red[2][t][i][lane];
-            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-            v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-            const int b = 4 * lg + i, row = r0 + 16 * t + lr;
-            if (lg < 2 && b < a.M && row < a.N) {
-                const float r = __builtin_amdgcn_ldexpf(v, 24 - a.sig[b]);
-                if (gridDim.y > 1) atomicAdd(a.out + (size_t)b * a.N + row, r);  // y cleared by the pre-pass
-                else a.out[(size_t)b * a.N + row] = r;
-            }
+            const float v = ((acc[t][i] + red[0][t][i][lane]) + red[1][t][i][lane]) + red[2][t][i][lane];
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            yv[t][i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
         }
+    if (ranges == 1) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int b = 4 * lg + i, row = r0 + 16 * t + lr;
+                if (lg < 2 && b < a.M && row < a.N) a.y[(size_t)b * a.N + row] = yv[t][i];
+            }
+        return;
+    }
+    // K split: the range's 512 sums ([batch][64 rows]) go to its workspace
+    // slot with agent-scope stores (written through to memory); once they are
+    // complete the row block's count goes up, and the workgroup that completes
+    // it adds the ranges' slots in range order (agent-scope loads) into y and
+    // resets the count.  No workgroup waits for another.
+    float *slot = a.out + ((size_t)rb * ranges + sp) * 512;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (lg < 2) __hip_atomic_store(slot + (4 * lg + i) * 64 + 16 * t + lr, yv[t][i], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    wait_memory();
+    unsigned done = 0;
+    if (lane == 0) done = __hip_atomic_fetch_add(a.cnt + rb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    done = __builtin_amdgcn_readfirstlane(done);
+    if (done != (unsigned)(ranges - 1)) return;
+    asm volatile("" ::: "memory");
+    // lane l, step j: batch j, row r0 + l; eight ranges' loads in flight at a time
+    const float *base = a.out + (size_t)rb * ranges * 512 + lane;
+    float sum[8] = {};
+    for (int r0r = 0; r0r < ranges; r0r += 8) {
+        float v[8][8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                v[q][j] = r0r + q < ranges
+                              ? __hip_atomic_load(base + (size_t)(r0r + q) * 512 + 64 * j, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (r0r + q < ranges) sum[j] = (r0r + q == 0) ? v[q][j] : sum[j] + v[q][j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (j < a.M && r0 + lane < a.N) a.y[(size_t)j * a.N + r0 + lane] = sum[j];
+    if (lane == 0) __hip_atomic_store(a.cnt + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Lane (row, q) holds the four words of group g + q of its row (one 16-byte
@@ -264,46 +344,48 @@ __device__ __forceinline__ void quad_transpose(const u32x4 v, uint32_t out[4]) {
     out[3] = t23[1];
 }
 
-// Streaming form: a workgroup owns one K range of 4 GPW groups (wave w the
-// GPW groups from 4 GPW split + w GPW) and walks the row blocks
-// j, j + wps, j + 2 wps, ... of 64 rows.  The wave's x image fragments and
-// corrections are loaded once; each row block's weights and scales are loaded
-// while the previous block is computed (two register sets), straight into the
-// MFMA layout: lane (row, q) loads the 16 bytes of group 4h + q of its row
-// and a lane-quarter transpose hands every lane its word of each group.  The
-// four waves' sums meet in LDS (double-buffered, one barrier per block), each
-// wave summing and adding one 16-row tile into y.
-template <int GPW>
+// Streaming form: a workgroup owns one K range of 4 kGpw groups (wave w the
+// kGpw groups from 4 kGpw split + w kGpw) and walks the row blocks
+// j, j + wps, j + 2 wps, ... of 64 rows.  The wave's x image is built once;
+// each row block's weights and scales are loaded while the previous block is
+// computed (two register sets), straight into the MFMA layout: lane (row, q)
+// loads the 16 bytes of group 4h + q of its row and a lane-quarter transpose
+// hands every lane its word of each group.  The four waves' sums meet in LDS
+// (double-buffered, one barrier per block), each wave summing and storing one
+// 16-row tile of the range's sums (out[split][M][N] when K is split).
 __global__ __launch_bounds__(256, 2) void int4_gemv_stream_kernel(Int4Args a, int wps, int row_blocks) {
-    static_assert(GPW == 8, "one 16-byte scale load per row tile covers eight groups");
     __shared__ float red[2][4][4][4][64];  // [buffer][source wave][tile][column][lane]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const int sp = blockIdx.x / wps, j = blockIdx.x - sp * wps;
-    const int g0 = (sp * 4 + wave) * GPW;
-    const bool active = g0 < a.G;  // a.G is a multiple of GPW
+    const int g0 = (sp * 4 + wave) * kGpw;
+    const bool active = g0 < a.G;  // a.G is a multiple of kGpw
     const int gb = active ? g0 : 0;
+    float *out = a.G > 4 * kGpw ? a.out + (size_t)sp * a.M * a.N : a.y;
 
-    half8 xa[GPW];
-    float4v cz[GPW];
-#pragma unroll
-    for (int u = 0; u < GPW; ++u) {
-        xa[u] = *reinterpret_cast<const half8 *>(a.img + ((size_t)(gb + u) * 64 + lane) * 8);
-        cz[u] = *reinterpret_cast<const float4v *>(a.corr + (gb + u) * 16 + 4 * lg);
-    }
     const size_t row_words = (size_t)a.K / 8;
-    u32x4 wq[2][4][GPW / 4], sv[2][4];
+    u32x4 wq[2][4][kGpw / 4], sv[2][4];
     auto load = [&](const int set, const int rb) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int row = min(rb * 64 + 16 * t + lr, a.N - 1);
             sv[set][t] = *reinterpret_cast<const u32x4 *>(a.scales + (size_t)row * a.G + gb);
 #pragma unroll
-            for (int h = 0; h < GPW / 4; ++h)
+            for (int h = 0; h < kGpw / 4; ++h)
                 wq[set][t][h] = __builtin_nontemporal_load(
                     reinterpret_cast<const u32x4 *>(a.q + row * row_words + 4 * (gb + 4 * h + lg)));
         }
     };
+    int rb = j;
+    if (rb >= row_blocks) return;
+    float xv[kGpw][8];
+    x_load(a, gb, lane, xv);
+    load(0, rb);
+    half8 xa[kGpw], ac;
+    const int sig = x_image(a, active, lane, xv, xa, ac);
+    int e[4];
+    column_exponents(sig, lg, e);
+
     auto step = [&](const int cur, const int rb) __attribute__((always_inline)) {
         if (rb + wps < row_blocks) load(cur ^ 1, rb + wps);
         // acc[t][i]: row 64 rb + 16 t + lr, column 4 lg + i (batch (4 lg + i) % 8, hi for lg < 2)
@@ -316,28 +398,31 @@ __global__ __launch_bounds__(256, 2) void int4_gemv_stream_kernel(Int4Args a, in
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
 #pragma unroll
-                for (int h = 0; h < GPW / 4; ++h) {
+                for (int h = 0; h < kGpw / 4; ++h) {
                     uint32_t wv[4];
                     quad_transpose(wq[cur][t][h], wv);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int u = 4 * h + q;
-                        // (the correction is added after the product: as the MFMA's
-                        // accumulator input it cost precision, rel-L2 1.9e-5 vs 4.8e-6)
                         const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
-                        const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u], unpack_int4(wv[q]), zero, 0, 0, 0) + cz[u];
+                        const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u], unpack_int4(wv[q]), zero, 0, 0, 0);
                         const uint32_t pair = sv[cur][t][u >> 1];
                         const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)((u & 1) ? (pair >> 16) : pair));
 #pragma unroll
                         for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(s, d[i], acc[t][i]);
                     }
                 }
+                // the -8 (see the one-shot kernel)
+                const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+                const float4v dc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac, __builtin_bit_cast(half8, sv[cur][t]), zero, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(-0.0001220703125f, dc[i], acc[t][i]);
             }
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[cur][wave][t][i][lane] = acc[t][i];
+            for (int i = 0; i < 4; ++i) red[cur][wave][t][i][lane] = __builtin_amdgcn_ldexpf(acc[t][i], e[i]);
         __syncthreads();
         // wave w sums row tile w over the four waves; x_hi columns sit in lanes
         // 0..31, x_lo in 32..63: one swap adds them
@@ -348,16 +433,9 @@ __global__ __launch_bounds__(256, 2) void int4_gemv_stream_kernel(Int4Args a, in
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
             v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
             const int b = 4 * lg + i, row = rb * 64 + 16 * wave + lr;
-            if (lg < 2 && b < a.M && row < a.N) {
-                const float r = __builtin_amdgcn_ldexpf(v, 24 - a.sig[b]);
-                if (a.G > 4 * GPW) atomicAdd(a.out + (size_t)b * a.N + row, r);  // y cleared by the pre-pass
-                else a.out[(size_t)b * a.N + row] = r;
-            }
+            if (lg < 2 && b < a.M && row < a.N) out[(size_t)b * a.N + row] = v;
         }
     };
-    int rb = j;
-    if (rb >= row_blocks) return;
-    load(0, rb);
     for (;;) {
         step(0, rb);
         rb += wps;
@@ -368,9 +446,29 @@ __global__ __launch_bounds__(256, 2) void int4_gemv_stream_kernel(Int4Args a, in
     }
 }
 
+// y[i] = sum over the K ranges r = 0, 1, ... of part[r][i], i < M N, in range
+// order; eight ranges' loads are in flight before their adds.
+__global__ __launch_bounds__(256) void int4_sum_ranges_kernel(const float *__restrict__ part, float *__restrict__ y,
+                                                              int64_t mn, int ranges) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= mn) return;
+    float s = part[i];
+    for (int r = 1; r < ranges; r += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = r + j < ranges ? part[(int64_t)(r + j) * mn + i] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (r + j < ranges) s += v[j];
+    }
+    y[i] = s;
+}
+
 std::mutex g_ws_mu;
-void *g_ws = nullptr;
+void *g_ws = nullptr;   // partial sums of the K ranges
 size_t g_ws_bytes = 0;
+void *g_cnt = nullptr;  // one-shot kernel: ranges done per row block, zero between calls
+size_t g_cnt_bytes = 0;
 int g_num_cus = 0;
 int g_int4_kernel = 0;  // 0 automatic, 1 one-shot workgroups, 2 streaming
 
@@ -396,6 +494,7 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     DOE_REQUIRE(n <= (1 << 26) && k <= (1 << 24), DOE_E_UNSUPPORTED, "int4g32_gemv shape too large");
     DOE_REQUIRE((((uintptr_t)w_u4 | (uintptr_t)scales_f16 | (uintptr_t)x) & 15) == 0, DOE_E_INVALID,
                 "weights, scales and x must be 16-byte aligned");
+    DOE_REQUIRE(x != y, DOE_E_INVALID, "int4g32_gemv: x and y must not alias");
     if (g_num_cus == 0) {
         int dev = 0, cus = 0;
         DOE_HIP_CHECK(hipGetDevice(&dev));
@@ -405,64 +504,77 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     const int G = (int)(k / 32);
     const int row_blocks = (int)((n + 63) / 64);
     // eight groups per wave (every load of a wave in flight at once), K split
-    // over the grid so that the rows times the splits fill the CUs
-    const int gpw = 8;
-    const int per_wg = 4 * gpw;
+    // over the grid so that the rows times the ranges fill the CUs
+    const int per_wg = 4 * kGpw;
     const int splits = (G + per_wg - 1) / per_wg;
-
-    const size_t img_bytes = (size_t)G * 64 * 8 * 2;
-    const size_t fac_bytes = (size_t)G * 16 * 4 + kMaxBatch * 4;  // corrections, exponents
-    const size_t need = img_bytes + fac_bytes;
-    void *ws;
-    {
-        std::lock_guard<std::mutex> lk(g_ws_mu);
-        if (g_ws_bytes < need) {
-            if (g_ws) {
-                // queued kernels (any stream) may still read the old workspace
-                DOE_HIP_CHECK(hipDeviceSynchronize());
-                DOE_HIP_CHECK(hipFree(g_ws));
-            }
-            g_ws = nullptr;
-            g_ws_bytes = 0;
-            DOE_HIP_CHECK(hipMalloc(&g_ws, need));
-            g_ws_bytes = need;
-        }
-        ws = g_ws;
-    }
-    _Float16 *img = (_Float16 *)ws;
-    float *corr = (float *)((char *)ws + img_bytes);
-    int *sig = (int *)(corr + (size_t)G * 16);
-    const int img_parts = G > 0 ? (G + kImgGroups - 1) / kImgGroups : 1;
-    hipLaunchKernelGGL(int4_x_image_kernel, dim3(kMaxBatch, (unsigned)img_parts), dim3(kImgThreads), 0, st, x, img, corr, sig,
-                       splits > 1 ? y : nullptr, (int)m, (int)n, (int)k);
-    DOE_LAUNCH_CHECK("int4_x_image_kernel");
-    Int4Args a;
-    a.q = w_u4;
-    a.scales = scales_f16;
-    a.img = img;
-    a.corr = corr;
-    a.sig = sig;
-    a.out = y;
-    a.M = (int)m;
-    a.N = (int)n;
-    a.K = (int)k;
-    a.G = G;
+    const int64_t mn = m * n;
     // the streaming form pays off once every workgroup walks several row blocks
     // (measured at batch 8: 25600 x 5120 and 5120 x 25600 faster, 9216 x 5120
     // slower than the one-shot form)
     const int64_t items = (int64_t)row_blocks * splits;
     const bool stream_ok = items >= 6 * (int64_t)g_num_cus;
-    if (g_int4_kernel == 1 || (g_int4_kernel == 0 && !stream_ok)) {
-        const dim3 grid((unsigned)row_blocks, (unsigned)splits);
-        hipLaunchKernelGGL(int4_gemv_kernel<8>, grid, dim3(256), 0, st, a);
+    const bool one_shot = g_int4_kernel == 1 || (g_int4_kernel == 0 && !stream_ok);
+
+    float *part = y;
+    unsigned *cnt = nullptr;
+    if (splits > 1) {
+        // one-shot: [row block][range][512] slots and a count per row block;
+        // streaming: [range][M][N], added by a second kernel
+        const size_t need = one_shot ? (size_t)row_blocks * splits * 512 * sizeof(float)
+                                     : (size_t)splits * mn * sizeof(float);
+        const size_t need_cnt = one_shot ? (size_t)row_blocks * sizeof(unsigned) : 0;
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        if (g_ws_bytes < need || g_cnt_bytes < need_cnt) {
+            // queued kernels (any stream) may still use the old buffers
+            DOE_HIP_CHECK(hipDeviceSynchronize());
+            if (g_ws_bytes < need) {
+                if (g_ws) DOE_HIP_CHECK(hipFree(g_ws));
+                g_ws = nullptr;
+                g_ws_bytes = 0;
+                DOE_HIP_CHECK(hipMalloc(&g_ws, need));
+                g_ws_bytes = need;
+            }
+            if (g_cnt_bytes < need_cnt) {
+                if (g_cnt) DOE_HIP_CHECK(hipFree(g_cnt));
+                g_cnt = nullptr;
+                g_cnt_bytes = 0;
+                DOE_HIP_CHECK(hipMalloc(&g_cnt, need_cnt));
+                // every call leaves the counts at zero again
+                DOE_HIP_CHECK(hipMemset(g_cnt, 0, need_cnt));
+                DOE_HIP_CHECK(hipDeviceSynchronize());
+                g_cnt_bytes = need_cnt;
+            }
+        }
+        part = (float *)g_ws;
+        cnt = (unsigned *)g_cnt;
+    }
+    Int4Args a;
+    a.q = w_u4;
+    a.scales = scales_f16;
+    a.x = x;
+    a.out = part;
+    a.y = y;
+    a.cnt = cnt;
+    a.M = (int)m;
+    a.N = (int)n;
+    a.K = (int)k;
+    a.G = G;
+    if (one_shot) {
+        hipLaunchKernelGGL(int4_gemv_kernel, dim3((unsigned)(row_blocks * splits)), dim3(256), 0, st, a, splits);
+        DOE_LAUNCH_CHECK("int4_gemv_kernel");
     } else {
         // about two workgroups per CU, each K range's row blocks dealt evenly
         const int64_t per_wg = (items + 2 * g_num_cus - 1) / (2 * g_num_cus);
         const int wps = (int)((row_blocks + per_wg - 1) / per_wg);
-        hipLaunchKernelGGL(int4_gemv_stream_kernel<8>, dim3((unsigned)(wps * splits)), dim3(256), 0, st, a, wps,
+        hipLaunchKernelGGL(int4_gemv_stream_kernel, dim3((unsigned)(wps * splits)), dim3(256), 0, st, a, wps,
                            row_blocks);
+        DOE_LAUNCH_CHECK("int4_gemv_stream_kernel");
+        if (splits > 1) {
+            hipLaunchKernelGGL(int4_sum_ranges_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st,
+                               (const float *)part, y, mn, splits);
+            DOE_LAUNCH_CHECK("int4_sum_ranges_kernel");
+        }
     }
-    DOE_LAUNCH_CHECK("int4_gemv_kernel");
     return DOE_OK;
 }
 

@@ -192,9 +192,11 @@ int doe_quant_gemm_f32_fused(const float *a, const void *b, float *c, int64_t m,
  * bench/kernels/compilation-corpus/complex_fused_gemv_dequant.wgsl:18-66
  * (bindings quant_weights, scales, input_vec, output; uniforms rows, cols,
  * group_size = 32), with f16 scales and an activation batch.  f16 matrix
- * cores, x split into two f16 halves (~22 bits), f32 accumulation.  Uses a
- * library-owned workspace (x image and split-K partials), grown on demand
- * (not during stream capture). */
+ * cores, x split into two f16 halves (21+ bits), f32 accumulation; y is the
+ * same bit for bit on every call (K ranges added in a fixed order).  x must
+ * not alias y.  Uses library-owned workspaces (split-K partials and per-row-
+ * block counts), grown on demand (not during stream capture); calls that
+ * overlap on two streams share them. */
 int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const float *x, float *y,
                      int64_t m, int64_t n, int64_t k, doe_stream_t stream);
 

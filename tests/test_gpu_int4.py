@@ -81,6 +81,30 @@ def test_int4_rejects_bad_shapes(dev):
         with pytest.raises(_lib.DoeError):
             _lib.call("doe_int4g32_gemv", C.c_void_p(buf.ptr), C.c_void_p(buf.ptr), C.c_void_p(buf.ptr),
                       C.c_void_p(buf.ptr), m, 4, k, C.c_void_p(None))
+    # x read by every workgroup while others write y: the two must not alias
+    w = DeviceBuffer(1 << 16)
+    with pytest.raises(_lib.DoeError):
+        _lib.call("doe_int4g32_gemv", C.c_void_p(w.ptr), C.c_void_p(w.ptr), C.c_void_p(buf.ptr),
+                  C.c_void_p(buf.ptr), 1, 4, 256, C.c_void_p(None))
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 9216, 5120), (8, 5120, 25600), (3, 777, 1536)])
+def test_int4_gemv_is_deterministic(dev, m, n, k):
+    # K ranges are summed in a fixed order (no atomics): repeated calls agree
+    # bit for bit, also after a call of another shape reused the workspace
+    rng = np.random.default_rng(n ^ k)
+    w, s = random_int4(rng, n, k)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    dw, ds, dx = up(w), up(s), up(x)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    ops.matmul_int4g32(dw, ds, dx, out, m, n, k)
+    first = out.download()
+    w2, s2 = random_int4(rng, 64, 2048)
+    other = DeviceBuffer.empty((8, 64), np.float32)
+    ops.matmul_int4g32(up(w2), up(s2), up(rng.standard_normal((8, 2048), dtype=np.float32)), other, 8, 64, 2048)
+    for _ in range(3):
+        ops.matmul_int4g32(dw, ds, dx, out, m, n, k)
+        assert np.array_equal(out.download(), first)
 
 
 @pytest.mark.parametrize("m,n,k", [(8, 25600, 5120), (8, 5120, 25600)])
