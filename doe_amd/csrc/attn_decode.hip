@@ -79,6 +79,7 @@ struct AttnArgs {
 };
 
 constexpr int kMaxSplits = 512;
+constexpr float kLazyMax = 8.0f;  // log2 headroom of the lazily raised running max
 
 // Max / sum over each 16-lane row with DPP (quad_perm ^1, ^2, row_half_mirror,
 // row_mirror): every lane of the row gets the result, no LDS round trip.
@@ -121,21 +122,32 @@ __device__ __forceinline__ int kv_row(const AttnArgs &a, int p) {
 }
 
 // rowk: this lane's key row (lane l holds key p0 + l % 16); lanes 0..15 give
-// the 16 rows every lane's V loads need.
+// the 16 rows every lane's V loads need.  A contiguous cache (vrow0 >= 0)
+// passes the rows directly: position n at min(vrow0 + n, vrow_last).
 template <int D>
 __device__ __forceinline__ void load_block(KVBlock<D> &blk, const uint16_t *kb, const uint16_t *vb,
-                                           int rowk, size_t pos_stride, int lane) {
+                                           int rowk, size_t pos_stride, int lane, int vrow0, int vrow_last) {
     constexpr int KSTEPS = D / 32, DPL = D / 64;
     // dims 8 (lane / 16) + 32 s of the lane's key
     const uint16_t *krow = kb + (size_t)rowk * pos_stride + 8 * (lane >> 4);
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) blk.kf[s] = *reinterpret_cast<const h8 *>(krow + 32 * s);
+    if (vrow0 >= 0) {  // wave-uniform
 #pragma unroll
-    for (int n = 0; n < 16; ++n) {
-        const _Float16 *vrow = reinterpret_cast<const _Float16 *>(
-            vb + (size_t)__builtin_amdgcn_readlane(rowk, n) * pos_stride + lane * DPL);
+        for (int n = 0; n < 16; ++n) {
+            const int r = min(vrow0 + n, vrow_last);
+            const _Float16 *vrow = reinterpret_cast<const _Float16 *>(vb + (size_t)r * pos_stride + lane * DPL);
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
+            for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < 16; ++n) {
+            const int r = __builtin_amdgcn_readlane(rowk, n);
+            const _Float16 *vrow = reinterpret_cast<const _Float16 *>(vb + (size_t)r * pos_stride + lane * DPL);
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
+        }
     }
 }
 
@@ -207,7 +219,15 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     __asm__ volatile("" ::: "memory");
     KVBlock<D> cur;
     int blk = blk_begin + wave;
-    if (blk < blk_end) load_block<D>(cur, kb, vb, kv_row(a, min(blk * 16 + (lane & 15), key_hi - 1)), pos_stride, lane);
+    // a contiguous cache (kv_map 0) addresses V rows without lane reads
+    const bool contig = a.kv_map == 0;
+    const int vrow_last = min(a.kv_start + key_hi - 1, a.kv_stride - 1);
+    auto vrow0 = [&](int bk) __attribute__((always_inline)) {
+        return contig ? __builtin_amdgcn_readfirstlane(a.kv_start + bk * 16) : -1;
+    };
+    if (blk < blk_end)
+        load_block<D>(cur, kb, vb, kv_row(a, min(blk * 16 + (lane & 15), key_hi - 1)), pos_stride, lane, vrow0(blk),
+                      vrow_last);
 #pragma unroll
     for (int it = 0; it < QITEMS; ++it) {
         const int idx = tid + it * kThreads;
@@ -258,7 +278,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         KVBlock<D> nxt;
         if (blk + kWaves < blk_end)
             load_block<D>(nxt, kb, vb, kv_row(a, min((blk + kWaves) * 16 + (lane & 15), key_hi - 1)), pos_stride,
-                          lane);
+                          lane, vrow0(blk + kWaves), vrow_last);
 
         const int p0 = blk * 16;
         const int pk = p0 + (lane & 15);
@@ -282,9 +302,12 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
             }
             const float sc = valid ? s : -INFINITY;  // score in log2 units
             const float m = max16(sc);
-            const float bm = fmaxf(mlane[i], m);
+            // The running max is raised only when a block's max exceeds it by
+            // more than 2^kLazyMax (probabilities then stay <= 2^kLazyMax in
+            // f32), so most blocks skip the rescale of o and l below.
+            const float bm = m > mlane[i] + kLazyMax ? m : mlane[i];
             mlane[i] = bm;
-            const float p = valid ? exp2f(sc - bm) : 0.0f;
+            const float p = valid ? __builtin_amdgcn_exp2f(sc - bm) : 0.0f;
             const float t = sum16(p);
             const int h = 4 * grp + i;
             if (h < G) {
@@ -302,12 +325,16 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            const float mnew = pbw[16 * (G4 * 4) + h];
-            const float alpha = (mnew == -INFINITY) ? 1.0f : exp2f(mrow[h] - mnew);
-            mrow[h] = mnew;
-            lrow[h] = lrow[h] * alpha + wl[wave][h];
+            const float mnew = pbw[16 * (G4 * 4) + h];  // the same in every lane
+            if (mnew != mrow[h]) {
+                // raised from mrow (-inf before the first valid key: o and l are 0)
+                const float alpha = __builtin_amdgcn_exp2f(mrow[h] - mnew);
+                mrow[h] = mnew;
+                lrow[h] *= alpha;
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) o[h][d] *= alpha;
+                for (int d = 0; d < DPL; ++d) o[h][d] *= alpha;
+            }
+            lrow[h] += wl[wave][h];
         }
 #pragma unroll
         for (int n = 0; n < 16; ++n) {
@@ -351,7 +378,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         if (M != -INFINITY) {
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
-                const float f = exp2f(wm[w][h] - M);
+                const float f = __builtin_amdgcn_exp2f(wm[w][h] - M);
                 L += wl[w][h] * f;
                 O += sm.wo[w][h][d] * f;
             }
@@ -417,8 +444,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float f0 = (m0 == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(m0 - M);
-    const float f1 = (m1 == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(m1 - M);
+    const float f0 = (m0 == -INFINITY || M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);
+    const float f1 = (m1 == -INFINITY || M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - M);
     if (tid < S) wts[tid] = f0;
     if (tid + 256 < S) wts[tid + 256] = f1;
     const float ls = wave_sum(l0 * f0 + l1 * f1);
