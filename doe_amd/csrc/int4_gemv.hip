@@ -353,8 +353,9 @@ __device__ __forceinline__ void quad_transpose(const u32x4 v, uint32_t out[4]) {
 // hands every lane its word of each group.  The four waves' sums meet in LDS
 // (double-buffered, one barrier per block), each wave summing and storing one
 // 16-row tile of the range's sums (out[split][M][N] when K is split).
+template <int DEPTH>
 __global__ __launch_bounds__(256, 2) void int4_gemv_stream_kernel(Int4Args a, int wps, int row_blocks) {
-    __shared__ float red[2][4][4][4][64];  // [buffer][source wave][tile][column][lane]
+    __shared__ float red[DEPTH][4][4][4][64];  // [buffer][source wave][tile][column][lane]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const int sp = blockIdx.x / wps, j = blockIdx.x - sp * wps;
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(256, 2) void int4_gemv_stream_kernel(Int4Args a, in
     float *out = a.G > 4 * kGpw ? a.out + (size_t)sp * a.M * a.N : a.y;
 
     const size_t row_words = (size_t)a.K / 8;
-    u32x4 wq[2][4][kGpw / 4], sv[2][4];
+    u32x4 wq[DEPTH][4][kGpw / 4], sv[DEPTH][4];
     auto load = [&](const int set, const int rb) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -380,14 +381,16 @@ __global__ __launch_bounds__(256, 2) void int4_gemv_stream_kernel(Int4Args a, in
     if (rb >= row_blocks) return;
     float xv[kGpw][8];
     x_load(a, gb, lane, xv);
-    load(0, rb);
+#pragma unroll
+    for (int d = 0; d < DEPTH - 1; ++d)
+        if (rb + d * wps < row_blocks) load(d, rb + d * wps);
     half8 xa[kGpw], ac;
     const int sig = x_image(a, active, lane, xv, xa, ac);
     int e[4];
     column_exponents(sig, lg, e);
 
     auto step = [&](const int cur, const int rb) __attribute__((always_inline)) {
-        if (rb + wps < row_blocks) load(cur ^ 1, rb + wps);
+        if (rb + (DEPTH - 1) * wps < row_blocks) load((cur + DEPTH - 1) % DEPTH, rb + (DEPTH - 1) * wps);
         // acc[t][i]: row 64 rb + 16 t + lr, column 4 lg + i (batch (4 lg + i) % 8, hi for lg < 2)
         float acc[4][4];
 #pragma unroll
@@ -437,12 +440,16 @@ __global__ __launch_bounds__(256, 2) void int4_gemv_stream_kernel(Int4Args a, in
         }
     };
     for (;;) {
-        step(0, rb);
-        rb += wps;
-        if (rb >= row_blocks) break;
-        step(1, rb);
-        rb += wps;
-        if (rb >= row_blocks) break;
+        bool done = false;
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            if (!done) {
+                step(d, rb);
+                rb += wps;
+                done = rb >= row_blocks;
+            }
+        }
+        if (done) break;
     }
 }
 
@@ -471,6 +478,7 @@ void *g_cnt = nullptr;  // one-shot kernel: ranges done per row block, zero betw
 size_t g_cnt_bytes = 0;
 int g_num_cus = 0;
 int g_int4_kernel = 0;  // 0 automatic, 1 one-shot workgroups, 2 streaming
+int g_int4_depth = 3;   // streaming: row blocks in flight per wave + 1 (2 or 3)
 
 }  // namespace
 
@@ -566,8 +574,12 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
         // about two workgroups per CU, each K range's row blocks dealt evenly
         const int64_t per_wg = (items + 2 * g_num_cus - 1) / (2 * g_num_cus);
         const int wps = (int)((row_blocks + per_wg - 1) / per_wg);
-        hipLaunchKernelGGL(int4_gemv_stream_kernel, dim3((unsigned)(wps * splits)), dim3(256), 0, st, a, wps,
-                           row_blocks);
+        if (g_int4_depth == 2)
+            hipLaunchKernelGGL(int4_gemv_stream_kernel<2>, dim3((unsigned)(wps * splits)), dim3(256), 0, st, a, wps,
+                               row_blocks);
+        else
+            hipLaunchKernelGGL(int4_gemv_stream_kernel<3>, dim3((unsigned)(wps * splits)), dim3(256), 0, st, a, wps,
+                               row_blocks);
         DOE_LAUNCH_CHECK("int4_gemv_stream_kernel");
         if (splits > 1) {
             hipLaunchKernelGGL(int4_sum_ranges_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st,
@@ -585,6 +597,12 @@ namespace doe {
 int int4_set_kernel(int v) {
     DOE_REQUIRE(v >= 0 && v <= 2, DOE_E_INVALID, "int4_gemv.kernel is 0, 1 or 2");
     g_int4_kernel = v;
+    return DOE_OK;
+}
+
+int int4_set_depth(int v) {
+    DOE_REQUIRE(v == 0 || v == 2 || v == 3, DOE_E_INVALID, "int4_gemv.depth is 0 (automatic), 2 or 3");
+    g_int4_depth = v == 0 ? 3 : v;
     return DOE_OK;
 }
 

@@ -1356,6 +1356,8 @@ int doe_tune_set(const char *key, int value) {
         return doe::q8_0_set_tune(key, value);
     } else if (!strcmp(key, "int4_gemv.kernel")) {
         return doe::int4_set_kernel(value);
+    } else if (!strcmp(key, "int4_gemv.depth")) {
+        return doe::int4_set_depth(value);
     } else if (!strcmp(key, "attn_mq.splits")) {
         return doe::mq_set_splits(value);
     } else if (!strcmp(key, "attn_decode.splits")) {
