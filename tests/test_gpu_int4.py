@@ -138,3 +138,28 @@ def test_int4_both_kernels_match_oracle(dev, ora, kernel, m, n, k):
         _lib.call("doe_tune_set", b"int4_gemv.kernel", 0)
     err = rel_l2(got, ora.int4g32_gemv(w, s, x, m, n, k))
     assert err <= 1e-5, (kernel, err)
+
+
+@pytest.mark.parametrize("depth", [2, 3])
+@pytest.mark.parametrize("m,n,k", [(8, 3000, 2048), (2, 64 * 9 + 7, 1024), (8, 25600, 5120)])
+def test_int4_streaming_prefetch_depths(dev, ora, depth, m, n, k):
+    # the streaming kernel with one and with two row blocks of weights in
+    # flight per wave (int4_gemv.depth), forced on ragged and config-4 shapes:
+    # both give the oracle's result and the same bits
+    rng = np.random.default_rng(7 * n + k + depth)
+    w, s = random_int4(rng, n, k)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    dw, ds, dx = up(w), up(s), up(x)
+    out = DeviceBuffer.empty((m, n), np.float32)
+    got = {}
+    _lib.call("doe_tune_set", b"int4_gemv.kernel", 2)
+    try:
+        for d in (depth, 5 - depth):
+            _lib.call("doe_tune_set", b"int4_gemv.depth", d)
+            ops.matmul_int4g32(dw, ds, dx, out, m, n, k)
+            got[d] = out.download()
+    finally:
+        _lib.call("doe_tune_set", b"int4_gemv.kernel", 0)
+        _lib.call("doe_tune_set", b"int4_gemv.depth", 0)
+    assert rel_l2(got[depth], ora.int4g32_gemv(w, s, x, m, n, k)) <= 1e-5
+    assert np.array_equal(got[2], got[3])
