@@ -578,6 +578,36 @@ def bench_q8_0(args, doe):
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "rel_l2_vs_oracle": rel}
 
 
+def bench_hbm_copy(args, doe):
+    """STREAM-style check of the HBM figure the rooflines use: 2 GiB copied
+    device to device (the runtime's copy kernel) ten times between HIP
+    events; read and written bytes both counted."""
+    from doe_amd import DeviceBuffer, Event, Stream
+
+    nbytes = 1 << 31
+    src, dst = DeviceBuffer(nbytes), DeviceBuffer(nbytes)
+    s = Stream()
+    dst.copy_from(src, s)
+    s.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(s)
+    reps = 10
+    for _ in range(reps):
+        dst.copy_from(src, s)
+    e1.record(s)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    gbs = 2 * nbytes / (ms * 1e-3) / 1e9
+    s.destroy()
+    src.free()
+    dst.free()
+    log(f"hbm copy: 2 GiB device-to-device in {ms * 1e3:.1f} us = {gbs:.0f} GB/s read + write "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of the {HBM_PEAK_GBS:.0f} GB/s figure)")
+    return {"kind": "STREAM copy: hipMemcpyAsync device to device, read + write bytes counted",
+            "bytes_per_copy": nbytes, "us_per_copy": round(ms * 1e3, 1), "achieved_gbs": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def traffic_bytes(summary: str):
     """HBM bytes per launch recorded in a committed rocprofv3 summary
     (line `traffic_bytes_per_launch: <int>`), or None."""
@@ -665,6 +695,7 @@ def main() -> int:
     pfa = None if args.no_gemm else bench_prefill_attention(args, doe_amd)
     c4 = None if args.no_gemm else bench_config4(args, doe_amd)
     q8 = bench_q8_0(args, doe_amd)
+    hbm = bench_hbm_copy(args, doe_amd)
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of the single-threaded oracle")
@@ -713,6 +744,7 @@ def main() -> int:
         "prefill_attention": pfa,
         "config4_decode_layer": c4,
         "q8_0_gemv": q8,
+        "hbm_stream_copy": hbm,
     }
     print(json.dumps(out), flush=True)
     return 0
