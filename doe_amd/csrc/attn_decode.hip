@@ -686,11 +686,7 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
         const size_t need = ml_off + ml_bytes;
         std::lock_guard<std::mutex> lk(g_ws_mu);
         if (need > g_ws_bytes) {
-            if (g_ws) {
-                // queued kernels (any stream) may still read the old workspace
-                DOE_HIP_CHECK(hipDeviceSynchronize());
-                DOE_HIP_CHECK(hipFree(g_ws));
-            }
+            doe::retire_workspace(g_ws);  // queued kernels and captured graphs may still use it
             g_ws = nullptr;
             g_ws_bytes = 0;
             DOE_HIP_CHECK(hipMalloc(&g_ws, need));

@@ -407,10 +407,7 @@ int launch_mq(const MqArgs &a0, hipStream_t st) {
         const size_t o_bytes = (size_t)splits * rows * D * 4, need = o_bytes + (size_t)splits * rows * 8;
         std::lock_guard<std::mutex> lk(g_mq_mu);
         if (g_mq_ws_bytes < need) {
-            if (g_mq_ws) {
-                DOE_HIP_CHECK(hipDeviceSynchronize());  // queued kernels may still use the old one
-                DOE_HIP_CHECK(hipFree(g_mq_ws));
-            }
+            doe::retire_workspace(g_mq_ws);  // queued kernels and captured graphs may still use it
             g_mq_ws = nullptr;
             g_mq_ws_bytes = 0;
             DOE_HIP_CHECK(hipMalloc(&g_mq_ws, need));

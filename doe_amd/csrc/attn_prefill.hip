@@ -424,11 +424,7 @@ int doe_attn_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, vo
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
         if (g_ws_bytes < need) {
-            if (g_ws) {
-                // queued kernels (any stream) may still read the old workspace
-                DOE_HIP_CHECK(hipDeviceSynchronize());
-                DOE_HIP_CHECK(hipFree(g_ws));
-            }
+            doe::retire_workspace(g_ws);  // queued kernels and captured graphs may still use it
             g_ws = nullptr;
             g_ws_bytes = 0;
             DOE_HIP_CHECK(hipMalloc(&g_ws, need));

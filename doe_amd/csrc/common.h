@@ -21,6 +21,10 @@ void clear_error();
 int hip_fail(hipError_t e, const char *what);
 // Checks that the library was initialised on the calling thread's device.
 int require_init();
+// Keeps a library workspace that a larger one has replaced allocated until
+// doe_shutdown: kernels still queued, and HIP graphs captured earlier, may
+// hold its address and keep using it.
+void retire_workspace(void *ptr);
 // Fills bytes [dst, dst + bytes) with `value` on a stream with a kernel
 // (capturable into a HIP graph; no memset node).  Returns a DOE status.
 int fill_bytes_async(void *dst, int value, size_t bytes, hipStream_t st);

@@ -533,17 +533,16 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
         const size_t need_cnt = one_shot ? (size_t)row_blocks * sizeof(unsigned) : 0;
         std::lock_guard<std::mutex> lk(g_ws_mu);
         if (g_ws_bytes < need || g_cnt_bytes < need_cnt) {
-            // queued kernels (any stream) may still use the old buffers
-            DOE_HIP_CHECK(hipDeviceSynchronize());
+            // queued kernels and captured graphs may still use the old buffers
             if (g_ws_bytes < need) {
-                if (g_ws) DOE_HIP_CHECK(hipFree(g_ws));
+                doe::retire_workspace(g_ws);
                 g_ws = nullptr;
                 g_ws_bytes = 0;
                 DOE_HIP_CHECK(hipMalloc(&g_ws, need));
                 g_ws_bytes = need;
             }
             if (g_cnt_bytes < need_cnt) {
-                if (g_cnt) DOE_HIP_CHECK(hipFree(g_cnt));
+                doe::retire_workspace(g_cnt);
                 g_cnt = nullptr;
                 g_cnt_bytes = 0;
                 DOE_HIP_CHECK(hipMalloc(&g_cnt, need_cnt));

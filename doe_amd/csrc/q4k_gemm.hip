@@ -872,11 +872,7 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
         if (g_ws_bytes < need) {
-            if (g_ws) {
-                // queued kernels (any stream) may still read the old workspace
-                DOE_HIP_CHECK(hipDeviceSynchronize());
-                DOE_HIP_CHECK(hipFree(g_ws));
-            }
+            doe::retire_workspace(g_ws);  // queued kernels and captured graphs may still use it
             g_ws = nullptr;
             g_ws_bytes = 0;
             DOE_HIP_CHECK(hipMalloc(&g_ws, need));

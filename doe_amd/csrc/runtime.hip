@@ -6,6 +6,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+#include <vector>
+
 namespace doe {
 
 static thread_local char g_err[1024] = "";
@@ -29,6 +32,16 @@ int hip_fail(hipError_t e, const char *what) {
 int require_init() {
     if (g_device < 0) return set_error(DOE_E_NOT_INIT, "doe_init() was not called");
     return DOE_OK;
+}
+
+// Workspaces replaced by larger ones, freed by doe_shutdown.
+static std::mutex g_retired_mu;
+static std::vector<void *> g_retired;
+
+void retire_workspace(void *ptr) {
+    if (!ptr) return;
+    std::lock_guard<std::mutex> lk(g_retired_mu);
+    g_retired.push_back(ptr);
 }
 
 // byte fill: the unaligned head and tail byte by byte, the middle 16 bytes
@@ -88,6 +101,11 @@ int doe_init(int device) {
 int doe_shutdown(void) {
     if (doe::g_device < 0) return DOE_OK;
     DOE_HIP_CHECK(hipDeviceSynchronize());
+    {
+        std::lock_guard<std::mutex> lk(doe::g_retired_mu);
+        for (void *p : doe::g_retired) DOE_HIP_CHECK(hipFree(p));
+        doe::g_retired.clear();
+    }
     doe::g_device = -1;
     return DOE_OK;
 }
