@@ -77,6 +77,9 @@ SIGNATURES: dict[str, list] = {
     "doe_q8_0_gemv": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
     "doe_q8_0_gemv_norm": [_vp, _vp, _vp, _i64, _i64, _vp, _f32, _i32, _vp, _vp],
     "doe_q8_0_gemv_attn_out": [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
+    "doe_q8_0_gemv_fused": [_vp, _vp, _vp, _i64, _i64, _vp, _f32, _i32, _vp, _i32, _vp],
+    "doe_q8_0_gemv_qkv_rope_kv": [_vp, _vp, _vp, _i64, _vp, _f32, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
+                                  _i64, _vp],
     "doe_attn_prefill": [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp],
     "doe_attn_decode_partials": [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i32, _f32, _f32, _i64, _vp, _i64, _i64, C.POINTER(_i32), _vp],
     "doe_attention_dispatch": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp],

@@ -77,3 +77,44 @@ __device__ __forceinline__ float doe_gelu_tanh_clamped(float x) {
 __device__ __forceinline__ float doe_half_bits_to_float(uint32_t bits16) {
     return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
 }
+
+// Epilogue of a fused q/k/v decode projection whose q and k rows come as
+// interleaved rotation pairs (row 2i = dim i, row 2i+1 = dim i + head_dim/2 of
+// the rotate-half form, rope.wgsl:1-35): the pair (row, row + 1) of finished
+// sums is rotated by freq_cis[pos][i] (q and k rows), stored to y, and k and v
+// rows are also written as f16 into the caches [kv_heads][max_seq][head_dim]
+// at pos (read on the device).  A position outside [0, max_seq) leaves the
+// rows unrotated and writes no cache row.
+struct DoeRopeKv {
+    const float *freq_cis;
+    const int32_t *pos_dev;
+    _Float16 *k_cache, *v_cache;
+    int q_rows, kv_rows, head_dim, max_seq;
+};
+
+__device__ __forceinline__ void doe_rope_kv_pair(const DoeRopeKv &rk, int row, float s0, float s1, float *y) {
+#pragma clang fp contract(off)
+    const int pos = rk.pos_dev[0];
+    const bool in_cache = pos >= 0 && pos < rk.max_seq;  // freq_cis holds max_seq positions
+    float r0 = s0, r1 = s1;
+    const int dim = row % rk.head_dim;
+    if (in_cache && row < rk.q_rows + rk.kv_rows) {
+        const int i = dim >> 1, half = rk.head_dim >> 1;
+        const float c = rk.freq_cis[((size_t)pos * half + i) * 2];
+        const float sn = rk.freq_cis[((size_t)pos * half + i) * 2 + 1];
+        r0 = s0 * c - s1 * sn;
+        r1 = s0 * sn + s1 * c;
+    }
+    y[row] = r0;
+    y[row + 1] = r1;
+    if (row >= rk.q_rows && in_cache) {
+        const int kvr = row - rk.q_rows;
+        const bool is_v = kvr >= rk.kv_rows;
+        const int rr = is_v ? kvr - rk.kv_rows : kvr;
+        const int h = rr / rk.head_dim;
+        _Float16 *cache = is_v ? rk.v_cache : rk.k_cache;
+        const size_t ci = ((size_t)h * rk.max_seq + pos) * rk.head_dim + dim;
+        cache[ci] = (_Float16)r0;
+        cache[ci + 1] = (_Float16)r1;
+    }
+}

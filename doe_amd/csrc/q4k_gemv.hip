@@ -190,30 +190,9 @@ struct GemvFusion {
 // Epilogue of one (even row, odd row) pair of a fused q/k/v projection.
 __device__ __forceinline__ void rope_kv_pair(const GemvFusion &fz, int row, float s0, float s1,
                                              float *__restrict__ y) {
-#pragma clang fp contract(off)
-    const int pos = fz.pos_dev[0];
-    const bool in_cache = pos >= 0 && pos < fz.max_seq;  // freq_cis holds max_seq positions
-    float r0 = s0, r1 = s1;
-    const int dim = row % fz.head_dim;
-    if (in_cache && row < fz.q_rows + fz.kv_rows) {
-        const int i = dim >> 1, half = fz.head_dim >> 1;
-        const float c = fz.freq_cis[((size_t)pos * half + i) * 2];
-        const float sn = fz.freq_cis[((size_t)pos * half + i) * 2 + 1];
-        r0 = s0 * c - s1 * sn;
-        r1 = s0 * sn + s1 * c;
-    }
-    y[row] = r0;
-    y[row + 1] = r1;
-    if (row >= fz.q_rows && in_cache) {
-        const int kvr = row - fz.q_rows;
-        const bool is_v = kvr >= fz.kv_rows;
-        const int rr = is_v ? kvr - fz.kv_rows : kvr;
-        const int h = rr / fz.head_dim;
-        _Float16 *cache = is_v ? fz.v_cache : fz.k_cache;
-        const size_t ci = ((size_t)h * fz.max_seq + pos) * fz.head_dim + dim;
-        cache[ci] = (_Float16)r0;
-        cache[ci + 1] = (_Float16)r1;
-    }
+    const DoeRopeKv rk{fz.freq_cis, fz.pos_dev, fz.k_cache, fz.v_cache, fz.q_rows, fz.kv_rows, fz.head_dim,
+                       fz.max_seq};
+    doe_rope_kv_pair(rk, row, s0, s1, y);
 }
 
 // PRO: activation prologue -- 0 plain f32 load, 1 fused RMSNorm, 2 combine of

@@ -111,11 +111,20 @@ __device__ __forceinline__ float4 attn_combine4(const Q8Attn &at, int e) {
     return make_float4(acc.x * rl, acc.y * rl, acc.z * rl, acc.w * rl);
 }
 
+// Epilogues over row pairs (2i, 2i + 1) of a wave group (R even): the GeGLU of
+// interleaved gate/up rows, y[i] = gelu_tanh(dot_2i) * dot_2i+1
+// (gelu_gated.wgsl:1-14), or RoPE + the K/V cache write of a fused q/k/v
+// projection whose q/k rows are interleaved rotation pairs (doe_rope_kv_pair).
+struct Q8Epi {
+    int gated, rope_kv;
+    DoeRopeKv rk;
+};
+
 template <int R, int D>
 __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
     const uint8_t *__restrict__ w, const float *__restrict__ x, float *y, const float *res, int n,
     int k, int nb, int q64, int r64, bool x_vec, const float *norm_w, float norm_eps, int norm_offset,
-    Q8Attn at) {
+    Q8Attn at, Q8Epi ep) {
     static_assert(D == 1 || D == 2, "one or two units in flight ahead");
     extern __shared__ float lds[];
     float *xs = lds;                          // [nb][kXStride]
@@ -241,14 +250,31 @@ __global__ __launch_bounds__(kWaves * 64) void q8_0_gemv_kernel(
                 o0 = on;
             }
         }
+        float sum[R];
 #pragma unroll
         for (int j = 0; j < R; ++j) {
             float s = acc[j];
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-            if (lane == 0 && j < rows) {
-                const int row = g * R + j;
-                y[row] = res ? fmaf(rms_inv, s, res[row]) : rms_inv * s;
+            sum[j] = s;
+        }
+        if (ep.gated || ep.rope_kv) {  // wave-uniform; R is even and so is n
+#pragma unroll
+            for (int j = 0; j + 1 < R; j += 2) {
+                if (lane == 0 && j < rows) {
+                    const int row = g * R + j;
+                    const float s0 = rms_inv * sum[j], s1 = rms_inv * sum[j + 1];
+                    if (ep.gated) y[row >> 1] = doe_gelu_tanh_clamped(s0) * s1;
+                    else doe_rope_kv_pair(ep.rk, row, s0, s1, y);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                if (lane == 0 && j < rows) {
+                    const int row = g * R + j;
+                    y[row] = res ? fmaf(rms_inv, sum[j], res[row]) : rms_inv * sum[j];
+                }
             }
         }
     }
@@ -267,7 +293,7 @@ struct Q8Norm {
 
 template <int R, int D>
 int q8_0_launch(const uint8_t *w, const float *x, float *y, const float *res, int n, int k, int nb,
-                const Q8Norm &fz, const Q8Attn &at, hipStream_t st) {
+                const Q8Norm &fz, const Q8Attn &at, const Q8Epi &ep, hipStream_t st) {
     static const hipError_t attr_rc = hipFuncSetAttribute(
         reinterpret_cast<const void *>(&q8_0_gemv_kernel<R, D>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxBlocks * (kXStride + 1) * 4 + kWaves * 4);
@@ -279,16 +305,16 @@ int q8_0_launch(const uint8_t *w, const float *x, float *y, const float *res, in
     const size_t lds = (size_t)nb * (kXStride + 1) * 4 + kWaves * 4;
     hipLaunchKernelGGL((q8_0_gemv_kernel<R, D>), dim3((unsigned)blocks), dim3(kWaves * 64), lds, st,
                        w, x, y, res, n, k, nb, 64 / nb, 64 % nb, ((uintptr_t)x & 15) == 0, fz.norm_w,
-                       fz.norm_eps, fz.norm_offset, at);
+                       fz.norm_eps, fz.norm_offset, at, ep);
     DOE_LAUNCH_CHECK("q8_0_gemv_kernel");
     return DOE_OK;
 }
 
 template <int R>
 int q8_0_launch_depth(const uint8_t *w, const float *x, float *y, const float *res, int n, int k,
-                      int nb, const Q8Norm &fz, const Q8Attn &at, hipStream_t st) {
-    if (g_tune_depth == 2) return q8_0_launch<R, 2>(w, x, y, res, n, k, nb, fz, at, st);
-    return q8_0_launch<R, 1>(w, x, y, res, n, k, nb, fz, at, st);
+                      int nb, const Q8Norm &fz, const Q8Attn &at, const Q8Epi &ep, hipStream_t st) {
+    if (g_tune_depth == 2) return q8_0_launch<R, 2>(w, x, y, res, n, k, nb, fz, at, ep, st);
+    return q8_0_launch<R, 1>(w, x, y, res, n, k, nb, fz, at, ep, st);
 }
 
 }  // namespace
@@ -297,13 +323,16 @@ namespace {
 
 int q8_0_gemv_impl(const void *weight_q8_0, const float *activation, float *output, int64_t n,
                    int64_t k, const float *residual, const Q8Norm &fz, doe_stream_t stream,
-                   const Q8Attn &at = Q8Attn{nullptr, nullptr, 0, 0}) {
+                   const Q8Attn &at = Q8Attn{nullptr, nullptr, 0, 0}, const Q8Epi &ep = Q8Epi{}) {
     int rc = doe::require_init();
     if (rc) return rc;
     const hipStream_t st = (hipStream_t)stream;
     DOE_REQUIRE(n >= 0 && k >= 0 && n <= 0x7fffffff, DOE_E_INVALID, "bad q8_0_gemv shape");
     if (n == 0) return DOE_OK;
     DOE_REQUIRE(output, DOE_E_INVALID, "null output");
+    const bool paired = ep.gated || ep.rope_kv;
+    DOE_REQUIRE(!paired || (n % 2 == 0 && k > 0 && !residual), DOE_E_INVALID,
+                "the GeGLU and RoPE epilogues need an even row count, k > 0 and no residual");
     if (k == 0) {  // empty reductions: the residual, or zeros
         if (!residual) return doe::fill_bytes_async(output, 0, (size_t)n * 4, st);
         if (residual != output)
@@ -341,9 +370,12 @@ int q8_0_gemv_impl(const void *weight_q8_0, const float *activation, float *outp
             r *= 2;
         while (r < 4 && (n + r - 1) / r > (int64_t)g_num_cus * 8 * kWaves) r *= 2;
     }
-    if (r == 4) return q8_0_launch_depth<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, at, st);
-    if (r == 2) return q8_0_launch_depth<2>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, at, st);
-    return q8_0_launch_depth<1>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, at, st);
+    if (paired && r == 1) r = 2;  // a wave group holds whole row pairs
+    if (r == 4)
+        return q8_0_launch_depth<4>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, at, ep, st);
+    if (r == 2)
+        return q8_0_launch_depth<2>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, at, ep, st);
+    return q8_0_launch_depth<1>(w, activation, output, residual, (int)n, (int)k, (int)nb, fz, at, ep, st);
 }
 
 }  // namespace
@@ -374,6 +406,38 @@ extern "C" int doe_q8_0_gemv_attn_out(const void *weight_q8_0, const float *attn
     const Q8Attn at{attn_partials, attn_partials + num_heads * splits * head_dim, (int)splits, (int)head_dim};
     return q8_0_gemv_impl(weight_q8_0, nullptr, output, n, num_heads * head_dim, residual,
                           Q8Norm{nullptr, 0.0f, 0}, stream, at);
+}
+
+extern "C" int doe_q8_0_gemv_fused(const void *weight_q8_0, const float *activation, float *output, int64_t n,
+                                   int64_t k, const float *norm_weight, float norm_eps, int norm_weight_offset,
+                                   const float *residual, int gated, doe_stream_t stream) {
+    DOE_REQUIRE(!gated || !residual, DOE_E_INVALID, "gated and residual are exclusive");
+    Q8Epi ep{};
+    ep.gated = gated ? 1 : 0;
+    return q8_0_gemv_impl(weight_q8_0, activation, output, n, k, residual,
+                          Q8Norm{norm_weight, norm_eps, norm_weight_offset ? 1 : 0}, stream,
+                          Q8Attn{nullptr, nullptr, 0, 0}, ep);
+}
+
+extern "C" int doe_q8_0_gemv_qkv_rope_kv(const void *weight_q8_0, const float *activation, float *output,
+                                         int64_t hidden, const float *norm_weight, float norm_eps,
+                                         int norm_weight_offset, int64_t num_heads, int64_t num_kv_heads,
+                                         int64_t head_dim, const float *freq_cis, const int32_t *position_dev,
+                                         uint16_t *key_cache, uint16_t *val_cache, int64_t max_seq_len,
+                                         doe_stream_t stream) {
+    DOE_REQUIRE(num_heads > 0 && num_kv_heads >= 0 && head_dim > 0 && (head_dim % 2) == 0 && max_seq_len > 0 &&
+                    (num_heads + 2 * num_kv_heads) * head_dim <= 0x7fffffff,
+                DOE_E_INVALID, "bad qkv shape");
+    DOE_REQUIRE(freq_cis && position_dev && (num_kv_heads == 0 || (key_cache && val_cache)), DOE_E_INVALID,
+                "null pointer");
+    Q8Epi ep{};
+    ep.rope_kv = 1;
+    ep.rk = DoeRopeKv{freq_cis, position_dev, (_Float16 *)key_cache, (_Float16 *)val_cache,
+                      (int)(num_heads * head_dim), (int)(num_kv_heads * head_dim), (int)head_dim, (int)max_seq_len};
+    const int64_t n = (num_heads + 2 * num_kv_heads) * head_dim;
+    return q8_0_gemv_impl(weight_q8_0, activation, output, n, hidden, nullptr,
+                          Q8Norm{norm_weight, norm_eps, norm_weight_offset ? 1 : 0}, stream,
+                          Q8Attn{nullptr, nullptr, 0, 0}, ep);
 }
 
 namespace doe {

@@ -148,9 +148,8 @@ class LayerWeights:
         self.q_dim = cfg.heads * hd
         self.kv_dim = 0 if shared_kv else cfg.kv_heads * hd
         self.qkv_rows = self.q_dim + 2 * self.kv_dim
-        # q4k: q/k rows as interleaved rotation pairs, gate/up rows interleaved
-        # (gate_0, up_0, gate_1, ...) for the fused kernels; q8_0: plain q/k
-        # rows (rotate-half RoPE op), gate rows then up rows
+        # q/k rows as interleaved rotation pairs, gate/up rows interleaved
+        # (gate_0, up_0, gate_1, ...) for the fused kernels (Q4_K and Q8_0)
         self.wqkv = DeviceBuffer(self.qkv_rows * rb(cfg.hidden))
         self.wo = DeviceBuffer(cfg.hidden * rb(self.q_dim))
         self.wgu = DeviceBuffer(2 * cfg.ffn * rb(cfg.hidden))
@@ -239,10 +238,6 @@ class Decoder:
             self.ple_yn = DeviceBuffer.empty((c.hidden,), np.float32)
             self.ple_u_views = [self.ple_u.view(li * P * 4, P * 4, np.float32) for li in range(L)]
         self.h = DeviceBuffer.empty((c.ffn,), np.float32)
-        if c.weight_format == "q8_0":  # unfused step: gate/up
-            self.gu = DeviceBuffer.empty((2 * c.ffn,), np.float32)
-            self.gate_view = self.gu.view(0, c.ffn * 4, np.float32)
-            self.up_view = self.gu.view(c.ffn * 4, c.ffn * 4, np.float32)
         self.logits = DeviceBuffer.empty((c.vocab,), np.float32)
         self.token = DeviceBuffer.empty((1,), np.int32)
         self.state = DeviceBuffer.empty((4,), np.int32)  # pos, kv_len, prompt_len, token
@@ -375,20 +370,18 @@ class Decoder:
         ops.residual(self.ple_yn, self.x, self.x, c.hidden, stream=stream)
 
     def _layer_q8_0(self, li: int, L: LayerWeights, scale: float, stream) -> None:
-        """One layer with Q8_0 projections: the step graph's ops, the norms,
-        residuals and the attention combine folded into the GEMVs (input_norm +
-        q/k/v_proj, rope_q / rope_k, the cache write, attention as split
-        partials into the decoder's own buffer, combine + o_proj +
-        attn_residual, post_attn_norm + gate/up_proj, activation, down_proj +
-        ffn_residual): eight dispatches, no library workspace, so a captured
-        graph stays valid whatever other attention calls the process makes."""
+        """One layer with Q8_0 projections in the five dispatches of the Q4_K
+        layer: input_norm + q/k/v_proj + rope_q / rope_k + the cache write,
+        attention as split partials into the decoder's own buffer, combine +
+        o_proj + attn_residual, post_attn_norm + gate/up_proj + activation,
+        down_proj + ffn_residual.  No library workspace, so a captured graph
+        stays valid whatever other attention calls the process makes."""
         c = self.cfg
-        ops.matmul_q8_0(L.wqkv, self.x, self.qkv, c.qkv_rows, c.hidden, stream=stream, norm_weight=L.norm_attn,
-                        norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset)
-        ops.rope(self.qk_view, self.freq_cis, 1, c.heads + c.kv_heads, c.head_dim, position_buffer=self.pos_view,
-                 stream=stream)
-        ops.kv_write(self.k_view, self.v_view, L.k_cache, L.v_cache, c.kv_heads, c.max_seq, c.head_dim,
-                     position_buffer=self.pos_view, stream=stream)
+        ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads, num_kv_heads=c.kv_heads,
+                        head_dim=c.head_dim, freq_cis=self.freq_by_layer[li], position_buffer=self.pos_view,
+                        key_cache=L.k_cache, val_cache=L.v_cache, max_seq_len=c.max_seq, norm_weight=L.norm_attn,
+                        norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset, stream=stream,
+                        weight_format="q8_0")
         splits = ops.attention_partials(self.q_view, L.k_cache, L.v_cache, self.attn_parts, batch=1,
                                         num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim, kv_len=0,
                                         kv_stride=c.max_seq, scale=scale, max_splits=self.max_attn_splits,
@@ -396,9 +389,9 @@ class Decoder:
                                         softcap=c.attn_softcap, stream=stream)
         ops.matmul_q8_0_attn_out(L.wo, self.attn_parts, splits, c.heads, c.head_dim, self.x, c.hidden,
                                  residual=self.x, stream=stream)
-        ops.matmul_q8_0(L.wgu, self.x, self.gu, 2 * c.ffn, c.hidden, stream=stream, norm_weight=L.norm_ffn,
-                        norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset)
-        ops.gelu_gated(self.gate_view, self.up_view, self.h, c.ffn, stream=stream)
+        ops.matmul_q4k_fused(L.wgu, self.x, self.h, 2 * c.ffn, c.hidden, norm_weight=L.norm_ffn, norm_eps=c.eps,
+                             norm_weight_offset=c.norm_weight_offset, gated=True, stream=stream,
+                             weight_format="q8_0")
         ops.matmul_q8_0(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)
 
     # ---- prompt ----------------------------------------------------------------
@@ -428,8 +421,8 @@ class Decoder:
         ffn_residual -- each "+" folded into the GEMM's pre-pass or the pass
         that sums its K splits), then the last token's final norm + lm_head +
         sample.
-        Q4_K layers run the Q4_K GEMM and the interleaved-pair RoPE, Q8_0
-        layers the Q8_0 GEMM and the rotate-half RoPE of their decode step.
+        Q4_K layers run the Q4_K GEMM, Q8_0 layers the Q8_0 GEMM; both the
+        interleaved-pair RoPE of their decode step.
         Leaves the decoder where teacher-forced decode steps over the prompt
         would: cache rows 0..P-1 written, the first new token in ids[P],
         state = (P, P + 1, P, token)."""
@@ -449,20 +442,15 @@ class Decoder:
         off = c.norm_weight_offset
         ids = self.ids.view(0, P * 4, np.int32)
         ops.embed(self.embed, ids, b["x"], P, c.vocab, c.hidden, c.embed_scale, stream=stream)
-        # Q4_K layers hold q/k rows as interleaved rotation pairs and gate/up
-        # rows interleaved; Q8_0 layers hold heads in order (rotate-half
-        # RoPE) and the gate rows before the up rows
-        q8 = c.weight_format == "q8_0"
+        # both formats hold q/k rows as interleaved rotation pairs and gate/up
+        # rows interleaved
         fmt = c.weight_format
-        rope_rows = ops.qkv_rope_half_kv_rows if q8 else ops.qkv_rope_kv_rows
-        act = ops.GEGLU_HALVES if q8 else ops.GEGLU_PAIRS
         gemm = ops.matmul_gemm_f32_fused  # the norms, residuals and GeGLU ride on the GEMMs
         for li, L in enumerate(self.layers):
             gemm(b["x"], L.wqkv, b["qkv"], P, c.qkv_rows, c.hidden, fmt, norm_weight=L.norm_attn, norm_eps=c.eps,
                  norm_weight_offset=off, stream=stream)
-            freq = self.freq_cis if q8 else self.freq_by_layer[li]  # the Q8_0 decode step's table
-            rope_rows(b["qkv"], P, c.qkv_rows, c.heads, c.kv_heads, hd, freq, 0, L.k_cache, L.v_cache, c.max_seq,
-                      stream=stream)
+            ops.qkv_rope_kv_rows(b["qkv"], P, c.qkv_rows, c.heads, c.kv_heads, hd, self.freq_by_layer[li], 0,
+                                 L.k_cache, L.v_cache, c.max_seq, stream=stream)
             ops.attention_prefill_f16kv(b["qkv"], L.k_cache, L.v_cache, b["att"], num_heads=c.heads,
                                         num_kv_heads=c.kv_heads, head_dim=hd, query_len=P, kv_len=P,
                                         kv_stride=c.max_seq, start_pos=0, scale=1.0 / math.sqrt(hd),
@@ -470,7 +458,7 @@ class Decoder:
                                         q_row_stride=c.qkv_rows, stream=stream)
             gemm(b["att"], L.wo, b["x"], P, c.hidden, c.q_dim, fmt, residual=b["x"], stream=stream)
             gemm(b["x"], L.wgu, b["h"], P, 2 * c.ffn, c.hidden, fmt, norm_weight=L.norm_ffn, norm_eps=c.eps,
-                 norm_weight_offset=off, activation=act, stream=stream)
+                 norm_weight_offset=off, activation=ops.GEGLU_PAIRS, stream=stream)
             gemm(b["h"], L.wd, b["x"], P, c.hidden, c.ffn, fmt, residual=b["x"], stream=stream)
         last = b["x"].view((P - 1) * c.hidden * 4, c.hidden * 4, np.float32)
         nparts = ops.lm_head_sample(self.lm_head, last, c.vocab, c.hidden, self.argmax_parts,

@@ -343,15 +343,26 @@ def matmul_q4k_attn_out(weight: DeviceBuffer, partials: DeviceBuffer, splits: in
               _stream_ptr(stream))
 
 
+def _weight_check(weight: DeviceBuffer, n: int, k: int, weight_format: str) -> None:
+    if weight_format == "q8_0":
+        if weight.nbytes != n * _q8_0.row_bytes(k):
+            raise ValueError(f"Q8_0 rowwise byte length {weight.nbytes} != expected {n * _q8_0.row_bytes(k)}")
+    elif weight_format == "q4k":
+        _q4k_weight_check(weight, n, k)
+    else:
+        raise ValueError(f"weight_format {weight_format!r} is not q4k or q8_0")
+
+
 def matmul_q4k_fused(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBuffer, n: int, k: int, *,
                      norm_weight: DeviceBuffer | None = None, norm_eps: float = 1e-6,
                      norm_weight_offset: bool = True, residual: DeviceBuffer | None = None,
-                     gated: bool = False, stream=None) -> None:
+                     gated: bool = False, stream=None, weight_format: str = "q4k") -> None:
     """``matmul_q4k`` with its step-list neighbours folded in: an ``rmsnorm``
     prologue (``norm_weight``), an ``attn_residual``/``ffn_residual``
     epilogue (``residual``) or a ``gelu_gated`` epilogue over interleaved
-    (gate, up) rows (``gated``: output has n/2 values)."""
-    _q4k_weight_check(weight, n, k)
+    (gate, up) rows (``gated``: output has n/2 values).  ``weight_format``
+    "q8_0": the same over Q8_0 rows (``doe_q8_0_gemv_fused``)."""
+    _weight_check(weight, n, k, weight_format)
     _need(activation, k * 4, "activation")
     _need(output, (n // 2 if gated else n) * 4, "output")
     if norm_weight is not None:
@@ -360,7 +371,8 @@ def matmul_q4k_fused(weight: DeviceBuffer, activation: DeviceBuffer, output: Dev
         _need(residual, n * 4, "residual")
     nw = C.c_void_p(norm_weight.ptr) if norm_weight is not None else C.c_void_p(None)
     rs = C.c_void_p(residual.ptr) if residual is not None else C.c_void_p(None)
-    _lib.call("doe_q4k_gemv_fused", _p(weight), _p(activation), _p(output), n, k, nw, norm_eps,
+    fn = "doe_q8_0_gemv_fused" if weight_format == "q8_0" else "doe_q4k_gemv_fused"
+    _lib.call(fn, _p(weight), _p(activation), _p(output), n, k, nw, norm_eps,
               int(norm_weight_offset), rs, int(gated), _stream_ptr(stream))
 
 
@@ -368,13 +380,14 @@ def qkv_rope_kv(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBu
                 num_heads: int, num_kv_heads: int, head_dim: int, freq_cis: DeviceBuffer,
                 position_buffer: DeviceBuffer, key_cache: DeviceBuffer, val_cache: DeviceBuffer,
                 max_seq_len: int, norm_weight: DeviceBuffer | None = None, norm_eps: float = 1e-6,
-                norm_weight_offset: bool = True, stream=None) -> None:
+                norm_weight_offset: bool = True, stream=None, weight_format: str = "q4k") -> None:
     """input_norm + q/k/v_proj + rope_q/rope_k + cache write in one dispatch.
 
     Q and K weight rows must be interleaved rotation pairs per head (see
-    ``interleave_rope_rows``); output holds [q; k; v] in that order."""
+    ``interleave_rope_rows``); output holds [q; k; v] in that order.
+    ``weight_format`` "q4k" or "q8_0" names the rows' block format."""
     n = (num_heads + 2 * num_kv_heads) * head_dim
-    _q4k_weight_check(weight, n, hidden)
+    _weight_check(weight, n, hidden, weight_format)
     _need(activation, hidden * 4, "activation")
     _need(output, n * 4, "output")
     cache = num_kv_heads * max_seq_len * head_dim * 2
@@ -386,7 +399,8 @@ def qkv_rope_kv(weight: DeviceBuffer, activation: DeviceBuffer, output: DeviceBu
     nw = C.c_void_p(norm_weight.ptr) if norm_weight is not None else C.c_void_p(None)
     kc = _p(key_cache) if num_kv_heads else C.c_void_p(None)
     vc = _p(val_cache) if num_kv_heads else C.c_void_p(None)
-    _lib.call("doe_q4k_gemv_qkv_rope_kv", _p(weight), _p(activation), _p(output), hidden, nw, norm_eps,
+    fn = "doe_q8_0_gemv_qkv_rope_kv" if weight_format == "q8_0" else "doe_q4k_gemv_qkv_rope_kv"
+    _lib.call(fn, _p(weight), _p(activation), _p(output), hidden, nw, norm_eps,
               int(norm_weight_offset), num_heads, num_kv_heads, head_dim, _p(freq_cis), _p(position_buffer),
               kc, vc, max_seq_len, _stream_ptr(stream))
 

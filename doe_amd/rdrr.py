@@ -207,9 +207,9 @@ def _expect(arr: np.ndarray, shape: tuple, what: str) -> np.ndarray:
 
 def load_decoder_weights(art: RdrrArtifact, dec) -> None:
     """Fills a doe_amd.model.Decoder's device weights from the artifact: the
-    Q4_K_M rows move unchanged (q/k rows reordered into rotation pairs, gate
-    and up rows interleaved; Q8_0 rows, for a decoder of that weight format,
-    in their own order), norms and the f16 embedding / lm_head are
+    Q4_K_M rows (or Q8_0 rows, for a decoder of that weight format) move
+    unchanged, q/k rows reordered into rotation pairs and gate and up rows
+    interleaved; norms and the f16 embedding / lm_head are
     uploaded as they are (BF16 or F32 sources converted to the decoder's
     dtype).  input_layernorm feeds attention, post_attention_layernorm the
     FFN (the step graph's post_attn_norm before gate_proj)."""
@@ -228,17 +228,14 @@ def load_decoder_weights(art: RdrrArtifact, dec) -> None:
         q = rows("self_attn.q_proj", (c.q_dim, rb_h))
         k = rows("self_attn.k_proj", (c.kv_dim, rb_h))
         v = rows("self_attn.v_proj", (c.kv_dim, rb_h))
-        if not q8:  # the fused Q4_K kernel rotates interleaved pairs
-            q, k = interleave_rope_rows(q, c.head_dim), interleave_rope_rows(k, c.head_dim)
+        # the fused q/k/v kernels rotate interleaved pairs
+        q, k = interleave_rope_rows(q, c.head_dim), interleave_rope_rows(k, c.head_dim)
         L.wqkv.upload(np.concatenate([q, k, v]))
         L.wo.upload(rows("self_attn.o_proj", (c.hidden, rb_q)))
         gate = rows("mlp.gate_proj", (c.ffn, rb_h))
         up = rows("mlp.up_proj", (c.ffn, rb_h))
-        if q8:
-            gu = np.concatenate([gate, up])
-        else:
-            gu = np.empty((2 * c.ffn, rb_h), np.uint8)
-            gu[0::2], gu[1::2] = gate, up
+        gu = np.empty((2 * c.ffn, rb_h), np.uint8)
+        gu[0::2], gu[1::2] = gate, up
         L.wgu.upload(gu)
         L.wd.upload(rows("mlp.down_proj", (c.hidden, rb_f)))
         for key, buf in (("input_layernorm", L.norm_attn), ("post_attention_layernorm", L.norm_ffn)):

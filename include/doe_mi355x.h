@@ -135,6 +135,27 @@ int doe_q8_0_gemv_attn_out(const void *weight_q8_0, const float *attn_partials, 
                            int64_t num_heads, int64_t head_dim, float *output, int64_t n,
                            const float *residual, doe_stream_t stream);
 
+/* doe_q8_0_gemv with the steps around a decode projection folded in, as
+ * doe_q4k_gemv_fused: norm_weight != NULL runs the activation through
+ * RMSNorm (the input_norm / post_attn_norm step); residual != NULL adds it
+ * (residual == output allowed); gated != 0 takes rows as interleaved (gate,
+ * up) pairs and writes n/2 values gelu_tanh(dot_2i) * dot_2i+1 (the
+ * gate/up_proj -> activation steps; gelu_gated.wgsl:1-14).  gated and
+ * residual are exclusive; gated needs n even. */
+int doe_q8_0_gemv_fused(const void *weight_q8_0, const float *activation, float *output, int64_t n,
+                        int64_t k, const float *norm_weight, float norm_eps, int norm_weight_offset,
+                        const float *residual, int gated, doe_stream_t stream);
+/* doe_q4k_gemv_qkv_rope_kv over Q8_0 rows: input_norm + q/k/v_proj + rope_q /
+ * rope_k + the K/V cache write of a decode step in one dispatch, the q/k
+ * rows of each head stored as interleaved rotation pairs (row 2i = dim i,
+ * row 2i+1 = dim i + head_dim/2), the same arguments and rules. */
+int doe_q8_0_gemv_qkv_rope_kv(const void *weight_q8_0, const float *activation, float *output,
+                              int64_t hidden, const float *norm_weight, float norm_eps,
+                              int norm_weight_offset, int64_t num_heads, int64_t num_kv_heads,
+                              int64_t head_dim, const float *freq_cis, const int32_t *position_dev,
+                              uint16_t *key_cache, uint16_t *val_cache, int64_t max_seq_len,
+                              doe_stream_t stream);
+
 /* The attention output projection of one sequence with the split-attention
  * combine folded into its activation load: output[i] = sum_k
  * dequant(W)[i][k] * attn[k] (+ residual[i]), attn = the combine of the

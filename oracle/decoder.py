@@ -25,8 +25,7 @@ class OracleDecoder:
             # oracle follows the rotate-half form of rope.wgsl on plain rows
             wqkv = L.wqkv.download().reshape(L.qkv_rows, -1)
             qk = L.q_dim + L.kv_dim
-            if c.weight_format == "q4k":  # Q8_0 rows are stored plain
-                wqkv[:qk] = deinterleave_rope_rows(wqkv[:qk], hd)
+            wqkv[:qk] = deinterleave_rope_rows(wqkv[:qk], hd)
             key = id(dec.freq_by_layer[li])
             if key not in tables:
                 tables[key] = dec.freq_by_layer[li].download()
@@ -143,10 +142,7 @@ class OracleDecoder:
             x = ora.residual(self.gemv(L["wo"], attn, c.hidden, L["q_dim"]), x)
             xn2 = ora.rmsnorm(x, L["n2"], c.eps, off)
             gu = self.gemv(L["wgu"], xn2, 2 * c.ffn, c.hidden)
-            if c.weight_format == "q8_0":  # gate rows then up rows
-                h = ora.geglu(gu[: c.ffn], gu[c.ffn:])
-            else:  # interleaved gate/up rows
-                h = ora.geglu(gu[0::2], gu[1::2])
+            h = ora.geglu(gu[0::2], gu[1::2])  # interleaved gate/up rows
             x = ora.residual(self.gemv(L["wd"], h, c.hidden, c.ffn), x)
             if u is not None:
                 g = ora.q4k_gemv(L["w_ple_gate"], x, c.ple_width, c.hidden)

@@ -61,8 +61,9 @@ SMALL_Q8 = dataclasses.replace(SMALL, weight_format="q8_0")
 
 
 def test_q8_0_decoder_matches_oracle(dev, ora):
-    # Q8_0 projections through the unfused ops, against the oracle decoder
-    # with Q8_0 GEMVs; a sliding window on layer 0 and a softcap included
+    # Q8_0 projections through the five fused dispatches of a layer, against
+    # the oracle decoder with Q8_0 GEMVs; a sliding window on layer 0 and a
+    # softcap included
     from doe_amd import execution
 
     cfg = dataclasses.replace(SMALL_Q8, attn_softcap=30.0)
@@ -218,7 +219,7 @@ def _write_rdrr(dec, root):
     rb = c.row_bytes
     q8 = c.weight_format == "q8_0"
     wdt = "Q8_0" if q8 else "Q4_K_M"
-    plain = (lambda rows, hd: rows) if q8 else deinterleave_rope_rows  # Q8_0 q/k rows are stored plain
+    plain = deinterleave_rope_rows  # the device holds q/k rows as rotation pairs
     tensors, blobs = {}, [bytearray(), bytearray()]
 
     def put(name, arr, dtype, shape, layout=None, split=False):
@@ -246,7 +247,7 @@ def _write_rdrr(dec, root):
         put(f"{p}.self_attn.v_proj.weight", v, wdt, (c.kv_dim, c.hidden), "row")
         put(f"{p}.self_attn.o_proj.weight", L.wo.download(), wdt, (c.hidden, c.q_dim), "row")
         gu = L.wgu.download().reshape(2 * c.ffn, rb(c.hidden))
-        gate, up = (gu[:c.ffn], gu[c.ffn:]) if q8 else (gu[0::2], gu[1::2])
+        gate, up = gu[0::2], gu[1::2]
         put(f"{p}.mlp.gate_proj.weight", gate, wdt, (c.ffn, c.hidden), "row")
         put(f"{p}.mlp.up_proj.weight", up, wdt, (c.ffn, c.hidden), "row")
         put(f"{p}.mlp.down_proj.weight", L.wd.download(), wdt, (c.hidden, c.ffn), "row", split=(i == 1))
@@ -450,14 +451,18 @@ Q8_PREFILL_DRIFT = {2: 5e-3, 26: 3e-2}
 
 
 def _layer0_cache_err(dec, oracle, P):
+    # the device caches K in the rotation-pair order of its q/k rows (dims i
+    # and i + head_dim/2 side by side); the oracle in plain dim order
     L, O = dec.layers[0], oracle.layers[0]
-    return max(rel_l2(L.k_cache.download()[:, :P], O["kc"][:, :P]),
+    kc = L.k_cache.download()[:, :P]
+    kc = np.concatenate([kc[..., 0::2], kc[..., 1::2]], axis=-1)
+    return max(rel_l2(kc, O["kc"][:, :P]),
                rel_l2(L.v_cache.download()[:, :P], O["vc"][:, :P]))
 
 
 def test_prefill_q8_0_matches_oracle_decoder(dev, ora):
-    # a Q8_0 model's prompt as one batched pass (Q8_0 GEMMs, rotate-half RoPE
-    # rows, GeGLU over gate/up halves), against the oracle decoder token by
+    # a Q8_0 model's prompt as one batched pass (Q8_0 GEMMs, the rotation-pair
+    # RoPE rows, GeGLU over interleaved gate/up rows), against the oracle decoder token by
     # token; then 4 decode steps on its cache
     dec = Decoder(SMALL_Q8, keep_logits=True)
     dec.init_random(seed=22)

@@ -186,3 +186,103 @@ def test_q8_0_gemv_rejects_aliased_activation(dev):
     with pytest.raises(DoeError, match="splits"):
         _lib.call("doe_q8_0_gemv_attn_out", C.c_void_p(dw.ptr), C.c_void_p(out.ptr), 9, 1, 64, C.c_void_p(x.ptr),
                   n, None, None)
+
+
+@pytest.mark.parametrize("ffn,k,offset", [(9216, 2304, True), (300, 1000, False), (7, 33, True)])
+def test_q8_0_gemv_gated_matches_oracle(dev, ora, ffn, k, offset):
+    # post_attn_norm + gate/up_proj + activation in one dispatch over
+    # interleaved (gate, up) rows: against the oracle rmsnorm, GEMV and GeGLU,
+    # and bit for bit against the unfused GEMV + doe_geglu_pairs at the same
+    # wave grouping
+    print(f"q8_0 gated ffn={ffn} k={k}", flush=True)
+    n = 2 * ffn
+    rng = np.random.default_rng(ffn + k)
+    w = q8_0.random_q8_0(rng, n, k)
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    nw = (rng.standard_normal(k) * 0.1).astype(np.float32)
+    g = ora.q8_0_gemv(w, ora.rmsnorm(x, nw, 1e-6, offset), n, k)
+    want = ora.geglu(g[0::2], g[1::2])
+    dw, dx, dn = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), DeviceBuffer.from_array(nw)
+    out = DeviceBuffer.empty((ffn,), np.float32)
+    ops.matmul_q4k_fused(dw, dx, out, n, k, norm_weight=dn, norm_eps=1e-6, norm_weight_offset=offset, gated=True,
+                         weight_format="q8_0")
+    got = out.download()
+    assert rel_l2(got, want) <= 1e-5
+    try:
+        ops.tune("q8_0_gemv.rows", 2)
+        gu = DeviceBuffer.empty((n,), np.float32)
+        ops.matmul_q8_0(dw, dx, gu, n, k, norm_weight=dn, norm_eps=1e-6, norm_weight_offset=offset)
+        h = DeviceBuffer.empty((ffn,), np.float32)
+        ops.geglu_pairs(gu, h, ffn)
+        fused = DeviceBuffer.empty((ffn,), np.float32)
+        ops.matmul_q4k_fused(dw, dx, fused, n, k, norm_weight=dn, norm_eps=1e-6, norm_weight_offset=offset,
+                             gated=True, weight_format="q8_0")
+        assert np.array_equal(fused.download().view(np.uint32), h.download().view(np.uint32))
+    finally:
+        ops.tune("q8_0_gemv.rows", 0)
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd,hidden,pos", [(8, 4, 256, 2304, 37), (4, 2, 64, 320, 0),
+                                                          (2, 1, 128, 96, 5), (4, 0, 64, 320, 3)])
+def test_q8_0_qkv_rope_kv_matches_oracle(dev, ora, heads, kv_heads, hd, hidden, pos):
+    # input_norm + q/k/v_proj + rope_q / rope_k + the cache write in one
+    # dispatch, the q/k rows stored as rotation pairs: q and the cached k
+    # against the oracle's rotate-half RoPE on plain rows, v as projected;
+    # other cache rows untouched; kv_heads 0 projects q alone
+    from doe_amd.model import rope_table
+    from doe_amd.ops import deinterleave_rope_rows, interleave_rope_rows
+
+    print(f"q8_0 qkv_rope_kv {heads}/{kv_heads}x{hd} hidden={hidden} pos={pos}", flush=True)
+    rng = np.random.default_rng(heads * 100 + hd + pos)
+    qd, kvd = heads * hd, kv_heads * hd
+    n = qd + 2 * kvd
+    rb = q8_0.row_bytes(hidden)
+    w = q8_0.random_q8_0(rng, n, hidden).reshape(n, rb)
+    dev_w = w.copy()
+    dev_w[:qd] = interleave_rope_rows(w[:qd], hd)
+    if kv_heads:
+        dev_w[qd:qd + kvd] = interleave_rope_rows(w[qd:qd + kvd], hd)
+    x = (rng.standard_normal(hidden) * 2).astype(np.float32)
+    nw = (rng.standard_normal(hidden) * 0.1).astype(np.float32)
+    max_seq = 64
+    table = rope_table(max_seq, hd, 10000.0)
+    qkv = ora.q8_0_gemv(w.reshape(-1), ora.rmsnorm(x, nw, 1e-6, True), n, hidden)
+    qk = ora.rope(qkv[:qd + kvd], table, 1, heads + kv_heads, hd, pos)
+    out = DeviceBuffer.empty((n,), np.float32)
+    posb = DeviceBuffer.from_array(np.array([pos], np.int32))
+    fill = np.full((max(kv_heads, 1), max_seq, hd), 7.0, np.float16)
+    kc, vc = DeviceBuffer.from_array(fill), DeviceBuffer.from_array(fill)
+    ops.qkv_rope_kv(DeviceBuffer.from_array(dev_w.reshape(-1)), DeviceBuffer.from_array(x), out, hidden=hidden,
+                    num_heads=heads, num_kv_heads=kv_heads, head_dim=hd, freq_cis=DeviceBuffer.from_array(table),
+                    position_buffer=posb, key_cache=kc, val_cache=vc, max_seq_len=max_seq,
+                    norm_weight=DeviceBuffer.from_array(nw), norm_eps=1e-6, norm_weight_offset=True,
+                    weight_format="q8_0")
+    got = out.download()
+    assert rel_l2(deinterleave_rope_rows(got[:qd], hd), qk[:qd]) <= 1e-5
+    if not kv_heads:
+        assert np.array_equal(kc.download(), fill) and np.array_equal(vc.download(), fill)
+        return
+    k_got = deinterleave_rope_rows(got[qd:qd + kvd], hd)
+    assert rel_l2(k_got, qk[qd:]) <= 1e-5
+    assert rel_l2(got[qd + kvd:], qkv[qd + kvd:]) <= 1e-5
+    kcg, vcg = kc.download(), vc.download()
+    kc_plain = np.concatenate([kcg[..., 0::2], kcg[..., 1::2]], axis=-1)  # cached in pair order
+    # the cache rows are the f16 of the device's own rotated rows
+    assert np.array_equal(kcg[:, pos].reshape(-1), got[qd:qd + kvd].astype(np.float16))
+    assert np.array_equal(vcg[:, pos].reshape(-1), got[qd + kvd:].astype(np.float16))
+    assert rel_l2(kc_plain[:, pos].reshape(-1).astype(np.float32), qk[qd:]) <= 1e-3
+    others = np.ones(max_seq, bool)
+    others[pos] = False
+    assert np.all(kcg[:, others] == 7.0) and np.all(vcg[:, others] == 7.0)
+
+
+def test_q8_0_fused_rejects(dev):
+    w = DeviceBuffer.from_array(q8_0.random_q8_0(np.random.default_rng(0), 6, 64))
+    x = DeviceBuffer.empty((64,), np.float32)
+    y = DeviceBuffer.empty((6,), np.float32)
+    with pytest.raises(DoeError):  # gated needs an even row count
+        _lib.call("doe_q8_0_gemv_fused", C.c_void_p(w.ptr), C.c_void_p(x.ptr), C.c_void_p(y.ptr), 5, 64,
+                  None, 1e-6, 0, None, 1, None)
+    with pytest.raises(DoeError):  # gated and residual are exclusive
+        _lib.call("doe_q8_0_gemv_fused", C.c_void_p(w.ptr), C.c_void_p(x.ptr), C.c_void_p(y.ptr), 6, 64,
+                  None, 1e-6, 0, C.c_void_p(y.ptr), 1, None)
