@@ -301,3 +301,26 @@ def test_reference_lowering_known_answers():
                                 {"phase": "decode", "op": "sample", "kernelKey": "sampler", "kind": "sample"}]})
     attns = [s for s in g.phase("decode") if s.op == "attention"]
     assert [ex._window(g, a, i) for i, a in enumerate(attns)] == [512, 0]
+
+
+def test_gemma4_31b_graphs_plan_per_layer():
+    # gemma-4-31b-smoke.json: 61 layers, layerPattern every 5 offset 4 (global
+    # layers 4, 9, ..., 59), the others sliding over 512 keys, the last 4
+    # layers (57..60) sharing KV: a sliding one reads layer 56's cache, the
+    # global layer 59 that of layer 54; per-layer embeddings (pleWidth 256).
+    g = ex.load_step_graph(GOLD / "gemma-4-31b-smoke.json")
+    mc = g.model_config
+    plan = ex.plan_decode(g, mc["numLayers"], mc["headDim"], mc.get("globalHeadDim"))
+    assert len(plan.windows) == 61
+    assert [i for i, w in enumerate(plan.windows) if w == 0] == list(range(4, 61, 5))
+    assert all(w == 512 for i, w in enumerate(plan.windows) if i % 5 != 4)
+    assert [(i, s) for i, s in enumerate(plan.kv_sources) if s != i] == [(57, 56), (58, 56), (59, 54), (60, 56)]
+    assert plan.ple is not None
+    # gemma-4-31b-af16-smoke.json lists only the sliding attention step: the
+    # one-layer template repeats it in all 60 layers, none shares KV
+    g16 = ex.load_step_graph(GOLD / "gemma-4-31b-af16-smoke.json")
+    mc16 = g16.model_config
+    plan16 = ex.plan_decode(g16, mc16["numLayers"], mc16["headDim"], mc16.get("globalHeadDim"))
+    assert plan16.windows == (512,) * 60
+    assert plan16.kv_sources in (None, (), tuple(range(60)))
+    assert plan16.ple is None
