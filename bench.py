@@ -4,16 +4,20 @@
 Headline (`value`): Q4_K_M decode GEMV throughput in GB/s of algorithmic
 bytes on the 2B-class FFN-up shape M=1, N=9216, K=2304 (weights 11,943,936 B
 + x 9,216 B + y 36,864 B = 11,990,016 B per GEMV).  One step is one GEMV
-over one of `--copies` distinct weight copies (rotated so the weights stream
-from HBM, not from the 256 MB Infinity Cache); steps are replayed from a HIP
-graph so host launch cost is not timed.  Inputs are synthetic and seeded.
+on one of at least 48 distinct weight copies (rotated, so every copy is read
+again only after 47 others, 561 MB: the weights stream from HBM, not from the
+256 MB Infinity Cache).  A timed window is exactly `--steps` back-to-back
+launches; `--windows` windows continue the rotation inside one HIP graph
+(host launch cost is not timed), with a device timestamp on the kernel's
+stream between windows, and the headline is the median window divided by
+`--steps`.  HIP events around the timed graph replay give the mean over the
+whole timed region beside it.  Inputs are synthetic and seeded.
 
-`roofline` reports the GEMV kernel's average launch duration -- HIP events on
-its stream around the timed region, divided by the launches in it (the graph
-replays back-to-back GEMVs only) -- against the 8 TB/s HBM peak, with the HBM
-traffic per launch measured by rocprofv3 counters (read from the committed
-profile summary).  `cpu_baseline` times the single-threaded CPU oracle on a
-bounded sample of the same workload on this host.
+`roofline` reports that per-launch time against the 8 TB/s HBM peak, with
+the HBM traffic per launch measured by rocprofv3 counters (read from the
+committed profile summary).  `cpu_baseline` times the single-threaded CPU
+oracle on a bounded sample of the same workload on this host: the median of
+its per-GEMV times.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -38,6 +42,8 @@ METRIC = "Q4_K GEMV HBM GB/s (% of peak) + decode tok/s, 2B-class bs=1"
 HBM_PEAK_GBS = 8000.0
 N, K = 9216, 2304
 GEMV_BYTES = N * (K // 256) * 144 + 4 * K + 4 * N  # 11,990,016
+CPU_DECODE_RUNS = 5  # oracle decode steps per CPU baseline (the median is reported)
+MIN_COPIES = 48  # 48 x 11.94 MB = 573 MB: more than twice the 256 MB Infinity Cache
 
 
 def log(msg: str) -> None:
@@ -54,17 +60,32 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def timed_gemv_replays(doe, n, k, steps, warmup, copies, seed):
-    """Q4_K GEMVs over `copies` distinct weight copies, replayed from HIP
-    graphs: exactly `steps` launches in the timed region (full replays of one
-    launch per copy, then a partial replay for the remainder), HIP events on
-    the kernel's stream after every replay.  Returns the per-launch times."""
-    from doe_amd import DeviceBuffer, Event, Graph, Stream, ops, q4k
+def timed_gemv_windows(doe, n, k, steps, warmup, copies, windows, seed):
+    """Q4_K GEMVs over distinct weight copies, timed in windows of exactly
+    `steps` back-to-back launches.  The windows continue one rotation over
+    the copies, so every copy is read again only after the `copies - 1`
+    others: with at least 48 copies of the 12 MB config that is more than
+    the 256 MB Infinity Cache holds.  All windows sit in one HIP graph with a
+    device timestamp (doe_device_timestamp, the GPU's constant 100 MHz clock,
+    on the kernel's stream) before the first window and after each one, and
+    the graph replays once untimed (a full rotation, and at least `warmup`
+    launches) before the timed replay, which HIP events on the same stream
+    also bracket.  A graph launch of its own per window would put ~10 us of
+    graph-launch time into every window (0.5 us per launch at 20 launches);
+    event records inside a graph cannot be timed.  Returns the per-window
+    times: the headline is the median window divided by `steps`, the events
+    give the mean over the timed region (timestamp kernels included)."""
+    import ctypes as C
+
+    from doe_amd import DeviceBuffer, Event, Graph, Stream, _lib, ops, q4k
 
     rng = np.random.default_rng(seed)
     w = q4k.random_q4k(rng, n, k)
     x = rng.standard_normal(k, dtype=np.float32)
-    copies = max(1, min(copies, steps))
+    if steps <= copies:
+        copies = steps * -(-copies // steps)  # whole windows per rotation
+    per_rot = copies // math.gcd(copies, steps)  # windows that end a rotation
+    windows = per_rot * -(-max(windows, per_rot) // per_rot)  # whole rotations per replay
     bufs = [DeviceBuffer.from_array(w)]
     for _ in range(copies - 1):
         b = DeviceBuffer(w.nbytes)
@@ -72,45 +93,55 @@ def timed_gemv_replays(doe, n, k, steps, warmup, copies, seed):
         bufs.append(b)
     dx = DeviceBuffer.from_array(x)
     dy = DeviceBuffer.empty((n,), np.float32)
+    ts = DeviceBuffer.empty((windows + 1,), np.uint64)
+    hz = C.c_int64()
+    _lib.call("doe_device_timestamp_hz", C.byref(hz))
     doe.synchronize()
     s = Stream()
-    full, rest = divmod(steps, copies)
-    graph = Graph.capture(s, lambda: [ops.matmul_q4k(c, dx, dy, n, k, s) for c in bufs])
-    tail = Graph.capture(s, lambda: [ops.matmul_q4k(c, dx, dy, n, k, s) for c in bufs[:rest]]) if rest else None
-    for _ in range(max(1, -(-warmup // copies))):
-        graph.launch(s)
+    sp = C.c_void_p(s.handle)
+
+    def body():
+        _lib.call("doe_device_timestamp", C.c_void_p(ts.ptr), sp)
+        for i in range(windows):
+            for j in range(steps):
+                ops.matmul_q4k(bufs[(i * steps + j) % copies], dx, dy, n, k, s)
+            _lib.call("doe_device_timestamp", C.c_void_p(ts.ptr + 8 * (i + 1)), sp)
+
+    graph = Graph.capture(s, body)
+    for _ in range(max(1, -(-warmup // (windows * steps)))):
+        graph.launch(s)  # untimed: a full rotation (and the warmup launches)
     s.synchronize()
-    ev = [Event() for _ in range(full + 2)]
     doe.synchronize()
+    e0, e1 = Event(), Event()
     t0 = time.perf_counter()
-    ev[0].record(s)
-    for i in range(full):
-        graph.launch(s)
-        ev[i + 1].record(s)
-    if tail is not None:
-        tail.launch(s)
-    ev[full + 1].record(s)
-    ev[full + 1].synchronize()
+    e0.record(s)
+    graph.launch(s)
+    e1.record(s)
+    e1.synchronize()
+    doe.synchronize()
     wall = time.perf_counter() - t0
-    total_ms = ev[0].elapsed_ms(ev[full + 1])
-    per_replay = [ev[i].elapsed_ms(ev[i + 1]) / copies for i in range(full)]
+    stamps = ts.download().astype(np.int64)
+    win_ms = [float(d) / hz.value * 1e3 for d in np.diff(stamps)]
+    ev_ms = e0.elapsed_ms(e1)
     from oracle import oracle as ora  # the checker, outside the timed region
 
     got = dy.download()
     want = ora.q4k_gemv(w, x, n, k)
     rel = float(np.linalg.norm(got.astype(np.float64) - want) / np.linalg.norm(want))
-    for g in (graph, tail):
-        if g is not None:
-            g.destroy()
+    graph.destroy()
     s.destroy()
-    for c in bufs:
+    for c in bufs + [dx, dy, ts]:
         c.free()
+    med = float(np.median(win_ms))
     return {
         "steps": steps,
         "copies": copies,
-        "replays": full + (1 if rest else 0),
-        "ms_per_step": total_ms / steps,
-        "median_ms_per_launch": float(np.median(per_replay)) if per_replay else total_ms / steps,
+        "windows": windows,
+        "reuse_distance_bytes": (copies - 1) * w.nbytes,
+        "ms_per_step": med / steps,
+        "mean_ms_per_step": float(np.mean(win_ms)) / steps,
+        "event_ms_per_step": ev_ms / (windows * steps),
+        "window_ms": win_ms,
         "wall_s": wall,
         "rel_l2": rel,
         "w": w,
@@ -119,13 +150,15 @@ def timed_gemv_replays(doe, n, k, steps, warmup, copies, seed):
 
 
 def bench_gemv(args, doe):
-    log(f"gemv: N={N} K={K}, {args.steps} launches over {args.copies} weight copies")
-    r = timed_gemv_replays(doe, N, K, args.steps, args.warmup, args.copies, seed=0)
-    log(f"gemv: rel_l2 vs oracle {r['rel_l2']:.3e}; {r['ms_per_step'] * 1e3:.3f} us/launch over "
-        f"{r['steps']} launches ({r['replays']} graph replays, median {r['median_ms_per_launch'] * 1e3:.3f} "
-        f"us/launch), wall {r['wall_s']:.3f}s")
+    copies = max(args.copies, MIN_COPIES)
+    log(f"gemv: N={N} K={K}, windows of {args.steps} launches over >= {copies} rotating weight copies")
+    r = timed_gemv_windows(doe, N, K, args.steps, args.warmup, copies, args.windows, seed=0)
+    log(f"gemv: rel_l2 vs oracle {r['rel_l2']:.3e}; {r['ms_per_step'] * 1e3:.3f} us/launch (median of "
+        f"{r['windows']} windows of {r['steps']} launches over {r['copies']} copies; window mean "
+        f"{r['mean_ms_per_step'] * 1e3:.3f}, HIP events over the timed region {r['event_ms_per_step'] * 1e3:.3f}), "
+        f"wall {r['wall_s']:.3f}s")
     r["value_gbs"] = GEMV_BYTES / (r["ms_per_step"] * 1e-3) / 1e9
-    r["kernel"] = "q4k_gemv_mfma_kernel<0> (doe_amd/csrc/q4k_gemv.hip)"
+    r["kernel"] = "q4k_gemv_mfma_kernel<0, 1, 1> (doe_amd/csrc/q4k_gemv.hip)"
     return r
 
 
@@ -133,17 +166,22 @@ GL_N = 65536
 
 
 def bench_gemv_large(args, doe):
-    """The same Q4_K GEMV kernel at N=65536, K=2304 (85 MB of weights per
-    launch), where the per-dispatch latency is amortised over more bytes."""
+    """The same Q4_K GEMV at N=65536, K=2304 (85 MB of weights per launch,
+    the streaming kernel), where the per-dispatch latency is amortised over
+    more bytes: windows of 50 launches over 10 rotating copies (850 MB)."""
     byt = GL_N * (K // 256) * 144 + 4 * K + 4 * GL_N
     copies = max(2, -(-768 * 2 ** 20 // (GL_N * (K // 256) * 144)))
-    r = timed_gemv_replays(doe, GL_N, K, max(args.large_steps, 5 * copies), 2 * copies, copies, seed=5)
+    r = timed_gemv_windows(doe, GL_N, K, 5 * copies, 0, copies, args.windows, seed=5)
     gbs = byt / (r["ms_per_step"] * 1e-3) / 1e9
     log(f"gemv N={GL_N} K={K}: {r['ms_per_step'] * 1e3:.2f} us/launch, {gbs:.0f} GB/s "
         f"({100 * gbs / HBM_PEAK_GBS:.1f}% of peak), rel_l2 {r['rel_l2']:.2e}")
-    return {"workload": f"q4k_gemv M=1 N={GL_N} K={K}, {copies} rotating weight copies, HIP-graph replay",
-            "launches": r["steps"], "us_per_launch": round(r["ms_per_step"] * 1e3, 3),
-            "median_us_per_launch": round(r["median_ms_per_launch"] * 1e3, 3), "bytes_per_launch": byt,
+    return {"workload": f"q4k_gemv M=1 N={GL_N} K={K}, {r['copies']} rotating weight copies, median of "
+                        f"{r['windows']} windows of {r['steps']} launches in one HIP graph",
+            "kernel": "q4k_gemv_stream_kernel<0, 1, 2> (doe_amd/csrc/q4k_gemv.hip)",
+            "launches_per_window": r["steps"], "windows": r["windows"],
+            "us_per_launch": round(r["ms_per_step"] * 1e3, 3),
+            "mean_us_per_launch": round(r["mean_ms_per_step"] * 1e3, 3),
+            "event_us_per_launch": round(r["event_ms_per_step"] * 1e3, 3), "bytes_per_launch": byt,
             "achieved_gbs": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "rel_l2_vs_oracle": r["rel_l2"]}
 
@@ -294,20 +332,24 @@ def decode_parity_and_cpu(dec, prompt, s):
     tok = int(dec.token.download()[0])
     dec.keep_logits = False
     oracle = OracleDecoder(dec)
-    t0 = time.perf_counter()
-    want = oracle.step(0, int(prompt[0]))
-    el = time.perf_counter() - t0
+    times = []
+    for _ in range(CPU_DECODE_RUNS):  # step 0 again each time: the same work, the same logits
+        t0 = time.perf_counter()
+        want = oracle.step(0, int(prompt[0]))
+        times.append(time.perf_counter() - t0)
+    el = float(np.median(times))
     rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
     del oracle
     log(f"  decode parity: step-0 logits rel_l2 {rel:.2e}, token {tok} vs oracle {int(np.argmax(want))}; "
-        f"oracle step {el:.2f} s")
+        f"oracle step {el:.2f} s (median of {len(times)})")
     parity = {"step0_logits_rel_l2_vs_oracle": rel, "step0_token_equal": tok == int(np.argmax(want)),
               "tolerance": 1e-3}
-    cpu = {"value": round(1.0 / el, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-           "sample": f"one full-size decode step (position 0, every weight of every layer and the lm_head) of "
-                     f"the single-threaded C oracle decoder (f32 left-fold, -O2 -ffp-contract=off) in {el:.2f} s "
-                     f"on {cpu_model()} ({os.cpu_count()} logical cores on host); attention at position 0 "
-                     f"reads 1 key (< 1% of a token's bytes at the benchmarked lengths)"}
+    cpu = {"value": round(1.0 / el, 4), "unit": "tok/s", "cores": 1, "kind": "port", "runs": len(times),
+           "sample": f"median of {len(times)} full-size decode steps (position 0, every weight of every layer and "
+                     f"the lm_head) of the single-threaded C oracle decoder (f32 left-fold, -O2 "
+                     f"-ffp-contract=off), {el:.2f} s each, on {cpu_model()} ({os.cpu_count()} logical cores on "
+                     f"host); attention at position 0 reads 1 key (< 1% of a token's bytes at the benchmarked "
+                     f"lengths)"}
     return parity, cpu
 
 
@@ -579,33 +621,56 @@ def bench_q8_0(args, doe):
 
 
 def bench_hbm_copy(args, doe):
-    """STREAM-style check of the HBM figure the rooflines use: 2 GiB copied
-    device to device (the runtime's copy kernel) ten times between HIP
-    events; read and written bytes both counted."""
-    from doe_amd import DeviceBuffer, Event, Stream
+    """STREAM-style checks of the HBM figure the rooflines use, on 2 GiB
+    buffers: a device-to-device copy by the runtime's copy kernel (read and
+    written bytes both counted), and this library's own read stream
+    (doe_read_xor_u32: every 16-byte word loaded once, XOR-folded to one
+    checksum), ten of each between HIP events."""
+    import ctypes as C
+
+    from doe_amd import DeviceBuffer, Event, Stream, _lib
 
     nbytes = 1 << 31
     src, dst = DeviceBuffer(nbytes), DeviceBuffer(nbytes)
     s = Stream()
+    sp = C.c_void_p(s.handle)
+    _lib.call("doe_fill_uniform_i32", C.c_void_p(src.ptr), nbytes // 4, 77, -2 ** 31, 2 ** 31 - 1, sp)
     dst.copy_from(src, s)
     s.synchronize()
-    e0, e1 = Event(), Event()
-    e0.record(s)
     reps = 10
-    for _ in range(reps):
-        dst.copy_from(src, s)
-    e1.record(s)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / reps
+
+    def timed(fn):
+        e0, e1 = Event(), Event()
+        e0.record(s)
+        for _ in range(reps):
+            fn()
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / reps
+
+    ms = timed(lambda: dst.copy_from(src, s))
     gbs = 2 * nbytes / (ms * 1e-3) / 1e9
+    ck = DeviceBuffer.empty((2,), np.uint32)
+    read = lambda: _lib.call("doe_read_xor_u32", C.c_void_p(src.ptr), nbytes, C.c_void_p(ck.ptr), 0, sp)
+    read()
+    s.synchronize()
+    first = int(ck.download()[0])
+    ms_r = timed(read)
+    same = int(ck.download()[0]) == first
+    gbs_r = nbytes / (ms_r * 1e-3) / 1e9
     s.destroy()
-    src.free()
-    dst.free()
+    for b in (src, dst, ck):
+        b.free()
     log(f"hbm copy: 2 GiB device-to-device in {ms * 1e3:.1f} us = {gbs:.0f} GB/s read + write "
-        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of the {HBM_PEAK_GBS:.0f} GB/s figure)")
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of the {HBM_PEAK_GBS:.0f} GB/s figure); read stream {ms_r * 1e3:.1f} us "
+        f"= {gbs_r:.0f} GB/s ({100 * gbs_r / HBM_PEAK_GBS:.1f}%), checksum stable: {same}")
     return {"kind": "STREAM copy: hipMemcpyAsync device to device, read + write bytes counted",
             "bytes_per_copy": nbytes, "us_per_copy": round(ms * 1e3, 1), "achieved_gbs": round(gbs, 1),
-            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "read_stream": {"kind": "doe_read_xor_u32: 2 GiB read once with 16-byte non-temporal loads "
+                                    "(512 x 256 threads), XOR-folded",
+                            "bytes": nbytes, "us": round(ms_r * 1e3, 1), "achieved_gbs": round(gbs_r, 1),
+                            "frac_of_hbm_peak": round(gbs_r / HBM_PEAK_GBS, 4), "checksum_stable": same}}
 
 
 def traffic_bytes(summary: str):
@@ -622,24 +687,28 @@ def traffic_bytes(summary: str):
 
 
 def cpu_baseline(w, x, seconds: float):
+    """The single-threaded C oracle on the full config-0 GEMV, called back to
+    back for about `seconds` (at least 5 calls); the value is the algorithmic
+    bytes over the median call time."""
     from oracle import oracle as ora
 
     ora.lib()
-    iters = 0
-    t0 = time.perf_counter()
-    while True:
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or time.perf_counter() - t_start < seconds:
+        t0 = time.perf_counter()
         ora.q4k_gemv(w, x, N, K)
-        iters += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
     return {
-        "value": GEMV_BYTES * iters / el / 1e9,
+        "value": GEMV_BYTES / med / 1e9,
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{iters} full N={N} K={K} Q4_K GEMVs (single-threaded C oracle, f32 left-fold, "
-                  f"-O2 -ffp-contract=off) in {el:.1f} s on {cpu_model()} "
+        "runs": len(times),
+        "median_s": med,
+        "sample": f"median of {len(times)} full N={N} K={K} Q4_K GEMVs ({med * 1e3:.2f} ms each; single-threaded "
+                  f"C oracle, f32 left-fold, -O2 -ffp-contract=off) on {cpu_model()} "
                   f"({os.cpu_count()} logical cores on host)",
     }
 
@@ -647,9 +716,10 @@ def cpu_baseline(w, x, seconds: float):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1280)
-    ap.add_argument("--warmup", type=int, default=128)
-    ap.add_argument("--copies", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=20, help="GEMV launches per timed window")
+    ap.add_argument("--warmup", type=int, default=5, help="untimed GEMV launches after the first full rotation")
+    ap.add_argument("--copies", type=int, default=64, help="rotating weight copies (at least 48 are used)")
+    ap.add_argument("--windows", type=int, default=12, help="timed windows; the headline is their median")
     ap.add_argument("--attn-copies", type=int, default=48)
     ap.add_argument("--attn-steps", type=int, default=480)
     ap.add_argument("--prompt-len", type=int, default=128)
@@ -658,7 +728,6 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="run prompts as teacher-forced decode steps")
     ap.add_argument("--gemm-steps", type=int, default=20)
-    ap.add_argument("--large-steps", type=int, default=45)
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -716,7 +785,11 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": f"q4k_gemv M=1 N={N} K={K} (Q4_K_M weights, f32 activation/output), "
-                        f"{g['copies']} rotating weight copies, HIP-graph replay",
+                        f"{g['copies']} rotating weight copies ({g['reuse_distance_bytes'] / 2 ** 20:.0f} MiB read "
+                        f"between two reads of a copy), median of {g['windows']} windows of {g['steps']} "
+                        f"back-to-back launches in one HIP graph, device timestamps between windows",
+            "weight_copies": g["copies"],
+            "windows": g["windows"],
             "bytes_per_step": GEMV_BYTES,
             "pct_of_hbm_peak": round(100.0 * g["value_gbs"] / HBM_PEAK_GBS, 2),
             "rel_l2_vs_oracle": g["rel_l2"],
@@ -730,9 +803,10 @@ def main() -> int:
             "traffic": traffic_bytes("q4k_gemv_n9216_k2304.md"),
             "kernel": g["kernel"],
             "kernel_us": round(g["ms_per_step"] * 1e3, 3),
-            "median_kernel_us": round(g["median_ms_per_launch"] * 1e3, 3),
-            "launches": g["steps"],
-            "graph_replays": g["replays"],
+            "mean_kernel_us": round(g["mean_ms_per_step"] * 1e3, 3),
+            "event_kernel_us": round(g["event_ms_per_step"] * 1e3, 3),
+            "launches_per_window": g["steps"],
+            "windows": g["windows"],
         },
         "cpu_baseline": cpu,
         "gemv_n65536": gl,

@@ -31,8 +31,11 @@
 // per wave, so an image fragment feeds four MFMAs) and 32 groups of K, eight
 // per wave with every load of a wave issued up front; the four waves' sums
 // meet in LDS.  When K spans more than one workgroup's 32 groups, the grid
-// splits K: each range writes its partial sums to a workspace and a second
-// kernel adds the ranges in order, so y is the same bit for bit on every run.
+// splits K and each range writes its partial sums to a workspace: in the
+// one-shot kernel the last range of a row block to finish adds the ranges in
+// order (a completion count per row block, cleared at the start of every
+// call), in the streaming form a second kernel does; either way y is the
+// same bit for bit on every run.
 #include "common.h"
 
 #include <math.h>
@@ -291,6 +294,15 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a, int ranges) 
     // complete the row block's count goes up, and the workgroup that completes
     // it adds the ranges' slots in range order (agent-scope loads) into y and
     // resets the count.  No workgroup waits for another.
+    // Ordering: the slot stores are acknowledged (vmcnt(0)) before the count
+    // is incremented, and the adding workgroup's loads are issued only after
+    // its increment has returned the final count; agent-scope stores write
+    // through and agent-scope loads miss the per-XCD caches, so those loads
+    // read what the stores wrote.  (A release / acquire pair would say the
+    // same to the compiler, but on gfx950 its agent-scope release writes back
+    // the whole L2 of the XCD, measured at ~75 ns per workgroup, serialised.)
+    // The host clears the counts before every call, so a count left behind by
+    // calls that overlapped on the shared workspace does not outlive them.
     float *slot = a.out + ((size_t)rb * ranges + sp) * 512;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -546,14 +558,18 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
                 g_cnt = nullptr;
                 g_cnt_bytes = 0;
                 DOE_HIP_CHECK(hipMalloc(&g_cnt, need_cnt));
-                // every call leaves the counts at zero again
-                DOE_HIP_CHECK(hipMemset(g_cnt, 0, need_cnt));
-                DOE_HIP_CHECK(hipDeviceSynchronize());
                 g_cnt_bytes = need_cnt;
             }
         }
         part = (float *)g_ws;
         cnt = (unsigned *)g_cnt;
+        if (one_shot) {
+            // counts start at zero on every call (a fill kernel, so the call
+            // stays capturable): a count left behind by calls that overlapped
+            // on the shared workspace is cleared here
+            const int frc = doe::fill_bytes_async(cnt, 0, need_cnt, st);
+            if (frc) return frc;
+        }
     }
     Int4Args a;
     a.q = w_u4;

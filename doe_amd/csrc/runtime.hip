@@ -76,6 +76,13 @@ int fill_bytes_async(void *dst, int value, size_t bytes, hipStream_t st) {
 
 }  // namespace doe
 
+namespace {
+// The device's constant-rate wall clock (s_memrealtime) stored by one lane.
+__global__ void timestamp_kernel(unsigned long long *dst) {
+    if (threadIdx.x == 0) dst[0] = wall_clock64();
+}
+}  // namespace
+
 extern "C" {
 
 int doe_init(int device) {
@@ -251,6 +258,26 @@ int doe_event_elapsed_ms(float *ms, doe_event_t start, doe_event_t end) {
     if (rc) return rc;
     DOE_REQUIRE(ms && start && end, DOE_E_INVALID, "null argument");
     DOE_HIP_CHECK(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+    return DOE_OK;
+}
+
+int doe_device_timestamp(uint64_t *dst, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(dst && ((uintptr_t)dst & 7) == 0, DOE_E_INVALID, "timestamp destination must be 8-byte aligned");
+    hipLaunchKernelGGL(timestamp_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, (unsigned long long *)dst);
+    DOE_LAUNCH_CHECK("timestamp_kernel");
+    return DOE_OK;
+}
+
+int doe_device_timestamp_hz(int64_t *hz) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(hz, DOE_E_INVALID, "null argument");
+    int dev = 0, khz = 0;
+    DOE_HIP_CHECK(hipGetDevice(&dev));
+    DOE_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+    *hz = (int64_t)khz * 1000;
     return DOE_OK;
 }
 

@@ -75,6 +75,13 @@ int doe_event_destroy(doe_event_t event);
 int doe_event_record(doe_event_t event, doe_stream_t stream);
 int doe_event_synchronize(doe_event_t event);
 int doe_event_elapsed_ms(float *ms, doe_event_t start, doe_event_t end);
+/* Stores the device's constant-rate wall clock (ticks of
+ * doe_device_timestamp_hz) to *dst when the stream reaches it: a kernel, so
+ * it can sit between the kernels of a captured graph, where event records
+ * cannot be timed (doe_event_elapsed_ms rejects events recorded inside a
+ * graph).  Measurement utility; no reference counterpart. */
+int doe_device_timestamp(uint64_t *dst, doe_stream_t stream);
+int doe_device_timestamp_hz(int64_t *hz);
 int doe_graph_capture_begin(doe_stream_t stream);
 int doe_graph_capture_end(doe_stream_t stream, doe_graph_t *graph);
 int doe_graph_launch(doe_graph_t graph, doe_stream_t stream);
@@ -523,6 +530,13 @@ int doe_fill_random_q4k(void *weight_q4k, int64_t nblocks, uint64_t seed, float 
 /* Q8_0 blocks: f16 scale |N(0, d_sigma)|, 32 uniform int8 quants. */
 int doe_fill_random_q8_0(void *weight_q8_0, int64_t nblocks, uint64_t seed, float d_sigma,
                          doe_stream_t stream);
+/* *checksum = XOR of the nbytes / 4 little-endian 32-bit words of buf
+ * (nbytes a multiple of 16, buf 16-byte aligned), read once as a plain
+ * stream by `workgroups` workgroups of 256 threads (0: automatic).  Used to
+ * measure the read bandwidth the HBM-bound kernels are held against; no
+ * reference counterpart. */
+int doe_read_xor_u32(const void *buf, int64_t nbytes, uint32_t *checksum, int32_t workgroups,
+                     doe_stream_t stream);
 /* After a decode step, on the device: state = {pos, kv_len, prompt_len,
  * token}; pos += 1, kv_len = pos + 1, and the next token is ids[pos] inside
  * the prompt or the sampled *token (also stored to ids[pos]) after it.  With

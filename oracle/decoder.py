@@ -9,8 +9,21 @@ import math
 
 import numpy as np
 
-from doe_amd.ops import deinterleave_rope_rows
 from . import oracle as ora
+
+
+def plain_rows_from_rotation_pairs(rows: np.ndarray, head_dim: int) -> np.ndarray:
+    """The device holds each head's q/k projection rows as rotation pairs:
+    row 2i of a head is dimension i, row 2i + 1 is dimension i + head_dim/2.
+    Returns the rows in plain dimension order (the order rope.wgsl rotates):
+    plain row i of a head is device row 2i, plain row i + head_dim/2 is
+    device row 2i + 1."""
+    n = rows.shape[0]
+    half = head_dim // 2
+    head0 = np.arange(0, n, head_dim)[:, None]
+    i = np.arange(half)[None, :]
+    src = np.concatenate([head0 + 2 * i, head0 + 2 * i + 1], axis=1).reshape(-1)
+    return np.ascontiguousarray(np.asarray(rows)[src])
 
 
 class OracleDecoder:
@@ -25,7 +38,7 @@ class OracleDecoder:
             # oracle follows the rotate-half form of rope.wgsl on plain rows
             wqkv = L.wqkv.download().reshape(L.qkv_rows, -1)
             qk = L.q_dim + L.kv_dim
-            wqkv[:qk] = deinterleave_rope_rows(wqkv[:qk], hd)
+            wqkv[:qk] = plain_rows_from_rotation_pairs(wqkv[:qk], hd)
             key = id(dec.freq_by_layer[li])
             if key not in tables:
                 tables[key] = dec.freq_by_layer[li].download()

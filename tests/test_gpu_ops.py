@@ -492,3 +492,46 @@ def test_fills_replay_in_graphs(dev):
         assert np.array_equal(got, want), i
     g.destroy()
     s.destroy()
+
+
+@pytest.mark.parametrize("nbytes,wgs", [(16, 0), (4096 * 16 + 48, 0), (3 << 20, 7), (1 << 24, 0)])
+def test_read_xor_checksum(dev, nbytes, wgs):
+    """doe_read_xor_u32 (the read-stream probe beside the HBM copy figure):
+    the XOR of every 32-bit word, for word counts that leave remainders in
+    its four-deep loop and with a forced small grid."""
+    import ctypes as C
+
+    from doe_amd import _lib
+
+    rng = np.random.default_rng(nbytes)
+    a = rng.integers(0, 2 ** 32, nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    buf = up(a)
+    ck = DeviceBuffer.empty((1,), np.uint32)
+    _lib.call("doe_read_xor_u32", C.c_void_p(buf.ptr), nbytes, C.c_void_p(ck.ptr), wgs, C.c_void_p(None))
+    dev.synchronize()
+    assert int(ck.download()[0]) == int(np.bitwise_xor.reduce(a))
+
+
+def test_device_timestamp_orders_stream_work(dev):
+    """doe_device_timestamp: the device clock stored when the stream reaches
+    it, so stamps around work on one stream increase, at the rate
+    doe_device_timestamp_hz reports (a 1 GiB read takes well over 10 us)."""
+    import ctypes as C
+
+    from doe_amd import Stream, _lib
+
+    hz = C.c_int64()
+    _lib.call("doe_device_timestamp_hz", C.byref(hz))
+    assert hz.value > 0
+    s = Stream()
+    ts = DeviceBuffer.empty((2,), np.uint64)
+    big = DeviceBuffer(1 << 30)
+    ck = DeviceBuffer.empty((1,), np.uint32)
+    _lib.call("doe_device_timestamp", C.c_void_p(ts.ptr), C.c_void_p(s.handle))
+    _lib.call("doe_read_xor_u32", C.c_void_p(big.ptr), big.nbytes, C.c_void_p(ck.ptr), 0, C.c_void_p(s.handle))
+    _lib.call("doe_device_timestamp", C.c_void_p(ts.ptr + 8), C.c_void_p(s.handle))
+    s.synchronize()
+    t = ts.download().astype(np.int64)
+    s.destroy()
+    big.free()
+    assert (t[1] - t[0]) / hz.value > 10e-6

@@ -103,3 +103,18 @@ def test_f16_attention_rounds_probabilities():
     np.testing.assert_allclose(out[0], (v[0] + v[1]) / 2, rtol=1e-7, atol=0)
     unrounded = (v[0] + 2.0 ** -delta * v[1]) / (1 + 2.0 ** -delta)
     assert np.abs(unrounded - (v[0] + v[1]) / 2).max() > 1e-4
+
+
+def test_rotation_pair_rows_back_to_plain_order():
+    # two heads of head_dim 4: the device holds each head's rows as rotation
+    # pairs (dim 0, dim 2, dim 1, dim 3); the oracle reads them in plain order
+    from oracle.decoder import plain_rows_from_rotation_pairs
+
+    dev_rows = np.array([[10], [12], [11], [13], [20], [22], [21], [23]])
+    got = plain_rows_from_rotation_pairs(dev_rows, 4)
+    assert got[:, 0].tolist() == [10, 11, 12, 13, 20, 21, 22, 23]
+    # and it undoes the product's own pairing of head_dim 256 rows
+    from doe_amd.ops import interleave_rope_rows
+
+    rows = np.arange(2 * 256 * 3).reshape(2 * 256, 3)
+    assert np.array_equal(plain_rows_from_rotation_pairs(interleave_rope_rows(rows, 256), 256), rows)
