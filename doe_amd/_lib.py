@@ -115,6 +115,7 @@ SIGNATURES: dict[str, list] = {
     "doe_fill_random_q4k": [_vp, _i64, C.c_uint64, _f32, _f32, _vp],
     "doe_decode_advance": [_vp, _vp, _vp, _i64, _vp, _i32, _vp],
     "doe_read_xor_u32": [_vp, _i64, _vp, _i32, _vp],
+    "doe_q4k_gemv_ex": [_vp, _vp],
     "doe_device_timestamp": [_vp, _vp],
     "doe_device_timestamp_hz": [C.POINTER(_i64)],
     "doe_tune_set": [C.c_char_p, _i32],

@@ -185,7 +185,18 @@ struct GemvFusion {
     const int32_t *pos_dev;
     _Float16 *k_cache, *v_cache;
     int q_rows, kv_rows, head_dim, max_seq;
+    // Activation given as x + x_parts[0] + ... + x_parts[x_nparts - 1]
+    // (each part k floats, added in that order); workgroup (0, 0) stores the
+    // sum to x_sum when non-NULL.  Matrix-core kernel only.
+    const float *x_parts;
+    int x_nparts;
+    float *x_sum;
+    // K split into parts: K range s stores its row sums to y_parts[s n + row]
+    // with plain stores (no residual, no atomics); the consumer adds them.
+    float *y_parts;
 };
+
+constexpr int kMaxXParts = 4;  // activation parts a GEMV adds in its prologue
 
 // Epilogue of one (even row, odd row) pair of a fused q/k/v projection.
 __device__ __forceinline__ void rope_kv_pair(const GemvFusion &fz, int row, float s0, float s1,
@@ -513,6 +524,9 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
     float v[BPW][4], nwv[NORM ? BPW : 1][4];
     float4 ao[ATTN ? kAttnMaxSplits : 1];
     float2 aml[ATTN ? kAttnMaxSplits : 1];
+    // activation parts (fz.x_parts): up to two blocks per wave
+    constexpr int XPB = (!ATTN && BPW <= 2) ? BPW : 0;
+    float4 xp[XPB > 0 ? XPB : 1][kMaxXParts];
 #pragma unroll
     for (int u = 0; u < BPW; ++u) {
         const int e = (b0 + u) * 256 + lane * 4;  // this lane's four activations of block b0 + u
@@ -534,6 +548,25 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
 #pragma unroll
             for (int j = 0; j < 4; ++j) v[u][j] = x[min(e + j, k - 1)];  // masked below
         }
+        if (XPB > 0 && fz.x_nparts > 0) {
+            // the activation's parts: loads issued with the activation's,
+            // added once the weight loads are out (below)
+#pragma unroll
+            for (int sp = 0; sp < kMaxXParts; ++sp) {
+                if (sp < fz.x_nparts) {
+                    const float *pp = fz.x_parts + (size_t)sp * k;
+                    float4 &t = xp[XPB > 0 ? u : 0][sp];
+                    if (XV) {
+                        t = *reinterpret_cast<const float4 *>(pp + min(e, k - 4));
+                    } else {
+                        t.x = pp[min(e, k - 1)];
+                        t.y = pp[min(e + 1, k - 1)];
+                        t.z = pp[min(e + 2, k - 1)];
+                        t.w = pp[min(e + 3, k - 1)];
+                    }
+                }
+            }
+        }
         if (NORM && XV) {  // (XV also covers the norm weight's alignment)
             const float4 f = *reinterpret_cast<const float4 *>(fz.norm_w + min(e, k - 4));
             nwv[NORM ? u : 0][0] = f.x; nwv[NORM ? u : 0][1] = f.y;
@@ -543,6 +576,12 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
             for (int j = 0; j < 4; ++j) nwv[NORM ? u : 0][j] = fz.norm_w[min(e + j, k - 1)];
         }
     }
+    // The residual of the epilogue's rows, loaded with the activation so the
+    // last store does not wait on a load (K split: range 0 adds it when the
+    // ranges go to parts; atomic ranges add into a y that holds it already).
+    const bool has_res = fz.residual && blockIdx.y == 0 && (fz.y_parts || gridDim.y == 1);
+    float rpre = 0.0f;
+    if (has_res && tid < 16) rpre = fz.residual[min(row0 + tid, n - 1)];
     // (x is not __restrict__: with it its loads count as invariant and were
     // sunk past the weight loads; this memory clobber keeps the order)
     __asm__ volatile("" ::: "memory");
@@ -560,6 +599,29 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+
+    if (XPB > 0 && fz.x_nparts > 0) {
+        // x + part 0 + part 1 + ..., in that order; workgroup (0, 0) keeps
+        // the sum (the residual stream the later steps read)
+        const bool keep = fz.x_sum && blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+        for (int u = 0; u < XPB; ++u) {
+#pragma unroll
+            for (int sp = 0; sp < kMaxXParts; ++sp) {
+                if (sp < fz.x_nparts) {
+                    const float4 t = xp[u][sp];
+                    v[u][0] += t.x; v[u][1] += t.y; v[u][2] += t.z; v[u][3] += t.w;
+                }
+            }
+            if (keep) {
+                const int e = (b0 + u) * 256 + lane * 4;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (e + j < kb1 * 256 && e + j < k)
+                        __hip_atomic_store(fz.x_sum + e + j, v[u][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
 
     if (ATTN) {
         const int S = fz.attn_splits;
@@ -725,8 +787,17 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
             const float other = dpp<kDppXor1>(s);
             if ((tid & 1) == 0 && row < n) rope_kv_pair(fz, row, s, other, y);
         } else if (row < n) {
-            if (gridDim.y > 1) atomicAdd(y + row, s);  // K split: y holds the residual already
-            else y[row] = fz.residual ? s + fz.residual[row] : s;
+            const float r = has_res ? s + rpre : s;
+            if (fz.y_parts) {
+                // the consumer adds the parts; written through (agent scope),
+                // so no dirty L2 line is left for the kernel's end to write back
+                __hip_atomic_store(fz.y_parts + (size_t)blockIdx.y * n + row, r, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            } else if (gridDim.y > 1) {
+                atomicAdd(y + row, s);  // K split: y holds the residual already
+            } else {
+                y[row] = r;
+            }
         }
     }
 }
@@ -1035,10 +1106,20 @@ int doe_q4k_dequant(const void *weight_q4k, float *out, int64_t n, int64_t k,
 
 namespace {
 
+// max_y_parts / y_nparts: with fz.y_parts, the most K ranges the caller's
+// parts buffer holds and where the number used is returned.
 int gemv_launch(const void *weight_q4k, const float *activation, float *output, int64_t n,
-                int64_t k, const GemvFusion &fz, hipStream_t st) {
+                int64_t k, const GemvFusion &fz, hipStream_t st, int max_y_parts = 0,
+                int32_t *y_nparts = nullptr) {
     int rc = doe::require_init();
     if (rc) return rc;
+    const bool xparts = fz.x_nparts > 0;
+    DOE_REQUIRE(fz.x_nparts >= 0 && fz.x_nparts <= kMaxXParts && (!xparts || fz.x_parts), DOE_E_INVALID,
+                "activation parts: 0..%d with a parts pointer (got %d)", kMaxXParts, fz.x_nparts);
+    DOE_REQUIRE(!xparts || !fz.attn_o, DOE_E_UNSUPPORTED, "activation parts exclude the attention prologue");
+    DOE_REQUIRE(!fz.y_parts || (!fz.gated && !fz.rope_kv && !fz.norm_w && y_nparts && max_y_parts >= 1),
+                DOE_E_UNSUPPORTED, "output parts: plain, residual or attention-prologue GEMVs, a count pointer "
+                                   "and room for at least one part");
     DOE_REQUIRE(n >= 0 && k >= 0, DOE_E_INVALID, "negative shape n=%lld k=%lld", (long long)n,
                 (long long)k);
     DOE_REQUIRE(!fz.gated || (n % 2) == 0, DOE_E_INVALID, "gated GEMV needs an even row count");
@@ -1050,6 +1131,10 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     if (k == 0) {
         // Empty reduction: the sum identity (reference_interpreter.zig:323-327).
         DOE_REQUIRE(!fz.residual && !fz.gated, DOE_E_UNSUPPORTED, "fused epilogues need k > 0");
+        if (fz.y_parts) {
+            *y_nparts = 1;
+            return doe::fill_bytes_async(fz.y_parts, 0, (size_t)n * sizeof(float), st);
+        }
         return doe::fill_bytes_async(output, 0, (size_t)n * sizeof(float), st);
     }
     DOE_REQUIRE(weight_q4k && (activation || fz.attn_o), DOE_E_INVALID, "null pointer");
@@ -1086,19 +1171,48 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         DOE_REQUIRE(!fz.norm_w && !fz.gated && !fz.rope_kv && !fz.attn_o, DOE_E_UNSUPPORTED,
                     "k=%lld (%d Q4_K blocks > %d): only the plain and residual forms", (long long)k, nb,
                     kMfmaMaxBlocks);
-        if (fz.residual && fz.residual != output) {
+        if (fz.y_parts) {
+            // K ranges of at most 64 blocks, each written to its own part
+            ksplit = (nb + kMfmaMaxBlocks - 1) / kMfmaMaxBlocks;
+            DOE_REQUIRE(ksplit <= max_y_parts && ksplit <= kMaxXParts, DOE_E_UNSUPPORTED,
+                        "k=%lld needs %d output parts (room for %d, at most %d)", (long long)k, ksplit,
+                        max_y_parts, kMaxXParts);
+            const int64_t fill = (g_num_cus + row_groups - 1) / row_groups;  // more ranges while CUs idle
+            int want = (int)(fill < nb ? fill : nb);
+            if (want < (nb + 15) / 16) want = (nb + 15) / 16;
+            if (want > max_y_parts) want = max_y_parts;
+            if (want > kMaxXParts) want = kMaxXParts;
+            if (want > ksplit && g_tune_ksplit != 1) ksplit = want;
+        } else if (fz.residual && fz.residual != output) {
             DOE_HIP_CHECK(hipMemcpyAsync(output, fz.residual, (size_t)n * sizeof(float), hipMemcpyDeviceToDevice, st));
         } else if (!fz.residual) {
             rc = doe::fill_bytes_async(output, 0, (size_t)n * sizeof(float), st);
             if (rc) return rc;
         }
-        ksplit = (nb + 15) / 16;
+        if (!fz.y_parts) ksplit = (nb + 15) / 16;
+    } else if (fz.y_parts) {
+        // K ranges while the rows alone leave CUs idle, one block per wave
+        // where the parts allow; each range writes its own part.  The
+        // attention prologue is single-block: at least one range per 16 blocks.
+        const int cap = max_y_parts < kMaxXParts ? max_y_parts : kMaxXParts;
+        const int need = fz.attn_o ? (nb + 15) / 16 : 1;
+        ksplit = need;
+        if (row_groups < g_num_cus && g_tune_ksplit != 1 && nb > 1) {
+            const int64_t fill = (g_num_cus + row_groups - 1) / row_groups;
+            int want = (int)(fill < nb ? fill : nb);
+            if (want < (nb + 15) / 16) want = (nb + 15) / 16;
+            if (want > cap) want = cap;
+            if (want > ksplit) ksplit = want;
+        }
+        DOE_REQUIRE(ksplit <= cap, DOE_E_UNSUPPORTED, "k=%lld needs %d output parts (room for %d, at most %d)",
+                    (long long)k, ksplit, max_y_parts, kMaxXParts);
     } else if (nb > 1 && fz.residual == output && !fz.norm_w && !fz.gated && !fz.rope_kv &&
                row_groups < g_num_cus && g_tune_ksplit != 1) {
         const int64_t fill = (g_num_cus + row_groups - 1) / row_groups;
         ksplit = (int)(fill < nb ? fill : nb);
         if (ksplit < (nb + 15) / 16) ksplit = (nb + 15) / 16;
     }
+    if (fz.y_parts) *y_nparts = ksplit;
     const int nbs = (nb + ksplit - 1) / ksplit;  // blocks per split
     int bpw = nbs <= 16 ? 1 : (nbs <= 32 ? 2 : (nbs <= 48 ? 3 : 4));
     if (g_tune_bpw > bpw && g_tune_bpw <= 4 && !fz.attn_o) bpw = g_tune_bpw;
@@ -1108,7 +1222,12 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     // Streaming kernel: one wave per block, whole rows, no attention
     // prologue; automatic from kStreamMinGroupsPerCu row groups per CU
     // (q4k_gemv.stream: -1 never, g > 0 forces g row groups per workgroup).
-    const bool stream_ok = use_mfma && bpw == 1 && ksplit == 1 && !fz.attn_o;
+    DOE_REQUIRE(!(xparts || fz.y_parts) || use_mfma, DOE_E_UNSUPPORTED,
+                "activation / output parts need the matrix-core kernel");
+    DOE_REQUIRE(!xparts || bpw <= 2, DOE_E_UNSUPPORTED,
+                "activation parts need k <= 8192 (two Q4_K blocks per wave; got k=%lld)", (long long)k);
+    DOE_REQUIRE(!fz.x_sum || ksplit == 1, DOE_E_UNSUPPORTED, "the activation sum needs whole rows");
+    const bool stream_ok = use_mfma && bpw == 1 && ksplit == 1 && !fz.attn_o && !xparts && !fz.y_parts;
     if (stream_ok && (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups >= kStreamMinGroupsPerCu * g_num_cus))) {
         const int nwaves = nb;
         // ring depth 2: deeper rings measured slower (65536 x 2304: 21.4 us
@@ -1164,7 +1283,7 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         const size_t lds = gemv_mfma_lds_bytes(nwaves, bpw);
         const dim3 grid((unsigned)row_groups, (unsigned)ksplit);
         const bool xv = activation && ((uintptr_t)activation & 15) == 0 && (k & 3) == 0 &&
-                        ((uintptr_t)fz.norm_w & 15) == 0;
+                        ((uintptr_t)fz.norm_w & 15) == 0 && ((uintptr_t)fz.x_parts & 15) == 0;
 #define DOE_GEMV_MFMA_LAUNCH(P, B, X)                                                             \
     do {                                                                                          \
         /* set once per process; a static's initialisation is thread-safe */                    \
@@ -1306,6 +1425,63 @@ int doe_q4k_gemv_attn_out(const void *weight_q4k, const float *attn_partials, in
     fz.attn_head_dim = (int)head_dim;
     fz.residual = residual;
     return gemv_launch(weight_q4k, nullptr, output, n, num_heads * head_dim, fz, (hipStream_t)stream);
+}
+
+int doe_q4k_gemv_ex(const doe_q4k_gemv_args *a, doe_stream_t stream) {
+    DOE_REQUIRE(a, DOE_E_INVALID, "null arguments");
+    DOE_REQUIRE(a->activation_nparts >= 0 && a->activation_nparts <= kMaxXParts, DOE_E_INVALID,
+                "activation_nparts %lld (0..%d)", (long long)a->activation_nparts, kMaxXParts);
+    DOE_REQUIRE(!a->activation_sum || a->activation_nparts > 0, DOE_E_INVALID,
+                "activation_sum without activation parts");
+    DOE_REQUIRE(!a->output_parts || (a->output_nparts && a->max_output_parts >= 1 && a->max_output_parts < 1024),
+                DOE_E_INVALID, "output_parts needs output_nparts and 1 <= max_output_parts");
+    GemvFusion fz{};
+    fz.norm_w = a->norm_weight;
+    fz.norm_eps = a->norm_eps;
+    fz.norm_offset = a->norm_weight_offset;
+    fz.residual = a->residual;
+    fz.gated = a->gated;
+    fz.x_parts = a->activation_parts;
+    fz.x_nparts = (int)a->activation_nparts;
+    fz.x_sum = a->activation_sum;
+    fz.y_parts = a->output_parts;
+    int64_t n = a->n, k = a->k;
+    if (a->rope_kv) {
+        DOE_REQUIRE(a->num_heads > 0 && a->num_kv_heads >= 0 && a->head_dim > 0 && (a->head_dim % 2) == 0 &&
+                        a->max_seq_len > 0,
+                    DOE_E_INVALID, "bad qkv shape");
+        DOE_REQUIRE(a->freq_cis && a->position_dev && (a->num_kv_heads == 0 || (a->key_cache && a->val_cache)),
+                    DOE_E_INVALID, "null pointer");
+        DOE_REQUIRE(n == (a->num_heads + 2 * a->num_kv_heads) * a->head_dim, DOE_E_INVALID,
+                    "n %lld is not (num_heads + 2 num_kv_heads) x head_dim", (long long)n);
+        fz.rope_kv = 1;
+        fz.freq_cis = a->freq_cis;
+        fz.pos_dev = a->position_dev;
+        fz.k_cache = (_Float16 *)a->key_cache;
+        fz.v_cache = (_Float16 *)a->val_cache;
+        fz.q_rows = (int)(a->num_heads * a->head_dim);
+        fz.kv_rows = (int)(a->num_kv_heads * a->head_dim);
+        fz.head_dim = (int)a->head_dim;
+        fz.max_seq = (int)a->max_seq_len;
+    }
+    if (a->attn_partials) {
+        DOE_REQUIRE(a->attn_splits >= 1 && a->attn_splits <= kAttnMaxSplits, DOE_E_UNSUPPORTED,
+                    "attention combine prologue supports 1..%d splits (got %lld)", kAttnMaxSplits,
+                    (long long)a->attn_splits);
+        DOE_REQUIRE(a->attn_num_heads > 0 && a->attn_head_dim > 0 && a->attn_head_dim % 4 == 0, DOE_E_INVALID,
+                    "bad head shape");
+        DOE_REQUIRE(((uintptr_t)a->attn_partials & 15) == 0, DOE_E_INVALID, "partials must be 16-byte aligned");
+        DOE_REQUIRE(!a->activation && k == a->attn_num_heads * a->attn_head_dim, DOE_E_INVALID,
+                    "with attn_partials the activation is NULL and k = num_heads x head_dim");
+        fz.attn_o = a->attn_partials;
+        fz.attn_ml = a->attn_partials + a->attn_num_heads * a->attn_splits * a->attn_head_dim;
+        fz.attn_splits = (int)a->attn_splits;
+        fz.attn_head_dim = (int)a->attn_head_dim;
+    }
+    float *out = a->output;
+    if (a->output_parts && !out) out = a->output_parts;  // (unused: the parts are the output)
+    return gemv_launch(a->weight_q4k, a->activation, out, n, k, fz, (hipStream_t)stream,
+                       (int)a->max_output_parts, a->output_nparts);
 }
 
 int doe_tune_set(const char *key, int value) {

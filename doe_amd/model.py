@@ -177,10 +177,20 @@ class LayerWeights:
 class Decoder:
     """Device-resident weights, KV cache and activations of one decoder."""
 
-    def __init__(self, cfg: DecoderConfig, keep_logits: bool = False, plan=None):
+    def __init__(self, cfg: DecoderConfig, keep_logits: bool = False, plan=None, ordered_residual: bool = True):
         """plan: an execution.DecodePlan (per-layer attention windows, head
         dims, KV-cache sources, per-layer embeddings); None = global attention
-        in every layer at the model's head_dim, every layer its own cache."""
+        in every layer at the model's head_dim, every layer its own cache.
+        ordered_residual: Q4_K layers add the o_proj / down_proj K ranges into
+        the residual stream in a fixed order (bit-identical steps); False adds
+        them atomically in place (the f32 addition order varies run to run)."""
+        self.ordered_residual = ordered_residual
+        # K ranges of o_proj and down_proj (ordered residual): o_proj in one
+        # range (its consumer, the 1152-workgroup gate/up GEMV, then reads a
+        # single vector), down_proj in up to four (measured at the 2B shape:
+        # 1043 tok/s against 1025 with o_proj in two ranges, 958 with
+        # down_proj in two; the atomic in-place form 1066)
+        self.wo_parts, self.wd_parts = 1, ops.MAX_GEMV_PARTS
         from .execution import UnsupportedStep
 
         self.cfg = cfg
@@ -238,6 +248,17 @@ class Decoder:
             self.ple_yn = DeviceBuffer.empty((c.hidden,), np.float32)
             self.ple_u_views = [self.ple_u.view(li * P * 4, P * 4, np.float32) for li in range(L)]
         self.h = DeviceBuffer.empty((c.ffn,), np.float32)
+        # the residual stream without atomics (Q4_K layers): o_proj and
+        # down_proj write their K ranges' row sums as parts, and the next
+        # GEMV adds the parts in order in its activation load, keeping the
+        # sum in x (entering a layer) or x_mid (after its attention block)
+        self.x_mid = DeviceBuffer.empty((c.hidden,), np.float32)
+        self.parts_o = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, c.hidden), np.float32)
+        self.parts_d = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, c.hidden), np.float32)
+        hb = c.hidden * 4
+        # (part 0, parts 1..) views: part 0 is the next GEMV's activation
+        self._po = (self.parts_o.view(0, hb, np.float32), self.parts_o.view(hb, self.parts_o.nbytes - hb, np.float32))
+        self._pd = (self.parts_d.view(0, hb, np.float32), self.parts_d.view(hb, self.parts_d.nbytes - hb, np.float32))
         self.logits = DeviceBuffer.empty((c.vocab,), np.float32)
         self.token = DeviceBuffer.empty((1,), np.int32)
         self.state = DeviceBuffer.empty((4,), np.int32)  # pos, kv_len, prompt_len, token
@@ -307,28 +328,56 @@ class Decoder:
         ops.embed(self.embed, self.tok_view, self.x, 1, c.vocab, c.hidden, c.embed_scale, stream=stream)
         if self.ple:
             self._ple_inputs(stream)
+        # Q4_K layers: the residual stream entering a layer is act + act_parts
+        # (na parts); o_proj and down_proj write their K ranges as parts, range
+        # 0 with the residual added, and the next GEMV adds them in range
+        # order in its activation load, keeping the sum (x, x_mid) for the
+        # next residual.  So every add happens in a fixed order: a step gives
+        # the same bits on every run.
+        act, act_parts, na = self.x, None, 0
+        last = len(self.layers) - 1
         for li, L in enumerate(self.layers):
             if c.weight_format == "q8_0":
                 self._layer_q8_0(li, L, 1.0 / math.sqrt(c.head_dim), stream)
                 continue
+            if not self.ordered_residual:
+                self._layer_q4k_atomic(li, L, stream)
+                continue
             hd = L.head_dim
             src = self.layers[self.kv_sources[li]]  # the layer whose KV cache this one reads
-            ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads,
-                            num_kv_heads=0 if L.shared_kv else c.kv_heads, head_dim=hd,
-                            freq_cis=self.freq_by_layer[li], position_buffer=self.pos_view, key_cache=L.k_cache,
-                            val_cache=L.v_cache, max_seq_len=c.max_seq, norm_weight=L.norm_attn, norm_eps=c.eps,
-                            norm_weight_offset=c.norm_weight_offset, stream=stream)
+            rope = dict(num_heads=c.heads, num_kv_heads=0 if L.shared_kv else c.kv_heads, head_dim=hd,
+                        freq_cis=self.freq_by_layer[li], position_buffer=self.pos_view, key_cache=L.k_cache,
+                        val_cache=L.v_cache, max_seq_len=c.max_seq)
+            # input_norm + q/k/v_proj + rope + cache write
+            ops.q4k_gemv_ex(L.wqkv, L.qkv_rows, c.hidden, activation=act, activation_parts=act_parts,
+                            activation_nparts=na, activation_sum=self.x if na else None, output=self.qkv,
+                            norm_weight=L.norm_attn, norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset,
+                            rope=rope, stream=stream)
+            resid = self.x if na else act
             splits = ops.attention_partials(self.q_views[li], src.k_cache, src.v_cache, self.attn_parts, batch=1,
                                             num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=hd,
                                             kv_len=0, kv_stride=c.max_seq, scale=1.0 / math.sqrt(hd),
                                             max_splits=self.max_attn_splits, kv_len_buffer=self.kvlen_view,
                                             sliding_window=self.attn_windows[li], softcap=c.attn_softcap,
                                             stream=stream)
-            ops.matmul_q4k_attn_out(L.wo, self.attn_parts, splits, c.heads, hd, self.x, c.hidden,
-                                    residual=self.x, stream=stream)
-            ops.matmul_q4k_fused(L.wgu, self.x, self.h, 2 * c.ffn, c.hidden, norm_weight=L.norm_ffn,
-                                 norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset, gated=True, stream=stream)
-            ops.matmul_q4k_fused(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)
+            # combine + o_proj + attn_residual as K-range parts
+            no = ops.q4k_gemv_ex(L.wo, c.hidden, L.q_dim, attn_partials=self.attn_parts, attn_splits=splits,
+                                 attn_num_heads=c.heads, attn_head_dim=hd, residual=resid,
+                                 output_parts=self.parts_o, max_output_parts=self.wo_parts, stream=stream)
+            # post_attn_norm + gate/up_proj + GeGLU over the summed parts (kept in x_mid)
+            ops.q4k_gemv_ex(L.wgu, 2 * c.ffn, c.hidden, activation=self._po[0], activation_parts=self._po[1],
+                            activation_nparts=no - 1, activation_sum=self.x_mid if no > 1 else None,
+                            output=self.h, norm_weight=L.norm_ffn, norm_eps=c.eps,
+                            norm_weight_offset=c.norm_weight_offset, gated=True, stream=stream)
+            mid = self.x_mid if no > 1 else self._po[0]
+            if li == last or self.ple:
+                # down_proj + ffn_residual into x whole (not in place: no K split)
+                ops.matmul_q4k_fused(L.wd, self.h, self.x, c.hidden, c.ffn, residual=mid, stream=stream)
+                act, act_parts, na = self.x, None, 0
+            else:
+                nd = ops.q4k_gemv_ex(L.wd, c.hidden, c.ffn, activation=self.h, residual=mid,
+                                     output_parts=self.parts_d, max_output_parts=self.wd_parts, stream=stream)
+                act, act_parts, na = self._pd[0], self._pd[1], nd - 1
             if self.ple:
                 self._ple_block(li, L, stream)
         nparts = ops.lm_head_sample(self.lm_head, self.x, c.vocab, c.hidden, self.argmax_parts,
@@ -337,6 +386,31 @@ class Decoder:
         _lib.call("doe_decode_advance", C.c_void_p(self.state.ptr), C.c_void_p(self.token.ptr),
                   C.c_void_p(self.ids.ptr), c.max_seq, C.c_void_p(self.argmax_parts.ptr), nparts,
                   _stream_ptr(stream))
+
+    def _layer_q4k_atomic(self, li: int, L: LayerWeights, stream) -> None:
+        """A Q4_K layer whose o_proj / down_proj add their K ranges into x
+        atomically (in place): the same five dispatches, but the f32 order of
+        the residual adds varies from run to run."""
+        c = self.cfg
+        hd = L.head_dim
+        src = self.layers[self.kv_sources[li]]
+        ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads,
+                        num_kv_heads=0 if L.shared_kv else c.kv_heads, head_dim=hd,
+                        freq_cis=self.freq_by_layer[li], position_buffer=self.pos_view, key_cache=L.k_cache,
+                        val_cache=L.v_cache, max_seq_len=c.max_seq, norm_weight=L.norm_attn, norm_eps=c.eps,
+                        norm_weight_offset=c.norm_weight_offset, stream=stream)
+        splits = ops.attention_partials(self.q_views[li], src.k_cache, src.v_cache, self.attn_parts, batch=1,
+                                        num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=hd,
+                                        kv_len=0, kv_stride=c.max_seq, scale=1.0 / math.sqrt(hd),
+                                        max_splits=self.max_attn_splits, kv_len_buffer=self.kvlen_view,
+                                        sliding_window=self.attn_windows[li], softcap=c.attn_softcap, stream=stream)
+        ops.matmul_q4k_attn_out(L.wo, self.attn_parts, splits, c.heads, hd, self.x, c.hidden, residual=self.x,
+                                stream=stream)
+        ops.matmul_q4k_fused(L.wgu, self.x, self.h, 2 * c.ffn, c.hidden, norm_weight=L.norm_ffn, norm_eps=c.eps,
+                             norm_weight_offset=c.norm_weight_offset, gated=True, stream=stream)
+        ops.matmul_q4k_fused(L.wd, self.h, self.x, c.hidden, c.ffn, residual=self.x, stream=stream)
+        if self.ple:
+            self._ple_block(li, L, stream)
 
     def _ple_inputs(self, stream) -> None:
         """The step graph's ple_gather, ple_project, ple_norm and ple_modulate

@@ -343,6 +343,85 @@ def matmul_q4k_attn_out(weight: DeviceBuffer, partials: DeviceBuffer, splits: in
               _stream_ptr(stream))
 
 
+class Q4kGemvArgs(C.Structure):
+    """``doe_q4k_gemv_args`` (include/doe_mi355x.h), field for field."""
+    _fields_ = [
+        ("weight_q4k", C.c_void_p), ("activation", C.c_void_p), ("activation_parts", C.c_void_p),
+        ("activation_nparts", C.c_int64), ("activation_sum", C.c_void_p), ("output", C.c_void_p),
+        ("n", C.c_int64), ("k", C.c_int64), ("norm_weight", C.c_void_p), ("norm_eps", C.c_float),
+        ("norm_weight_offset", C.c_int32), ("residual", C.c_void_p), ("gated", C.c_int32), ("rope_kv", C.c_int32),
+        ("num_heads", C.c_int64), ("num_kv_heads", C.c_int64), ("head_dim", C.c_int64), ("freq_cis", C.c_void_p),
+        ("position_dev", C.c_void_p), ("key_cache", C.c_void_p), ("val_cache", C.c_void_p),
+        ("max_seq_len", C.c_int64), ("attn_partials", C.c_void_p), ("attn_splits", C.c_int64),
+        ("attn_num_heads", C.c_int64), ("attn_head_dim", C.c_int64), ("output_parts", C.c_void_p),
+        ("max_output_parts", C.c_int64), ("output_nparts", C.c_void_p),
+    ]
+
+
+MAX_GEMV_PARTS = 4  # activation / output parts of doe_q4k_gemv_ex
+
+
+def q4k_gemv_ex(weight: DeviceBuffer, n: int, k: int, *, activation: DeviceBuffer | None = None,
+                activation_parts: DeviceBuffer | None = None, activation_nparts: int = 0,
+                activation_sum: DeviceBuffer | None = None, output: DeviceBuffer | None = None,
+                norm_weight: DeviceBuffer | None = None, norm_eps: float = 1e-6, norm_weight_offset: bool = True,
+                residual: DeviceBuffer | None = None, gated: bool = False, rope: dict | None = None,
+                attn_partials: DeviceBuffer | None = None, attn_splits: int = 0, attn_num_heads: int = 0,
+                attn_head_dim: int = 0, output_parts: DeviceBuffer | None = None, max_output_parts: int = 0,
+                stream=None) -> int:
+    """``doe_q4k_gemv_ex``: the Q4_K decode GEMV with every fused form, plus
+    activation parts (activation + parts[0] + ... in order, the sum kept in
+    ``activation_sum``) and output parts (the K ranges' row sums, one part
+    each, for the next GEMV's activation parts).  ``rope``: the keyword
+    arguments of ``qkv_rope_kv``'s epilogue (num_heads, num_kv_heads,
+    head_dim, freq_cis, position_buffer, key_cache, val_cache, max_seq_len).
+    Returns the number of output parts written (1 without them)."""
+    _q4k_weight_check(weight, n, k)
+    a = Q4kGemvArgs()
+    a.weight_q4k, a.n, a.k = weight.ptr, n, k
+    if attn_partials is not None:
+        _need(attn_partials, attn_num_heads * attn_splits * (attn_head_dim + 2) * 4, "attn_partials")
+        a.attn_partials, a.attn_splits = attn_partials.ptr, attn_splits
+        a.attn_num_heads, a.attn_head_dim = attn_num_heads, attn_head_dim
+    else:
+        _need(activation, k * 4, "activation")
+        a.activation = activation.ptr
+    if activation_nparts:
+        _need(activation_parts, activation_nparts * k * 4, "activation_parts")
+        a.activation_parts, a.activation_nparts = activation_parts.ptr, activation_nparts
+        if activation_sum is not None:
+            _need(activation_sum, k * 4, "activation_sum")
+            a.activation_sum = activation_sum.ptr
+    if norm_weight is not None:
+        _need(norm_weight, k * 4, "norm_weight")
+        a.norm_weight = norm_weight.ptr
+    a.norm_eps, a.norm_weight_offset = norm_eps, int(norm_weight_offset)
+    if residual is not None:
+        _need(residual, n * 4, "residual")
+        a.residual = residual.ptr
+    a.gated = int(gated)
+    if rope is not None:
+        hd, nh, nkv, ms = rope["head_dim"], rope["num_heads"], rope["num_kv_heads"], rope["max_seq_len"]
+        _need(rope["freq_cis"], ms * hd * 4, "freq_cis")
+        _need(rope["position_buffer"], 4, "position_buffer")
+        a.rope_kv, a.num_heads, a.num_kv_heads, a.head_dim, a.max_seq_len = 1, nh, nkv, hd, ms
+        a.freq_cis, a.position_dev = rope["freq_cis"].ptr, rope["position_buffer"].ptr
+        if nkv:
+            _need(rope["key_cache"], nkv * ms * hd * 2, "key_cache")
+            _need(rope["val_cache"], nkv * ms * hd * 2, "val_cache")
+            a.key_cache, a.val_cache = rope["key_cache"].ptr, rope["val_cache"].ptr
+    nparts = C.c_int32(1)
+    if output_parts is not None:
+        _need(output_parts, max_output_parts * n * 4, "output_parts")
+        a.output_parts, a.max_output_parts = output_parts.ptr, max_output_parts
+        a.output_nparts = C.cast(C.pointer(nparts), C.c_void_p)
+    else:
+        _need(output, (n // 2 if gated else n) * 4, "output")
+        a.output = output.ptr
+    _lib.call("doe_q4k_gemv_ex", C.byref(a), _stream_ptr(stream))
+    return int(nparts.value)
+
+
 def _weight_check(weight: DeviceBuffer, n: int, k: int, weight_format: str) -> None:
     if weight_format == "q8_0":
         if weight.nbytes != n * _q8_0.row_bytes(k):

@@ -163,6 +163,56 @@ int doe_q8_0_gemv_qkv_rope_kv(const void *weight_q8_0, const float *activation, 
                               uint16_t *key_cache, uint16_t *val_cache, int64_t max_seq_len,
                               doe_stream_t stream);
 
+/* Every form of the Q4_K decode GEMV in one call, plus two that chain GEMVs
+ * without atomics (no reference counterpart: the reference's decode step
+ * adds the residual in its own `residual` op, which the fused forms here
+ * fold in):
+ *   activation_parts: the activation is activation + parts[0] + ... +
+ *     parts[activation_nparts - 1] (each k floats, 16-byte aligned, added in
+ *     that order; at most 4 parts, k <= 8192); activation_sum, when
+ *     non-NULL, receives that sum (the residual stream a later step reads).
+ *   output_parts: the K reduction is split into ranges and range s stores
+ *     its row sums to output_parts[s * n + row] (max_output_parts x n
+ *     floats; the count used, 1..4, is returned in *output_nparts and
+ *     depends only on n, k and the device), range 0 with the residual (if
+ *     any) added; the GEMV result is their sum in range order, which the
+ *     next GEMV forms by taking part 0 as its activation and the others as
+ *     its activation_parts.  No norm or epilogue; the attention prologue may
+ *     be used.
+ * So a decode layer's residual adds happen in a fixed order: bit-identical
+ * results on every run, where an in-place residual K split adds atomically.
+ * The other fields are those of doe_q4k_gemv_fused (norm_weight, residual,
+ * gated), doe_q4k_gemv_qkv_rope_kv (rope_kv != 0 with the head shape, rotary
+ * table, device position and caches; n = (num_heads + 2 num_kv_heads) x
+ * head_dim) and doe_q4k_gemv_attn_out (attn_partials != NULL with its
+ * splits and head shape; activation NULL, k = num_heads x head_dim). */
+typedef struct doe_q4k_gemv_args {
+    const void *weight_q4k;
+    const float *activation;
+    const float *activation_parts;
+    int64_t activation_nparts;
+    float *activation_sum;
+    float *output;
+    int64_t n, k;
+    const float *norm_weight;
+    float norm_eps;
+    int32_t norm_weight_offset;
+    const float *residual;
+    int32_t gated;
+    int32_t rope_kv;
+    int64_t num_heads, num_kv_heads, head_dim;
+    const float *freq_cis;
+    const int32_t *position_dev;
+    uint16_t *key_cache, *val_cache;
+    int64_t max_seq_len;
+    const float *attn_partials;
+    int64_t attn_splits, attn_num_heads, attn_head_dim;
+    float *output_parts;
+    int64_t max_output_parts;
+    int32_t *output_nparts;
+} doe_q4k_gemv_args;
+int doe_q4k_gemv_ex(const doe_q4k_gemv_args *args, doe_stream_t stream);
+
 /* The attention output projection of one sequence with the split-attention
  * combine folded into its activation load: output[i] = sum_k
  * dequant(W)[i][k] * attn[k] (+ residual[i]), attn = the combine of the

@@ -41,3 +41,25 @@ def test_calls_before_init_report_not_init():
     ptr = C.c_void_p()
     assert lib.doe_malloc(C.byref(ptr), 16) == -2
     assert b"doe_init" in lib.doe_last_error()
+
+
+def test_gemv_args_struct_layout_matches_the_header(tmp_path):
+    """ops.Q4kGemvArgs mirrors doe_q4k_gemv_args: every field at the offset
+    a C compiler gives it (gcc on the header), and the same size."""
+    import shutil
+    import subprocess
+
+    from doe_amd.ops import Q4kGemvArgs
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    names = [f[0] for f in Q4kGemvArgs._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "doe_mi355x.h"\nint main(void) {\n'
+                   + "".join(f'  printf("%zu\\n", offsetof(doe_q4k_gemv_args, {n}));\n' for n in names)
+                   + '  printf("%zu\\n", sizeof(doe_q4k_gemv_args));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    want = [getattr(Q4kGemvArgs, n).offset for n in names] + [C.sizeof(Q4kGemvArgs)]
+    assert got == want

@@ -512,6 +512,29 @@ def test_full_size_graph_trajectory_equals_eager(dev):
     assert out[:128].tolist() == prompt.tolist()
 
 
+def test_full_size_trajectory_bit_reproducible(dev):
+    # the bench's 2B-class trajectory twice (128-token batched prompt, then
+    # 24 greedy steps from 8-step graphs): every token and the last step's
+    # logits are the same bits on both runs (no atomics in the decode step)
+    cfg = DecoderConfig(max_seq=128 + 24 + 1)
+    dec = Decoder(cfg, keep_logits=True)
+    dec.init_random(seed=2)
+    s = Stream()
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab, 128).astype(np.int32)
+    dec.reset(prompt)
+    dec.step(s)
+    s.synchronize()
+    g = dec.capture(s, 8)
+    runs = []
+    for _ in range(2):
+        ids = dec.generate(prompt, 25, s, graph=g, steps_per_graph=8, prefill=True)
+        runs.append((ids.tolist(), dec.logits.download().view(np.uint32).copy(), dec.x.download().view(np.uint32)))
+    g.destroy()
+    assert runs[0][0] == runs[1][0]
+    assert np.array_equal(runs[0][1], runs[1][1])
+    assert np.array_equal(runs[0][2], runs[1][2])
+
+
 def test_prefill_q8_0_full_size(dev, ora):
     # the 2B-class shape with Q8_0 projections: a 6-token prompt through the
     # batched pass against 6 oracle decode steps, then 1 decode step
