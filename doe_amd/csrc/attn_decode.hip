@@ -487,6 +487,61 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     }
 }
 
+// Combine with one wave per column quad and one lane per split (S <= 64):
+// lane s loads split s's (m, l) and its four columns of o, and the max and
+// the sums are full-wave reductions in registers (DPP within rows, then the
+// cross-row lane swaps) -- no LDS, no barrier, one memory round trip.  A
+// workgroup is four waves over 16 columns of one query head.
+constexpr int kWaveCombineMaxSplits = 64;
+
+__device__ __forceinline__ float wave_max64(float v) {
+    v = max16(v);
+    auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+    auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+    v = sum16(v);
+    auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+    auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_wave_kernel(AttnArgs a) {
+    constexpr int NS = D / 16;  // 16-column slices per head
+    const int bh = blockIdx.x / NS, lane = threadIdx.x & 63;
+    const int col = (blockIdx.x % NS) * 16 + (threadIdx.x >> 6) * 4;
+    const int S = a.splits;
+    const bool on = lane < S;
+    const size_t pi = (size_t)bh * S + (on ? lane : 0);
+    float4 o = *reinterpret_cast<const float4 *>(a.ws_o + pi * D + col);
+    float2 ml = *reinterpret_cast<const float2 *>(a.ws_ml + pi * 2);
+    if (!on) {
+        o = make_float4(0.f, 0.f, 0.f, 0.f);
+        ml = make_float2(-INFINITY, 0.0f);
+    }
+    const float M = wave_max64(ml.x);
+    const float f = (M == -INFINITY || ml.x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
+    const float L = wave_sum64(ml.y * f);
+    const float o0 = wave_sum64(o.x * f), o1 = wave_sum64(o.y * f);
+    const float o2 = wave_sum64(o.z * f), o3 = wave_sum64(o.w * f);
+    if (lane == 0) {
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const size_t oi = (size_t)bh * D + col;
+        if (a.out_f16) {
+            _Float16 *out = reinterpret_cast<_Float16 *>(a.out) + oi;
+            out[0] = (_Float16)(o0 * inv); out[1] = (_Float16)(o1 * inv);
+            out[2] = (_Float16)(o2 * inv); out[3] = (_Float16)(o3 * inv);
+        } else {
+            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(a.out) + oi) =
+                make_float4(o0 * inv, o1 * inv, o2 * inv, o3 * inv);
+        }
+    }
+}
+
 // Library-owned workspace (grow-only) for split partials.
 std::mutex g_ws_mu;
 void *g_ws = nullptr;
@@ -496,6 +551,7 @@ size_t g_ws_bytes = 0;
 int g_num_cus = 0;
 int g_tune_splits = 0;
 int g_tune_waves = 0;
+int g_tune_combine = 0;  // 0 automatic, 1 the block-reduction combine kernel
 
 // The wide (short-context) workgroup: 16 waves up to head_dim 128, 8 at 256
 // (the head-256 kernel needs more than the 128 VGPRs a 16-wave workgroup
@@ -528,8 +584,14 @@ template <int D>
 int launch_d(int g, bool w, dim3 grid, hipStream_t st, const AttnArgs &a) {
     int rc = launch_main<D>(g, w, grid, st, a);
     if (rc || a.splits == 1 || a.partials_only) return rc;
-    const unsigned slices = D < kCombineCols ? 1u : (unsigned)(D / kCombineCols);
     const unsigned total_heads = grid.z * (unsigned)a.num_heads;
+    if (a.splits <= kWaveCombineMaxSplits && g_tune_combine != 1) {
+        hipLaunchKernelGGL((attn_combine_wave_kernel<D>), dim3(total_heads * (unsigned)(D / 16)), dim3(256), 0, st,
+                           a);
+        DOE_LAUNCH_CHECK("attn_combine_wave_kernel");
+        return DOE_OK;
+    }
+    const unsigned slices = D < kCombineCols ? 1u : (unsigned)(D / kCombineCols);
     hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(total_heads * slices), dim3(256), 0, st, a);
     DOE_LAUNCH_CHECK("attn_combine_kernel");
     return DOE_OK;
@@ -554,6 +616,11 @@ int attn_set_splits(int v) {
 }
 int attn_set_waves(int v) {
     g_tune_waves = v;
+    return DOE_OK;
+}
+int attn_set_combine(int v) {
+    DOE_REQUIRE(v == 0 || v == 1, DOE_E_INVALID, "attn_decode.combine is 0 (automatic) or 1 (block reduction)");
+    g_tune_combine = v;
     return DOE_OK;
 }
 }  // namespace doe

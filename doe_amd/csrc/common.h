@@ -38,6 +38,7 @@ int attn_scratch_setup(int device);
 int attn_set_splits(int value);
 int mq_set_splits(int value);
 int attn_set_waves(int value);
+int attn_set_combine(int value);
 int int4_set_kernel(int value);
 int int4_set_depth(int value);
 int q8_0_set_tune(const char *key, int value);  // "q8_0_gemv.rows" / ".depth"

@@ -1519,6 +1519,8 @@ int doe_tune_set(const char *key, int value) {
         return doe::attn_set_splits(value);
     } else if (!strcmp(key, "attn_decode.waves")) {
         return doe::attn_set_waves(value);
+    } else if (!strcmp(key, "attn_decode.combine")) {
+        return doe::attn_set_combine(value);
     } else {
         return doe::set_error(DOE_E_INVALID, "unknown tuning key '%s'", key);
     }

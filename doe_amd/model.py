@@ -185,12 +185,18 @@ class Decoder:
         the residual stream in a fixed order (bit-identical steps); False adds
         them atomically in place (the f32 addition order varies run to run)."""
         self.ordered_residual = ordered_residual
-        # K ranges of o_proj and down_proj (ordered residual): o_proj in one
-        # range (its consumer, the 1152-workgroup gate/up GEMV, then reads a
-        # single vector), down_proj in up to four (measured at the 2B shape:
-        # 1043 tok/s against 1025 with o_proj in two ranges, 958 with
-        # down_proj in two; the atomic in-place form 1066)
-        self.wo_parts, self.wd_parts = 1, ops.MAX_GEMV_PARTS
+        # K ranges of o_proj and down_proj (ordered residual).  Every workgroup
+        # of the consuming GEMV reads every part, and those few lines are
+        # shared by all of them: o_proj stays one range when its consumer,
+        # gate/up, has at least four row groups per CU (2B shape: 1043 tok/s
+        # against 1025 with two ranges; the atomic in-place form 1066), else
+        # up to four (Gemma 3 270M: 2400 against 2381 with one; atomic 2465);
+        # down_proj up to four (2B: 958 tok/s with two)
+        from .device import device_info
+
+        cus = device_info().get("cus", 256) or 256
+        self.wo_parts = 1 if (2 * c.ffn + 15) // 16 >= 4 * cus else ops.MAX_GEMV_PARTS
+        self.wd_parts = ops.MAX_GEMV_PARTS
         from .execution import UnsupportedStep
 
         self.cfg = cfg

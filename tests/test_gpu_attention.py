@@ -343,3 +343,32 @@ def test_reference_dispatch_rejects_unsupported(dev):
         ops.attention_dispatch(buf, buf, buf, buf, kv_capacity=8, kv_layout=2, **kw)
     with pytest.raises(DoeError, match="kv_len_buffer"):
         ops.attention_dispatch(buf, buf, buf, buf, kv_capacity=8, kv_len_source=1, **kw)
+
+
+@pytest.mark.parametrize("splits", [2, 7, 33, 64, 100])
+@pytest.mark.parametrize("d,out_f16", [(256, True), (128, False), (64, True), (512, False)])
+def test_split_combine_kernels(dev, ora, splits, d, out_f16):
+    # the one-wave-per-column combine (up to 64 splits, lanes over splits)
+    # and the block-reduction combine (any count; forced, and automatic past
+    # 64) against the oracle and each other, with empty splits at the end
+    # (kv_len not a multiple of the split size)
+    rng = np.random.default_rng(splits + d)
+    hq, hkv, t = 4, 2, 16 * splits * 4 + 16 * 3
+    kv_len = t - 37
+    q = rng.standard_normal((1, hq, d)).astype(np.float16)
+    k = rng.standard_normal((1, hkv, t, d)).astype(np.float16)
+    v = rng.standard_normal((1, hkv, t, d)).astype(np.float16)
+    want = oracle_attn(ora, q, k, v, batch=1, hq=hq, hkv=hkv, d=d, kv_len=kv_len, kv_stride=t, scale=d ** -0.5)
+    outs = []
+    ops.tune("attn_decode.splits", splits)
+    try:
+        for combine in (0, 1):
+            ops.tune("attn_decode.combine", combine)
+            outs.append(run_attn(q, k, v, hq=hq, hkv=hkv, d=d, kv_len=kv_len, kv_stride=t, scale=d ** -0.5,
+                                 q_f16=True, out_f16=out_f16))
+    finally:
+        ops.tune("attn_decode.combine", 0)
+        ops.tune("attn_decode.splits", 0)
+    for got in outs:
+        assert rel_l2(got, want) <= ATTN_REL_L2
+    assert rel_l2(outs[0], outs[1]) <= (1e-3 if out_f16 else 1e-6)
