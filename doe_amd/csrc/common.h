@@ -39,6 +39,7 @@ int attn_set_splits(int value);
 int mq_set_splits(int value);
 int attn_set_waves(int value);
 int attn_set_combine(int value);
+int gemm_set_f16_operands(int value);
 int int4_set_kernel(int value);
 int int4_set_depth(int value);
 int q8_0_set_tune(const char *key, int value);  // "q8_0_gemv.rows" / ".depth"

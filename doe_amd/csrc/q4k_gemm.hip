@@ -137,10 +137,13 @@ __global__ __launch_bounds__(256) void a_rows_to_f16_kernel(const uint16_t *__re
 // four-wave sum, inv = 1 / sqrt(ss / K + eps), y = x * inv * (w or 1 + w)).
 // R > 0: each thread holds its R elements of the row in registers (K <= 256
 // R), so the row is read from memory once; R = 0: the general form re-reads it.
+// a16lo != NULL: also the f16 remainder of each scaled value, x * 2^s -
+// f16(x * 2^s), so hi + lo carries ~22 bits of the f32 activation.
 template <int R, bool NORM>
 __global__ __launch_bounds__(256) void a_rows_f32_kernel(const float *__restrict__ a, const float *__restrict__ w,
                                                          float eps, int weight_offset, _Float16 *__restrict__ a16,
-                                                         int *__restrict__ sig, int K, int Kp) {
+                                                         _Float16 *__restrict__ a16lo, int *__restrict__ sig, int K,
+                                                         int Kp) {
     const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float *row = a + (size_t)m * K;
     _Float16 *out = a16 + (size_t)m * Kp;
@@ -205,30 +208,44 @@ __global__ __launch_bounds__(256) void a_rows_f32_kernel(const float *__restrict
     }
     __syncthreads();
     const float scale = __builtin_amdgcn_ldexpf(1.0f, ssig);
+    _Float16 *outlo = a16lo ? a16lo + (size_t)m * Kp : nullptr;
     if (R > 0) {
 #pragma unroll
         for (int j = 0; j < R; ++j) {
             const int k = t + 256 * j;
-            if (k < K) out[k] = (_Float16)(xv[R > 0 ? j : 0] * scale);
+            if (k < K) {
+                const float v = xv[R > 0 ? j : 0] * scale;
+                const _Float16 h = (_Float16)v;
+                out[k] = h;
+                if (outlo) outlo[k] = (_Float16)(v - (float)h);
+            }
         }
-        for (int k = K + t; k < Kp; k += 256) out[k] = (_Float16)0.0f;  // K padding
+        for (int k = K + t; k < Kp; k += 256) {  // K padding
+            out[k] = (_Float16)0.0f;
+            if (outlo) outlo[k] = (_Float16)0.0f;
+        }
     } else {
-        for (int k = t; k < Kp; k += 256) out[k] = k < K ? (_Float16)(y_at(0, k) * scale) : (_Float16)0.0f;
+        for (int k = t; k < Kp; k += 256) {
+            const float v = k < K ? y_at(0, k) * scale : 0.0f;
+            const _Float16 h = (_Float16)v;
+            out[k] = h;
+            if (outlo) outlo[k] = (_Float16)(v - (float)h);
+        }
     }
 }
 
 // Launch of the f32 pre-pass: the register form up to K = 256 x 48.
-void launch_a_rows_f32(const float *a, const float *w, float eps, int offset, _Float16 *a16, int *sig, int64_t m,
-                       int64_t k, int64_t kp, hipStream_t st) {
+void launch_a_rows_f32(const float *a, const float *w, float eps, int offset, _Float16 *a16, _Float16 *a16lo,
+                       int *sig, int64_t m, int64_t k, int64_t kp, hipStream_t st) {
     const int r = (int)((k + 255) / 256);
 #define DOE_A_ROWS(R)                                                                                          \
     do {                                                                                                       \
         if (w)                                                                                                 \
             hipLaunchKernelGGL((a_rows_f32_kernel<R, true>), dim3((unsigned)m), dim3(256), 0, st, a, w, eps, offset, \
-                               a16, sig, (int)k, (int)kp);                                                     \
+                               a16, a16lo, sig, (int)k, (int)kp);                                              \
         else                                                                                                   \
             hipLaunchKernelGGL((a_rows_f32_kernel<R, false>), dim3((unsigned)m), dim3(256), 0, st, a, w, eps, offset, \
-                               a16, sig, (int)k, (int)kp);                                                     \
+                               a16, a16lo, sig, (int)k, (int)kp);                                              \
     } while (0)
     if (r <= 4) DOE_A_ROWS(4);
     else if (r <= 12) DOE_A_ROWS(12);
@@ -243,6 +260,7 @@ void launch_a_rows_f32(const float *a, const float *w, float eps, int offset, _F
 // ---------------------------------------------------------------------------
 struct GemmArgs {
     const _Float16 *a16;
+    const _Float16 *a16lo;  // the f32-accurate kernel: the f16 remainders of A
     const int *sig;
     const uint8_t *b;
     float *c;
@@ -440,6 +458,198 @@ __global__ __launch_bounds__(256) void quant_gemm_kernel(GemmArgs g) {
     }
 #undef DOE_GEMM_LOAD_CHUNK
 #undef DOE_GEMM_STORE_CHUNK
+
+    // epilogue: D lane l, r: row (r%4) + 8(r/4) + 4(l/32), column l%32
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int mt = wm * 32 * TM + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+            const int m = m0 + mt;
+            if (m >= g.M) continue;
+            const float us = rowscale[mt];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = n0 + wn * 32 * TN + j * 32 + lr;
+                if (n < g.N) cout[(size_t)m * g.N + n] = acc[i][j][r] * us;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// f32-accurate GEMM for f32 activations (the decoder's batched prompt): the
+// 128 x 128 tile of quant_gemm_kernel with both operands carried as f16 hi +
+// lo pairs.  A = a_hi + a_lo from the pre-pass (~22 bits of the scaled f32
+// row); B = b_hi + b_lo from the f32 dequantised weight -- Q4_K: fmaf(d sc,
+// q, -(dmin m)), the canonical decode rounded once to f32; Q8_0: d q, exact
+// in f32 -- (b_hi + b_lo is that f32 weight to ~22 bits).  Each 16-k step
+// runs a_hi b_hi + a_lo b_hi + a_hi b_lo on the matrix cores (every product
+// exact in f32, f32 accumulation; the dropped a_lo b_lo is ~2^-22 of the
+// product), so the result sits at f32-GEMV accuracy instead of the ~2^-12
+// of one f16 rounding per operand.  K runs in 32-element chunks (one Q4_K
+// sub-block or one Q8_0 block per row), four f16 tiles double-buffered in
+// LDS (73.7 KB: two workgroups per CU).
+// ---------------------------------------------------------------------------
+constexpr int kXBK = 32;        // K per chunk
+constexpr int kXLdsRow = 36;    // halves per LDS row: 72 bytes (73.7 KB in all: two workgroups per CU)
+
+template <int FMT>
+__global__ __launch_bounds__(256) void quant_gemm_exact_kernel(GemmArgs g) {
+    constexpr int TM = 2, TN = 2, BM = 128, BN = 128;
+    __shared__ __attribute__((aligned(16))) _Float16 Ah[2][BM * kXLdsRow];
+    __shared__ __attribute__((aligned(16))) _Float16 Al[2][BM * kXLdsRow];
+    __shared__ __attribute__((aligned(16))) _Float16 Bh[2][BN * kXLdsRow];
+    __shared__ __attribute__((aligned(16))) _Float16 Bl[2][BN * kXLdsRow];
+    __shared__ float rowscale[BM];
+
+    // tile order: XCD-contiguous ranges of an M-grouped raster (as quant_gemm_kernel)
+    const int T = g.tiles_m * g.tiles_n;
+    int t = blockIdx.x;
+    if ((T & 7) == 0) t = (blockIdx.x & 7) * (T >> 3) + (blockIdx.x >> 3);
+    const int per_group = kGroupM * g.tiles_n;
+    const int grp = t / per_group;
+    const int first_m = grp * kGroupM;
+    const int gsize = min(kGroupM, g.tiles_m - first_m);
+    const int within = t - grp * per_group;
+    const int tm = first_m + within % gsize;
+    const int tn = within / gsize;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    // A: thread t stages granules t and t + 256 (row gi >> 2, halves (gi & 3) * 8) of hi and lo
+    // B: thread t stages row t >> 1, elements (t & 1) * 16 .. + 15 of the chunk
+    const int brow = tid >> 1, bhalf = tid & 1;
+    const int nrow = min(n0 + brow, g.N - 1);
+    const _Float16 *ah_ptr[2], *al_ptr[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int gi = tid + 256 * i;
+        const size_t off = (size_t)min(m0 + (gi >> 2), g.M - 1) * g.Kp + (gi & 3) * 8;
+        ah_ptr[i] = g.a16 + off;
+        al_ptr[i] = g.a16lo + off;
+    }
+    const uint8_t *brow_ptr = g.b + (size_t)nrow * g.nb * DOE_Q4K_BLOCK_BYTES;
+    const __amdgpu_buffer_rsrc_t b8rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)g.b, (short)0, FMT == 1 ? (int)(((uint32_t)g.N * (uint32_t)g.nb * 34u + 3u) & ~3u) : 0, 0x00020000);
+    const uint32_t b8row = (uint32_t)nrow * (uint32_t)g.nb;
+
+    u32x4 rah[2], ral[2], rh, rq, r8a, r8b;
+    uint32_t r8c = 0, r8sh = 0;
+#define DOE_XGEMM_LOAD(KC)                                                                               \
+    do {                                                                                                 \
+        _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                                  \
+            rah[i] = *reinterpret_cast<const u32x4 *>(ah_ptr[i] + (KC) * kXBK);                          \
+            ral[i] = *reinterpret_cast<const u32x4 *>(al_ptr[i] + (KC) * kXBK);                          \
+        }                                                                                                \
+        if constexpr (FMT == 0) {                                                                        \
+            /* sub-block KC % 8 of block KC / 8: nibble bytes of chunk (KC % 8) / 2, low or high */      \
+            const uint8_t *blk_ = brow_ptr + (size_t)((KC) >> 3) * DOE_Q4K_BLOCK_BYTES;                  \
+            rh = *reinterpret_cast<const u32x4 *>(blk_);                                                 \
+            rq = *reinterpret_cast<const u32x4 *>(blk_ + 16 + 32 * (((KC) & 7) >> 1) + 16 * bhalf);      \
+        } else {                                                                                         \
+            const uint32_t o_ = (KC) < g.nb ? (b8row + (uint32_t)(KC)) * 34u : 0x80000000u;              \
+            const uint32_t al_ = o_ & ~3u;                                                               \
+            r8a = __builtin_amdgcn_raw_buffer_load_b128(b8rsrc, al_, 0, 0);                             \
+            r8b = __builtin_amdgcn_raw_buffer_load_b128(b8rsrc, al_ + 16u, 0, 0);                       \
+            r8c = __builtin_amdgcn_raw_buffer_load_b32(b8rsrc, al_ + 32u, 0, 0);                        \
+            r8sh = o_ & 2u;                                                                              \
+        }                                                                                                \
+    } while (0)
+#define DOE_XGEMM_STORE(BUF, KC)                                                                         \
+    do {                                                                                                 \
+        _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                                  \
+            const int gi = tid + 256 * i;                                                                \
+            const int lo_ = (gi >> 2) * kXLdsRow + (gi & 3) * 8;                                         \
+            *reinterpret_cast<u32x4 *>(&Ah[BUF][lo_]) = rah[i];                                          \
+            *reinterpret_cast<u32x4 *>(&Al[BUF][lo_]) = ral[i];                                          \
+        }                                                                                                \
+        float w_[16];                                                                                    \
+        if constexpr (FMT == 0) {                                                                        \
+            const int sb_ = (KC) & 7, c4_ = sb_ >> 1;                                                    \
+            uint32_t scp_, mnp_;                                                                         \
+            scale_min_pair(rh.y, rh.z, rh.w, c4_, scp_, mnp_);                                           \
+            const int sh8_ = (sb_ & 1) * 8;                                                              \
+            const float dsc_ = doe_half_bits_to_float(rh.x) * (float)((scp_ >> sh8_) & 0xffu);           \
+            const float dmm_ = doe_half_bits_to_float(rh.x >> 16) * (float)((mnp_ >> sh8_) & 0xffu);     \
+            const int nsh_ = (sb_ & 1) * 4;                                                              \
+            _Pragma("unroll") for (int j = 0; j < 16; ++j) {                                             \
+                const uint32_t byte_ = (rq[j >> 2] >> (8 * (j & 3))) & 0xffu;                            \
+                w_[j] = fmaf(dsc_, (float)((byte_ >> nsh_) & 15u), -dmm_);                               \
+            }                                                                                            \
+        } else {                                                                                         \
+            const uint32_t dw_[9] = {r8a.x, r8a.y, r8a.z, r8a.w, r8b.x, r8b.y, r8b.z, r8b.w, r8c};       \
+            const uint32_t sh_ = r8sh << 3; /* the block starts at byte 0 or 2 of the window */         \
+            const uint32_t sel_ = sh_ ? 0x07060504u : 0x05040302u;                                       \
+            const float d8_ = doe_half_bits_to_float(__builtin_amdgcn_ubfe(dw_[0], sh_, 16));            \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                              \
+                const uint32_t u_ = __builtin_amdgcn_perm(dw_[4 * bhalf + j + 1], dw_[4 * bhalf + j], sel_); \
+                _Pragma("unroll") for (int e = 0; e < 4; ++e)                                            \
+                    w_[4 * j + e] = d8_ * (float)(int8_t)((u_ >> (8 * e)) & 0xffu);                      \
+            }                                                                                            \
+        }                                                                                                \
+        uint32_t hv_[8], lv_[8];                                                                         \
+        _Pragma("unroll") for (int j = 0; j < 8; ++j) {                                                  \
+            const _Float16 h0 = (_Float16)w_[2 * j], h1 = (_Float16)w_[2 * j + 1];                       \
+            const _Float16 l0 = (_Float16)(w_[2 * j] - (float)h0), l1 = (_Float16)(w_[2 * j + 1] - (float)h1); \
+            hv_[j] = as_u32(half2v{h0, h1});                                                             \
+            lv_[j] = as_u32(half2v{l0, l1});                                                             \
+        }                                                                                                \
+        const int bo_ = brow * kXLdsRow + 16 * bhalf;                                                    \
+        *reinterpret_cast<u32x4 *>(&Bh[BUF][bo_]) = u32x4{hv_[0], hv_[1], hv_[2], hv_[3]};               \
+        *reinterpret_cast<u32x4 *>(&Bh[BUF][bo_ + 8]) = u32x4{hv_[4], hv_[5], hv_[6], hv_[7]};           \
+        *reinterpret_cast<u32x4 *>(&Bl[BUF][bo_]) = u32x4{lv_[0], lv_[1], lv_[2], lv_[3]};               \
+        *reinterpret_cast<u32x4 *>(&Bl[BUF][bo_ + 8]) = u32x4{lv_[4], lv_[5], lv_[6], lv_[7]};           \
+    } while (0)
+
+    float16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    for (int r = tid; r < BM; r += 256) rowscale[r] = __builtin_amdgcn_ldexpf(1.0f, -g.sig[min(m0 + r, g.M - 1)]);
+    const int kc0 = (int)blockIdx.y * g.kps, kc1 = min(g.nchunk, kc0 + g.kps);
+    float *cout = gridDim.y > 1 ? g.part + (size_t)blockIdx.y * g.M * g.N : g.c;
+    DOE_XGEMM_LOAD(kc0);
+    DOE_XGEMM_STORE(0, kc0);
+    __syncthreads();
+    const int lr = lane & 31, lk = 8 * (lane >> 5);
+    for (int kc = kc0; kc < kc1; ++kc) {
+        const int buf = (kc - kc0) & 1;
+        if (kc + 1 < kc1) DOE_XGEMM_LOAD(kc + 1);
+#pragma unroll
+        for (int ks = 0; ks < kXBK / 16; ++ks) {
+            half8 ah[TM], al[TM], bh[TN], bl[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int o = (wm * 32 * TM + i * 32 + lr) * kXLdsRow + ks * 16 + lk;
+                ah[i] = *reinterpret_cast<const half8 *>(&Ah[buf][o]);
+                al[i] = *reinterpret_cast<const half8 *>(&Al[buf][o]);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int o = (wn * 32 * TN + j * 32 + lr) * kXLdsRow + ks * 16 + lk;
+                bh[j] = *reinterpret_cast<const half8 *>(&Bh[buf][o]);
+                bl[j] = *reinterpret_cast<const half8 *>(&Bl[buf][o]);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+                }
+        }
+        if (kc + 1 < kc1) DOE_XGEMM_STORE(buf ^ 1, kc + 1);
+        __syncthreads();
+    }
+#undef DOE_XGEMM_LOAD
+#undef DOE_XGEMM_STORE
 
     // epilogue: D lane l, r: row (r%4) + 8(r/4) + 4(l/32), column l%32
 #pragma unroll
@@ -794,6 +1004,7 @@ std::mutex g_ws_mu;
 void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
 int g_num_cus = 0;
+int g_gemm_f16_operands = 0;  // 1: f32 activations through the f16-operand kernels (one rounding per operand)
 
 // Steps folded around the prompt GEMM (f32 activations only): RMSNorm of
 // A's rows in the f16 pre-pass, and a residual add or a GeGLU over gate/up
@@ -836,11 +1047,15 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     DOE_REQUIRE(m <= (1 << 24) && n <= (1 << 24) && k <= (1 << 20) && m * n <= ((int64_t)1 << 40),
                 DOE_E_UNSUPPORTED, "q4k_gemm shape too large (m=%lld n=%lld k=%lld)", (long long)m,
                 (long long)n, (long long)k);
-    // 256 x 256 tiles once there are enough of them to fill the CUs, else 128 x 128
-    const bool big = fmt == 0 && m >= 256 && n >= 256 && ((m + 255) / 256) * ((n + 255) / 256) >= 256;
+    // f32 activations run the f32-accurate 128 x 128 kernel (both operands as
+    // f16 hi + lo pairs) unless tuned to the f16-operand form; bf16 ones (8
+    // significant bits, exact in f16) take 256 x 256 tiles once there are
+    // enough of them to fill the CUs, else 128 x 128
+    const bool exact = a_f32 && g_gemm_f16_operands == 0;
+    const bool big = !exact && fmt == 0 && m >= 256 && n >= 256 && ((m + 255) / 256) * ((n + 255) / 256) >= 256;
     // the large-tile kernel streams whole Q4_K blocks: A padded to 256 nb columns
     const int64_t kp = big ? (k + 255) / 256 * 256 : (k + kBK - 1) / kBK * kBK;
-    const size_t a16_bytes = (size_t)m * (size_t)kp * 2;
+    const size_t a16_bytes = (size_t)m * (size_t)kp * 2 * (exact ? 2 : 1);  // (+ the remainders)
     if (g_num_cus == 0) {
         int dev = 0, cus = 0;
         DOE_HIP_CHECK(hipGetDevice(&dev));
@@ -854,13 +1069,15 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     // partial tiles are written and summed once more; a 128-token prompt
     // measured 4.61, 4.50 and 4.43 ms with at most 8, 16 and 32), each at
     // least one Q4_K block of K.
-    const int64_t nchunk = kp / kBK;
+    // (the f32-accurate kernel: 32-element chunks)
+    const int64_t chunk_k = exact ? kXBK : kBK, resident = 2;
+    const int64_t nchunk = kp / chunk_k;
     const int64_t small_tiles = ((m + 127) / 128) * ((n + 127) / 128);
     int64_t splits = 1;
-    if (!big && small_tiles < 2 * g_num_cus) {
-        splits = (2 * g_num_cus) / small_tiles;
+    if (!big && small_tiles < resident * g_num_cus) {
+        splits = (resident * g_num_cus) / small_tiles;
         if (splits > 32) splits = 32;
-        if (splits > nchunk / 4) splits = nchunk / 4;
+        if (splits > nchunk / (256 / chunk_k)) splits = nchunk / (256 / chunk_k);
         if (splits < 1) splits = 1;
     }
     const int64_t kps = (nchunk + splits - 1) / splits;
@@ -881,15 +1098,17 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
         ws = g_ws;
     }
     _Float16 *a16 = (_Float16 *)ws;
+    _Float16 *a16lo = exact ? a16 + (size_t)m * (size_t)kp : nullptr;
     int *sig = (int *)((char *)ws + a16_bytes);
     if (a_f32)
-        launch_a_rows_f32((const float *)a, fu.norm_w, fu.norm_eps, fu.norm_offset, a16, sig, m, k, kp, st);
+        launch_a_rows_f32((const float *)a, fu.norm_w, fu.norm_eps, fu.norm_offset, a16, a16lo, sig, m, k, kp, st);
     else
         hipLaunchKernelGGL(a_rows_to_f16_kernel, dim3((unsigned)m), dim3(256), 0, st, a_bf16, a16, sig, (int)k,
                            (int)kp);
     DOE_LAUNCH_CHECK("a_rows_to_f16_kernel");
     GemmArgs g;
     g.a16 = a16;
+    g.a16lo = a16lo;
     g.sig = sig;
     g.b = (const uint8_t *)b_q4k;
     float *part = use_part ? (float *)((char *)ws + part_off) : nullptr;
@@ -898,7 +1117,7 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     g.N = (int)n;
     g.Kp = (int)kp;
     g.nb = (int)(fmt ? (k + 31) / 32 : (k + 255) / 256);
-    g.nchunk = (int)(kp / kBK);
+    g.nchunk = (int)nchunk;
     g.kps = (int)kps;
     g.part = splits > 1 ? part : nullptr;
     const int bm = big ? 256 : 128, bn = big ? 256 : 128;
@@ -908,6 +1127,10 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
     DOE_REQUIRE(tiles <= 0x7fffffff, DOE_E_UNSUPPORTED, "too many tiles");
     if (big)
         hipLaunchKernelGGL(q4k_gemm_pipe_kernel, dim3((unsigned)tiles), dim3(256), 0, st, g);
+    else if (exact && fmt)
+        hipLaunchKernelGGL(quant_gemm_exact_kernel<1>, dim3((unsigned)tiles, (unsigned)splits), dim3(256), 0, st, g);
+    else if (exact)
+        hipLaunchKernelGGL(quant_gemm_exact_kernel<0>, dim3((unsigned)tiles, (unsigned)splits), dim3(256), 0, st, g);
     else if (fmt)
         hipLaunchKernelGGL((quant_gemm_kernel<2, 2, 1>), dim3((unsigned)tiles, (unsigned)splits), dim3(256), 0, st, g);
     else
@@ -932,6 +1155,18 @@ int gemm_impl(const void *a, bool a_f32, const void *b_q4k, float *c, int64_t m,
 }
 
 }  // namespace
+
+extern "C" {
+
+}  // extern "C"
+
+namespace doe {
+int gemm_set_f16_operands(int v) {
+    DOE_REQUIRE(v == 0 || v == 1, DOE_E_INVALID, "quant_gemm.f16_operands is 0 or 1");
+    g_gemm_f16_operands = v;
+    return DOE_OK;
+}
+}  // namespace doe
 
 extern "C" {
 

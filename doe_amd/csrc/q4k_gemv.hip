@@ -1521,6 +1521,8 @@ int doe_tune_set(const char *key, int value) {
         return doe::attn_set_waves(value);
     } else if (!strcmp(key, "attn_decode.combine")) {
         return doe::attn_set_combine(value);
+    } else if (!strcmp(key, "quant_gemm.f16_operands")) {
+        return doe::gemm_set_f16_operands(value);
     } else {
         return doe::set_error(DOE_E_INVALID, "unknown tuning key '%s'", key);
     }

@@ -195,7 +195,7 @@ class Decoder:
         from .device import device_info
 
         cus = device_info().get("cus", 256) or 256
-        self.wo_parts = 1 if (2 * c.ffn + 15) // 16 >= 4 * cus else ops.MAX_GEMV_PARTS
+        self.wo_parts = 1 if (2 * cfg.ffn + 15) // 16 >= 4 * cus else ops.MAX_GEMV_PARTS
         self.wd_parts = ops.MAX_GEMV_PARTS
         from .execution import UnsupportedStep
 

@@ -60,6 +60,7 @@ class OracleDecoder:
         self.nf = dec.norm_final.download()
         self.windows = dec.attn_windows
         self.f16_operands = False
+        self.f16_probs = False
         self._f16w = {}
         self.ple = dec.ple
         if self.ple:
@@ -118,17 +119,21 @@ class OracleDecoder:
         u = np.add(pn, e, dtype=np.float32) * np.float32(2.0 ** -0.5)
         return u.astype(np.float32).reshape(c.layers, P)
 
-    def step(self, pos: int, token: int, f16_operands: bool = False) -> np.ndarray:
-        """One decode step.  With `f16_operands` the step models the batched
-        prompt's precision: the layer projections round their operands to f16
-        as its GEMMs do, and attention rounds its probabilities to f16 (for a
-        prompt of at most 32 tokens, one key block); the lm_head and
+    def step(self, pos: int, token: int, f16_operands: bool = False, f16_probs: bool = False) -> np.ndarray:
+        """One decode step.  Models of the batched prompt's precision (for a
+        prompt of at most 32 tokens, one key block of its attention):
+        `f16_probs` rounds the attention probabilities to f16 as the prompt's
+        attention does (its f32-accurate GEMMs need no model);
+        `f16_operands` also rounds the layer projections' operands to f16, as
+        the prompt GEMMs' f16-operand form does.  The lm_head and
         per-layer-embedding GEMVs stay f32."""
         self.f16_operands = f16_operands
+        self.f16_probs = f16_probs or f16_operands
         try:
             return self._step(pos, token)
         finally:
             self.f16_operands = False
+            self.f16_probs = False
 
     def _step(self, pos: int, token: int) -> np.ndarray:
         c = self.cfg
@@ -146,7 +151,7 @@ class OracleDecoder:
                 k = qk[L["q_dim"]:]
                 v = qkv[L["q_dim"] + L["kv_dim"]:]
                 ora.kv_write(k, v, L["kc"], L["vc"], c.kv_heads, c.max_seq, hd, pos)
-            if self.f16_operands:
+            if self.f16_probs:
                 attn = self._attn_p_f16(qk[: L["q_dim"]], src["kc"], src["vc"], hd, pos + 1, self.windows[li])
             else:
                 attn = ora.attn_decode(qk[: L["q_dim"]], src["kc"], src["vc"], c.heads, c.kv_heads, hd, pos + 1,
