@@ -253,7 +253,7 @@ def bench_attention(args, doe):
     }
 
 
-def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
+def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder", cpu_runs=CPU_DECODE_RUNS):
     """2B-class decode loop at batch 1 (26 layers, hidden 2304, 8/4 heads of
     256, FFN 9216 GeGLU, Q4_K projections, f16 lm_head over 256000): a
     128-token prompt then `--decode-steps` greedy steps, each step a replay of
@@ -287,7 +287,7 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
     ids = dec.generate(prompt, n_new, s, graph=graph, steps_per_graph=max(spg, 1), timing=timing, prefill=pf)
     if graph is not None:
         graph.destroy()
-    parity, cpu = decode_parity_and_cpu(dec, prompt, s)
+    parity, cpu = decode_parity_and_cpu(dec, prompt, s, cpu_runs)
     tok_s = args.decode_steps / timing["decode_s"]
     mean_len = args.prompt_len + (args.decode_steps + 1) / 2.0
     bpt = cfg.decode_bytes_per_token(mean_len)
@@ -317,7 +317,7 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder"):
     }
 
 
-def decode_parity_and_cpu(dec, prompt, s):
+def decode_parity_and_cpu(dec, prompt, s, runs=CPU_DECODE_RUNS):
     """Outside the timed region: one eager decode step at position 0 with the
     logits kept, against the oracle decoder (the CPU restatement composed from
     the oracle's kernels, on the device's weights); the oracle step's own
@@ -333,7 +333,7 @@ def decode_parity_and_cpu(dec, prompt, s):
     dec.keep_logits = False
     oracle = OracleDecoder(dec)
     times = []
-    for _ in range(CPU_DECODE_RUNS):  # step 0 again each time: the same work, the same logits
+    for _ in range(runs):  # step 0 again each time: the same work, the same logits
         t0 = time.perf_counter()
         want = oracle.step(0, int(prompt[0]))
         times.append(time.perf_counter() - t0)
@@ -345,7 +345,8 @@ def decode_parity_and_cpu(dec, prompt, s):
     parity = {"step0_logits_rel_l2_vs_oracle": rel, "step0_token_equal": tok == int(np.argmax(want)),
               "tolerance": 1e-3}
     cpu = {"value": round(1.0 / el, 4), "unit": "tok/s", "cores": 1, "kind": "port", "runs": len(times),
-           "sample": f"median of {len(times)} full-size decode steps (position 0, every weight of every layer and "
+           "sample": f"{'median of ' if len(times) > 1 else ''}{len(times)} full-size decode step"
+                     f"{'s' if len(times) > 1 else ''} (position 0, every weight of every layer and "
                      f"the lm_head) of the single-threaded C oracle decoder (f32 left-fold, -O2 "
                      f"-ffp-contract=off), {el:.2f} s each, on {cpu_model()} ({os.cpu_count()} logical cores on "
                      f"host); attention at position 0 reads 1 key (< 1% of a token's bytes at the benchmarked "
@@ -367,6 +368,24 @@ def bench_decode_graph(args, doe):
     res = bench_decode(args, doe, cfg, ex.plan_decode(graph, cfg.layers),
                        label=f"{graph.model_id} (execution-v1 manifest graph)")
     return res
+
+
+def bench_decode_31b(args, doe):
+    """The decode loop planned from the reference's Gemma 4 31B af16 graph
+    (runtime/zig/examples/execution-v1/gemma-4-31b-af16-smoke.json, kept as
+    a test fixture) at that model's full shapes: 60 layers, hidden 5376, 32 /
+    16 heads of 256, FFN 21504 GeGLU, vocab 262144, every layer sliding over
+    512 keys (the graph's attention_sliding step); Q4_K projections, f16
+    lm_head and KV; random-init weights.  Step-0 parity against the oracle
+    decoder; its CPU baseline is one oracle step (~16 GB of Q4_K weights)."""
+    from doe_amd import execution as ex
+    from doe_amd.model import DecoderConfig
+
+    graph = ex.load_step_graph(ROOT / "tests" / "golden" / "execution_v1" / "gemma-4-31b-af16-smoke.json")
+    mc = graph.model_config
+    cfg = DecoderConfig.from_model_config(mc, max_seq=384, norm_weight_offset=False, rope_base_global=1e6)
+    plan = ex.plan_decode(graph, cfg.layers, cfg.head_dim, cfg.global_head_dim)
+    return bench_decode(args, doe, cfg, plan, label=f"{graph.model_id} (execution-v1 graph, 31B-class)", cpu_runs=1)
 
 
 GEMM_M, GEMM_N, GEMM_K = 2048, 21504, 5376
@@ -726,6 +745,7 @@ def main() -> int:
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--steps-per-graph", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-31b", action="store_true", help="skip the 31B-class decode line")
     ap.add_argument("--no-prefill", action="store_true", help="run prompts as teacher-forced decode steps")
     ap.add_argument("--gemm-steps", type=int, default=20)
     ap.add_argument("--no-gemm", action="store_true")
@@ -760,6 +780,7 @@ def main() -> int:
 
         dec_q8 = bench_decode(args, doe_amd, cfg=DecoderConfig(weight_format="q8_0"),
                               label="2B-class decoder, Q8_0 weights")
+    dec_31b = None if args.no_decode or args.no_31b else bench_decode_31b(args, doe_amd)
     gemm = None if args.no_gemm else bench_gemm(args, doe_amd)
     pfa = None if args.no_gemm else bench_prefill_attention(args, doe_amd)
     c4 = None if args.no_gemm else bench_config4(args, doe_amd)
@@ -814,6 +835,7 @@ def main() -> int:
         "decode": dec,
         "decode_graph_gemma3_270m": dec_graph,
         "decode_q8_0": dec_q8,
+        "decode_graph_gemma4_31b_af16": dec_31b,
         "prefill_gemm": gemm,
         "prefill_attention": pfa,
         "config4_decode_layer": c4,

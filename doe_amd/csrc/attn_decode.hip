@@ -100,11 +100,19 @@ __device__ __forceinline__ float sum16(float v) {
     return v + dpp<0x140>(v);
 }
 
+// P.V dims per lane: D / 64 for head dims that are multiples of 64, else
+// four (head_dim 160: lanes 0..39 own four dims each, lanes 40..63 load a
+// clamped copy of lane 39's and keep nothing).
+template <int D>
+constexpr int dims_per_lane() { return D % 64 == 0 ? D / 64 : 4; }
+template <int D>
+constexpr int v_lanes() { return D / dims_per_lane<D>(); }
+
 // K fragment and V rows of one 16-position block, as loaded by one lane.
 template <int D>
 struct KVBlock {
     h8 kf[D / 32];
-    _Float16 vv[16][D / 64];
+    _Float16 vv[16][dims_per_lane<D>()];
 };
 
 // Cache row of logical key p (see AttnArgs), clamped into the cache.
@@ -127,7 +135,8 @@ __device__ __forceinline__ int kv_row(const AttnArgs &a, int p) {
 template <int D>
 __device__ __forceinline__ void load_block(KVBlock<D> &blk, const uint16_t *kb, const uint16_t *vb,
                                            int rowk, size_t pos_stride, int lane, int vrow0, int vrow_last) {
-    constexpr int KSTEPS = D / 32, DPL = D / 64;
+    constexpr int KSTEPS = D / 32, DPL = dims_per_lane<D>(), VL = v_lanes<D>();
+    const int vlane = lane < VL ? lane : VL - 1;
     // dims 8 (lane / 16) + 32 s of the lane's key
     const uint16_t *krow = kb + (size_t)rowk * pos_stride + 8 * (lane >> 4);
 #pragma unroll
@@ -136,7 +145,7 @@ __device__ __forceinline__ void load_block(KVBlock<D> &blk, const uint16_t *kb, 
 #pragma unroll
         for (int n = 0; n < 16; ++n) {
             const int r = min(vrow0 + n, vrow_last);
-            const _Float16 *vrow = reinterpret_cast<const _Float16 *>(vb + (size_t)r * pos_stride + lane * DPL);
+            const _Float16 *vrow = reinterpret_cast<const _Float16 *>(vb + (size_t)r * pos_stride + vlane * DPL);
 #pragma unroll
             for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
         }
@@ -144,7 +153,7 @@ __device__ __forceinline__ void load_block(KVBlock<D> &blk, const uint16_t *kb, 
 #pragma unroll
         for (int n = 0; n < 16; ++n) {
             const int r = __builtin_amdgcn_readlane(rowk, n);
-            const _Float16 *vrow = reinterpret_cast<const _Float16 *>(vb + (size_t)r * pos_stride + lane * DPL);
+            const _Float16 *vrow = reinterpret_cast<const _Float16 *>(vb + (size_t)r * pos_stride + vlane * DPL);
 #pragma unroll
             for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
         }
@@ -155,7 +164,8 @@ template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     constexpr int kWaves = W, kThreads = 64 * W;
     constexpr int KSTEPS = D / 32;  // MFMA k-steps over the head dimension
-    constexpr int DPL = D / 64;     // P.V dims per lane
+    constexpr int DPL = dims_per_lane<D>();  // P.V dims per lane
+    constexpr int VL = v_lanes<D>();         // lanes that own P.V dims
     constexpr int G4 = (G + 3) / 4; // 4-head groups of the probability broadcast
     constexpr float kLog2e = 1.4426950408889634f;
     // The query fragments are dead once the block loop ends; the wave
@@ -365,7 +375,8 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) sm.wo[wave][h][lane * DPL + d] = o[h][d];
+        for (int d = 0; d < DPL; ++d)
+            if (lane < VL) sm.wo[wave][h][lane * DPL + d] = o[h][d];
     __syncthreads();
 
     const size_t bh0 = (size_t)b * a.num_heads + hq0;
@@ -419,7 +430,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    constexpr int SL = D < kCombineCols ? D : kCombineCols;  // columns per workgroup
+    constexpr int SL = D % kCombineCols == 0 ? kCombineCols : (D < kCombineCols ? D : 32);  // columns per workgroup
     constexpr int C4 = SL / 4, PH = 256 / C4;
     constexpr int NS = D / SL;                                 // slices per head
     __shared__ float wts[kMaxSplits];
@@ -591,7 +602,8 @@ int launch_d(int g, bool w, dim3 grid, hipStream_t st, const AttnArgs &a) {
         DOE_LAUNCH_CHECK("attn_combine_wave_kernel");
         return DOE_OK;
     }
-    const unsigned slices = D < kCombineCols ? 1u : (unsigned)(D / kCombineCols);
+    constexpr int SL = D % kCombineCols == 0 ? kCombineCols : (D < kCombineCols ? D : 32);
+    const unsigned slices = (unsigned)(D / SL);
     hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(total_heads * slices), dim3(256), 0, st, a);
     DOE_LAUNCH_CHECK("attn_combine_kernel");
     return DOE_OK;
@@ -655,8 +667,8 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
                 (long long)num_kv_heads);
     DOE_REQUIRE(kv_layout == 0 || kv_layout == 1, DOE_E_UNSUPPORTED,
                 "kv_layout %d unsupported (0: [kv_head][pos][dim], 1: [pos][kv_head][dim])", kv_layout);
-    DOE_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512,
-                DOE_E_UNSUPPORTED, "head_dim %lld unsupported (64, 128, 256, 512)", (long long)head_dim);
+    DOE_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 160 || head_dim == 256 || head_dim == 512,
+                DOE_E_UNSUPPORTED, "head_dim %lld unsupported (64, 128, 160, 256, 512)", (long long)head_dim);
     const bool plain = map.kv_map == 0 && map.kv_start == 0;  // logical key p is cache row p
     DOE_REQUIRE(kv_len_dev != nullptr || (kv_len >= 0 && (!plain || kv_len <= kv_stride) && kv_len < (1 << 30)),
                 DOE_E_INVALID, "kv_len %lld out of range [0, kv_stride=%lld]", (long long)kv_len,
@@ -772,6 +784,7 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
     switch (head_dim) {
         case 64: return launch_d<64>(g, wide, grid, st, a);
         case 128: return launch_d<128>(g, wide, grid, st, a);
+        case 160: return launch_d<160>(g, false, grid, st, a);
         case 256: return launch_d<256>(g, wide, grid, st, a);
         default:
             return launch_d<512>(g / a.head_groups, false, grid, st, a);

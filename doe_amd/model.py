@@ -107,8 +107,11 @@ class DecoderConfig:
         fmt = mc.get("quantFormat", "q4k")
         if fmt not in ("q4k", "q8_0"):
             raise UnsupportedStep(f"quantFormat {fmt!r}")
+        # numKeyValueHeads absent: one kv head per query head (the reference's
+        # kv_dim = (num_key_value_heads orelse num_heads) * head_dim,
+        # csl_host_plan_tool.zig:412)
         kw = dict(layers=mc["numLayers"], hidden=mc["hiddenDim"], heads=mc["numHeads"],
-                  kv_heads=mc["numKeyValueHeads"], head_dim=mc["headDim"], vocab=mc["vocabSize"],
+                  kv_heads=mc.get("numKeyValueHeads") or mc["numHeads"], head_dim=mc["headDim"], vocab=mc["vocabSize"],
                   ffn=mc["hiddenDim"] * mc.get("ffnExpansionFactor", 4), weight_format=fmt,
                   global_head_dim=mc.get("globalHeadDim") or 0, ple_width=mc.get("pleWidth") or 0,
                   ple_vocab=mc.get("pleVocabSize") or 0)
@@ -367,22 +370,26 @@ class Decoder:
                                             sliding_window=self.attn_windows[li], softcap=c.attn_softcap,
                                             stream=stream)
             # combine + o_proj + attn_residual as K-range parts
+            # (the attention prologue takes one Q4_K block per wave: past 16
+            # blocks o_proj needs more than one range)
+            wo_parts = max(self.wo_parts, -(-L.q_dim // 4096))
             no = ops.q4k_gemv_ex(L.wo, c.hidden, L.q_dim, attn_partials=self.attn_parts, attn_splits=splits,
                                  attn_num_heads=c.heads, attn_head_dim=hd, residual=resid,
-                                 output_parts=self.parts_o, max_output_parts=self.wo_parts, stream=stream)
+                                 output_parts=self.parts_o, max_output_parts=wo_parts, stream=stream)
             # post_attn_norm + gate/up_proj + GeGLU over the summed parts (kept in x_mid)
             ops.q4k_gemv_ex(L.wgu, 2 * c.ffn, c.hidden, activation=self._po[0], activation_parts=self._po[1],
                             activation_nparts=no - 1, activation_sum=self.x_mid if no > 1 else None,
                             output=self.h, norm_weight=L.norm_ffn, norm_eps=c.eps,
                             norm_weight_offset=c.norm_weight_offset, gated=True, stream=stream)
             mid = self.x_mid if no > 1 else self._po[0]
+            # down_proj + ffn_residual as K-range parts
+            nd = ops.q4k_gemv_ex(L.wd, c.hidden, c.ffn, activation=self.h, residual=mid,
+                                 output_parts=self.parts_d, max_output_parts=self.wd_parts, stream=stream)
             if li == last or self.ple:
-                # down_proj + ffn_residual into x whole (not in place: no K split)
-                ops.matmul_q4k_fused(L.wd, self.h, self.x, c.hidden, c.ffn, residual=mid, stream=stream)
+                # the lm_head and the per-layer input block read x whole
+                self._sum_parts(self.parts_d, nd, self.x, stream)
                 act, act_parts, na = self.x, None, 0
             else:
-                nd = ops.q4k_gemv_ex(L.wd, c.hidden, c.ffn, activation=self.h, residual=mid,
-                                     output_parts=self.parts_d, max_output_parts=self.wd_parts, stream=stream)
                 act, act_parts, na = self._pd[0], self._pd[1], nd - 1
             if self.ple:
                 self._ple_block(li, L, stream)
@@ -392,6 +399,17 @@ class Decoder:
         _lib.call("doe_decode_advance", C.c_void_p(self.state.ptr), C.c_void_p(self.token.ptr),
                   C.c_void_p(self.ids.ptr), c.max_seq, C.c_void_p(self.argmax_parts.ptr), nparts,
                   _stream_ptr(stream))
+
+    def _sum_parts(self, parts: DeviceBuffer, n: int, out: DeviceBuffer, stream) -> None:
+        """out = parts[0] + parts[1] + ... + parts[n - 1], added in that order."""
+        hb = self.cfg.hidden * 4
+        p = [parts.view(i * hb, hb, np.float32) for i in range(n)]
+        if n == 1:
+            out.copy_from(p[0], stream)
+            return
+        ops.residual(p[0], p[1], out, self.cfg.hidden, stream=stream)
+        for i in range(2, n):
+            ops.residual(out, p[i], out, self.cfg.hidden, stream=stream)
 
     def _layer_q4k_atomic(self, li: int, L: LayerWeights, stream) -> None:
         """A Q4_K layer whose o_proj / down_proj add their K ranges into x

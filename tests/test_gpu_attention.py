@@ -54,7 +54,7 @@ def test_config1_gqa_decode(dev, ora):
     assert err <= ATTN_REL_L2
 
 
-@pytest.mark.parametrize("d", [64, 128, 256, 512])
+@pytest.mark.parametrize("d", [64, 128, 160, 256, 512])
 @pytest.mark.parametrize("g", [1, 2, 4, 8])
 def test_head_dims_and_groups(dev, ora, d, g):
     # (head_dim 512 with more than two query heads per kv head runs as g / 2
@@ -346,7 +346,7 @@ def test_reference_dispatch_rejects_unsupported(dev):
 
 
 @pytest.mark.parametrize("splits", [2, 7, 33, 64, 100])
-@pytest.mark.parametrize("d,out_f16", [(256, True), (128, False), (64, True), (512, False)])
+@pytest.mark.parametrize("d,out_f16", [(256, True), (128, False), (64, True), (512, False), (160, False)])
 def test_split_combine_kernels(dev, ora, splits, d, out_f16):
     # the one-wave-per-column combine (up to 64 splits, lanes over splits)
     # and the block-reduction combine (any count; forced, and automatic past
@@ -372,3 +372,23 @@ def test_split_combine_kernels(dev, ora, splits, d, out_f16):
     for got in outs:
         assert rel_l2(got, want) <= ATTN_REL_L2
     assert rel_l2(outs[0], outs[1]) <= (1e-3 if out_f16 else 1e-6)
+
+
+def test_head160_sliding_layout1_kv_len_device(dev, ora):
+    # head_dim 160 (Gemma 4 31B smoke graph: 32 heads x 160): the
+    # [pos][kv_head][dim] layout, a sliding window, a device kv_len and a
+    # softcap, f16 query and output
+    from doe_amd import DeviceBuffer
+
+    rng = np.random.default_rng(160)
+    hq, hkv, d, t, stride = 32, 32, 160, 900, 1024
+    q = rng.standard_normal((1, hq, d)).astype(np.float16)
+    k = rng.standard_normal((1, stride, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((1, stride, hkv, d)).astype(np.float16)
+    klen = DeviceBuffer.from_array(np.array([t], np.int32))
+    for softcap, window in ((0.0, 512), (30.0, 0)):
+        got = run_attn(q, k, v, hq=hq, hkv=hkv, d=d, kv_len=0, kv_stride=stride, scale=d ** -0.5, q_f16=True,
+                       out_f16=True, softcap=softcap, window=window, layout=1, kv_len_buffer=klen)
+        want = oracle_attn(ora, q, k, v, batch=1, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=d ** -0.5,
+                           softcap=softcap, window=window, layout=1)
+        assert rel_l2(got, want) <= ATTN_REL_L2, (softcap, window)

@@ -372,6 +372,58 @@ def test_gemma4_e2b_graph_replay_equals_eager(dev):
     assert out.tolist() == eager.tolist()
 
 
+def _gemma4_31b(name, layers, vocab=32768):
+    """A reference Gemma 4 31B step graph (gemma-4-31b-smoke.json: 32 heads
+    x 160, one kv head per query head, hidden 5120, FFN 20480, per-layer
+    embeddings of width 256, global layers every 5th, the last 4 layers
+    sharing KV; gemma-4-31b-af16-smoke.json: hidden 5376, 32 / 16 heads x
+    256, FFN 21504, every layer sliding over 512 keys) at its full width
+    over `layers` layers and a smaller vocabulary."""
+    from doe_amd import execution as ex
+
+    g = json.loads((Path(__file__).parent / "golden" / "execution_v1" / name).read_text())
+    mc = {**g["modelConfig"], "numLayers": layers, "vocabSize": vocab, "pleVocabSize": vocab, "maxSeqLen": 64}
+    g["modelConfig"] = mc
+    graph = ex.load_step_graph(g)
+    cfg = DecoderConfig.from_model_config(mc, norm_weight_offset=False, rope_base_global=1e6)
+    plan = ex.plan_decode(graph, cfg.layers, cfg.head_dim, cfg.global_head_dim)
+    return cfg, plan
+
+
+def test_gemma4_31b_head160_graph_decodes_against_oracle(dev, ora):
+    # gemma-4-31b-smoke.json at full width, 10 layers (global 4 and 9; 6, 7,
+    # 8 read layer 5's cache, 9 reads layer 4's): head_dim 160 attention,
+    # 32 kv heads, per-layer embeddings; 4 teacher-forced steps
+    cfg, plan = _gemma4_31b("gemma-4-31b-smoke.json", 10)
+    assert (cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ffn, cfg.ple_width) == (5120, 32, 32, 160, 20480, 256)
+    assert plan.windows == (512,) * 4 + (0,) + (512,) * 4 + (0,)
+    assert plan.kv_sources == (0, 1, 2, 3, 4, 5, 5, 5, 5, 4)
+    dec = Decoder(cfg, keep_logits=True, plan=plan)
+    dec.init_random(seed=31)
+    s = Stream()
+    oracle = OracleDecoder(dec)
+    ids, errs = run_teacher_forced(dec, oracle, np.array([17, 30000, 4242], np.int32), 2, s)
+    print(f"[decode 31b head160] logits rel_l2 {['%.1e' % e for e in errs]}", flush=True)
+    assert max(errs) <= 1e-3
+
+
+def test_gemma4_31b_af16_graph_decodes_against_oracle(dev, ora):
+    # gemma-4-31b-af16-smoke.json at full width, 4 layers: o_proj over K =
+    # 8192 (two K ranges for the attention prologue), down_proj over K =
+    # 21504 (past 16384: K ranges of at most 64 blocks), the last layer's
+    # ranges summed for the lm_head; 4 teacher-forced steps
+    cfg, plan = _gemma4_31b("gemma-4-31b-af16-smoke.json", 4)
+    assert (cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ffn) == (5376, 32, 16, 256, 21504)
+    assert plan.windows == (512,) * 4
+    dec = Decoder(cfg, keep_logits=True, plan=plan)
+    dec.init_random(seed=32)
+    s = Stream()
+    oracle = OracleDecoder(dec)
+    ids, errs = run_teacher_forced(dec, oracle, np.array([5, 31000, 77], np.int32), 2, s)
+    print(f"[decode 31b af16] logits rel_l2 {['%.1e' % e for e in errs]}", flush=True)
+    assert max(errs) <= 1e-3
+
+
 def _prefill_then_decode(dec, oracle, prompt, n_after, s, f16_prompt=False):
     """Batched prompt, then decode steps; every logits vector against the
     oracle decoder stepping through the same tokens.  Returns the errors.
