@@ -116,6 +116,10 @@ SIGNATURES: dict[str, list] = {
     "doe_decode_advance": [_vp, _vp, _vp, _i64, _vp, _i32, _vp],
     "doe_read_xor_u32": [_vp, _i64, _vp, _i32, _vp],
     "doe_q4k_gemv_ex": [_vp, _vp],
+    "doe_gated": [_vp, _vp, _vp, _i64, _i32, _vp],
+    "doe_l2_normalize": [_vp, _vp, _i64, _i64, _f32, _vp],
+    "doe_conv1d_depthwise": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "doe_linear_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp],
     "doe_device_timestamp": [_vp, _vp],
     "doe_device_timestamp_hz": [C.POINTER(_i64)],
     "doe_tune_set": [C.c_char_p, _i32],

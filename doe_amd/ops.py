@@ -537,6 +537,56 @@ def residual(input: DeviceBuffer, residual_in: DeviceBuffer, output: DeviceBuffe
     _lib.call("doe_residual_add", _p(input), _p(residual_in), _p(output), n, _stream_ptr(stream))
 
 
+GATED_KINDS = {"gelu": 0, "silu": 1, "sigmoid": 2}
+
+
+def gated(gate: DeviceBuffer, input: DeviceBuffer, output: DeviceBuffer, n: int, kind: str, stream=None) -> None:
+    """``gelu_gated`` / ``silu_gated`` / ``sigmoid_gated`` (the graph's
+    ``o_gate``): output = act(gate) * input, the reference's clamps."""
+    if kind not in GATED_KINDS:
+        raise ValueError(f"kind {kind!r} is not one of {sorted(GATED_KINDS)}")
+    for buf, role in ((gate, "gate"), (input, "input"), (output, "output")):
+        _need(buf, n * 4, role)
+    _lib.call("doe_gated", _p(gate), _p(input), _p(output), n, GATED_KINDS[kind], _stream_ptr(stream))
+
+
+def l2_normalize(input: DeviceBuffer, output: DeviceBuffer, rows: int, hidden: int, eps: float = 1e-6,
+                 stream=None) -> None:
+    """``l2_normalize``: each row / sqrt(sum of squares + eps)."""
+    _need(input, rows * hidden * 4, "input")
+    _need(output, rows * hidden * 4, "output")
+    _lib.call("doe_l2_normalize", _p(input), _p(output), rows, hidden, eps, _stream_ptr(stream))
+
+
+def conv1d_depthwise(input: DeviceBuffer, weight: DeviceBuffer, bias: DeviceBuffer | None, output: DeviceBuffer,
+                     tokens: int, channels: int, kernel_size: int, stream=None) -> None:
+    """``conv1d_depthwise``: causal depthwise conv over [tokens][channels]."""
+    _need(input, tokens * channels * 4, "input")
+    _need(output, tokens * channels * 4, "output")
+    _need(weight, channels * kernel_size * 4, "weight")
+    if bias is not None:
+        _need(bias, channels * 4, "bias")
+    b = _p(bias) if bias is not None else C.c_void_p(None)
+    _lib.call("doe_conv1d_depthwise", _p(input), _p(weight), b, _p(output), tokens, channels, kernel_size,
+              _stream_ptr(stream))
+
+
+def linear_attention(q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, gate: DeviceBuffer, state: DeviceBuffer,
+                     output: DeviceBuffer, tokens: int, heads: int, key_dim: int, value_dim: int,
+                     a_log: DeviceBuffer | None = None, stream=None) -> None:
+    """``linear_attention`` (gated DeltaNet): `tokens` tokens in order
+    through the per-head state [heads][value_dim][key_dim] (in place)."""
+    for buf, role, n in ((q, "q", value_dim), (gate, "gate", value_dim), (output, "output", value_dim),
+                         (k, "k", key_dim), (v, "v", key_dim)):
+        _need(buf, tokens * heads * n * 4, role)
+    _need(state, heads * value_dim * key_dim * 4, "state")
+    al = _p(a_log) if a_log is not None else C.c_void_p(None)
+    if a_log is not None:
+        _need(a_log, heads * 4, "a_log")
+    _lib.call("doe_linear_attention", _p(q), _p(k), _p(v), _p(gate), _p(state), _p(output), tokens, heads, key_dim,
+              value_dim, al, _stream_ptr(stream))
+
+
 def ple_modulate(projected: DeviceBuffer, gathered: DeviceBuffer, output: DeviceBuffer, n: int, scale: float,
                  stream=None) -> None:
     """``ple_modulate`` step: output = (projected + gathered) * scale."""

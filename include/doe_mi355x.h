@@ -562,6 +562,44 @@ int doe_f16_gemv_argmax(const uint16_t *b_f16, const float *a, float *logits, in
                         int norm_weight_offset, uint64_t *argmax_partials,
                         int64_t partials_capacity, int32_t *num_partials, doe_stream_t stream);
 
+/* ---- Qwen 3.6 graph ops: gated activations and the gated-DeltaNet body ------
+ * The ops of runtime/zig/examples/execution-v1/qwen-3-6-27b-smoke.json that
+ * the attention path above does not cover, with the reference interpreter's
+ * semantics (runtime/zig/src/tsir/reference_interpreter.zig).  f32 tensors,
+ * caller-owned device buffers. */
+/* output = act(gate) * input: kind 0 gelu (inner argument clamped to
+ * [-15, 15]), 1 silu x / (1 + exp(z)), 2 sigmoid 1 / (1 + exp(z)), z =
+ * clamp(-x, -15, 15).  Replaces the gelu_gated / silu_gated / sigmoid_gated
+ * (o_gate) ops (tryGated, reference_interpreter.zig:954-1052: bindings gate,
+ * input, output). */
+int doe_gated(const float *gate, const float *input, float *output, int64_t n, int kind,
+              doe_stream_t stream);
+/* Per row of `hidden` values: output = input / sqrt(sum(input^2) + eps).
+ * Replaces `l2_normalize` (tryL2Normalize, reference_interpreter.zig:
+ * 1284-1361: bindings input, output; body hidden, eps). */
+int doe_l2_normalize(const float *input, float *output, int64_t rows, int64_t hidden, float eps,
+                     doe_stream_t stream);
+/* Causal depthwise conv: input / output [tokens][channels], weight
+ * [channels][kernel_size], bias [channels] or NULL; output[t][c] = bias[c]
+ * + sum_k input[t - (kernel_size-1-k)][c] * weight[c][k] over the rows that
+ * exist, rounded as the interpreter's f32 loop (bit for bit).  Replaces
+ * `conv1d_depthwise` (tryConv1DDepthwise, reference_interpreter.zig:
+ * 1363-1455: bindings input, weight, bias, output). */
+int doe_conv1d_depthwise(const float *input, const float *weight, const float *bias, float *output,
+                         int64_t tokens, int64_t channels, int64_t kernel_size, doe_stream_t stream);
+/* Gated DeltaNet, single-query shared-norm form, over `tokens` tokens in
+ * order: q, gate, output [tokens][heads][value_dim]; k, v
+ * [tokens][heads][key_dim]; state [heads][value_dim][key_dim] updated in
+ * place.  Per head alpha = 1 - exp(-a_log[h]) (a_log NULL: 0.5, the
+ * interpreter's value); per state row d: dot = S[d] . k, S[d] = (1 - alpha)
+ * S[d] + alpha (q[d] - dot) k, output[d] = S[d] . v + sigmoid(gate[d]) q[d].
+ * key_dim <= 256.  Replaces `linear_attention` (tryLinearAttention,
+ * reference_interpreter.zig:1457-1596; emit_kernel_body_linear_attention.zig:
+ * bindings query, key, value, gate, linear_state, output). */
+int doe_linear_attention(const float *q, const float *k, const float *v, const float *gate, float *state,
+                         float *output, int64_t tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
+                         const float *a_log, doe_stream_t stream);
+
 /* ---- synthetic inputs and decode-loop bookkeeping -----------------------------
  * No reference counterpart: the reference's decode numbers come from real
  * model weights (Doppler RDRR shards); benchmarks here run on seeded random

@@ -19,6 +19,9 @@
  *                                                   GQA head mapping, causal and
  *                                                   sliding-window limits, softcap
  *   runtime/zig/tests/tsir/real/lm_head_gemv/lm_head_gemv.wgsl   f16-weight GEMV
+ *   runtime/zig/src/tsir/reference_interpreter.zig:954-1052, 1284-1596
+ *                                                   gated activations, l2_normalize,
+ *                                                   conv1d_depthwise, linear_attention
  *   bench/kernels/compilation-corpus/complex_fused_gemv_dequant.wgsl  int4 group GEMV
  *
  * Build: gcc -O2 -ffp-contract=off -fPIC -shared (see oracle/Makefile).
@@ -458,6 +461,113 @@ int ora_geglu(const float *gate, const float *up, float *out, int64_t n) {
         if (inner > 15.0f) inner = 15.0f;
         float act = 0.5f * x * (1.0f + tanhf(inner));
         out[i] = act * up[i];
+    }
+    return 0;
+}
+
+int ora_gated(const float *gate, const float *input, float *out, int64_t n, int kind) {
+    /* reference_interpreter.zig:1023-1052 (tryGated): act(gate) * input with
+     *   kind 0 gelu    : inner = a*(x + b*x^3) clamped to [-15, 15],
+     *                    0.5*x*(1 + tanh(inner))
+     *   kind 1 silu    : x / (1 + exp(z)),  z = clamp(-x, -15, 15)
+     *   kind 2 sigmoid : 1 / (1 + exp(z)),  z = clamp(-x, -15, 15)
+     * all in f32 (the platform expf / tanhf). */
+    if (n < 0 || kind < 0 || kind > 2) return -1;
+    const float ga = 0.7978845608028654f;
+    const float gb = 0.044715f;
+    for (int64_t i = 0; i < n; ++i) {
+        float x = gate[i];
+        float act;
+        if (kind == 0) {
+            float inner = ga * (x + gb * x * x * x);
+            if (inner < -15.0f) inner = -15.0f;
+            if (inner > 15.0f) inner = 15.0f;
+            act = 0.5f * x * (1.0f + tanhf(inner));
+        } else {
+            float z = -x;
+            if (z < -15.0f) z = -15.0f;
+            if (z > 15.0f) z = 15.0f;
+            act = (kind == 1 ? x : 1.0f) / (1.0f + expf(z));
+        }
+        out[i] = act * input[i];
+    }
+    return 0;
+}
+
+int ora_l2_normalize(const float *in, float *out, int64_t rows, int64_t hidden, float eps) {
+    /* reference_interpreter.zig:1284-1361 (tryL2Normalize), per row:
+     * sq = f32 left-fold of x*x, inv = 1 / sqrt(sq + eps), out = x * inv. */
+    if (rows < 0 || hidden <= 0) return -1;
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *x = in + r * hidden;
+        float sq = 0.0f;
+        for (int64_t d = 0; d < hidden; ++d) sq += x[d] * x[d];
+        float inv = 1.0f / sqrtf(sq + eps);
+        for (int64_t d = 0; d < hidden; ++d) out[r * hidden + d] = x[d] * inv;
+    }
+    return 0;
+}
+
+int ora_conv1d_depthwise(const float *in, const float *w, const float *bias, float *out, int64_t tokens,
+                         int64_t channels, int64_t kernel_size) {
+    /* reference_interpreter.zig:1363-1455 (tryConv1DDepthwise): input and
+     * output [token][channel], weight [channel][kernel_size], causal:
+     * out[t][c] = bias[c] + sum_{k, t - (K-1-k) >= 0} in[t-(K-1-k)][c] w[c][k],
+     * the terms in k order from the bias (or 0). */
+    if (tokens < 0 || channels <= 0 || kernel_size <= 0) return -1;
+    for (int64_t t = 0; t < tokens; ++t) {
+        for (int64_t c = 0; c < channels; ++c) {
+            float acc = bias ? bias[c] : 0.0f;
+            for (int64_t k = 0; k < kernel_size; ++k) {
+                int64_t ti = t - (kernel_size - 1 - k);
+                if (ti < 0) continue;
+                acc += in[ti * channels + c] * w[c * kernel_size + k];
+            }
+            out[t * channels + c] = acc;
+        }
+    }
+    return 0;
+}
+
+int ora_linear_attention(const float *q, const float *k, const float *v, const float *gate, float *state,
+                         float *out, int64_t tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
+                         const float *a_log) {
+    /* reference_interpreter.zig:1457-1596 (tryLinearAttention; the gated
+     * DeltaNet single-query shared-norm form of
+     * emit_kernel_body_linear_attention.zig), per token and head, with
+     * alpha = 1 - exp(-A_log) (A_log = 0.5 when a_log is NULL, the
+     * interpreter's fixed value) and decay = 1 - alpha:
+     *   for d: dot = sum_k S[d][k] kin[k]            (f32 left-fold)
+     *          S[d][k] = decay * S[d][k] + (alpha * (q[d] - dot)) * kin[k]
+     *   out[d] = sum_k S[d][k] v[k] + sigmoid(g[d]) * q[d]
+     * q, gate, out [token][head][value_dim]; k, v [token][head][key_dim];
+     * state [head][value_dim][key_dim], updated in place token after token. */
+    if (tokens < 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) return -1;
+    for (int64_t t = 0; t < tokens; ++t) {
+        for (int64_t h = 0; h < heads; ++h) {
+            const float al = a_log ? a_log[h] : 0.5f;
+            const float alpha = 1.0f - expf(-al);
+            const float decay = 1.0f - alpha;
+            const float *qh = q + (t * heads + h) * value_dim;
+            const float *gh = gate + (t * heads + h) * value_dim;
+            const float *kh = k + (t * heads + h) * key_dim;
+            const float *vh = v + (t * heads + h) * key_dim;
+            float *S = state + h * value_dim * key_dim;
+            for (int64_t d = 0; d < value_dim; ++d) {
+                float dot = 0.0f;
+                for (int64_t j = 0; j < key_dim; ++j) dot += S[d * key_dim + j] * kh[j];
+                const float scaled = alpha * (qh[d] - dot);
+                for (int64_t j = 0; j < key_dim; ++j)
+                    S[d * key_dim + j] = decay * S[d * key_dim + j] + scaled * kh[j];
+            }
+            float *oh = out + (t * heads + h) * value_dim;
+            for (int64_t d = 0; d < value_dim; ++d) {
+                float acc = 0.0f;
+                for (int64_t j = 0; j < key_dim; ++j) acc += S[d * key_dim + j] * vh[j];
+                const float sg = 1.0f / (1.0f + expf(-gh[d]));
+                oh[d] = acc + sg * qh[d];
+            }
+        }
     }
     return 0;
 }

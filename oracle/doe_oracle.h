@@ -91,6 +91,15 @@ int ora_attn_prefill(const float *q, const float *k, const float *v, float *o,
                      int64_t q_len, int64_t kv_len, int64_t start_pos, float scale,
                      int causal, int64_t row_begin, int64_t row_end);
 
+/* ---- Qwen 3.6 graph ops (gated DeltaNet body, gated activations) ---------- */
+int ora_gated(const float *gate, const float *input, float *out, int64_t n, int kind);
+int ora_l2_normalize(const float *in, float *out, int64_t rows, int64_t hidden, float eps);
+int ora_conv1d_depthwise(const float *in, const float *w, const float *bias, float *out, int64_t tokens,
+                         int64_t channels, int64_t kernel_size);
+int ora_linear_attention(const float *q, const float *k, const float *v, const float *gate, float *state,
+                         float *out, int64_t tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
+                         const float *a_log);
+
 #ifdef __cplusplus
 }
 #endif

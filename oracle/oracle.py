@@ -62,6 +62,10 @@ def lib() -> C.CDLL:
             "ora_kv_write": ([vp, vp, vp, vp, i64, i64, i64, i64, i32], i32),
             "ora_attn_decode": ([vp, vp, vp, vp, i64, i64, i64, i64, i64, f32, f32, i64, i32], i32),
             "ora_attn_prefill": ([vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, f32, i32, i64, i64], i32),
+            "ora_gated": ([vp, vp, vp, i64, i32], i32),
+            "ora_l2_normalize": ([vp, vp, i64, i64, f32], i32),
+            "ora_conv1d_depthwise": ([vp, vp, vp, vp, i64, i64, i64], i32),
+            "ora_linear_attention": ([vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -240,6 +244,52 @@ def geglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     out = np.zeros_like(g)
     _ok(lib().ora_geglu(_ptr(g), _ptr(u), _ptr(out), g.size), "geglu")
     return out
+
+
+GATED_KINDS = {"gelu": 0, "silu": 1, "sigmoid": 2}
+
+
+def gated(gate: np.ndarray, inp: np.ndarray, kind: str) -> np.ndarray:
+    """act(gate) * input, act gelu / silu / sigmoid with the interpreter's clamps."""
+    g = _c(gate, np.float32)
+    x = _c(inp, np.float32)
+    out = np.zeros_like(g)
+    _ok(lib().ora_gated(_ptr(g), _ptr(x), _ptr(out), g.size, GATED_KINDS[kind]), "gated")
+    return out
+
+
+def l2_normalize(x: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    x = _c(x, np.float32)
+    hidden = x.shape[-1]
+    out = np.zeros_like(x)
+    _ok(lib().ora_l2_normalize(_ptr(x), _ptr(out), x.size // hidden, hidden, eps), "l2_normalize")
+    return out
+
+
+def conv1d_depthwise(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None) -> np.ndarray:
+    """x [tokens][channels], w [channels][kernel_size], causal."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    tokens, channels = x.shape
+    out = np.zeros_like(x)
+    b = _c(bias, np.float32) if bias is not None else None
+    _ok(lib().ora_conv1d_depthwise(_ptr(x), _ptr(w), _ptr(b) if b is not None else None, _ptr(out), tokens,
+                                    channels, w.shape[1]), "conv1d_depthwise")
+    return out
+
+
+def linear_attention(q, k, v, gate, state, a_log=None):
+    """q, gate [tokens][heads][value_dim]; k, v [tokens][heads][key_dim];
+    state [heads][value_dim][key_dim] (a copy is updated and returned)."""
+    q, k, v, g = (_c(a, np.float32) for a in (q, k, v, gate))
+    s = np.array(state, np.float32, copy=True)
+    tokens, heads, vd = q.shape
+    kd = k.shape[-1]
+    out = np.zeros_like(q)
+    al = _c(a_log, np.float32) if a_log is not None else None
+    _ok(lib().ora_linear_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(s), _ptr(out), tokens, heads, kd, vd,
+                                    _ptr(al) if al is not None else None), "linear_attention")
+    return s, out
 
 
 def residual(a: np.ndarray, b: np.ndarray) -> np.ndarray:

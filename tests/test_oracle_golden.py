@@ -527,6 +527,10 @@ PINS = {
     "ora_kv_write": ["test_kv_write_and_gather"],
     "ora_attn_decode": ["test_emulator_attention_known_answer", "test_attention_invariants_and_gqa"],
     "ora_attn_prefill": ["test_attention_prefill_causal_matches_float64"],
+    "ora_gated": ["test_oracle_ssm.py::test_gated_closed_forms_and_clamps"],
+    "ora_l2_normalize": ["test_oracle_ssm.py::test_l2_normalize_fixture_closed_form_and_eps"],
+    "ora_conv1d_depthwise": ["test_oracle_ssm.py::test_conv1d_depthwise_brute_force_fixture_and_causality"],
+    "ora_linear_attention": ["test_oracle_ssm.py::test_linear_attention_recurrence_and_closed_forms"],
 }
 
 
