@@ -76,6 +76,14 @@ struct AttnArgs {
     // The query's absolute position: kv_start + kv_len - 1 (query_at_end) or
     // start_pos; causal keeps keys <= it, a sliding window the last `window`.
     int query_at_end, start_pos, causal;
+    // > 0: split s owns the fixed blocks [s * spec_bps, (s + 1) * spec_bps),
+    // at most one per wave, and each wave loads its block before the device
+    // kv_len arrives (a contiguous cache whose length the host knows only as
+    // kv_stride); 0: the blocks are divided by the kv_len the kernel reads.
+    int spec_bps;
+    // (host side) every wave owns at most one block: the launch picks the
+    // kernel form without a prefetch, holding the query in registers
+    int one_block;
 };
 
 constexpr int kMaxSplits = 512;
@@ -116,12 +124,14 @@ struct KVBlock {
 };
 
 // Cache row of logical key p (see AttnArgs), clamped into the cache.
+// PAGED false: the caller guarantees kv_map != 2 (no page-table load).
+template <bool PAGED = true>
 __device__ __forceinline__ int kv_row(const AttnArgs &a, int p) {
     const int64_t abs_key = (int64_t)a.kv_start + p;
     int64_t r = abs_key;
     if (a.kv_map == 1) {
         r = abs_key % a.ring;
-    } else if (a.kv_map == 2) {
+    } else if (PAGED && a.kv_map == 2) {
         int64_t pg = abs_key / a.page_size;
         pg = pg < a.page_table_len ? pg : a.page_table_len - 1;
         r = (int64_t)a.page_table[pg] * a.page_size + (abs_key - (abs_key / a.page_size) * a.page_size);
@@ -141,26 +151,19 @@ __device__ __forceinline__ void load_block(KVBlock<D> &blk, const uint16_t *kb, 
     const uint16_t *krow = kb + (size_t)rowk * pos_stride + 8 * (lane >> 4);
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) blk.kf[s] = *reinterpret_cast<const h8 *>(krow + 32 * s);
-    if (vrow0 >= 0) {  // wave-uniform
+    // (a select, not a branch: one straight run of loads)
 #pragma unroll
-        for (int n = 0; n < 16; ++n) {
-            const int r = min(vrow0 + n, vrow_last);
-            const _Float16 *vrow = reinterpret_cast<const _Float16 *>(vb + (size_t)r * pos_stride + vlane * DPL);
+    for (int n = 0; n < 16; ++n) {
+        const int r = vrow0 >= 0 ? min(vrow0 + n, vrow_last) : __builtin_amdgcn_readlane(rowk, n);
+        const _Float16 *vrow = reinterpret_cast<const _Float16 *>(vb + (size_t)r * pos_stride + vlane * DPL);
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
-        }
-    } else {
-#pragma unroll
-        for (int n = 0; n < 16; ++n) {
-            const int r = __builtin_amdgcn_readlane(rowk, n);
-            const _Float16 *vrow = reinterpret_cast<const _Float16 *>(vb + (size_t)r * pos_stride + vlane * DPL);
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
-        }
+        for (int d = 0; d < DPL; ++d) blk.vv[n][d] = vrow[d];
     }
 }
 
-template <int D, int G, int W>
+// ONE: every wave owns at most one block (no prefetch of a next block; the
+// query fragments, up to head_dim 256, stay in registers).
+template <int D, int G, int W, bool ONE>
 __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     constexpr int kWaves = W, kThreads = 64 * W;
     constexpr int KSTEPS = D / 32;  // MFMA k-steps over the head dimension
@@ -168,13 +171,16 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     constexpr int VL = v_lanes<D>();         // lanes that own P.V dims
     constexpr int G4 = (G + 3) / 4; // 4-head groups of the probability broadcast
     constexpr float kLog2e = 1.4426950408889634f;
-    // The query fragments are dead once the block loop ends; the wave
-    // combine and the cross-split combine reuse their LDS.
+    // Query fragments (the MFMA A operand) are staged once per workgroup in
+    // LDS; the one-block form up to head_dim 256 then reads them all into
+    // registers at once, before its K/V block arrives.  The wave combine and
+    // the cross-split combine reuse the LDS.
+    constexpr bool QREG = ONE && D <= 256;
     __shared__ union {
         h8 qfrag[2][KSTEPS][64];
         float wo[kWaves][G][D];
     } sm;
-    __shared__ float4 pb[kWaves][17][G4];  // per wave: probabilities [position][head], row 16: max/sum
+    __shared__ float4 pb[kWaves][16][G4];  // per wave: probabilities [position][head]
     __shared__ float wm[kWaves][G], wl[kWaves][G];
 
     // blockIdx.y = kv head * head_groups + group: G query heads per workgroup
@@ -182,7 +188,63 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hq0 = (int)blockIdx.y * G;  // first query head of this group
 
-    int kv_len = a.kv_len_dev ? a.kv_len_dev[0] : a.kv_len;
+    const size_t pos_stride = a.kv_layout == 0 ? (size_t)D : (size_t)a.num_kv_heads * D;
+    const size_t kv_base = a.kv_layout == 0
+                               ? ((size_t)b * a.num_kv_heads + kvh) * a.kv_stride * D
+                               : (size_t)b * a.kv_stride * a.num_kv_heads * D + (size_t)kvh * D;
+    const uint16_t *kb = a.k + kv_base;
+    const uint16_t *vb = a.v + kv_base;
+
+    // Query loads first (vector-memory returns are in order: staging the
+    // query then never waits on the K/V stream).  Fragment s of lane l is
+    // row l % 16 (query head hq0 + l % 16 when < G, else zero), dims 32 s +
+    // 8 (l / 16) .. + 7.  Raw bytes first: no conversion between the loads,
+    // so every query load and the first K/V block are in flight together.
+    // Two 16-byte loads per item whatever the query's type (an f16 query
+    // loads its 16 bytes twice) and, in the one-block form, no branch up to
+    // the K/V loads: the compiler then counts the loads still in flight
+    // exactly, and converting the query waits for the query loads only.
+    constexpr int QITEMS = (KSTEPS * 64 + kThreads - 1) / kThreads;
+    u32x4 qraw[QITEMS][2];
+#pragma unroll
+    for (int it = 0; it < QITEMS; ++it) {
+        const int idx = tid + it * kThreads;
+        const int s = (idx >> 6) % KSTEPS, l = idx & 63, m = l & 15;
+        // rows >= G (and items past the fragment count) read row 0; zeroed below
+        const size_t qi = ((size_t)b * a.num_heads + hq0 + (m < G ? m : 0)) * D + 32 * s + 8 * (l >> 4);
+        const char *q0 = reinterpret_cast<const char *>(a.q) + (a.q_f16 ? 2 * qi : 4 * qi);
+        qraw[it][0] = *reinterpret_cast<const u32x4 *>(q0);
+        qraw[it][1] = *reinterpret_cast<const u32x4 *>(q0 + (a.q_f16 ? 0 : 16));
+    }
+    KVBlock<D> cur;
+    // a contiguous cache (kv_map 0) addresses V rows without lane reads
+    const bool contig = a.kv_map == 0;
+    int blk = 0;
+    if constexpr (ONE) {
+        // The wave's block from the arguments alone: with spec_bps, the fixed
+        // ranges over the whole cache (rows past the visible keys are masked
+        // in the scores and zeroed in V once the device kv_len is known);
+        // else the host kv_len's ranges.  Rows are clamped into [0, kv_stride)
+        // (the host picks this form only for kv_stride >= 1), and a wave past
+        // its split's blocks loads a clamped copy it does not use.
+        int hkl = a.kv_len < 0 ? 0 : a.kv_len;
+        if (a.kv_map == 0 && a.kv_start == 0 && hkl > a.kv_stride) hkl = a.kv_stride;
+        const int hqpos = a.query_at_end ? a.kv_start + hkl - 1 : a.start_pos;
+        const int hkey_hi = !a.causal ? hkl : (hqpos < a.kv_start ? 0 : min(hkl, hqpos - a.kv_start + 1));
+        const int hbps = (((hkey_hi + 15) >> 4) + a.splits - 1) / a.splits;
+        const bool spec = a.spec_bps > 0;
+        blk = spec ? split * a.spec_bps + wave : split * hbps + wave;
+        const int hi_row = spec ? a.kv_stride - 1 : hkey_hi - 1;  // last key a lane may address
+        const int rowk = kv_row<false>(a, min(blk * 16 + (lane & 15), hi_row));
+        const int vlast = max(spec ? a.kv_stride - 1 : min(a.kv_start + hkey_hi - 1, a.kv_stride - 1), 0);
+        const int v0 = contig ? __builtin_amdgcn_readfirstlane(min(a.kv_start + blk * 16, vlast)) : -1;
+        load_block<D>(cur, kb, vb, rowk, pos_stride, lane, v0, vlast);
+    }
+
+    // a scalar load (constant address space): its wait does not include the
+    // K/V loads above
+    int kv_len = a.kv_len_dev ? *(const __attribute__((address_space(4))) int32_t *)a.kv_len_dev
+                              : a.kv_len;
     kv_len = kv_len < 0 ? 0 : kv_len;
     if (a.kv_map == 0 && a.kv_start == 0 && kv_len > a.kv_stride) kv_len = a.kv_stride;
     // visible keys [min_key, key_hi) (attention_head256_f16kv.wgsl:115-131)
@@ -194,50 +256,20 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         min_key = min_abs > a.kv_start ? min(min_abs - a.kv_start, kv_len) : 0;
     }
     const int nblk = (key_hi + 15) >> 4;
-    const int bps = (nblk + a.splits - 1) / a.splits;
+    const int bps = ONE && a.spec_bps > 0 ? a.spec_bps : (nblk + a.splits - 1) / a.splits;
     const int blk_begin = split * bps;
     const int blk_end = min(nblk, blk_begin + bps);
 
-    const size_t pos_stride = a.kv_layout == 0 ? (size_t)D : (size_t)a.num_kv_heads * D;
-    const size_t kv_base = a.kv_layout == 0
-                               ? ((size_t)b * a.num_kv_heads + kvh) * a.kv_stride * D
-                               : (size_t)b * a.kv_stride * a.num_kv_heads * D + (size_t)kvh * D;
-    const uint16_t *kb = a.k + kv_base;
-    const uint16_t *vb = a.v + kv_base;
-
-    // Query fragments (A operand) into LDS: lane l holds row l % 16 (query
-    // head hq0 + l % 16 when < G), dims 32 s + 8 (l / 16) .. + 7.  The query
-    // loads go out before the first K/V block's (vector-memory returns are in
-    // order: staging the query then never waits on the K/V stream).
-    constexpr int QITEMS = (KSTEPS * 64 + kThreads - 1) / kThreads;
-    // raw bytes first: no conversion between the loads, so every query load
-    // and the first K/V block are in flight together
-    u32x4 qraw[QITEMS][2];
-#pragma unroll
-    for (int it = 0; it < QITEMS; ++it) {
-        const int idx = tid + it * kThreads;
-        const int s = (idx >> 6) % KSTEPS, l = idx & 63, m = l & 15;
-        // rows >= G (and items past the fragment count) read row 0; zeroed below
-        const size_t qi = ((size_t)b * a.num_heads + hq0 + (m < G ? m : 0)) * D + 32 * s + 8 * (l >> 4);
-        if (a.q_f16) {
-            qraw[it][0] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const _Float16 *>(a.q) + qi);
-        } else {
-            qraw[it][0] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(a.q) + qi);
-            qraw[it][1] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(a.q) + qi + 4);
-        }
-    }
-    __asm__ volatile("" ::: "memory");
-    KVBlock<D> cur;
-    int blk = blk_begin + wave;
-    // a contiguous cache (kv_map 0) addresses V rows without lane reads
-    const bool contig = a.kv_map == 0;
     const int vrow_last = min(a.kv_start + key_hi - 1, a.kv_stride - 1);
     auto vrow0 = [&](int bk) __attribute__((always_inline)) {
         return contig ? __builtin_amdgcn_readfirstlane(a.kv_start + bk * 16) : -1;
     };
-    if (blk < blk_end)
-        load_block<D>(cur, kb, vb, kv_row(a, min(blk * 16 + (lane & 15), key_hi - 1)), pos_stride, lane, vrow0(blk),
-                      vrow_last);
+    if constexpr (!ONE) {
+        blk = blk_begin + wave;
+        if (blk < blk_end)
+            load_block<D>(cur, kb, vb, kv_row(a, min(blk * 16 + (lane & 15), key_hi - 1)), pos_stride, lane,
+                          vrow0(blk), vrow_last);
+    }
 #pragma unroll
     for (int it = 0; it < QITEMS; ++it) {
         const int idx = tid + it * kThreads;
@@ -267,6 +299,14 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
+    h8 qh[QREG ? KSTEPS : 1], ql[QREG ? KSTEPS : 1];
+    if constexpr (QREG) {
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            qh[s] = sm.qfrag[0][s][lane];
+            if (!a.q_f16) ql[s] = sm.qfrag[1][s][lane];
+        }
+    }
 
     float o[G][DPL];
     float mrow[G], lrow[G];
@@ -280,28 +320,41 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     // running max of the heads whose scores this lane holds (4*(lane/16)+i)
     float mlane[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     const int grp = lane >> 4;
-    float *pbw = reinterpret_cast<float *>(&pb[wave][0][0]);  // [17][G4*4]
+    float *pbw = reinterpret_cast<float *>(&pb[wave][0][0]);  // [16][G4*4]
 
     for (; blk < blk_end; blk += kWaves) {
         // Prefetch the next block of this wave while this one is computed
         // (only when there is one: a wave retires only once its loads are back).
         KVBlock<D> nxt;
-        if (blk + kWaves < blk_end)
+        if (!ONE && blk + kWaves < blk_end)
             load_block<D>(nxt, kb, vb, kv_row(a, min((blk + kWaves) * 16 + (lane & 15), key_hi - 1)), pos_stride,
                           lane, vrow0(blk + kWaves), vrow_last);
 
         const int p0 = blk * 16;
         const int pk = p0 + (lane & 15);
-        f4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+        // two independent accumulation chains (even / odd k-steps)
+        auto qfrag = [&](int part, int s) __attribute__((always_inline)) -> h8 {
+            if constexpr (QREG) return part ? ql[s] : qh[s];
+            else return sm.qfrag[part][s][lane];
+        };
+        f4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0;
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s)
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(sm.qfrag[0][s][lane], cur.kf[s], c, 0, 0, 0);
+        for (int s = 0; s < KSTEPS; ++s) {
+            const h8 qa = qfrag(0, s);
+            if (s & 1) c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c1, 0, 0, 0);
+            else c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c0, 0, 0, 0);
+        }
         if (!a.q_f16) {
 #pragma unroll
-            for (int s = 0; s < KSTEPS; ++s)
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(sm.qfrag[1][s][lane], cur.kf[s], c, 0, 0, 0);
+            for (int s = 0; s < KSTEPS; ++s) {
+                const h8 qa = qfrag(1, s);
+                if (s & 1) c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c1, 0, 0, 0);
+                else c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c0, 0, 0, 0);
+            }
         }
+        const f4 c = c0 + c1;
         const bool valid = pk < key_hi && pk >= min_key;
+        float tsum[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float s = c[i];
@@ -318,24 +371,16 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
             const float bm = m > mlane[i] + kLazyMax ? m : mlane[i];
             mlane[i] = bm;
             const float p = valid ? __builtin_amdgcn_exp2f(sc - bm) : 0.0f;
-            const float t = sum16(p);
+            tsum[i] = sum16(p);
             const int h = 4 * grp + i;
-            if (h < G) {
-                pbw[(lane & 15) * (G4 * 4) + h] = p;
-                if ((lane & 15) == 0) {
-                    pbw[16 * (G4 * 4) + h] = bm;  // new running max of head h
-                }
-                if ((lane & 15) == 1) {
-                    wl[wave][h] = t;  // block probability sum of head h (scratch)
-                }
-            }
+            if (h < G) pbw[(lane & 15) * (G4 * 4) + h] = p;
         }
-        // The wave reads back what its own lanes wrote (LDS ops are ordered
-        // within a wave); every lane gets each head's max and sum.
-        __builtin_amdgcn_wave_barrier();
+        // Head h's running max and block sum are in every lane of 16-lane
+        // row h / 4 (the DPP reductions leave them there): one lane read each.
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            const float mnew = pbw[16 * (G4 * 4) + h];  // the same in every lane
+            const float mnew = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mlane[h & 3]), 16 * (h >> 2)));
+            const float bsum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tsum[h & 3]), 16 * (h >> 2)));
             if (mnew != mrow[h]) {
                 // raised from mrow (-inf before the first valid key: o and l are 0)
                 const float alpha = __builtin_amdgcn_exp2f(mrow[h] - mnew);
@@ -344,22 +389,48 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
                 for (int d = 0; d < DPL; ++d) o[h][d] *= alpha;
             }
-            lrow[h] += wl[wave][h];
+            lrow[h] += bsum;
         }
+        // The wave reads back the probabilities its own lanes wrote (LDS ops
+        // are ordered within a wave).
+        __builtin_amdgcn_wave_barrier();
+        // (after the softmax, which thus overlaps the V loads' arrival)
+        if (p0 + 16 > key_hi) {
+            // the block past the visible keys: its rows there get probability
+            // 0, and their V (never written, in a block loaded before kv_len
+            // was known) is zeroed so that 0 * V stays 0
 #pragma unroll
-        for (int n = 0; n < 16; ++n) {
-            float pv[G4 * 4];
+            for (int n = 0; n < 16; ++n)
+                if (p0 + n >= key_hi)
 #pragma unroll
-            for (int g4 = 0; g4 < G4; ++g4) {
-                const float4 t = pb[wave][n][g4];
-                pv[4 * g4] = t.x; pv[4 * g4 + 1] = t.y; pv[4 * g4 + 2] = t.z; pv[4 * g4 + 3] = t.w;
+                    for (int d = 0; d < DPL; ++d) cur.vv[n][d] = (_Float16)0.0f;
+        }
+        // P.V in batches of CH positions: the batch's probability reads all
+        // go out before its FMAs (one LDS wait per batch)
+        constexpr int CH = G4 == 1 ? 16 : (G4 == 2 ? 8 : 4);
+#pragma unroll
+        for (int n0 = 0; n0 < 16; n0 += CH) {
+            float4 pr[CH][G4];
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+#pragma unroll
+                for (int g4 = 0; g4 < G4; ++g4) pr[c][g4] = pb[wave][n0 + c][g4];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                float pv[G4 * 4];
+#pragma unroll
+                for (int g4 = 0; g4 < G4; ++g4) {
+                    pv[4 * g4] = pr[c][g4].x; pv[4 * g4 + 1] = pr[c][g4].y;
+                    pv[4 * g4 + 2] = pr[c][g4].z; pv[4 * g4 + 3] = pr[c][g4].w;
+                }
+#pragma unroll
+                for (int h = 0; h < G; ++h)
+#pragma unroll
+                    for (int d = 0; d < DPL; ++d) o[h][d] = fmaf(pv[h], (float)cur.vv[n0 + c][d], o[h][d]);
             }
-#pragma unroll
-            for (int h = 0; h < G; ++h)
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) o[h][d] = fmaf(pv[h], (float)cur.vv[n][d], o[h][d]);
         }
         __builtin_amdgcn_wave_barrier();  // pb is rewritten by the next block
+        if constexpr (ONE) break;  // a single block: straight code, no loop
         cur = nxt;
     }
 
@@ -573,9 +644,11 @@ template <int D, int G>
 int launch_g(bool wide, dim3 grid, hipStream_t st, const AttnArgs &a) {
     constexpr int WW = wide_waves(D, G);
     if (wide && WW > 0)
-        hipLaunchKernelGGL((attn_decode_kernel<D, G, (WW > 0 ? WW : 4)>), grid, dim3(64 * WW), 0, st, a);
+        hipLaunchKernelGGL((attn_decode_kernel<D, G, (WW > 0 ? WW : 4), false>), grid, dim3(64 * WW), 0, st, a);
+    else if (a.one_block)
+        hipLaunchKernelGGL((attn_decode_kernel<D, G, 4, true>), grid, dim3(256), 0, st, a);
     else
-        hipLaunchKernelGGL((attn_decode_kernel<D, G, 4>), grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((attn_decode_kernel<D, G, 4, false>), grid, dim3(256), 0, st, a);
     DOE_LAUNCH_CHECK("attn_decode_kernel");
     return DOE_OK;
 }
@@ -738,6 +811,18 @@ int attn_decode_impl(const void *q, int q_f16, const uint16_t *k_cache, const ui
     a.query_at_end = map.query_at_end;
     a.start_pos = map.start_pos;
     a.causal = map.causal;
+    // kv_len on the device over a contiguous cache whose blocks the splits
+    // cover with at most one block per wave: fixed block ranges, so every
+    // wave's K/V loads leave before the kv_len load returns.
+    if (kv_len_dev && plain && !wide) {
+        const int64_t bps = (nblk + splits - 1) / splits;
+        if (bps <= 4) a.spec_bps = (int)bps;
+    }
+    // at most one block per wave: the spec ranges above, or a host kv_len
+    // whose blocks (nblk bounds the kernel's) divide into ranges of <= 4
+    // (not over a paged cache: the one-block form reads no page table)
+    a.one_block = !wide && kv_stride > 0 && map.kv_map != 2 &&
+                  (a.spec_bps > 0 || (!kv_len_dev && (nblk + splits - 1) / splits <= 4));
     if (parts) {
         const int64_t o_count = batch * num_heads * splits * head_dim;
         const int64_t need = o_count + batch * num_heads * splits * 2;
