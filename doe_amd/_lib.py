@@ -53,6 +53,7 @@ SIGNATURES: dict[str, list] = {
     "doe_memcpy_h2d": [_vp, _vp, _sz],
     "doe_memcpy_d2h": [_vp, _vp, _sz],
     "doe_memcpy_d2d": [_vp, _vp, _sz, _vp],
+    "doe_memcpy2d_d2d": [_vp, _sz, _vp, _sz, _sz, _sz, _vp],
     "doe_memset": [_vp, _i32, _sz, _vp],
     "doe_stream_create": [C.POINTER(_vp)],
     "doe_stream_destroy": [_vp],

@@ -188,6 +188,19 @@ int doe_memcpy_d2d(void *dst, const void *src, size_t bytes, doe_stream_t stream
     return DOE_OK;
 }
 
+int doe_memcpy2d_d2d(void *dst, size_t dst_pitch, const void *src, size_t src_pitch, size_t row_bytes,
+                     size_t rows, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    if (row_bytes == 0 || rows == 0) return DOE_OK;
+    DOE_REQUIRE(dst && src, DOE_E_INVALID, "null pointer");
+    DOE_REQUIRE(row_bytes <= dst_pitch && row_bytes <= src_pitch, DOE_E_INVALID,
+                "row of %zu bytes wider than a pitch (dst %zu, src %zu)", row_bytes, dst_pitch, src_pitch);
+    DOE_HIP_CHECK(hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, row_bytes, rows, hipMemcpyDeviceToDevice,
+                                   (hipStream_t)stream));
+    return DOE_OK;
+}
+
 int doe_memset(void *dst, int value, size_t bytes, doe_stream_t stream) {
     int rc = doe::require_init();
     if (rc) return rc;

@@ -494,20 +494,32 @@ class Decoder:
 
     # ---- prompt ----------------------------------------------------------------
     def can_prefill(self) -> bool:
-        """Batched prompts run for uniform Q4_K and Q8_0 models (no per-layer
-        embeddings, shared-KV layers or second head_dim)."""
-        return (self.cfg.weight_format in ("q4k", "q8_0") and not self.ple and len(set(self.head_dims)) == 1
-                and self.kv_sources == tuple(range(self.cfg.layers)))
+        """Batched prompts run for Q4_K and Q8_0 models, per-layer embeddings,
+        shared-KV layers and a second (global) head_dim included."""
+        return self.cfg.weight_format in ("q4k", "q8_0")
 
     def _prefill_buffers(self):
         if getattr(self, "_pf", None) is None:
             c, S = self.cfg, self.cfg.max_seq
             self._pf = {
                 "x": DeviceBuffer.empty((S, c.hidden), np.float32),
-                "qkv": DeviceBuffer.empty((S, c.qkv_rows), np.float32),
-                "att": DeviceBuffer.empty((S, c.q_dim), np.float32),
+                "qkv": DeviceBuffer.empty((S, max(L.qkv_rows for L in self.layers)), np.float32),
+                "att": DeviceBuffer.empty((S, max(L.q_dim for L in self.layers)), np.float32),
                 "h": DeviceBuffer.empty((S, c.ffn), np.float32),
             }
+            if self.ple:
+                P, PD = c.ple_width, c.ple_dim
+                self._pf.update({
+                    "pe": DeviceBuffer.empty((S, PD), np.float32),   # gathered rows
+                    "pp": DeviceBuffer.empty((S, PD), np.float32),   # projected
+                    "pn": DeviceBuffer.empty((S, PD), np.float32),   # normalised per layer
+                    "pu": DeviceBuffer.empty((S, PD), np.float32),   # per-layer inputs [token][layer][P]
+                    "pul": DeviceBuffer.empty((S, P), np.float32),   # one layer's inputs [token][P]
+                    "pg": DeviceBuffer.empty((S, P), np.float32),
+                    "ph": DeviceBuffer.empty((S, P), np.float32),
+                    "py": DeviceBuffer.empty((S, c.hidden), np.float32),
+                    "pyn": DeviceBuffer.empty((S, c.hidden), np.float32),
+                })
         return self._pf
 
     def prefill(self, prompt: np.ndarray, stream=None) -> None:
@@ -527,7 +539,7 @@ class Decoder:
         from .execution import UnsupportedStep
 
         if not self.can_prefill():
-            raise UnsupportedStep("batched prompts need a uniform Q4_K or Q8_0 model")
+            raise UnsupportedStep("batched prompts need Q4_K or Q8_0 projections")
         c = self.cfg
         prompt = np.asarray(prompt, np.int32)
         P = int(prompt.size)
@@ -536,7 +548,6 @@ class Decoder:
         self.reset(prompt)
         self.state.upload(np.array([P - 1, P, P, prompt[-1]], np.int32))
         b = self._prefill_buffers()
-        hd = c.head_dim
         off = c.norm_weight_offset
         ids = self.ids.view(0, P * 4, np.int32)
         ops.embed(self.embed, ids, b["x"], P, c.vocab, c.hidden, c.embed_scale, stream=stream)
@@ -544,20 +555,29 @@ class Decoder:
         # rows interleaved
         fmt = c.weight_format
         gemm = ops.matmul_gemm_f32_fused  # the norms, residuals and GeGLU ride on the GEMMs
+        if self.ple:
+            self._prefill_ple_inputs(ids, P, b, stream)
         for li, L in enumerate(self.layers):
-            gemm(b["x"], L.wqkv, b["qkv"], P, c.qkv_rows, c.hidden, fmt, norm_weight=L.norm_attn, norm_eps=c.eps,
+            hd = L.head_dim
+            # a shared-KV layer writes no cache: its attention reads the cache
+            # its source layer wrote earlier in this pass
+            kvh = 0 if L.shared_kv else c.kv_heads
+            src = self.layers[self.kv_sources[li]]
+            gemm(b["x"], L.wqkv, b["qkv"], P, L.qkv_rows, c.hidden, fmt, norm_weight=L.norm_attn, norm_eps=c.eps,
                  norm_weight_offset=off, stream=stream)
-            ops.qkv_rope_kv_rows(b["qkv"], P, c.qkv_rows, c.heads, c.kv_heads, hd, self.freq_by_layer[li], 0,
-                                 L.k_cache, L.v_cache, c.max_seq, stream=stream)
-            ops.attention_prefill_f16kv(b["qkv"], L.k_cache, L.v_cache, b["att"], num_heads=c.heads,
+            ops.qkv_rope_kv_rows(b["qkv"], P, L.qkv_rows, c.heads, kvh, hd, self.freq_by_layer[li], 0,
+                                 L.k_cache if kvh else None, L.v_cache if kvh else None, c.max_seq, stream=stream)
+            ops.attention_prefill_f16kv(b["qkv"], src.k_cache, src.v_cache, b["att"], num_heads=c.heads,
                                         num_kv_heads=c.kv_heads, head_dim=hd, query_len=P, kv_len=P,
                                         kv_stride=c.max_seq, start_pos=0, scale=1.0 / math.sqrt(hd),
                                         softcap=c.attn_softcap, sliding_window=self.attn_windows[li],
-                                        q_row_stride=c.qkv_rows, stream=stream)
-            gemm(b["att"], L.wo, b["x"], P, c.hidden, c.q_dim, fmt, residual=b["x"], stream=stream)
+                                        q_row_stride=L.qkv_rows, out_row_stride=L.q_dim, stream=stream)
+            gemm(b["att"], L.wo, b["x"], P, c.hidden, L.q_dim, fmt, residual=b["x"], stream=stream)
             gemm(b["x"], L.wgu, b["h"], P, 2 * c.ffn, c.hidden, fmt, norm_weight=L.norm_ffn, norm_eps=c.eps,
                  norm_weight_offset=off, activation=ops.GEGLU_PAIRS, stream=stream)
             gemm(b["h"], L.wd, b["x"], P, c.hidden, c.ffn, fmt, residual=b["x"], stream=stream)
+            if self.ple:
+                self._prefill_ple_block(li, L, P, b, stream)
         last = b["x"].view((P - 1) * c.hidden * 4, c.hidden * 4, np.float32)
         nparts = ops.lm_head_sample(self.lm_head, last, c.vocab, c.hidden, self.argmax_parts,
                                     logits=self.logits if self.keep_logits else None, norm_weight=self.norm_final,
@@ -565,6 +585,33 @@ class Decoder:
         _lib.call("doe_decode_advance", C.c_void_p(self.state.ptr), C.c_void_p(self.token.ptr),
                   C.c_void_p(self.ids.ptr), c.max_seq, C.c_void_p(self.argmax_parts.ptr), nparts,
                   _stream_ptr(stream))
+
+    def _prefill_ple_inputs(self, ids, P: int, b: dict, stream) -> None:
+        """_ple_inputs for the P prompt tokens at once: the gathered rows, the
+        f16 projection of the embeddings as one M = P GEMM, the per-layer
+        RMSNorm over P * layers rows, then (projected + gathered) / sqrt(2)
+        into pu [token][layer][ple_width]."""
+        c = self.cfg
+        W, PD = c.ple_width, c.ple_dim
+        ops.embed(self.ple_table, ids, b["pe"], P, c.ple_vocab or c.vocab, PD, math.sqrt(W), stream=stream)
+        ops.lm_head_gemv(b["x"], self.ple_proj, b["pp"], P, PD, c.hidden, alpha=c.hidden ** -0.5, stream=stream)
+        ops.rmsnorm(b["pp"], self.ple_norm, b["pn"], P * c.layers, W, c.eps, weight_offset=c.norm_weight_offset,
+                    stream=stream)
+        ops.ple_modulate(b["pn"], b["pe"], b["pu"], P * PD, 2.0 ** -0.5, stream=stream)
+
+    def _prefill_ple_block(self, li: int, L: LayerWeights, P: int, b: dict, stream) -> None:
+        """_ple_block for the P prompt rows: x += rmsnorm(W_out . (gelu(W_gate
+        . x) * u)), u the layer's slice of every token's per-layer inputs."""
+        c = self.cfg
+        W, fmt = c.ple_width, c.weight_format
+        ops.copy_rows(b["pul"], W * 4, b["pu"].view(li * W * 4, b["pu"].nbytes - li * W * 4), c.ple_dim * 4,
+                      W * 4, P, stream=stream)
+        ops.matmul_gemm_f32_fused(b["x"], L.w_ple_gate, b["pg"], P, W, c.hidden, fmt, stream=stream)
+        ops.gelu_gated(b["pg"], b["pul"], b["ph"], P * W, stream=stream)
+        ops.matmul_gemm_f32_fused(b["ph"], L.w_ple_out, b["py"], P, c.hidden, W, fmt, stream=stream)
+        ops.rmsnorm(b["py"], L.norm_ple, b["pyn"], P, c.hidden, c.eps, weight_offset=c.norm_weight_offset,
+                    stream=stream)
+        ops.residual(b["pyn"], b["x"], b["x"], P * c.hidden, stream=stream)
 
     # ---- generation ----------------------------------------------------------
     def reset(self, prompt: np.ndarray) -> None:

@@ -530,6 +530,18 @@ def gelu_gated(gate: DeviceBuffer, up: DeviceBuffer, output: DeviceBuffer, n: in
     _lib.call("doe_geglu", _p(gate), _p(up), _p(output), n, _stream_ptr(stream))
 
 
+def copy_rows(dst: DeviceBuffer, dst_pitch: int, src: DeviceBuffer, src_pitch: int, row_bytes: int, rows: int,
+              stream=None) -> None:
+    """``rows`` rows of ``row_bytes`` from ``src`` (rows ``src_pitch`` bytes
+    apart) into ``dst`` (rows ``dst_pitch`` apart), on the device."""
+    if rows and row_bytes:
+        if row_bytes > min(dst_pitch, src_pitch):
+            raise ValueError(f"row of {row_bytes} bytes wider than a pitch ({dst_pitch}, {src_pitch})")
+        _need(dst, (rows - 1) * dst_pitch + row_bytes, "dst")
+        _need(src, (rows - 1) * src_pitch + row_bytes, "src")
+    _lib.call("doe_memcpy2d_d2d", _p(dst), dst_pitch, _p(src), src_pitch, row_bytes, rows, _stream_ptr(stream))
+
+
 def residual(input: DeviceBuffer, residual_in: DeviceBuffer, output: DeviceBuffer, n: int, stream=None) -> None:
     """``residual`` op: input + residual."""
     for buf, role in ((input, "input"), (residual_in, "residual"), (output, "output")):

@@ -61,6 +61,12 @@ int doe_free(void *ptr);
 int doe_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int doe_memcpy_d2h(void *dst, const void *src, size_t bytes);
 int doe_memcpy_d2d(void *dst, const void *src, size_t bytes, doe_stream_t stream);
+/* `rows` rows of `row_bytes` from src (rows `src_pitch` bytes apart) to dst
+ * (rows `dst_pitch` apart), device to device, on `stream`.  No counterpart
+ * in the reference: the decoder's batched prompt takes each layer's slice
+ * of the per-layer inputs with it. */
+int doe_memcpy2d_d2d(void *dst, size_t dst_pitch, const void *src, size_t src_pitch, size_t row_bytes,
+                     size_t rows, doe_stream_t stream);
 int doe_memset(void *dst, int value, size_t bytes, doe_stream_t stream);
 
 /* ---- streams, events, graphs -----------------------------------------------

@@ -372,6 +372,27 @@ def test_gemma4_e2b_graph_replay_equals_eager(dev):
     assert out.tolist() == eager.tolist()
 
 
+def test_gemma4_e2b_prefill_matches_oracle_decoder(dev, ora):
+    # the E2B-class graph's prompt as one batched pass: the per-layer inputs
+    # of all prompt tokens at once (gather, one M-row f16 projection, the
+    # per-layer norm, modulate), global layers at head_dim 512, shared-KV
+    # layers attending over the cache their source layer wrote earlier in the
+    # pass, each layer's per-layer input block over the prompt rows; the last
+    # token's logits against the oracle decoder stepped token by token, then
+    # decode steps on the prompt's caches.  The 12-token prompt runs past the
+    # 8-key window.
+    cfg, plan = _e2b_small()
+    dec = Decoder(cfg, keep_logits=True, plan=plan)
+    dec.init_random(seed=14)
+    assert dec.can_prefill()
+    s = Stream()
+    oracle = OracleDecoder(dec)
+    prompt = np.array([7, 4000, 123, 123, 2048, 9, 3001, 77, 5, 1024, 64, 4095], np.int32)
+    errs = _prefill_then_decode(dec, oracle, prompt, 4, s)
+    print(f"[prefill e2b] logits rel_l2 {['%.1e' % e for e in errs]}", flush=True)
+    assert max(errs) <= 1e-3
+
+
 def _gemma4_31b(name, layers, vocab=32768):
     """A reference Gemma 4 31B step graph (gemma-4-31b-smoke.json: 32 heads
     x 160, one kv head per query head, hidden 5120, FFN 20480, per-layer
