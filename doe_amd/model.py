@@ -65,6 +65,9 @@ class DecoderConfig:
     rope_base_global: float = 0.0
     ple_width: int = 0
     ple_vocab: int = 0
+    # the per-layer model projection's weights: "q4k" (Q4_K_M rows, as the
+    # reference's E2B artifact stores per_layer_model_projection) or "f16"
+    ple_proj_format: str = "q4k"
 
     @property
     def q_dim(self) -> int:
@@ -245,7 +248,12 @@ class Decoder:
         if self.ple:
             P, PD = c.ple_width, c.ple_dim
             self.ple_table = DeviceBuffer.empty((c.ple_vocab or c.vocab, PD), np.float16)
-            self.ple_proj = DeviceBuffer.empty((PD, c.hidden), np.float16)
+            if c.ple_proj_format == "q4k":
+                self.ple_proj = DeviceBuffer(PD * _q4k.row_bytes(c.hidden))
+            elif c.ple_proj_format == "f16":
+                self.ple_proj = DeviceBuffer.empty((PD, c.hidden), np.float16)
+            else:
+                raise ValueError(f"ple_proj_format {c.ple_proj_format!r} is not q4k or f16")
             self.ple_norm = DeviceBuffer.empty((P,), np.float32)
             self.ple_e = DeviceBuffer.empty((PD,), np.float32)   # gathered rows
             self.ple_p = DeviceBuffer.empty((PD,), np.float32)   # projected
@@ -327,7 +335,11 @@ class Decoder:
         nrm(self.norm_final, 9, 0.1, mean=nmean)
         if self.ple:
             nrm(self.ple_table, 13, 0.02, True)
-            nrm(self.ple_proj, 14, 0.02, True)
+            if c.ple_proj_format == "q4k":
+                _lib.call("doe_fill_random_q4k", C.c_void_p(self.ple_proj.ptr),
+                          self.ple_proj.nbytes // _q4k.BLOCK_BYTES, s + 14, 0.02, 0.01, sp)
+            else:
+                nrm(self.ple_proj, 14, 0.02, True)
             nrm(self.ple_norm, 15, 0.1, mean=nmean)
 
     # ---- one decode step -------------------------------------------------------
@@ -449,10 +461,30 @@ class Decoder:
         P, PD = c.ple_width, c.ple_dim
         ops.embed(self.ple_table, self.tok_view, self.ple_e, 1, c.ple_vocab or c.vocab, PD, math.sqrt(P),
                   stream=stream)
-        ops.lm_head(self.ple_proj, self.x, self.ple_p, PD, c.hidden, alpha=c.hidden ** -0.5, stream=stream)
-        ops.rmsnorm(self.ple_p, self.ple_norm, self.ple_pn, c.layers, P, c.eps,
+        self._ple_project(self.x, self.ple_p, 1, stream)
+        ops.rmsnorm(self.ple_p, self.ple_norm, self.ple_pn, c.layers, P, self._ple_norm_eps(),
                     weight_offset=c.norm_weight_offset, stream=stream)
         ops.ple_modulate(self.ple_pn, self.ple_e, self.ple_u, PD, 2.0 ** -0.5, stream=stream)
+
+    def _ple_project(self, x, out, rows: int, stream) -> None:
+        """The ple_project step over `rows` embedding rows: W_proj x, scaled
+        by hidden^-1/2 (the f16 form) or left unscaled for the per-layer
+        RMSNorm to absorb (the Q4_K form: rmsnorm(a p, eps) = rmsnorm(p,
+        eps / a^2), _ple_norm_eps)."""
+        c = self.cfg
+        if c.ple_proj_format == "q4k":
+            if rows == 1:
+                ops.matmul_q4k(self.ple_proj, x, out, c.ple_dim, c.hidden, stream)
+            else:
+                ops.matmul_gemm_f32_fused(x, self.ple_proj, out, rows, c.ple_dim, c.hidden, "q4k", stream=stream)
+        elif rows == 1:
+            ops.lm_head(self.ple_proj, x, out, c.ple_dim, c.hidden, alpha=c.hidden ** -0.5, stream=stream)
+        else:
+            ops.lm_head_gemv(x, self.ple_proj, out, rows, c.ple_dim, c.hidden, alpha=c.hidden ** -0.5, stream=stream)
+
+    def _ple_norm_eps(self) -> float:
+        c = self.cfg
+        return c.eps * c.hidden if c.ple_proj_format == "q4k" else c.eps
 
     def _ple_block(self, li: int, L: LayerWeights, stream) -> None:
         """A layer's use of its per-layer input u (after ffn_residual): x +=
@@ -594,8 +626,9 @@ class Decoder:
         c = self.cfg
         W, PD = c.ple_width, c.ple_dim
         ops.embed(self.ple_table, ids, b["pe"], P, c.ple_vocab or c.vocab, PD, math.sqrt(W), stream=stream)
-        ops.lm_head_gemv(b["x"], self.ple_proj, b["pp"], P, PD, c.hidden, alpha=c.hidden ** -0.5, stream=stream)
-        ops.rmsnorm(b["pp"], self.ple_norm, b["pn"], P * c.layers, W, c.eps, weight_offset=c.norm_weight_offset,
+        self._ple_project(b["x"], b["pp"], P, stream)
+        ops.rmsnorm(b["pp"], self.ple_norm, b["pn"], P * c.layers, W, self._ple_norm_eps(),
+                    weight_offset=c.norm_weight_offset,
                     stream=stream)
         ops.ple_modulate(b["pn"], b["pe"], b["pu"], P * PD, 2.0 ** -0.5, stream=stream)
 

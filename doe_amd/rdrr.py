@@ -42,6 +42,15 @@ def weight_key_candidates(key: str) -> list[str]:
         return ["model.language_model.norm.weight", "model.norm.weight", "norm.weight"]
     if key == "embed_tokens":
         return ["model.language_model.embed_tokens.weight", "model.embed_tokens.weight", "embed_tokens.weight"]
+    # the per-layer-embedding weights (gemma-4-e2b-smoke.json weightsKey
+    # per_layer_inputs.*; tensor names of the reference's E2B artifact,
+    # config/gemma-4-e2b-doppler-rdrr-int4ple-fixture.json:34,140)
+    if key == "per_layer_inputs.embedTokensPerLayer":
+        return ["model.language_model.embed_tokens_per_layer.weight", "model.embed_tokens_per_layer.weight"]
+    if key == "per_layer_inputs.perLayerModelProjection":
+        return ["model.language_model.per_layer_model_projection.weight", "model.per_layer_model_projection.weight"]
+    if key == "per_layer_inputs.perLayerProjectionNorm":
+        return ["model.language_model.per_layer_projection_norm.weight", "model.per_layer_projection_norm.weight"]
     if key == "lm_head":  # a tied head falls back to the embedding
         return ["model.language_model.lm_head.weight", "language_model.lm_head.weight", "model.lm_head.weight",
                 "lm_head.weight"] + weight_key_candidates("embed_tokens")
@@ -212,34 +221,60 @@ def load_decoder_weights(art: RdrrArtifact, dec) -> None:
     interleaved; norms and the f16 embedding / lm_head are
     uploaded as they are (BF16 or F32 sources converted to the decoder's
     dtype).  input_layernorm feeds attention, post_attention_layernorm the
-    FFN (the step graph's post_attn_norm before gate_proj)."""
-    c = dec.cfg
-    if dec.ple or len(set(dec.head_dims)) > 1 or dec.kv_sources != tuple(range(c.layers)):
-        from .execution import UnsupportedStep
+    FFN (the step graph's post_attn_norm before gate_proj;
+    int4ple_runtime_weight_mappings.py:136-153).
 
-        raise UnsupportedStep("loading per-layer embeddings, shared-KV layers or a global head_dim from RDRR")
+    Per layer the decoder's plan decides the shapes: a global layer's
+    head_dim, and a shared-KV layer takes only its q_proj (its attention reads
+    an earlier layer's cache; the artifact's k/v tensors of such a layer are
+    not read).  With per-layer embeddings the table
+    (embed_tokens_per_layer, F16), the model projection
+    (per_layer_model_projection, Q4_K_M rows, or F16 for an f16-projection
+    decoder), its norm, and every layer's per_layer_input_gate,
+    per_layer_projection and post_per_layer_input_norm load too (the tensor
+    names of config/gemma-4-e2b-doppler-rdrr-int4ple-fixture.json)."""
+    c = dec.cfg
     q8 = c.weight_format == "q8_0"
-    rb_h, rb_q, rb_f = c.row_bytes(c.hidden), c.row_bytes(c.q_dim), c.row_bytes(c.ffn)
+    rb_h, rb_f = c.row_bytes(c.hidden), c.row_bytes(c.ffn)
     for i, L in enumerate(dec.layers):
         def rows(key, shape):
             name = art.resolve(f"layer.{i}.{key}")
             return _expect(art.q8_0_rows(name) if q8 else art.q4k_rows(name), shape, key)
 
-        q = rows("self_attn.q_proj", (c.q_dim, rb_h))
-        k = rows("self_attn.k_proj", (c.kv_dim, rb_h))
-        v = rows("self_attn.v_proj", (c.kv_dim, rb_h))
+        def vec(key):
+            return _expect(art.dense(art.resolve(f"layer.{i}.{key}"), np.float32), (c.hidden,), key)
+
+        hd = L.head_dim
         # the fused q/k/v kernels rotate interleaved pairs
-        q, k = interleave_rope_rows(q, c.head_dim), interleave_rope_rows(k, c.head_dim)
-        L.wqkv.upload(np.concatenate([q, k, v]))
-        L.wo.upload(rows("self_attn.o_proj", (c.hidden, rb_q)))
+        parts = [interleave_rope_rows(rows("self_attn.q_proj", (L.q_dim, rb_h)), hd)]
+        if L.kv_dim:
+            parts.append(interleave_rope_rows(rows("self_attn.k_proj", (L.kv_dim, rb_h)), hd))
+            parts.append(rows("self_attn.v_proj", (L.kv_dim, rb_h)))
+        L.wqkv.upload(np.concatenate(parts))
+        L.wo.upload(rows("self_attn.o_proj", (c.hidden, c.row_bytes(L.q_dim))))
         gate = rows("mlp.gate_proj", (c.ffn, rb_h))
         up = rows("mlp.up_proj", (c.ffn, rb_h))
         gu = np.empty((2 * c.ffn, rb_h), np.uint8)
         gu[0::2], gu[1::2] = gate, up
         L.wgu.upload(gu)
         L.wd.upload(rows("mlp.down_proj", (c.hidden, rb_f)))
-        for key, buf in (("input_layernorm", L.norm_attn), ("post_attention_layernorm", L.norm_ffn)):
-            buf.upload(_expect(art.dense(art.resolve(f"layer.{i}.{key}"), np.float32), (c.hidden,), key))
+        L.norm_attn.upload(vec("input_layernorm"))
+        L.norm_ffn.upload(vec("post_attention_layernorm"))
+        if dec.ple:
+            L.w_ple_gate.upload(rows("per_layer_input_gate", (c.ple_width, rb_h)))
+            L.w_ple_out.upload(rows("per_layer_projection", (c.hidden, c.row_bytes(c.ple_width))))
+            L.norm_ple.upload(vec("post_per_layer_input_norm"))
+    if dec.ple:
+        PD = c.ple_dim
+        dec.ple_table.upload(_expect(art.dense(art.resolve("per_layer_inputs.embedTokensPerLayer"), np.float16),
+                                     (c.ple_vocab or c.vocab, PD), "embed_tokens_per_layer"))
+        proj = art.resolve("per_layer_inputs.perLayerModelProjection")
+        if c.ple_proj_format == "q4k":
+            dec.ple_proj.upload(_expect(art.q4k_rows(proj), (PD, _q4k.row_bytes(c.hidden)), "per_layer_model_projection"))
+        else:
+            dec.ple_proj.upload(_expect(art.dense(proj, np.float16), (PD, c.hidden), "per_layer_model_projection"))
+        dec.ple_norm.upload(_expect(art.dense(art.resolve("per_layer_inputs.perLayerProjectionNorm"), np.float32),
+                                    (c.ple_width,), "per_layer_projection_norm"))
     dec.embed.upload(_expect(art.dense(art.resolve("embed_tokens"), np.float16), (c.vocab, c.hidden), "embed_tokens"))
     dec.lm_head.upload(_expect(art.dense(art.resolve("lm_head"), np.float16), (c.vocab, c.hidden), "lm_head"))
     dec.norm_final.upload(_expect(art.dense(art.resolve("norm"), np.float32), (c.hidden,), "norm"))

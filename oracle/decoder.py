@@ -12,6 +12,36 @@ import numpy as np
 from . import oracle as ora
 
 
+def ple_inputs(table: np.ndarray, proj: np.ndarray, norm_w: np.ndarray, token: int, x: np.ndarray, layers: int,
+               width: int, hidden: int, eps: float, norm_offset: bool) -> np.ndarray:
+    """Per-layer inputs [layers][width] of one token
+    (bench/tools/run_gemma4_e2b_manifest_shape_execution.py:383-404,
+    compute_per_layer_inputs): (rmsnorm_width(proj x / sqrt(hidden)) +
+    sqrt(width) table[token]) / sqrt(2), each step an oracle function (the
+    final combine one f32 add and one f32 multiply, as the kernel).  proj:
+    f16 [layers * width][hidden], or Q4_K rows (uint8) whose product is
+    scaled by hidden^-1/2 after the GEMV."""
+    e = ora.embed_gather(table, np.array([token], np.int32), math.sqrt(width))[0]
+    if proj.dtype == np.uint8:
+        p = ora.q4k_gemv(proj, x, layers * width, hidden) * np.float32(hidden ** -0.5)
+    else:
+        p = ora.f16_gemv(proj, x, hidden ** -0.5)
+    pn = ora.rmsnorm(p.reshape(layers, width), norm_w, eps, norm_offset).reshape(-1)
+    u = np.add(pn, e, dtype=np.float32) * np.float32(2.0 ** -0.5)
+    return u.astype(np.float32).reshape(layers, width)
+
+
+def ple_block(w_gate: np.ndarray, w_out: np.ndarray, norm_w: np.ndarray, x: np.ndarray, u: np.ndarray, width: int,
+              hidden: int, eps: float, norm_offset: bool) -> np.ndarray:
+    """A layer's per-layer input block on the residual stream x
+    (run_gemma4_e2b_manifest_shape_execution.py:358-367, the end of
+    execute_layer, at layer_scalar 1): x + rmsnorm(W_out (gelu_tanh(W_gate
+    x) * u)), W_gate and W_out Q4_K rows."""
+    g = ora.q4k_gemv(w_gate, x, width, hidden)
+    y = ora.q4k_gemv(w_out, ora.geglu(g, u), hidden, width)
+    return ora.residual(ora.rmsnorm(y, norm_w, eps, norm_offset), x)
+
+
 def plain_rows_from_rotation_pairs(rows: np.ndarray, head_dim: int) -> np.ndarray:
     """The device holds each head's q/k projection rows as rotation pairs:
     row 2i of a head is dimension i, row 2i + 1 is dimension i + head_dim/2.
@@ -108,16 +138,9 @@ class OracleDecoder:
         return self._f16w[key]
 
     def ple_inputs(self, token: int, x: np.ndarray) -> np.ndarray:
-        """Per-layer inputs [layers][P]: (rmsnorm_P(W_proj x / sqrt(hidden)) +
-        sqrt(P) table[token]) / sqrt(2), each step an oracle function (the
-        final combine one f32 add and one f32 multiply, as the kernel)."""
         c = self.cfg
-        P = c.ple_width
-        e = ora.embed_gather(self.ple_table, np.array([token], np.int32), math.sqrt(P))[0]
-        p = ora.f16_gemv(self.ple_proj, x, c.hidden ** -0.5)
-        pn = ora.rmsnorm(p.reshape(c.layers, P), self.ple_norm, c.eps, c.norm_weight_offset).reshape(-1)
-        u = np.add(pn, e, dtype=np.float32) * np.float32(2.0 ** -0.5)
-        return u.astype(np.float32).reshape(c.layers, P)
+        return ple_inputs(self.ple_table, self.ple_proj, self.ple_norm, token, x, c.layers, c.ple_width, c.hidden,
+                          c.eps, c.norm_weight_offset)
 
     def step(self, pos: int, token: int, f16_operands: bool = False, f16_probs: bool = False) -> np.ndarray:
         """One decode step.  Models of the batched prompt's precision (for a
@@ -163,8 +186,7 @@ class OracleDecoder:
             h = ora.geglu(gu[0::2], gu[1::2])  # interleaved gate/up rows
             x = ora.residual(self.gemv(L["wd"], h, c.hidden, c.ffn), x)
             if u is not None:
-                g = ora.q4k_gemv(L["w_ple_gate"], x, c.ple_width, c.hidden)
-                y = ora.q4k_gemv(L["w_ple_out"], ora.geglu(g, u[li]), c.hidden, c.ple_width)
-                x = ora.residual(ora.rmsnorm(y, L["n_ple"], c.eps, off), x)
+                x = ple_block(L["w_ple_gate"], L["w_ple_out"], L["n_ple"], x, u[li], c.ple_width, c.hidden, c.eps,
+                              off)
         xn = ora.rmsnorm(x, self.nf, c.eps, off)
         return ora.f16_gemv(self.lm_head, xn)

@@ -240,12 +240,14 @@ def _write_rdrr(dec, root):
 
     for i, L in enumerate(dec.layers):
         p = f"model.layers.{i}"
-        wqkv = L.wqkv.download().reshape(c.qkv_rows, rb(c.hidden))
-        q, k, v = wqkv[:c.q_dim], wqkv[c.q_dim:c.q_dim + c.kv_dim], wqkv[c.q_dim + c.kv_dim:]
-        put(f"{p}.self_attn.q_proj.weight", plain(q, c.head_dim), wdt, (c.q_dim, c.hidden), "row")
-        put(f"{p}.self_attn.k_proj.weight", plain(k, c.head_dim), wdt, (c.kv_dim, c.hidden), "row")
-        put(f"{p}.self_attn.v_proj.weight", v, wdt, (c.kv_dim, c.hidden), "row")
-        put(f"{p}.self_attn.o_proj.weight", L.wo.download(), wdt, (c.hidden, c.q_dim), "row")
+        hd, qd, kd = L.head_dim, L.q_dim, L.kv_dim
+        wqkv = L.wqkv.download().reshape(L.qkv_rows, rb(c.hidden))
+        q, k, v = wqkv[:qd], wqkv[qd:qd + kd], wqkv[qd + kd:]
+        put(f"{p}.self_attn.q_proj.weight", plain(q, hd), wdt, (qd, c.hidden), "row")
+        if kd:  # a shared-KV layer holds only its q rows
+            put(f"{p}.self_attn.k_proj.weight", plain(k, hd), wdt, (kd, c.hidden), "row")
+            put(f"{p}.self_attn.v_proj.weight", v, wdt, (kd, c.hidden), "row")
+        put(f"{p}.self_attn.o_proj.weight", L.wo.download(), wdt, (c.hidden, qd), "row")
         gu = L.wgu.download().reshape(2 * c.ffn, rb(c.hidden))
         gate, up = gu[0::2], gu[1::2]
         put(f"{p}.mlp.gate_proj.weight", gate, wdt, (c.ffn, c.hidden), "row")
@@ -253,6 +255,17 @@ def _write_rdrr(dec, root):
         put(f"{p}.mlp.down_proj.weight", L.wd.download(), wdt, (c.hidden, c.ffn), "row", split=(i == 1))
         put(f"{p}.input_layernorm.weight", L.norm_attn.download(), "F32", (c.hidden,))
         put(f"{p}.post_attention_layernorm.weight", L.norm_ffn.download(), "F32", (c.hidden,))
+        if dec.ple:
+            put(f"{p}.per_layer_input_gate.weight", L.w_ple_gate.download(), wdt, (c.ple_width, c.hidden), "row")
+            put(f"{p}.per_layer_projection.weight", L.w_ple_out.download(), wdt, (c.hidden, c.ple_width), "row")
+            put(f"{p}.post_per_layer_input_norm.weight", L.norm_ple.download(), "F32", (c.hidden,))
+    if dec.ple:
+        lp = "model.language_model"
+        put(f"{lp}.embed_tokens_per_layer.weight", dec.ple_table.download(), "F16",
+            (c.ple_vocab or c.vocab, c.ple_dim), split=True)
+        put(f"{lp}.per_layer_model_projection.weight", dec.ple_proj.download(), "Q4_K_M", (c.ple_dim, c.hidden),
+            "row")
+        put(f"{lp}.per_layer_projection_norm.weight", dec.ple_norm.download(), "F32", (c.ple_width,))
     put("model.embed_tokens.weight", dec.embed.download(), "F16", (c.vocab, c.hidden))
     put("lm_head.weight", dec.lm_head.download(), "F16", (c.vocab, c.hidden), split=True)
     put("model.norm.weight", dec.norm_final.download(), "F32", (c.hidden,))
@@ -290,6 +303,39 @@ def test_rdrr_artifact_loads_byte_identical(dev, tmp_path, fmt):
             d.step(s)
     s.synchronize()
     assert rel_l2(dst.logits.download(), src.logits.download()) <= 1e-6
+    assert src.ids.download()[:7].tolist() == dst.ids.download()[:7].tolist()
+
+
+def test_rdrr_e2b_artifact_loads_byte_identical(dev, tmp_path):
+    # an E2B-class artifact (the reference artifact's tensor names: per-layer
+    # embedding table, Q4_K_M model projection and its norm, each layer's
+    # per_layer_input_gate / per_layer_projection / post_per_layer_input_norm;
+    # global layers at head_dim 512, shared-KV layers holding only q_proj)
+    # loads byte for byte, and the loaded decoder decodes the same tokens
+    from doe_amd import rdrr
+
+    cfg, plan = _e2b_small()
+    src = Decoder(cfg, keep_logits=True, plan=plan)
+    src.init_random(seed=16)
+    _write_rdrr(src, tmp_path)
+    dst = Decoder(cfg, keep_logits=True, plan=plan)
+    rdrr.load_decoder_weights(rdrr.RdrrArtifact(tmp_path), dst)
+    pairs = [(src.embed, dst.embed), (src.lm_head, dst.lm_head), (src.norm_final, dst.norm_final),
+             (src.ple_table, dst.ple_table), (src.ple_proj, dst.ple_proj), (src.ple_norm, dst.ple_norm)]
+    for a, b in zip(src.layers, dst.layers):
+        pairs += [(a.wqkv, b.wqkv), (a.wo, b.wo), (a.wgu, b.wgu), (a.wd, b.wd), (a.norm_attn, b.norm_attn),
+                  (a.norm_ffn, b.norm_ffn), (a.w_ple_gate, b.w_ple_gate), (a.w_ple_out, b.w_ple_out),
+                  (a.norm_ple, b.norm_ple)]
+    for a, b in pairs:
+        assert a.download().tobytes() == b.download().tobytes()
+    s = Stream()
+    prompt = np.array([3, 1000, 7], np.int32)
+    for d in (src, dst):
+        d.reset(prompt)
+        for _ in range(4):
+            d.step(s)
+    s.synchronize()
+    assert dst.logits.download().tobytes() == src.logits.download().tobytes()
     assert src.ids.download()[:7].tolist() == dst.ids.download()[:7].tolist()
 
 

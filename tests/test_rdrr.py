@@ -125,3 +125,18 @@ def test_weight_keys_resolve_to_tensor_names(tmp_path):
     assert art.resolve("lm_head") == "model.embed_tokens.weight"
     with pytest.raises(KeyError, match="norm"):
         art.resolve("norm")
+
+
+def test_per_layer_embedding_keys_resolve_to_the_reference_names():
+    # gemma-4-e2b-smoke.json's per_layer_inputs.* weight keys and the
+    # per-layer block's tensors, named as in the reference's E2B artifact
+    # (config/gemma-4-e2b-doppler-rdrr-int4ple-fixture.json:34,116-140)
+    lp = "model.language_model"
+    assert rdrr.weight_key_candidates("per_layer_inputs.embedTokensPerLayer")[0] == \
+        f"{lp}.embed_tokens_per_layer.weight"
+    assert rdrr.weight_key_candidates("per_layer_inputs.perLayerModelProjection")[0] == \
+        f"{lp}.per_layer_model_projection.weight"
+    assert rdrr.weight_key_candidates("per_layer_inputs.perLayerProjectionNorm")[0] == \
+        f"{lp}.per_layer_projection_norm.weight"
+    for tail in ("per_layer_input_gate", "per_layer_projection", "post_per_layer_input_norm"):
+        assert rdrr.weight_key_candidates(f"layer.0.{tail}")[0] == f"{lp}.layers.0.{tail}.weight"
