@@ -290,7 +290,7 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder", cpu_r
     parity, cpu = decode_parity_and_cpu(dec, prompt, s, cpu_runs)
     tok_s = args.decode_steps / timing["decode_s"]
     mean_len = args.prompt_len + (args.decode_steps + 1) / 2.0
-    bpt = cfg.decode_bytes_per_token(mean_len)
+    bpt = dec.decode_bytes_per_token(mean_len)
     gbs = bpt * tok_s / 1e9
     prompt_mode = "one batched prefill pass" if pf else f"{args.prompt_len - 1} teacher-forced decode steps"
     log(f"decode ({label}): {tok_s:.1f} tok/s ({timing['decode_s'] * 1e3 / args.decode_steps:.3f} ms/token), "

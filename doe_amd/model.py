@@ -63,6 +63,9 @@ class DecoderConfig:
     # table rows of the per-layer embeddings (0: none; rows 0: vocab)
     global_head_dim: int = 0
     rope_base_global: float = 0.0
+    # KV heads of global-attention layers (modelConfig numGlobalKeyValueHeads,
+    # gemma-4-31b-af16-smoke.json:9); 0: kv_heads
+    global_kv_heads: int = 0
     ple_width: int = 0
     ple_vocab: int = 0
     # the per-layer model projection's weights: "q4k" (Q4_K_M rows, as the
@@ -103,7 +106,8 @@ class DecoderConfig:
     def from_model_config(cls, mc: dict, **overrides) -> "DecoderConfig":
         """From a step graph's modelConfig (hiddenDim, numHeads, headDim,
         numKeyValueHeads, numLayers, vocabSize, maxSeqLen, ffnExpansionFactor,
-        globalHeadDim, pleWidth, pleVocabSize); quantFormat q4k or q8_0
+        globalHeadDim, numGlobalKeyValueHeads, pleWidth, pleVocabSize);
+        quantFormat q4k or q8_0
         (f16 is not supported)."""
         from .execution import UnsupportedStep
 
@@ -116,7 +120,8 @@ class DecoderConfig:
         kw = dict(layers=mc["numLayers"], hidden=mc["hiddenDim"], heads=mc["numHeads"],
                   kv_heads=mc.get("numKeyValueHeads") or mc["numHeads"], head_dim=mc["headDim"], vocab=mc["vocabSize"],
                   ffn=mc["hiddenDim"] * mc.get("ffnExpansionFactor", 4), weight_format=fmt,
-                  global_head_dim=mc.get("globalHeadDim") or 0, ple_width=mc.get("pleWidth") or 0,
+                  global_head_dim=mc.get("globalHeadDim") or 0,
+                  global_kv_heads=mc.get("numGlobalKeyValueHeads") or 0, ple_width=mc.get("pleWidth") or 0,
                   ple_vocab=mc.get("pleVocabSize") or 0)
         if "maxSeqLen" in mc:
             kw["max_seq"] = mc["maxSeqLen"]
@@ -144,15 +149,17 @@ def rope_table(max_pos: int, head_dim: int, base: float) -> np.ndarray:
 
 
 class LayerWeights:
-    def __init__(self, cfg: DecoderConfig, head_dim: int | None = None, shared_kv: bool = False):
-        """head_dim: this layer's (a global layer's may differ); shared_kv: the
-        layer projects q only and its attention reads an earlier layer's cache,
-        so it has no k/v rows and no cache of its own."""
+    def __init__(self, cfg: DecoderConfig, head_dim: int | None = None, shared_kv: bool = False,
+                 kv_heads: int | None = None):
+        """head_dim, kv_heads: this layer's (a global layer's may differ);
+        shared_kv: the layer projects q only and its attention reads an
+        earlier layer's cache, so it has no k/v rows and no cache of its own."""
         rb = cfg.row_bytes
         self.head_dim = hd = head_dim or cfg.head_dim
+        self.kv_heads = kv_heads or cfg.kv_heads
         self.shared_kv = shared_kv
         self.q_dim = cfg.heads * hd
-        self.kv_dim = 0 if shared_kv else cfg.kv_heads * hd
+        self.kv_dim = 0 if shared_kv else self.kv_heads * hd
         self.qkv_rows = self.q_dim + 2 * self.kv_dim
         # q/k rows as interleaved rotation pairs, gate/up rows interleaved
         # (gate_0, up_0, gate_1, ...) for the fused kernels (Q4_K and Q8_0)
@@ -164,8 +171,8 @@ class LayerWeights:
         self.norm_ffn = DeviceBuffer.empty((cfg.hidden,), np.float32)
         self.k_cache = self.v_cache = None
         if not shared_kv:
-            self.k_cache = DeviceBuffer.empty((cfg.kv_heads, cfg.max_seq, hd), np.float16)
-            self.v_cache = DeviceBuffer.empty((cfg.kv_heads, cfg.max_seq, hd), np.float16)
+            self.k_cache = DeviceBuffer.empty((self.kv_heads, cfg.max_seq, hd), np.float16)
+            self.v_cache = DeviceBuffer.empty((self.kv_heads, cfg.max_seq, hd), np.float16)
         if cfg.ple_width:
             # the per-layer input block: gate [P][hidden], projection [hidden][P]
             # (Q4_K) and the norm of the projection
@@ -224,7 +231,14 @@ class Decoder:
         gemma4 = self.ple or any(s != li for li, s in enumerate(self.kv_sources)) or len(set(self.head_dims)) > 1
         if gemma4 and c.weight_format != "q4k":
             raise UnsupportedStep("per-layer embeddings, shared-KV layers and a global head_dim need q4k weights")
-        self.layers = [LayerWeights(c, self.head_dims[li], self.kv_sources[li] != li) for li in range(L)]
+        # a global-attention layer's KV heads (numGlobalKeyValueHeads)
+        self.kv_heads = tuple((c.global_kv_heads or c.kv_heads) if self.attn_windows[li] == 0 else c.kv_heads
+                              for li in range(L))
+        for li, s in enumerate(self.kv_sources):
+            if self.kv_heads[s] != self.kv_heads[li]:
+                raise ValueError(f"layer {li} reads the cache of layer {s}, which has other KV heads")
+        self.layers = [LayerWeights(c, self.head_dims[li], self.kv_sources[li] != li, self.kv_heads[li])
+                       for li in range(L)]
         self.embed = DeviceBuffer.empty((c.vocab, c.hidden), np.float16)
         self.lm_head = DeviceBuffer.empty((c.vocab, c.hidden), np.float16)
         self.norm_final = DeviceBuffer.empty((c.hidden,), np.float32)
@@ -292,6 +306,22 @@ class Decoder:
         self.pos_view = self.state.view(0, 4, np.int32)
         self.kvlen_view = self.state.view(4, 4, np.int32)
         self.tok_view = self.state.view(12, 4, np.int32)
+
+    def decode_bytes_per_token(self, kv_len: float) -> float:
+        """Algorithmic HBM bytes of one decode step of this decoder: every
+        layer's weights once (its own head width and KV heads), the K and V
+        rows each layer's attention reads (a sliding layer at most its
+        window), the lm_head, the embedding row and, with per-layer
+        embeddings, the table row and the model projection."""
+        c = self.cfg
+        b = sum(L.weight_bytes() for L in self.layers) + c.vocab * c.hidden * 2 + c.hidden * 2
+        for li, L in enumerate(self.layers):
+            w = self.attn_windows[li]
+            keys = min(kv_len, w) if w else kv_len
+            b += 2 * L.kv_heads * keys * L.head_dim * 2
+        if self.ple:
+            b += c.ple_dim * 2 + self.ple_proj.nbytes
+        return float(b)
 
     # ---- weights -------------------------------------------------------------
     def init_random(self, seed: int = 2, stream=None) -> None:
@@ -366,7 +396,7 @@ class Decoder:
                 continue
             hd = L.head_dim
             src = self.layers[self.kv_sources[li]]  # the layer whose KV cache this one reads
-            rope = dict(num_heads=c.heads, num_kv_heads=0 if L.shared_kv else c.kv_heads, head_dim=hd,
+            rope = dict(num_heads=c.heads, num_kv_heads=0 if L.shared_kv else L.kv_heads, head_dim=hd,
                         freq_cis=self.freq_by_layer[li], position_buffer=self.pos_view, key_cache=L.k_cache,
                         val_cache=L.v_cache, max_seq_len=c.max_seq)
             # input_norm + q/k/v_proj + rope + cache write
@@ -376,7 +406,7 @@ class Decoder:
                             rope=rope, stream=stream)
             resid = self.x if na else act
             splits = ops.attention_partials(self.q_views[li], src.k_cache, src.v_cache, self.attn_parts, batch=1,
-                                            num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=hd,
+                                            num_heads=c.heads, num_kv_heads=L.kv_heads, head_dim=hd,
                                             kv_len=0, kv_stride=c.max_seq, scale=1.0 / math.sqrt(hd),
                                             max_splits=self.max_attn_splits, kv_len_buffer=self.kvlen_view,
                                             sliding_window=self.attn_windows[li], softcap=c.attn_softcap,
@@ -431,12 +461,12 @@ class Decoder:
         hd = L.head_dim
         src = self.layers[self.kv_sources[li]]
         ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads,
-                        num_kv_heads=0 if L.shared_kv else c.kv_heads, head_dim=hd,
+                        num_kv_heads=0 if L.shared_kv else L.kv_heads, head_dim=hd,
                         freq_cis=self.freq_by_layer[li], position_buffer=self.pos_view, key_cache=L.k_cache,
                         val_cache=L.v_cache, max_seq_len=c.max_seq, norm_weight=L.norm_attn, norm_eps=c.eps,
                         norm_weight_offset=c.norm_weight_offset, stream=stream)
         splits = ops.attention_partials(self.q_views[li], src.k_cache, src.v_cache, self.attn_parts, batch=1,
-                                        num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=hd,
+                                        num_heads=c.heads, num_kv_heads=L.kv_heads, head_dim=hd,
                                         kv_len=0, kv_stride=c.max_seq, scale=1.0 / math.sqrt(hd),
                                         max_splits=self.max_attn_splits, kv_len_buffer=self.kvlen_view,
                                         sliding_window=self.attn_windows[li], softcap=c.attn_softcap, stream=stream)
@@ -507,13 +537,13 @@ class Decoder:
         down_proj + ffn_residual.  No library workspace, so a captured graph
         stays valid whatever other attention calls the process makes."""
         c = self.cfg
-        ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads, num_kv_heads=c.kv_heads,
+        ops.qkv_rope_kv(L.wqkv, self.x, self.qkv, hidden=c.hidden, num_heads=c.heads, num_kv_heads=L.kv_heads,
                         head_dim=c.head_dim, freq_cis=self.freq_by_layer[li], position_buffer=self.pos_view,
                         key_cache=L.k_cache, val_cache=L.v_cache, max_seq_len=c.max_seq, norm_weight=L.norm_attn,
                         norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset, stream=stream,
                         weight_format="q8_0")
         splits = ops.attention_partials(self.q_view, L.k_cache, L.v_cache, self.attn_parts, batch=1,
-                                        num_heads=c.heads, num_kv_heads=c.kv_heads, head_dim=c.head_dim, kv_len=0,
+                                        num_heads=c.heads, num_kv_heads=L.kv_heads, head_dim=c.head_dim, kv_len=0,
                                         kv_stride=c.max_seq, scale=scale, max_splits=self.max_attn_splits,
                                         kv_len_buffer=self.kvlen_view, sliding_window=self.attn_windows[li],
                                         softcap=c.attn_softcap, stream=stream)
@@ -593,14 +623,14 @@ class Decoder:
             hd = L.head_dim
             # a shared-KV layer writes no cache: its attention reads the cache
             # its source layer wrote earlier in this pass
-            kvh = 0 if L.shared_kv else c.kv_heads
+            kvh = 0 if L.shared_kv else L.kv_heads
             src = self.layers[self.kv_sources[li]]
             gemm(b["x"], L.wqkv, b["qkv"], P, L.qkv_rows, c.hidden, fmt, norm_weight=L.norm_attn, norm_eps=c.eps,
                  norm_weight_offset=off, stream=stream)
             ops.qkv_rope_kv_rows(b["qkv"], P, L.qkv_rows, c.heads, kvh, hd, self.freq_by_layer[li], 0,
                                  L.k_cache if kvh else None, L.v_cache if kvh else None, c.max_seq, stream=stream)
             ops.attention_prefill_f16kv(b["qkv"], src.k_cache, src.v_cache, b["att"], num_heads=c.heads,
-                                        num_kv_heads=c.kv_heads, head_dim=hd, query_len=P, kv_len=P,
+                                        num_kv_heads=L.kv_heads, head_dim=hd, query_len=P, kv_len=P,
                                         kv_stride=c.max_seq, start_pos=0, scale=1.0 / math.sqrt(hd),
                                         softcap=c.attn_softcap, sliding_window=self.attn_windows[li],
                                         q_row_stride=L.qkv_rows, out_row_stride=L.q_dim, stream=stream)

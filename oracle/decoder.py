@@ -73,14 +73,15 @@ class OracleDecoder:
             if key not in tables:
                 tables[key] = dec.freq_by_layer[li].download()
             layer = {
-                "hd": hd, "shared": L.shared_kv, "src": dec.kv_sources[li], "q_dim": L.q_dim, "kv_dim": L.kv_dim,
+                "hd": hd, "kvh": L.kv_heads, "shared": L.shared_kv, "src": dec.kv_sources[li], "q_dim": L.q_dim,
+                "kv_dim": L.kv_dim,
                 "rows": L.qkv_rows, "table": tables[key],
                 "wqkv": wqkv, "wo": L.wo.download(), "wgu": L.wgu.download(), "wd": L.wd.download(),
                 "n1": L.norm_attn.download(), "n2": L.norm_ffn.download(),
             }
             if not L.shared_kv:
-                layer["kc"] = np.zeros((c.kv_heads, c.max_seq, hd), np.float16)
-                layer["vc"] = np.zeros((c.kv_heads, c.max_seq, hd), np.float16)
+                layer["kc"] = np.zeros((L.kv_heads, c.max_seq, hd), np.float16)
+                layer["vc"] = np.zeros((L.kv_heads, c.max_seq, hd), np.float16)
             if dec.ple:
                 layer.update(w_ple_gate=L.w_ple_gate.download(), w_ple_out=L.w_ple_out.download(),
                              n_ple=L.norm_ple.download())
@@ -109,13 +110,13 @@ class OracleDecoder:
             return ora.q8_0_gemv(w, x, n, k)
         return ora.q4k_gemv(w, x, n, k)
 
-    def _attn_p_f16(self, q, kc, vc, hd, n, window):
+    def _attn_p_f16(self, q, kc, vc, hd, n, window, kvh):
         """The batched prompt's attention (attn_mq.hip) for a prompt within
         one 32-key block: exact scores (Q is split hi/lo there), the
         probabilities exp2(x - max) rounded to f16 and normalised by their
         own sum; the window and softcap of ora_attn_decode."""
         c = self.cfg
-        G = c.heads // c.kv_heads
+        G = c.heads // kvh
         lo = n - window if 0 < window <= n - 1 else 0
         out = np.zeros((c.heads, hd), np.float32)
         qh = np.asarray(q, np.float64).reshape(c.heads, hd)
@@ -168,16 +169,17 @@ class OracleDecoder:
             src = self.layers[L["src"]]
             xn = ora.rmsnorm(x, L["n1"], c.eps, off)
             qkv = self.gemv(L["wqkv"], xn, L["rows"], c.hidden)
-            nh = c.heads + (0 if L["shared"] else c.kv_heads)
+            kvh = L["kvh"]
+            nh = c.heads + (0 if L["shared"] else kvh)
             qk = ora.rope(qkv[: L["q_dim"] + L["kv_dim"]], L["table"], 1, nh, hd, pos)
             if not L["shared"]:
                 k = qk[L["q_dim"]:]
                 v = qkv[L["q_dim"] + L["kv_dim"]:]
-                ora.kv_write(k, v, L["kc"], L["vc"], c.kv_heads, c.max_seq, hd, pos)
+                ora.kv_write(k, v, L["kc"], L["vc"], kvh, c.max_seq, hd, pos)
             if self.f16_probs:
-                attn = self._attn_p_f16(qk[: L["q_dim"]], src["kc"], src["vc"], hd, pos + 1, self.windows[li])
+                attn = self._attn_p_f16(qk[: L["q_dim"]], src["kc"], src["vc"], hd, pos + 1, self.windows[li], kvh)
             else:
-                attn = ora.attn_decode(qk[: L["q_dim"]], src["kc"], src["vc"], c.heads, c.kv_heads, hd, pos + 1,
+                attn = ora.attn_decode(qk[: L["q_dim"]], src["kc"], src["vc"], c.heads, kvh, hd, pos + 1,
                                        c.max_seq, 1.0 / math.sqrt(hd), softcap=c.attn_softcap,
                                        sliding_window=self.windows[li]).reshape(-1)
             x = ora.residual(self.gemv(L["wo"], attn, c.hidden, L["q_dim"]), x)

@@ -439,16 +439,29 @@ def test_gemma4_e2b_prefill_matches_oracle_decoder(dev, ora):
     assert max(errs) <= 1e-3
 
 
-def _gemma4_31b(name, layers, vocab=32768):
+def _gemma4_31b(name, layers, vocab=32768, global_step=False):
     """A reference Gemma 4 31B step graph (gemma-4-31b-smoke.json: 32 heads
     x 160, one kv head per query head, hidden 5120, FFN 20480, per-layer
     embeddings of width 256, global layers every 5th, the last 4 layers
     sharing KV; gemma-4-31b-af16-smoke.json: hidden 5376, 32 / 16 heads x
-    256, FFN 21504, every layer sliding over 512 keys) at its full width
-    over `layers` layers and a smaller vocabulary."""
+    256, FFN 21504, every layer sliding over 512 keys -- its one decode
+    attention step is attention_sliding, so the lowering makes every layer
+    sliding) at its full width over `layers` layers and a smaller
+    vocabulary.  global_step: the af16 graph with a global attention variant
+    step added after its layer (as gemma-4-e2b-smoke.json lists one), so its
+    layerPattern makes every 5th layer global, at globalHeadDim 512 on
+    numGlobalKeyValueHeads 4."""
     from doe_amd import execution as ex
 
     g = json.loads((Path(__file__).parent / "golden" / "execution_v1" / name).read_text())
+    if global_step:
+        dec = [s for s in g["steps"] if s["phase"] == "decode"]
+        at = next(i for i, s in enumerate(dec) if s["op"] == "attention_sliding")
+        end = max(i for i, s in enumerate(dec) if s["name"] == "ffn_residual")
+        dec.insert(end + 1, {"name": "attention_global", "phase": "decode", "op": "attention",
+                             "kernelKey": "attn_decode", "attentionType": "global"})
+        assert at < end
+        g["steps"] = [s for s in g["steps"] if s["phase"] != "decode"] + dec
     mc = {**g["modelConfig"], "numLayers": layers, "vocabSize": vocab, "pleVocabSize": vocab, "maxSeqLen": 64}
     g["modelConfig"] = mc
     graph = ex.load_step_graph(g)
@@ -488,6 +501,39 @@ def test_gemma4_31b_af16_graph_decodes_against_oracle(dev, ora):
     oracle = OracleDecoder(dec)
     ids, errs = run_teacher_forced(dec, oracle, np.array([5, 31000, 77], np.int32), 2, s)
     print(f"[decode 31b af16] logits rel_l2 {['%.1e' % e for e in errs]}", flush=True)
+    assert max(errs) <= 1e-3
+
+
+def test_gemma4_31b_af16_global_layers_decode_against_oracle(dev, ora):
+    # the af16 graph with a global attention step (every 5th layer global):
+    # 5 layers at full width, layer 4 at head_dim 512 on 4 KV heads (8 query
+    # heads per KV head, numGlobalKeyValueHeads), its o_proj over K = 16384;
+    # 4 teacher-forced steps
+    cfg, plan = _gemma4_31b("gemma-4-31b-af16-smoke.json", 5, global_step=True)
+    assert (cfg.global_head_dim, cfg.global_kv_heads) == (512, 4)
+    assert plan.windows == (512,) * 4 + (0,)
+    dec = Decoder(cfg, keep_logits=True, plan=plan)
+    assert dec.kv_heads == (16,) * 4 + (4,)
+    assert dec.layers[4].qkv_rows == 32 * 512 + 2 * 4 * 512
+    dec.init_random(seed=34)
+    s = Stream()
+    oracle = OracleDecoder(dec)
+    ids, errs = run_teacher_forced(dec, oracle, np.array([5, 31000, 77], np.int32), 2, s)
+    print(f"[decode 31b af16 global] logits rel_l2 {['%.1e' % e for e in errs]}", flush=True)
+    assert max(errs) <= 1e-3
+
+
+def test_gemma4_31b_af16_prefill_matches_oracle_decoder(dev, ora):
+    # the same 5-layer graph's prompt as one batched pass: the global layer's
+    # prompt attention at head_dim 512 over 4 KV heads
+    cfg, plan = _gemma4_31b("gemma-4-31b-af16-smoke.json", 5, global_step=True)
+    dec = Decoder(cfg, keep_logits=True, plan=plan)
+    dec.init_random(seed=33)
+    assert dec.can_prefill()
+    s = Stream()
+    oracle = OracleDecoder(dec)
+    errs = _prefill_then_decode(dec, oracle, np.array([5, 31000, 77, 9, 1234, 2], np.int32), 1, s)
+    print(f"[prefill 31b af16] logits rel_l2 {['%.1e' % e for e in errs]}", flush=True)
     assert max(errs) <= 1e-3
 
 

@@ -67,11 +67,11 @@ def test_f16_attention_equal_scores_give_the_mean():
     kc = np.zeros((1, 8, hd), np.float16)
     vc = _cache(1, 8, hd, rng.standard_normal((n, hd)))
     q = rng.standard_normal(2 * hd).astype(np.float32)
-    out = _bare()._attn_p_f16(q, kc, vc, hd, n, 0).reshape(2, hd)
+    out = _bare()._attn_p_f16(q, kc, vc, hd, n, 0, 1).reshape(2, hd)
     want = vc[0, :n].astype(np.float64).mean(axis=0)
     np.testing.assert_allclose(out, np.stack([want, want]), rtol=1e-6)
     # a window of 2 keeps keys n-2 and n-1 only
-    out = _bare()._attn_p_f16(q, kc, vc, hd, n, 2).reshape(2, hd)
+    out = _bare()._attn_p_f16(q, kc, vc, hd, n, 2, 1).reshape(2, hd)
     np.testing.assert_allclose(out[0], vc[0, n - 2:n].astype(np.float64).mean(axis=0), rtol=1e-6)
 
 
@@ -83,7 +83,7 @@ def test_f16_attention_half_weight_and_underflow():
     kc = _cache(1, 8, hd, [[0, 0, 0, 0], [-1, 0, 0, 0]])
     vc = _cache(1, 8, hd, [[1, 2, 3, 4], [4, 2, -2, 1]])
     q = np.array([2 * math.log(2), 0, 0, 0, -80, 0, 0, 0], np.float32)  # / sqrt(4)
-    out = _bare()._attn_p_f16(q, kc, vc, hd, 2, 0).reshape(2, hd)
+    out = _bare()._attn_p_f16(q, kc, vc, hd, 2, 0, 1).reshape(2, hd)
     v = vc[0, :2].astype(np.float64)
     np.testing.assert_allclose(out[0], (v[0] + 0.5 * v[1]) / 1.5, rtol=1e-6)
     assert np.array_equal(out[1], v[1].astype(np.float32))
@@ -98,7 +98,7 @@ def test_f16_attention_rounds_probabilities():
     kc = _cache(1, 8, hd, [[0, 0, 0, 0], [-1, 0, 0, 0]])
     vc = _cache(1, 8, hd, [[1, 2, 3, 4], [4, 2, -2, 1]])
     q = np.array([2 * delta * math.log(2), 0, 0, 0, 0, 0, 0, 0], np.float32)
-    out = _bare()._attn_p_f16(q, kc, vc, hd, 2, 0).reshape(2, hd)
+    out = _bare()._attn_p_f16(q, kc, vc, hd, 2, 0, 1).reshape(2, hd)
     v = vc[0, :2].astype(np.float64)
     np.testing.assert_allclose(out[0], (v[0] + v[1]) / 2, rtol=1e-7, atol=0)
     unrounded = (v[0] + 2.0 ** -delta * v[1]) / (1 + 2.0 ** -delta)
