@@ -428,6 +428,12 @@ class DecodePlan:
     # the per-layer-embedding steps before the layers (ple_gather, ple_project,
     # ple_norm, ple_modulate), None when the graph has none
     ple: Dispatch | None = None
+    # hybrid graphs (qwen-3-6-27b-smoke.json): per layer "attention" or
+    # "linear_attention", and the linear-attention layers' steps (input_norm,
+    # conv1d_depthwise, l2_normalize x 2, linear_attention); None = every
+    # layer an attention layer
+    layer_types: tuple[str, ...] | None = None
+    linear: Dispatch | None = None
 
 
 # One decoder layer: groups of ops, each group one fused dispatch.  Within a
@@ -441,11 +447,28 @@ _LAYER = (
 )
 
 
-def _take_layer(steps: list[Step], i: int) -> tuple[list[Dispatch], Step, int]:
+# The gated-attention layer of qwen-3-6-27b-smoke.json: q/k RMSNorms after the
+# projections (queryKeyNorm), the attention output gate (o_gate: the
+# attention output times sigmoid of q_proj's gate half, inputsFrom [q_proj,
+# attention]) before o_proj, and a SwiGLU FFN (silu_gated).
+_LAYER_GATED = (
+    ("qkv_norm_rope_kv", ("rmsnorm", {"matmul_q4k": 3}, {"rmsnorm": 2}, {"rope": 2}, "kv_write?")),
+    ("attention", (("attention", "attention_sliding"),)),
+    ("gated_attn_out", ("o_gate", "matmul_q4k", "residual")),
+    ("gate_up", ("rmsnorm", {"matmul_q4k": 2}, ("gelu", "gelu_gated", "silu_gated"))),
+    ("down", ("matmul_q4k", "residual")),
+)
+
+# The linear-attention (gated DeltaNet) layer body of a hybrid graph, each
+# op repeated once per such layer (repeat = their count).
+_LINEAR_BODY = ("conv1d_depthwise", "l2_normalize", "l2_normalize", "linear_attention")
+
+
+def _take_layer(steps: list[Step], i: int, layer=_LAYER) -> tuple[list[Dispatch], Step, int]:
     """Matches one layer starting at steps[i]; returns its dispatches, its
     attention step and the index after it."""
     out, attn = [], None
-    for kind, pattern in _LAYER:
+    for kind, pattern in layer:
         names = []
         for item in pattern:
             if isinstance(item, dict):  # ops in any order
@@ -531,14 +554,26 @@ def plan_decode(graph: StepGraph, num_layers: int, head_dim: int | None = None,
             raise UnsupportedStep(f"per-layer embedding steps {ops_}, expected {_PLE_STEPS}")
         ple = Dispatch("ple", tuple(st.name or st.op for st in body[:4]))
         body = body[4:]
-    # trailing variant steps of a one-layer template
+    # a hybrid graph: input_norm, then the linear-attention body (each op
+    # `repeat` times), then the attention layer, which starts from the same
+    # input_norm
     body = list(body)
+    linear, n_linear = None, 0
+    if len(body) > 5 and body[0].op == "rmsnorm" and tuple(st.op for st in body[1:5]) == _LINEAR_BODY:
+        reps = {st.repeat for st in body[1:5]}
+        if len(reps) != 1:
+            raise StepGraphError(f"linear-attention body steps repeat {sorted(reps)} times, not equally")
+        n_linear = reps.pop()
+        linear = Dispatch("linear_attention_layer", tuple(st.name or st.op for st in body[:5]))
+        body = body[:1] + body[5:]
+    # trailing variant steps of a one-layer template
     variants = []
     while body and body[-1].op in ("kv_write_shared", "attention", "attention_sliding"):
         variants.insert(0, body.pop())
+    layer_pattern = _LAYER_GATED if any(st.op == "o_gate" for st in body) else _LAYER
     layers, attns, i = [], [], 0
     while i < len(body):
-        disp, attn, i = _take_layer(body, i)
+        disp, attn, i = _take_layer(body, i, layer_pattern)
         layers.append(disp)
         attns.append(attn)
     if not layers:
@@ -549,6 +584,20 @@ def plan_decode(graph: StepGraph, num_layers: int, head_dim: int | None = None,
     if shared_listed and not graph.num_kv_shared_layers:
         raise StepGraphError("kv_write_shared step without numKvSharedLayers")
     var_attn = [v for v in variants if v.op != "kv_write_shared"]
+    layer_types = None
+    if linear is not None:
+        # n_linear linear-attention layers and one full-attention layer closing
+        # each group of `period` (the Qwen3-Next layout, layer_types
+        # [linear_attention] * (period - 1) + [full_attention] repeated: 16
+        # attention and 48 linear layers of 64 at period 4; the reference's
+        # frozen Qwen 3.6 activations of layer 3 are those of an attention
+        # layer, bench/fixtures/r3-2-27b-doppler-frozen-af16/layer_3)
+        n_attn = num_layers - n_linear
+        if len(layers) != 1 or n_attn <= 0 or num_layers % n_attn:
+            raise StepGraphError(f"{n_linear} linear-attention layers of {num_layers} do not tile into groups")
+        period = num_layers // n_attn
+        layer_types = tuple("attention" if li % period == period - 1 else "linear_attention"
+                            for li in range(num_layers))
     if len(layers) == 1:
         attns = attns * num_layers
     elif len(layers) != num_layers:
@@ -586,4 +635,4 @@ def plan_decode(graph: StepGraph, num_layers: int, head_dim: int | None = None,
             src.append(owners[-1])
         kv_sources = tuple(src)
     return DecodePlan(tuple(layers[0]), (Dispatch("lm_head_sample", tuple(post)),), windows, graph.eos_token_id,
-                      head_dims, kv_sources, ple)
+                      head_dims, kv_sources, ple, layer_types, linear)

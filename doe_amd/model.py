@@ -197,6 +197,16 @@ class Decoder:
         ordered_residual: Q4_K layers add the o_proj / down_proj K ranges into
         the residual stream in a fixed order (bit-identical steps); False adds
         them atomically in place (the f32 addition order varies run to run)."""
+        from .execution import UnsupportedStep
+
+        if plan is not None and plan.layer_types and "linear_attention" in plan.layer_types:
+            # the step graph names the body's ops (doe_conv1d_depthwise,
+            # doe_l2_normalize, doe_linear_attention run them) but not the
+            # projections that feed them or the layer's output path
+            raise UnsupportedStep("linear-attention (gated DeltaNet) layers: the graph lists conv1d_depthwise, "
+                                  "l2_normalize and linear_attention but not the projections around them")
+        if plan is not None and any(d.kind in ("qkv_norm_rope_kv", "gated_attn_out") for d in plan.layer):
+            raise UnsupportedStep("q/k RMSNorm and attention-output-gate layers are planned, not decoded")
         self.ordered_residual = ordered_residual
         # K ranges of o_proj and down_proj (ordered residual).  Every workgroup
         # of the consuming GEMV reads every part, and those few lines are

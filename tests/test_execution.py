@@ -37,9 +37,44 @@ def test_both_forms_of_the_270m_graph_plan_alike():
     assert ops["q_proj"] == "matmul_q4k" and ops["attention"] == "attention" and ops["activation"] == "gelu"
 
 
+def test_qwen_hybrid_graph_plans_and_the_decoder_refuses_it():
+    # qwen-3-6-27b-smoke.json: input_norm, the linear-attention body
+    # (conv1d_depthwise, l2_normalize q and k, linear_attention, each
+    # repeat 48), then the gated attention layer (q/k norms, rope, attention,
+    # o_gate, o_proj, SwiGLU FFN): 48 linear and 16 attention layers, a full
+    # attention layer closing each group of four
+    g = ex.load_step_graph(GOLD / "qwen-3-6-27b-smoke.json")
+    plan = ex.plan_decode(g, 64)
+    assert [d.kind for d in plan.layer] == ["qkv_norm_rope_kv", "attention", "gated_attn_out", "gate_up", "down"]
+    assert plan.linear.steps == ("input_norm", "ssm_conv1d_depthwise", "ssm_q_l2_normalize", "ssm_k_l2_normalize",
+                                 "ssm_linear_attention")
+    assert plan.layer_types == ("linear_attention",) * 3 + ("attention",) + plan.layer_types[4:]
+    assert [i for i, t in enumerate(plan.layer_types) if t == "attention"] == list(range(3, 64, 4))
+    assert plan.windows == (0,) * 64
+    # every decode step is carried out by one dispatch
+    covered = [n for d in plan.layer + plan.post + (plan.linear,) for n in d.steps]
+    assert sorted(set(covered)) == sorted({s.name for s in g.phase("decode")})
+    # the host plan launches each body op once per linear-attention layer
+    # (decode and prefill)
+    hp = ex.lower_host_plan(g)
+    counts = {k["name"]: k["count"] for k in hp["kernels"]}
+    assert counts["ssm_conv1d_depthwise"] == counts["ssm_linear_attention"] == 96
+    # a body whose ops repeat unequally is malformed
+    q = graph_json("qwen-3-6-27b-smoke.json")
+    bad = copy.deepcopy(q)
+    next(s for s in bad["steps"] if s["phase"] == "decode" and s["op"] == "l2_normalize")["repeat"] = 47
+    with pytest.raises(ex.StepGraphError, match="not equally"):
+        ex.plan_decode(ex.load_step_graph(bad), 64)
+    # the decoder refuses what the graph does not define: the projections
+    # around the linear-attention body
+    from doe_amd.model import Decoder
+
+    cfg = DecoderConfig(layers=64, hidden=256, heads=2, kv_heads=1, head_dim=128, ffn=512, vocab=256, max_seq=16)
+    with pytest.raises(ex.UnsupportedStep, match="linear-attention"):
+        Decoder(cfg, plan=plan)
+
+
 def test_graphs_this_library_does_not_execute_are_refused_by_step():
-    with pytest.raises(ex.UnsupportedStep, match="conv1d_depthwise"):
-        ex.plan_decode(ex.load_step_graph(GOLD / "qwen-3-6-27b-smoke.json"), 64)
     # per-layer embedding steps out of their order
     e2b = graph_json("gemma-4-e2b-smoke.json")
     dec = [s for s in e2b["steps"] if s["phase"] == "decode"]
