@@ -95,6 +95,7 @@ SIGNATURES: dict[str, list] = {
                                  _vp],
     "doe_rmsnorm": [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp],
     "doe_rope": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp],
+    "doe_rope_partial": [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "doe_geglu": [_vp, _vp, _vp, _i64, _vp],
     "doe_residual_add": [_vp, _vp, _vp, _i64, _vp],
     "doe_ple_modulate": [_vp, _vp, _vp, _i64, _f32, _vp],

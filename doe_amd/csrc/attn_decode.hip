@@ -659,8 +659,10 @@ int launch_main(int g, bool w, dim3 grid, hipStream_t st, const AttnArgs &a) {
         case 1: return launch_g<D, 1>(w, grid, st, a);
         case 2: return launch_g<D, 2>(w, grid, st, a);
         case 4: return launch_g<D, 4>(w, grid, st, a);
+        case 6: return launch_g<D, 6>(w, grid, st, a);  // Qwen 3.6: 24 query heads on 4 KV heads
         case 8: return launch_g<D, 8>(w, grid, st, a);
-        default: return doe::set_error(DOE_E_UNSUPPORTED, "query heads per kv head must be 1, 2, 4 or 8 (got %d)", g);
+        default:
+            return doe::set_error(DOE_E_UNSUPPORTED, "query heads per kv head must be 1, 2, 4, 6 or 8 (got %d)", g);
     }
 }
 

@@ -47,12 +47,15 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
 
 // RoPE, rotate-half pairs (i, i + D/2) (rope.wgsl:12-35).  Products and
 // differences are rounded separately, as the reference's scalar code does.
+// rot < head_dim: partial rotary (the rope_partial kernel of
+// qwen-3-6-27b-smoke.json, partialRotaryFactor): pairs (i, i + rot/2) of each
+// head's first rot dims, the others unchanged; freq_cis [pos][rot/2][2].
 __global__ __launch_bounds__(256) void rope_kernel(float *__restrict__ qk,
                                                    const float *__restrict__ freq_cis, int seq_len,
-                                                   int num_heads, int head_dim, int pos_off,
+                                                   int num_heads, int head_dim, int rot, int pos_off,
                                                    const int32_t *__restrict__ pos_dev) {
 #pragma clang fp contract(off)
-    const int half = head_dim >> 1;
+    const int half = rot >> 1;
     const long total = (long)seq_len * num_heads * half;
     const int base_pos = pos_dev ? pos_dev[0] : pos_off;
     for (long g = (long)blockIdx.x * 256 + threadIdx.x; g < total; g += (long)gridDim.x * 256) {
@@ -321,7 +324,25 @@ int doe_rope(float *qk, const float *freq_cis, int64_t seq_len, int64_t num_head
     if (total == 0) return DOE_OK;
     DOE_REQUIRE(qk && freq_cis, DOE_E_INVALID, "null pointer");
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, qk,
-                       freq_cis, (int)seq_len, (int)num_heads, (int)head_dim, (int)position_offset,
+                       freq_cis, (int)seq_len, (int)num_heads, (int)head_dim, (int)head_dim, (int)position_offset,
+                       position_dev);
+    DOE_LAUNCH_CHECK("rope_kernel");
+    return DOE_OK;
+}
+
+int doe_rope_partial(float *qk, const float *freq_cis, int64_t seq_len, int64_t num_heads, int64_t head_dim,
+                     int64_t rotary_dim, int64_t position_offset, const int32_t *position_dev, doe_stream_t stream) {
+    int rc = doe::require_init();
+    if (rc) return rc;
+    DOE_REQUIRE(seq_len >= 0 && num_heads >= 0 && head_dim > 0 && rotary_dim > 0 && (rotary_dim % 2) == 0 &&
+                    rotary_dim <= head_dim && position_offset >= 0 && seq_len * num_heads * head_dim < (1L << 31),
+                DOE_E_INVALID, "bad rope shape (rotary_dim %lld of head_dim %lld)", (long long)rotary_dim,
+                (long long)head_dim);
+    const long total = (long)seq_len * num_heads * (rotary_dim / 2);
+    if (total == 0) return DOE_OK;
+    DOE_REQUIRE(qk && freq_cis, DOE_E_INVALID, "null pointer");
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream, qk,
+                       freq_cis, (int)seq_len, (int)num_heads, (int)head_dim, (int)rotary_dim, (int)position_offset,
                        position_dev);
     DOE_LAUNCH_CHECK("rope_kernel");
     return DOE_OK;

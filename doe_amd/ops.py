@@ -523,6 +523,16 @@ def rope(qk: DeviceBuffer, freq_cis: DeviceBuffer, seq_len: int, num_heads: int,
               _stream_ptr(stream))
 
 
+def rope_partial(qk: DeviceBuffer, freq_cis: DeviceBuffer, seq_len: int, num_heads: int, head_dim: int,
+                 rotary_dim: int, position_offset: int = 0, stream=None) -> None:
+    """``rope`` over each head's first ``rotary_dim`` dims (rotate-half pairs
+    within them; freq_cis [pos][rotary_dim/2][2])."""
+    _need(qk, seq_len * num_heads * head_dim * 4, "qk")
+    _need(freq_cis, (position_offset + seq_len) * rotary_dim * 4, "freq_cis")
+    _lib.call("doe_rope_partial", _p(qk), _p(freq_cis), seq_len, num_heads, head_dim, rotary_dim, position_offset,
+              C.c_void_p(None), _stream_ptr(stream))
+
+
 def gelu_gated(gate: DeviceBuffer, up: DeviceBuffer, output: DeviceBuffer, n: int, stream=None) -> None:
     """``gelu_gated`` op: gelu_tanh(gate) * up."""
     for buf, role in ((gate, "gate"), (up, "up"), (output, "output")):

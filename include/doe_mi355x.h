@@ -476,6 +476,14 @@ int doe_rmsnorm(const float *input, const float *weight, float *output, int64_t 
 int doe_rope(float *qk, const float *freq_cis, int64_t seq_len, int64_t num_heads,
              int64_t head_dim, int64_t position_offset, const int32_t *position_dev,
              doe_stream_t stream);
+/* doe_rope over the first rotary_dim dims of each head only (rotate-half
+ * pairs (i, i + rotary_dim/2), the other dims unchanged; freq_cis
+ * [pos][rotary_dim/2][2]).  Replaces the `rope_partial` kernel of
+ * qwen-3-6-27b-smoke.json (partialRotaryFactor 0.25: 64 of 256 dims; its
+ * text-only mropeSection positions reduce to this 1D rotation). */
+int doe_rope_partial(float *qk, const float *freq_cis, int64_t seq_len, int64_t num_heads, int64_t head_dim,
+                     int64_t rotary_dim, int64_t position_offset, const int32_t *position_dev,
+                     doe_stream_t stream);
 /* out = gelu_tanh(gate) * up (clamped inner, gelu_gated.wgsl:1-14). */
 int doe_geglu(const float *gate, const float *up, float *output, int64_t n, doe_stream_t stream);
 /* out = input + residual (residual.wgsl; run_csl_webgpu_emulator.mjs:482-489);

@@ -229,6 +229,17 @@ def rope(qk: np.ndarray, freq_cis: np.ndarray, seq_len: int, num_heads: int, hea
     return out
 
 
+def rope_partial(qk: np.ndarray, freq_cis: np.ndarray, seq_len: int, num_heads: int, head_dim: int,
+                 rotary_dim: int, position_offset: int) -> np.ndarray:
+    """ora_rope on each head's first rotary_dim dims (rotate-half pairs (i,
+    i + rotary_dim/2); freq_cis [pos][rotary_dim/2][2]), the other dims
+    unchanged: the rope_partial kernel of qwen-3-6-27b-smoke.json."""
+    x = _c(qk, np.float32).reshape(seq_len, num_heads, head_dim).copy()
+    r = rope(np.ascontiguousarray(x[..., :rotary_dim]), freq_cis, seq_len, num_heads, rotary_dim, position_offset)
+    x[..., :rotary_dim] = r.reshape(seq_len, num_heads, rotary_dim)
+    return x.reshape(-1)
+
+
 def rope_pairs(x: np.ndarray, cos_t: np.ndarray, sin_t: np.ndarray, head_dim: int, num_pairs: int,
                interleaved: bool) -> np.ndarray:
     out = _c(x, np.float32).copy()

@@ -1,6 +1,7 @@
 """GPU parity of GQA decode attention (f16 KV cache) against the CPU oracle,
 through the C ABI.  Tolerance: rel-L2 <= 1e-3 (fp32 accumulate)."""
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -392,3 +393,40 @@ def test_head160_sliding_layout1_kv_len_device(dev, ora):
         want = oracle_attn(ora, q, k, v, batch=1, hq=hq, hkv=hkv, d=d, kv_len=t, kv_stride=stride, scale=d ** -0.5,
                            softcap=softcap, window=window, layout=1)
         assert rel_l2(got, want) <= ATTN_REL_L2, (softcap, window)
+
+
+def test_qwen36_partial_rope_gqa6_attention_on_real_activations(dev, ora):
+    # Qwen 3.6 27B layer 3 (tests/golden/qwen36_layer3_attention.npz, the
+    # reference's frozen Doppler activations): doe_rope_partial over the first
+    # 64 of 256 dims (theta 1e7), doe_kv_write into an f16 cache, then decode
+    # attention per prompt position with six query heads on one KV head.
+    # Against the oracle on the same steps within 1e-5; against the
+    # reference run's output (computed in f16) within 3e-3, where the oracle
+    # itself sits (tests/test_oracle_qwen_attention.py).
+    from doe_amd.model import rope_table
+
+    from test_oracle_qwen_attention import D, G, ROT, T, THETA, oracle_attention, rel
+
+    with np.load(Path(__file__).parent / "golden" / "qwen36_layer3_attention.npz", allow_pickle=False) as z:
+        fx = {k: z[k].astype(np.float32) for k in z.files}
+    tab = DeviceBuffer.from_array(rope_table(T, ROT, THETA))
+    q = DeviceBuffer.from_array(fx["q"])
+    k = DeviceBuffer.from_array(fx["k"])
+    v = DeviceBuffer.from_array(fx["v"])
+    ops.rope_partial(q, tab, T, G, D, ROT)
+    ops.rope_partial(k, tab, T, 1, D, ROT)
+    kc = DeviceBuffer.empty((1, T, D), np.float16)
+    vc = DeviceBuffer.empty((1, T, D), np.float16)
+    out = DeviceBuffer.empty((T, G, D), np.float32)
+    for t in range(T):
+        ops.kv_write(k.view(t * D * 4, D * 4, np.float32), v.view(t * D * 4, D * 4, np.float32), kc, vc, 1, T, D,
+                     position=t)
+        ops.attention(q.view(t * G * D * 4, G * D * 4, np.float32), kc, vc,
+                      out.view(t * G * D * 4, G * D * 4, np.float32), batch=1, num_heads=G, num_kv_heads=1,
+                      head_dim=D, kv_len=t + 1, kv_stride=T, scale=1.0 / 16)
+    got = out.download().reshape(T, G, D)
+    want = oracle_attention(ora, fx, ROT)
+    e_oracle, e_run = rel(got, want), rel(got, fx["out"])
+    print(f"[qwen36 layer 3] vs oracle {e_oracle:.1e}, vs reference run {e_run:.1e}", flush=True)
+    assert e_oracle <= 1e-5
+    assert e_run <= 3e-3
