@@ -180,7 +180,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         h8 qfrag[2][KSTEPS][64];
         float wo[kWaves][G][D];
     } sm;
-    __shared__ float4 pb[kWaves][16][G4];  // per wave: probabilities [position][head]
+    __shared__ float4 pb[kWaves][17][G4];  // per wave: probabilities [position][head], row 16: max
     __shared__ float wm[kWaves][G], wl[kWaves][G];
 
     // blockIdx.y = kv head * head_groups + group: G query heads per workgroup
@@ -200,10 +200,10 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     // row l % 16 (query head hq0 + l % 16 when < G, else zero), dims 32 s +
     // 8 (l / 16) .. + 7.  Raw bytes first: no conversion between the loads,
     // so every query load and the first K/V block are in flight together.
-    // Two 16-byte loads per item whatever the query's type (an f16 query
-    // loads its 16 bytes twice) and, in the one-block form, no branch up to
-    // the K/V loads: the compiler then counts the loads still in flight
-    // exactly, and converting the query waits for the query loads only.
+    // In the one-block form two 16-byte loads per item whatever the query's
+    // type (an f16 query loads its 16 bytes twice) and no branch up to the
+    // K/V loads: the compiler then counts the loads still in flight exactly,
+    // and converting the query waits for the query loads only.
     constexpr int QITEMS = (KSTEPS * 64 + kThreads - 1) / kThreads;
     u32x4 qraw[QITEMS][2];
 #pragma unroll
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         const size_t qi = ((size_t)b * a.num_heads + hq0 + (m < G ? m : 0)) * D + 32 * s + 8 * (l >> 4);
         const char *q0 = reinterpret_cast<const char *>(a.q) + (a.q_f16 ? 2 * qi : 4 * qi);
         qraw[it][0] = *reinterpret_cast<const u32x4 *>(q0);
-        qraw[it][1] = *reinterpret_cast<const u32x4 *>(q0 + (a.q_f16 ? 0 : 16));
+        if (ONE || !a.q_f16) qraw[it][1] = *reinterpret_cast<const u32x4 *>(q0 + (a.q_f16 ? 0 : 16));
     }
     KVBlock<D> cur;
     // a contiguous cache (kv_map 0) addresses V rows without lane reads
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
     // running max of the heads whose scores this lane holds (4*(lane/16)+i)
     float mlane[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     const int grp = lane >> 4;
-    float *pbw = reinterpret_cast<float *>(&pb[wave][0][0]);  // [16][G4*4]
+    float *pbw = reinterpret_cast<float *>(&pb[wave][0][0]);  // [17][G4*4]
 
     for (; blk < blk_end; blk += kWaves) {
         // Prefetch the next block of this wave while this one is computed
@@ -332,7 +332,8 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
 
         const int p0 = blk * 16;
         const int pk = p0 + (lane & 15);
-        // two independent accumulation chains (even / odd k-steps)
+        // the one-block form: two independent accumulation chains (even / odd
+        // k-steps); the multi-block form one chain
         auto qfrag = [&](int part, int s) __attribute__((always_inline)) -> h8 {
             if constexpr (QREG) return part ? ql[s] : qh[s];
             else return sm.qfrag[part][s][lane];
@@ -341,14 +342,14 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s) {
             const h8 qa = qfrag(0, s);
-            if (s & 1) c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c1, 0, 0, 0);
+            if (ONE && (s & 1)) c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c1, 0, 0, 0);
             else c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c0, 0, 0, 0);
         }
         if (!a.q_f16) {
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
                 const h8 qa = qfrag(1, s);
-                if (s & 1) c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c1, 0, 0, 0);
+                if (ONE && (s & 1)) c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c1, 0, 0, 0);
                 else c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, cur.kf[s], c0, 0, 0, 0);
             }
         }
@@ -373,14 +374,29 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
             const float p = valid ? __builtin_amdgcn_exp2f(sc - bm) : 0.0f;
             tsum[i] = sum16(p);
             const int h = 4 * grp + i;
-            if (h < G) pbw[(lane & 15) * (G4 * 4) + h] = p;
+            if (h < G) {
+                pbw[(lane & 15) * (G4 * 4) + h] = p;
+                if (!ONE && (lane & 15) == 0) pbw[16 * (G4 * 4) + h] = bm;  // new running max of head h
+                if (!ONE && (lane & 15) == 1) wl[wave][h] = tsum[i];     // block sum of head h (scratch)
+            }
         }
         // Head h's running max and block sum are in every lane of 16-lane
-        // row h / 4 (the DPP reductions leave them there): one lane read each.
+        // row h / 4 (the DPP reductions leave them there).  The one-block
+        // form reads them from there (one lane read each, no LDS round trip
+        // before the rescale); the multi-block form, whose next block is
+        // already in flight, takes them through LDS (its lane reads measured
+        // 4 % slower at 8 query heads per KV head).
+        if constexpr (!ONE) __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            const float mnew = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mlane[h & 3]), 16 * (h >> 2)));
-            const float bsum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tsum[h & 3]), 16 * (h >> 2)));
+            float mnew, bsum;
+            if constexpr (ONE) {
+                mnew = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mlane[h & 3]), 16 * (h >> 2)));
+                bsum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tsum[h & 3]), 16 * (h >> 2)));
+            } else {
+                mnew = pbw[16 * (G4 * 4) + h];  // the same in every lane
+                bsum = wl[wave][h];
+            }
             if (mnew != mrow[h]) {
                 // raised from mrow (-inf before the first valid key: o and l are 0)
                 const float alpha = __builtin_amdgcn_exp2f(mrow[h] - mnew);
@@ -395,10 +411,13 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
         // are ordered within a wave).
         __builtin_amdgcn_wave_barrier();
         // (after the softmax, which thus overlaps the V loads' arrival)
-        if (p0 + 16 > key_hi) {
+        if (ONE && a.spec_bps > 0 && p0 + 16 > key_hi) {
             // the block past the visible keys: its rows there get probability
             // 0, and their V (never written, in a block loaded before kv_len
-            // was known) is zeroed so that 0 * V stays 0
+            // was known) is zeroed so that 0 * V stays 0.  (Other blocks
+            // clamp their V rows to visible keys.  In the multi-block form
+            // this branch made the compiler wait for the prefetched next
+            // block before the softmax: 12 % slower at 32k keys.)
 #pragma unroll
             for (int n = 0; n < 16; ++n)
                 if (p0 + n >= key_hi)
@@ -406,8 +425,11 @@ __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnArgs a) {
                     for (int d = 0; d < DPL; ++d) cur.vv[n][d] = (_Float16)0.0f;
         }
         // P.V in batches of CH positions: the batch's probability reads all
-        // go out before its FMAs (one LDS wait per batch)
-        constexpr int CH = G4 == 1 ? 16 : (G4 == 2 ? 8 : 4);
+        // go out before its FMAs (one LDS wait per batch) in the one-block
+        // form up to four query heads; row by row otherwise (batches of 8
+        // rows at 8 query heads per KV head measured 9 % slower, long
+        // contexts)
+        constexpr int CH = (ONE && G4 == 1) ? 16 : 1;
 #pragma unroll
         for (int n0 = 0; n0 < 16; n0 += CH) {
             float4 pr[CH][G4];
