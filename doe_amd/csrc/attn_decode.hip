@@ -23,6 +23,11 @@
 //   * P.V on the VALU: lane l owns dims l*D/64 .. of every head; the block's
 //     probabilities are broadcast through LDS into f32 FMAs against the f16
 //     V row.  Each wave prefetches its next block while computing this one.
+//   * one-block form (every wave owns at most one block: short contexts,
+//     the decode step): no prefetch; the query fragments held in registers;
+//     with a device kv_len over a small contiguous cache, fixed block
+//     ranges so the K/V loads leave before the kv_len load returns (rows
+//     past the context masked, their V zeroed).
 //   * the W waves combine through LDS; with more than one split, each
 //     workgroup writes (m, l, o) partials to the workspace and a second,
 //     small kernel combines them (a kernel boundary orders the partials
