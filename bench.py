@@ -264,8 +264,9 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder", cpu_r
 
     cfg = cfg or DecoderConfig()
     # a batched prompt samples one token before the first decode step: room
-    # for prompt + 1 + decode_steps ids (the KV cache uses one row fewer)
-    need = args.prompt_len + args.decode_steps + 1
+    # for prompt + 1 + decode_steps ids (the KV cache uses one row fewer),
+    # and a row for the parity step after the trajectory
+    need = args.prompt_len + args.decode_steps + 2
     if cfg.max_seq < need:
         cfg = dataclasses.replace(cfg, max_seq=need)
     dec = Decoder(cfg, plan=plan)
@@ -287,7 +288,10 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder", cpu_r
     ids = dec.generate(prompt, n_new, s, graph=graph, steps_per_graph=max(spg, 1), timing=timing, prefill=pf)
     if graph is not None:
         graph.destroy()
+    end = trajectory_end_parity(dec, s) if cpu_runs > 1 else None
     parity, cpu = decode_parity_and_cpu(dec, prompt, s, cpu_runs)
+    if end is not None:
+        parity.update(end)
     tok_s = args.decode_steps / timing["decode_s"]
     mean_len = args.prompt_len + (args.decode_steps + 1) / 2.0
     bpt = dec.decode_bytes_per_token(mean_len)
@@ -315,6 +319,32 @@ def bench_decode(args, doe, cfg=None, plan=None, label="2B-class decoder", cpu_r
         "parity": parity,
         "cpu_baseline": cpu,
     }
+
+
+def trajectory_end_parity(dec, s):
+    """Outside the timed region, where the timed trajectory ended: one more
+    eager decode step (attention over every key the prompt pass and the
+    decode steps wrote) against the oracle decoder's step at that position,
+    which reads the KV cache the device wrote."""
+    from oracle.decoder import OracleDecoder
+
+    pos, _, _, tok = (int(v) for v in dec.state.download())
+    if pos + 1 > dec.cfg.max_seq:
+        return None
+    oracle = OracleDecoder(dec)
+    oracle.load_kv(dec)
+    dec.keep_logits = True
+    dec.step(s)
+    s.synchronize()
+    got = dec.logits.download().astype(np.float64)
+    gtok = int(dec.token.download()[0])
+    dec.keep_logits = False
+    want = oracle.step(pos, tok)
+    del oracle
+    rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    log(f"  decode parity at the trajectory's end: position {pos} ({pos + 1} keys), logits rel_l2 {rel:.2e}, "
+        f"token {gtok} vs oracle {int(np.argmax(want))}")
+    return {"end_position": pos, "end_logits_rel_l2_vs_oracle": rel, "end_token_equal": gtok == int(np.argmax(want))}
 
 
 def decode_parity_and_cpu(dec, prompt, s, runs=CPU_DECODE_RUNS):

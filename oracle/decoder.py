@@ -99,6 +99,22 @@ class OracleDecoder:
             self.ple_proj = dec.ple_proj.download()
             self.ple_norm = dec.ple_norm.download()
 
+    def load_kv(self, dec, plain_k: bool = True) -> None:
+        """Takes the device's KV caches ([kv_head][pos][dim] f16) as the
+        oracle's own: a step at a later position then reads the context the
+        device wrote (the prompt pass and the decode steps before it).  The
+        device holds K in the rotation-pair order of its q/k rows (dims i and
+        i + head_dim/2 at 2i and 2i + 1); the oracle in plain dim order.
+        plain_k False keeps the device's order (a deliberate mismatch, for
+        tests that show the check depends on the cache)."""
+        for L, Ld in zip(self.layers, dec.layers):
+            if not L["shared"]:
+                kc = Ld.k_cache.download().reshape(L["kc"].shape).astype(np.float16)
+                if plain_k:
+                    kc = np.concatenate([kc[..., 0::2], kc[..., 1::2]], axis=-1)
+                L["kc"] = np.ascontiguousarray(kc)
+                L["vc"] = Ld.v_cache.download().reshape(L["vc"].shape).astype(np.float16)
+
     def gemv(self, w, x, n, k):
         if self.f16_operands:
             # the batched prompt's GEMM (q4k_gemm.hip): activation and

@@ -709,6 +709,54 @@ def test_full_size_graph_trajectory_equals_eager(dev):
     assert out[:128].tolist() == prompt.tolist()
 
 
+@pytest.mark.parametrize("fmt", ["q4k", "q8_0"])
+def test_full_size_trajectory_end_step_matches_oracle(dev, fmt):
+    # the bench's trajectory at the 2B-class shape: a 128-token batched
+    # prompt, 64 greedy steps from 8-step graphs, then one more step at
+    # position 192 (attention over 193 keys) against the oracle decoder's
+    # step at that position over the KV cache the device wrote.  The Q4_K
+    # q/k/v rows get zero-mean weights (dmin ~ 7.5 d cancels the mean of
+    # d sc q - dmin m, which makes the random model's attention one-hot on
+    # nearly parallel keys); the Q8_0 ones are zero-mean already.  The check
+    # depends on the context: over the same cache with K left in the device's
+    # rotation-pair dim order the oracle's step is far off.
+    import ctypes as C
+
+    from doe_amd import _lib, q4k
+
+    cfg = DecoderConfig(max_seq=128 + 64 + 2, weight_format=fmt)
+    dec = Decoder(cfg, keep_logits=True)
+    dec.init_random(seed=2)
+    if fmt == "q4k":
+        for i, L in enumerate(dec.layers):
+            _lib.call("doe_fill_random_q4k", C.c_void_p(L.wqkv.ptr), L.wqkv.nbytes // q4k.BLOCK_BYTES, 7000 + i,
+                      0.002, 0.015, C.c_void_p(None))
+    s = Stream()
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab, 128).astype(np.int32)
+    dec.reset(prompt)
+    dec.step(s)
+    s.synchronize()
+    g = dec.capture(s, 8)
+    dec.generate(prompt, 65, s, graph=g, steps_per_graph=8, prefill=True)
+    g.destroy()
+    pos, _, _, tok = (int(v) for v in dec.state.download())
+    assert pos == 192
+    oracle = OracleDecoder(dec)
+    oracle.load_kv(dec)
+    dec.step(s)
+    s.synchronize()
+    got = dec.logits.download()
+    want = oracle.step(pos, tok)
+    err = rel_l2(got, want)
+    oracle.load_kv(dec, plain_k=False)
+    wrong = rel_l2(got, oracle.step(pos, tok))
+    print(f"[trajectory end step 192, {fmt}] logits rel_l2 {err:.1e}; with K in the wrong dim order {wrong:.1e}",
+          flush=True)
+    assert err <= 1e-3
+    assert int(np.argmax(got)) == int(np.argmax(want))
+    assert wrong > 2e-3 and wrong > 100 * err  # the tolerance would catch the mistake
+
+
 def test_full_size_trajectory_bit_reproducible(dev):
     # the bench's 2B-class trajectory twice (128-token batched prompt, then
     # 24 greedy steps from 8-step graphs): every token and the last step's
