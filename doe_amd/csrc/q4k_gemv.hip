@@ -194,6 +194,12 @@ struct GemvFusion {
     // K split into parts: K range s stores its row sums to y_parts[s n + row]
     // with plain stores (no residual, no atomics); the consumer adds them.
     float *y_parts;
+    // Residual given as residual + res_parts[0] + ... + res_parts[res_nparts
+    // - 1] (each n floats, added in that order): a consumer forms the sum a
+    // producer's activation prologue formed, instead of reading it stored.
+    // Matrix-core kernel, whole rows or output parts.
+    const float *res_parts;
+    int res_nparts;
 };
 
 constexpr int kMaxXParts = 4;  // activation parts a GEMV adds in its prologue
@@ -501,7 +507,9 @@ __device__ __forceinline__ float sum_rows4(float v) {
 // XV: the activation is read as one float4 per lane (x 16-byte aligned and
 // k % 4 == 0), else as four clamped dwords.  Both forms are branch-free so the
 // activation loads stay ahead of the weight stream.
-template <int PRO, int BPW, int XV>
+// RP: the residual comes with parts (fz.res_parts), a form of its own so the
+// others keep their register count.
+template <int PRO, int BPW, int XV, bool RP = false>
 __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__restrict__ w,
                                                              const float *x,
                                                              float *__restrict__ y, int n, int k,
@@ -580,8 +588,18 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
     // last store does not wait on a load (K split: range 0 adds it when the
     // ranges go to parts; atomic ranges add into a y that holds it already).
     const bool has_res = fz.residual && blockIdx.y == 0 && (fz.y_parts || gridDim.y == 1);
-    float rpre = 0.0f;
-    if (has_res && tid < 16) rpre = fz.residual[min(row0 + tid, n - 1)];
+    // (its parts are loaded here and added once the weight loads are out:
+    // an add here would wait for them before the weight loads go out)
+    float rres[RP ? 1 + kMaxXParts : 1] = {};
+    if (has_res && tid < 16) {
+        const int rr = min(row0 + tid, n - 1);
+        rres[0] = fz.residual[rr];
+        if constexpr (RP) {
+#pragma unroll
+            for (int sp = 0; sp < kMaxXParts; ++sp)
+                if (sp < fz.res_nparts) rres[1 + sp] = fz.res_parts[(size_t)sp * n + rr];
+        }
+    }
     // (x is not __restrict__: with it its loads count as invariant and were
     // sunk past the weight loads; this memory clobber keeps the order)
     __asm__ volatile("" ::: "memory");
@@ -599,6 +617,12 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    float rpre = rres[0];
+    if constexpr (RP) {
+#pragma unroll
+        for (int sp = 0; sp < kMaxXParts; ++sp)
+            if (sp < fz.res_nparts) rpre += rres[1 + sp];
+    }
 
     if (XPB > 0 && fz.x_nparts > 0) {
         // x + part 0 + part 1 + ..., in that order; workgroup (0, 0) keeps
@@ -1126,6 +1150,12 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     DOE_REQUIRE(!(fz.gated && fz.rope_kv) && !(fz.rope_kv && fz.residual), DOE_E_UNSUPPORTED,
                 "rope/kv epilogue excludes gated and residual");
     DOE_REQUIRE(!(fz.gated && fz.residual), DOE_E_UNSUPPORTED, "gated and residual are exclusive");
+    DOE_REQUIRE(fz.res_nparts >= 0 && fz.res_nparts <= kMaxXParts &&
+                    (fz.res_nparts == 0 || (fz.res_parts && fz.residual)),
+                DOE_E_INVALID, "residual parts: 0..%d with a residual and a parts pointer (got %d)", kMaxXParts,
+                fz.res_nparts);
+    DOE_REQUIRE(fz.res_nparts == 0 || (fz.residual != output && !fz.norm_w), DOE_E_UNSUPPORTED,
+                "residual parts need an output apart from the residual and no RMSNorm prologue");
     if (n == 0) return DOE_OK;
     DOE_REQUIRE(output, DOE_E_INVALID, "null output");
     if (k == 0) {
@@ -1222,12 +1252,15 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     // Streaming kernel: one wave per block, whole rows, no attention
     // prologue; automatic from kStreamMinGroupsPerCu row groups per CU
     // (q4k_gemv.stream: -1 never, g > 0 forces g row groups per workgroup).
-    DOE_REQUIRE(!(xparts || fz.y_parts) || use_mfma, DOE_E_UNSUPPORTED,
-                "activation / output parts need the matrix-core kernel");
+    DOE_REQUIRE(!(xparts || fz.y_parts || fz.res_nparts) || use_mfma, DOE_E_UNSUPPORTED,
+                "activation / output / residual parts need the matrix-core kernel");
+    DOE_REQUIRE(!fz.res_nparts || ksplit == 1 || fz.y_parts, DOE_E_UNSUPPORTED,
+                "residual parts need whole rows or output parts");
     DOE_REQUIRE(!xparts || bpw <= 2, DOE_E_UNSUPPORTED,
                 "activation parts need k <= 8192 (two Q4_K blocks per wave; got k=%lld)", (long long)k);
     DOE_REQUIRE(!fz.x_sum || ksplit == 1, DOE_E_UNSUPPORTED, "the activation sum needs whole rows");
-    const bool stream_ok = use_mfma && bpw == 1 && ksplit == 1 && !fz.attn_o && !xparts && !fz.y_parts;
+    const bool stream_ok =
+        use_mfma && bpw == 1 && ksplit == 1 && !fz.attn_o && !xparts && !fz.y_parts && !fz.res_nparts;
     if (stream_ok && (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups >= kStreamMinGroupsPerCu * g_num_cus))) {
         const int nwaves = nb;
         // ring depth 2: deeper rings measured slower (65536 x 2304: 21.4 us
@@ -1284,29 +1317,33 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         const dim3 grid((unsigned)row_groups, (unsigned)ksplit);
         const bool xv = activation && ((uintptr_t)activation & 15) == 0 && (k & 3) == 0 &&
                         ((uintptr_t)fz.norm_w & 15) == 0 && ((uintptr_t)fz.x_parts & 15) == 0;
-#define DOE_GEMV_MFMA_LAUNCH(P, B, X)                                                             \
+#define DOE_GEMV_MFMA_LAUNCH(P, B, X, R)                                                             \
     do {                                                                                          \
         /* set once per process; a static's initialisation is thread-safe */                    \
         static const hipError_t attr_rc = hipFuncSetAttribute(                                    \
-            (const void *)q4k_gemv_mfma_kernel<P, B, X>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+            (const void *)q4k_gemv_mfma_kernel<P, B, X, R>, hipFuncAttributeMaxDynamicSharedMemorySize, \
             (int)gemv_mfma_lds_bytes(16, B));                                                     \
         DOE_HIP_CHECK(attr_rc);                                                                   \
-        hipLaunchKernelGGL((q4k_gemv_mfma_kernel<P, B, X>), grid, dim3(64 * nwaves), lds, st, wp, \
+        hipLaunchKernelGGL((q4k_gemv_mfma_kernel<P, B, X, R>), grid, dim3(64 * nwaves), lds, st, wp, \
                            activation, output, (int)n, (int)k, nb, nbs, fz);                      \
     } while (0)
-#define DOE_GEMV_MFMA_BPW(P, X)                                                                   \
+#define DOE_GEMV_MFMA_BPW(P, X, R)                                                                   \
     switch (bpw) {                                                                                \
-        case 1: DOE_GEMV_MFMA_LAUNCH(P, 1, X); break;                                             \
-        case 2: DOE_GEMV_MFMA_LAUNCH(P, 2, X); break;                                             \
-        case 3: DOE_GEMV_MFMA_LAUNCH(P, 3, X); break;                                             \
-        default: DOE_GEMV_MFMA_LAUNCH(P, 4, X); break;                                            \
+        case 1: DOE_GEMV_MFMA_LAUNCH(P, 1, X, R); break;                                             \
+        case 2: DOE_GEMV_MFMA_LAUNCH(P, 2, X, R); break;                                             \
+        case 3: DOE_GEMV_MFMA_LAUNCH(P, 3, X, R); break;                                             \
+        default: DOE_GEMV_MFMA_LAUNCH(P, 4, X, R); break;                                            \
     }
-        if (fz.attn_o) {
-            DOE_GEMV_MFMA_LAUNCH(2, 1, 0);
+        if (fz.attn_o && fz.res_nparts) {
+            DOE_GEMV_MFMA_LAUNCH(2, 1, 0, true);
+        } else if (fz.attn_o) {
+            DOE_GEMV_MFMA_LAUNCH(2, 1, 0, false);
         } else if (fz.norm_w) {
-            if (xv) DOE_GEMV_MFMA_BPW(1, 1) else DOE_GEMV_MFMA_BPW(1, 0)
+            if (xv) DOE_GEMV_MFMA_BPW(1, 1, false) else DOE_GEMV_MFMA_BPW(1, 0, false)
+        } else if (fz.res_nparts) {
+            if (xv) DOE_GEMV_MFMA_BPW(0, 1, true) else DOE_GEMV_MFMA_BPW(0, 0, true)
         } else {
-            if (xv) DOE_GEMV_MFMA_BPW(0, 1) else DOE_GEMV_MFMA_BPW(0, 0)
+            if (xv) DOE_GEMV_MFMA_BPW(0, 1, false) else DOE_GEMV_MFMA_BPW(0, 0, false)
         }
 #undef DOE_GEMV_MFMA_BPW
 #undef DOE_GEMV_MFMA_LAUNCH
@@ -1441,6 +1478,10 @@ int doe_q4k_gemv_ex(const doe_q4k_gemv_args *a, doe_stream_t stream) {
     fz.norm_offset = a->norm_weight_offset;
     fz.residual = a->residual;
     fz.gated = a->gated;
+    fz.res_parts = a->residual_parts;
+    fz.res_nparts = (int)a->residual_nparts;
+    DOE_REQUIRE(a->residual_nparts >= 0 && a->residual_nparts <= kMaxXParts, DOE_E_INVALID,
+                "residual_nparts %lld (0..%d)", (long long)a->residual_nparts, kMaxXParts);
     fz.x_parts = a->activation_parts;
     fz.x_nparts = (int)a->activation_nparts;
     fz.x_sum = a->activation_sum;

@@ -290,10 +290,9 @@ class Decoder:
             self.ple_u_views = [self.ple_u.view(li * P * 4, P * 4, np.float32) for li in range(L)]
         self.h = DeviceBuffer.empty((c.ffn,), np.float32)
         # the residual stream without atomics (Q4_K layers): o_proj and
-        # down_proj write their K ranges' row sums as parts, and the next
-        # GEMV adds the parts in order in its activation load, keeping the
-        # sum in x (entering a layer) or x_mid (after its attention block)
-        self.x_mid = DeviceBuffer.empty((c.hidden,), np.float32)
+        # down_proj write their K ranges' row sums as parts; the next GEMV
+        # adds the parts in order in its activation load, and the GEMV that
+        # adds that stream as its residual forms the same sum in its epilogue
         self.parts_o = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, c.hidden), np.float32)
         self.parts_d = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, c.hidden), np.float32)
         hb = c.hidden * 4
@@ -391,10 +390,11 @@ class Decoder:
             self._ple_inputs(stream)
         # Q4_K layers: the residual stream entering a layer is act + act_parts
         # (na parts); o_proj and down_proj write their K ranges as parts, range
-        # 0 with the residual added, and the next GEMV adds them in range
-        # order in its activation load, keeping the sum (x, x_mid) for the
-        # next residual.  So every add happens in a fixed order: a step gives
-        # the same bits on every run.
+        # 0 with the residual added; the next GEMV adds them in range order in
+        # its activation load, and the one after it (o_proj after q/k/v_proj,
+        # down_proj after gate/up_proj) adds the same parts in the same order
+        # to its residual, so the sum is never stored.  Every add happens in a
+        # fixed order: a step gives the same bits on every run.
         act, act_parts, na = self.x, None, 0
         last = len(self.layers) - 1
         for li, L in enumerate(self.layers):
@@ -411,10 +411,9 @@ class Decoder:
                         val_cache=L.v_cache, max_seq_len=c.max_seq)
             # input_norm + q/k/v_proj + rope + cache write
             ops.q4k_gemv_ex(L.wqkv, L.qkv_rows, c.hidden, activation=act, activation_parts=act_parts,
-                            activation_nparts=na, activation_sum=self.x if na else None, output=self.qkv,
+                            activation_nparts=na, output=self.qkv,
                             norm_weight=L.norm_attn, norm_eps=c.eps, norm_weight_offset=c.norm_weight_offset,
                             rope=rope, stream=stream)
-            resid = self.x if na else act
             splits = ops.attention_partials(self.q_views[li], src.k_cache, src.v_cache, self.attn_parts, batch=1,
                                             num_heads=c.heads, num_kv_heads=L.kv_heads, head_dim=hd,
                                             kv_len=0, kv_stride=c.max_seq, scale=1.0 / math.sqrt(hd),
@@ -426,17 +425,17 @@ class Decoder:
             # blocks o_proj needs more than one range)
             wo_parts = max(self.wo_parts, -(-L.q_dim // 4096))
             no = ops.q4k_gemv_ex(L.wo, c.hidden, L.q_dim, attn_partials=self.attn_parts, attn_splits=splits,
-                                 attn_num_heads=c.heads, attn_head_dim=hd, residual=resid,
-                                 output_parts=self.parts_o, max_output_parts=wo_parts, stream=stream)
-            # post_attn_norm + gate/up_proj + GeGLU over the summed parts (kept in x_mid)
+                                 attn_num_heads=c.heads, attn_head_dim=hd, residual=act, residual_parts=act_parts,
+                                 residual_nparts=na, output_parts=self.parts_o, max_output_parts=wo_parts,
+                                 stream=stream)
+            # post_attn_norm + gate/up_proj + GeGLU over the summed parts
             ops.q4k_gemv_ex(L.wgu, 2 * c.ffn, c.hidden, activation=self._po[0], activation_parts=self._po[1],
-                            activation_nparts=no - 1, activation_sum=self.x_mid if no > 1 else None,
-                            output=self.h, norm_weight=L.norm_ffn, norm_eps=c.eps,
+                            activation_nparts=no - 1, output=self.h, norm_weight=L.norm_ffn, norm_eps=c.eps,
                             norm_weight_offset=c.norm_weight_offset, gated=True, stream=stream)
-            mid = self.x_mid if no > 1 else self._po[0]
-            # down_proj + ffn_residual as K-range parts
-            nd = ops.q4k_gemv_ex(L.wd, c.hidden, c.ffn, activation=self.h, residual=mid,
-                                 output_parts=self.parts_d, max_output_parts=self.wd_parts, stream=stream)
+            # down_proj + ffn_residual (the same sum of o_proj's parts) as K-range parts
+            nd = ops.q4k_gemv_ex(L.wd, c.hidden, c.ffn, activation=self.h, residual=self._po[0],
+                                 residual_parts=self._po[1], residual_nparts=no - 1, output_parts=self.parts_d,
+                                 max_output_parts=self.wd_parts, stream=stream)
             if li == last or self.ple:
                 # the lm_head and the per-layer input block read x whole
                 self._sum_parts(self.parts_d, nd, self.x, stream)

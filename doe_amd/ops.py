@@ -354,7 +354,8 @@ class Q4kGemvArgs(C.Structure):
         ("position_dev", C.c_void_p), ("key_cache", C.c_void_p), ("val_cache", C.c_void_p),
         ("max_seq_len", C.c_int64), ("attn_partials", C.c_void_p), ("attn_splits", C.c_int64),
         ("attn_num_heads", C.c_int64), ("attn_head_dim", C.c_int64), ("output_parts", C.c_void_p),
-        ("max_output_parts", C.c_int64), ("output_nparts", C.c_void_p),
+        ("max_output_parts", C.c_int64), ("output_nparts", C.c_void_p), ("residual_parts", C.c_void_p),
+        ("residual_nparts", C.c_int64),
     ]
 
 
@@ -368,11 +369,13 @@ def q4k_gemv_ex(weight: DeviceBuffer, n: int, k: int, *, activation: DeviceBuffe
                 residual: DeviceBuffer | None = None, gated: bool = False, rope: dict | None = None,
                 attn_partials: DeviceBuffer | None = None, attn_splits: int = 0, attn_num_heads: int = 0,
                 attn_head_dim: int = 0, output_parts: DeviceBuffer | None = None, max_output_parts: int = 0,
-                stream=None) -> int:
+                residual_parts: DeviceBuffer | None = None, residual_nparts: int = 0, stream=None) -> int:
     """``doe_q4k_gemv_ex``: the Q4_K decode GEMV with every fused form, plus
     activation parts (activation + parts[0] + ... in order, the sum kept in
     ``activation_sum``) and output parts (the K ranges' row sums, one part
-    each, for the next GEMV's activation parts).  ``rope``: the keyword
+    each, for the next GEMV's activation parts) and residual parts (residual
+    + parts[0] + ... in order: the sum an earlier GEMV's activation parts
+    formed, not stored).  ``rope``: the keyword
     arguments of ``qkv_rope_kv``'s epilogue (num_heads, num_kv_heads,
     head_dim, freq_cis, position_buffer, key_cache, val_cache, max_seq_len).
     Returns the number of output parts written (1 without them)."""
@@ -399,6 +402,9 @@ def q4k_gemv_ex(weight: DeviceBuffer, n: int, k: int, *, activation: DeviceBuffe
     if residual is not None:
         _need(residual, n * 4, "residual")
         a.residual = residual.ptr
+    if residual_nparts:
+        _need(residual_parts, residual_nparts * n * 4, "residual_parts")
+        a.residual_parts, a.residual_nparts = residual_parts.ptr, residual_nparts
     a.gated = int(gated)
     if rope is not None:
         hd, nh, nkv, ms = rope["head_dim"], rope["num_heads"], rope["num_kv_heads"], rope["max_seq_len"]

@@ -185,6 +185,11 @@ int doe_q8_0_gemv_qkv_rope_kv(const void *weight_q8_0, const float *activation, 
  *     next GEMV forms by taking part 0 as its activation and the others as
  *     its activation_parts.  No norm or epilogue; the attention prologue may
  *     be used.
+ *   residual_parts: the residual is residual + residual_parts[0] + ... +
+ *     residual_parts[residual_nparts - 1] (each n floats, added in that
+ *     order; at most 4, output apart from the residual, matrix-core kernel):
+ *     a later GEMV takes the parts an earlier one added in its activation
+ *     load and forms the same sum, where activation_sum would store it.
  * So a decode layer's residual adds happen in a fixed order: bit-identical
  * results on every run, where an in-place residual K split adds atomically.
  * The other fields are those of doe_q4k_gemv_fused (norm_weight, residual,
@@ -216,6 +221,8 @@ typedef struct doe_q4k_gemv_args {
     float *output_parts;
     int64_t max_output_parts;
     int32_t *output_nparts;
+    const float *residual_parts;
+    int64_t residual_nparts;
 } doe_q4k_gemv_args;
 int doe_q4k_gemv_ex(const doe_q4k_gemv_args *args, doe_stream_t stream);
 

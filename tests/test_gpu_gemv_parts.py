@@ -3,7 +3,8 @@ the decode layer's GEMVs without atomics.  Producer: the parts summed in
 range order equal the GEMV (against the oracle, within the GEMV contract).
 Consumer: activation + parts is added in order, so a consumer given
 (x, parts) is bit-identical to the same GEMV given the host's in-order f32
-sum, and keeps that sum bit for bit.  Through the C ABI."""
+sum, and keeps that sum bit for bit; residual + parts likewise in the
+epilogue.  Through the C ABI."""
 import numpy as np
 import pytest
 
@@ -124,6 +125,51 @@ def test_activation_parts_bit_identical_to_host_sum(dev, nparts, form):
             assert np.array_equal(a.download()[:, 5].view(np.uint16), b.download()[:, 5].view(np.uint16))
 
 
+@pytest.mark.parametrize("nparts", [1, 2, 4])
+@pytest.mark.parametrize("form", ["plain", "output_parts", "attention"])
+def test_residual_parts_bit_identical_to_host_sum(dev, nparts, form):
+    # residual + parts added in order in the epilogue: the same bits as the
+    # GEMV given the host's in-order f32 sum as its residual (whole rows,
+    # K-range output parts where range 0 carries it, the attention prologue)
+    rng = np.random.default_rng(nparts * 11 + len(form))
+    n = 2304
+    res = (rng.standard_normal(n) * 4).astype(np.float32)
+    rparts = (rng.standard_normal((nparts, n)) * 0.5).astype(np.float32)
+    rs = res.copy()
+    for p in rparts:
+        rs = (rs + p).astype(np.float32)
+    if form == "attention":
+        heads, hd, S = 8, 256, 3
+        k = heads * hd
+        o = rng.standard_normal((heads, S, hd)).astype(np.float32)
+        ml = np.stack([rng.standard_normal((heads, S)) * 3, rng.uniform(1, 5, (heads, S))], -1).astype(np.float32)
+        src = dict(attn_partials=up(np.concatenate([o.reshape(-1), ml.reshape(-1)])), attn_splits=S,
+                   attn_num_heads=heads, attn_head_dim=hd)
+    else:
+        k = 9216 if form == "output_parts" else 2048
+        src = dict(activation=up(rng.standard_normal(k).astype(np.float32)))
+    dw = up(q4k.random_q4k(rng, n, k))
+    if form == "plain":
+        got, want = DeviceBuffer.empty((n,), np.float32), DeviceBuffer.empty((n,), np.float32)
+        # (a residual apart from the output: whole rows, no atomic K split)
+        ops.q4k_gemv_ex(dw, n, k, residual=up(res), residual_parts=up(rparts), residual_nparts=nparts, output=got,
+                        **src)
+        ops.q4k_gemv_ex(dw, n, k, residual=up(rs), output=want, **src)
+        dev.synchronize()
+        a, b = got.download(), want.download()
+    else:
+        got = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, n), np.float32)
+        want = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, n), np.float32)
+        n1 = ops.q4k_gemv_ex(dw, n, k, residual=up(res), residual_parts=up(rparts), residual_nparts=nparts,
+                             output_parts=got, max_output_parts=ops.MAX_GEMV_PARTS, **src)
+        n2 = ops.q4k_gemv_ex(dw, n, k, residual=up(rs), output_parts=want, max_output_parts=ops.MAX_GEMV_PARTS,
+                             **src)
+        dev.synchronize()
+        assert n1 == n2 and n1 > 1
+        a, b = got.download()[:n1], want.download()[:n2]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_parts_argument_checks(dev):
     rng = np.random.default_rng(1)
     w = up(q4k.random_q4k(rng, 64, 512))
@@ -135,6 +181,19 @@ def test_parts_argument_checks(dev):
     with pytest.raises(DoeError):  # output parts with the RMSNorm prologue (it needs whole rows)
         ops.q4k_gemv_ex(w, 64, 512, activation=x, norm_weight=x, output_parts=DeviceBuffer.empty((4, 64), np.float32),
                         max_output_parts=4)
+    r = up(np.ones(64, np.float32))
+    with pytest.raises(DoeError):  # residual parts without a residual
+        ops.q4k_gemv_ex(w, 64, 512, activation=x, residual_parts=up(np.zeros((1, 64), np.float32)),
+                        residual_nparts=1, output=y)
+    with pytest.raises(DoeError):  # residual parts with the residual in place (the atomic K split)
+        ops.q4k_gemv_ex(w, 64, 512, activation=x, residual=y, residual_parts=up(np.zeros((1, 64), np.float32)),
+                        residual_nparts=1, output=y)
+    with pytest.raises(DoeError):  # residual parts with the RMSNorm prologue
+        ops.q4k_gemv_ex(w, 64, 512, activation=x, norm_weight=x, residual=r,
+                        residual_parts=up(np.zeros((1, 64), np.float32)), residual_nparts=1, output=y)
+    with pytest.raises(DoeError):  # five residual parts
+        ops.q4k_gemv_ex(w, 64, 512, activation=x, residual=r, residual_parts=up(np.zeros((5, 64), np.float32)),
+                        residual_nparts=5, output=y)
     with pytest.raises(DoeError):  # k = 65536 needs 4 output parts, room for 2
         big = up(q4k.random_q4k(rng, 16, 65536))
         ops.q4k_gemv_ex(big, 16, 65536, activation=up(np.ones(65536, np.float32)),
