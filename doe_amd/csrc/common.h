@@ -94,29 +94,50 @@ struct DoeRopeKv {
     int q_rows, kv_rows, head_dim, max_seq;
 };
 
-__device__ __forceinline__ void doe_rope_kv_pair(const DoeRopeKv &rk, int row, float s0, float s1, float *y) {
+// The rotation of one row pair fetched ahead of its sums: the position and,
+// for q / k rows at a position inside the cache, the pair's cos / sin.
+struct DoeRopeAhead {
+    int pos;
+    float c, sn;
+    bool rot;
+};
+
+// The position as a scalar load (one value for the wave, waited for on the
+// scalar counter, so vector loads issued after it are not held back).
+__device__ __forceinline__ int doe_rope_pos_scalar(const int32_t *pos_dev) {
+    return *(const __attribute__((address_space(4))) int32_t *)pos_dev;
+}
+
+__device__ __forceinline__ void doe_rope_kv_pair_ahead(const DoeRopeKv &rk, const DoeRopeAhead &ra, int row,
+                                                       float s0, float s1, float *y) {
 #pragma clang fp contract(off)
-    const int pos = rk.pos_dev[0];
-    const bool in_cache = pos >= 0 && pos < rk.max_seq;  // freq_cis holds max_seq positions
     float r0 = s0, r1 = s1;
-    const int dim = row % rk.head_dim;
-    if (in_cache && row < rk.q_rows + rk.kv_rows) {
-        const int i = dim >> 1, half = rk.head_dim >> 1;
-        const float c = rk.freq_cis[((size_t)pos * half + i) * 2];
-        const float sn = rk.freq_cis[((size_t)pos * half + i) * 2 + 1];
-        r0 = s0 * c - s1 * sn;
-        r1 = s0 * sn + s1 * c;
+    if (ra.rot) {
+        r0 = s0 * ra.c - s1 * ra.sn;
+        r1 = s0 * ra.sn + s1 * ra.c;
     }
     y[row] = r0;
     y[row + 1] = r1;
-    if (row >= rk.q_rows && in_cache) {
+    if (row >= rk.q_rows && ra.pos >= 0 && ra.pos < rk.max_seq) {
         const int kvr = row - rk.q_rows;
         const bool is_v = kvr >= rk.kv_rows;
         const int rr = is_v ? kvr - rk.kv_rows : kvr;
         const int h = rr / rk.head_dim;
         _Float16 *cache = is_v ? rk.v_cache : rk.k_cache;
-        const size_t ci = ((size_t)h * rk.max_seq + pos) * rk.head_dim + dim;
+        const size_t ci = ((size_t)h * rk.max_seq + ra.pos) * rk.head_dim + row % rk.head_dim;
         cache[ci] = (_Float16)r0;
         cache[ci + 1] = (_Float16)r1;
     }
+}
+
+__device__ __forceinline__ void doe_rope_kv_pair(const DoeRopeKv &rk, int row, float s0, float s1, float *y) {
+    const int pos = rk.pos_dev[0];
+    DoeRopeAhead ra{pos, 1.0f, 0.0f, false};
+    if (pos >= 0 && pos < rk.max_seq && row < rk.q_rows + rk.kv_rows) {  // freq_cis holds max_seq positions
+        const int i = (row % rk.head_dim) >> 1, half = rk.head_dim >> 1;
+        ra.c = rk.freq_cis[((size_t)pos * half + i) * 2];
+        ra.sn = rk.freq_cis[((size_t)pos * half + i) * 2 + 1];
+        ra.rot = true;
+    }
+    doe_rope_kv_pair_ahead(rk, ra, row, s0, s1, y);
 }

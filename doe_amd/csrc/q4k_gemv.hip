@@ -205,11 +205,13 @@ struct GemvFusion {
 constexpr int kMaxXParts = 4;  // activation parts a GEMV adds in its prologue
 
 // Epilogue of one (even row, odd row) pair of a fused q/k/v projection.
+__device__ __forceinline__ DoeRopeKv rope_kv_of(const GemvFusion &fz) {
+    return DoeRopeKv{fz.freq_cis, fz.pos_dev, fz.k_cache, fz.v_cache, fz.q_rows, fz.kv_rows, fz.head_dim,
+                     fz.max_seq};
+}
 __device__ __forceinline__ void rope_kv_pair(const GemvFusion &fz, int row, float s0, float s1,
                                              float *__restrict__ y) {
-    const DoeRopeKv rk{fz.freq_cis, fz.pos_dev, fz.k_cache, fz.v_cache, fz.q_rows, fz.kv_rows, fz.head_dim,
-                       fz.max_seq};
-    doe_rope_kv_pair(rk, row, s0, s1, y);
+    doe_rope_kv_pair(rope_kv_of(fz), row, s0, s1, y);
 }
 
 // PRO: activation prologue -- 0 plain f32 load, 1 fused RMSNorm, 2 combine of
@@ -507,9 +509,12 @@ __device__ __forceinline__ float sum_rows4(float v) {
 // XV: the activation is read as one float4 per lane (x 16-byte aligned and
 // k % 4 == 0), else as four clamped dwords.  Both forms are branch-free so the
 // activation loads stay ahead of the weight stream.
-// RP: the residual comes with parts (fz.res_parts), a form of its own so the
-// others keep their register count.
-template <int PRO, int BPW, int XV, bool RP = false>
+// EPI: 1 the residual comes with parts (fz.res_parts); 2 the q/k/v epilogue
+// with its rotation fetched ahead (the position a scalar load at the start,
+// each row pair's cos / sin once the weight loads are out).  Forms of their
+// own, so the others keep their register count (61 VGPRs: eight waves per
+// SIMD; 65 measured slower).
+template <int PRO, int BPW, int XV, int EPI = 0>
 __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__restrict__ w,
                                                              const float *x,
                                                              float *__restrict__ y, int n, int k,
@@ -590,6 +595,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
     const bool has_res = fz.residual && blockIdx.y == 0 && (fz.y_parts || gridDim.y == 1);
     // (its parts are loaded here and added once the weight loads are out:
     // an add here would wait for them before the weight loads go out)
+    constexpr bool RP = EPI == 1, ROPE = EPI == 2;
     float rres[RP ? 1 + kMaxXParts : 1] = {};
     if (has_res && tid < 16) {
         const int rr = min(row0 + tid, n - 1);
@@ -600,6 +606,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
                 if (sp < fz.res_nparts) rres[1 + sp] = fz.res_parts[(size_t)sp * n + rr];
         }
     }
+    const int rope_pos = ROPE ? doe_rope_pos_scalar(fz.pos_dev) : 0;
     // (x is not __restrict__: with it its loads count as invariant and were
     // sunk past the weight loads; this memory clobber keeps the order)
     __asm__ volatile("" ::: "memory");
@@ -617,6 +624,16 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    // (every lane issues the two rotation loads, from an in-range position,
+    // so no path skips them and the waits count the loads exactly)
+    float rope_c = 1.0f, rope_s = 0.0f;
+    if constexpr (ROPE) {
+        const int i = ((row0 + (tid & 15)) % fz.head_dim) >> 1;
+        const int p = min(max(rope_pos, 0), fz.max_seq - 1);
+        const float *src = fz.freq_cis + ((size_t)p * (fz.head_dim >> 1) + i) * 2;
+        rope_c = src[0];
+        rope_s = src[1];
+    }
     float rpre = rres[0];
     if constexpr (RP) {
 #pragma unroll
@@ -807,6 +824,11 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
         if (fz.gated) {
             const float other = dpp<kDppXor1>(s);  // row ^ 1
             if ((tid & 1) == 0 && row < n) y[row >> 1] = doe_gelu_tanh_clamped(s) * other;
+        } else if (ROPE) {
+            const float other = dpp<kDppXor1>(s);
+            const DoeRopeAhead ra{rope_pos, rope_c, rope_s,
+                                  rope_pos >= 0 && rope_pos < fz.max_seq && row < fz.q_rows + fz.kv_rows};
+            if ((tid & 1) == 0 && row < n) doe_rope_kv_pair_ahead(rope_kv_of(fz), ra, row, s, other, y);
         } else if (fz.rope_kv) {
             const float other = dpp<kDppXor1>(s);
             if ((tid & 1) == 0 && row < n) rope_kv_pair(fz, row, s, other, y);
@@ -1335,15 +1357,17 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         default: DOE_GEMV_MFMA_LAUNCH(P, 4, X, R); break;                                            \
     }
         if (fz.attn_o && fz.res_nparts) {
-            DOE_GEMV_MFMA_LAUNCH(2, 1, 0, true);
+            DOE_GEMV_MFMA_LAUNCH(2, 1, 0, 1);
         } else if (fz.attn_o) {
-            DOE_GEMV_MFMA_LAUNCH(2, 1, 0, false);
+            DOE_GEMV_MFMA_LAUNCH(2, 1, 0, 0);
+        } else if (fz.norm_w && fz.rope_kv && bpw == 1 && xv) {
+            DOE_GEMV_MFMA_LAUNCH(1, 1, 1, 2);  // the decode step's q/k/v projection
         } else if (fz.norm_w) {
-            if (xv) DOE_GEMV_MFMA_BPW(1, 1, false) else DOE_GEMV_MFMA_BPW(1, 0, false)
+            if (xv) DOE_GEMV_MFMA_BPW(1, 1, 0) else DOE_GEMV_MFMA_BPW(1, 0, 0)
         } else if (fz.res_nparts) {
-            if (xv) DOE_GEMV_MFMA_BPW(0, 1, true) else DOE_GEMV_MFMA_BPW(0, 0, true)
+            if (xv) DOE_GEMV_MFMA_BPW(0, 1, 1) else DOE_GEMV_MFMA_BPW(0, 0, 1)
         } else {
-            if (xv) DOE_GEMV_MFMA_BPW(0, 1, false) else DOE_GEMV_MFMA_BPW(0, 0, false)
+            if (xv) DOE_GEMV_MFMA_BPW(0, 1, 0) else DOE_GEMV_MFMA_BPW(0, 0, 0)
         }
 #undef DOE_GEMV_MFMA_BPW
 #undef DOE_GEMV_MFMA_LAUNCH
