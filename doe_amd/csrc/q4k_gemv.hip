@@ -1076,6 +1076,7 @@ int g_tune_rowslots = 0;
 int g_tune_rows = 0;
 int g_tune_kernel = 0;  // 0 automatic, 1 dot-product kernel, 2 matrix-core kernel
 int g_tune_ksplit = 0;  // 0 automatic, 1 never split K over workgroups
+int g_tune_forms = 0;   // 1: the q/k/v epilogue without its fetched-ahead rotation
 int g_tune_bpw = 0;     // 0 automatic, else at least this many blocks per wave (<= 4)
 int g_tune_stream = 0;  // 0 automatic, -1 never stream, g > 0: stream g row groups per workgroup
 int g_tune_stream_depth = 0;  // 0 automatic, else 2, 4 or 6 units in flight per wave (if the LDS allows)
@@ -1360,7 +1361,7 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
             DOE_GEMV_MFMA_LAUNCH(2, 1, 0, 1);
         } else if (fz.attn_o) {
             DOE_GEMV_MFMA_LAUNCH(2, 1, 0, 0);
-        } else if (fz.norm_w && fz.rope_kv && bpw == 1 && xv) {
+        } else if (fz.norm_w && fz.rope_kv && bpw == 1 && xv && g_tune_forms == 0) {
             DOE_GEMV_MFMA_LAUNCH(1, 1, 1, 2);  // the decode step's q/k/v projection
         } else if (fz.norm_w) {
             if (xv) DOE_GEMV_MFMA_BPW(1, 1, 0) else DOE_GEMV_MFMA_BPW(1, 0, 0)
@@ -1569,6 +1570,9 @@ int doe_tune_set(const char *key, int value) {
     } else if (!strcmp(key, "q4k_gemv.ksplit")) {
         DOE_REQUIRE(value == 0 || value == 1, DOE_E_INVALID, "q4k_gemv.ksplit is 0 or 1");
         g_tune_ksplit = value;
+    } else if (!strcmp(key, "q4k_gemv.forms")) {
+        DOE_REQUIRE(value == 0 || value == 1, DOE_E_INVALID, "q4k_gemv.forms is 0 or 1");
+        g_tune_forms = value;
     } else if (!strcmp(key, "q4k_gemv.kernel")) {
         DOE_REQUIRE(value >= 0 && value <= 2, DOE_E_INVALID, "q4k_gemv.kernel is 0, 1 or 2");
         g_tune_kernel = value;
