@@ -33,12 +33,13 @@
 // meet in LDS.  When K spans more than one workgroup's 32 groups, the grid
 // splits K and each range writes its partial sums to a workspace: in the
 // one-shot kernel the last range of a row block to finish adds the ranges in
-// order (a completion count per row block, cleared at the start of every
-// call), in the streaming form a second kernel does; either way y is the
-// same bit for bit on every run.
+// order (a 64-bit count per row block that only grows: the range that brings
+// it to a multiple of the range count adds), in the streaming form a second
+// kernel does; either way y is the same bit for bit on every run.
 #include "common.h"
 
 #include <math.h>
+#include <map>
 #include <mutex>
 
 namespace {
@@ -71,7 +72,8 @@ struct Int4Args {
     const float *x;  // [M][K]
     float *out;      // one K range: y [M][N]; else the ranges' partial sums
     float *y;        // [M][N]
-    unsigned *cnt;   // one-shot kernel, K split: ranges done per row block (zero between calls)
+    unsigned long long *cnt;  // one-shot kernel, K split: ranges done per row block, a multiple of the
+                              // range count between calls
     int M, N, K, G;
 };
 
@@ -291,9 +293,13 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a, int ranges) 
     }
     // K split: the range's 512 sums ([batch][64 rows]) go to its workspace
     // slot with agent-scope stores (written through to memory); once they are
-    // complete the row block's count goes up, and the workgroup that completes
-    // it adds the ranges' slots in range order (agent-scope loads) into y and
-    // resets the count.  No workgroup waits for another.
+    // complete the row block's count goes up, and the workgroup that brings it
+    // to a multiple of the range count adds the ranges' slots in range order
+    // (agent-scope loads) into y.  No workgroup waits for another, and no
+    // count is ever reset: every call adds exactly `ranges` to each of its row
+    // blocks' counts (one region of counts per range count), so calls that
+    // overlapped on the shared workspace (and raced on its slots) leave the
+    // counts consistent for every later call.
     // Ordering: the slot stores are acknowledged (vmcnt(0)) before the count
     // is incremented, and the adding workgroup's loads are issued only after
     // its increment has returned the final count; agent-scope stores write
@@ -301,8 +307,6 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a, int ranges) 
     // read what the stores wrote.  (A release / acquire pair would say the
     // same to the compiler, but on gfx950 its agent-scope release writes back
     // the whole L2 of the XCD, measured at ~75 ns per workgroup, serialised.)
-    // The host clears the counts before every call, so a count left behind by
-    // calls that overlapped on the shared workspace does not outlive them.
     float *slot = a.out + ((size_t)rb * ranges + sp) * 512;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -311,10 +315,11 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a, int ranges) 
             if (lg < 2) __hip_atomic_store(slot + (4 * lg + i) * 64 + 16 * t + lr, yv[t][i], __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
     wait_memory();
-    unsigned done = 0;
-    if (lane == 0) done = __hip_atomic_fetch_add(a.cnt + rb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    done = __builtin_amdgcn_readfirstlane(done);
-    if (done != (unsigned)(ranges - 1)) return;
+    unsigned long long done = 0;
+    if (lane == 0) done = __hip_atomic_fetch_add(a.cnt + rb, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    done = ((unsigned long long)__builtin_amdgcn_readfirstlane((unsigned)(done >> 32)) << 32) |
+           (unsigned)__builtin_amdgcn_readfirstlane((unsigned)done);
+    if ((done + 1) % (unsigned)ranges != 0) return;
     asm volatile("" ::: "memory");
     // lane l, step j: batch j, row r0 + l; eight ranges' loads in flight at a time
     const float *base = a.out + (size_t)rb * ranges * 512 + lane;
@@ -338,7 +343,6 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a, int ranges) 
 #pragma unroll
     for (int j = 0; j < 8; ++j)
         if (j < a.M && r0 + lane < a.N) a.y[(size_t)j * a.N + r0 + lane] = sum[j];
-    if (lane == 0) __hip_atomic_store(a.cnt + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Lane (row, q) holds the four words of group g + q of its row (one 16-byte
@@ -486,8 +490,13 @@ __global__ __launch_bounds__(256) void int4_sum_ranges_kernel(const float *__res
 std::mutex g_ws_mu;
 void *g_ws = nullptr;   // partial sums of the K ranges
 size_t g_ws_bytes = 0;
-void *g_cnt = nullptr;  // one-shot kernel: ranges done per row block, zero between calls
-size_t g_cnt_bytes = 0;
+// One-shot kernel: per range count, a region of 64-bit counts (one per row
+// block), zero when allocated.
+struct CountRegion {
+    void *p = nullptr;
+    size_t bytes = 0;
+};
+std::map<int, CountRegion> g_counts;
 int g_num_cus = 0;
 int g_int4_kernel = 0;  // 0 automatic, 1 one-shot workgroups, 2 streaming
 int g_int4_depth = 3;   // streaming: row blocks in flight per wave + 1 (2 or 3)
@@ -536,39 +545,41 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     const bool one_shot = g_int4_kernel == 1 || (g_int4_kernel == 0 && !stream_ok);
 
     float *part = y;
-    unsigned *cnt = nullptr;
+    unsigned long long *cnt = nullptr;
     if (splits > 1) {
         // one-shot: [row block][range][512] slots and a count per row block;
         // streaming: [range][M][N], added by a second kernel
         const size_t need = one_shot ? (size_t)row_blocks * splits * 512 * sizeof(float)
                                      : (size_t)splits * mn * sizeof(float);
-        const size_t need_cnt = one_shot ? (size_t)row_blocks * sizeof(unsigned) : 0;
         std::lock_guard<std::mutex> lk(g_ws_mu);
-        if (g_ws_bytes < need || g_cnt_bytes < need_cnt) {
-            // queued kernels and captured graphs may still use the old buffers
-            if (g_ws_bytes < need) {
-                doe::retire_workspace(g_ws);
-                g_ws = nullptr;
-                g_ws_bytes = 0;
-                DOE_HIP_CHECK(hipMalloc(&g_ws, need));
-                g_ws_bytes = need;
-            }
-            if (g_cnt_bytes < need_cnt) {
-                doe::retire_workspace(g_cnt);
-                g_cnt = nullptr;
-                g_cnt_bytes = 0;
-                DOE_HIP_CHECK(hipMalloc(&g_cnt, need_cnt));
-                g_cnt_bytes = need_cnt;
-            }
+        // queued kernels and captured graphs may still use the old buffers
+        if (g_ws_bytes < need) {
+            doe::retire_workspace(g_ws);
+            g_ws = nullptr;
+            g_ws_bytes = 0;
+            DOE_HIP_CHECK(hipMalloc(&g_ws, need));
+            g_ws_bytes = need;
         }
         part = (float *)g_ws;
-        cnt = (unsigned *)g_cnt;
         if (one_shot) {
-            // counts start at zero on every call (a fill kernel, so the call
-            // stays capturable): a count left behind by calls that overlapped
-            // on the shared workspace is cleared here
-            const int frc = doe::fill_bytes_async(cnt, 0, need_cnt, st);
-            if (frc) return frc;
+            // the counts of this range count, zeroed once when allocated (a
+            // fill kernel on this stream, so the call stays capturable)
+            CountRegion &cr = g_counts[splits];
+            const size_t need_cnt = (size_t)row_blocks * sizeof(unsigned long long);
+            if (cr.bytes < need_cnt) {
+                doe::retire_workspace(cr.p);
+                cr.p = nullptr;
+                cr.bytes = 0;
+                DOE_HIP_CHECK(hipMalloc(&cr.p, need_cnt));
+                const int frc = doe::fill_bytes_async(cr.p, 0, need_cnt, st);
+                if (frc) {
+                    DOE_HIP_CHECK(hipFree(cr.p));
+                    cr.p = nullptr;
+                    return frc;
+                }
+                cr.bytes = need_cnt;
+            }
+            cnt = (unsigned long long *)cr.p;
         }
     }
     Int4Args a;

@@ -163,3 +163,48 @@ def test_int4_streaming_prefetch_depths(dev, ora, depth, m, n, k):
         _lib.call("doe_tune_set", b"int4_gemv.depth", 0)
     assert rel_l2(got[depth], ora.int4g32_gemv(w, s, x, m, n, k)) <= 1e-5
     assert np.array_equal(got[2], got[3])
+
+
+def test_int4_one_shot_counts_across_shapes_and_graphs(dev, ora):
+    # the one-shot kernel's per-row-block counts only grow (the range that
+    # brings a count to a multiple of the range count adds the ranges): calls
+    # of other range counts and row-block counts in between, a region that
+    # grows, and replays of a captured graph with eager calls between them all
+    # leave every later call exact and bit-identical
+    from doe_amd import Graph, Stream
+
+    rng = np.random.default_rng(21)
+    shapes = [(8, 9216, 5120), (4, 512, 2048), (8, 20000, 5120), (2, 64, 8192), (8, 9216, 3072)]
+    data = []
+    for m, n, k in shapes:
+        w, s = random_int4(rng, n, k)
+        x = rng.standard_normal((m, k), dtype=np.float32)
+        data.append((m, n, k, up(w), up(s), up(x), DeviceBuffer.empty((m, n), np.float32), w, s, x))
+    ops.tune("int4_gemv.kernel", 1)  # one-shot workgroups on every shape
+    try:
+        first = []
+        for m, n, k, dw, ds, dx, out, w, s, x in data:
+            ops.matmul_int4g32(dw, ds, dx, out, m, n, k)
+            got = out.download()
+            assert rel_l2(got, ora.int4g32_gemv(w, s, x, m, n, k)) <= 1e-5, (m, n, k)
+            first.append(got)
+        for rnd in range(3):
+            for i in ([0, 2, 1, 4, 3] if rnd % 2 else [4, 1, 3, 0, 2]):
+                m, n, k, dw, ds, dx, out, *_ = data[i]
+                ops.matmul_int4g32(dw, ds, dx, out, m, n, k)
+                assert np.array_equal(out.download(), first[i]), (rnd, i)
+        st = Stream()
+        m, n, k, dw, ds, dx, out, *_ = data[0]
+        g = Graph.capture(st, lambda: [ops.matmul_int4g32(dw, ds, dx, out, m, n, k, stream=st) for _ in range(3)])
+        for rep in range(4):
+            out.upload(np.zeros((m, n), np.float32))
+            g.launch(st)
+            st.synchronize()
+            assert np.array_equal(out.download(), first[0]), rep
+            m1, n1, k1, dw1, ds1, dx1, out1, *_ = data[1 + rep % 4]
+            ops.matmul_int4g32(dw1, ds1, dx1, out1, m1, n1, k1)
+            assert np.array_equal(out1.download(), first[1 + rep % 4]), rep
+        g.destroy()
+        st.destroy()
+    finally:
+        ops.tune("int4_gemv.kernel", 0)
