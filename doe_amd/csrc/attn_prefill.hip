@@ -77,12 +77,20 @@ __global__ __launch_bounds__(256) void v_to_f16t_kernel(const uint16_t *__restri
                                                         int kv_len, int kv_stride, int kv_pad) {
     __shared__ _Float16 tile[kBKV][kD + 2];  // [key][dim], odd dword stride
     const int kvh = blockIdx.y, key0 = blockIdx.x * kBKV, tid = threadIdx.x;
+    // the four loads go out together (a key past kv_len reads a clamped key
+    // and is zeroed after: no branch, so no load waits for the one before)
+    u32x4 wl[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int gi = tid + 256 * i, kl = gi >> 4, d0 = (gi & 15) * 8;
-        u32x4 w = {0, 0, 0, 0};
-        if (key0 + kl < kv_len)
-            w = *reinterpret_cast<const u32x4 *>(v + ((size_t)kvh * kv_stride + key0 + kl) * kD + d0);
+        const int key = max(min(key0 + kl, kv_len - 1), 0);
+        wl[i] = *reinterpret_cast<const u32x4 *>(v + ((size_t)kvh * kv_stride + key) * kD + d0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int gi = tid + 256 * i, kl = gi >> 4, d0 = (gi & 15) * 8;
+        const uint32_t keep = key0 + kl < kv_len ? 0xffffffffu : 0u;  // (an and: the load is used either way)
+        const u32x4 w = wl[i] & keep;
         const uint32_t p[4] = {bf16pair_to_f16pair(w.x), bf16pair_to_f16pair(w.y), bf16pair_to_f16pair(w.z),
                                bf16pair_to_f16pair(w.w)};
 #pragma unroll
