@@ -850,8 +850,10 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
 
 // Streaming form of the matrix-core kernel, for GEMVs of many more 16-row
 // groups than CUs: a persistent workgroup of one wave per Q4_K block (nb <=
-// 16) walks a contiguous range of row groups.  A wave's block, and so its
-// activation image, is the same in every group: it is staged once.  The
+// 16), or per two blocks (B = 2, nb <= 22: 21-block rows of the 31B-class
+// shapes as eleven waves), walks a contiguous range of row groups.  A wave's
+// blocks, and so their activation images, are the same in every group: they
+// are staged once (the activation parts, if any, added first).  The
 // weights go straight from memory into a ring of D LDS slots per wave
 // (global_load_lds_dwordx4: lane i's 16 bytes land at slot + 16 i, so granule
 // q of a unit -- row q / 9, piece q % 9 -- sits at row * 144 + piece * 16,
@@ -870,11 +872,15 @@ __global__ __launch_bounds__(1024) void q4k_gemv_mfma_kernel(const uint8_t *__re
 // per-group barrier, measured 25.0 us.)
 constexpr int kStreamMaxGroups = 16;  // row groups per workgroup (LDS row partials)
 constexpr int kStreamMinGroupsPerCu = 8;  // automatic choice: at least 8 row groups per CU
+// (two blocks per wave: from 4 -- the one-shot kernel holds one 11-wave
+// workgroup per CU there; measured at k 5376: 16384 rows 16.6 against 19.8
+// us, 21504 rows 19.4 against 24.3, 43008 rows 31.1 against 45.5)
+constexpr int kStreamMinGroupsPerCu2 = 4;
 constexpr int kStreamUnitBytes = 16 * DOE_Q4K_BLOCK_BYTES;  // 16 rows x one block
 constexpr int kStreamLdsMax = 160 * 1024;                  // one workgroup per CU
 
-size_t gemv_stream_lds_bytes(int nwaves, int depth) {
-    return (size_t)nwaves * ((size_t)depth * kStreamUnitBytes + kMfmaAImgDwords * 4) +
+size_t gemv_stream_lds_bytes(int nwaves, int depth, int bpw = 1) {
+    return (size_t)nwaves * bpw * ((size_t)depth * kStreamUnitBytes + kMfmaAImgDwords * 4) +
            (size_t)kStreamMaxGroups * 16 * nwaves * 4 + (size_t)nwaves * 4;
 }
 
@@ -888,19 +894,19 @@ __device__ __forceinline__ void wait_vmcnt() {
     __asm__ volatile("" ::: "memory");
 }
 
-template <int PRO, int XV, int D>
+template <int PRO, int XV, int D, int B = 1>
 __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__restrict__ w, const float *x,
                                                                float *__restrict__ y, int n, int k, int nb,
                                                                int ngroups, GemvFusion fz) {
     constexpr bool NORM = PRO == 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-    uint8_t *ring = lds + (size_t)wave * D * kStreamUnitBytes;                        // [D][16 rows][144]
-    uint32_t *aimg = reinterpret_cast<uint32_t *>(lds + (size_t)nwaves * D * kStreamUnitBytes +
-                                                  (size_t)wave * kMfmaAImgDwords * 4);
-    float *rpart = reinterpret_cast<float *>(lds + (size_t)nwaves * (D * kStreamUnitBytes + kMfmaAImgDwords * 4));
+    // per wave: D ring slots of B units ([16 rows][144] each), then B images
+    uint8_t *ring = lds + (size_t)wave * D * B * kStreamUnitBytes;
+    uint32_t *aimg = reinterpret_cast<uint32_t *>(lds + (size_t)nwaves * D * B * kStreamUnitBytes +
+                                                  (size_t)wave * B * kMfmaAImgDwords * 4);
+    float *rpart = reinterpret_cast<float *>(lds + (size_t)nwaves * B * (D * kStreamUnitBytes + kMfmaAImgDwords * 4));
     float *ssq = rpart + kStreamMaxGroups * 16 * nwaves;  // [nwaves]
-    const int b = wave;
     // this workgroup's groups [g0, g1): a balanced contiguous split (the host
     // keeps g1 - g0 <= kStreamMaxGroups)
     const int g0 = (int)(((int64_t)blockIdx.x * ngroups) / gridDim.x);
@@ -908,39 +914,63 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
     const int my = g1 - g0;
     const int glast = min(max(g1 - 1, g0), ngroups - 1);
 
-    // Activation (and norm weight) loads first; they are waited on (vmcnt 0)
-    // before the ring's first loads are issued.
-    float v[4], nwv[4];
-    const int e = b * 256 + lane * 4;
-    if (XV) {
-        const float4 f = *reinterpret_cast<const float4 *>(x + min(e, k - 4));  // masked below
-        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-    } else {
+    // Activation (norm weight, activation parts) loads first; they are waited
+    // on (vmcnt 0) before the ring's first loads are issued.  Wave w owns
+    // blocks B w .. B w + B - 1 (a block past nb reads as zero activations and
+    // a clamped copy of the last block's weights).
+    float v[B][4], nwv[B][4];
+    float4 xp[B][kMaxXParts];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = x[min(e + j, k - 1)];
-    }
-    if (NORM && XV) {
-        const float4 f = *reinterpret_cast<const float4 *>(fz.norm_w + min(e, k - 4));
-        nwv[0] = f.x; nwv[1] = f.y; nwv[2] = f.z; nwv[3] = f.w;
-    } else if (NORM) {
+    for (int u = 0; u < B; ++u) {
+        const int e = (wave * B + u) * 256 + lane * 4;
+        if (XV) {
+            const float4 f = *reinterpret_cast<const float4 *>(x + min(e, k - 4));  // masked below
+            v[u][0] = f.x; v[u][1] = f.y; v[u][2] = f.z; v[u][3] = f.w;
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) nwv[j] = fz.norm_w[min(e + j, k - 1)];
+            for (int j = 0; j < 4; ++j) v[u][j] = x[min(e + j, k - 1)];
+        }
+#pragma unroll
+        for (int sp = 0; sp < kMaxXParts; ++sp) {
+            if (sp < fz.x_nparts) {
+                const float *pp = fz.x_parts + (size_t)sp * k;
+                if (XV) {
+                    xp[u][sp] = *reinterpret_cast<const float4 *>(pp + min(e, k - 4));
+                } else {
+                    xp[u][sp] = make_float4(pp[min(e, k - 1)], pp[min(e + 1, k - 1)], pp[min(e + 2, k - 1)],
+                                            pp[min(e + 3, k - 1)]);
+                }
+            }
+        }
+        if (NORM && XV) {
+            const float4 f = *reinterpret_cast<const float4 *>(fz.norm_w + min(e, k - 4));
+            nwv[u][0] = f.x; nwv[u][1] = f.y; nwv[u][2] = f.z; nwv[u][3] = f.w;
+        } else if (NORM) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) nwv[u][j] = fz.norm_w[min(e + j, k - 1)];
+        }
     }
     wait_vmcnt<0>();
     const size_t rowbytes = (size_t)nb * DOE_Q4K_BLOCK_BYTES;
-    // group gi (clamped to the range), block b, into ring slot d: three load
-    // instructions (lanes 0..63, 64..127 and 128..143 of the 144 granules)
+    // group gi (clamped to the range), the wave's B blocks, into ring slot d:
+    // three load instructions per block (lanes 0..63, 64..127 and 128..143
+    // of the 144 granules)
     auto load_unit = [&](int gi, int d) __attribute__((always_inline)) {
         gi = min(gi, glast);
-        uint8_t *slot = ring + d * kStreamUnitBytes;
 #pragma unroll
-        for (int s = 0; s < 3; ++s) {
-            const int q = min(lane + 64 * s, 143);
-            const int r = min(gi * 16 + q / 9, n - 1);
-            const uint8_t *src = w + (size_t)r * rowbytes + (size_t)b * DOE_Q4K_BLOCK_BYTES + (q % 9) * 16;
-            if (s < 2 || lane < 16)
-                __builtin_amdgcn_global_load_lds((const void *)src,
-                                                 (__attribute__((address_space(3))) void *)(slot + s * 1024), 16, 0, 0);
+        for (int u = 0; u < B; ++u) {
+            const int bu = min(wave * B + u, nb - 1);
+            uint8_t *slot = ring + (size_t)(d * B + u) * kStreamUnitBytes;
+#pragma unroll
+            for (int s = 0; s < 3; ++s) {
+                const int q = min(lane + 64 * s, 143);
+                const int r = min(gi * 16 + q / 9, n - 1);
+                const uint8_t *src = w + (size_t)r * rowbytes + (size_t)bu * DOE_Q4K_BLOCK_BYTES + (q % 9) * 16;
+                if (s < 2 || lane < 16)
+                    __builtin_amdgcn_global_load_lds((const void *)src,
+                                                     (__attribute__((address_space(3))) void *)(slot + s * 1024), 16,
+                                                     0, 0);
+            }
         }
     };
 #pragma unroll
@@ -948,33 +978,46 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
 
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        if (e + j >= k) v[j] = 0.0f;
-        if (NORM) {
-            ss = fmaf(v[j], v[j], ss);
-            v[j] *= fz.norm_offset ? 1.0f + nwv[j] : nwv[j];
+    for (int u = 0; u < B; ++u) {
+        const int e = (wave * B + u) * 256 + lane * 4;
+#pragma unroll
+        for (int sp = 0; sp < kMaxXParts; ++sp) {
+            if (sp < fz.x_nparts) {  // x + part 0 + part 1 + ..., in that order
+                v[u][0] += xp[u][sp].x; v[u][1] += xp[u][sp].y; v[u][2] += xp[u][sp].z; v[u][3] += xp[u][sp].w;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (e + j >= k) v[u][j] = 0.0f;
+            if (NORM) {
+                ss = fmaf(v[u][j], v[u][j], ss);
+                v[u][j] *= fz.norm_offset ? 1.0f + nwv[u][j] : nwv[u][j];
+            }
         }
     }
     if (NORM) {
         ss = sum_rows4(sum16(ss));
         if (lane == 0) ssq[wave] = ss;
     }
-    // The block's activation image, staged once (as the one-shot kernel's
+    // Each block's activation image, staged once (as the one-shot kernel's
     // stage(): lane 16 g + i holds chunk g, quad i).
     const int g = lane >> 4, i16 = lane & 15, m = lane & 15;
     const int nchunk = (k + 63) >> 6;
-    float sxl, sxh;
-    int sgm = 0;
-    {
-        const float ssum = sum8((v[0] + v[1]) + (v[2] + v[3]));
+    float sxl[B], sxh[B], lo_scale[B], hi_scale[B];
+    u32x4 areg[B][8];  // the blocks' A operands: the same in every group
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+        uint32_t *img = aimg + u * kMfmaAImgDwords;
+        const float ssum = sum8((v[u][0] + v[u][1]) + (v[u][2] + v[u][3]));
         const float sother = dpp<kDppMirror>(ssum);
-        sxl = i16 < 8 ? ssum : sother;
-        sxh = i16 < 8 ? sother : ssum;
-        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        sxl[u] = i16 < 8 ? ssum : sother;
+        sxh[u] = i16 < 8 ? sother : ssum;
+        float amax = fmaxf(fmaxf(fabsf(v[u][0]), fabsf(v[u][1])), fmaxf(fabsf(v[u][2]), fabsf(v[u][3])));
         amax = fmaxf(amax, dpp<kDppXor1>(amax));
         amax = fmaxf(amax, dpp<kDppXor2>(amax));
         amax = fmaxf(amax, dpp<kDppHalfMirror>(amax));
         amax = fmaxf(amax, dpp<kDppMirror>(amax));
+        int sgm = 0;
         if (amax > 0.0f && amax <= 3.0e38f) {
             sgm = 14 - __builtin_amdgcn_frexp_expf(amax);
             sgm = sgm < -100 ? -100 : (sgm > 100 ? 100 : sgm);
@@ -983,57 +1026,66 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
         _Float16 hi[4], lo[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float t = v[j] * xs;
+            const float t = v[u][j] * xs;
             hi[j] = (_Float16)t;
             lo[j] = (_Float16)(t - (float)hi[j]);
         }
         const int s = i16 >> 3, jj = i16 & 7;
         const uint32_t h0 = pack_half2(hi[0], hi[2]), h1 = pack_half2(hi[1], hi[3]);
         const uint32_t l0 = pack_half2(lo[0], lo[2]), l1 = pack_half2(lo[1], lo[3]);
-        uint32_t *dst = aimg + jj * kMfmaAStep + g * 16 + s * 4;
+        uint32_t *dst = img + jj * kMfmaAStep + g * 16 + s * 4;
         *reinterpret_cast<u32x4 *>(dst) = s ? u32x4{0, 0, h0, h1} : u32x4{h0, h1, 0, 0};
         *reinterpret_cast<u32x4 *>(dst + 8) = s ? u32x4{0, 0, l0, l1} : u32x4{l0, l1, 0, 0};
-        if (lane < 8) *reinterpret_cast<u32x4 *>(aimg + lane * kMfmaAStep + 64) = u32x4{0, 0, 0, 0};
+        if (lane < 8) *reinterpret_cast<u32x4 *>(img + lane * kMfmaAStep + 64) = u32x4{0, 0, 0, 0};
+        lo_scale[u] = __builtin_amdgcn_ldexpf(1.0f, 24 - sgm);
+        hi_scale[u] = __builtin_amdgcn_ldexpf(1.0f, 20 - sgm);
     }
     __builtin_amdgcn_wave_barrier();
-    const int c = 4 * b + g;
-    const bool act = (m >> 2) == g && c < nchunk;
-    const int abase = act ? g * 16 + (m & 1) * 8 + ((m >> 1) & 1) * 4 : 64;
-    const float lo_scale = __builtin_amdgcn_ldexpf(1.0f, 24 - sgm), hi_scale = __builtin_amdgcn_ldexpf(1.0f, 20 - sgm);
-    u32x4 areg[8];  // the block's A operands: the same in every group
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) areg[jj] = *reinterpret_cast<const u32x4 *>(aimg + jj * kMfmaAStep + abase);
+    for (int u = 0; u < B; ++u) {
+        const int c = 4 * (wave * B + u) + g;
+        const bool act = (m >> 2) == g && c < nchunk;
+        const int abase = act ? g * 16 + (m & 1) * 8 + ((m >> 1) & 1) * 4 : 64;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+            areg[u][jj] = *reinterpret_cast<const u32x4 *>(aimg + u * kMfmaAImgDwords + jj * kMfmaAStep + abase);
+    }
 
     for (int j0 = 0; j0 < my; j0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int j = j0 + d;
-            // slot d's three loads are the oldest of the 3 D in flight
-            wait_vmcnt<3 * (D - 1)>();
+            // slot d's 3 B loads are the oldest of the 3 B D in flight
+            wait_vmcnt<3 * B * (D - 1)>();
             if (j < my) {  // wave-uniform; LDS and arithmetic only
-                const uint8_t *rp = ring + d * kStreamUnitBytes + i16 * DOE_Q4K_BLOCK_BYTES;  // lane (g, row i16)
-                const u32x4 hdr = *reinterpret_cast<const u32x4 *>(rp);
-                const u32x4 qa = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
-                const u32x4 qb = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
-                f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const uint32_t dw = jj < 4 ? qa[jj] : qb[jj - 4], ew = dw >> 8;
-                    const u32x4 bw = {dw & 0x000f000fu, ew & 0x000f000fu, dw & 0x00f000f0u, ew & 0x00f000f0u};
-                    acc[jj & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, areg[jj]),
-                                                                         __builtin_bit_cast(half8, bw), acc[jj & 1], 0, 0, 0);
-                }
-                const f32x4 dsum = acc[0] + acc[1];
                 float part = 0.0f;
-                if (c < nchunk) {
-                    uint32_t scp, mnp;
-                    q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
-                    const float d_ = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
-                    const float qx_lo = (dsum[0] + dsum[1]) * lo_scale;
-                    const float qx_hi = (dsum[2] + dsum[3]) * hi_scale;
-                    const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
-                    const float m_lo = (float)(mnp & 0xffu), m_hi = (float)(mnp >> 8);
-                    part = d_ * (sc_lo * qx_lo + sc_hi * qx_hi) - dmin * (m_lo * sxl + m_hi * sxh);
+#pragma unroll
+                for (int u = 0; u < B; ++u) {
+                    const uint8_t *rp = ring + (size_t)(d * B + u) * kStreamUnitBytes +
+                                        i16 * DOE_Q4K_BLOCK_BYTES;  // lane (g, row i16)
+                    const u32x4 hdr = *reinterpret_cast<const u32x4 *>(rp);
+                    const u32x4 qa = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
+                    const u32x4 qb = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
+                    f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const uint32_t dw = jj < 4 ? qa[jj] : qb[jj - 4], ew = dw >> 8;
+                        const u32x4 bw = {dw & 0x000f000fu, ew & 0x000f000fu, dw & 0x00f000f0u, ew & 0x00f000f0u};
+                        acc[jj & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8, areg[u][jj]), __builtin_bit_cast(half8, bw), acc[jj & 1], 0, 0,
+                            0);
+                    }
+                    const f32x4 dsum = acc[0] + acc[1];
+                    if (4 * (wave * B + u) + g < nchunk) {
+                        uint32_t scp, mnp;
+                        q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
+                        const float d_ = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
+                        const float qx_lo = (dsum[0] + dsum[1]) * lo_scale[u];
+                        const float qx_hi = (dsum[2] + dsum[3]) * hi_scale[u];
+                        const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
+                        const float m_lo = (float)(mnp & 0xffu), m_hi = (float)(mnp >> 8);
+                        part += d_ * (sc_lo * qx_lo + sc_hi * qx_hi) - dmin * (m_lo * sxl[u] + m_hi * sxh[u]);
+                    }
                 }
                 part = sum_rows4(part);
                 if (lane < 16) rpart[(j * 16 + lane) * nwaves + wave] = part;
@@ -1282,19 +1334,25 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     DOE_REQUIRE(!xparts || bpw <= 2, DOE_E_UNSUPPORTED,
                 "activation parts need k <= 8192 (two Q4_K blocks per wave; got k=%lld)", (long long)k);
     DOE_REQUIRE(!fz.x_sum || ksplit == 1, DOE_E_UNSUPPORTED, "the activation sum needs whole rows");
-    const bool stream_ok =
-        use_mfma && bpw == 1 && ksplit == 1 && !fz.attn_o && !xparts && !fz.y_parts && !fz.res_nparts;
-    if (stream_ok && (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups >= kStreamMinGroupsPerCu * g_num_cus))) {
-        const int nwaves = nb;
+    // (two blocks per wave while the ring and images fit the LDS: k <= 22
+    // blocks; activation parts summed in its prologue, the sum not kept)
+    const bool stream_ok = use_mfma && (bpw == 1 || (bpw == 2 && gemv_stream_lds_bytes((nb + 1) / 2, 2, 2) <=
+                                                                      (size_t)kStreamLdsMax)) &&
+                           ksplit == 1 && !fz.attn_o && !fz.x_sum && !fz.y_parts && !fz.res_nparts;
+    const int stream_min = bpw == 2 ? kStreamMinGroupsPerCu2 : kStreamMinGroupsPerCu;
+    if (stream_ok && (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups >= stream_min * g_num_cus))) {
+        const int sb = bpw;  // blocks per wave
+        const int nwaves = (nb + sb - 1) / sb;
         // ring depth 2: deeper rings measured slower (65536 x 2304: 21.4 us
         // at 2, 23.0 at 3, 23.4 at 4, 25.8 at 6) -- the more units each wave
         // has in flight, the further a workgroup's waves drift apart over
         // the groups and the less DRAM row locality their reads keep
         int depth = 2;
-        if (g_tune_stream_depth > 0 && gemv_stream_lds_bytes(nwaves, g_tune_stream_depth) <= kStreamLdsMax)
+        if (sb == 1 && g_tune_stream_depth > 0 && gemv_stream_lds_bytes(nwaves, g_tune_stream_depth) <= kStreamLdsMax)
             depth = g_tune_stream_depth;
-        const size_t lds = gemv_stream_lds_bytes(nwaves, depth);
-        const bool xv = ((uintptr_t)activation & 15) == 0 && (k & 3) == 0 && ((uintptr_t)fz.norm_w & 15) == 0;
+        const size_t lds = gemv_stream_lds_bytes(nwaves, depth, sb);
+        const bool xv = ((uintptr_t)activation & 15) == 0 && (k & 3) == 0 && ((uintptr_t)fz.norm_w & 15) == 0 &&
+                        ((uintptr_t)fz.x_parts & 15) == 0;
         static const hipError_t attr_all = [] {
             hipError_t e = hipSuccess;
             for (const void *f : {(const void *)q4k_gemv_stream_kernel<0, 0, 2>, (const void *)q4k_gemv_stream_kernel<0, 1, 2>,
@@ -1304,7 +1362,9 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
                                   (const void *)q4k_gemv_stream_kernel<0, 0, 6>, (const void *)q4k_gemv_stream_kernel<0, 1, 6>,
                                   (const void *)q4k_gemv_stream_kernel<1, 0, 6>, (const void *)q4k_gemv_stream_kernel<1, 1, 6>,
                                   (const void *)q4k_gemv_stream_kernel<0, 0, 3>, (const void *)q4k_gemv_stream_kernel<0, 1, 3>,
-                                  (const void *)q4k_gemv_stream_kernel<1, 0, 3>, (const void *)q4k_gemv_stream_kernel<1, 1, 3>})
+                                  (const void *)q4k_gemv_stream_kernel<1, 0, 3>, (const void *)q4k_gemv_stream_kernel<1, 1, 3>,
+                                  (const void *)q4k_gemv_stream_kernel<0, 0, 2, 2>, (const void *)q4k_gemv_stream_kernel<0, 1, 2, 2>,
+                                  (const void *)q4k_gemv_stream_kernel<1, 0, 2, 2>, (const void *)q4k_gemv_stream_kernel<1, 1, 2, 2>})
                 if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kStreamLdsMax);
             return e;
         }();
@@ -1319,7 +1379,10 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
                        activation, output, (int)n, (int)k, nb, (int)row_groups, fz)
 #define DOE_GEMV_STREAM_DEPTH(P, X)                                                                       \
     do {                                                                                                  \
-        if (depth == 4) DOE_GEMV_STREAM_LAUNCH(P, X, 4);                                                 \
+        if (sb == 2)                                                                                      \
+            hipLaunchKernelGGL((q4k_gemv_stream_kernel<P, X, 2, 2>), dim3((unsigned)grid), dim3(64 * nwaves), lds, \
+                               st, wp, activation, output, (int)n, (int)k, nb, (int)row_groups, fz);     \
+        else if (depth == 4) DOE_GEMV_STREAM_LAUNCH(P, X, 4);                                            \
         else if (depth == 6) DOE_GEMV_STREAM_LAUNCH(P, X, 6);                                            \
         else if (depth == 3) DOE_GEMV_STREAM_LAUNCH(P, X, 3);                                            \
         else DOE_GEMV_STREAM_LAUNCH(P, X, 2);                                                            \

@@ -311,3 +311,79 @@ def test_gemv_streaming_fused_forms(dev, ora, stream_groups):
     kg = kc.download()
     assert rel_l2(kg[:, pos].astype(np.float32),
                   ops.interleave_rope_rows(qk[qd:], d).reshape(hkv, d).astype(np.float32)) < 1e-3
+
+
+@pytest.mark.parametrize("stream_groups", [1, 3, 11], indirect=True)
+@pytest.mark.parametrize("n,k", [(16384, 5376), (1000, 4352), (77, 5376), (4100, 5632)])
+def test_gemv_streaming_two_blocks_per_wave(dev, ora, n, k, stream_groups):
+    # rows of 17..22 Q4_K blocks: the streaming kernel with two blocks per
+    # wave (the last wave's second block past the row where the count is odd)
+    print(f"[gemv stream 2bpw {stream_groups}] {n}x{k}", flush=True)
+    rng = np.random.default_rng(n + k + 7 * stream_groups)
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    err = rel_l2(_gemv(w, x, n, k), ora.q4k_gemv(w, x, n, k))
+    assert err < 1e-5, err
+
+
+@pytest.mark.parametrize("form", ["norm_gated_parts", "rope_parts", "residual"])
+def test_gemv_streaming_two_blocks_bit_identical_to_one_shot(dev, form):
+    # the two-blocks-per-wave streaming kernel and the one-shot kernel sum
+    # every block, wave and row in the same order: the same bits, with the
+    # RMSNorm prologue and activation parts, the gated and RoPE / KV-cache
+    # epilogues, and the residual
+    from doe_amd.model import rope_table
+
+    rng = np.random.default_rng(len(form))
+    k = 5376
+    up = DeviceBuffer.from_array
+    x = up((rng.standard_normal(k) * 2).astype(np.float32))
+    parts = up((rng.standard_normal((2, k)) * 0.5).astype(np.float32))
+    nw = up((0.1 * rng.standard_normal(k)).astype(np.float32))
+    outs = []
+    for st in (3, -1):  # streaming (three row groups per workgroup), then never
+        ops.tune("q4k_gemv.stream", st)
+        try:
+            if form == "norm_gated_parts":
+                n = 4096
+                w = up(q4k.random_q4k(np.random.default_rng(1), n, k))
+                y = DeviceBuffer.empty((n // 2,), np.float32)
+                ops.q4k_gemv_ex(w, n, k, activation=x, activation_parts=parts, activation_nparts=2, output=y,
+                                norm_weight=nw, norm_eps=1e-6, gated=True)
+                outs.append([y.download()])
+            elif form == "rope_parts":
+                hq, hkv, d, ms = 8, 4, 256, 16
+                n = (hq + 2 * hkv) * d
+                w = up(q4k.random_q4k(np.random.default_rng(2), n, k))
+                y = DeviceBuffer.empty((n,), np.float32)
+                kc = DeviceBuffer.from_array(np.zeros((hkv, ms, d), np.float16))
+                vc = DeviceBuffer.from_array(np.zeros((hkv, ms, d), np.float16))
+                r = dict(num_heads=hq, num_kv_heads=hkv, head_dim=d, freq_cis=up(rope_table(ms, d, 10000.0)),
+                         position_buffer=up(np.array([7], np.int32)), key_cache=kc, val_cache=vc, max_seq_len=ms)
+                ops.q4k_gemv_ex(w, n, k, activation=x, activation_parts=parts, activation_nparts=1, output=y,
+                                norm_weight=nw, norm_eps=1e-6, rope=r)
+                outs.append([y.download(), kc.download().view(np.uint16), vc.download().view(np.uint16)])
+            else:
+                n = 3000
+                w = up(q4k.random_q4k(np.random.default_rng(3), n, k))
+                res = up(np.random.default_rng(4).standard_normal(n).astype(np.float32))
+                y = DeviceBuffer.empty((n,), np.float32)
+                ops.q4k_gemv_ex(w, n, k, activation=x, output=y, residual=res)
+                outs.append([y.download()])
+        finally:
+            ops.tune("q4k_gemv.stream", 0)
+    dev.synchronize()
+    for a, b in zip(*outs):
+        assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                              b.view(np.uint32) if b.dtype == np.float32 else b)
+
+
+def test_gemv_streaming_two_blocks_automatic(dev, ora):
+    # the 31B-class gate/up shape (43008 x 5376, 2688 row groups): streamed
+    # automatically with two blocks per wave
+    n, k = 43008, 5376
+    rng = np.random.default_rng(43)
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    err = rel_l2(_gemv(w, x, n, k), ora.q4k_gemv(w, x, n, k))
+    assert err < 1e-5, err
