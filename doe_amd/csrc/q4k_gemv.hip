@@ -897,8 +897,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <int PRO, int XV, int D, int B = 1>
 __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__restrict__ w, const float *x,
                                                                float *__restrict__ y, int n, int k, int nb,
-                                                               int ngroups, GemvFusion fz) {
+                                                               int ngroups, int nbs, GemvFusion fz) {
     constexpr bool NORM = PRO == 1;
+    // K range blockIdx.y: blocks [kb0, kb1) (the whole row when not split);
+    // a split GEMV writes each range's row sums to its output part
+    const int kb0 = (int)blockIdx.y * nbs, kb1 = min(nb, kb0 + nbs);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
     // per wave: D ring slots of B units ([16 rows][144] each), then B images
@@ -922,7 +925,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
     float4 xp[B][kMaxXParts];
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-        const int e = (wave * B + u) * 256 + lane * 4;
+        const int e = (kb0 + wave * B + u) * 256 + lane * 4;
         if (XV) {
             const float4 f = *reinterpret_cast<const float4 *>(x + min(e, k - 4));  // masked below
             v[u][0] = f.x; v[u][1] = f.y; v[u][2] = f.z; v[u][3] = f.w;
@@ -959,7 +962,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
         gi = min(gi, glast);
 #pragma unroll
         for (int u = 0; u < B; ++u) {
-            const int bu = min(wave * B + u, nb - 1);
+            const int bu = min(kb0 + wave * B + u, kb1 - 1);
             uint8_t *slot = ring + (size_t)(d * B + u) * kStreamUnitBytes;
 #pragma unroll
             for (int s = 0; s < 3; ++s) {
@@ -979,7 +982,8 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-        const int e = (wave * B + u) * 256 + lane * 4;
+        const int e = (kb0 + wave * B + u) * 256 + lane * 4;
+        const int e_end = min(k, kb1 * 256);  // past the range: zero (a block of the next range)
 #pragma unroll
         for (int sp = 0; sp < kMaxXParts; ++sp) {
             if (sp < fz.x_nparts) {  // x + part 0 + part 1 + ..., in that order
@@ -988,7 +992,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            if (e + j >= k) v[u][j] = 0.0f;
+            if (e + j >= e_end) v[u][j] = 0.0f;
             if (NORM) {
                 ss = fmaf(v[u][j], v[u][j], ss);
                 v[u][j] *= fz.norm_offset ? 1.0f + nwv[u][j] : nwv[u][j];
@@ -1043,7 +1047,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-        const int c = 4 * (wave * B + u) + g;
+        const int c = 4 * (kb0 + wave * B + u) + g;
         const bool act = (m >> 2) == g && c < nchunk;
         const int abase = act ? g * 16 + (m & 1) * 8 + ((m >> 1) & 1) * 4 : 64;
 #pragma unroll
@@ -1076,7 +1080,7 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
                             0);
                     }
                     const f32x4 dsum = acc[0] + acc[1];
-                    if (4 * (wave * B + u) + g < nchunk) {
+                    if (kb0 + wave * B + u < kb1 && 4 * (kb0 + wave * B + u) + g < nchunk) {
                         uint32_t scp, mnp;
                         q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
                         const float d_ = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
@@ -1118,7 +1122,18 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
             if ((r16 & 1) == 0 && row < n) rope_kv_pair(fz, row, row_sum(t), row_sum(t + 1), y);
         } else if (row < n) {
             const float sv = row_sum(t);
-            y[row] = fz.residual ? sv + fz.residual[row] : sv;
+            // the residual (and its parts, added in order) with range 0
+            float r = sv;
+            if (fz.residual && blockIdx.y == 0) {
+                float rs = fz.residual[row];
+                for (int sp = 0; sp < fz.res_nparts; ++sp) rs += fz.res_parts[(size_t)sp * n + row];
+                r = sv + rs;
+            }
+            if (fz.y_parts)  // written through (agent scope), as the one-shot kernel's parts
+                __hip_atomic_store(fz.y_parts + (size_t)blockIdx.y * n + row, r, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            else
+                y[row] = r;
         }
     }
 }
@@ -1336,13 +1351,17 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     DOE_REQUIRE(!fz.x_sum || ksplit == 1, DOE_E_UNSUPPORTED, "the activation sum needs whole rows");
     // (two blocks per wave while the ring and images fit the LDS: k <= 22
     // blocks; activation parts summed in its prologue, the sum not kept)
-    const bool stream_ok = use_mfma && (bpw == 1 || (bpw == 2 && gemv_stream_lds_bytes((nb + 1) / 2, 2, 2) <=
+    // (two blocks per wave while the ring and images fit the LDS: up to 22
+    // blocks per row or K range; activation parts summed in its prologue,
+    // the sum not kept; K ranges only as output parts)
+    const bool stream_ok = use_mfma && (bpw == 1 || (bpw == 2 && gemv_stream_lds_bytes((nbs + 1) / 2, 2, 2) <=
                                                                       (size_t)kStreamLdsMax)) &&
-                           ksplit == 1 && !fz.attn_o && !fz.x_sum && !fz.y_parts && !fz.res_nparts;
+                           (ksplit == 1 || fz.y_parts) && !fz.attn_o && !fz.x_sum;
     const int stream_min = bpw == 2 ? kStreamMinGroupsPerCu2 : kStreamMinGroupsPerCu;
-    if (stream_ok && (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups >= stream_min * g_num_cus))) {
+    if (stream_ok &&
+        (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups * ksplit >= (int64_t)stream_min * g_num_cus))) {
         const int sb = bpw;  // blocks per wave
-        const int nwaves = (nb + sb - 1) / sb;
+        const int nwaves = (nbs + sb - 1) / sb;
         // ring depth 2: deeper rings measured slower (65536 x 2304: 21.4 us
         // at 2, 23.0 at 3, 23.4 at 4, 25.8 at 6) -- the more units each wave
         // has in flight, the further a workgroup's waves drift apart over
@@ -1370,18 +1389,19 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         }();
         DOE_HIP_CHECK(attr_all);
         // groups per workgroup: forced, or one workgroup per CU (LDS-bound)
-        // with at most kStreamMaxGroups each
-        int64_t per_wg = g_tune_stream > 0 ? g_tune_stream : (row_groups + g_num_cus - 1) / g_num_cus;
+        // over the row groups of every K range, at most kStreamMaxGroups each
+        int64_t per_wg = g_tune_stream > 0 ? g_tune_stream : (row_groups * ksplit + g_num_cus - 1) / g_num_cus;
         if (per_wg > kStreamMaxGroups) per_wg = kStreamMaxGroups;
         const int64_t grid = (row_groups + per_wg - 1) / per_wg;
+        const dim3 sgrid((unsigned)grid, (unsigned)ksplit);
 #define DOE_GEMV_STREAM_LAUNCH(P, X, D)                                                                   \
-    hipLaunchKernelGGL((q4k_gemv_stream_kernel<P, X, D>), dim3((unsigned)grid), dim3(64 * nwaves), lds, st, wp, \
-                       activation, output, (int)n, (int)k, nb, (int)row_groups, fz)
+    hipLaunchKernelGGL((q4k_gemv_stream_kernel<P, X, D>), sgrid, dim3(64 * nwaves), lds, st, wp, activation, output, \
+                       (int)n, (int)k, nb, (int)row_groups, nbs, fz)
 #define DOE_GEMV_STREAM_DEPTH(P, X)                                                                       \
     do {                                                                                                  \
         if (sb == 2)                                                                                      \
-            hipLaunchKernelGGL((q4k_gemv_stream_kernel<P, X, 2, 2>), dim3((unsigned)grid), dim3(64 * nwaves), lds, \
-                               st, wp, activation, output, (int)n, (int)k, nb, (int)row_groups, fz);     \
+            hipLaunchKernelGGL((q4k_gemv_stream_kernel<P, X, 2, 2>), sgrid, dim3(64 * nwaves), lds, st, wp,      \
+                               activation, output, (int)n, (int)k, nb, (int)row_groups, nbs, fz);        \
         else if (depth == 4) DOE_GEMV_STREAM_LAUNCH(P, X, 4);                                            \
         else if (depth == 6) DOE_GEMV_STREAM_LAUNCH(P, X, 6);                                            \
         else if (depth == 3) DOE_GEMV_STREAM_LAUNCH(P, X, 3);                                            \

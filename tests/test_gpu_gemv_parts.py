@@ -198,3 +198,35 @@ def test_parts_argument_checks(dev):
         big = up(q4k.random_q4k(rng, 16, 65536))
         ops.q4k_gemv_ex(big, 16, 65536, activation=up(np.ones(65536, np.float32)),
                         output_parts=DeviceBuffer.empty((2, 16), np.float32), max_output_parts=2)
+
+
+@pytest.mark.parametrize("n,k,nres", [(5376, 21504, 1), (2304, 9216, 2), (3000, 8192, 0)])
+def test_streaming_output_parts_bit_identical_to_one_shot(dev, ora, n, k, nres):
+    # K ranges as output parts through the streaming kernel (two blocks per
+    # wave where a range holds 17..22 blocks), range 0 with the residual and
+    # its parts: the same parts, bit for bit, as the one-shot kernel's, and
+    # their sum the GEMV
+    rng = np.random.default_rng(n + k + nres)
+    w = up(q4k.random_q4k(rng, n, k))
+    xh = rng.standard_normal(k).astype(np.float32)
+    res = (rng.standard_normal(n) * 3).astype(np.float32)
+    rparts = (rng.standard_normal((max(nres, 1), n)) * 0.5).astype(np.float32)
+    x, dres, drp = up(xh), up(res), up(rparts)
+    got = []
+    for st in (4, -1):  # streaming (four row groups per workgroup), then never
+        ops.tune("q4k_gemv.stream", st)
+        try:
+            parts = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, n), np.float32)
+            np_ = ops.q4k_gemv_ex(w, n, k, activation=x, residual=dres, residual_parts=drp if nres else None,
+                                  residual_nparts=nres, output_parts=parts, max_output_parts=ops.MAX_GEMV_PARTS)
+            dev.synchronize()
+            got.append(parts.download()[:np_])
+        finally:
+            ops.tune("q4k_gemv.stream", 0)
+    assert got[0].shape == got[1].shape and got[0].shape[0] > 1
+    assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32))
+    rs = res.copy()
+    for i in range(nres):
+        rs = (rs + rparts[i]).astype(np.float32)
+    want = ora.q4k_gemv(w.download().reshape(n, -1), xh, n, k) + rs.astype(np.float64)
+    assert rel_l2(got[0].astype(np.float64).sum(0), want) < 1e-5
