@@ -876,6 +876,10 @@ constexpr int kStreamMinGroupsPerCu = 8;  // automatic choice: at least 8 row gr
 // workgroup per CU there; measured at k 5376: 16384 rows 16.6 against 19.8
 // us, 21504 rows 19.4 against 24.3, 43008 rows 31.1 against 45.5)
 constexpr int kStreamMinGroupsPerCu2 = 4;
+// (the attention-combine prologue over >= 12 blocks per range: from 2 -- the
+// one-shot form then holds one workgroup per CU (78-82 VGPRs); measured at
+// 5376 x 8192, two K ranges, 7 splits: 11.6 against 16.1 us)
+constexpr int kStreamMinGroupsPerCuAttn = 2;
 constexpr int kStreamUnitBytes = 16 * DOE_Q4K_BLOCK_BYTES;  // 16 rows x one block
 constexpr int kStreamLdsMax = 160 * 1024;                  // one workgroup per CU
 
@@ -898,7 +902,8 @@ template <int PRO, int XV, int D, int B = 1>
 __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__restrict__ w, const float *x,
                                                                float *__restrict__ y, int n, int k, int nb,
                                                                int ngroups, int nbs, GemvFusion fz) {
-    constexpr bool NORM = PRO == 1;
+    constexpr bool NORM = PRO == 1, ATTN = PRO == 2;
+    static_assert(!ATTN || B == 1, "the attention-combine prologue: one block per wave");
     // K range blockIdx.y: blocks [kb0, kb1) (the whole row when not split);
     // a split GEMV writes each range's row sums to its output part
     const int kb0 = (int)blockIdx.y * nbs, kb1 = min(nb, kb0 + nbs);
@@ -917,16 +922,31 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
     const int my = g1 - g0;
     const int glast = min(max(g1 - 1, g0), ngroups - 1);
 
-    // Activation (norm weight, activation parts) loads first; they are waited
-    // on (vmcnt 0) before the ring's first loads are issued.  Wave w owns
+    // Activation (norm weight, activation parts) loads first, then the ring's
+    // first loads; the image is built once the activation loads have
+    // returned, with the ring's loads still in flight.  Wave w owns
     // blocks B w .. B w + B - 1 (a block past nb reads as zero activations and
     // a clamped copy of the last block's weights).
     float v[B][4], nwv[B][4];
     float4 xp[B][kMaxXParts];
+    // the attention prologue's split partials of this lane's four elements
+    // (a quad never straddles heads: head_dim % 4 == 0)
+    float4 ao[ATTN ? kAttnMaxSplits : 1];
+    float2 aml[ATTN ? kAttnMaxSplits : 1];
 #pragma unroll
     for (int u = 0; u < B; ++u) {
         const int e = (kb0 + wave * B + u) * 256 + lane * 4;
-        if (XV) {
+        if (ATTN) {
+            const int S = fz.attn_splits, hd = fz.attn_head_dim;
+            const int ec = min(e, k - 4), h = ec / hd, dd = ec - h * hd;
+#pragma unroll
+            for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+                if (sp < S) {
+                    ao[sp] = *reinterpret_cast<const float4 *>(fz.attn_o + ((size_t)h * S + sp) * hd + dd);
+                    aml[sp] = *reinterpret_cast<const float2 *>(fz.attn_ml + ((size_t)h * S + sp) * 2);
+                }
+            }
+        } else if (XV) {
             const float4 f = *reinterpret_cast<const float4 *>(x + min(e, k - 4));  // masked below
             v[u][0] = f.x; v[u][1] = f.y; v[u][2] = f.z; v[u][3] = f.w;
         } else {
@@ -953,7 +973,6 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
             for (int j = 0; j < 4; ++j) nwv[u][j] = fz.norm_w[min(e + j, k - 1)];
         }
     }
-    wait_vmcnt<0>();
     const size_t rowbytes = (size_t)nb * DOE_Q4K_BLOCK_BYTES;
     // group gi (clamped to the range), the wave's B blocks, into ring slot d:
     // three load instructions per block (lanes 0..63, 64..127 and 128..143
@@ -978,6 +997,32 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
     };
 #pragma unroll
     for (int d = 0; d < D; ++d) load_unit(g0 + d, d);
+    wait_vmcnt<3 * B * D>();  // the activation loads (older than the ring's) have returned
+    if (ATTN) {
+        // sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s (as the
+        // one-shot kernel's prologue)
+        const int S = fz.attn_splits;
+        float M = -INFINITY;
+#pragma unroll
+        for (int sp = 0; sp < kAttnMaxSplits; ++sp)
+            if (sp < S) M = fmaxf(M, aml[sp].x);
+        float L = 0.0f, O0 = 0.0f, O1 = 0.0f, O2 = 0.0f, O3 = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int sp = 0; sp < kAttnMaxSplits; ++sp) {
+                if (sp < S) {
+                    const float f = exp2f(aml[sp].x - M);
+                    L = fmaf(aml[sp].y, f, L);
+                    O0 = fmaf(ao[sp].x, f, O0);
+                    O1 = fmaf(ao[sp].y, f, O1);
+                    O2 = fmaf(ao[sp].z, f, O2);
+                    O3 = fmaf(ao[sp].w, f, O3);
+                }
+            }
+        }
+        const float rl = L > 0.0f ? 1.0f / L : 0.0f;
+        v[0][0] = O0 * rl; v[0][1] = O1 * rl; v[0][2] = O2 * rl; v[0][3] = O3 * rl;
+    }
 
     float ss = 0.0f;
 #pragma unroll
@@ -1356,8 +1401,10 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
     // the sum not kept; K ranges only as output parts)
     const bool stream_ok = use_mfma && (bpw == 1 || (bpw == 2 && gemv_stream_lds_bytes((nbs + 1) / 2, 2, 2) <=
                                                                       (size_t)kStreamLdsMax)) &&
-                           (ksplit == 1 || fz.y_parts) && !fz.attn_o && !fz.x_sum;
-    const int stream_min = bpw == 2 ? kStreamMinGroupsPerCu2 : kStreamMinGroupsPerCu;
+                           (ksplit == 1 || fz.y_parts) && (!fz.attn_o || bpw == 1) && !fz.x_sum;
+    const int stream_min = bpw == 2                       ? kStreamMinGroupsPerCu2
+                           : (fz.attn_o && nbs >= 12) ? kStreamMinGroupsPerCuAttn
+                                                      : kStreamMinGroupsPerCu;
     if (stream_ok &&
         (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups * ksplit >= (int64_t)stream_min * g_num_cus))) {
         const int sb = bpw;  // blocks per wave
@@ -1383,7 +1430,8 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
                                   (const void *)q4k_gemv_stream_kernel<0, 0, 3>, (const void *)q4k_gemv_stream_kernel<0, 1, 3>,
                                   (const void *)q4k_gemv_stream_kernel<1, 0, 3>, (const void *)q4k_gemv_stream_kernel<1, 1, 3>,
                                   (const void *)q4k_gemv_stream_kernel<0, 0, 2, 2>, (const void *)q4k_gemv_stream_kernel<0, 1, 2, 2>,
-                                  (const void *)q4k_gemv_stream_kernel<1, 0, 2, 2>, (const void *)q4k_gemv_stream_kernel<1, 1, 2, 2>})
+                                  (const void *)q4k_gemv_stream_kernel<1, 0, 2, 2>, (const void *)q4k_gemv_stream_kernel<1, 1, 2, 2>,
+                                  (const void *)q4k_gemv_stream_kernel<2, 0, 2, 1>})
                 if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kStreamLdsMax);
             return e;
         }();
@@ -1407,7 +1455,10 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         else if (depth == 3) DOE_GEMV_STREAM_LAUNCH(P, X, 3);                                            \
         else DOE_GEMV_STREAM_LAUNCH(P, X, 2);                                                            \
     } while (0)
-        if (fz.norm_w) {
+        if (fz.attn_o) {
+            hipLaunchKernelGGL((q4k_gemv_stream_kernel<2, 0, 2, 1>), sgrid, dim3(64 * nwaves), lds, st, wp, activation,
+                               output, (int)n, (int)k, nb, (int)row_groups, nbs, fz);
+        } else if (fz.norm_w) {
             if (xv) DOE_GEMV_STREAM_DEPTH(1, 1); else DOE_GEMV_STREAM_DEPTH(1, 0);
         } else {
             if (xv) DOE_GEMV_STREAM_DEPTH(0, 1); else DOE_GEMV_STREAM_DEPTH(0, 0);

@@ -230,3 +230,32 @@ def test_streaming_output_parts_bit_identical_to_one_shot(dev, ora, n, k, nres):
         rs = (rs + rparts[i]).astype(np.float32)
     want = ora.q4k_gemv(w.download().reshape(n, -1), xh, n, k) + rs.astype(np.float64)
     assert rel_l2(got[0].astype(np.float64).sum(0), want) < 1e-5
+
+
+@pytest.mark.parametrize("splits,nparts", [(7, 2), (3, 4), (1, 2)])
+def test_streaming_attention_prologue_bit_identical_to_one_shot(dev, splits, nparts):
+    # o_proj over the combine of the attention splits through the streaming
+    # kernel (32 heads of 256, K ranges as output parts, the residual with a
+    # part): the same bits as the one-shot kernel
+    rng = np.random.default_rng(splits * 10 + nparts)
+    heads, hd, n = 32, 256, 5376
+    k = heads * hd
+    w = up(q4k.random_q4k(rng, n, k))
+    o = rng.standard_normal((heads, splits, hd)).astype(np.float32)
+    ml = np.stack([rng.standard_normal((heads, splits)) * 3, rng.uniform(1, 5, (heads, splits))], -1)
+    pb = up(np.concatenate([o.reshape(-1), ml.astype(np.float32).reshape(-1)]))
+    res, rp = up(rng.standard_normal(n).astype(np.float32)), up(rng.standard_normal((1, n)).astype(np.float32))
+    got = []
+    for st in (3, -1):
+        ops.tune("q4k_gemv.stream", st)
+        try:
+            parts = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, n), np.float32)
+            np_ = ops.q4k_gemv_ex(w, n, k, attn_partials=pb, attn_splits=splits, attn_num_heads=heads,
+                                  attn_head_dim=hd, residual=res, residual_parts=rp, residual_nparts=1,
+                                  output_parts=parts, max_output_parts=nparts)
+            dev.synchronize()
+            got.append(parts.download()[:np_])
+        finally:
+            ops.tune("q4k_gemv.stream", 0)
+    assert got[0].shape == got[1].shape
+    assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32))
