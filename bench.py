@@ -123,7 +123,7 @@ def timed_gemv_windows(doe, n, k, steps, warmup, copies, windows, seed):
     stamps = ts.download().astype(np.int64)
     win_ms = [float(d) / hz.value * 1e3 for d in np.diff(stamps)]
     ev_ms = e0.elapsed_ms(e1)
-    from oracle import oracle as ora  # the checker, outside the timed region
+    from oracle import oracle as ora  # the reference answer, outside the timed region
 
     got = dy.download()
     want = ora.q4k_gemv(w, x, n, k)
@@ -784,7 +784,7 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the library has no "
               f"multi-GPU path", file=sys.stderr)
         return 2
     if int(os.environ.get("RANK", "0")) != 0:

@@ -1,5 +1,5 @@
-"""CPU oracle of the decode step (TEST INFRASTRUCTURE ONLY: the checker of
-the decode loop in tests/ and bench.py, never on the product path): the same
+"""CPU oracle of the decode step (TEST INFRASTRUCTURE ONLY: it checks the
+decode loop in tests/ and bench.py, never on the product path): the same
 step the Decoder runs, composed from the oracle's kernel restatements, on
 weights downloaded from the device.  Per layer it follows the decoder's plan:
 attention window, head_dim, the layer whose KV cache it reads (shared-KV

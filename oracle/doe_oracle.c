@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY: a plain-C restatement of the reference's CPU
  * evaluation of each kernel, used by tests/, the smoke check and bench.py's
- * cpu_baseline leg as the checker.  It is never linked into, loaded by or
+ * cpu_baseline leg to check results.  It is never linked into, loaded by or
  * called from the product library.
  *
  * Reference sources restated here (paths relative to the doerun/doe root):
@@ -396,8 +396,8 @@ int ora_rmsnorm(const float *x, const float *w, float *out, int64_t rows, int64_
 int ora_rope_table(float *freq_cis, int64_t max_pos, int64_t head_dim, double base) {
     /* freq_cis[(pos*half + i)*2 + {0,1}] = {cos, sin}(pos * base^(-2i/D)), the
      * table layout rope.wgsl:27-29 reads.  The reference builds it on the host
-     * outside this tree; this build computes the angle in double and rounds
-     * cos/sin once to f32. */
+     * outside this tree; here the angle is computed in double and cos/sin
+     * are rounded once to f32. */
     if (max_pos < 0 || head_dim <= 0 || (head_dim % 2) != 0) return -1;
     int64_t half = head_dim / 2;
     for (int64_t p = 0; p < max_pos; ++p) {

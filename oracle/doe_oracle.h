@@ -5,7 +5,7 @@
  * CPU evaluation of each hot-path kernel (the TSIR reference interpreter, the
  * CSL/WebGPU emulator's CPU backend and the Doppler RDRR Q4_K decoder).  Only
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it,
- * and only as the checker.  The product library (doe_amd) never calls it.
+ * and only to check results.  The product library (doe_amd) never calls it.
  *
  * Numerics: every function runs single-threaded, in the reference's strict
  * order (f32 left-fold accumulation unless noted), built with

@@ -1,7 +1,7 @@
 """ctypes wrapper of the CPU oracle ``oracle/liboracle.so``.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
-bench.py's cpu_baseline leg, where it is the checker.  The product package
+bench.py's cpu_baseline leg, to check results.  The product package
 ``doe_amd`` never imports it.
 """
 from __future__ import annotations
