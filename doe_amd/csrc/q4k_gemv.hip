@@ -881,7 +881,7 @@ constexpr int kStreamMinGroupsPerCu2 = 4;
 // 5376 x 8192, two K ranges, 7 splits: 11.6 against 16.1 us)
 constexpr int kStreamMinGroupsPerCuAttn = 2;
 constexpr int kStreamUnitBytes = 16 * DOE_Q4K_BLOCK_BYTES;  // 16 rows x one block
-constexpr int kStreamLdsMax = 160 * 1024;                  // the LDS of one CU
+constexpr int kStreamLdsMax = 160 * 1024;                  // one workgroup per CU
 
 size_t gemv_stream_lds_bytes(int nwaves, int depth, int bpw = 1) {
     return (size_t)nwaves * bpw * ((size_t)depth * kStreamUnitBytes + kMfmaAImgDwords * 4) +
@@ -1436,15 +1436,12 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
             return e;
         }();
         DOE_HIP_CHECK(attr_all);
-        // groups per workgroup: forced, or as many workgroups per CU as the
-        // LDS holds (two for the one-block form without the attention
-        // prologue when each takes at most half, else one) over the row
-        // groups of every K range, at most kStreamMaxGroups each (65536 x
-        // 2304: two 70 KB workgroups per CU of 8 groups 19.8-20.2 us, one of
-        // 16 groups 20.5-21.4; 32768 x 2304: 12.9 against 16.8 us)
-        const int64_t wg_per_cu = sb == 1 && !fz.attn_o && lds * 2 <= (size_t)kStreamLdsMax ? 2 : 1;
-        int64_t per_wg = g_tune_stream > 0 ? g_tune_stream
-                                           : (row_groups * ksplit + wg_per_cu * g_num_cus - 1) / (wg_per_cu * g_num_cus);
+        // groups per workgroup: forced, or one workgroup per CU (LDS-bound)
+        // over the row groups of every K range, at most kStreamMaxGroups each
+        // (two workgroups per CU of half the groups measured slower with the
+        // same buffers: 65536 x 2304 22.9 against 20.0 us, 32768 x 2304 14.2
+        // against 12.3)
+        int64_t per_wg = g_tune_stream > 0 ? g_tune_stream : (row_groups * ksplit + g_num_cus - 1) / g_num_cus;
         if (per_wg > kStreamMaxGroups) per_wg = kStreamMaxGroups;
         const int64_t grid = (row_groups + per_wg - 1) / per_wg;
         const dim3 sgrid((unsigned)grid, (unsigned)ksplit);
