@@ -876,9 +876,10 @@ constexpr int kStreamMinGroupsPerCu = 8;  // automatic choice: at least 8 row gr
 // workgroup per CU there; measured at k 5376: 16384 rows 16.6 against 19.8
 // us, 21504 rows 19.4 against 24.3, 43008 rows 31.1 against 45.5)
 constexpr int kStreamMinGroupsPerCu2 = 4;
-// (the attention-combine prologue over >= 12 blocks per range: from 2 -- the
-// one-shot form then holds one workgroup per CU (78-82 VGPRs); measured at
-// 5376 x 8192, two K ranges, 7 splits: 11.6 against 16.1 us)
+// (the attention-combine prologue over >= 12 blocks per range, or split into
+// K ranges: from 2 -- the one-shot form then holds one workgroup per CU
+// (78-82 VGPRs); measured at 5376 x 8192, two K ranges, 7 splits: 11.6
+// against 16.1 us; four ranges, 6 splits: 9.7 against 12.9)
 constexpr int kStreamMinGroupsPerCuAttn = 2;
 constexpr int kStreamUnitBytes = 16 * DOE_Q4K_BLOCK_BYTES;  // 16 rows x one block
 constexpr int kStreamLdsMax = 160 * 1024;                  // one workgroup per CU
@@ -1187,8 +1188,9 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
 int g_tune_rowslots = 0;
 int g_tune_rows = 0;
 int g_tune_kernel = 0;  // 0 automatic, 1 dot-product kernel, 2 matrix-core kernel
-int g_tune_ksplit = 0;  // 0 automatic, 1 never split K over workgroups
-int g_tune_forms = 0;   // 1: the q/k/v epilogue without its fetched-ahead rotation
+int g_tune_ksplit = 0;  // 0 automatic, 1 never split K over workgroups, 2-4: at least that many output parts
+int g_tune_forms = 0;   // bits: 1 the q/k/v epilogue without its fetched-ahead rotation,
+                        // 2 the attention-prologue o_proj in its fewest K ranges
 int g_tune_bpw = 0;     // 0 automatic, else at least this many blocks per wave (<= 4)
 int g_tune_stream = 0;  // 0 automatic, -1 never stream, g > 0: stream g row groups per workgroup
 int g_tune_stream_depth = 0;  // 0 automatic, else 2, 4 or 6 units in flight per wave (if the LDS allows)
@@ -1362,6 +1364,11 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         const int cap = max_y_parts < kMaxXParts ? max_y_parts : kMaxXParts;
         const int need = fz.attn_o ? (nb + 15) / 16 : 1;
         ksplit = need;
+        // past 16 blocks the attention prologue takes as many K ranges as the
+        // parts allow: fewer blocks per range, each wave walking more row
+        // groups (5376 x 8192, six splits of 32 heads: four ranges of 8
+        // blocks 9.7 us against 10.7 for two of 16, same buffers)
+        if (need > 1 && !(g_tune_forms & 2)) ksplit = cap < nb ? cap : nb;
         if (row_groups < g_num_cus && g_tune_ksplit != 1 && nb > 1) {
             const int64_t fill = (g_num_cus + row_groups - 1) / row_groups;
             int want = (int)(fill < nb ? fill : nb);
@@ -1369,6 +1376,7 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
             if (want > cap) want = cap;
             if (want > ksplit) ksplit = want;
         }
+        if (g_tune_ksplit > ksplit) ksplit = (int)(g_tune_ksplit < cap ? (g_tune_ksplit < nb ? g_tune_ksplit : nb) : cap);
         DOE_REQUIRE(ksplit <= cap, DOE_E_UNSUPPORTED, "k=%lld needs %d output parts (room for %d, at most %d)",
                     (long long)k, ksplit, max_y_parts, kMaxXParts);
     } else if (nb > 1 && fz.residual == output && !fz.norm_w && !fz.gated && !fz.rope_kv &&
@@ -1403,7 +1411,7 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
                                                                       (size_t)kStreamLdsMax)) &&
                            (ksplit == 1 || fz.y_parts) && (!fz.attn_o || bpw == 1) && !fz.x_sum;
     const int stream_min = bpw == 2                       ? kStreamMinGroupsPerCu2
-                           : (fz.attn_o && nbs >= 12) ? kStreamMinGroupsPerCuAttn
+                           : (fz.attn_o && (nbs >= 12 || ksplit > 1)) ? kStreamMinGroupsPerCuAttn
                                                       : kStreamMinGroupsPerCu;
     if (stream_ok &&
         (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups * ksplit >= (int64_t)stream_min * g_num_cus))) {
@@ -1498,7 +1506,7 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
             DOE_GEMV_MFMA_LAUNCH(2, 1, 0, 1);
         } else if (fz.attn_o) {
             DOE_GEMV_MFMA_LAUNCH(2, 1, 0, 0);
-        } else if (fz.norm_w && fz.rope_kv && bpw == 1 && xv && g_tune_forms == 0) {
+        } else if (fz.norm_w && fz.rope_kv && bpw == 1 && xv && !(g_tune_forms & 1)) {
             DOE_GEMV_MFMA_LAUNCH(1, 1, 1, 2);  // the decode step's q/k/v projection
         } else if (fz.norm_w) {
             if (xv) DOE_GEMV_MFMA_BPW(1, 1, 0) else DOE_GEMV_MFMA_BPW(1, 0, 0)
@@ -1705,10 +1713,10 @@ int doe_tune_set(const char *key, int value) {
                     "q4k_gemv.stream_depth is 0, 2, 3, 4 or 6");
         g_tune_stream_depth = value;
     } else if (!strcmp(key, "q4k_gemv.ksplit")) {
-        DOE_REQUIRE(value == 0 || value == 1, DOE_E_INVALID, "q4k_gemv.ksplit is 0 or 1");
+        DOE_REQUIRE(value >= 0 && value <= kMaxXParts, DOE_E_INVALID, "q4k_gemv.ksplit is 0..%d", kMaxXParts);
         g_tune_ksplit = value;
     } else if (!strcmp(key, "q4k_gemv.forms")) {
-        DOE_REQUIRE(value == 0 || value == 1, DOE_E_INVALID, "q4k_gemv.forms is 0 or 1");
+        DOE_REQUIRE(value >= 0 && value <= 3, DOE_E_INVALID, "q4k_gemv.forms is 0..3");
         g_tune_forms = value;
     } else if (!strcmp(key, "q4k_gemv.kernel")) {
         DOE_REQUIRE(value >= 0 && value <= 2, DOE_E_INVALID, "q4k_gemv.kernel is 0, 1 or 2");

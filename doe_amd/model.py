@@ -422,8 +422,9 @@ class Decoder:
                                             stream=stream)
             # combine + o_proj + attn_residual as K-range parts
             # (the attention prologue takes one Q4_K block per wave: past 16
-            # blocks o_proj needs more than one range)
-            wo_parts = max(self.wo_parts, -(-L.q_dim // 4096))
+            # blocks o_proj needs more than one range, and then takes as many
+            # as the parts allow)
+            wo_parts = self.wo_parts if L.q_dim <= 4096 else ops.MAX_GEMV_PARTS
             no = ops.q4k_gemv_ex(L.wo, c.hidden, L.q_dim, attn_partials=self.attn_parts, attn_splits=splits,
                                  attn_num_heads=c.heads, attn_head_dim=hd, residual=act, residual_parts=act_parts,
                                  residual_nparts=na, output_parts=self.parts_o, max_output_parts=wo_parts,

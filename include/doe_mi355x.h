@@ -669,8 +669,10 @@ int doe_decode_advance(int32_t *state, int32_t *token, int32_t *ids, int64_t max
  * "attn_decode.waves" (4: narrow workgroups; 8 or 16: the wide short-context
  * workgroup where the head shape allows it), "attn_decode.combine" (1: the
  * block-reduction split combine instead of the one-wave-per-column form),
- * "q4k_gemv.ksplit" (1: no K split over workgroups), "q4k_gemv.forms" (1:
- * the q/k/v epilogue without its fetched-ahead rotation).  No
+ * "q4k_gemv.ksplit" (1: no K split over workgroups; 2-4: at least that many
+ * K ranges where output parts are written), "q4k_gemv.forms" (bit 1: the
+ * q/k/v epilogue without its fetched-ahead rotation; bit 2: the
+ * attention-prologue o_proj in its fewest K ranges).  No
  * reference counterpart:
  * the reference fixes workgroup shapes per WGSL override constant
  * (lm_head_gemv.wgsl:168-169 MULTICOL_* overrides). */

@@ -232,15 +232,17 @@ def test_streaming_output_parts_bit_identical_to_one_shot(dev, ora, n, k, nres):
     assert rel_l2(got[0].astype(np.float64).sum(0), want) < 1e-5
 
 
-@pytest.mark.parametrize("splits,nparts", [(7, 2), (3, 4), (1, 2)])
-def test_streaming_attention_prologue_bit_identical_to_one_shot(dev, splits, nparts):
+@pytest.mark.parametrize("splits,nparts", [(7, 2), (3, 4), (1, 2), (6, 4)])
+def test_streaming_attention_prologue_bit_identical_to_one_shot(dev, ora, splits, nparts):
     # o_proj over the combine of the attention splits through the streaming
-    # kernel (32 heads of 256, K ranges as output parts, the residual with a
-    # part): the same bits as the one-shot kernel
+    # kernel (32 heads of 256, K ranges as output parts -- as many as the
+    # parts allow past 16 blocks -- the residual with a part): the same bits
+    # as the one-shot kernel, and the oracle GEMV over the combine
     rng = np.random.default_rng(splits * 10 + nparts)
     heads, hd, n = 32, 256, 5376
     k = heads * hd
-    w = up(q4k.random_q4k(rng, n, k))
+    wn = q4k.random_q4k(rng, n, k)
+    w = up(wn)
     o = rng.standard_normal((heads, splits, hd)).astype(np.float32)
     ml = np.stack([rng.standard_normal((heads, splits)) * 3, rng.uniform(1, 5, (heads, splits))], -1)
     pb = up(np.concatenate([o.reshape(-1), ml.astype(np.float32).reshape(-1)]))
@@ -257,5 +259,10 @@ def test_streaming_attention_prologue_bit_identical_to_one_shot(dev, splits, npa
             got.append(parts.download()[:np_])
         finally:
             ops.tune("q4k_gemv.stream", 0)
-    assert got[0].shape == got[1].shape
+    assert got[0].shape == got[1].shape == (nparts, n)
     assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32))
+    m = ml[..., 0].max(1, keepdims=True)
+    f = np.exp2(ml[..., 0] - m)
+    attn = ((o * f[..., None]).sum(1) / (ml[..., 1] * f).sum(1, keepdims=True)).reshape(-1).astype(np.float32)
+    want = ora.q4k_gemv(wn, attn, n, k) + res.download().astype(np.float64) + rp.download()[0].astype(np.float64)
+    assert rel_l2(got[0].astype(np.float64).sum(0), want) < 1e-5
