@@ -266,3 +266,49 @@ def test_streaming_attention_prologue_bit_identical_to_one_shot(dev, ora, splits
     attn = ((o * f[..., None]).sum(1) / (ml[..., 1] * f).sum(1, keepdims=True)).reshape(-1).astype(np.float32)
     want = ora.q4k_gemv(wn, attn, n, k) + res.download().astype(np.float64) + rp.download()[0].astype(np.float64)
     assert rel_l2(got[0].astype(np.float64).sum(0), want) < 1e-5
+
+
+def test_range_count_tuning(dev, ora):
+    # q4k_gemv.ksplit 2-4 sets the least number of K ranges where output
+    # parts are written; q4k_gemv.forms bit 2 keeps the attention-prologue
+    # o_proj in its fewest ranges.  Every count sums to the same GEMV.
+    rng = np.random.default_rng(77)
+    n, k = 9216, 2304  # 576 row groups: one range unless forced
+    w = q4k.random_q4k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    want = ora.q4k_gemv(w, x, n, k)
+    dw, dx = up(w), up(x)
+    for least in (2, 3, 4):
+        ops.tune("q4k_gemv.ksplit", least)
+        try:
+            parts = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, n), np.float32)
+            got_n = ops.q4k_gemv_ex(dw, n, k, activation=dx, output_parts=parts, max_output_parts=ops.MAX_GEMV_PARTS)
+            dev.synchronize()
+        finally:
+            ops.tune("q4k_gemv.ksplit", 0)
+        assert got_n == least
+        assert rel_l2(parts.download()[:got_n].astype(np.float64).sum(0), want) < 1e-5
+    with pytest.raises(DoeError):
+        ops.tune("q4k_gemv.ksplit", ops.MAX_GEMV_PARTS + 1)
+    heads, hd, S, n = 32, 256, 2, 5376  # 336 row groups
+    k = heads * hd
+    wn = q4k.random_q4k(rng, n, k)
+    o = rng.standard_normal((heads, S, hd)).astype(np.float32)
+    ml = np.stack([rng.standard_normal((heads, S)), rng.uniform(1, 5, (heads, S))], -1).astype(np.float32)
+    pb = up(np.concatenate([o.reshape(-1), ml.reshape(-1)]))
+    m = ml[..., 0].max(1, keepdims=True)
+    f = np.exp2(ml[..., 0] - m)
+    attn = ((o * f[..., None]).sum(1) / (ml[..., 1] * f).sum(1, keepdims=True)).reshape(-1).astype(np.float32)
+    want = ora.q4k_gemv(wn, attn, n, k)
+    dw = up(wn)
+    for forms, expect in ((0, 4), (2, 2)):
+        ops.tune("q4k_gemv.forms", forms)
+        try:
+            parts = DeviceBuffer.empty((ops.MAX_GEMV_PARTS, n), np.float32)
+            got_n = ops.q4k_gemv_ex(dw, n, k, attn_partials=pb, attn_splits=S, attn_num_heads=heads,
+                                    attn_head_dim=hd, output_parts=parts, max_output_parts=ops.MAX_GEMV_PARTS)
+            dev.synchronize()
+        finally:
+            ops.tune("q4k_gemv.forms", 0)
+        assert got_n == expect
+        assert rel_l2(parts.download()[:got_n].astype(np.float64).sum(0), want) < 1e-5
