@@ -122,6 +122,27 @@ def q4k_gemv(w: np.ndarray, x: np.ndarray, n: int, k: int, rows: tuple[int, int]
     return y
 
 
+def q4k_gemv_threads(w: np.ndarray, x: np.ndarray, n: int, k: int, threads: int) -> np.ndarray:
+    """The same GEMV with its rows split over `threads` host threads (each
+    row computed exactly as in q4k_gemv, so the result is the same bits);
+    the calls release the GIL.  For the all-core CPU baseline."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    w = _c(w, np.uint8)
+    x = _c(x, np.float32)
+    y = np.zeros(n, np.float32)
+    threads = max(1, min(int(threads), n)) if n else 1
+    cuts = [n * i // threads for i in range(threads + 1)]
+
+    def part(i):
+        return lib().ora_q4k_gemv_rows(_ptr(w), _ptr(x), _ptr(y), n, k, cuts[i], cuts[i + 1])
+
+    with ThreadPoolExecutor(threads) as ex:
+        for rc in ex.map(part, range(threads)):
+            _ok(rc, "q4k_gemv_rows")
+    return y
+
+
 def q4k_gemm_sampled(a_bf16: np.ndarray, b: np.ndarray, m: int, n: int, k: int, mi, ni) -> np.ndarray:
     a = _c(a_bf16, np.uint16)
     b = _c(b, np.uint8)

@@ -142,6 +142,9 @@ def test_q4k_gemv_matches_float64_dense(ora):
         # row-range variant is the same computation
         part = ora.q4k_gemv(w, x, n, k, rows=(1, n))
         assert np.array_equal(part[1:], y[1:])
+        # and so is the rows-over-threads form (the all-core CPU baseline)
+        for threads in (1, 3, 8):
+            assert np.array_equal(ora.q4k_gemv_threads(w, x, n, k, threads), y)
 
 
 def test_q4k_gemv_one_hot_selects_a_column(ora):
