@@ -42,6 +42,7 @@ int attn_set_combine(int value);
 int gemm_set_f16_operands(int value);
 int int4_set_kernel(int value);
 int int4_set_depth(int value);
+int int4_set_xcd(int value);
 int q8_0_set_tune(const char *key, int value);  // "q8_0_gemv.rows" / ".depth"
 
 }  // namespace doe

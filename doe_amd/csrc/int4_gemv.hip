@@ -75,7 +75,20 @@ struct Int4Args {
     unsigned long long *cnt;  // one-shot kernel, K split: ranges done per row block, a multiple of the
                               // range count between calls
     int M, N, K, G;
+    int xcd_map;  // 1: workgroup ids dealt so that a row block's K ranges share an XCD
 };
+
+// Workgroup id -> work item such that consecutive items run on one XCD
+// (workgroups are dealt to the eight XCDs by id % 8): XCD x takes items
+// [x * base + min(x, rem), + base + (x < rem)).  The K ranges of a row block
+// are consecutive items, so the scale line two neighbouring ranges share
+// (a range's 32 groups are 64 bytes of a 128-byte line) is fetched into one
+// L2 instead of two.
+__device__ __forceinline__ int xcd_item(int id, int total, int on) {
+    if (!on) return id;
+    const int base = total >> 3, rem = total & 7, x = id & 7;
+    return x * base + min(x, rem) + (id >> 3);
+}
 
 // s_waitcnt vmcnt(0) (every load and store of the wave complete), as the
 // compiler's own wait so that it tracks it; the empty asm keeps memory
@@ -181,7 +194,8 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a, int ranges) 
     __shared__ __attribute__((aligned(16))) uint32_t wl[4][64 * 4 * kGpw];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int rb = blockIdx.x / ranges, sp = blockIdx.x - rb * ranges;
+    const int item = xcd_item(blockIdx.x, gridDim.x, a.xcd_map);
+    const int rb = item / ranges, sp = item - rb * ranges;
     const int r0 = rb * 64;
     const int g0 = (sp * 4 + wave) * kGpw;
     const bool active = g0 < a.G;  // a.G is a multiple of kGpw
@@ -374,7 +388,15 @@ __global__ __launch_bounds__(256, 2) void int4_gemv_stream_kernel(Int4Args a, in
     __shared__ float red[DEPTH][4][4][4][64];  // [buffer][source wave][tile][column][lane]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int sp = blockIdx.x / wps, j = blockIdx.x - sp * wps;
+    // With xcd_map, a few K ranges (< 8): item = j * ranges + sp, the ranges
+    // walking the same row blocks neighbours on one XCD (their shared scale
+    // lines fetched once); many ranges: item = sp * wps + j, each XCD holding
+    // a contiguous run of ranges (so it reads its own slices of x, not all
+    // of x, and neighbouring ranges still meet on one XCD but at its edges)
+    const int ranges = gridDim.x / wps, item = xcd_item(blockIdx.x, gridDim.x, a.xcd_map);
+    const bool range_major = !a.xcd_map || ranges >= 8;
+    const int sp = range_major ? item / wps : item % ranges;
+    const int j = range_major ? item - sp * wps : item / ranges;
     const int g0 = (sp * 4 + wave) * kGpw;
     const bool active = g0 < a.G;  // a.G is a multiple of kGpw
     const int gb = active ? g0 : 0;
@@ -500,6 +522,7 @@ std::map<int, CountRegion> g_counts;
 int g_num_cus = 0;
 int g_int4_kernel = 0;  // 0 automatic, 1 one-shot workgroups, 2 streaming
 int g_int4_depth = 3;   // streaming: row blocks in flight per wave + 1 (2 or 3)
+int g_int4_plain = 0;   // 0: a row block's K ranges on one XCD, 1: workgroup ids in plain order
 
 }  // namespace
 
@@ -593,6 +616,7 @@ int doe_int4g32_gemv(const uint32_t *w_u4, const uint16_t *scales_f16, const flo
     a.N = (int)n;
     a.K = (int)k;
     a.G = G;
+    a.xcd_map = !g_int4_plain;
     if (one_shot) {
         hipLaunchKernelGGL(int4_gemv_kernel, dim3((unsigned)(row_blocks * splits)), dim3(256), 0, st, a, splits);
         DOE_LAUNCH_CHECK("int4_gemv_kernel");
@@ -623,6 +647,12 @@ namespace doe {
 int int4_set_kernel(int v) {
     DOE_REQUIRE(v >= 0 && v <= 2, DOE_E_INVALID, "int4_gemv.kernel is 0, 1 or 2");
     g_int4_kernel = v;
+    return DOE_OK;
+}
+
+int int4_set_xcd(int v) {
+    DOE_REQUIRE(v == 0 || v == 1, DOE_E_INVALID, "int4_gemv.xcd is 0 (automatic) or 1 (plain workgroup order)");
+    g_int4_plain = v;
     return DOE_OK;
 }
 

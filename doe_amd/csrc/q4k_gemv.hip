@@ -1727,6 +1727,8 @@ int doe_tune_set(const char *key, int value) {
         return doe::int4_set_kernel(value);
     } else if (!strcmp(key, "int4_gemv.depth")) {
         return doe::int4_set_depth(value);
+    } else if (!strcmp(key, "int4_gemv.xcd")) {
+        return doe::int4_set_xcd(value);
     } else if (!strcmp(key, "attn_mq.splits")) {
         return doe::mq_set_splits(value);
     } else if (!strcmp(key, "attn_decode.splits")) {

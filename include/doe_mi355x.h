@@ -663,7 +663,9 @@ int doe_decode_advance(int32_t *state, int32_t *token, int32_t *ids, int64_t max
  * Keys: "q4k_gemv.rowslots", "q4k_gemv.rows", "q4k_gemv.stream" (v > 0: the
  * streaming GEMV walking v row groups per workgroup, -1: never streaming),
  * "q4k_gemv.stream_depth" (2, 3, 4 or 6 units in flight per wave),
- * "q8_0_gemv.rows" (1, 2 or 4 rows per wave group), "q8_0_gemv.depth" (1 or
+ * "int4_gemv.kernel" (1 one-shot, 2 streaming), "int4_gemv.depth" (2 or 3),
+ * "int4_gemv.xcd" (1: workgroup ids in plain order, not a row block's K
+ * ranges grouped on one XCD), "q8_0_gemv.rows" (1, 2 or 4 rows per wave group), "q8_0_gemv.depth" (1 or
  * 2 blocks loaded ahead), "attn_mq.splits" (1..16 key splits of the
  * multi-query attention), "attn_decode.splits",
  * "attn_decode.waves" (4: narrow workgroups; 8 or 16: the wide short-context
