@@ -45,7 +45,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 128, kBQ = 128, kBKV = 64;
 constexpr int kKRow = kD + 8;    // bf16 per K row in LDS (272 B: b128 reads conflict-free)
-constexpr int kVRow = kBKV + 8;  // f16 per V^T row in LDS (144 B: 16-byte rows, b64 reads conflict-free)
+constexpr int kVRow = kBKV + 4;  // f16 per V^T row in LDS (136 B = 34 dwords: 16 lanes' b64 reads hit 32 distinct banks)
 constexpr float kLazy = 8.0f;    // the running max is raised only past m + 8 (P <= 2^8)
 
 struct PrefillArgs {
@@ -167,7 +167,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         *reinterpret_cast<u32x4 *>(&Ks[BUF][(gi >> 4) * kKRow + (gi & 15) * 8]) = rk[i];             \
     }
 #define DOE_PF_STORE_V(BUF)                                                                          \
-    _Pragma("unroll") for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4 *>(&Vt[BUF][vd * kVRow + 32 * vh + 8 * i]) = rv[i]
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                                  \
+        /* rows are 8-byte aligned: two b64 stores */                                                \
+        u32x2 *dst = reinterpret_cast<u32x2 *>(&Vt[BUF][vd * kVRow + 32 * vh + 8 * i]);              \
+        dst[0] = u32x2{rv[i].x, rv[i].y};                                                            \
+        dst[1] = u32x2{rv[i].z, rv[i].w};                                                            \
+    }
 
     float16v o[4];
 #pragma unroll
