@@ -219,22 +219,28 @@ __global__ __launch_bounds__(256) void int4_gemv_kernel(Int4Args a, int ranges) 
     }
     half8 xa[kGpw], ac;
     const int sig = x_image(a, active, lane, xv, xa, ac);
-    // regroup: wl[(row * 4 + word) * kGpw + group]
+    // regroup: row r's 32 dwords hold (word e, group u) at (8 e + u) ^ 4 sw(r),
+    // sw(r) = 0 2 4 6 1 3 5 7 over r % 8: the stores (32 lanes: 4 rows x 8
+    // groups) and the 16-byte reads (8 lanes: 8 rows) each fall on distinct
+    // banks (unswizzled, 8 rows' words met on one bank)
+    static_assert(kGpw == 8, "the swizzle assumes 32 dwords per row");
     uint32_t *my = wl[wave];
+    auto swz = [](int r) __attribute__((always_inline)) { return 4 * (((r << 1) & 7) | ((r >> 2) & 1)); };
 #pragma unroll
     for (int j = 0; j < kGpw; ++j) {
         const int row = j * RPI + lane / kGpw, u = lane % kGpw;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) my[(row * 4 + e) * kGpw + u] = wg[j][e];
+        for (int e = 0; e < 4; ++e) my[row * 32 + ((e * kGpw + u) ^ swz(row))] = wg[j][e];
     }
     // (each wave reads back only its own slice: no workgroup barrier needed)
     uint32_t w[4][kGpw];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(my + ((16 * t + lr) * 4 + lg) * kGpw);
+        const int row = 16 * t + lr;
+        const uint32_t *rowp = my + row * 32;
 #pragma unroll
         for (int h = 0; h < kGpw / 4; ++h) {
-            const u32x4 v = src[h];
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(rowp + ((lg * kGpw + 4 * h) ^ swz(row)));
             w[t][4 * h] = v.x;
             w[t][4 * h + 1] = v.y;
             w[t][4 * h + 2] = v.z;
