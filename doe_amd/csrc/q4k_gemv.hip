@@ -883,6 +883,7 @@ constexpr int kStreamMinGroupsPerCu2 = 4;
 constexpr int kStreamMinGroupsPerCuAttn = 2;
 constexpr int kStreamUnitBytes = 16 * DOE_Q4K_BLOCK_BYTES;  // 16 rows x one block
 constexpr int kStreamLdsMax = 160 * 1024;                  // one workgroup per CU
+constexpr int kStreamMaxThreads2 = 768;                    // two-block form: at most 12 waves
 
 size_t gemv_stream_lds_bytes(int nwaves, int depth, int bpw = 1) {
     return (size_t)nwaves * bpw * ((size_t)depth * kStreamUnitBytes + kMfmaAImgDwords * 4) +
@@ -899,10 +900,12 @@ __device__ __forceinline__ void wait_vmcnt() {
     __asm__ volatile("" ::: "memory");
 }
 
+// (two blocks per wave: at most 11 waves -- the LDS holds no more -- so
+// three waves per SIMD and up to 168 VGPRs)
 template <int PRO, int XV, int D, int B = 1>
-__global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__restrict__ w, const float *x,
-                                                               float *__restrict__ y, int n, int k, int nb,
-                                                               int ngroups, int nbs, GemvFusion fz) {
+__global__ __launch_bounds__(B == 2 ? kStreamMaxThreads2 : 1024) void q4k_gemv_stream_kernel(
+    const uint8_t *__restrict__ w, const float *x, float *__restrict__ y, int n, int k, int nb, int ngroups, int nbs,
+    GemvFusion fz) {
     constexpr bool NORM = PRO == 1, ATTN = PRO == 2;
     static_assert(!ATTN || B == 1, "the attention-combine prologue: one block per wave");
     // K range blockIdx.y: blocks [kb0, kb1) (the whole row when not split);
@@ -1107,19 +1110,38 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
             const int j = j0 + d;
             // slot d's 3 B loads are the oldest of the 3 B D in flight
             wait_vmcnt<3 * B * (D - 1)>();
-            if (j < my) {  // wave-uniform; LDS and arithmetic only
-                float part = 0.0f;
+            // The slot's bytes go to registers; the slot is refilled with unit
+            // j + D once those reads have returned (before the next unit's
+            // bytes may land in it).  Two blocks per wave refill before the
+            // arithmetic, so the loads fly during it (31B-class decode +0.3 to
+            // +0.8 %, three A/B pairs); one block per wave after it (refilling first
+            // measured no faster at 65536 x 2304 and costs 7 VGPRs).
+            constexpr bool EARLY = B == 2;
+            u32x4 hdr[B], qa[B], qb[B];
+            auto read_slot = [&]() __attribute__((always_inline)) {
 #pragma unroll
                 for (int u = 0; u < B; ++u) {
                     const uint8_t *rp = ring + (size_t)(d * B + u) * kStreamUnitBytes +
                                         i16 * DOE_Q4K_BLOCK_BYTES;  // lane (g, row i16)
-                    const u32x4 hdr = *reinterpret_cast<const u32x4 *>(rp);
-                    const u32x4 qa = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
-                    const u32x4 qb = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
+                    hdr[u] = *reinterpret_cast<const u32x4 *>(rp);
+                    qa[u] = *reinterpret_cast<const u32x4 *>(rp + 16 + 32 * g);
+                    qb[u] = *reinterpret_cast<const u32x4 *>(rp + 32 + 32 * g);
+                }
+            };
+            if constexpr (EARLY) {
+                if (j < my) read_slot();  // wave-uniform
+                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                load_unit(g0 + j + D, d);
+            }
+            if (j < my) {  // wave-uniform; LDS and arithmetic only
+                if constexpr (!EARLY) read_slot();
+                float part = 0.0f;
+#pragma unroll
+                for (int u = 0; u < B; ++u) {
                     f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj) {
-                        const uint32_t dw = jj < 4 ? qa[jj] : qb[jj - 4], ew = dw >> 8;
+                        const uint32_t dw = jj < 4 ? qa[u][jj] : qb[u][jj - 4], ew = dw >> 8;
                         const u32x4 bw = {dw & 0x000f000fu, ew & 0x000f000fu, dw & 0x00f000f0u, ew & 0x00f000f0u};
                         acc[jj & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                             __builtin_bit_cast(half8, areg[u][jj]), __builtin_bit_cast(half8, bw), acc[jj & 1], 0, 0,
@@ -1128,8 +1150,9 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
                     const f32x4 dsum = acc[0] + acc[1];
                     if (kb0 + wave * B + u < kb1 && 4 * (kb0 + wave * B + u) + g < nchunk) {
                         uint32_t scp, mnp;
-                        q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, g, scp, mnp);
-                        const float d_ = doe_half_bits_to_float(hdr.x), dmin = doe_half_bits_to_float(hdr.x >> 16);
+                        q4k_scale_min_pair(hdr[u].y, hdr[u].z, hdr[u].w, g, scp, mnp);
+                        const float d_ = doe_half_bits_to_float(hdr[u].x);
+                        const float dmin = doe_half_bits_to_float(hdr[u].x >> 16);
                         const float qx_lo = (dsum[0] + dsum[1]) * lo_scale[u];
                         const float qx_hi = (dsum[2] + dsum[3]) * hi_scale[u];
                         const float sc_lo = (float)(scp & 0xffu), sc_hi = (float)(scp >> 8);
@@ -1140,10 +1163,10 @@ __global__ __launch_bounds__(1024) void q4k_gemv_stream_kernel(const uint8_t *__
                 part = sum_rows4(part);
                 if (lane < 16) rpart[(j * 16 + lane) * nwaves + wave] = part;
             }
-            // the slot's reads have returned (the arithmetic above used them)
-            // before the next unit's bytes may land in it
-            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            load_unit(g0 + j + D, d);
+            if constexpr (!EARLY) {
+                __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                load_unit(g0 + j + D, d);
+            }
         }
     }
     wait_vmcnt<0>();  // the dropped loads past the range land before the LDS is released
@@ -1417,6 +1440,8 @@ int gemv_launch(const void *weight_q4k, const float *activation, float *output, 
         (g_tune_stream > 0 || (g_tune_stream == 0 && row_groups * ksplit >= (int64_t)stream_min * g_num_cus))) {
         const int sb = bpw;  // blocks per wave
         const int nwaves = (nbs + sb - 1) / sb;
+        DOE_REQUIRE(sb == 1 || 64 * nwaves <= kStreamMaxThreads2, DOE_E_UNSUPPORTED,
+                    "two-block streaming GEMV: %d waves (at most %d)", nwaves, kStreamMaxThreads2 / 64);
         // ring depth 2: deeper rings measured slower (65536 x 2304: 21.4 us
         // at 2, 23.0 at 3, 23.4 at 4, 25.8 at 6) -- the more units each wave
         // has in flight, the further a workgroup's waves drift apart over
