@@ -158,7 +158,7 @@ def bench_gemv(args, doe):
         f"{r['mean_ms_per_step'] * 1e3:.3f}, HIP events over the timed region {r['event_ms_per_step'] * 1e3:.3f}), "
         f"wall {r['wall_s']:.3f}s")
     r["value_gbs"] = GEMV_BYTES / (r["ms_per_step"] * 1e-3) / 1e9
-    r["kernel"] = "q4k_gemv_mfma_kernel<0, 1, 1> (doe_amd/csrc/q4k_gemv.hip)"
+    r["kernel"] = "q4k_gemv_mfma_kernel<0, 1, 1, 0> (doe_amd/csrc/q4k_gemv.hip)"
     return r
 
 
@@ -177,7 +177,7 @@ def bench_gemv_large(args, doe):
         f"({100 * gbs / HBM_PEAK_GBS:.1f}% of peak), rel_l2 {r['rel_l2']:.2e}")
     return {"workload": f"q4k_gemv M=1 N={GL_N} K={K}, {r['copies']} rotating weight copies, median of "
                         f"{r['windows']} windows of {r['steps']} launches in one HIP graph",
-            "kernel": "q4k_gemv_stream_kernel<0, 1, 2> (doe_amd/csrc/q4k_gemv.hip)",
+            "kernel": "q4k_gemv_stream_kernel<0, 1, 2, 1> (doe_amd/csrc/q4k_gemv.hip)",
             "launches_per_window": r["steps"], "windows": r["windows"],
             "us_per_launch": round(r["ms_per_step"] * 1e3, 3),
             "mean_us_per_launch": round(r["mean_ms_per_step"] * 1e3, 3),
