@@ -63,3 +63,34 @@ def test_gemv_args_struct_layout_matches_the_header(tmp_path):
     got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
     want = [getattr(Q4kGemvArgs, n).offset for n in names] + [C.sizeof(Q4kGemvArgs)]
     assert got == want
+
+
+def test_tune_keys_take_their_documented_values():
+    """doe_tune_set (host state only, no GPU needed): each key accepts the
+    values the header documents and rejects the rest with DOE_E_INVALID;
+    0 restores the automatic choice.  Unknown keys are rejected."""
+    from doe_amd import _lib
+    lib = _lib.load()
+    cases = {
+        "q4k_gemv.bpw": ([0, 1, 4], [-1, 5]),
+        "q4k_gemv.stream": ([-1, 0, 1, 16], [-2, 17]),
+        "q4k_gemv.stream_depth": ([0, 2, 3, 4, 6], [1, 5, 7]),
+        "q4k_gemv.ksplit": ([0, 1, 2, 4], [-1, 5]),
+        "q4k_gemv.forms": ([0, 1, 2, 3], [-1, 4]),
+        "q4k_gemv.kernel": ([0, 1, 2], [3]),
+        "int4_gemv.kernel": ([0, 1, 2], [3]),
+        "int4_gemv.depth": ([0, 2, 3], [1, 4]),
+        "int4_gemv.xcd": ([0, 1], [2, -1]),
+    }
+    try:
+        for key, (good, bad) in cases.items():
+            for v in good:
+                assert lib.doe_tune_set(key.encode(), v) == 0, (key, v, lib.doe_last_error())
+            for v in bad:
+                assert lib.doe_tune_set(key.encode(), v) == -1, (key, v)
+                assert key.encode() in lib.doe_last_error()
+    finally:
+        for key in cases:
+            lib.doe_tune_set(key.encode(), 0)
+    assert lib.doe_tune_set(b"no_such.key", 1) == -1
+    assert b"unknown tuning key" in lib.doe_last_error()
