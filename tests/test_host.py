@@ -39,3 +39,18 @@ def test_matmul_q4k_rejects_wrong_weight_length():
         ops.matmul_q4k(FakeBuf(144 * 9 * 10), FakeBuf(2303 * 4), FakeBuf(40), 10, 2304)
     with pytest.raises(ValueError, match="output"):
         ops.matmul_q4k(FakeBuf(144 * 9 * 10), FakeBuf(2304 * 4), FakeBuf(36), 10, 2304)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    # bench.py measures one GPU: --gpus above 1 exits with status 2 and a
+    # message, before anything touches a device
+    import subprocess
+    import sys
+
+    from conftest import ROOT
+
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120, cwd="/tmp")
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
+    assert r.stdout == ""
